@@ -1,0 +1,147 @@
+/*
+ * uttt_hip.h - C ABI of libuttt_hip.so, the gfx950 (MI355X) implementation of
+ * uTTT's fast-weight hot path: routing, token permute/unpermute by expert,
+ * the grouped SwiGLU fast-weight apply and its dot-product-loss update, and
+ * the norm-preserving write.
+ *
+ * Conventions shared by every entry point
+ *   - Plain pointers to device memory, sizes and element strides; no torch
+ *     types.  `stream` is a hipStream_t (passed as void*; NULL = default).
+ *   - Every call is asynchronous on `stream`, never synchronises the host and
+ *     never allocates: scratch memory is passed in by the caller, sized by the
+ *     matching *_workspace_bytes() query.
+ *   - Return value: UTTT_OK (0) or a negative UTTT_ERR_* code; the message of
+ *     the last failure on the calling thread is uttt_last_error().
+ *   - dtype codes: UTTT_F32, UTTT_BF16, UTTT_F16.
+ *   - Layouts are the reference's: activations [B, T, H] with H contiguous,
+ *     row_id_map [B, T, 2E+1] int32, routing masks / probs [B, E, T] addressed
+ *     by (batch, expert, token) element strides, fast weights [B, E, rows, cols].
+ *
+ * Reference interfaces are cited as paths under
+ * uttt_llm/flame/custom_models/uttt_moe/ (abbreviated L/ for its
+ * lact_moe_triton/ sub-package).
+ */
+#ifndef UTTT_HIP_H_
+#define UTTT_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define UTTT_OK 0
+#define UTTT_ERR_ARG (-1)         /* shape / dtype / pointer contract violated */
+#define UTTT_ERR_HIP (-2)         /* a HIP runtime call or launch failed       */
+#define UTTT_ERR_UNSUPPORTED (-3) /* valid request outside what is built       */
+
+#define UTTT_F32 0
+#define UTTT_BF16 1
+#define UTTT_F16 2
+
+/* Version of this ABI (bumped on any signature change). */
+int uttt_abi_version(void);
+/* Message of the last failed call on this thread ("" if none). */
+const char* uttt_last_error(void);
+
+/* ------------------------------------------------------------------------ */
+/* Routing map                                                              */
+/* ------------------------------------------------------------------------ */
+
+/* Scratch bytes for uttt_make_row_id_map at (B, T, E). */
+size_t uttt_row_id_map_workspace_bytes(int B, int T, int E);
+
+/* Replaces make_row_id_map (L/triton_permute.py:283-393).
+ * routing_map: 0/1 mask, element size mask_bytes (1 = bool/uint8, 4 = int32),
+ *   addressed as map[b*s_b + e*s_e + t*s_t].
+ * row_id_map: out [B, T, 2E+1] int32, bit-identical to the reference's,
+ *   including the stale entries it leaves in columns [n, E).
+ * group_sizes: optional out [B, E] int32 (tokens routed to each expert);
+ *   may be NULL.
+ * E <= 128. */
+int uttt_make_row_id_map(const void* routing_map, int mask_bytes, int64_t s_b,
+                         int64_t s_e, int64_t s_t, int B, int T, int E,
+                         int32_t* row_id_map, int32_t* group_sizes,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Permute / unpermute                                                      */
+/* ------------------------------------------------------------------------ */
+
+/* Replaces triton_permute_with_mask_map / _permute_kernel
+ * (L/triton_permute.py:396-571).  inp [B, T, H] contiguous of `dtype`;
+ * out [B, num_out, H]; for every token t and slot j < n_routed(t):
+ * out[row_j] = inp[t], or zeros if probs is given and probs[e_j, t] == 0.
+ * probs: optional fp32, strides (p_sb, p_se, p_st); permuted_probs: optional
+ * out [B, num_out] fp32 (required iff probs is given).  Rows >= num_out are
+ * never written. */
+int uttt_permute_fwd(const void* inp, int dtype, int B, int T, int H,
+                     const int32_t* row_id_map, int E, const float* probs,
+                     int64_t p_sb, int64_t p_se, int64_t p_st, void* out,
+                     int num_out, float* permuted_probs, void* stream);
+
+/* Replaces triton_permute_with_mask_map_bwd_batched
+ * (L/triton_permute.py:579-762).  grad_inp[t] = sum_j grad_out[row_j]
+ * (fp32 sum in slot order, one rounding); if grad_permuted_probs is given,
+ * grad_probs [B, E, T] (contiguous) gets grad_permuted_probs[row_j] at
+ * (e_j, t) and 0 elsewhere. */
+int uttt_permute_bwd(const void* grad_out, int dtype, int B, int T, int H,
+                     const int32_t* row_id_map, int E, int num_out,
+                     const float* grad_permuted_probs, void* grad_inp,
+                     float* grad_probs, void* stream);
+
+/* Replaces triton_unpermute_with_mask_map / _unpermute_kernel
+ * (L/triton_permute.py:765-930).  out[t] = cast(sum_j fma(inp[row_j], p_j))
+ * accumulated in fp32 in slot order, p_j = probs[e_j, t] (fp32, strided);
+ * probs may be NULL (plain sum). */
+int uttt_unpermute_fwd(const void* inp, int dtype, int B, int num_out, int H,
+                       const int32_t* row_id_map, int T, int E,
+                       const float* probs, int64_t p_sb, int64_t p_se,
+                       int64_t p_st, void* out, void* stream);
+
+/* Replaces triton_unpermute_with_mask_map_bwd_with_merging_probs
+ * (L/triton_permute.py:931-1141).  grad_inp[row_j] = cast(g[t] * p_j);
+ * grad_probs[e_j, t] = sum_h fwd_inp[row_j, h] * g[t, h] (fp32), 0 for
+ * experts not routed; grad_probs uses strides (gp_sb, gp_se, gp_st). */
+int uttt_unpermute_bwd(const void* grad_out, const void* fwd_inp, int dtype,
+                       int B, int T, int H, const int32_t* row_id_map, int E,
+                       int num_out, const float* probs, int64_t p_sb,
+                       int64_t p_se, int64_t p_st, void* grad_inp,
+                       float* grad_probs, int64_t gp_sb, int64_t gp_se,
+                       int64_t gp_st, void* stream);
+
+/* Replaces _permute_kv_with_lrs_kernel (L/triton_permute.py:1333-1493) as
+ * launched by PermuteKVAndLRs.forward (:1732-1900).  k, v [B, T, H]
+ * contiguous (k_dtype, v_dtype); lr0/1/2 [B, T] with element size lr_bytes
+ * (2 or 4) and token stride 1, batch stride T.  Outputs: k_out [B, num_out, H]
+ * (k_dtype), v_out [B, num_out, H] (k_dtype) = cast(fp32(v) * p),
+ * lr*_out [B, num_out] (copies). */
+int uttt_permute_kv_lrs_fwd(const void* k, int k_dtype, const void* v,
+                            int v_dtype, const void* lr0, const void* lr1,
+                            const void* lr2, int lr_bytes, int B, int T, int H,
+                            const int32_t* row_id_map, int E,
+                            const float* probs, int64_t p_sb, int64_t p_se,
+                            int64_t p_st, void* k_out, void* v_out,
+                            void* lr0_out, void* lr1_out, void* lr2_out,
+                            int num_out, void* stream);
+
+/* Replaces _permute_kv_with_lrs_bwd_kernel (L/triton_permute.py:1496-1727).
+ * gk, gv [B, num_out, H] (k_dtype); glr* [B, num_out] (glr_dtype, F32 or
+ * BF16/F16).  Writes grad_k [B,T,H] (k_dtype), grad_v [B,T,H] (v_dtype),
+ * grad_lr* [B,T] (glr_dtype), grad_probs [B,E,T] fp32 contiguous. */
+int uttt_permute_kv_lrs_bwd(const void* gk, const void* gv, int k_dtype,
+                            const void* glr0, const void* glr1,
+                            const void* glr2, int glr_dtype, const void* v,
+                            int v_dtype, const float* probs, int64_t p_sb,
+                            int64_t p_se, int64_t p_st, int B, int T, int H,
+                            const int32_t* row_id_map, int E, int num_out,
+                            void* grad_k, void* grad_v, void* grad_lr0,
+                            void* grad_lr1, void* grad_lr2, float* grad_probs,
+                            void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* UTTT_HIP_H_ */

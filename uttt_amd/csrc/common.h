@@ -1,0 +1,91 @@
+// Shared helpers for the gfx950 kernels of libuttt_hip.so: status handling,
+// dtype conversion (round-to-nearest-even bf16, as torch and Triton use) and
+// small wave-level primitives for 64-lane CDNA wavefronts.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <initializer_list>
+
+#include "../../include/uttt_hip.h"
+
+namespace uttt {
+
+// ---------------------------------------------------------------- status ----
+void set_error(const char* fmt, ...);
+int check_launch(const char* what);
+
+#define UTTT_REQUIRE(cond, ...)          \
+  do {                                   \
+    if (!(cond)) {                       \
+      ::uttt::set_error(__VA_ARGS__);    \
+      return UTTT_ERR_ARG;               \
+    }                                    \
+  } while (0)
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline int dtype_bytes(int dt) {
+  switch (dt) {
+    case UTTT_F32: return 4;
+    case UTTT_BF16: return 2;
+    case UTTT_F16: return 2;
+    default: return 0;
+  }
+}
+
+// ------------------------------------------------------------ conversion ----
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// fp32 -> bf16, round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+// fp32 -> fp16 with the hardware conversion (round to nearest even).
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+// Element traits: storage type and conversions for the three payload dtypes.
+struct F32T {
+  using S = float;
+  static constexpr int code = UTTT_F32;
+  __device__ __forceinline__ static float load(S v) { return v; }
+  __device__ __forceinline__ static S store(float f) { return f; }
+};
+struct BF16T {
+  using S = uint16_t;
+  static constexpr int code = UTTT_BF16;
+  __device__ __forceinline__ static float load(S v) { return bf16_to_f32(v); }
+  __device__ __forceinline__ static S store(float f) { return f32_to_bf16(f); }
+};
+struct F16T {
+  using S = uint16_t;
+  static constexpr int code = UTTT_F16;
+  __device__ __forceinline__ static float load(S v) { return f16_to_f32(v); }
+  __device__ __forceinline__ static S store(float f) { return f32_to_f16(f); }
+};
+
+// ------------------------------------------------------------------ wave ----
+constexpr int kWave = 64;
+
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+// Number of set bits of `mask` strictly below this lane.
+__device__ __forceinline__ int lanes_below(uint64_t mask) {
+  return __popcll(mask & ((1ull << lane_id()) - 1ull));
+}
+
+}  // namespace uttt

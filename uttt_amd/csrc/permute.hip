@@ -1,0 +1,753 @@
+// Token permute / unpermute by expert for gfx950.
+//
+// Row map (reference: make_row_id_map, L/triton_permute.py:283-393).  The
+// destination of (token t, expert e) is row(e, t) = off_e + rank(e, t): the
+// permuted buffer is expert-major and token-ascending.  Three launches:
+//   count : one workgroup per 256-token tile; each wave ballots the 0/1 mask
+//           of every expert and the per-tile counts go to a [B, E, tiles]
+//           table (expert-major, so the global order is a linear scan);
+//   scan  : one workgroup per batch does the exclusive prefix over that table
+//           (it also yields group_sizes);
+//   emit  : re-ballots the tile's mask, ranks each routed token inside its
+//           wave with popcount, and writes the packed per-token entry in the
+//           reference format (rows and experts in descending order, n_routed
+//           last, the reference's stale values in columns [n, E)).
+// No atomics are used, so the result is deterministic by construction.
+//
+// Payload kernels give one 64-lane wave to one token and move its row in
+// 16-byte vectors: permute reads the row once and writes it to each of the
+// token's slots; unpermute gathers the slots and reduces in fp32 registers.
+#include "common.h"
+
+namespace uttt {
+namespace {
+
+constexpr int kTile = 256;         // tokens per row-map workgroup
+constexpr int kMaxExperts = 128;   // row-map LDS tables are sized for this
+constexpr int kTokPerBlock = 4;    // payload kernels: 4 waves = 4 tokens
+
+__device__ __forceinline__ bool mask_bit(const void* map, int mask_bytes, int64_t idx) {
+  if (mask_bytes == 1) return reinterpret_cast<const uint8_t*>(map)[idx] != 0;
+  return reinterpret_cast<const int32_t*>(map)[idx] != 0;
+}
+
+// ------------------------------------------------------------ row map ------
+__global__ __launch_bounds__(kTile) void rowmap_count_kernel(
+    const void* map, int mask_bytes, int64_t s_b, int64_t s_e, int64_t s_t, int T, int E,
+    int ntiles, int32_t* counts) {
+  __shared__ int wcnt[kTile / kWave][kMaxExperts];
+  const int tile = blockIdx.x, b = blockIdx.y;
+  const int t = tile * kTile + threadIdx.x;
+  const int w = threadIdx.x / kWave;
+  const int64_t base = (int64_t)b * s_b + (int64_t)t * s_t;
+  for (int e = 0; e < E; ++e) {
+    bool bit = (t < T) && mask_bit(map, mask_bytes, base + (int64_t)e * s_e);
+    uint64_t bal = __ballot(bit);
+    if (lane_id() == 0) wcnt[w][e] = __popcll(bal);
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += kTile) {
+    int c = 0;
+#pragma unroll
+    for (int i = 0; i < kTile / kWave; ++i) c += wcnt[i][e];
+    counts[((int64_t)b * E + e) * ntiles + tile] = c;
+  }
+}
+
+// Exclusive scan of counts[b] (E * ntiles entries, expert-major) in place.
+constexpr int kScanThreads = 1024;
+constexpr int kScanPer = 4;
+
+__global__ __launch_bounds__(kScanThreads) void rowmap_scan_kernel(int32_t* counts, int E,
+                                                                   int ntiles,
+                                                                   int32_t* group_sizes) {
+  __shared__ int wave_tot[kScanThreads / kWave];
+  __shared__ int expert_start[kMaxExperts + 1];
+  __shared__ int carry_s;
+  const int b = blockIdx.x;
+  const int n = E * ntiles;
+  int32_t* c = counts + (int64_t)b * n;
+  const int tid = threadIdx.x, w = tid / kWave, lane = lane_id();
+  if (tid == 0) carry_s = 0;
+  __syncthreads();
+  for (int base = 0; base < n; base += kScanThreads * kScanPer) {
+    int v[kScanPer];
+    int sum = 0;
+#pragma unroll
+    for (int i = 0; i < kScanPer; ++i) {
+      int idx = base + tid * kScanPer + i;
+      v[i] = idx < n ? c[idx] : 0;
+      sum += v[i];
+    }
+    // inclusive scan of per-thread sums across the wave
+    int incl = sum;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      int o = __shfl_up(incl, d, kWave);
+      if (lane >= d) incl += o;
+    }
+    if (lane == kWave - 1) wave_tot[w] = incl;
+    __syncthreads();
+    int wave_off = 0;
+    for (int i = 0; i < w; ++i) wave_off += wave_tot[i];
+    int block_tot = 0;
+    for (int i = 0; i < kScanThreads / kWave; ++i) block_tot += wave_tot[i];
+    int run = carry_s + wave_off + incl - sum;  // exclusive prefix of this thread
+#pragma unroll
+    for (int i = 0; i < kScanPer; ++i) {
+      int idx = base + tid * kScanPer + i;
+      if (idx < n) {
+        c[idx] = run;
+        if (idx % ntiles == 0) expert_start[idx / ntiles] = run;
+      }
+      run += v[i];
+    }
+    __syncthreads();
+    if (tid == 0) carry_s += block_tot;
+    __syncthreads();
+  }
+  if (tid == 0) expert_start[E] = carry_s;
+  __syncthreads();
+  if (group_sizes != nullptr) {
+    for (int e = tid; e < E; e += kScanThreads)
+      group_sizes[(int64_t)b * E + e] = expert_start[e + 1] - expert_start[e];
+  }
+}
+
+__global__ __launch_bounds__(kTile) void rowmap_emit_kernel(
+    const void* map, int mask_bytes, int64_t s_b, int64_t s_e, int64_t s_t, int T, int E,
+    int ntiles, const int32_t* offsets, int32_t* row_id_map) {
+  __shared__ int wcnt[kTile / kWave][kMaxExperts];
+  __shared__ int toff[kMaxExperts];
+  const int tile = blockIdx.x, b = blockIdx.y;
+  const int t = tile * kTile + threadIdx.x;
+  const int w = threadIdx.x / kWave;
+  const int64_t base = (int64_t)b * s_b + (int64_t)t * s_t;
+  uint32_t bits[kMaxExperts / 32] = {0u, 0u, 0u, 0u};
+  for (int e = 0; e < E; ++e) {
+    bool bit = (t < T) && mask_bit(map, mask_bytes, base + (int64_t)e * s_e);
+    bits[e >> 5] |= (uint32_t)bit << (e & 31);
+    uint64_t bal = __ballot(bit);
+    if (lane_id() == 0) wcnt[w][e] = __popcll(bal);
+  }
+  for (int e = threadIdx.x; e < E; e += kTile)
+    toff[e] = offsets[((int64_t)b * E + e) * ntiles + tile];
+  __syncthreads();
+
+  const int n = __popc(bits[0]) + __popc(bits[1]) + __popc(bits[2]) + __popc(bits[3]);
+  const int W = 2 * E + 1;
+  int32_t* row = row_id_map + ((int64_t)b * T + t) * W;
+  int j = 0;
+  for (int e = E - 1; e >= 0; --e) {
+    const bool bit = (bits[e >> 5] >> (e & 31)) & 1u;
+    const uint64_t bal = __ballot(bit);  // every lane of the wave takes part
+    if (t < T) {
+      int r = -1;
+      if (bit) {
+        r = toff[e] + lanes_below(bal);
+        for (int i = 0; i < w; ++i) r += wcnt[i][e];
+        row[j] = r;
+        row[E + j] = e;
+        ++j;
+      }
+      if (e >= n) row[e] = r;  // stale column: row if routed, else -1
+    }
+  }
+  if (t < T) {
+    for (int c = E + n; c < 2 * E; ++c) row[c] = 0;
+    row[2 * E] = n;
+  }
+}
+
+// ---------------------------------------------------------- vector copy ----
+template <int VB>
+struct Vec;
+template <>
+struct Vec<16> { using T = uint4; };
+template <>
+struct Vec<8> { using T = uint2; };
+template <>
+struct Vec<4> { using T = uint32_t; };
+template <>
+struct Vec<2> { using T = uint16_t; };
+
+// Largest of 16/8/4/2 dividing the row size and the base addresses.
+inline int pick_vec_bytes(int64_t row_bytes, std::initializer_list<const void*> ptrs) {
+  for (int vb : {16, 8, 4, 2}) {
+    bool ok = (row_bytes % vb) == 0;
+    for (const void* p : ptrs) ok = ok && ((reinterpret_cast<uintptr_t>(p) % vb) == 0);
+    if (ok) return vb;
+  }
+  return 1;
+}
+
+__device__ __forceinline__ int64_t tok_index(int b, int t, int T) { return (int64_t)b * T + t; }
+
+// --------------------------------------------------------------- permute ---
+template <int VB>
+__global__ __launch_bounds__(kTokPerBlock* kWave) void permute_fwd_kernel(
+    const uint8_t* __restrict__ inp, int64_t row_bytes, int T, const int32_t* __restrict__ rmap,
+    int E, const float* __restrict__ probs, int64_t p_sb, int64_t p_se, int64_t p_st,
+    uint8_t* __restrict__ out, int num_out, float* __restrict__ pprobs) {
+  using V = typename Vec<VB>::T;
+  const int t = blockIdx.x * kTokPerBlock + threadIdx.x / kWave;
+  const int b = blockIdx.y;
+  if (t >= T) return;
+  const int lane = lane_id();
+  const int32_t* rm = rmap + tok_index(b, t, T) * (2 * E + 1);
+  const int n = rm[2 * E];
+  if (probs != nullptr && lane < n && lane < kWave) {
+    for (int j = lane; j < n; j += kWave) {
+      const int row = rm[j];
+      const int e = rm[E + j];
+      if (row >= 0 && row < num_out)
+        pprobs[(int64_t)b * num_out + row] = probs[b * p_sb + e * p_se + t * p_st];
+    }
+  }
+  const uint8_t* src = inp + tok_index(b, t, T) * row_bytes;
+  uint8_t* dst_b = out + (int64_t)b * num_out * row_bytes;
+  for (int64_t off = (int64_t)lane * VB; off < row_bytes; off += (int64_t)kWave * VB) {
+    const V v = *reinterpret_cast<const V*>(src + off);
+    for (int j = 0; j < n; ++j) {
+      const int row = rm[j];
+      if (row < 0 || row >= num_out) continue;
+      V o = v;
+      if (probs != nullptr) {
+        const int e = rm[E + j];
+        if (probs[b * p_sb + e * p_se + t * p_st] == 0.0f) o = V{};
+      }
+      *reinterpret_cast<V*>(dst_b + (int64_t)row * row_bytes + off) = o;
+    }
+  }
+}
+
+// grad_inp[t] = sum_j grad_out[row_j], fp32 in slot order.
+template <class TT, int VE>
+__global__ __launch_bounds__(kTokPerBlock* kWave) void permute_bwd_kernel(
+    const typename TT::S* __restrict__ gout, int H, int T, const int32_t* __restrict__ rmap,
+    int E, int num_out, const float* __restrict__ gpp, typename TT::S* __restrict__ ginp,
+    float* __restrict__ gprobs) {
+  using S = typename TT::S;
+  const int t = blockIdx.x * kTokPerBlock + threadIdx.x / kWave;
+  const int b = blockIdx.y;
+  if (t >= T) return;
+  const int lane = lane_id();
+  const int32_t* rm = rmap + tok_index(b, t, T) * (2 * E + 1);
+  const int n = rm[2 * E];
+  for (int h0 = lane * VE; h0 < H; h0 += kWave * VE) {
+    float acc[VE];
+#pragma unroll
+    for (int i = 0; i < VE; ++i) acc[i] = 0.0f;
+    for (int j = 0; j < n; ++j) {
+      const int row = rm[j];
+      if (row < 0 || row >= num_out) continue;
+      const S* src = gout + ((int64_t)b * num_out + row) * H + h0;
+#pragma unroll
+      for (int i = 0; i < VE; ++i) acc[i] += TT::load(src[i]);
+    }
+    S* dst = ginp + tok_index(b, t, T) * H + h0;
+#pragma unroll
+    for (int i = 0; i < VE; ++i) dst[i] = TT::store(acc[i]);
+  }
+  if (gprobs != nullptr) {
+    for (int e = lane; e < E; e += kWave) {
+      float val = 0.0f;
+      for (int j = 0; j < n; ++j) {
+        const int row = rm[j];
+        if (rm[E + j] == e && row >= 0 && row < num_out) val = gpp[(int64_t)b * num_out + row];
+      }
+      gprobs[((int64_t)b * E + e) * T + t] = val;
+    }
+  }
+}
+
+// ------------------------------------------------------------- unpermute ---
+template <class TT, int VE>
+__global__ __launch_bounds__(kTokPerBlock* kWave) void unpermute_fwd_kernel(
+    const typename TT::S* __restrict__ inp, int H, int num_out, const int32_t* __restrict__ rmap,
+    int T, int E, const float* __restrict__ probs, int64_t p_sb, int64_t p_se, int64_t p_st,
+    typename TT::S* __restrict__ out) {
+  using S = typename TT::S;
+  const int t = blockIdx.x * kTokPerBlock + threadIdx.x / kWave;
+  const int b = blockIdx.y;
+  if (t >= T) return;
+  const int lane = lane_id();
+  const int32_t* rm = rmap + tok_index(b, t, T) * (2 * E + 1);
+  const int n = rm[2 * E];
+  for (int h0 = lane * VE; h0 < H; h0 += kWave * VE) {
+    float acc[VE];
+#pragma unroll
+    for (int i = 0; i < VE; ++i) acc[i] = 0.0f;
+    for (int j = 0; j < n; ++j) {
+      const int row = rm[j];
+      if (row < 0 || row >= num_out) continue;
+      const S* src = inp + ((int64_t)b * num_out + row) * H + h0;
+      S x[VE];
+#pragma unroll
+      for (int i = 0; i < VE; ++i) x[i] = src[i];
+      if (probs != nullptr) {
+        const float p = probs[b * p_sb + (int64_t)rm[E + j] * p_se + (int64_t)t * p_st];
+#pragma unroll
+        for (int i = 0; i < VE; ++i) acc[i] = __builtin_fmaf(TT::load(x[i]), p, acc[i]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < VE; ++i) acc[i] += TT::load(x[i]);
+      }
+    }
+    S* dst = out + tok_index(b, t, T) * H + h0;
+#pragma unroll
+    for (int i = 0; i < VE; ++i) dst[i] = TT::store(acc[i]);
+  }
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int d = kWave / 2; d > 0; d >>= 1) v += __shfl_xor(v, d, kWave);
+  return v;
+}
+
+template <class TT, int VE>
+__global__ __launch_bounds__(kTokPerBlock* kWave) void unpermute_bwd_kernel(
+    const typename TT::S* __restrict__ gout, const typename TT::S* __restrict__ fwd_inp, int H,
+    int T, const int32_t* __restrict__ rmap, int E, int num_out, const float* __restrict__ probs,
+    int64_t p_sb, int64_t p_se, int64_t p_st, typename TT::S* __restrict__ ginp,
+    float* __restrict__ gprobs, int64_t g_sb, int64_t g_se, int64_t g_st) {
+  using S = typename TT::S;
+  const int t = blockIdx.x * kTokPerBlock + threadIdx.x / kWave;
+  const int b = blockIdx.y;
+  if (t >= T) return;
+  const int lane = lane_id();
+  const int32_t* rm = rmap + tok_index(b, t, T) * (2 * E + 1);
+  const int n = rm[2 * E];
+  // experts that are not routed get a zero gradient
+  for (int e = lane; e < E; e += kWave) {
+    bool routed = false;
+    for (int j = 0; j < n; ++j) routed = routed || (rm[E + j] == e);
+    if (!routed) gprobs[b * g_sb + (int64_t)e * g_se + (int64_t)t * g_st] = 0.0f;
+  }
+  const S* g = gout + tok_index(b, t, T) * H;
+  for (int j = 0; j < n; ++j) {
+    const int row = rm[j];
+    const int e = rm[E + j];
+    if (row < 0 || row >= num_out) continue;
+    const float p = probs[b * p_sb + (int64_t)e * p_se + (int64_t)t * p_st];
+    const S* y = fwd_inp + ((int64_t)b * num_out + row) * H;
+    S* gi = ginp + ((int64_t)b * num_out + row) * H;
+    float dot = 0.0f;
+    for (int h0 = lane * VE; h0 < H; h0 += kWave * VE) {
+#pragma unroll
+      for (int i = 0; i < VE; ++i) {
+        const float gv = TT::load(g[h0 + i]);
+        gi[h0 + i] = TT::store(gv * p);
+        dot = __builtin_fmaf(TT::load(y[h0 + i]), gv, dot);
+      }
+    }
+    dot = wave_sum(dot);
+    if (lane == 0) gprobs[b * g_sb + (int64_t)e * g_se + (int64_t)t * g_st] = dot;
+  }
+}
+
+// ------------------------------------------------------ permute k, v, lr ---
+template <class KT, class VT, int VE>
+__global__ __launch_bounds__(kTokPerBlock* kWave) void permute_kv_fwd_kernel(
+    const typename KT::S* __restrict__ k, const typename VT::S* __restrict__ v,
+    const uint8_t* __restrict__ lr0, const uint8_t* __restrict__ lr1,
+    const uint8_t* __restrict__ lr2, int lr_bytes, int H, int T,
+    const int32_t* __restrict__ rmap, int E, const float* __restrict__ probs, int64_t p_sb,
+    int64_t p_se, int64_t p_st, typename KT::S* __restrict__ k_out,
+    typename KT::S* __restrict__ v_out, uint8_t* __restrict__ lr0_out,
+    uint8_t* __restrict__ lr1_out, uint8_t* __restrict__ lr2_out, int num_out) {
+  using SK = typename KT::S;
+  using SV = typename VT::S;
+  const int t = blockIdx.x * kTokPerBlock + threadIdx.x / kWave;
+  const int b = blockIdx.y;
+  if (t >= T) return;
+  const int lane = lane_id();
+  const int32_t* rm = rmap + tok_index(b, t, T) * (2 * E + 1);
+  const int n = rm[2 * E];
+  // per-token learning rates: plain copies, one lane per slot
+  for (int j = lane; j < n; j += kWave) {
+    const int row = rm[j];
+    if (row < 0 || row >= num_out) continue;
+    const int64_t src = tok_index(b, t, T) * lr_bytes;
+    const int64_t dst = ((int64_t)b * num_out + row) * lr_bytes;
+    if (lr_bytes == 4) {
+      *reinterpret_cast<uint32_t*>(lr0_out + dst) = *reinterpret_cast<const uint32_t*>(lr0 + src);
+      *reinterpret_cast<uint32_t*>(lr1_out + dst) = *reinterpret_cast<const uint32_t*>(lr1 + src);
+      *reinterpret_cast<uint32_t*>(lr2_out + dst) = *reinterpret_cast<const uint32_t*>(lr2 + src);
+    } else {
+      *reinterpret_cast<uint16_t*>(lr0_out + dst) = *reinterpret_cast<const uint16_t*>(lr0 + src);
+      *reinterpret_cast<uint16_t*>(lr1_out + dst) = *reinterpret_cast<const uint16_t*>(lr1 + src);
+      *reinterpret_cast<uint16_t*>(lr2_out + dst) = *reinterpret_cast<const uint16_t*>(lr2 + src);
+    }
+  }
+  const SK* ks = k + tok_index(b, t, T) * H;
+  const SV* vs = v + tok_index(b, t, T) * H;
+  for (int h0 = lane * VE; h0 < H; h0 += kWave * VE) {
+    SK kx[VE];
+    float vx[VE];
+#pragma unroll
+    for (int i = 0; i < VE; ++i) {
+      kx[i] = ks[h0 + i];
+      vx[i] = VT::load(vs[h0 + i]);
+    }
+    for (int j = 0; j < n; ++j) {
+      const int row = rm[j];
+      if (row < 0 || row >= num_out) continue;
+      const float p = probs[b * p_sb + (int64_t)rm[E + j] * p_se + (int64_t)t * p_st];
+      SK* kd = k_out + ((int64_t)b * num_out + row) * H + h0;
+      SK* vd = v_out + ((int64_t)b * num_out + row) * H + h0;
+#pragma unroll
+      for (int i = 0; i < VE; ++i) {
+        kd[i] = kx[i];
+        vd[i] = KT::store(vx[i] * p);
+      }
+    }
+  }
+}
+
+template <class KT, class VT, class LT, int VE>
+__global__ __launch_bounds__(kTokPerBlock* kWave) void permute_kv_bwd_kernel(
+    const typename KT::S* __restrict__ gk, const typename KT::S* __restrict__ gv,
+    const typename LT::S* __restrict__ glr0, const typename LT::S* __restrict__ glr1,
+    const typename LT::S* __restrict__ glr2, const typename VT::S* __restrict__ v,
+    const float* __restrict__ probs, int64_t p_sb, int64_t p_se, int64_t p_st, int H, int T,
+    const int32_t* __restrict__ rmap, int E, int num_out, typename KT::S* __restrict__ grad_k,
+    typename VT::S* __restrict__ grad_v, typename LT::S* __restrict__ grad_lr0,
+    typename LT::S* __restrict__ grad_lr1, typename LT::S* __restrict__ grad_lr2,
+    float* __restrict__ grad_probs) {
+  using SK = typename KT::S;
+  using SV = typename VT::S;
+  const int t = blockIdx.x * kTokPerBlock + threadIdx.x / kWave;
+  const int b = blockIdx.y;
+  if (t >= T) return;
+  const int lane = lane_id();
+  const int32_t* rm = rmap + tok_index(b, t, T) * (2 * E + 1);
+  const int n = rm[2 * E];
+  if (lane == 0) {
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f;
+    for (int j = 0; j < n; ++j) {
+      const int row = rm[j];
+      if (row < 0 || row >= num_out) continue;
+      const int64_t r = (int64_t)b * num_out + row;
+      a0 += LT::load(glr0[r]);
+      a1 += LT::load(glr1[r]);
+      a2 += LT::load(glr2[r]);
+    }
+    grad_lr0[tok_index(b, t, T)] = LT::store(a0);
+    grad_lr1[tok_index(b, t, T)] = LT::store(a1);
+    grad_lr2[tok_index(b, t, T)] = LT::store(a2);
+  }
+  for (int e = lane; e < E; e += kWave) {
+    bool routed = false;
+    for (int j = 0; j < n; ++j) routed = routed || (rm[E + j] == e);
+    if (!routed) grad_probs[((int64_t)b * E + e) * T + t] = 0.0f;
+  }
+  // fp32 partial dot products for the prob gradient, one per slot (n <= E)
+  const SV* vs = v + tok_index(b, t, T) * H;
+  for (int j = 0; j < n; ++j) {
+    const int row = rm[j];
+    if (row < 0 || row >= num_out) continue;
+    const float p = probs[b * p_sb + (int64_t)rm[E + j] * p_se + (int64_t)t * p_st];
+    const SK* gvr = gv + ((int64_t)b * num_out + row) * H;
+    float dot = 0.0f;
+    if (p != 0.0f) {
+      for (int h0 = lane * VE; h0 < H; h0 += kWave * VE) {
+#pragma unroll
+        for (int i = 0; i < VE; ++i) dot = __builtin_fmaf(KT::load(gvr[h0 + i]), VT::load(vs[h0 + i]), dot);
+      }
+    }
+    dot = wave_sum(dot);
+    if (lane == 0) grad_probs[((int64_t)b * E + rm[E + j]) * T + t] = dot;
+  }
+  for (int h0 = lane * VE; h0 < H; h0 += kWave * VE) {
+    float ak[VE], av[VE];
+#pragma unroll
+    for (int i = 0; i < VE; ++i) ak[i] = av[i] = 0.0f;
+    for (int j = 0; j < n; ++j) {
+      const int row = rm[j];
+      if (row < 0 || row >= num_out) continue;
+      const float p = probs[b * p_sb + (int64_t)rm[E + j] * p_se + (int64_t)t * p_st];
+      const int64_t r = ((int64_t)b * num_out + row) * H + h0;
+#pragma unroll
+      for (int i = 0; i < VE; ++i) {
+        ak[i] += KT::load(gk[r + i]);
+        av[i] = __builtin_fmaf(KT::load(gv[r + i]), p, av[i]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < VE; ++i) {
+      grad_k[tok_index(b, t, T) * H + h0 + i] = KT::store(ak[i]);
+      grad_v[tok_index(b, t, T) * H + h0 + i] = VT::store(av[i]);
+    }
+  }
+}
+
+inline dim3 tok_grid(int T, int B) { return dim3((T + kTokPerBlock - 1) / kTokPerBlock, B); }
+inline dim3 tok_block() { return dim3(kTokPerBlock * kWave); }
+
+// Elements per lane chunk: 16 bytes when the row and the pointers allow it.
+template <class TT>
+int pick_ve(int H, std::initializer_list<const void*> ptrs) {
+  const int eb = sizeof(typename TT::S);
+  const int vb = pick_vec_bytes((int64_t)H * eb, ptrs);
+  const int ve = vb / eb;
+  return ve >= 8 ? 8 : ve >= 4 ? 4 : ve >= 2 ? 2 : 1;
+}
+
+#define UTTT_VE_SWITCH(ve, ...)          \
+  switch (ve) {                          \
+    case 8: { constexpr int VE = 8; __VA_ARGS__; } break; \
+    case 4: { constexpr int VE = 4; __VA_ARGS__; } break; \
+    case 2: { constexpr int VE = 2; __VA_ARGS__; } break; \
+    default: { constexpr int VE = 1; __VA_ARGS__; } break; \
+  }
+
+#define UTTT_DTYPE_SWITCH(dt, TT, ...)                             \
+  switch (dt) {                                                    \
+    case UTTT_F32: { using TT = F32T; __VA_ARGS__; } break;         \
+    case UTTT_BF16: { using TT = BF16T; __VA_ARGS__; } break;       \
+    case UTTT_F16: { using TT = F16T; __VA_ARGS__; } break;         \
+    default: set_error("unsupported dtype code %d", (int)dt); return UTTT_ERR_ARG; \
+  }
+
+}  // namespace
+}  // namespace uttt
+
+using namespace uttt;
+
+extern "C" size_t uttt_row_id_map_workspace_bytes(int B, int T, int E) {
+  if (B <= 0 || T <= 0 || E <= 0) return 0;
+  const int ntiles = (T + kTile - 1) / kTile;
+  return (size_t)B * E * ntiles * sizeof(int32_t);
+}
+
+extern "C" int uttt_make_row_id_map(const void* routing_map, int mask_bytes, int64_t s_b,
+                                    int64_t s_e, int64_t s_t, int B, int T, int E,
+                                    int32_t* row_id_map, int32_t* group_sizes, void* workspace,
+                                    size_t workspace_bytes, void* stream) {
+  UTTT_REQUIRE(B >= 0 && T >= 0 && E >= 1, "make_row_id_map: bad sizes B=%d T=%d E=%d", B, T, E);
+  UTTT_REQUIRE(E <= kMaxExperts, "make_row_id_map: E=%d exceeds %d", E, kMaxExperts);
+  UTTT_REQUIRE(mask_bytes == 1 || mask_bytes == 4, "make_row_id_map: mask element size %d", mask_bytes);
+  if (B == 0) return UTTT_OK;
+  const size_t need = uttt_row_id_map_workspace_bytes(B, T > 0 ? T : 1, E);
+  UTTT_REQUIRE(workspace != nullptr && workspace_bytes >= need,
+               "make_row_id_map: workspace %zu < %zu bytes", workspace_bytes, need);
+  UTTT_REQUIRE(row_id_map != nullptr, "make_row_id_map: null row_id_map");
+  hipStream_t st = as_stream(stream);
+  if (T == 0) {
+    if (group_sizes != nullptr) {
+      if (hipMemsetAsync(group_sizes, 0, sizeof(int32_t) * B * E, st) != hipSuccess) {
+        set_error("make_row_id_map: memset failed");
+        return UTTT_ERR_HIP;
+      }
+    }
+    return UTTT_OK;
+  }
+  UTTT_REQUIRE(routing_map != nullptr, "make_row_id_map: null routing_map");
+  const int ntiles = (T + kTile - 1) / kTile;
+  int32_t* counts = reinterpret_cast<int32_t*>(workspace);
+  hipLaunchKernelGGL(rowmap_count_kernel, dim3(ntiles, B), dim3(kTile), 0, st, routing_map,
+                     mask_bytes, s_b, s_e, s_t, T, E, ntiles, counts);
+  hipLaunchKernelGGL(rowmap_scan_kernel, dim3(B), dim3(kScanThreads), 0, st, counts, E, ntiles,
+                     group_sizes);
+  hipLaunchKernelGGL(rowmap_emit_kernel, dim3(ntiles, B), dim3(kTile), 0, st, routing_map,
+                     mask_bytes, s_b, s_e, s_t, T, E, ntiles, counts, row_id_map);
+  return check_launch("make_row_id_map");
+}
+
+extern "C" int uttt_permute_fwd(const void* inp, int dtype, int B, int T, int H,
+                                const int32_t* row_id_map, int E, const float* probs, int64_t p_sb,
+                                int64_t p_se, int64_t p_st, void* out, int num_out,
+                                float* permuted_probs, void* stream) {
+  const int eb = dtype_bytes(dtype);
+  UTTT_REQUIRE(eb > 0, "permute_fwd: unsupported dtype %d", dtype);
+  UTTT_REQUIRE(B >= 0 && T >= 0 && H >= 0 && E >= 1 && num_out >= 0, "permute_fwd: bad sizes");
+  UTTT_REQUIRE(probs == nullptr || permuted_probs != nullptr || num_out == 0,
+               "permute_fwd: probs given without permuted_probs");
+  if (B == 0 || T == 0 || H == 0) {
+    if (probs != nullptr && B > 0 && T > 0 && H == 0) {
+      // rows are empty but the permuted probs still have to be produced
+    } else {
+      return UTTT_OK;
+    }
+  }
+  const int64_t row_bytes = (int64_t)H * eb;
+  const int vb = pick_vec_bytes(row_bytes > 0 ? row_bytes : 16, {inp, out});
+  hipStream_t st = as_stream(stream);
+#define UTTT_LAUNCH_PERM(VBv)                                                                   \
+  hipLaunchKernelGGL(permute_fwd_kernel<VBv>, tok_grid(T, B), tok_block(), 0, st,              \
+                     reinterpret_cast<const uint8_t*>(inp), row_bytes, T, row_id_map, E, probs, \
+                     p_sb, p_se, p_st, reinterpret_cast<uint8_t*>(out), num_out, permuted_probs)
+  switch (vb) {
+    case 16: UTTT_LAUNCH_PERM(16); break;
+    case 8: UTTT_LAUNCH_PERM(8); break;
+    case 4: UTTT_LAUNCH_PERM(4); break;
+    default: UTTT_LAUNCH_PERM(2); break;
+  }
+#undef UTTT_LAUNCH_PERM
+  return check_launch("permute_fwd");
+}
+
+extern "C" int uttt_permute_bwd(const void* grad_out, int dtype, int B, int T, int H,
+                                const int32_t* row_id_map, int E, int num_out,
+                                const float* grad_permuted_probs, void* grad_inp,
+                                float* grad_probs, void* stream) {
+  UTTT_REQUIRE(B >= 0 && T >= 0 && H >= 0 && E >= 1, "permute_bwd: bad sizes");
+  UTTT_REQUIRE((grad_permuted_probs == nullptr) == (grad_probs == nullptr),
+               "permute_bwd: grad_permuted_probs and grad_probs go together");
+  if (B == 0 || T == 0) return UTTT_OK;
+  hipStream_t st = as_stream(stream);
+  UTTT_DTYPE_SWITCH(dtype, TT, {
+    using S = typename TT::S;
+    const int ve = pick_ve<TT>(H, {grad_out, grad_inp});
+    UTTT_VE_SWITCH(ve, hipLaunchKernelGGL((permute_bwd_kernel<TT, VE>), tok_grid(T, B), tok_block(),
+                                          0, st, reinterpret_cast<const S*>(grad_out), H, T,
+                                          row_id_map, E, num_out, grad_permuted_probs,
+                                          reinterpret_cast<S*>(grad_inp), grad_probs));
+  });
+  return check_launch("permute_bwd");
+}
+
+extern "C" int uttt_unpermute_fwd(const void* inp, int dtype, int B, int num_out, int H,
+                                  const int32_t* row_id_map, int T, int E, const float* probs,
+                                  int64_t p_sb, int64_t p_se, int64_t p_st, void* out,
+                                  void* stream) {
+  UTTT_REQUIRE(B >= 0 && T >= 0 && H >= 0 && E >= 1 && num_out >= 0, "unpermute_fwd: bad sizes");
+  if (B == 0 || T == 0 || H == 0) return UTTT_OK;
+  hipStream_t st = as_stream(stream);
+  UTTT_DTYPE_SWITCH(dtype, TT, {
+    using S = typename TT::S;
+    const int ve = pick_ve<TT>(H, {inp, out});
+    UTTT_VE_SWITCH(ve, hipLaunchKernelGGL((unpermute_fwd_kernel<TT, VE>), tok_grid(T, B),
+                                          tok_block(), 0, st, reinterpret_cast<const S*>(inp), H,
+                                          num_out, row_id_map, T, E, probs, p_sb, p_se, p_st,
+                                          reinterpret_cast<S*>(out)));
+  });
+  return check_launch("unpermute_fwd");
+}
+
+extern "C" int uttt_unpermute_bwd(const void* grad_out, const void* fwd_inp, int dtype, int B,
+                                  int T, int H, const int32_t* row_id_map, int E, int num_out,
+                                  const float* probs, int64_t p_sb, int64_t p_se, int64_t p_st,
+                                  void* grad_inp, float* grad_probs, int64_t gp_sb, int64_t gp_se,
+                                  int64_t gp_st, void* stream) {
+  UTTT_REQUIRE(B >= 0 && T >= 0 && H >= 0 && E >= 1, "unpermute_bwd: bad sizes");
+  UTTT_REQUIRE(probs != nullptr && grad_probs != nullptr, "unpermute_bwd: probs are required");
+  if (B == 0 || T == 0) return UTTT_OK;
+  hipStream_t st = as_stream(stream);
+  UTTT_DTYPE_SWITCH(dtype, TT, {
+    using S = typename TT::S;
+    const int ve = pick_ve<TT>(H, {grad_out, fwd_inp, grad_inp});
+    UTTT_VE_SWITCH(ve, hipLaunchKernelGGL((unpermute_bwd_kernel<TT, VE>), tok_grid(T, B),
+                                          tok_block(), 0, st,
+                                          reinterpret_cast<const S*>(grad_out),
+                                          reinterpret_cast<const S*>(fwd_inp), H, T, row_id_map,
+                                          E, num_out, probs, p_sb, p_se, p_st,
+                                          reinterpret_cast<S*>(grad_inp), grad_probs, gp_sb,
+                                          gp_se, gp_st));
+  });
+  return check_launch("unpermute_bwd");
+}
+
+namespace {
+template <class KT, class VT>
+int launch_permute_kv_fwd(const void* k, const void* v, const void* lr0, const void* lr1,
+                          const void* lr2, int lr_bytes, int B, int T, int H,
+                          const int32_t* row_id_map, int E, const float* probs, int64_t p_sb,
+                          int64_t p_se, int64_t p_st, void* k_out, void* v_out, void* lr0_out,
+                          void* lr1_out, void* lr2_out, int num_out, hipStream_t st) {
+  const int vek = pick_ve<KT>(H, {k, k_out, v_out});
+  const int vev = pick_ve<VT>(H, {v});
+  const int ve = vek < vev ? vek : vev;
+  UTTT_VE_SWITCH(
+      ve, hipLaunchKernelGGL((permute_kv_fwd_kernel<KT, VT, VE>), tok_grid(T, B), tok_block(), 0,
+                             st, reinterpret_cast<const typename KT::S*>(k),
+                             reinterpret_cast<const typename VT::S*>(v),
+                             reinterpret_cast<const uint8_t*>(lr0),
+                             reinterpret_cast<const uint8_t*>(lr1),
+                             reinterpret_cast<const uint8_t*>(lr2), lr_bytes, H, T, row_id_map, E,
+                             probs, p_sb, p_se, p_st, reinterpret_cast<typename KT::S*>(k_out),
+                             reinterpret_cast<typename KT::S*>(v_out),
+                             reinterpret_cast<uint8_t*>(lr0_out),
+                             reinterpret_cast<uint8_t*>(lr1_out),
+                             reinterpret_cast<uint8_t*>(lr2_out), num_out));
+  return check_launch("permute_kv_lrs_fwd");
+}
+
+template <class KT, class VT, class LT>
+int launch_permute_kv_bwd(const void* gk, const void* gv, const void* glr0, const void* glr1,
+                          const void* glr2, const void* v, const float* probs, int64_t p_sb,
+                          int64_t p_se, int64_t p_st, int B, int T, int H,
+                          const int32_t* row_id_map, int E, int num_out, void* grad_k,
+                          void* grad_v, void* grad_lr0, void* grad_lr1, void* grad_lr2,
+                          float* grad_probs, hipStream_t st) {
+  const int vek = pick_ve<KT>(H, {gk, gv, grad_k});
+  const int vev = pick_ve<VT>(H, {v, grad_v});
+  const int ve = vek < vev ? vek : vev;
+  using SL = typename LT::S;
+  UTTT_VE_SWITCH(
+      ve, hipLaunchKernelGGL((permute_kv_bwd_kernel<KT, VT, LT, VE>), tok_grid(T, B), tok_block(),
+                             0, st, reinterpret_cast<const typename KT::S*>(gk),
+                             reinterpret_cast<const typename KT::S*>(gv),
+                             reinterpret_cast<const SL*>(glr0), reinterpret_cast<const SL*>(glr1),
+                             reinterpret_cast<const SL*>(glr2),
+                             reinterpret_cast<const typename VT::S*>(v), probs, p_sb, p_se, p_st,
+                             H, T, row_id_map, E, num_out,
+                             reinterpret_cast<typename KT::S*>(grad_k),
+                             reinterpret_cast<typename VT::S*>(grad_v),
+                             reinterpret_cast<SL*>(grad_lr0), reinterpret_cast<SL*>(grad_lr1),
+                             reinterpret_cast<SL*>(grad_lr2), grad_probs));
+  return check_launch("permute_kv_lrs_bwd");
+}
+}  // namespace
+
+extern "C" int uttt_permute_kv_lrs_fwd(const void* k, int k_dtype, const void* v, int v_dtype,
+                                       const void* lr0, const void* lr1, const void* lr2,
+                                       int lr_bytes, int B, int T, int H,
+                                       const int32_t* row_id_map, int E, const float* probs,
+                                       int64_t p_sb, int64_t p_se, int64_t p_st, void* k_out,
+                                       void* v_out, void* lr0_out, void* lr1_out, void* lr2_out,
+                                       int num_out, void* stream) {
+  UTTT_REQUIRE(B >= 0 && T >= 0 && H >= 0 && E >= 1 && num_out >= 0,
+               "permute_kv_lrs_fwd: bad sizes");
+  UTTT_REQUIRE(lr_bytes == 2 || lr_bytes == 4, "permute_kv_lrs_fwd: lr element size %d", lr_bytes);
+  UTTT_REQUIRE(probs != nullptr, "permute_kv_lrs_fwd: probs are required");
+  if (B == 0 || T == 0) return UTTT_OK;
+  hipStream_t st = as_stream(stream);
+  UTTT_DTYPE_SWITCH(k_dtype, KT, {
+    UTTT_DTYPE_SWITCH(v_dtype, VT, {
+      return launch_permute_kv_fwd<KT, VT>(k, v, lr0, lr1, lr2, lr_bytes, B, T, H, row_id_map, E,
+                                           probs, p_sb, p_se, p_st, k_out, v_out, lr0_out,
+                                           lr1_out, lr2_out, num_out, st);
+    });
+  });
+  return UTTT_OK;
+}
+
+extern "C" int uttt_permute_kv_lrs_bwd(const void* gk, const void* gv, int k_dtype,
+                                       const void* glr0, const void* glr1, const void* glr2,
+                                       int glr_dtype, const void* v, int v_dtype,
+                                       const float* probs, int64_t p_sb, int64_t p_se,
+                                       int64_t p_st, int B, int T, int H,
+                                       const int32_t* row_id_map, int E, int num_out,
+                                       void* grad_k, void* grad_v, void* grad_lr0,
+                                       void* grad_lr1, void* grad_lr2, float* grad_probs,
+                                       void* stream) {
+  UTTT_REQUIRE(B >= 0 && T >= 0 && H >= 0 && E >= 1 && num_out >= 0,
+               "permute_kv_lrs_bwd: bad sizes");
+  UTTT_REQUIRE(probs != nullptr && grad_probs != nullptr, "permute_kv_lrs_bwd: probs required");
+  if (B == 0 || T == 0) return UTTT_OK;
+  hipStream_t st = as_stream(stream);
+  UTTT_DTYPE_SWITCH(k_dtype, KT, {
+    UTTT_DTYPE_SWITCH(v_dtype, VT, {
+      UTTT_DTYPE_SWITCH(glr_dtype, LT, {
+        return launch_permute_kv_bwd<KT, VT, LT>(gk, gv, glr0, glr1, glr2, v, probs, p_sb, p_se,
+                                                 p_st, B, T, H, row_id_map, E, num_out, grad_k,
+                                                 grad_v, grad_lr0, grad_lr1, grad_lr2, grad_probs,
+                                                 st);
+      });
+    });
+  });
+  return UTTT_OK;
+}
