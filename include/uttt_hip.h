@@ -140,6 +140,79 @@ int uttt_permute_kv_lrs_bwd(const void* gk, const void* gv, int k_dtype,
                             void* grad_lr1, void* grad_lr2, float* grad_probs,
                             void* stream);
 
+
+/* ------------------------------------------------------------------------ */
+/* Grouped SwiGLU fast-weight GEMMs (bf16 operands, fp32 accumulation)      */
+/* ------------------------------------------------------------------------ */
+/* Common contract: group_sizes [B, E] int32 on the device; the tokens of
+ * expert e in batch b are the contiguous segment that starts after the
+ * segments of experts < e (clamped to [0, N)).  Token columns past the last
+ * segment are never written.  I, D, M, K must be multiples of 8 and every
+ * tensor 16-byte aligned.  "token-major" intermediates are [B, N, rows]
+ * (rows contiguous); the reference's layout is [B, rows, N]. */
+
+/* APPLY, first GEMM pair.  Replaces fused_two_mm_swiglu_triton
+ * (L/triton_grouped_swiglu_kernels.py:273-338; kernel :83-270).
+ * w0_w2 [B, E, 2I, D] bf16, x [B, N, D] bf16 ->
+ * hidden = silu(w0 x^T) * (w2 x^T) in bf16: [B, I, N] (token_major = 0, the
+ * reference layout) or [B, N, I] (token_major = 1). */
+int uttt_grouped_gate_up(const void* w0_w2, const void* x, const int32_t* group_sizes, int B,
+                         int E, int I, int D, int N, void* hidden, int token_major,
+                         void* stream);
+
+/* APPLY, down projection (and every "W times token rows" product).
+ * Replaces grouped_gemm_transpose_triton (L/triton_grouped_gemm.py:170-243;
+ * kernel :50-167) with its X operand token-major: w [B, E, M, K] bf16,
+ * x [B, N, K] bf16 -> y [B, N, M] bf16, y[b, n] = w[b, e(n)] x[b, n]. */
+int uttt_grouped_gemm_nt(const void* w, const void* x, const int32_t* group_sizes, int B, int E,
+                         int M, int K, int N, void* y, void* stream);
+
+/* Transposed-weight variant: w [B, E, K, M] (the product with w^T), e.g. the
+ * APPLY backward's grad_X = W0_W2^T DY, which the reference computes as
+ * grouped_gemm_transpose_triton(W0_W2.transpose(2, 3).contiguous(), DY0_DY2)
+ * (L/lact_swiglu_ffn.py:94-96): x [B, N, K] -> y [B, N, M],
+ * y[b, n] = w[b, e(n)]^T x[b, n]. */
+int uttt_grouped_gemm_tn(const void* w, const void* x, const int32_t* group_sizes, int B, int E,
+                         int M, int K, int N, void* y, void* stream);
+
+/* UPDATE, stage 1.  Replaces swiglu_backward_three_bmm_grouped_with_lr_triton
+ * (L/triton_grouped_swiglu_bwd_with_lr_kernels.py:255-353; kernel :49-252).
+ * w0_w2 [B,E,2I,D], w1 [B,E,D,I], k, v [B,N,D] (bf16); lr0/1/2 [B,N] of
+ * lr_dtype (UTTT_F32/BF16/F16, widened to fp32) ->
+ * dy0_dy2 ([B,2I,N] or token-major [B,N,2I]) and hidden ([B,I,N] or
+ * [B,N,I]), bf16:
+ *   Y0 = w0 k, Y2 = w2 k, DH = w1^T v;
+ *   DY0 = lr0 sig(Y0) Y2 DH (1 + Y0 (1 - sig(Y0))), DY2 = lr2 silu(Y0) DH,
+ *   hidden = lr1 silu(Y0) Y2.
+ * lr0 = lr1 = lr2 = NULL means lr = 1: the APPLY backward's three-GEMM pass
+ * (swiglu_backward_three_bmm_grouped_triton,
+ * L/triton_grouped_swiglu_bwd_kernels.py:49-320, with v = grad_out). */
+int uttt_grouped_update_stage1(const void* w0_w2, const void* w1, const void* k, const void* v,
+                               const void* lr0, const void* lr1, const void* lr2, int lr_dtype,
+                               const int32_t* group_sizes, int B, int E, int I, int D, int N,
+                               void* dy0_dy2, void* hidden, int token_major, void* stream);
+
+/* UPDATE, stage 2 (weight gradients).  Replaces grouped_two_gemm_fw_bwd_triton
+ * (L/triton_lact_bwd_grouped_two_mm_grad_fw.py:231-312; kernel :55-225) with
+ * token-major intermediates: dy0_dy2_tok [B,N,2I], hidden_tok [B,N,I],
+ * k, v [B,N,D] (bf16) -> dw0_w2 [B,E,2I,D] = DY[seg]^T K[seg] and
+ * dw1 [B,E,D,I] = V[seg]^T Hid[seg], bf16; an empty expert gets zeros. */
+int uttt_grouped_wgrad_pair(const void* dy0_dy2_tok, const void* k, const void* hidden_tok,
+                            const void* v, const int32_t* group_sizes, int B, int E, int I,
+                            int D, int N, void* dw0_w2, void* dw1, void* stream);
+
+/* One weight-gradient product.  Replaces grouped_gemm_bwd_triton
+ * (L/triton_grouped_gemm.py:349-404; kernel :251-346) with token-major
+ * operands: a_tok [B,N,R], b_tok [B,N,C] (bf16) ->
+ * out[b,e] = A[seg]^T B[seg], [B,E,R,C] (transposed = 0) or [B,E,C,R]
+ * (transposed = 1), bf16; an empty expert gets zeros. */
+int uttt_grouped_wgrad(const void* a_tok, const void* b_tok, const int32_t* group_sizes, int B,
+                       int E, int R, int C, int N, void* out, int transposed, void* stream);
+
+/* Layout helper (no reference counterpart; used to accept the reference's
+ * [B, rows, N] intermediates): out[b, c, r] = in[b, r, c], 2-byte elements. */
+int uttt_transpose_2byte(const void* in, int B, int R, int C, void* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

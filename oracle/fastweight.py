@@ -1,0 +1,160 @@
+"""Oracle of the grouped SwiGLU fast-weight ops (checker only; see
+oracle/__init__.py).  fp32 torch on the CPU, with the reference's bf16
+rounding points.
+
+Reference: uttt_llm/flame/custom_models/uttt_moe/lact_moe_triton/ (L/):
+  two_mm_swiglu      triton_grouped_swiglu_kernels.py:204-270  (cited S:)
+  gemm_transpose     triton_grouped_gemm.py:118-167            (cited G:)
+  swiglu_ffn_fwd     lact_swiglu_ffn.py:37-61                  (cited F:)
+  three_bmm_with_lr  triton_grouped_swiglu_bwd_with_lr_kernels.py:174-252 (cited U1:)
+  two_gemm_fw_bwd    triton_lact_bwd_grouped_two_mm_grad_fw.py:117-225    (cited U2:)
+  fast_weight_grads  lact_fw_grad.py:54-114                    (cited FG:)
+
+Every GEMM takes bf16 operands, accumulates in fp32 (the oracle uses fp64
+products summed in fp64, then rounds to fp32: a tighter statement of "fp32
+accumulate" than any fixed order) and rounds the stored result to bf16 where
+the reference stores bf16.  Columns of a batch beyond sum(group_sizes) are
+never written by the reference (outputs come from torch.empty); the oracle
+leaves them zero and the tests compare only written columns.
+
+`exact=True` switches every bf16 rounding off (fp64 throughout): the
+autograd and finite-difference checks in tests/test_oracle_fastweight.py use
+it to pin the formulas themselves.
+"""
+from __future__ import annotations
+
+import torch
+
+
+def _r(x, exact):
+    """Store point: bf16 in the reference, identity in exact mode."""
+    return x if exact else x.to(torch.bfloat16)
+
+
+def _f(x, exact):
+    return x.double() if exact else x.float().double()
+
+
+def segments(group_sizes_row):
+    """[(e, start, size)] of one batch: expert e owns [start, start+size)."""
+    out, s = [], 0
+    for e, g in enumerate(group_sizes_row.tolist()):
+        out.append((e, s, int(g)))
+        s += int(g)
+    return out
+
+
+def two_mm_swiglu(W0_W2, X, group_sizes, exact=False):
+    """S:204-270.  Hidden[b, :, seg_e] = silu(w0 X_e^T) * (w2 X_e^T), bf16 [B, I, N]."""
+    B, E, I2, D = W0_W2.shape
+    I = I2 // 2
+    N = X.shape[1]
+    out = torch.zeros(B, I, N, dtype=torch.float64)
+    for b in range(B):
+        for e, s, g in segments(group_sizes[b]):
+            if g == 0:
+                continue
+            w = _f(W0_W2[b, e], exact)
+            x = _f(X[b, s:s + g], exact)
+            y0 = (w[:I] @ x.T)
+            y2 = (w[I:] @ x.T)
+            if not exact:
+                y0, y2 = y0.float().double(), y2.float().double()
+            out[b, :, s:s + g] = y2 * (y0 * torch.sigmoid(y0))
+    return _r(out, exact)
+
+
+def gemm_transpose(W, X, group_sizes, exact=False):
+    """G:118-167.  Y[b, seg_e, :] = (W[b,e] @ X[b, :, seg_e])^T, bf16 [B, N, M]."""
+    B, E, M, K = W.shape
+    N = X.shape[2]
+    out = torch.zeros(B, N, M, dtype=torch.float64)
+    for b in range(B):
+        for e, s, g in segments(group_sizes[b]):
+            if g == 0:
+                continue
+            out[b, s:s + g] = (_f(W[b, e], exact) @ _f(X[b, :, s:s + g], exact)).T
+    return _r(out, exact)
+
+
+def swiglu_ffn_fwd(W0_W2, W1, X, group_sizes, exact=False):
+    """F:37-61: the APPLY op.  Hidden is stored bf16 between the two GEMMs."""
+    H = two_mm_swiglu(W0_W2, X, group_sizes, exact)
+    return gemm_transpose(W1, H, group_sizes, exact)
+
+
+def three_bmm_with_lr(W0_W2, W1, K, V, lr0, lr1, lr2, group_sizes, exact=False):
+    """U1:174-252.  Returns DY0_DY2 [B, 2I, N] and Hidden [B, I, N] (bf16):
+      Y0 = w0 K^T, Y2 = w2 K^T, DH = w1^T V^T   (fp32 accumulate)
+      DY0 = lr0 * sig*Y2*DH*(1 + Y0(1-sig)); DY2 = lr2 * silu(Y0)*DH;
+      Hidden = lr1 * silu(Y0)*Y2     (lr loaded as stored, widened to fp32)."""
+    B, E, I2, D = W0_W2.shape
+    I = I2 // 2
+    N = K.shape[1]
+    dy = torch.zeros(B, I2, N, dtype=torch.float64)
+    hid = torch.zeros(B, I, N, dtype=torch.float64)
+    l0, l1, l2 = (_f(x.reshape(B, N), True) for x in (lr0, lr1, lr2))
+    for b in range(B):
+        for e, s, g in segments(group_sizes[b]):
+            if g == 0:
+                continue
+            w = _f(W0_W2[b, e], exact)
+            k = _f(K[b, s:s + g], exact)
+            v = _f(V[b, s:s + g], exact)
+            y0 = w[:I] @ k.T
+            y2 = w[I:] @ k.T
+            dh = _f(W1[b, e], exact).T @ v.T
+            if not exact:
+                y0, y2, dh = (t.float().double() for t in (y0, y2, dh))
+            sig = torch.sigmoid(y0)
+            sw = sig * y0
+            dy[b, :I, s:s + g] = sig * y2 * dh * (1.0 + y0 * (1.0 - sig)) * l0[b, s:s + g]
+            dy[b, I:, s:s + g] = sw * dh * l2[b, s:s + g]
+            hid[b, :, s:s + g] = sw * y2 * l1[b, s:s + g]
+    return _r(dy, exact), _r(hid, exact)
+
+
+def two_gemm_fw_bwd(DY0_DY2, K, Hidden, V, group_sizes, exact=False):
+    """U2:117-225.  dW0_W2[b,e] = DY0_DY2[:, seg] @ K[seg] ([B,E,2I,D]);
+    dW1[b,e] = (Hidden[:, seg] @ V[seg])^T ([B,E,D,I]); bf16; an empty expert
+    gets zeros."""
+    B, I2, N = DY0_DY2.shape
+    I = I2 // 2
+    D = K.shape[2]
+    E = group_sizes.shape[1]
+    dw02 = torch.zeros(B, E, I2, D, dtype=torch.float64)
+    dw1 = torch.zeros(B, E, D, I, dtype=torch.float64)
+    for b in range(B):
+        for e, s, g in segments(group_sizes[b]):
+            if g == 0:
+                continue
+            dw02[b, e] = _f(DY0_DY2[b, :, s:s + g], exact) @ _f(K[b, s:s + g], exact)
+            dw1[b, e] = (_f(Hidden[b, :, s:s + g], exact) @ _f(V[b, s:s + g], exact)).T
+    return _r(dw02, exact), _r(dw1, exact)
+
+
+def fast_weight_grads(W0_W2, W1, K, V, lr0, lr1, lr2, group_sizes, exact=False):
+    """FG:54-114: the UPDATE op = U1 then U2 (DY0_DY2 and Hidden stored bf16)."""
+    dy, hid = three_bmm_with_lr(W0_W2, W1, K, V, lr0, lr1, lr2, group_sizes, exact)
+    return two_gemm_fw_bwd(dy, K, hid, V, group_sizes, exact)
+
+
+def written_columns(group_sizes, N):
+    """[B, N] bool: token columns some expert segment covers."""
+    B = group_sizes.shape[0]
+    tot = group_sizes.sum(1)
+    return torch.arange(N).unsqueeze(0) < tot.unsqueeze(1)
+
+
+def swiglu_ffn_bwd(W0_W2, W1, X, grad_out, group_sizes, exact=False):
+    """F:63-104: backward of the APPLY op.
+      DY0_DY2, Hidden = three-GEMM pass with lr = 1 and V = grad_out (bf16),
+      grad_W0_W2, grad_W1 = two_gemm_fw_bwd(DY0_DY2, X, Hidden, grad_out),
+      grad_X[seg] = (W0_W2^T DY0_DY2[:, seg])^T   (bf16).
+    Returns (grad_W0_W2, grad_W1, grad_X)."""
+    B, N = X.shape[0], X.shape[1]
+    ones = torch.ones(B, N)
+    dy, hid = three_bmm_with_lr(W0_W2, W1, X, grad_out, ones, ones, ones, group_sizes, exact)
+    gw02, gw1 = two_gemm_fw_bwd(dy, X, hid, grad_out, group_sizes, exact)
+    gx = gemm_transpose(W0_W2.transpose(2, 3), dy, group_sizes, exact)
+    return gw02, gw1, gx

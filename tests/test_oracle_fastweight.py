@@ -1,0 +1,157 @@
+"""Pins the grouped fast-weight oracle (oracle/fastweight.py) on the CPU.
+
+Each check is chosen so a plausible slip fails it:
+  - E=1 grouped ops equal one dense batched matmul of the whole token set
+    (a wrong segment offset or a transposed operand breaks it);
+  - in exact mode the UPDATE equals torch.autograd's gradient of the
+    lr-weighted dot-product loss sum_n lr_j[n] <f(k_n), v_n> for each of the
+    three matrices (a dropped SiLU' term, a wrong sign or a swapped lr fails);
+  - a central finite difference of the same loss agrees with one dW entry;
+  - an empty expert yields zero weight gradients and leaves its neighbours'
+    segments unchanged (segment bookkeeping);
+  - the APPLY equals W1 (silu(W0 x) * (W2 x)) built from torch.nn.functional.
+"""
+import torch
+import torch.nn.functional as F
+
+from oracle import fastweight as FW
+
+
+def _inputs(B, E, D, I, gs, seed=0, dtype=torch.bfloat16):
+    g = torch.Generator().manual_seed(seed)
+    N = int(max(sum(r) for r in gs))
+    W02 = (torch.randn(B, E, 2 * I, D, generator=g) / D ** 0.5).to(dtype)
+    W1 = (torch.randn(B, E, D, I, generator=g) / I ** 0.5).to(dtype)
+    K = torch.randn(B, N, D, generator=g).to(dtype)
+    V = torch.randn(B, N, D, generator=g).to(dtype)
+    lr = [torch.sigmoid(torch.randn(B, N, generator=g)) * 0.1 for _ in range(3)]
+    return W02, W1, K, V, lr, torch.tensor(gs, dtype=torch.int32)
+
+
+def _f(t):
+    return t.double()
+
+
+def test_apply_e1_equals_dense_formula():
+    W02, W1, X, _, _, gs = _inputs(2, 1, 24, 40, [[37], [37]])
+    out = FW.swiglu_ffn_fwd(W02, W1, X, gs, exact=True)
+    I = 40
+    w0, w2, w1, x = _f(W02[:, 0, :I]), _f(W02[:, 0, I:]), _f(W1[:, 0]), _f(X)
+    h = F.silu(torch.bmm(x, w0.transpose(1, 2))) * torch.bmm(x, w2.transpose(1, 2))
+    ref = torch.bmm(h, w1.transpose(1, 2))
+    assert torch.allclose(out, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_apply_grouped_equals_per_expert_dense():
+    gs = [[5, 0, 17, 9], [1, 30, 0, 0]]
+    W02, W1, X, _, _, gsz = _inputs(2, 4, 16, 24, gs, seed=1)
+    out = FW.swiglu_ffn_fwd(W02, W1, X, gsz, exact=True)
+    I = 24
+    for b in range(2):
+        s = 0
+        for e, g in enumerate(gs[b]):
+            x = _f(X[b, s:s + g])
+            h = F.silu(x @ _f(W02[b, e, :I]).T) * (x @ _f(W02[b, e, I:]).T)
+            assert torch.allclose(out[b, s:s + g], h @ _f(W1[b, e]).T, rtol=1e-12, atol=1e-12)
+            s += g
+
+
+def _loss_grads(W02, W1, K, V, lr, gs, b, e):
+    """Autograd of sum_n lr_j[n] <f(k_n), v_n> over expert e's segment."""
+    I = W02.shape[2] // 2
+    s = int(gs[b, :e].sum())
+    g = int(gs[b, e])
+    k, v = _f(K[b, s:s + g]), _f(V[b, s:s + g])
+    grads = []
+    for j, wname in ((0, "w0"), (1, "w1"), (2, "w2")):
+        w0 = _f(W02[b, e, :I]).clone().requires_grad_(wname == "w0")
+        w2 = _f(W02[b, e, I:]).clone().requires_grad_(wname == "w2")
+        w1 = _f(W1[b, e]).clone().requires_grad_(wname == "w1")
+        f = (F.silu(k @ w0.T) * (k @ w2.T)) @ w1.T          # [g, D]
+        loss = (lr[j][b, s:s + g].double() * (f * v).sum(-1)).sum()
+        loss.backward()
+        grads.append({"w0": w0, "w1": w1, "w2": w2}[wname].grad)
+    return grads  # dW0 (lr0), dW1 (lr1), dW2 (lr2)
+
+
+def test_update_is_gradient_of_dot_product_loss():
+    gs = [[6, 0, 11], [3, 9, 5]]
+    W02, W1, K, V, lr, gsz = _inputs(2, 3, 12, 20, gs, seed=2)
+    dw02, dw1 = FW.fast_weight_grads(W02, W1, K, V, *lr, gsz, exact=True)
+    I = 20
+    for b in range(2):
+        for e in range(3):
+            if gs[b][e] == 0:
+                assert torch.count_nonzero(dw02[b, e]) == 0 and torch.count_nonzero(dw1[b, e]) == 0
+                continue
+            g0, g1, g2 = _loss_grads(W02, W1, K, V, lr, gsz, b, e)
+            assert torch.allclose(dw02[b, e, :I], g0, rtol=1e-10, atol=1e-12)
+            assert torch.allclose(dw02[b, e, I:], g2, rtol=1e-10, atol=1e-12)
+            assert torch.allclose(dw1[b, e], g1, rtol=1e-10, atol=1e-12)
+
+
+def test_update_finite_difference():
+    gs = [[7, 4]]
+    W02, W1, K, V, lr, gsz = _inputs(1, 2, 8, 10, gs, seed=3)
+    dw02, dw1 = FW.fast_weight_grads(W02, W1, K, V, *lr, gsz, exact=True)
+    I, e, s, g = 10, 1, 7, 4
+    k, v = _f(K[0, s:s + g]), _f(V[0, s:s + g])
+
+    def loss(w0, w2, w1, lrv):
+        f = (F.silu(k @ w0.T) * (k @ w2.T)) @ w1.T
+        return (lrv * (f * v).sum(-1)).sum()
+
+    w0, w2, w1 = _f(W02[0, e, :I]), _f(W02[0, e, I:]), _f(W1[0, e])
+    h = 1e-6
+    for (mat, i, j) in (("w0", 3, 5), ("w2", 7, 1), ("w1", 2, 9)):
+        lrv = lr[{"w0": 0, "w1": 1, "w2": 2}[mat]][0, s:s + g].double()
+        args = {"w0": w0.clone(), "w2": w2.clone(), "w1": w1.clone()}
+        args[mat][i, j] += h
+        lp = loss(args["w0"], args["w2"], args["w1"], lrv)
+        args[mat][i, j] -= 2 * h
+        lm = loss(args["w0"], args["w2"], args["w1"], lrv)
+        fd = (lp - lm) / (2 * h)
+        ana = {"w0": lambda: dw02[0, e, i, j], "w2": lambda: dw02[0, e, I + i, j],
+               "w1": lambda: dw1[0, e, i, j]}[mat]()
+        assert abs(fd - ana) < 1e-6 * max(1.0, abs(fd)), (mat, fd, ana)
+
+
+def test_empty_expert_and_segment_independence():
+    # removing an empty expert's slot must not change anyone else's result
+    W02, W1, K, V, lr, gsz = _inputs(1, 3, 8, 12, [[5, 0, 6]], seed=4)
+    a02, a1 = FW.fast_weight_grads(W02, W1, K, V, *lr, gsz)
+    b02, b1 = FW.fast_weight_grads(W02[:, [0, 2]], W1[:, [0, 2]], K, V, *lr,
+                                   torch.tensor([[5, 6]], dtype=torch.int32))
+    assert torch.equal(a02[:, [0, 2]], b02) and torch.equal(a1[:, [0, 2]], b1)
+    assert torch.count_nonzero(a02[0, 1]) == 0 and torch.count_nonzero(a1[0, 1]) == 0
+
+
+def test_bf16_rounding_points_are_close_to_exact():
+    # the rounded pipeline stays within the bf16 bar of the exact one
+    W02, W1, K, V, lr, gsz = _inputs(1, 2, 64, 96, [[40, 24]], seed=5)
+    r02, r1 = FW.fast_weight_grads(W02, W1, K, V, *lr, gsz)
+    e02, e1 = FW.fast_weight_grads(W02, W1, K, V, *lr, gsz, exact=True)
+    for r, e in ((r02, e02), (r1, e1)):
+        err = (r.double() - e).abs().max()
+        assert err <= 2e-2 * e.abs().max()
+
+
+def test_apply_backward_is_autograd_of_apply():
+    gs = [[9, 0, 14], [4, 4, 4]]
+    W02, W1, X, G, _, gsz = _inputs(2, 3, 16, 20, gs, seed=6)
+    gw02, gw1, gx = FW.swiglu_ffn_bwd(W02, W1, X, G, gsz, exact=True)
+    I = 20
+    for b in range(2):
+        s = 0
+        for e, g in enumerate(gs[b]):
+            w0 = _f(W02[b, e, :I]).requires_grad_()
+            w2 = _f(W02[b, e, I:]).requires_grad_()
+            w1 = _f(W1[b, e]).requires_grad_()
+            x = _f(X[b, s:s + g]).requires_grad_()
+            f = (F.silu(x @ w0.T) * (x @ w2.T)) @ w1.T
+            (f * _f(G[b, s:s + g])).sum().backward()
+            assert torch.allclose(gw02[b, e, :I], w0.grad, rtol=1e-10, atol=1e-12)
+            assert torch.allclose(gw02[b, e, I:], w2.grad, rtol=1e-10, atol=1e-12)
+            assert torch.allclose(gw1[b, e], w1.grad, rtol=1e-10, atol=1e-12)
+            assert torch.allclose(gx[b, s:s + g], x.grad, rtol=1e-10, atol=1e-12)
+            s += g

@@ -59,6 +59,27 @@ SIGNATURES = {
         [c_p, c_p, c_int, c_p, c_p, c_p, c_int, c_p, c_int, c_p, c_i64, c_i64, c_i64, c_int,
          c_int, c_int, c_p, c_int, c_int, c_p, c_p, c_p, c_p, c_p, c_p, c_p],
     ),
+    "uttt_grouped_gate_up": (
+        c_int, [c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int, c_p, c_int, c_p],
+    ),
+    "uttt_grouped_gemm_nt": (
+        c_int, [c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int, c_p, c_p],
+    ),
+    "uttt_grouped_gemm_tn": (
+        c_int, [c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int, c_p, c_p],
+    ),
+    "uttt_grouped_update_stage1": (
+        c_int,
+        [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_int, c_p, c_int, c_int, c_int, c_int, c_int,
+         c_p, c_p, c_int, c_p],
+    ),
+    "uttt_grouped_wgrad_pair": (
+        c_int, [c_p, c_p, c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int, c_p, c_p, c_p],
+    ),
+    "uttt_grouped_wgrad": (
+        c_int, [c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int, c_p, c_int, c_p],
+    ),
+    "uttt_transpose_2byte": (c_int, [c_p, c_int, c_int, c_int, c_p, c_p]),
 }
 
 _lib = None

@@ -78,6 +78,15 @@ struct F16T {
   __device__ __forceinline__ static S store(float f) { return f32_to_f16(f); }
 };
 
+// Dispatch on a float dtype code: binds TT to the element traits.
+#define UTTT_DTYPE_SWITCH_LR(dt, TT, ...)                                           \
+  switch (dt) {                                                                     \
+    case UTTT_F32: { using TT = ::uttt::F32T; __VA_ARGS__; } break;                 \
+    case UTTT_BF16: { using TT = ::uttt::BF16T; __VA_ARGS__; } break;               \
+    case UTTT_F16: { using TT = ::uttt::F16T; __VA_ARGS__; } break;                 \
+    default: ::uttt::set_error("unsupported dtype code %d", (int)(dt)); return UTTT_ERR_ARG; \
+  }
+
 // ------------------------------------------------------------------ wave ----
 constexpr int kWave = 64;
 

@@ -1,0 +1,154 @@
+"""Launch helpers shared by the grouped fast-weight modules: thin wrappers
+over the C-ABI of csrc/grouped_gemm.hip that allocate outputs with torch and
+launch on torch's current stream.  No CPU path: CPU tensors raise.
+
+Token-major intermediates ("_tok" suffix) are [B, N, rows] with rows
+contiguous; the reference's kernel-level functions exchange [B, rows, N].
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _lib as L
+
+
+def _check_bf16(*ts):
+    for t in ts:
+        assert t.dtype == torch.bfloat16, f"expected bf16, got {t.dtype}"
+        assert t.is_contiguous(), "expected a contiguous tensor"
+
+
+def group_sizes_i32(group_sizes: torch.Tensor) -> torch.Tensor:
+    gs = group_sizes if group_sizes.dtype == torch.int32 else group_sizes.to(torch.int32)
+    return gs.contiguous()
+
+
+def gate_up(W0_W2, X, group_sizes, token_major: bool):
+    """silu(w0 x) * (w2 x) per routed token: [B, N, I] (token_major) or [B, I, N]."""
+    L.require_device(W0_W2, X, group_sizes)
+    _check_bf16(W0_W2, X)
+    B, E, I2, D = W0_W2.shape
+    Bx, N, Dx = X.shape
+    assert Bx == B and Dx == D, "X must be [B, N, D] with matching B, D"
+    assert I2 % 2 == 0
+    I = I2 // 2
+    gs = group_sizes_i32(group_sizes)
+    assert gs.shape == (B, E)
+    shape = (B, N, I) if token_major else (B, I, N)
+    H = torch.empty(shape, dtype=torch.bfloat16, device=X.device)
+    L.call("uttt_grouped_gate_up", L.ptr(W0_W2), L.ptr(X), L.ptr(gs), B, E, I, D, N, L.ptr(H),
+           int(token_major), L.stream_of(X))
+    return H
+
+
+def gemm_nt(W, X_tok, group_sizes):
+    """Y[b, n] = W[b, e(n)] @ X_tok[b, n]: W [B, E, M, K], X_tok [B, N, K] -> [B, N, M]."""
+    L.require_device(W, X_tok, group_sizes)
+    _check_bf16(W, X_tok)
+    B, E, M, K = W.shape
+    Bx, N, Kx = X_tok.shape
+    assert Bx == B and Kx == K, "X must be [B, N, K] with matching B, K"
+    gs = group_sizes_i32(group_sizes)
+    assert gs.shape == (B, E)
+    Y = torch.empty((B, N, M), dtype=torch.bfloat16, device=X_tok.device)
+    L.call("uttt_grouped_gemm_nt", L.ptr(W), L.ptr(X_tok), L.ptr(gs), B, E, M, K, N, L.ptr(Y),
+           L.stream_of(X_tok))
+    return Y
+
+
+def gemm_tn(W, X_tok, group_sizes):
+    """Y[b, n] = W[b, e(n)]^T @ X_tok[b, n]: W [B, E, K, M], X_tok [B, N, K] -> [B, N, M]."""
+    L.require_device(W, X_tok, group_sizes)
+    _check_bf16(W, X_tok)
+    B, E, K, M = W.shape
+    Bx, N, Kx = X_tok.shape
+    assert Bx == B and Kx == K, "X must be [B, N, K] with matching B, K"
+    gs = group_sizes_i32(group_sizes)
+    assert gs.shape == (B, E)
+    Y = torch.empty((B, N, M), dtype=torch.bfloat16, device=X_tok.device)
+    L.call("uttt_grouped_gemm_tn", L.ptr(W), L.ptr(X_tok), L.ptr(gs), B, E, M, K, N, L.ptr(Y),
+           L.stream_of(X_tok))
+    return Y
+
+
+def update_stage1(W0_W2, W1, K, V, lr0, lr1, lr2, group_sizes, token_major: bool):
+    """(DY0_DY2, Hidden) of the UPDATE, token-major ([B,N,2I], [B,N,I]) or the
+    reference layout ([B,2I,N], [B,I,N]).  lr0 = lr1 = lr2 = None means lr = 1
+    (the APPLY backward's pass with V = grad_out)."""
+    L.require_device(W0_W2, W1, K, V, lr0, lr1, lr2, group_sizes)
+    _check_bf16(W0_W2, W1, K, V)
+    B, E, I2, D = W0_W2.shape
+    I = I2 // 2
+    N = K.shape[1]
+    assert K.shape == (B, N, D) and V.shape == (B, N, D)
+    assert W1.shape == (B, E, D, I)
+    lrs = []
+    if lr0 is None:
+        assert lr1 is None and lr2 is None
+        lrs = [None, None, None]
+        lr_code = L.F32
+    else:
+        for lr in (lr0, lr1, lr2):
+            lr = lr.reshape(B, N) if lr.numel() == B * N else lr
+            assert lr.shape == (B, N), f"lr must be [B, N], got {tuple(lr.shape)}"
+            lrs.append(lr.contiguous())
+        assert lrs[0].dtype == lrs[1].dtype == lrs[2].dtype
+        lr_code = L.dtype_code(lrs[0].dtype)
+    gs = group_sizes_i32(group_sizes)
+    assert gs.shape == (B, E)
+    dev = K.device
+    if token_major:
+        DY = torch.empty((B, N, I2), dtype=torch.bfloat16, device=dev)
+        H = torch.empty((B, N, I), dtype=torch.bfloat16, device=dev)
+    else:
+        DY = torch.empty((B, I2, N), dtype=torch.bfloat16, device=dev)
+        H = torch.empty((B, I, N), dtype=torch.bfloat16, device=dev)
+    L.call("uttt_grouped_update_stage1", L.ptr(W0_W2), L.ptr(W1), L.ptr(K), L.ptr(V),
+           L.ptr(lrs[0]), L.ptr(lrs[1]), L.ptr(lrs[2]), lr_code, L.ptr(gs),
+           B, E, I, D, N, L.ptr(DY), L.ptr(H), int(token_major), L.stream_of(K))
+    return DY, H
+
+
+def wgrad_pair(DY_tok, K, H_tok, V, group_sizes):
+    """dW0_W2 [B,E,2I,D] = DY[seg]^T K[seg]; dW1 [B,E,D,I] = V[seg]^T H[seg]."""
+    L.require_device(DY_tok, K, H_tok, V, group_sizes)
+    _check_bf16(DY_tok, K, H_tok, V)
+    B, N, I2 = DY_tok.shape
+    I = I2 // 2
+    D = K.shape[2]
+    assert K.shape == (B, N, D) and V.shape == (B, N, D) and H_tok.shape == (B, N, I)
+    gs = group_sizes_i32(group_sizes)
+    E = gs.shape[1]
+    dev = K.device
+    dW02 = torch.empty((B, E, I2, D), dtype=torch.bfloat16, device=dev)
+    dW1 = torch.empty((B, E, D, I), dtype=torch.bfloat16, device=dev)
+    L.call("uttt_grouped_wgrad_pair", L.ptr(DY_tok), L.ptr(K), L.ptr(H_tok), L.ptr(V), L.ptr(gs),
+           B, E, I, D, N, L.ptr(dW02), L.ptr(dW1), L.stream_of(K))
+    return dW02, dW1
+
+
+def wgrad(A_tok, B_tok, group_sizes, transposed: bool):
+    """out[b,e] = A[seg]^T B[seg] as [B,E,R,C] (or [B,E,C,R] when transposed)."""
+    L.require_device(A_tok, B_tok, group_sizes)
+    _check_bf16(A_tok, B_tok)
+    B, N, R = A_tok.shape
+    C = B_tok.shape[2]
+    assert B_tok.shape[:2] == (B, N)
+    gs = group_sizes_i32(group_sizes)
+    E = gs.shape[1]
+    shape = (B, E, C, R) if transposed else (B, E, R, C)
+    out = torch.empty(shape, dtype=torch.bfloat16, device=A_tok.device)
+    L.call("uttt_grouped_wgrad", L.ptr(A_tok), L.ptr(B_tok), L.ptr(gs), B, E, R, C, N,
+           L.ptr(out), int(transposed), L.stream_of(A_tok))
+    return out
+
+
+def transpose_last2(X):
+    """[B, R, C] -> [B, C, R] (2-byte elements) on the GPU."""
+    L.require_device(X)
+    assert X.element_size() == 2
+    X = X.contiguous()
+    B, R, C = X.shape
+    out = torch.empty((B, C, R), dtype=X.dtype, device=X.device)
+    L.call("uttt_transpose_2byte", L.ptr(X), B, R, C, L.ptr(out), L.stream_of(X))
+    return out
