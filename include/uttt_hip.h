@@ -209,6 +209,28 @@ int uttt_grouped_wgrad_pair(const void* dy0_dy2_tok, const void* k, const void* 
 int uttt_grouped_wgrad(const void* a_tok, const void* b_tok, const int32_t* group_sizes, int B,
                        int E, int R, int C, int N, void* out, int transposed, void* stream);
 
+/* Scratch bytes for uttt_grouped_update_bwd at (B, I, N). */
+size_t uttt_update_bwd_workspace_bytes(int B, int I, int N);
+
+/* UPDATE backward.  Replaces FusedLactSwiGLUFFNBwd.backward
+ * (L/lact_fw_grad.py:116-300): grouping_four_grouped_gemm_triton
+ * (L/triton_lact_bwd_grouped_four_mm.py:300-439),
+ * ref_pytorch_swiglu_bwd_bwd_fused_cat_inp_out (L/triton_pointwise_kernels.py:354-436),
+ * fused_grouped_grad_kv (L/triton_lact_bwd_grouped_grad_kv.py:227-340) and
+ * grouped_two_gemm_fw_bwd_triton, as five launches with no host sync.
+ * Inputs: the forward's w0_w2, w1, k, v, lr0/1/2 (lr_dtype), group_sizes and
+ * the upstream gradients grad_dw0_w2 [B,E,2I,D], grad_dw1 [B,E,D,I] (bf16).
+ * Outputs: grad_w0_w2 [B,E,2I,D], grad_w1 [B,E,D,I], grad_k, grad_v [B,N,D]
+ * (bf16), grad_lr0/1/2 [B,N] (lr_dtype; zero past the routed tokens).
+ * workspace: uttt_update_bwd_workspace_bytes(B, I, N) bytes. */
+int uttt_grouped_update_bwd(const void* w0_w2, const void* w1, const void* k, const void* v,
+                            const void* lr0, const void* lr1, const void* lr2, int lr_dtype,
+                            const int32_t* group_sizes, const void* grad_dw0_w2,
+                            const void* grad_dw1, int B, int E, int I, int D, int N,
+                            void* grad_w0_w2, void* grad_w1, void* grad_k, void* grad_v,
+                            void* grad_lr0, void* grad_lr1, void* grad_lr2, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
 /* Layout helper (no reference counterpart; used to accept the reference's
  * [B, rows, N] intermediates): out[b, c, r] = in[b, r, c], 2-byte elements. */
 int uttt_transpose_2byte(const void* in, int B, int R, int C, void* out, void* stream);

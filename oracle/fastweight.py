@@ -158,3 +158,78 @@ def swiglu_ffn_bwd(W0_W2, W1, X, grad_out, group_sizes, exact=False):
     gw02, gw1 = two_gemm_fw_bwd(dy, X, hid, grad_out, group_sizes, exact)
     gx = gemm_transpose(W0_W2.transpose(2, 3), dy, group_sizes, exact)
     return gw02, gw1, gx
+
+
+def fast_weight_grads_bwd(W0_W2, W1, K, V, lr0, lr1, lr2, group_sizes, G_W0_W2, G_W1,
+                          exact=False):
+    """FG:116-300: backward of the UPDATE op given the upstream gradients
+    G_W0_W2 [B,E,2I,D] and G_W1 [B,E,D,I].  Rounding points as the reference:
+      four GEMMs (L/triton_lact_bwd_grouped_four_mm.py:30-297) store bf16
+        Y0_Y2 = W0_W2 K^T, GY = G_W0_W2 K^T, DH = W1^T V^T, GDH = G_W1^T V^T;
+      the pointwise pass (L/triton_pointwise_kernels.py:354-436) computes in
+        fp32 from those bf16 values and stores grad_dh, grad_x0_x2, dx0_x2,
+        hidden_lr1 in bf16; grad_lr* = fp32 sums over the hidden rows, cast
+        to the lr dtype;
+      grad_K = G_W0_W2^T dx0_x2 + W0_W2^T grad_x0_x2 and
+      grad_V = W1 grad_dh + G_W1 hidden_lr1 (L/triton_lact_bwd_grouped_grad_kv.py:29-224,
+        bf16);
+      grad_W0_W2, grad_W1 = two_gemm_fw_bwd(grad_x0_x2, K, grad_dh, V).
+    Returns (grad_W0_W2, grad_W1, grad_K, grad_V, grad_lr0, grad_lr1, grad_lr2)."""
+    B, E, I2, D = W0_W2.shape
+    I = I2 // 2
+    N = K.shape[1]
+    lr_dtype = lr0.dtype
+    l = [_f(x.reshape(B, N), True) for x in (lr0, lr1, lr2)]
+    gdh = torch.zeros(B, I, N, dtype=torch.float64)
+    gx02 = torch.zeros(B, I2, N, dtype=torch.float64)
+    dx02 = torch.zeros(B, I2, N, dtype=torch.float64)
+    hlr = torch.zeros(B, I, N, dtype=torch.float64)
+    glr = [torch.zeros(B, N, dtype=torch.float64) for _ in range(3)]
+    for b in range(B):
+        for e, s, g in segments(group_sizes[b]):
+            if g == 0:
+                continue
+            k = _f(K[b, s:s + g], exact)
+            v = _f(V[b, s:s + g], exact)
+
+            def mm(w, a):
+                y = _f(w, exact) @ a.T
+                return y if exact else y.to(torch.bfloat16).double()
+
+            x02 = mm(W0_W2[b, e], k)
+            gy = mm(G_W0_W2[b, e], k)
+            dh = mm(W1[b, e].transpose(0, 1), v)
+            gd = mm(G_W1[b, e].transpose(0, 1), v)
+            x0, x2 = x02[:I], x02[I:]
+            gdx0, gdx2 = gy[:I], gy[I:]
+            L0, L1, L2 = (t[b, s:s + g] for t in l)
+            sg = torch.sigmoid(x0)
+            silu = sg * x0
+            m = sg * (1 + x0 * (1 - sg))
+            gdh[b, :, s:s + g] = gdx0 * L0 * x2 * m + gdx2 * L2 * silu
+            gx2 = gdx0 * L0 * dh * m + gd * L1 * silu
+            gsig = gdx0 * L0 * dh * x2 * (1 + x0 - 2 * sg * x0)
+            gx0 = ((gdx2 * L2 * dh + gd * L1 * x2) * m + gdx0 * L0 * dh * x2 * sg * (1 - sg)
+                   + gsig * sg * (1 - sg))
+            gx02[b, :I, s:s + g] = gx0
+            gx02[b, I:, s:s + g] = gx2
+            glr[0][b, s:s + g] = (gdx0 * dh * x2 * m).sum(0)
+            glr[1][b, s:s + g] = (gd * x2 * silu).sum(0)
+            glr[2][b, s:s + g] = (gdx2 * dh * silu).sum(0)
+            dx02[b, :I, s:s + g] = dh * x2 * m * L0
+            dx02[b, I:, s:s + g] = silu * dh * L2
+            hlr[b, :, s:s + g] = L1 * x2 * silu
+    gdh, gx02, dx02, hlr = (_r(t, exact) for t in (gdh, gx02, dx02, hlr))
+    gk = torch.zeros(B, N, D, dtype=torch.float64)
+    gv = torch.zeros(B, N, D, dtype=torch.float64)
+    for b in range(B):
+        for e, s, g in segments(group_sizes[b]):
+            if g == 0:
+                continue
+            gk[b, s:s + g] = (_f(G_W0_W2[b, e], exact).T @ _f(dx02[b, :, s:s + g], exact)
+                              + _f(W0_W2[b, e], exact).T @ _f(gx02[b, :, s:s + g], exact)).T
+            gv[b, s:s + g] = (_f(W1[b, e], exact) @ _f(gdh[b, :, s:s + g], exact)
+                              + _f(G_W1[b, e], exact) @ _f(hlr[b, :, s:s + g], exact)).T
+    gw02, gw1 = two_gemm_fw_bwd(gx02, K, gdh, V, group_sizes, exact)
+    glr = [t if exact else t.to(lr_dtype) for t in glr]
+    return gw02, gw1, _r(gk, exact), _r(gv, exact), glr[0], glr[1], glr[2]

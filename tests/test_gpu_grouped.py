@@ -213,3 +213,28 @@ def test_group_sizes_overcount_is_clamped():
     clamped = torch.tensor([[50, 50, 20]], dtype=torch.int32)
     ref = FW.swiglu_ffn_fwd(c["W02"], c["W1"], c["K"], clamped)
     assert_bf16_close(out.cpu(), ref, name="clamped apply")
+
+
+@pytest.mark.parametrize("name,lr_dtype", [("ragged", torch.bfloat16), ("slack", torch.float32),
+                                           ("c3_chunk", torch.bfloat16)])
+def test_update_backward(name, lr_dtype):
+    c = case(name, lr_dtype=lr_dtype)
+    g = torch.Generator().manual_seed(11)
+    GW02 = (torch.randn(c["W02"].shape, generator=g) * 0.02).to(torch.bfloat16)
+    GW1 = (torch.randn(c["W1"].shape, generator=g) * 0.02).to(torch.bfloat16)
+    W02, W1, K, V, gs = dev(c, "W02", "W1", "K", "V", "gs")
+    ins = [W02, W1, K, V] + [x.to(DEV) for x in c["lr"]]
+    for t in ins:
+        t.requires_grad_()
+    dw02, dw1 = FG.grouped_lact_swiglu_ffn_fast_weight_grads(*ins, gs)
+    torch.autograd.backward([dw02, dw1], [GW02.to(DEV), GW1.to(DEV)])
+    torch.cuda.synchronize()
+    ref = FW.fast_weight_grads_bwd(c["W02"], c["W1"], c["K"], c["V"], *c["lr"], c["gs"], GW02, GW1)
+    m = tok_mask(c)
+    names = ["grad_W0_W2", "grad_W1", "grad_K", "grad_V", "grad_lr0", "grad_lr1", "grad_lr2"]
+    for t, r, nm in zip(ins, ref, names):
+        got = t.grad.cpu()
+        assert got.dtype == r.dtype, (nm, got.dtype, r.dtype)
+        if nm in ("grad_K", "grad_V", "grad_lr0", "grad_lr1", "grad_lr2"):
+            got, r = got[m], r[m]
+        assert_bf16_close(got, r, name=nm)

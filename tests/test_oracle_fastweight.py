@@ -155,3 +155,46 @@ def test_apply_backward_is_autograd_of_apply():
             assert torch.allclose(gw1[b, e], w1.grad, rtol=1e-10, atol=1e-12)
             assert torch.allclose(gx[b, s:s + g], x.grad, rtol=1e-10, atol=1e-12)
             s += g
+
+
+def test_update_backward_is_autograd_of_update():
+    """The exact-mode UPDATE backward equals torch.autograd through the exact
+    UPDATE formula, for every input (W0, W2, W1, K, V, lr0, lr1, lr2)."""
+    gs = [[5, 0, 9], [7, 3, 4]]
+    W02, W1, K, V, lr, gsz = _inputs(2, 3, 10, 14, gs, seed=7)
+    g = torch.Generator().manual_seed(8)
+    GW02 = torch.randn(W02.shape, generator=g).to(torch.bfloat16)
+    GW1 = torch.randn(W1.shape, generator=g).to(torch.bfloat16)
+    out = FW.fast_weight_grads_bwd(W02, W1, K, V, *lr, gsz, GW02, GW1, exact=True)
+    gw02, gw1, gk, gv, gl0, gl1, gl2 = out
+    I = 14
+    for b in range(2):
+        s = 0
+        for e, n in enumerate(gs[b]):
+            w0 = _f(W02[b, e, :I]).requires_grad_()
+            w2 = _f(W02[b, e, I:]).requires_grad_()
+            w1 = _f(W1[b, e]).requires_grad_()
+            k = _f(K[b, s:s + n]).requires_grad_()
+            v = _f(V[b, s:s + n]).requires_grad_()
+            l0, l1, l2 = (x[b, s:s + n].double().requires_grad_() for x in lr)
+            y0, y2, dh = k @ w0.T, k @ w2.T, v @ w1
+            sg = torch.sigmoid(y0)
+            sw = sg * y0
+            dy0 = l0[:, None] * sg * y2 * dh * (1 + y0 * (1 - sg))
+            dy2 = l2[:, None] * sw * dh
+            hl = l1[:, None] * sw * y2
+            d_w0, d_w2, d_w1 = dy0.T @ k, dy2.T @ k, (hl.T @ v).T
+            loss = ((d_w0 * _f(GW02[b, e, :I])).sum() + (d_w2 * _f(GW02[b, e, I:])).sum()
+                    + (d_w1 * _f(GW1[b, e])).sum())
+            loss.backward()
+            tol = dict(rtol=1e-9, atol=1e-11)
+            assert torch.allclose(gw02[b, e, :I], w0.grad, **tol)
+            assert torch.allclose(gw02[b, e, I:], w2.grad, **tol)
+            assert torch.allclose(gw1[b, e], w1.grad, **tol)
+            if n:
+                assert torch.allclose(gk[b, s:s + n], k.grad, **tol)
+                assert torch.allclose(gv[b, s:s + n], v.grad, **tol)
+                assert torch.allclose(gl0[b, s:s + n], l0.grad, **tol)
+                assert torch.allclose(gl1[b, s:s + n], l1.grad, **tol)
+                assert torch.allclose(gl2[b, s:s + n], l2.grad, **tol)
+            s += n

@@ -79,6 +79,12 @@ SIGNATURES = {
     "uttt_grouped_wgrad": (
         c_int, [c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int, c_p, c_int, c_p],
     ),
+    "uttt_update_bwd_workspace_bytes": (c_sz, [c_int, c_int, c_int]),
+    "uttt_grouped_update_bwd": (
+        c_int,
+        [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_int, c_p, c_p, c_p, c_int, c_int, c_int, c_int,
+         c_int, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_sz, c_p],
+    ),
     "uttt_transpose_2byte": (c_int, [c_p, c_int, c_int, c_int, c_p, c_p]),
 }
 

@@ -134,16 +134,23 @@ __global__ __launch_bounds__(kThreads) void gate_up_kernel(
 }
 
 // ============================================= APPLY: down projection / NT ==
-// Y[b, tok, m] = sum_k W[b, e, m, k] X[b, tok, k] for tok in seg(b, e)
-// (AMAJOR = KMajor, W stored [M, K]); with AMAJOR = RMajor W is stored
-// [K, M] (the transposed product, e.g. grad_X = W0_W2^T DY).
-template <int BM, int BN, int AMAJOR>
+// Y[b, tok, m] = sum_p sum_k W_p[b, e, m, k] X_p[b, tok, k] for tok in
+// seg(b, e), over NPAIR operand pairs accumulated into one result (NPAIR = 1:
+// the down projection; NPAIR = 2: the UPDATE backward's grad_K / grad_V).
+// AMAJOR = KMajor: W stored [M, K]; RMajor: W stored [K, M] (the product with
+// W^T, e.g. grad_X = W0_W2^T DY).
+struct NtPair {
+  const uint16_t* w;
+  const uint16_t* x;
+};
+
+template <int BM, int BN, int AMAJOR, int NPAIR>
 __global__ __launch_bounds__(kThreads) void gemm_nt_kernel(
-    const uint16_t* __restrict__ wt, const uint16_t* __restrict__ x,
-    const int32_t* __restrict__ gs, uint16_t* __restrict__ y, int E, int M, int K, int N,
-    int m_tiles, int n_tiles_ub) {
+    NtPair p0, NtPair p1, const int32_t* __restrict__ gs, uint16_t* __restrict__ y, int E, int M,
+    int K, int N, int m_tiles, int n_tiles_ub) {
   constexpr int MB = BM / 64, NB = BN / 64;
-  constexpr int kStage = (BM + BN) * kLdsRow;
+  constexpr int kPair = (BM + BN) * kLdsRow;
+  constexpr int kStage = NPAIR * kPair;
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * kStage];
   __shared__ int scratch[4];
 
@@ -155,17 +162,28 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_kernel(
   if (tt.e < 0) return;
   const int m0 = mt * BM;
 
-  const Operand A0{wt + ((int64_t)b * E + tt.e) * M * K, AMAJOR == KMajor ? K : M, M, K};
-  const Operand B0{x + ((int64_t)b * N + tt.start) * K, K, tt.size, K};
-  TileRegs<BM, AMAJOR> ra0;
-  TileRegs<BN, KMajor> rb0;
+  const int64_t woff = ((int64_t)b * E + tt.e) * M * K;
+  const int64_t xoff = ((int64_t)b * N + tt.start) * K;
+  const int64_t lda = AMAJOR == KMajor ? K : M;
+  Operand A[NPAIR], Bo[NPAIR];
+  A[0] = Operand{p0.w + woff, lda, M, K};
+  Bo[0] = Operand{p0.x + xoff, K, tt.size, K};
+  if constexpr (NPAIR > 1) {
+    A[1] = Operand{p1.w + woff, lda, M, K};
+    Bo[1] = Operand{p1.x + xoff, K, tt.size, K};
+  }
+  TileRegs<BM, AMAJOR> ra[NPAIR];
+  TileRegs<BN, KMajor> rb[NPAIR];
   f32x16 acc[MB][NB];
   zero_acc(acc);
 
-  ra0.load(A0, m0, 0);
-  rb0.load(B0, tt.n0, 0);
-  ra0.store(lds);
-  rb0.store(lds + BM * kLdsRow);
+#pragma unroll
+  for (int q = 0; q < NPAIR; ++q) {
+    ra[q].load(A[q], m0, 0);
+    rb[q].load(Bo[q], tt.n0, 0);
+    ra[q].store(lds + q * kPair);
+    rb[q].store(lds + q * kPair + BM * kLdsRow);
+  }
   __syncthreads();
 
   const int w = wave_id();
@@ -175,15 +193,23 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_kernel(
   for (int k0 = 0; k0 < K; k0 += kBK) {
     const bool next = k0 + kBK < K;
     if (next) {
-      ra0.load(A0, m0, k0 + kBK);
-      rb0.load(B0, tt.n0, k0 + kBK);
+#pragma unroll
+      for (int q = 0; q < NPAIR; ++q) {
+        ra[q].load(A[q], m0, k0 + kBK);
+        rb[q].load(Bo[q], tt.n0, k0 + kBK);
+      }
     }
     const uint16_t* st = lds + cur * kStage;
-    mma_stage<MB, NB>(acc, st + wa, st + BM * kLdsRow + wb);
+#pragma unroll
+    for (int q = 0; q < NPAIR; ++q)
+      mma_stage<MB, NB>(acc, st + q * kPair + wa, st + q * kPair + BM * kLdsRow + wb);
     if (next) {
       uint16_t* nx = lds + (cur ^ 1) * kStage;
-      ra0.store(nx);
-      rb0.store(nx + BM * kLdsRow);
+#pragma unroll
+      for (int q = 0; q < NPAIR; ++q) {
+        ra[q].store(nx + q * kPair);
+        rb[q].store(nx + q * kPair + BM * kLdsRow);
+      }
     }
     __syncthreads();
     cur ^= 1;
@@ -444,6 +470,214 @@ __global__ __launch_bounds__(kThreads) void wgrad_kernel(WgradTask t0, WgradTask
   }
 }
 
+// ============================================ UPDATE backward, stage 1 ======
+// Backward of the UPDATE op given the upstream gradients GW0_W2 = dL/dDW0_W2
+// and GW1 = dL/dDW1.  Six accumulators per tile:
+//   Y0, Y2 = w0 k, w2 k;  GY0, GY2 = gw0 k, gw2 k;  DH = w1^T v;  GDH = gw1^T v
+// each rounded to bf16 (the reference stores them bf16 between its four-GEMM
+// kernel and its pointwise pass), then the second-order SwiGLU pointwise pass
+// in fp32 in the epilogue.  Writes token-major bf16 dx0_x2 / grad_x0_x2
+// ([N, 2I]), grad_dh / hidden_lr1 ([N, I]) and, per m-tile, fp32 partial
+// sums over the tile's hidden rows of the three learning-rate gradients
+// (lr_part[3][m_tiles][B][N]).
+__device__ __forceinline__ float bf16r(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+
+template <int BM, int BN, class LR>
+__global__ __launch_bounds__(kThreads) void update_bwd_s1_kernel(
+    const uint16_t* __restrict__ w02, const uint16_t* __restrict__ w1,
+    const uint16_t* __restrict__ gw02, const uint16_t* __restrict__ gw1,
+    const uint16_t* __restrict__ kk, const uint16_t* __restrict__ vv,
+    const typename LR::S* __restrict__ lr0, const typename LR::S* __restrict__ lr1,
+    const typename LR::S* __restrict__ lr2, const int32_t* __restrict__ gs,
+    uint16_t* __restrict__ dx02, uint16_t* __restrict__ gx02, uint16_t* __restrict__ gdh,
+    uint16_t* __restrict__ hlr, float* __restrict__ lr_part, int B, int E, int I, int D, int N,
+    int m_tiles, int n_tiles_ub) {
+  constexpr int MB = BM / 64, NB = BN / 64;
+  static_assert(NB == 1, "one 32-column block per wave");
+  constexpr int kA = BM * kLdsRow, kB = BN * kLdsRow;
+  constexpr int kStage = 6 * kA + 2 * kB;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * kStage];
+  __shared__ int scratch[4];
+  __shared__ float red[3][2][BN];  // lr partials of the two row-halves of the tile
+
+  const int bid = blockIdx.x;
+  const int mt = bid % m_tiles;
+  const int nt = (bid / m_tiles) % n_tiles_ub;
+  const int b = bid / (m_tiles * n_tiles_ub);
+  const TokenTile tt = find_token_tile<BN>(gs + (int64_t)b * E, E, N, nt, scratch);
+  if (tt.e < 0) return;
+  const int m0 = mt * BM;
+
+  const int64_t we = ((int64_t)b * E + tt.e) * 2 * I * D;
+  const int64_t w1e = ((int64_t)b * E + tt.e) * D * I;
+  Operand A[6] = {
+      Operand{w02 + we, D, I, D},
+      Operand{w02 + we + (int64_t)I * D, D, I, D},
+      Operand{gw02 + we, D, I, D},
+      Operand{gw02 + we + (int64_t)I * D, D, I, D},
+      Operand{w1 + w1e, I, I, D},    // w1^T: (r=i, k=d) at d*I + i
+      Operand{gw1 + w1e, I, I, D},
+  };
+  const Operand B0{kk + ((int64_t)b * N + tt.start) * D, D, tt.size, D};
+  const Operand B1{vv + ((int64_t)b * N + tt.start) * D, D, tt.size, D};
+
+  TileRegs<BM, KMajor> ra[4];
+  TileRegs<BM, RMajor> rt[2];
+  TileRegs<BN, KMajor> rb0, rb1;
+  f32x16 acc[6][MB][NB];
+#pragma unroll
+  for (int q = 0; q < 6; ++q) zero_acc(acc[q]);
+
+  auto load = [&](int k0) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) ra[q].load(A[q], m0, k0);
+    rt[0].load(A[4], m0, k0);
+    rt[1].load(A[5], m0, k0);
+    rb0.load(B0, tt.n0, k0);
+    rb1.load(B1, tt.n0, k0);
+  };
+  auto store = [&](uint16_t* st) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) ra[q].store(st + q * kA);
+    rt[0].store(st + 4 * kA);
+    rt[1].store(st + 5 * kA);
+    rb0.store(st + 6 * kA);
+    rb1.store(st + 6 * kA + kB);
+  };
+  load(0);
+  store(lds);
+  __syncthreads();
+
+  const int w = wave_id();
+  const int wa = (w >> 1) * (BM / 2) * kLdsRow;
+  const int wb = (w & 1) * (BN / 2) * kLdsRow;
+  int cur = 0;
+  for (int k0 = 0; k0 < D; k0 += kBK) {
+    const bool next = k0 + kBK < D;
+    if (next) load(k0 + kBK);
+    const uint16_t* st = lds + cur * kStage;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) mma_stage<MB, NB>(acc[q], st + q * kA + wa, st + 6 * kA + wb);
+    mma_stage<MB, NB>(acc[4], st + 4 * kA + wa, st + 6 * kA + kB + wb);
+    mma_stage<MB, NB>(acc[5], st + 5 * kA + wa, st + 6 * kA + kB + wb);
+    if (next) store(lds + (cur ^ 1) * kStage);
+    __syncthreads();
+    cur ^= 1;
+  }
+
+  const int I2 = 2 * I;
+  const int mw = m0 + (w >> 1) * (BM / 2);
+  const int ncol = (w & 1) * (BN / 2) + acc_col();   // column inside the tile
+  const int n = tt.n0 + ncol;
+  const bool nvalid = n < tt.size;
+  const int tok = tt.start + n;
+  float L0 = 0.f, L1 = 0.f, L2 = 0.f;
+  if (nvalid) {
+    const int64_t li = (int64_t)b * N + tok;
+    L0 = LR::load(lr0[li]);
+    L1 = LR::load(lr1[li]);
+    L2 = LR::load(lr2[li]);
+  }
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f;
+  uint16_t* dxb = dx02 + (int64_t)b * N * I2;
+  uint16_t* gxb = gx02 + (int64_t)b * N * I2;
+  uint16_t* ghb = gdh + (int64_t)b * N * I;
+  uint16_t* hlb = hlr + (int64_t)b * N * I;
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int m = mw + i * 32 + acc_row(q * 4);
+      if (!nvalid || m >= I) continue;
+      float o_gdh[4], o_gx0[4], o_gx2[4], o_dx0[4], o_dx2[4], o_hl[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int v = q * 4 + r;
+        const float x0 = bf16r(acc[0][i][0][v]);
+        const float x2 = bf16r(acc[1][i][0][v]);
+        const float gd0 = bf16r(acc[2][i][0][v]);
+        const float gd2 = bf16r(acc[3][i][0][v]);
+        const float dh = bf16r(acc[4][i][0][v]);
+        const float gd = bf16r(acc[5][i][0][v]);
+        const float sg = sigmoidf_(x0);
+        const float silu = sg * x0;
+        const float mul = sg * (1.0f + x0 * (1.0f - sg));   // silu'(x0)
+        const float ds = sg * (1.0f - sg);                   // sigmoid'(x0)
+        o_gdh[r] = gd0 * L0 * x2 * mul + gd2 * L2 * silu;
+        o_gx2[r] = gd0 * L0 * dh * mul + gd * L1 * silu;
+        const float gsig = gd0 * L0 * dh * x2 * (1.0f + x0 - 2.0f * sg * x0);
+        o_gx0[r] = (gd2 * L2 * dh + gd * L1 * x2) * mul + gd0 * L0 * dh * x2 * ds + gsig * ds;
+        s0 += gd0 * dh * x2 * mul;
+        s1 += gd * x2 * silu;
+        s2 += gd2 * dh * silu;
+        o_dx0[r] = dh * x2 * mul * L0;
+        o_dx2[r] = silu * dh * L2;
+        o_hl[r] = L1 * x2 * silu;
+      }
+      store4_tok(ghb, I, tok, m, o_gdh[0], o_gdh[1], o_gdh[2], o_gdh[3]);
+      store4_tok(gxb, I2, tok, m, o_gx0[0], o_gx0[1], o_gx0[2], o_gx0[3]);
+      store4_tok(gxb, I2, tok, I + m, o_gx2[0], o_gx2[1], o_gx2[2], o_gx2[3]);
+      store4_tok(dxb, I2, tok, m, o_dx0[0], o_dx0[1], o_dx0[2], o_dx0[3]);
+      store4_tok(dxb, I2, tok, I + m, o_dx2[0], o_dx2[1], o_dx2[2], o_dx2[3]);
+      store4_tok(hlb, I, tok, m, o_hl[0], o_hl[1], o_hl[2], o_hl[3]);
+    }
+  // lanes l and l^32 hold the same column (other rows): fold them, then the
+  // two waves of a column half meet in LDS
+  s0 += __shfl_xor(s0, 32, 64);
+  s1 += __shfl_xor(s1, 32, 64);
+  s2 += __shfl_xor(s2, 32, 64);
+  if ((threadIdx.x & 63) < 32) {
+    red[0][w >> 1][ncol] = s0;
+    red[1][w >> 1][ncol] = s1;
+    red[2][w >> 1][ncol] = s2;
+  }
+  __syncthreads();
+  if (threadIdx.x < BN) {
+    const int c = threadIdx.x;
+    const int nn = tt.n0 + c;
+    if (nn < tt.size) {
+      const int64_t o = ((int64_t)mt * B + b) * N + tt.start + nn;
+      const int64_t plane = (int64_t)m_tiles * B * N;
+      lr_part[o] = red[0][0][c] + red[0][1][c];
+      lr_part[plane + o] = red[1][0][c] + red[1][1][c];
+      lr_part[2 * plane + o] = red[2][0][c] + red[2][1][c];
+    }
+  }
+}
+
+// grad_lr_j[b, tok] = sum over m-tiles of lr_part[j][mt][b][tok] (fixed
+// order); tokens past the batch's routed total get 0.
+template <class LR>
+__global__ __launch_bounds__(256) void lr_grad_reduce_kernel(const float* __restrict__ lr_part,
+                                                             const int32_t* __restrict__ gs,
+                                                             int B, int E, int N, int m_tiles,
+                                                             typename LR::S* __restrict__ g0,
+                                                             typename LR::S* __restrict__ g1,
+                                                             typename LR::S* __restrict__ g2) {
+  const int b = blockIdx.y;
+  const int tok = blockIdx.x * 256 + threadIdx.x;
+  if (tok >= N) return;
+  int total = 0;
+  for (int e = 0; e < E; ++e) {
+    const int g = gs[(int64_t)b * E + e];
+    total += g > 0 ? g : 0;
+  }
+  const int64_t plane = (int64_t)m_tiles * B * N;
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f;
+  if (tok < total) {
+    for (int mt = 0; mt < m_tiles; ++mt) {
+      const int64_t o = ((int64_t)mt * B + b) * N + tok;
+      a0 += lr_part[o];
+      a1 += lr_part[plane + o];
+      a2 += lr_part[2 * plane + o];
+    }
+  }
+  const int64_t li = (int64_t)b * N + tok;
+  g0[li] = LR::store(a0);
+  g1[li] = LR::store(a1);
+  g2[li] = LR::store(a2);
+}
+
 // =============================================================== transpose ==
 // out[b, c, r] = in[b, r, c] for 2-byte elements, via a 64x64 LDS tile.
 __global__ __launch_bounds__(256) void transpose16_kernel(const uint16_t* __restrict__ in,
@@ -520,10 +754,10 @@ extern "C" int uttt_grouped_gemm_nt(const void* w, const void* x, const int32_t*
   const int n_ub = (N + kApplyBN - 1) / kApplyBN + E;
   const int64_t blocks = (int64_t)m_tiles * n_ub * B;
   if (int rc = check_grid(blocks, "grouped_gemm_nt")) return rc;
-  hipLaunchKernelGGL((gemm_nt_kernel<kApplyBM, kApplyBN, KMajor>), dim3((unsigned)blocks),
-                     dim3(kThreads), 0, as_stream(stream), static_cast<const uint16_t*>(w),
-                     static_cast<const uint16_t*>(x), group_sizes, static_cast<uint16_t*>(y), E, M,
-                     K, N, m_tiles, n_ub);
+  const NtPair p{static_cast<const uint16_t*>(w), static_cast<const uint16_t*>(x)};
+  hipLaunchKernelGGL((gemm_nt_kernel<kApplyBM, kApplyBN, KMajor, 1>), dim3((unsigned)blocks),
+                     dim3(kThreads), 0, as_stream(stream), p, p, group_sizes,
+                     static_cast<uint16_t*>(y), E, M, K, N, m_tiles, n_ub);
   return check_launch("grouped_gemm_nt");
 }
 
@@ -539,10 +773,10 @@ extern "C" int uttt_grouped_gemm_tn(const void* w, const void* x, const int32_t*
   const int n_ub = (N + kApplyBN - 1) / kApplyBN + E;
   const int64_t blocks = (int64_t)m_tiles * n_ub * B;
   if (int rc = check_grid(blocks, "grouped_gemm_tn")) return rc;
-  hipLaunchKernelGGL((gemm_nt_kernel<kApplyBM, kApplyBN, RMajor>), dim3((unsigned)blocks),
-                     dim3(kThreads), 0, as_stream(stream), static_cast<const uint16_t*>(w),
-                     static_cast<const uint16_t*>(x), group_sizes, static_cast<uint16_t*>(y), E, M,
-                     K, N, m_tiles, n_ub);
+  const NtPair p{static_cast<const uint16_t*>(w), static_cast<const uint16_t*>(x)};
+  hipLaunchKernelGGL((gemm_nt_kernel<kApplyBM, kApplyBN, RMajor, 1>), dim3((unsigned)blocks),
+                     dim3(kThreads), 0, as_stream(stream), p, p, group_sizes,
+                     static_cast<uint16_t*>(y), E, M, K, N, m_tiles, n_ub);
   return check_launch("grouped_gemm_tn");
 }
 
@@ -654,4 +888,106 @@ extern "C" int uttt_transpose_2byte(const void* in, int B, int R, int C, void* o
   hipLaunchKernelGGL(transpose16_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream),
                      static_cast<const uint16_t*>(in), static_cast<uint16_t*>(out), R, C, rt, ct);
   return check_launch("transpose_2byte");
+}
+
+namespace uttt {
+namespace {
+constexpr int kUbBM = 128, kUbBN = 64;
+
+struct UpdateBwdWs {
+  size_t dx, gx, gdh, hlr, part, total;
+};
+UpdateBwdWs update_bwd_ws(int B, int I, int N) {
+  auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  const int m_tiles = (I + kUbBM - 1) / kUbBM;
+  UpdateBwdWs w;
+  w.dx = 0;
+  w.gx = w.dx + up((size_t)B * N * 2 * I * 2);
+  w.gdh = w.gx + up((size_t)B * N * 2 * I * 2);
+  w.hlr = w.gdh + up((size_t)B * N * I * 2);
+  w.part = w.hlr + up((size_t)B * N * I * 2);
+  w.total = w.part + up((size_t)3 * m_tiles * B * N * 4);
+  return w;
+}
+}  // namespace
+}  // namespace uttt
+
+extern "C" size_t uttt_update_bwd_workspace_bytes(int B, int I, int N) {
+  if (B <= 0 || I <= 0 || N <= 0) return 0;
+  return update_bwd_ws(B, I, N).total;
+}
+
+extern "C" int uttt_grouped_update_bwd(
+    const void* w0_w2, const void* w1, const void* k, const void* v, const void* lr0,
+    const void* lr1, const void* lr2, int lr_dtype, const int32_t* group_sizes,
+    const void* grad_dw0_w2, const void* grad_dw1, int B, int E, int I, int D, int N,
+    void* grad_w0_w2, void* grad_w1, void* grad_k, void* grad_v, void* grad_lr0, void* grad_lr1,
+    void* grad_lr2, void* workspace, size_t workspace_bytes, void* stream) {
+  UTTT_REQUIRE(B >= 0 && E >= 1 && I >= 0 && D >= 0 && N >= 0, "grouped_update_bwd: bad sizes");
+  UTTT_REQUIRE(I % 8 == 0 && D % 8 == 0,
+               "grouped_update_bwd: I=%d and D=%d must be multiples of 8", I, D);
+  if (B == 0 || N == 0 || I == 0 || D == 0) return UTTT_OK;
+  UTTT_REQUIRE(w0_w2 && w1 && k && v && lr0 && lr1 && lr2 && group_sizes && grad_dw0_w2 &&
+                   grad_dw1 && grad_w0_w2 && grad_w1 && grad_k && grad_v && grad_lr0 &&
+                   grad_lr1 && grad_lr2 && workspace,
+               "grouped_update_bwd: null pointer");
+  UTTT_REQUIRE(aligned16(w0_w2) && aligned16(w1) && aligned16(k) && aligned16(v) &&
+                   aligned16(grad_dw0_w2) && aligned16(grad_dw1) && aligned16(grad_w0_w2) &&
+                   aligned16(grad_w1) && aligned16(grad_k) && aligned16(grad_v) &&
+                   aligned16(workspace),
+               "grouped_update_bwd: tensors must be 16-byte aligned");
+  const UpdateBwdWs ws = update_bwd_ws(B, I, N);
+  UTTT_REQUIRE(workspace_bytes >= ws.total, "grouped_update_bwd: workspace %zu < %zu bytes",
+               workspace_bytes, ws.total);
+  uint8_t* wsb = static_cast<uint8_t*>(workspace);
+  uint16_t* dx = reinterpret_cast<uint16_t*>(wsb + ws.dx);
+  uint16_t* gx = reinterpret_cast<uint16_t*>(wsb + ws.gx);
+  uint16_t* gdh = reinterpret_cast<uint16_t*>(wsb + ws.gdh);
+  uint16_t* hlr = reinterpret_cast<uint16_t*>(wsb + ws.hlr);
+  float* part = reinterpret_cast<float*>(wsb + ws.part);
+  hipStream_t st = as_stream(stream);
+  const auto* W02 = static_cast<const uint16_t*>(w0_w2);
+  const auto* W1 = static_cast<const uint16_t*>(w1);
+  const auto* GW02 = static_cast<const uint16_t*>(grad_dw0_w2);
+  const auto* GW1 = static_cast<const uint16_t*>(grad_dw1);
+
+  // 1. six GEMMs + second-order pointwise pass
+  const int m_tiles = (I + kUbBM - 1) / kUbBM;
+  const int n_ub = (N + kUbBN - 1) / kUbBN + E;
+  const int64_t blocks = (int64_t)m_tiles * n_ub * B;
+  if (int rc = check_grid(blocks, "grouped_update_bwd")) return rc;
+  UTTT_DTYPE_SWITCH_LR(lr_dtype, LR, {
+    using S = typename LR::S;
+    hipLaunchKernelGGL((update_bwd_s1_kernel<kUbBM, kUbBN, LR>), dim3((unsigned)blocks),
+                       dim3(kThreads), 0, st, W02, W1, GW02, GW1,
+                       static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
+                       static_cast<const S*>(lr0), static_cast<const S*>(lr1),
+                       static_cast<const S*>(lr2), group_sizes, dx, gx, gdh, hlr, part, B, E, I,
+                       D, N, m_tiles, n_ub);
+    if (int rc = check_launch("grouped_update_bwd(stage 1)")) return rc;
+    // 2. learning-rate gradients
+    hipLaunchKernelGGL((lr_grad_reduce_kernel<LR>), dim3((N + 255) / 256, B), dim3(256), 0, st,
+                       part, group_sizes, B, E, N, m_tiles, static_cast<S*>(grad_lr0),
+                       static_cast<S*>(grad_lr1), static_cast<S*>(grad_lr2));
+    if (int rc = check_launch("grouped_update_bwd(lr grads)")) return rc;
+  });
+  // 3. grad_K = GW0_W2^T dx0_x2 + W0_W2^T grad_x0_x2;  grad_V = W1 grad_dh + GW1 hidden_lr1
+  {
+    const int mt2 = (D + kApplyBM - 1) / kApplyBM;
+    const int nub2 = (N + kApplyBN - 1) / kApplyBN + E;
+    const int64_t blocks2 = (int64_t)mt2 * nub2 * B;
+    if (int rc = check_grid(blocks2, "grouped_update_bwd")) return rc;
+    hipLaunchKernelGGL((gemm_nt_kernel<kApplyBM, kApplyBN, RMajor, 2>), dim3((unsigned)blocks2),
+                       dim3(kThreads), 0, st, NtPair{GW02, dx}, NtPair{W02, gx}, group_sizes,
+                       static_cast<uint16_t*>(grad_k), E, D, 2 * I, N, mt2, nub2);
+    if (int rc = check_launch("grouped_update_bwd(grad_K)")) return rc;
+    hipLaunchKernelGGL((gemm_nt_kernel<kApplyBM, kApplyBN, KMajor, 2>), dim3((unsigned)blocks2),
+                       dim3(kThreads), 0, st, NtPair{W1, gdh}, NtPair{GW1, hlr}, group_sizes,
+                       static_cast<uint16_t*>(grad_v), E, D, I, N, mt2, nub2);
+    if (int rc = check_launch("grouped_update_bwd(grad_V)")) return rc;
+  }
+  // 4. weight gradients of the weights
+  const WgradTask t0 = make_task(gx, k, grad_w0_w2, 2 * I, D, 0);
+  const WgradTask t1 = make_task(gdh, v, grad_w1, I, D, 1);
+  return launch_wgrad(t0, t1, group_sizes, B, E, N, st, "grouped_update_bwd(weights)");
 }
