@@ -6,9 +6,17 @@
 Prints ONE JSON line (rank 0).  Workloads (seeded synthetic inputs, resident
 in HBM before the timed region starts):
 
-  permute   token permute + gate-weighted unpermute by expert, T=65536, E=16,
-            top-2, payload bf16 [T, 768]; one step = row map + permute +
-            unpermute of one batch; value = algorithmic GB/s of the step.
+  moe760m   (default) configs[4]: uTTT-MoE 760M training slice, E=32 experts,
+            top-2, d=1536, expert hidden 3072, Zipf(1.1) routing prior, 24
+            layers sharing the pool, seq 32768 in chunks of 2048.  One step =
+            one shifted block-causal sweep: APPLY (row map, permute, grouped
+            SwiGLU apply, unpermute) on 16 chunks x 24 layers, UPDATE forward
+            and backward on 15 x 24; value = tokens/s of the sweep.
+  moe124m   configs[3]: uTTT-MoE 124M, E=16, d=768, hidden 1536, 12 layers,
+            APPLY + UPDATE forward.
+  permute   configs[2]: token permute + gate-weighted unpermute by expert,
+            T=65536, E=16, top-2, payload bf16 [T, 768]; one step = row map +
+            permute + unpermute of one batch; value = algorithmic GB/s.
 
 Timing: W untimed steps, then K steps bracketed by torch.cuda.synchronize();
 per-kernel durations come from HIP events recorded on the stream the kernels
@@ -239,21 +247,309 @@ def copy_calibration():
     print(f"copy_calibration: {n} bytes read, {n} bytes written", file=sys.stderr)
 
 
-WORKLOADS = {"permute": bench_permute}
-DEFAULT_WORKLOAD = "permute"
+# ------------------------------------------------------------ MoE sweep ----
+MOE_CONFIGS = {
+    # uTTT-MoE 124M, apply + update forward, 12 layers share the pool
+    "moe124m": dict(E=16, D=768, I=1536, L=12, zipf=None, train=False,
+                    label="uTTT-MoE 124M grouped apply+update (configs[3])"),
+    # uTTT-MoE 760M training slice: apply fwd + update fwd + update bwd
+    "moe760m": dict(E=32, D=1536, I=3072, L=24, zipf=1.1, train=True,
+                    label="uTTT-MoE 760M apply+update fwd+bwd training slice (configs[4])"),
+}
+SEQ, CHUNK, TOPK = 32768, 2048, 2
+
+
+class MoeSweep:
+    """Buffers and C-ABI launches of one shifted block-causal sweep over the
+    sequence: for every chunk and layer the APPLY (row map, permute, grouped
+    SwiGLU apply, gate-weighted unpermute), and for every chunk but the last
+    the UPDATE (row map, permute of k, v*p and the learning rates, grouped
+    update) plus, for the training slice, the UPDATE backward seeded with
+    fixed upstream weight gradients.  Each kernel launch is bracketed by HIP
+    events on the launch stream when `timed`."""
+
+    NSETS = 4   # distinct per-layer input sets, cycled over (chunk, layer)
+
+    def __init__(self, cfg, dev):
+        import torch
+
+        from uttt_amd import _lib as L
+
+        self.L, self.cfg, self.dev = L, cfg, dev
+        E, D, I = cfg["E"], cfg["D"], cfg["I"]
+        T, k = CHUNK, TOPK
+        N = k * T
+        self.E, self.D, self.I, self.T, self.k, self.N = E, D, I, T, k, N
+        g = torch.Generator(device=dev).manual_seed(0)
+        bf = torch.bfloat16
+
+        def randn(*shape, scale=1.0):
+            return (torch.randn(*shape, generator=g, device=dev) * scale).to(bf)
+
+        # the shared expert pool (W0_W2 = cat(w0, w2) rows, W1 = down proj)
+        self.W02 = randn(1, E, 2 * I, D, scale=D ** -0.5)
+        self.W1 = randn(1, E, D, I, scale=D ** -0.5)
+        self.sets = []
+        for s in range(self.NSETS):
+            st = {}
+            for name in ("x", "k", "v"):
+                t = torch.randn(1, T, D, generator=g, device=dev)
+                st[name] = (t / (t.norm(dim=-1, keepdim=True) + 1e-5)).to(bf)
+            st["lr"] = [(torch.sigmoid(torch.randn(1, T, generator=g, device=dev)) * 0.1).to(bf)
+                        for _ in range(3)]
+            for role in ("a", "u"):   # routing of the apply (x) and of the update (k)
+                logits = torch.randn(1, E, T, generator=g, device=dev)
+                if cfg["zipf"] is not None:
+                    prior = -cfg["zipf"] * torch.log(torch.arange(E, device=dev, dtype=torch.float32) + 1)
+                    logits = logits + prior.view(1, E, 1)
+                    bias = torch.zeros(1, E, 1, device=dev)
+                else:
+                    bias = (torch.randn(E, generator=g, device=dev) * 0.5).view(1, E, 1)
+                idx = torch.topk(logits + bias, k, dim=1).indices
+                mask = torch.zeros(1, E, T, dtype=torch.bool, device=dev).scatter_(1, idx, True)
+                sm = torch.softmax(logits, dim=1) * mask
+                st["mask_" + role] = mask
+                st["gates_" + role] = (sm / sm.sum(1, keepdim=True)).contiguous()
+                st["gs_" + role] = mask.sum(-1).to(torch.int32).contiguous()
+            self.sets.append(st)
+        if cfg["train"]:
+            self.GW02 = randn(1, E, 2 * I, D, scale=0.02)
+            self.GW1 = randn(1, E, D, I, scale=0.02)
+        e = lambda *shape, dt=bf: torch.empty(*shape, dtype=dt, device=dev)
+        self.rmap = e(1, T, 2 * E + 1, dt=torch.int32)
+        self.ws_map = e(L.lib().uttt_row_id_map_workspace_bytes(1, T, E), dt=torch.uint8)
+        self.xp, self.pp = e(1, N, D), e(1, N, dt=torch.float32)
+        self.hid, self.yp, self.y = e(1, N, I), e(1, N, D), e(1, T, D)
+        self.kp, self.vp = e(1, N, D), e(1, N, D)
+        self.lrp = [e(1, N) for _ in range(3)]
+        self.dy, self.hl = e(1, N, 2 * I), e(1, N, I)
+        self.dW02, self.dW1 = e(1, E, 2 * I, D), e(1, E, D, I)
+        if cfg["train"]:
+            self.gW02, self.gW1 = e(1, E, 2 * I, D), e(1, E, D, I)
+            self.gK, self.gV = e(1, N, D), e(1, N, D)
+            self.glr = [e(1, N) for _ in range(3)]
+            wsb = L.lib().uttt_update_bwd_workspace_bytes(1, I, N)
+            self.ws_bwd, self.ws_bwd_bytes = e(wsb, dt=torch.uint8), wsb
+        self.stream = torch.cuda.current_stream(dev).cuda_stream
+        self.events = None
+
+    # algorithmic FLOPs per launch, NID = N * I * D
+    def flops(self):
+        nid = self.N * self.I * self.D
+        return {"gate_up": 4 * nid, "down_proj": 2 * nid, "update_s1": 6 * nid,
+                "wgrad": 6 * nid, "update_bwd_s1": 12 * nid, "grad_k": 8 * nid, "grad_v": 4 * nid,
+                "wgrad_bwd": 6 * nid}
+
+    def _mark(self, name):
+        if self.events is not None:
+            import torch
+
+            ev = torch.cuda.Event(enable_timing=True)
+            ev.record()
+            self.events.append((name, ev))
+
+    def apply(self, st):
+        L, E, D, I, T, N, s = self.L, self.E, self.D, self.I, self.T, self.N, self.stream
+        m, p = st["mask_a"], st["gates_a"]
+        self._mark("row_map")
+        L.call("uttt_make_row_id_map", L.ptr(m), 1, m.stride(0), m.stride(1), m.stride(2), 1, T,
+               E, L.ptr(self.rmap), None, L.ptr(self.ws_map), self.ws_map.numel(), s)
+        self._mark("permute")
+        L.call("uttt_permute_fwd", L.ptr(st["x"]), L.BF16, 1, T, D, L.ptr(self.rmap), E,
+               L.ptr(p), p.stride(0), p.stride(1), p.stride(2), L.ptr(self.xp), N,
+               L.ptr(self.pp), s)
+        self._mark("gate_up")
+        L.call("uttt_grouped_gate_up", L.ptr(self.W02), L.ptr(self.xp), L.ptr(st["gs_a"]), 1, E,
+               I, D, N, L.ptr(self.hid), 1, s)
+        self._mark("down_proj")
+        L.call("uttt_grouped_gemm_nt", L.ptr(self.W1), L.ptr(self.hid), L.ptr(st["gs_a"]), 1, E,
+               D, I, N, L.ptr(self.yp), s)
+        self._mark("unpermute")
+        L.call("uttt_unpermute_fwd", L.ptr(self.yp), L.BF16, 1, N, D, L.ptr(self.rmap), T, E,
+               L.ptr(p), p.stride(0), p.stride(1), p.stride(2), L.ptr(self.y), s)
+        self._mark(None)
+
+    def update(self, st):
+        L, E, D, I, T, N, s = self.L, self.E, self.D, self.I, self.T, self.N, self.stream
+        m, p, gs = st["mask_u"], st["gates_u"], st["gs_u"]
+        lr = st["lr"]
+        self._mark("row_map")
+        L.call("uttt_make_row_id_map", L.ptr(m), 1, m.stride(0), m.stride(1), m.stride(2), 1, T,
+               E, L.ptr(self.rmap), None, L.ptr(self.ws_map), self.ws_map.numel(), s)
+        self._mark("permute_kv_lrs")
+        L.call("uttt_permute_kv_lrs_fwd", L.ptr(st["k"]), L.BF16, L.ptr(st["v"]), L.BF16,
+               L.ptr(lr[0]), L.ptr(lr[1]), L.ptr(lr[2]), 2, 1, T, D, L.ptr(self.rmap), E,
+               L.ptr(p), p.stride(0), p.stride(1), p.stride(2), L.ptr(self.kp), L.ptr(self.vp),
+               L.ptr(self.lrp[0]), L.ptr(self.lrp[1]), L.ptr(self.lrp[2]), N, s)
+        self._mark("update_s1")
+        L.call("uttt_grouped_update_stage1", L.ptr(self.W02), L.ptr(self.W1), L.ptr(self.kp),
+               L.ptr(self.vp), L.ptr(self.lrp[0]), L.ptr(self.lrp[1]), L.ptr(self.lrp[2]), L.BF16,
+               L.ptr(gs), 1, E, I, D, N, L.ptr(self.dy), L.ptr(self.hl), 1, s)
+        self._mark("wgrad")
+        L.call("uttt_grouped_wgrad_pair", L.ptr(self.dy), L.ptr(self.kp), L.ptr(self.hl),
+               L.ptr(self.vp), L.ptr(gs), 1, E, I, D, N, L.ptr(self.dW02), L.ptr(self.dW1), s)
+        if self.cfg["train"]:
+            self._mark("update_bwd(5 launches)")
+            L.call("uttt_grouped_update_bwd", L.ptr(self.W02), L.ptr(self.W1), L.ptr(self.kp),
+                   L.ptr(self.vp), L.ptr(self.lrp[0]), L.ptr(self.lrp[1]), L.ptr(self.lrp[2]),
+                   L.BF16, L.ptr(gs), L.ptr(self.GW02), L.ptr(self.GW1), 1, E, I, D, N,
+                   L.ptr(self.gW02), L.ptr(self.gW1), L.ptr(self.gK), L.ptr(self.gV),
+                   L.ptr(self.glr[0]), L.ptr(self.glr[1]), L.ptr(self.glr[2]),
+                   L.ptr(self.ws_bwd), self.ws_bwd_bytes, s)
+        self._mark(None)
+
+    def sweep(self, layers, chunks):
+        i = 0
+        for c in range(chunks):
+            for l in range(layers):
+                self.apply(self.sets[i % self.NSETS])
+                i += 1
+            if c < chunks - 1:   # the last chunk is read but never written
+                for l in range(layers):
+                    self.update(self.sets[i % self.NSETS])
+                    i += 1
+
+
+def _event_times(events):
+    """{name: [seconds]} from consecutive (name, event) marks."""
+    out = {}
+    for (name, ev), (_, ev2) in zip(events, events[1:]):
+        if name is None:
+            continue
+        out.setdefault(name, []).append(ev.elapsed_time(ev2) * 1e-3)
+    return out
+
+
+def bench_moe(args, key):
+    import torch
+
+    cfg = MOE_CONFIGS[key]
+    dev = torch.device("cuda", 0)
+    sw = MoeSweep(cfg, dev)
+    layers, chunks = cfg["L"], SEQ // CHUNK
+    # warmup: W sweeps untimed (at least one layer-chunk of each op)
+    for _ in range(max(args.warmup, 1)):
+        sw.sweep(1, 2)
+    torch.cuda.synchronize()
+    walls = []
+    for _ in range(args.steps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        sw.sweep(layers, chunks)
+        torch.cuda.synchronize()
+        walls.append(time.perf_counter() - t0)
+    wall = statistics.mean(walls)
+    # one more sweep with every launch bracketed by events (per-kernel table)
+    sw.events = []
+    sw.sweep(layers, chunks)
+    torch.cuda.synchronize()
+    per = _event_times(sw.events)
+    sw.events = None
+
+    fl = sw.flops()
+    fl["update_bwd(5 launches)"] = 30 * sw.N * sw.I * sw.D
+    kern = {}
+    for name, ts in per.items():
+        t = statistics.mean(ts)
+        d = dict(us=round(t * 1e6, 2), launches_per_sweep=len(ts))
+        if name in fl:
+            tf = fl[name] / t / 1e12
+            d.update(TFLOPs=round(tf, 1), mfma_frac=round(tf / BF16_PEAK_TFLOPS, 4))
+        kern[name] = d
+    # dominant MFMA kernel by time per sweep
+    dom = max((n for n in kern if "TFLOPs" in kern[n] and "(" not in n),
+              key=lambda n: kern[n]["us"] * kern[n]["launches_per_sweep"])
+    t_dom = statistics.mean(per[dom])
+    tokens = SEQ  # B = 1
+    value = tokens / wall
+    nid = sw.N * sw.I * sw.D
+    sweep_flops = layers * (chunks * 6 + (chunks - 1) * (42 if cfg["train"] else 12)) * nid
+    res = dict(
+        metric="fast-weight apply+update tokens/s",
+        value=round(value, 1),
+        unit="tokens/s",
+        ms_per_step=round(wall * 1e3, 3),
+        dtype="bf16",
+        config={"workload": cfg["label"], "seq_len": SEQ, "chunk": CHUNK, "layers": layers,
+                "experts": cfg["E"], "topk": TOPK, "d": cfg["D"], "expert_hidden": cfg["I"],
+                "routing": "Zipf(1.1) prior" if cfg["zipf"] else "N(0,1) logits + N(0,0.5) bias",
+                "step": "one sweep: apply on 16 chunks x L layers, update on 15 x L"
+                        + (" (+ update backward)" if cfg["train"] else ""),
+                "excluded": "router logits/top-k (inputs precomputed); write step"},
+        roofline=dict(bound="mfma", kernel=dom, achieved=round(fl[dom] / t_dom / 1e12, 2),
+                      peak=BF16_PEAK_TFLOPS, unit="TFLOP/s",
+                      frac=round(fl[dom] / t_dom / 1e12 / BF16_PEAK_TFLOPS, 4), traffic=None,
+                      algorithmic_flops=fl[dom], avg_launch_us=round(t_dom * 1e6, 2)),
+        sweep=dict(algorithmic_flops=sweep_flops,
+                   TFLOPs=round(sweep_flops / wall / 1e12, 1),
+                   mfma_frac=round(sweep_flops / wall / 1e12 / BF16_PEAK_TFLOPS, 4)),
+        kernels=kern,
+    )
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline_moe(sw, cfg, layers, chunks)
+    return res
+
+
+def cpu_baseline_moe(sw, cfg, layers, chunks):
+    """The fp32 PyTorch restatement (oracle/fastweight.py, fp32 accumulation)
+    of one layer-chunk's grouped APPLY, UPDATE (and UPDATE backward for the
+    training slice) at the full shape, on this host's cores; the sweep time is
+    extrapolated as layers * (chunks * t_apply + (chunks-1) * t_update)."""
+    import torch
+
+    from oracle import fastweight as FW
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    st = sw.sets[0]
+    gs_a, gs_u = st["gs_a"].cpu(), st["gs_u"].cpu()
+    W02, W1 = sw.W02.cpu(), sw.W1.cpu()
+    x = torch.randn(1, sw.N, sw.D).to(torch.bfloat16)
+    kk = torch.randn(1, sw.N, sw.D).to(torch.bfloat16)
+    vv = torch.randn(1, sw.N, sw.D).to(torch.bfloat16)
+    lr = [torch.full((1, sw.N), 0.05).to(torch.bfloat16) for _ in range(3)]
+    with FW.fp32_accumulate():
+        t0 = time.perf_counter()
+        FW.swiglu_ffn_fwd(W02, W1, x, gs_a)
+        t_apply = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        FW.fast_weight_grads(W02, W1, kk, vv, *lr, gs_u)
+        t_update = time.perf_counter() - t0
+        if cfg["train"]:
+            t0 = time.perf_counter()
+            FW.fast_weight_grads_bwd(W02, W1, kk, vv, *lr, gs_u, sw.GW02.cpu(), sw.GW1.cpu())
+            t_update += time.perf_counter() - t0
+    t_sweep = layers * (chunks * t_apply + (chunks - 1) * t_update)
+    return dict(value=round(SEQ / t_sweep, 2), unit="tokens/s", cores=threads, kind="port",
+                sample=f"one layer-chunk at full shape: apply {t_apply:.2f} s, update"
+                       f"{' fwd+bwd' if cfg['train'] else ''} {t_update:.2f} s (fp32 torch, "
+                       f"{threads} threads); sweep extrapolated x{layers} layers x{chunks} chunks",
+                cpu=_cpu_model())
+
+
+WORKLOADS = {"permute": bench_permute,
+             "moe124m": lambda a: bench_moe(a, "moe124m"),
+             "moe760m": lambda a: bench_moe(a, "moe760m")}
+DEFAULT_WORKLOAD = "moe760m"
 
 
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed steps (default 20 for permute, 2 sweeps for the MoE workloads)")
+    ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true",
                     help="skip the CPU baseline leg (profiling runs)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one plain 256 MiB device copy (PMC scaling)")
     args = ap.parse_args()
+    moe = args.workload.startswith("moe")
+    if args.steps is None:
+        args.steps = 2 if moe else 20
+    if args.warmup is None:
+        args.warmup = 1 if moe else 5
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only; multi-GPU runs are not part of it "
               "(use --gpus 1)", file=sys.stderr)

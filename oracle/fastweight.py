@@ -23,7 +23,25 @@ it to pin the formulas themselves.
 """
 from __future__ import annotations
 
+import contextlib
+
 import torch
+
+# Accumulation dtype of the non-exact mode: fp64 for parity checks; the CPU
+# baseline timing in bench.py switches it to fp32 (the reference's CPU path
+# is fp32 PyTorch) with `fp32_accumulate()`.
+_ACC = torch.float64
+
+
+@contextlib.contextmanager
+def fp32_accumulate():
+    global _ACC
+    old = _ACC
+    _ACC = torch.float32
+    try:
+        yield
+    finally:
+        _ACC = old
 
 
 def _r(x, exact):
@@ -32,7 +50,7 @@ def _r(x, exact):
 
 
 def _f(x, exact):
-    return x.double() if exact else x.float().double()
+    return x.double() if exact else x.float().to(_ACC)
 
 
 def segments(group_sizes_row):
@@ -59,7 +77,7 @@ def two_mm_swiglu(W0_W2, X, group_sizes, exact=False):
             y0 = (w[:I] @ x.T)
             y2 = (w[I:] @ x.T)
             if not exact:
-                y0, y2 = y0.float().double(), y2.float().double()
+                y0, y2 = y0.float().to(_ACC), y2.float().to(_ACC)
             out[b, :, s:s + g] = y2 * (y0 * torch.sigmoid(y0))
     return _r(out, exact)
 
@@ -105,7 +123,7 @@ def three_bmm_with_lr(W0_W2, W1, K, V, lr0, lr1, lr2, group_sizes, exact=False):
             y2 = w[I:] @ k.T
             dh = _f(W1[b, e], exact).T @ v.T
             if not exact:
-                y0, y2, dh = (t.float().double() for t in (y0, y2, dh))
+                y0, y2, dh = (t.float().to(_ACC) for t in (y0, y2, dh))
             sig = torch.sigmoid(y0)
             sw = sig * y0
             dy[b, :I, s:s + g] = sig * y2 * dh * (1.0 + y0 * (1.0 - sig)) * l0[b, s:s + g]
@@ -194,7 +212,7 @@ def fast_weight_grads_bwd(W0_W2, W1, K, V, lr0, lr1, lr2, group_sizes, G_W0_W2, 
 
             def mm(w, a):
                 y = _f(w, exact) @ a.T
-                return y if exact else y.to(torch.bfloat16).double()
+                return y if exact else y.to(torch.bfloat16).to(_ACC)
 
             x02 = mm(W0_W2[b, e], k)
             gy = mm(G_W0_W2[b, e], k)
