@@ -324,6 +324,8 @@ class MoeSweep:
         self.lrp = [e(1, N) for _ in range(3)]
         self.dy, self.hl = e(1, N, 2 * I), e(1, N, I)
         self.dW02, self.dW1 = e(1, E, 2 * I, D), e(1, E, D, I)
+        s1b = L.lib().uttt_update_stage1_workspace_bytes(1, I, N)
+        self.ws_s1, self.ws_s1_bytes = e(s1b, dt=torch.uint8), s1b
         if cfg["train"]:
             self.gW02, self.gW1 = e(1, E, 2 * I, D), e(1, E, D, I)
             self.gK, self.gV = e(1, N, D), e(1, N, D)
@@ -332,11 +334,47 @@ class MoeSweep:
             self.ws_bwd, self.ws_bwd_bytes = e(wsb, dt=torch.uint8), wsb
         self.stream = torch.cuda.current_stream(dev).cuda_stream
         self.events = None
+        self.batched = None
+
+    def prepare_batched(self, layers):
+        """Inputs and buffers of the cross-layer batched UPDATE: the k, v, lr and
+        routing of all `layers` writers of a chunk concatenated along the token
+        axis (writer l uses input set l % NSETS), so one grouped UPDATE call
+        produces sum_l dW_l -- the reference's aggregate write sums the
+        writers' raw gradients (modeling_recurrent_lact.py:2428-2445) -- and
+        its backward the per-writer k, v, lr gradients."""
+        import torch
+
+        L, E, D, I, k = self.L, self.E, self.D, self.I, self.k
+        sets = [self.sets[l % self.NSETS] for l in range(layers)]
+        T = self.T * layers
+        N = k * T
+        bt = dict(T=T, N=N, layers=layers)
+        bt["k"] = torch.cat([st["k"] for st in sets], dim=1).contiguous()
+        bt["v"] = torch.cat([st["v"] for st in sets], dim=1).contiguous()
+        bt["lr"] = [torch.cat([st["lr"][j] for st in sets], dim=1).contiguous() for j in range(3)]
+        bt["mask"] = torch.cat([st["mask_u"] for st in sets], dim=2).contiguous()
+        bt["gates"] = torch.cat([st["gates_u"] for st in sets], dim=2).contiguous()
+        bt["gs"] = bt["mask"].sum(-1).to(torch.int32).contiguous()
+        e = lambda *shape, dt=torch.bfloat16: torch.empty(*shape, dtype=dt, device=self.dev)
+        bt["rmap"] = e(1, T, 2 * E + 1, dt=torch.int32)
+        bt["ws_map"] = e(L.lib().uttt_row_id_map_workspace_bytes(1, T, E), dt=torch.uint8)
+        bt["kp"], bt["vp"] = e(1, N, D), e(1, N, D)
+        bt["lrp"] = [e(1, N) for _ in range(3)]
+        bt["dy"], bt["hl"] = e(1, N, 2 * I), e(1, N, I)
+        s1b = L.lib().uttt_update_stage1_workspace_bytes(1, I, N)
+        bt["ws_s1"], bt["ws_s1_bytes"] = e(s1b, dt=torch.uint8), s1b
+        if self.cfg["train"]:
+            bt["gK"], bt["gV"] = e(1, N, D), e(1, N, D)
+            bt["glr"] = [e(1, N) for _ in range(3)]
+            wsb = L.lib().uttt_update_bwd_workspace_bytes(1, I, N)
+            bt["ws_bwd"], bt["ws_bwd_bytes"] = e(wsb, dt=torch.uint8), wsb
+        self.batched = bt
 
     # algorithmic FLOPs per launch, NID = N * I * D
     def flops(self):
         nid = self.N * self.I * self.D
-        return {"gate_up": 4 * nid, "down_proj": 2 * nid, "update_s1": 6 * nid,
+        return {"gate_up": 4 * nid, "down_proj": 2 * nid, "update_s1(2 launches)": 6 * nid,
                 "wgrad": 6 * nid, "update_bwd_s1": 12 * nid, "grad_k": 8 * nid, "grad_v": 4 * nid,
                 "wgrad_bwd": 6 * nid}
 
@@ -370,44 +408,62 @@ class MoeSweep:
         self._mark(None)
 
     def update(self, st):
-        L, E, D, I, T, N, s = self.L, self.E, self.D, self.I, self.T, self.N, self.stream
-        m, p, gs = st["mask_u"], st["gates_u"], st["gs_u"]
-        lr = st["lr"]
-        self._mark("row_map")
+        """One writer's UPDATE (the reference's per-layer call pattern)."""
+        buf = dict(T=self.T, N=self.N, k=st["k"], v=st["v"], lr=st["lr"], mask=st["mask_u"],
+                   gates=st["gates_u"], gs=st["gs_u"], rmap=self.rmap, ws_map=self.ws_map,
+                   kp=self.kp, vp=self.vp, lrp=self.lrp, dy=self.dy, hl=self.hl,
+                   ws_s1=self.ws_s1, ws_s1_bytes=self.ws_s1_bytes)
+        if self.cfg["train"]:
+            buf.update(gK=self.gK, gV=self.gV, glr=self.glr, ws_bwd=self.ws_bwd,
+                       ws_bwd_bytes=self.ws_bwd_bytes)
+        self._update(buf)
+
+    def update_batched(self):
+        self._update(self.batched)
+
+    def _update(self, bt):
+        L, E, D, I, s = self.L, self.E, self.D, self.I, self.stream
+        T, N = bt["T"], bt["N"]
+        m, p, gs, lr = bt["mask"], bt["gates"], bt["gs"], bt["lr"]
+        self._mark("row_map(update)")
         L.call("uttt_make_row_id_map", L.ptr(m), 1, m.stride(0), m.stride(1), m.stride(2), 1, T,
-               E, L.ptr(self.rmap), None, L.ptr(self.ws_map), self.ws_map.numel(), s)
+               E, L.ptr(bt["rmap"]), None, L.ptr(bt["ws_map"]), bt["ws_map"].numel(), s)
         self._mark("permute_kv_lrs")
-        L.call("uttt_permute_kv_lrs_fwd", L.ptr(st["k"]), L.BF16, L.ptr(st["v"]), L.BF16,
-               L.ptr(lr[0]), L.ptr(lr[1]), L.ptr(lr[2]), 2, 1, T, D, L.ptr(self.rmap), E,
-               L.ptr(p), p.stride(0), p.stride(1), p.stride(2), L.ptr(self.kp), L.ptr(self.vp),
-               L.ptr(self.lrp[0]), L.ptr(self.lrp[1]), L.ptr(self.lrp[2]), N, s)
-        self._mark("update_s1")
-        L.call("uttt_grouped_update_stage1", L.ptr(self.W02), L.ptr(self.W1), L.ptr(self.kp),
-               L.ptr(self.vp), L.ptr(self.lrp[0]), L.ptr(self.lrp[1]), L.ptr(self.lrp[2]), L.BF16,
-               L.ptr(gs), 1, E, I, D, N, L.ptr(self.dy), L.ptr(self.hl), 1, s)
+        L.call("uttt_permute_kv_lrs_fwd", L.ptr(bt["k"]), L.BF16, L.ptr(bt["v"]), L.BF16,
+               L.ptr(lr[0]), L.ptr(lr[1]), L.ptr(lr[2]), 2, 1, T, D, L.ptr(bt["rmap"]), E,
+               L.ptr(p), p.stride(0), p.stride(1), p.stride(2), L.ptr(bt["kp"]), L.ptr(bt["vp"]),
+               L.ptr(bt["lrp"][0]), L.ptr(bt["lrp"][1]), L.ptr(bt["lrp"][2]), N, s)
+        self._mark("update_s1(2 launches)")
+        L.call("uttt_grouped_update_stage1", L.ptr(self.W02), L.ptr(self.W1), L.ptr(bt["kp"]),
+               L.ptr(bt["vp"]), L.ptr(bt["lrp"][0]), L.ptr(bt["lrp"][1]), L.ptr(bt["lrp"][2]),
+               L.BF16, L.ptr(gs), 1, E, I, D, N, L.ptr(bt["dy"]), L.ptr(bt["hl"]), 1,
+               L.ptr(bt["ws_s1"]), bt["ws_s1_bytes"], s)
         self._mark("wgrad")
-        L.call("uttt_grouped_wgrad_pair", L.ptr(self.dy), L.ptr(self.kp), L.ptr(self.hl),
-               L.ptr(self.vp), L.ptr(gs), 1, E, I, D, N, L.ptr(self.dW02), L.ptr(self.dW1), s)
+        L.call("uttt_grouped_wgrad_pair", L.ptr(bt["dy"]), L.ptr(bt["kp"]), L.ptr(bt["hl"]),
+               L.ptr(bt["vp"]), L.ptr(gs), 1, E, I, D, N, L.ptr(self.dW02), L.ptr(self.dW1), s)
         if self.cfg["train"]:
             self._mark("update_bwd(5 launches)")
-            L.call("uttt_grouped_update_bwd", L.ptr(self.W02), L.ptr(self.W1), L.ptr(self.kp),
-                   L.ptr(self.vp), L.ptr(self.lrp[0]), L.ptr(self.lrp[1]), L.ptr(self.lrp[2]),
-                   L.BF16, L.ptr(gs), L.ptr(self.GW02), L.ptr(self.GW1), 1, E, I, D, N,
-                   L.ptr(self.gW02), L.ptr(self.gW1), L.ptr(self.gK), L.ptr(self.gV),
-                   L.ptr(self.glr[0]), L.ptr(self.glr[1]), L.ptr(self.glr[2]),
-                   L.ptr(self.ws_bwd), self.ws_bwd_bytes, s)
+            L.call("uttt_grouped_update_bwd", L.ptr(self.W02), L.ptr(self.W1), L.ptr(bt["kp"]),
+                   L.ptr(bt["vp"]), L.ptr(bt["lrp"][0]), L.ptr(bt["lrp"][1]),
+                   L.ptr(bt["lrp"][2]), L.BF16, L.ptr(gs), L.ptr(self.GW02), L.ptr(self.GW1), 1,
+                   E, I, D, N, L.ptr(self.gW02), L.ptr(self.gW1), L.ptr(bt["gK"]),
+                   L.ptr(bt["gV"]), L.ptr(bt["glr"][0]), L.ptr(bt["glr"][1]),
+                   L.ptr(bt["glr"][2]), L.ptr(bt["ws_bwd"]), bt["ws_bwd_bytes"], s)
         self._mark(None)
 
-    def sweep(self, layers, chunks):
+    def sweep(self, layers, chunks, batched):
         i = 0
         for c in range(chunks):
             for l in range(layers):
                 self.apply(self.sets[i % self.NSETS])
                 i += 1
             if c < chunks - 1:   # the last chunk is read but never written
-                for l in range(layers):
-                    self.update(self.sets[i % self.NSETS])
-                    i += 1
+                if batched:
+                    self.update_batched()
+                else:
+                    for l in range(layers):
+                        self.update(self.sets[i % self.NSETS])
+                        i += 1
 
 
 def _event_times(events):
@@ -427,27 +483,33 @@ def bench_moe(args, key):
     dev = torch.device("cuda", 0)
     sw = MoeSweep(cfg, dev)
     layers, chunks = cfg["L"], SEQ // CHUNK
-    # warmup: W sweeps untimed (at least one layer-chunk of each op)
+    batched = args.update_schedule == "batched"
+    if batched:
+        sw.prepare_batched(layers)
+    # warmup: W sweeps untimed
     for _ in range(max(args.warmup, 1)):
-        sw.sweep(1, 2)
+        sw.sweep(layers, 2, batched)
     torch.cuda.synchronize()
     walls = []
     for _ in range(args.steps):
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        sw.sweep(layers, chunks)
+        sw.sweep(layers, chunks, batched)
         torch.cuda.synchronize()
         walls.append(time.perf_counter() - t0)
     wall = statistics.mean(walls)
     # one more sweep with every launch bracketed by events (per-kernel table)
     sw.events = []
-    sw.sweep(layers, chunks)
+    sw.sweep(layers, chunks, batched)
     torch.cuda.synchronize()
     per = _event_times(sw.events)
     sw.events = None
 
     fl = sw.flops()
-    fl["update_bwd(5 launches)"] = 30 * sw.N * sw.I * sw.D
+    Nu = sw.batched["N"] if batched else sw.N   # routed rows per UPDATE call
+    nid_u = Nu * sw.I * sw.D
+    fl.update({"update_s1(2 launches)": 6 * nid_u, "wgrad": 6 * nid_u,
+               "update_bwd(5 launches)": 30 * nid_u})
     kern = {}
     for name, ts in per.items():
         t = statistics.mean(ts)
@@ -473,8 +535,11 @@ def bench_moe(args, key):
         config={"workload": cfg["label"], "seq_len": SEQ, "chunk": CHUNK, "layers": layers,
                 "experts": cfg["E"], "topk": TOPK, "d": cfg["D"], "expert_hidden": cfg["I"],
                 "routing": "Zipf(1.1) prior" if cfg["zipf"] else "N(0,1) logits + N(0,0.5) bias",
-                "step": "one sweep: apply on 16 chunks x L layers, update on 15 x L"
+                "step": "one sweep: apply on 16 chunks x L layers, update on 15 chunks x L writers"
                         + (" (+ update backward)" if cfg["train"] else ""),
+                "update_schedule": ("batched: the L writers of a chunk in one grouped UPDATE "
+                                    "call (aggregate write = sum of writer gradients)"
+                                    if batched else "per-layer: one UPDATE call per writer"),
                 "excluded": "router logits/top-k (inputs precomputed); write step"},
         roofline=dict(bound="mfma", kernel=dom, achieved=round(fl[dom] / t_dom / 1e12, 2),
                       peak=BF16_PEAK_TFLOPS, unit="TFLOP/s",
@@ -540,6 +605,9 @@ def main():
                     help="timed steps (default 20 for permute, 2 sweeps for the MoE workloads)")
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS))
+    ap.add_argument("--update-schedule", default="batched", choices=["batched", "per-layer"],
+                    help="MoE workloads: one grouped UPDATE per chunk over all writer layers "
+                         "(batched) or one per writer (per-layer)")
     ap.add_argument("--no-cpu-baseline", action="store_true",
                     help="skip the CPU baseline leg (profiling runs)")
     ap.add_argument("--copy-calibration", action="store_true",

@@ -175,22 +175,27 @@ int uttt_grouped_gemm_nt(const void* w, const void* x, const int32_t* group_size
 int uttt_grouped_gemm_tn(const void* w, const void* x, const int32_t* group_sizes, int B, int E,
                          int M, int K, int N, void* y, void* stream);
 
+/* Scratch bytes for uttt_grouped_update_stage1 at (B, I, N). */
+size_t uttt_update_stage1_workspace_bytes(int B, int I, int N);
+
 /* UPDATE, stage 1.  Replaces swiglu_backward_three_bmm_grouped_with_lr_triton
  * (L/triton_grouped_swiglu_bwd_with_lr_kernels.py:255-353; kernel :49-252).
  * w0_w2 [B,E,2I,D], w1 [B,E,D,I], k, v [B,N,D] (bf16); lr0/1/2 [B,N] of
  * lr_dtype (UTTT_F32/BF16/F16, widened to fp32) ->
  * dy0_dy2 ([B,2I,N] or token-major [B,N,2I]) and hidden ([B,I,N] or
  * [B,N,I]), bf16:
- *   Y0 = w0 k, Y2 = w2 k, DH = w1^T v;
+ *   Y0 = w0 k, Y2 = w2 k, DH = w1^T v (fp32, as the reference keeps it);
  *   DY0 = lr0 sig(Y0) Y2 DH (1 + Y0 (1 - sig(Y0))), DY2 = lr2 silu(Y0) DH,
  *   hidden = lr1 silu(Y0) Y2.
  * lr0 = lr1 = lr2 = NULL means lr = 1: the APPLY backward's three-GEMM pass
  * (swiglu_backward_three_bmm_grouped_triton,
- * L/triton_grouped_swiglu_bwd_kernels.py:49-320, with v = grad_out). */
+ * L/triton_grouped_swiglu_bwd_kernels.py:49-320, with v = grad_out).
+ * workspace: uttt_update_stage1_workspace_bytes(B, I, N) bytes (DH). */
 int uttt_grouped_update_stage1(const void* w0_w2, const void* w1, const void* k, const void* v,
                                const void* lr0, const void* lr1, const void* lr2, int lr_dtype,
                                const int32_t* group_sizes, int B, int E, int I, int D, int N,
-                               void* dy0_dy2, void* hidden, int token_major, void* stream);
+                               void* dy0_dy2, void* hidden, int token_major, void* workspace,
+                               size_t workspace_bytes, void* stream);
 
 /* UPDATE, stage 2 (weight gradients).  Replaces grouped_two_gemm_fw_bwd_triton
  * (L/triton_lact_bwd_grouped_two_mm_grad_fw.py:231-312; kernel :55-225) with

@@ -68,10 +68,11 @@ SIGNATURES = {
     "uttt_grouped_gemm_tn": (
         c_int, [c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int, c_p, c_p],
     ),
+    "uttt_update_stage1_workspace_bytes": (c_sz, [c_int, c_int, c_int]),
     "uttt_grouped_update_stage1": (
         c_int,
         [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_int, c_p, c_int, c_int, c_int, c_int, c_int,
-         c_p, c_p, c_int, c_p],
+         c_p, c_p, c_int, c_p, c_sz, c_p],
     ),
     "uttt_grouped_wgrad_pair": (
         c_int, [c_p, c_p, c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int, c_p, c_p, c_p],

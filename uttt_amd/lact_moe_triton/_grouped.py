@@ -103,9 +103,12 @@ def update_stage1(W0_W2, W1, K, V, lr0, lr1, lr2, group_sizes, token_major: bool
     else:
         DY = torch.empty((B, I2, N), dtype=torch.bfloat16, device=dev)
         H = torch.empty((B, I, N), dtype=torch.bfloat16, device=dev)
+    ws_bytes = L.lib().uttt_update_stage1_workspace_bytes(B, I, N)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     L.call("uttt_grouped_update_stage1", L.ptr(W0_W2), L.ptr(W1), L.ptr(K), L.ptr(V),
            L.ptr(lrs[0]), L.ptr(lrs[1]), L.ptr(lrs[2]), lr_code, L.ptr(gs),
-           B, E, I, D, N, L.ptr(DY), L.ptr(H), int(token_major), L.stream_of(K))
+           B, E, I, D, N, L.ptr(DY), L.ptr(H), int(token_major), L.ptr(ws), ws_bytes,
+           L.stream_of(K))
     return DY, H
 
 
