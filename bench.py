@@ -451,6 +451,40 @@ class MoeSweep:
                    L.ptr(bt["glr"][2]), L.ptr(bt["ws_bwd"]), bt["ws_bwd_bytes"], s)
         self._mark(None)
 
+    def time_isolated(self, batched, reps=5):
+        """Mean launch duration of each single-launch kernel of a sweep, timed
+        as `reps` back-to-back launches between two events on the stream."""
+        import torch
+
+        L, E, D, I, s = self.L, self.E, self.D, self.I, self.stream
+        st = self.sets[0]
+        bt = self.batched if batched else None
+        out = {}
+
+        def timed(name, fn):
+            fn()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            out[name] = e0.elapsed_time(e1) * 1e-3 / reps
+
+        N = self.N
+        timed("gate_up", lambda: L.call("uttt_grouped_gate_up", L.ptr(self.W02), L.ptr(self.xp),
+                                        L.ptr(st["gs_a"]), 1, E, I, D, N, L.ptr(self.hid), 1, s))
+        timed("down_proj", lambda: L.call("uttt_grouped_gemm_nt", L.ptr(self.W1), L.ptr(self.hid),
+                                          L.ptr(st["gs_a"]), 1, E, D, I, N, L.ptr(self.yp), s))
+        if bt is not None:
+            Nu, gs, kp, vp, dy, hl = bt["N"], bt["gs"], bt["kp"], bt["vp"], bt["dy"], bt["hl"]
+        else:
+            Nu, gs, kp, vp, dy, hl = N, st["gs_u"], self.kp, self.vp, self.dy, self.hl
+        timed("wgrad", lambda: L.call("uttt_grouped_wgrad_pair", L.ptr(dy), L.ptr(kp), L.ptr(hl),
+                                      L.ptr(vp), L.ptr(gs), 1, E, I, D, Nu, L.ptr(self.dW02),
+                                      L.ptr(self.dW1), s))
+        return out
+
     def sweep(self, layers, chunks, batched):
         i = 0
         for c in range(chunks):
@@ -505,6 +539,10 @@ def bench_moe(args, key):
     per = _event_times(sw.events)
     sw.events = None
 
+    # launch durations of the main kernels, each timed back to back between two
+    # HIP events on the launch stream (no host gaps inside the interval)
+    iso = sw.time_isolated(batched, reps=5)
+
     fl = sw.flops()
     Nu = sw.batched["N"] if batched else sw.N   # routed rows per UPDATE call
     nid_u = Nu * sw.I * sw.D
@@ -512,16 +550,30 @@ def bench_moe(args, key):
                "update_bwd(5 launches)": 30 * nid_u})
     kern = {}
     for name, ts in per.items():
-        t = statistics.mean(ts)
-        d = dict(us=round(t * 1e6, 2), launches_per_sweep=len(ts))
+        t = iso.get(name, statistics.mean(ts))
+        d = dict(us=round(t * 1e6, 2), launches_per_sweep=len(ts),
+                 timing="isolated loop" if name in iso else "in-sweep events")
         if name in fl:
             tf = fl[name] / t / 1e12
             d.update(TFLOPs=round(tf, 1), mfma_frac=round(tf / BF16_PEAK_TFLOPS, 4))
         kern[name] = d
-    # dominant MFMA kernel by time per sweep
+    # algorithmic HBM bytes per launch (each tensor once: the expert weights
+    # read, token activations read, outputs written; bf16)
+    E, D, I, N = sw.E, sw.D, sw.I, sw.N
+    by = {"gate_up": 2 * (E * 2 * I * D + N * D + N * I),
+          "down_proj": 2 * (E * D * I + N * I + N * D),
+          "wgrad": 2 * (Nu * 2 * I + Nu * D + Nu * I + Nu * D + 3 * E * I * D)}
+    for name, b in by.items():
+        if name in kern:
+            kern[name]["GBs"] = round(b / kern[name]["us"] / 1e3, 1)
+            kern[name]["hbm_frac"] = round(b / kern[name]["us"] / 1e3 / HBM_PEAK_GBS, 4)
+    # dominant single-kernel launch by time per sweep; its roofline is HBM
+    # when its arithmetic intensity is below the ridge (2.5 PFLOP/s / 8 TB/s)
     dom = max((n for n in kern if "TFLOPs" in kern[n] and "(" not in n),
               key=lambda n: kern[n]["us"] * kern[n]["launches_per_sweep"])
-    t_dom = statistics.mean(per[dom])
+    t_dom = iso.get(dom, statistics.mean(per[dom]))
+    ridge = BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
+    ai = fl[dom] / by[dom] if dom in by else float("inf")
     tokens = SEQ  # B = 1
     value = tokens / wall
     nid = sw.N * sw.I * sw.D
@@ -541,10 +593,17 @@ def bench_moe(args, key):
                                     "call (aggregate write = sum of writer gradients)"
                                     if batched else "per-layer: one UPDATE call per writer"),
                 "excluded": "router logits/top-k (inputs precomputed); write step"},
-        roofline=dict(bound="mfma", kernel=dom, achieved=round(fl[dom] / t_dom / 1e12, 2),
-                      peak=BF16_PEAK_TFLOPS, unit="TFLOP/s",
-                      frac=round(fl[dom] / t_dom / 1e12 / BF16_PEAK_TFLOPS, 4), traffic=None,
-                      algorithmic_flops=fl[dom], avg_launch_us=round(t_dom * 1e6, 2)),
+        roofline=(dict(bound="hbm", kernel=dom, achieved=round(by[dom] / t_dom / 1e9, 1),
+                       peak=HBM_PEAK_GBS, unit="GB/s",
+                       frac=round(by[dom] / t_dom / 1e9 / HBM_PEAK_GBS, 4), traffic=None,
+                       algorithmic_bytes=by[dom], algorithmic_flops=fl[dom],
+                       arithmetic_intensity=round(ai, 1), avg_launch_us=round(t_dom * 1e6, 2),
+                       mfma_frac=round(fl[dom] / t_dom / 1e12 / BF16_PEAK_TFLOPS, 4))
+                  if ai < ridge else
+                  dict(bound="mfma", kernel=dom, achieved=round(fl[dom] / t_dom / 1e12, 2),
+                       peak=BF16_PEAK_TFLOPS, unit="TFLOP/s",
+                       frac=round(fl[dom] / t_dom / 1e12 / BF16_PEAK_TFLOPS, 4), traffic=None,
+                       algorithmic_flops=fl[dom], avg_launch_us=round(t_dom * 1e6, 2))),
         sweep=dict(algorithmic_flops=sweep_flops,
                    TFLOPs=round(sweep_flops / wall / 1e12, 1),
                    mfma_frac=round(sweep_flops / wall / 1e12 / BF16_PEAK_TFLOPS, 4)),

@@ -1,30 +1,35 @@
 // Asynchronous MFMA GEMM pipeline for gfx950 (the core of every grouped
 // fast-weight GEMM).
 //
-// Workgroup: 256 threads = 4 waves in a 2x2 grid.  A workgroup multiplies two
-// 128-row A tiles (A0, A1) by one 128-row B tile per K step of kBK = 64 into
-// two fp32 accumulators (acc0 = A0 B^T, acc1 = A1 B^T); each wave owns a 64x64
-// quadrant of both, as 2x2 blocks of v_mfma_f32_32x32x16_bf16.
+// Workgroup: 256 threads = 4 waves in a 2x2 grid.  Per K step of kBK = 32 a
+// workgroup multiplies two 128-row A tiles (A0, A1) by a 256-row B tile (two
+// 128-row halves B0, B1) into two fp32 accumulators acc0 = A0 B^T and
+// acc1 = A1 B^T (each 128 x 256).  Wave (wm, wn) owns rows [64 wm, 64 wm + 64)
+// of both accumulators and columns [128 wn, 128 wn + 128): 2 x 4 blocks of
+// 32x32 per accumulator, each fed by v_mfma_f32_32x32x16_bf16 (fp32
+// accumulate), i.e. 16 MFMAs per 8 fragment reads.
 //
 // Global -> LDS: global_load_lds_dwordx4 (16 bytes per lane straight into LDS,
-// no register staging) into a ring of three stages, so the loads of step k+2
-// are in flight while step k is multiplied; the only waits are explicit
-// s_waitcnt vmcnt counts and one s_barrier per step.  Each stage lives in its
-// own __shared__ array so the compiler can tell the in-flight LDS writes from
-// the LDS reads of the current stage.
+// no register staging) into a ring of four 32 KiB stages, so the loads of
+// steps k+1..k+3 are in flight while step k is multiplied; the only waits are
+// explicit s_waitcnt vmcnt counts and one s_barrier per step.  Each stage lives
+// in its own __shared__ array so the compiler can tell the in-flight LDS
+// writes from the LDS reads of the current stage.
 //
 // LDS tile layouts (16-byte chunks, XOR-swizzled against bank conflicts):
-//   KMajor tile (operand stored [rows][K], K contiguous): 128 rows x 8 chunks;
-//     chunk c of row r sits at slot r*8 + (c ^ (r & 7)).  Fragments are one
+//   KMajor tile (operand stored [rows][K], K contiguous): 128 rows x 4 chunks;
+//     chunk c of row r sits at slot r*4 + (c ^ kswz(r)).  Fragments are one
 //     ds_read_b128 (8 consecutive k of one row).
-//   RMajor tile (operand stored [K][rows], rows contiguous): 64 k-rows x 16
-//     chunks; chunk c of k-row k sits at slot k*16 + (c ^ swz(k)).  Fragments
+//   RMajor tile (operand stored [K][rows], rows contiguous): 32 k-rows x 16
+//     chunks; chunk c of k-row k sits at slot k*16 + (c ^ rswz(k)).  Fragments
 //     are two ds_read_b64_tr_b16: within a group of 16 lanes, source lane
 //     s = 4j + q reads k-row j, rows 4q..4q+3, and the hardware hands lane i
 //     the column i of that 4x16 block, i.e. 4 consecutive k of row i.
 // Lanes whose chunk lies outside the operand read a 16-byte zero block, so
 // partial tiles need no special casing in the MFMA loop.
 #pragma once
+
+#include <utility>
 
 #include "common.h"
 
@@ -37,12 +42,14 @@ typedef short i16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kThreads = 256;
-constexpr int kBK = 64;
-constexpr int kTileRows = 128;
-constexpr int kTileBytes = kTileRows * kBK * 2;                  // 16 KiB
-constexpr int kStageBytes = 3 * kTileBytes;                      // A0 | A1 | B
-constexpr int kLoadsPerTile = kTileBytes / 16 / kThreads;        // 4 per thread
-constexpr int kLoadsPerStage = 3 * kLoadsPerTile;                // 12 per wave
+constexpr int kBK = 32;
+constexpr int kTileRows = 128;                                   // rows per LDS tile
+constexpr int kBRows = 2 * kTileRows;                            // B rows per workgroup
+constexpr int kTileBytes = kTileRows * kBK * 2;                  // 8 KiB
+constexpr int kStageBytes = 4 * kTileBytes;                      // A0 | A1 | B0 | B1
+constexpr int kLoadsPerTile = kTileBytes / 16 / kThreads;        // 2 per thread
+constexpr int kLoadsPerStage = 4 * kLoadsPerTile;                // 8 per wave
+constexpr int kNB = 4;                                           // 32-col blocks per wave
 
 enum Major { KMajor = 0, RMajor = 1 };
 
@@ -74,33 +81,77 @@ struct Operand {
   int k_end;
 };
 
-__device__ __forceinline__ int rswz(int k) { return ((k & 7) << 1) & 15; }
+// Swizzles.  A 16-lane group of ds_read_b128 reads 16 consecutive rows of one
+// logical chunk; rows are 64 bytes, so row r sits in quarter (r & 3) of a
+// 256-byte bank line and the 4 rows sharing a quarter must use 4 different
+// chunk slots: slot = c ^ ((r >> 2) & 3).  A 32-lane half of
+// ds_read_b64_tr_b16 reads 4 k-rows x 4 chunks (a 64-byte aligned block) of
+// 256-byte rows; XOR with 4 * (k & 3) sends the 4 k-rows to 4 different
+// 64-byte blocks of the bank line.
+__device__ __forceinline__ int kswz(int r) { return (r >> 2) & 3; }
+__device__ __forceinline__ int rswz(int k) { return (k & 3) << 2; }
 
-// Issue this wave's share (kLoadsPerTile instructions) of the loads of the
-// 128-row x kBK tile at (r0, k0) of `op` into the LDS tile at `dst`.
+// Per-lane state of the loads of one 128-row x kBK tile of an operand for a
+// whole K loop: the element offsets of this lane's kLoadsPerTile chunks
+// relative to the tile origin, their k position (for the k-range test) and
+// whether their row is valid (fixed for the workgroup).
 template <int MAJOR>
-__device__ __forceinline__ void load_tile(const Operand& op, int r0, int k0, uint8_t* dst) {
-  const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
-#pragma unroll
-  for (int t = 0; t < kLoadsPerTile; ++t) {
-    const int base = (t * 4 + w) * 64;  // first slot of this instruction
-    const int s = base + lane;
-    const void* src = &g_zero16;
+struct TileLoader {
+  const uint16_t* base;   // operand element (r0, 0)
+  int64_t kstep;          // elements advanced per K step
+  int k_end;
+  int off[kLoadsPerTile];
+  int kk[kLoadsPerTile];  // k of the lane's chunk inside the tile
+  bool rok[kLoadsPerTile];
+
+  __device__ __forceinline__ void init(const Operand& op, int r0) {
+    const int lane = threadIdx.x & 63;
+    const int w = threadIdx.x >> 6;
+    k_end = op.k_end;
     if constexpr (MAJOR == KMajor) {
-      const int r = s >> 3;
-      const int c = (s & 7) ^ (r & 7);
-      const int gr = r0 + r, gk = k0 + c * 8;
-      if (gr < op.r_end && gk < op.k_end) src = op.base + (int64_t)gr * op.ld + gk;
+      base = op.base + (int64_t)r0 * op.ld;
+      kstep = kBK;
     } else {
-      const int k = s >> 4;
-      const int c = (s & 15) ^ rswz(k);
-      const int gk = k0 + k, gr = r0 + c * 8;
-      if (gk < op.k_end && gr < op.r_end) src = op.base + (int64_t)gk * op.ld + gr;
+      base = op.base + r0;
+      kstep = (int64_t)kBK * op.ld;
     }
-    __builtin_amdgcn_global_load_lds(src, UTTT_LDS(dst + base * 16), 16, 0, 0);
+#pragma unroll
+    for (int t = 0; t < kLoadsPerTile; ++t) {
+      const int s = (t * 4 + w) * 64 + lane;
+      if constexpr (MAJOR == KMajor) {
+        const int r = s >> 2;
+        const int c = (s & 3) ^ kswz(r);
+        off[t] = r * (int)op.ld + c * 8;
+        kk[t] = c * 8;
+        rok[t] = r0 + r < op.r_end;
+      } else {
+        const int k = s >> 4;
+        const int c = (s & 15) ^ rswz(k);
+        off[t] = k * (int)op.ld + c * 8;
+        kk[t] = k;
+        rok[t] = r0 + c * 8 < op.r_end;
+      }
+    }
   }
-}
+
+  // Issue this wave's loads of K step `step` into the LDS tile at `dst`.
+  __device__ __forceinline__ void load(int step, uint8_t* dst) const {
+    const int w = threadIdx.x >> 6;
+    const int k0 = step * kBK;
+    const uint16_t* b = base + kstep * step;
+    const uintptr_t zero = reinterpret_cast<uintptr_t>(&g_zero16);
+#pragma unroll
+    for (int t = 0; t < kLoadsPerTile; ++t) {
+      // branch-free select (a branch here would split the straight-line path
+      // the wait-count pass needs, see run_pipeline)
+      const uintptr_t a = reinterpret_cast<uintptr_t>(b + off[t]);
+      const bool ok = rok[t] & (k0 + kk[t] < k_end);
+      const uintptr_t src = ok ? a : zero;
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
+                                       UTTT_LDS(dst + (t * 4 + w) * 64 * 16), 16, 0, 0);
+    }
+  }
+};
 
 // MFMA operand fragment of rows [rb, rb+32), k-substep ks (16 k) of an LDS tile.
 template <int MAJOR>
@@ -109,7 +160,7 @@ __device__ __forceinline__ bf16x8 frag(const uint8_t* tile, int rb, int ks) {
   if constexpr (MAJOR == KMajor) {
     const int r = rb + (lane & 31);
     const int c = 2 * ks + (lane >> 5);
-    return *reinterpret_cast<const bf16x8*>(tile + (r * 8 + (c ^ (r & 7))) * 16);
+    return *reinterpret_cast<const bf16x8*>(tile + (r * 4 + (c ^ kswz(r))) * 16);
   } else {
     const int g = lane >> 4, s = lane & 15;
     const int j = s >> 2, q = s & 3;
@@ -128,66 +179,104 @@ __device__ __forceinline__ bf16x8 frag(const uint8_t* tile, int rb, int ks) {
   }
 }
 
-// acc_a[i][j] += A_a(wave rows i) * B(wave cols j) over one stage, a = 0, 1.
+// Fragments of one stage: both k-substeps of B (this wave's 4 column blocks)
+// and of A0 / A1 (this wave's 2 row blocks).
+struct StageFrags {
+  bf16x8 b[kBK / 16][kNB], a0[kBK / 16][2], a1[kBK / 16][2];
+};
+
 template <int AMAJ, int BMAJ>
-__device__ __forceinline__ void mma_stage(f32x16 (&acc0)[2][2], f32x16 (&acc1)[2][2],
-                                          const uint8_t* st, int wm, int wn, bool two) {
+__device__ __forceinline__ void read_stage(StageFrags& f, const uint8_t* st, int wm, int wn) {
   const uint8_t* a0 = st;
   const uint8_t* a1 = st + kTileBytes;
-  const uint8_t* b = st + 2 * kTileBytes;
+  const uint8_t* b = st + (2 + wn) * kTileBytes;  // this wave's B half
 #pragma unroll
   for (int ks = 0; ks < kBK / 16; ++ks) {
-    bf16x8 fb[2], fa[2];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) fb[j] = frag<BMAJ>(b, wn * 64 + j * 32, ks);
+    for (int j = 0; j < kNB; ++j) f.b[ks][j] = frag<BMAJ>(b, j * 32, ks);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) fa[i] = frag<AMAJ>(a0, wm * 64 + i * 32, ks);
+    for (int i = 0; i < 2; ++i) f.a0[ks][i] = frag<AMAJ>(a0, wm * 64 + i * 32, ks);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) f.a1[ks][i] = frag<AMAJ>(a1, wm * 64 + i * 32, ks);
+  }
+}
+
+// acc_a[i][j] += A_a(wave rows i) * B(wave cols j) over one stage, a = 0, 1.
+__device__ __forceinline__ void mma_frags(f32x16 (&acc0)[2][kNB], f32x16 (&acc1)[2][kNB],
+                                          const StageFrags& f) {
+#pragma unroll
+  for (int ks = 0; ks < kBK / 16; ++ks) {
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
-        acc0[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc0[i][j], 0, 0, 0);
-    if (two) {
+      for (int j = 0; j < kNB; ++j)
+        acc0[i][j] =
+            __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a0[ks][i], f.b[ks][j], acc0[i][j], 0, 0, 0);
 #pragma unroll
-      for (int i = 0; i < 2; ++i) fa[i] = frag<AMAJ>(a1, wm * 64 + i * 32, ks);
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc1[i][j] =
-              __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc1[i][j], 0, 0, 0);
-    }
+      for (int j = 0; j < kNB; ++j)
+        acc1[i][j] =
+            __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a1[ks][i], f.b[ks][j], acc1[i][j], 0, 0, 0);
   }
 }
 
-// Three-stage ring: load(step, stage) issues kLoadsPerStage loads per wave;
-// mma(stage) consumes one.  Step kt waits for its own loads while step kt+1's
-// may still be in flight, then issues step kt+2 into the stage step kt-1 used.
-template <class LoadFn, class MmaFn>
-__device__ __forceinline__ void run_pipeline(int nk, LoadFn&& load, MmaFn&& mma, uint8_t* s0,
-                                             uint8_t* s1, uint8_t* s2) {
-  if (nk > 0) load(0, s0);
-  if (nk > 1) load(1, s1);
-  auto step = [&](int kt, uint8_t* cur, uint8_t* nxt) {
-    if (kt + 1 < nk)
-      wait_vmcnt<kLoadsPerStage>();
-    else
-      wait_vmcnt<0>();
+// Four-stage ring: load(step, stage) issues kLoadsPerStage loads per wave;
+// read(stage) fetches the stage's MFMA fragments into registers and mma()
+// consumes them.  Step kt waits for its own loads while those of steps kt+1
+// and kt+2 are still in flight, reads its fragments, then issues step kt+3
+// into the stage step kt-1 used and runs the MFMAs.  Two rules keep the
+// compiler from inserting a wait for every outstanding load (vmcnt(0)) before
+// LDS reads, which would serialise the pipeline: the loads are issued
+// unconditionally (steps past the end read the zero block), since its
+// wait-count pass tracks LDS DMA per __shared__ array only along straight-line
+// paths; and the stage's fragment reads are issued before the step's new
+// loads (scheduling barriers keep that order).
+template <class LoadFn, class ReadFn, class MmaFn>
+__device__ __forceinline__ void run_pipeline(int nk, LoadFn&& load, ReadFn&& read, MmaFn&& mma,
+                                             uint8_t* s0, uint8_t* s1, uint8_t* s2,
+                                             uint8_t* s3) {
+  load(0, s0);
+  load(1, s1);
+  load(2, s2);
+  auto step = [&](int kt, const uint8_t* cur, uint8_t* nxt) {
+    wait_vmcnt<2 * kLoadsPerStage>();
     block_barrier();
-    if (kt + 2 < nk) load(kt + 2, nxt);
-    mma(cur);
+    read(cur);
+    __builtin_amdgcn_sched_barrier(0);
+    load(kt + 3, nxt);
+    __builtin_amdgcn_sched_barrier(0);
+    mma();
   };
-  for (int kt = 0; kt < nk; kt += 3) {
-    step(kt, s0, s2);
-    if (kt + 1 < nk) step(kt + 1, s1, s0);
-    if (kt + 2 < nk) step(kt + 2, s2, s1);
+  int kt = 0;
+  for (; kt + 4 <= nk; kt += 4) {
+    step(kt, s0, s3);
+    step(kt + 1, s1, s0);
+    step(kt + 2, s2, s1);
+    step(kt + 3, s3, s2);
   }
+  if (kt < nk) step(kt, s0, s3);
+  if (kt + 1 < nk) step(kt + 1, s1, s0);
+  if (kt + 2 < nk) step(kt + 2, s2, s1);
+  wait_vmcnt<0>();  // drain the loads issued past the end
 }
 
-template <int N>
-__device__ __forceinline__ void zero(f32x16 (&acc)[N][N]) {
+// f(std::integral_constant<int, i>) for i = 0 .. N-1 with compile-time i, so
+// that accumulator indices stay constants whatever the unroller decides (a
+// runtime index would move the accumulator arrays to scratch memory).
+template <class F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+template <int M, int N>
+__device__ __forceinline__ void zero(f32x16 (&acc)[M][N]) {
 #pragma unroll
-  for (int i = 0; i < N; ++i)
+  for (int i = 0; i < M; ++i)
 #pragma unroll
     for (int j = 0; j < N; ++j)
 #pragma unroll
@@ -200,12 +289,6 @@ __device__ __forceinline__ int acc_row(int v) {
   return 8 * (v >> 2) + 4 * ((threadIdx.x & 63) >> 5) + (v & 3);
 }
 __device__ __forceinline__ int acc_col() { return threadIdx.x & 31; }
-
-}  // namespace pipe
-}  // namespace uttt
-
-namespace uttt {
-namespace pipe {
 
 // ------------------------------------------------------------ scheduling ----
 // Token-grouped problems (N = routed tokens): the tokens of expert e in batch

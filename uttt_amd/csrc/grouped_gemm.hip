@@ -9,7 +9,7 @@
 // Two kernel families:
 //   tn_kernel  token-grouped products Y[n, m] = sum_k A[m, k] X[n, k] for the
 //              tokens n of each expert: two 128-row A tiles against one
-//              128-token tile, with a problem-specific epilogue (SwiGLU for the
+//              256-token tile, with a problem-specific epilogue (SwiGLU for the
 //              APPLY, the lr-scaled SwiGLU' for the UPDATE, the second-order
 //              SwiGLU pass for the UPDATE backward, or a plain store).  An
 //              optional second operand pair is chained along K (grad_K =
@@ -42,43 +42,37 @@ struct TnArgs {
 };
 
 // Loop over this wave's accumulator quads: f(t, r, n, v[4]) with tile t, tile
-// row r (rows r..r+3 hold v[0..3]) and tile token column n.
+// row r (rows r..r+3 hold v[0..3]) and tile token column n.  Indices are
+// compile-time (static_for) so the accumulators stay in registers.
 template <class F>
-__device__ __forceinline__ void for_quads(const f32x16 (&acc0)[2][2], const f32x16 (&acc1)[2][2],
+__device__ __forceinline__ void for_quads(const f32x16 (&acc0)[2][kNB], const f32x16 (&acc1)[2][kNB],
                                           int wm, int wn, bool two, F&& f) {
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    if (t == 1 && !two) break;
-    const f32x16(&acc)[2][2] = t == 0 ? acc0 : acc1;
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float v[4] = {acc[i][j][q * 4], acc[i][j][q * 4 + 1], acc[i][j][q * 4 + 2],
-                              acc[i][j][q * 4 + 3]};
-          f(t, wm * 64 + i * 32 + acc_row(q * 4), wn * 64 + j * 32 + acc_col(), v);
-        }
-  }
+  static_for<2 * 2 * kNB * 4>([&](auto idx) __attribute__((always_inline)) {
+    constexpr int t = idx / (2 * kNB * 4);
+    constexpr int i = (idx / (kNB * 4)) % 2;
+    constexpr int j = (idx / 4) % kNB;
+    constexpr int q = idx % 4;
+    if (t == 1 && !two) return;
+    const f32x16& a = t == 0 ? acc0[i][j] : acc1[i][j];
+    const float v[4] = {a[q * 4], a[q * 4 + 1], a[q * 4 + 2], a[q * 4 + 3]};
+    f(t, wm * 64 + i * 32 + acc_row(q * 4), wn * 128 + j * 32 + acc_col(), v);
+  });
 }
 
 // Paired quads of the two accumulators (same rows of A0 and A1): f(r, n, a[4], b[4]).
 template <class F>
-__device__ __forceinline__ void for_pairs(const f32x16 (&acc0)[2][2], const f32x16 (&acc1)[2][2],
+__device__ __forceinline__ void for_pairs(const f32x16 (&acc0)[2][kNB], const f32x16 (&acc1)[2][kNB],
                                           int wm, int wn, F&& f) {
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float a[4] = {acc0[i][j][q * 4], acc0[i][j][q * 4 + 1], acc0[i][j][q * 4 + 2],
-                            acc0[i][j][q * 4 + 3]};
-        const float b[4] = {acc1[i][j][q * 4], acc1[i][j][q * 4 + 1], acc1[i][j][q * 4 + 2],
-                            acc1[i][j][q * 4 + 3]};
-        f(wm * 64 + i * 32 + acc_row(q * 4), wn * 64 + j * 32 + acc_col(), a, b);
-      }
+  static_for<2 * kNB * 4>([&](auto idx) __attribute__((always_inline)) {
+    constexpr int i = idx / (kNB * 4);
+    constexpr int j = (idx / 4) % kNB;
+    constexpr int q = idx % 4;
+    const float a[4] = {acc0[i][j][q * 4], acc0[i][j][q * 4 + 1], acc0[i][j][q * 4 + 2],
+                        acc0[i][j][q * 4 + 3]};
+    const float b[4] = {acc1[i][j][q * 4], acc1[i][j][q * 4 + 1], acc1[i][j][q * 4 + 2],
+                        acc1[i][j][q * 4 + 3]};
+    f(wm * 64 + i * 32 + acc_row(q * 4), wn * 128 + j * 32 + acc_col(), a, b);
+  });
 }
 
 struct TileCtx {
@@ -96,10 +90,10 @@ struct EpiStore {
     int col_end[2];  // stored while that column < col_end[t]
     int N;
   };
-  __device__ __forceinline__ static void apply(const Args& ea, const f32x16 (&acc0)[2][2],
-                               const f32x16 (&acc1)[2][2], const TileCtx& c, bool two) {
+  __device__ __forceinline__ static void apply(const Args& ea, const f32x16 (&acc0)[2][kNB],
+                               const f32x16 (&acc1)[2][kNB], const TileCtx& c, bool two) {
     OutT* ob = ea.out + (int64_t)c.b * ea.N * ea.ld;
-    for_quads(acc0, acc1, c.wm, c.wn, two, [&](int t, int r, int n, const float* v) {
+    for_quads(acc0, acc1, c.wm, c.wn, two, [&](int t, int r, int n, const float* v) __attribute__((always_inline)) {
       const int col = c.m0 + ea.col_off[t] + r;
       if (c.tt.n0 + n < c.tt.size && col < ea.col_end[t])
         store4(ob, ea.ld, c.tt.start + c.tt.n0 + n, col, v[0], v[1], v[2], v[3]);
@@ -113,10 +107,10 @@ struct EpiSwiGLU {
     uint16_t* out;
     int I, N, token_major;
   };
-  __device__ __forceinline__ static void apply(const Args& ea, const f32x16 (&acc0)[2][2],
-                               const f32x16 (&acc1)[2][2], const TileCtx& c, bool) {
+  __device__ __forceinline__ static void apply(const Args& ea, const f32x16 (&acc0)[2][kNB],
+                               const f32x16 (&acc1)[2][kNB], const TileCtx& c, bool) {
     uint16_t* hb = ea.out + (int64_t)c.b * ea.N * ea.I;
-    for_pairs(acc0, acc1, c.wm, c.wn, [&](int r, int n, const float* y0, const float* y2) {
+    for_pairs(acc0, acc1, c.wm, c.wn, [&](int r, int n, const float* y0, const float* y2) __attribute__((always_inline)) {
       const int m = c.m0 + r;
       if (c.tt.n0 + n >= c.tt.size || m >= ea.I) return;
       const int tok = c.tt.start + c.tt.n0 + n;
@@ -145,13 +139,13 @@ struct EpiS1 {
     uint16_t* hid;    // [B, N, I] or [B, I, N]
     int I, N, token_major;
   };
-  __device__ __forceinline__ static void apply(const Args& ea, const f32x16 (&acc0)[2][2],
-                               const f32x16 (&acc1)[2][2], const TileCtx& c, bool) {
+  __device__ __forceinline__ static void apply(const Args& ea, const f32x16 (&acc0)[2][kNB],
+                               const f32x16 (&acc1)[2][kNB], const TileCtx& c, bool) {
     const int I = ea.I, I2 = 2 * I;
     const float* dhb = ea.dh + (int64_t)c.b * ea.N * I;
     uint16_t* dyb = ea.dy + (int64_t)c.b * ea.N * I2;
     uint16_t* hb = ea.hid + (int64_t)c.b * ea.N * I;
-    for_pairs(acc0, acc1, c.wm, c.wn, [&](int r, int n, const float* y0, const float* y2) {
+    for_pairs(acc0, acc1, c.wm, c.wn, [&](int r, int n, const float* y0, const float* y2) __attribute__((always_inline)) {
       const int m = c.m0 + r;
       if (c.tt.n0 + n >= c.tt.size || m >= I) return;
       const int tok = c.tt.start + c.tt.n0 + n;
@@ -202,79 +196,84 @@ struct EpiBwd {
     float* lr_part;
     int I, N, B, m_tiles;
   };
-  __device__ __forceinline__ static void apply(const Args& ea, const f32x16 (&acc0)[2][2],
-                               const f32x16 (&acc1)[2][2], const TileCtx& c, bool) {
-    __shared__ float red[3][2][128];
+  __device__ __forceinline__ static void apply(const Args& ea, const f32x16 (&acc0)[2][kNB],
+                               const f32x16 (&acc1)[2][kNB], const TileCtx& c, bool) {
+    __shared__ float red[3][2][kBRows];
     const int I = ea.I, I2 = 2 * I;
     const int64_t bo2 = (int64_t)c.b * ea.N * I2, bo1 = (int64_t)c.b * ea.N * I;
     // per-lane partial lr sums for the two token columns j = 0, 1 of this lane
-    float s[3][2] = {{0.f, 0.f}, {0.f, 0.f}, {0.f, 0.f}};
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int n = c.wn * 64 + j * 32 + acc_col();
-        const bool nvalid = c.tt.n0 + n < c.tt.size;
-        const int tok = c.tt.start + c.tt.n0 + n;
-        float L0 = 0.f, L1 = 0.f, L2 = 0.f;
-        if (nvalid) {
-          const int64_t li = (int64_t)c.b * ea.N + tok;
-          L0 = LR::load(ea.lr0[li]);
-          L1 = LR::load(ea.lr1[li]);
-          L2 = LR::load(ea.lr2[li]);
-        }
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int m = c.m0 + c.wm * 64 + i * 32 + acc_row(q * 4);
-          if (!nvalid || m >= I) continue;
-          float gd0[4], gd2[4], dh[4], gd[4];
-          load4(ea.gy + bo2, I2, tok, m, gd0);
-          load4(ea.gy + bo2, I2, tok, I + m, gd2);
-          load4(ea.dhg + bo2, I2, tok, m, dh);
-          load4(ea.dhg + bo2, I2, tok, I + m, gd);
-          float o_gdh[4], o_gx0[4], o_gx2[4], o_dx0[4], o_dx2[4], o_hl[4];
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const float x0 = bf16r(acc0[i][j][q * 4 + u]);
-            const float x2 = bf16r(acc1[i][j][q * 4 + u]);
-            const float sg = sigmoidf_(x0);
-            const float silu = sg * x0;
-            const float mul = sg * (1.0f + x0 * (1.0f - sg));  // silu'(x0)
-            const float ds = sg * (1.0f - sg);                  // sigmoid'(x0)
-            o_gdh[u] = gd0[u] * L0 * x2 * mul + gd2[u] * L2 * silu;
-            o_gx2[u] = gd0[u] * L0 * dh[u] * mul + gd[u] * L1 * silu;
-            const float gsig = gd0[u] * L0 * dh[u] * x2 * (1.0f + x0 - 2.0f * sg * x0);
-            o_gx0[u] = (gd2[u] * L2 * dh[u] + gd[u] * L1 * x2) * mul +
-                       gd0[u] * L0 * dh[u] * x2 * ds + gsig * ds;
-            s[0][j] += gd0[u] * dh[u] * x2 * mul;
-            s[1][j] += gd[u] * x2 * silu;
-            s[2][j] += gd2[u] * dh[u] * silu;
-            o_dx0[u] = dh[u] * x2 * mul * L0;
-            o_dx2[u] = silu * dh[u] * L2;
-            o_hl[u] = L1 * x2 * silu;
-          }
-          store4(ea.gdh + bo1, I, tok, m, o_gdh[0], o_gdh[1], o_gdh[2], o_gdh[3]);
-          store4(ea.gx + bo2, I2, tok, m, o_gx0[0], o_gx0[1], o_gx0[2], o_gx0[3]);
-          store4(ea.gx + bo2, I2, tok, I + m, o_gx2[0], o_gx2[1], o_gx2[2], o_gx2[3]);
-          store4(ea.dx + bo2, I2, tok, m, o_dx0[0], o_dx0[1], o_dx0[2], o_dx0[3]);
-          store4(ea.dx + bo2, I2, tok, I + m, o_dx2[0], o_dx2[1], o_dx2[2], o_dx2[3]);
-          store4(ea.hlr + bo1, I, tok, m, o_hl[0], o_hl[1], o_hl[2], o_hl[3]);
-        }
+    float s[3][kNB] = {};
+    float L[kNB][3];
+    int tokj[kNB];
+    bool nv[kNB];
+    static_for<kNB>([&](auto jj) __attribute__((always_inline)) {
+      constexpr int j = jj;
+      const int n = c.wn * 128 + j * 32 + acc_col();
+      nv[j] = c.tt.n0 + n < c.tt.size;
+      tokj[j] = c.tt.start + c.tt.n0 + n;
+      L[j][0] = L[j][1] = L[j][2] = 0.f;
+      if (nv[j]) {
+        const int64_t li = (int64_t)c.b * ea.N + tokj[j];
+        L[j][0] = LR::load(ea.lr0[li]);
+        L[j][1] = LR::load(ea.lr1[li]);
+        L[j][2] = LR::load(ea.lr2[li]);
       }
+    });
+    static_for<2 * kNB * 4>([&](auto idx) __attribute__((always_inline)) {
+      constexpr int i = idx / (kNB * 4);
+      constexpr int j = (idx / 4) % kNB;
+      constexpr int q = idx % 4;
+      const int m = c.m0 + c.wm * 64 + i * 32 + acc_row(q * 4);
+      if (!nv[j] || m >= I) return;
+      const int tok = tokj[j];
+      const float L0 = L[j][0], L1 = L[j][1], L2 = L[j][2];
+      float gd0[4], gd2[4], dh[4], gd[4];
+      load4(ea.gy + bo2, I2, tok, m, gd0);
+      load4(ea.gy + bo2, I2, tok, I + m, gd2);
+      load4(ea.dhg + bo2, I2, tok, m, dh);
+      load4(ea.dhg + bo2, I2, tok, I + m, gd);
+      float o_gdh[4], o_gx0[4], o_gx2[4], o_dx0[4], o_dx2[4], o_hl[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float x0 = bf16r(acc0[i][j][q * 4 + u]);
+        const float x2 = bf16r(acc1[i][j][q * 4 + u]);
+        const float sg = sigmoidf_(x0);
+        const float silu = sg * x0;
+        const float mul = sg * (1.0f + x0 * (1.0f - sg));  // silu'(x0)
+        const float ds = sg * (1.0f - sg);                  // sigmoid'(x0)
+        o_gdh[u] = gd0[u] * L0 * x2 * mul + gd2[u] * L2 * silu;
+        o_gx2[u] = gd0[u] * L0 * dh[u] * mul + gd[u] * L1 * silu;
+        const float gsig = gd0[u] * L0 * dh[u] * x2 * (1.0f + x0 - 2.0f * sg * x0);
+        o_gx0[u] = (gd2[u] * L2 * dh[u] + gd[u] * L1 * x2) * mul +
+                   gd0[u] * L0 * dh[u] * x2 * ds + gsig * ds;
+        s[0][j] += gd0[u] * dh[u] * x2 * mul;
+        s[1][j] += gd[u] * x2 * silu;
+        s[2][j] += gd2[u] * dh[u] * silu;
+        o_dx0[u] = dh[u] * x2 * mul * L0;
+        o_dx2[u] = silu * dh[u] * L2;
+        o_hl[u] = L1 * x2 * silu;
+      }
+      store4(ea.gdh + bo1, I, tok, m, o_gdh[0], o_gdh[1], o_gdh[2], o_gdh[3]);
+      store4(ea.gx + bo2, I2, tok, m, o_gx0[0], o_gx0[1], o_gx0[2], o_gx0[3]);
+      store4(ea.gx + bo2, I2, tok, I + m, o_gx2[0], o_gx2[1], o_gx2[2], o_gx2[3]);
+      store4(ea.dx + bo2, I2, tok, m, o_dx0[0], o_dx0[1], o_dx0[2], o_dx0[3]);
+      store4(ea.dx + bo2, I2, tok, I + m, o_dx2[0], o_dx2[1], o_dx2[2], o_dx2[3]);
+      store4(ea.hlr + bo1, I, tok, m, o_hl[0], o_hl[1], o_hl[2], o_hl[3]);
+    });
     // lanes l and l^32 hold the same token column (other rows); then the two
     // waves of one column half (wm = 0, 1) meet in LDS
 #pragma unroll
     for (int k = 0; k < 3; ++k)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) s[k][j] += __shfl_xor(s[k][j], 32, 64);
+      for (int j = 0; j < kNB; ++j) s[k][j] += __shfl_xor(s[k][j], 32, 64);
     if ((threadIdx.x & 63) < 32) {
 #pragma unroll
       for (int k = 0; k < 3; ++k)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) red[k][c.wm][c.wn * 64 + j * 32 + acc_col()] = s[k][j];
+        for (int j = 0; j < kNB; ++j) red[k][c.wm][c.wn * 128 + j * 32 + acc_col()] = s[k][j];
     }
     __syncthreads();
-    if (threadIdx.x < 128) {
+    if (threadIdx.x < kBRows) {
       const int n = threadIdx.x;
       if (c.tt.n0 + n < c.tt.size) {
         const int64_t plane = (int64_t)ea.m_tiles * ea.B * ea.N;
@@ -291,13 +290,14 @@ __global__ __launch_bounds__(kThreads) void tn_kernel(TnArgs a, typename Epi::Ar
   __shared__ __attribute__((aligned(16))) uint8_t st0[kStageBytes];
   __shared__ __attribute__((aligned(16))) uint8_t st1[kStageBytes];
   __shared__ __attribute__((aligned(16))) uint8_t st2[kStageBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t st3[kStageBytes];
   __shared__ int scratch[4];
 
   const int bid = blockIdx.x;
   const int mt = bid % a.m_tiles;
   const int nt = (bid / a.m_tiles) % a.n_tiles_ub;
   const int b = bid / (a.m_tiles * a.n_tiles_ub);
-  const TokenTile tt = find_token_tile<kTileRows>(a.gs + (int64_t)b * a.E, a.E, a.N, nt, scratch);
+  const TokenTile tt = find_token_tile<kBRows>(a.gs + (int64_t)b * a.E, a.E, a.N, nt, scratch);
   if (tt.e < 0) return;
   const int m0 = mt * a.m_step;
 
@@ -313,33 +313,42 @@ __global__ __launch_bounds__(kThreads) void tn_kernel(TnArgs a, typename Epi::Ar
   const int r0 = m0 + a.row_off[0], r1 = m0 + a.row_off[1];
   const bool two = a.two != 0;
 
-  f32x16 acc0[2][2], acc1[2][2];
+  f32x16 acc0[2][kNB], acc1[2][kNB];
   zero(acc0);
   zero(acc1);
+  TileLoader<AMAJ> la0, la1;
+  TileLoader<KMajor> lx0, lx1;
+  la0.init(A00, r0);
+  la1.init(A01, r1);
+  lx0.init(X0, tt.n0);
+  lx1.init(X0, tt.n0 + kTileRows);
   auto load = [&](int kt, uint8_t* st) {
-    if (kt < nk0) {
-      const int k0 = kt * kBK;
-      load_tile<AMAJ>(A00, r0, k0, st);
-      load_tile<AMAJ>(A01, r1, k0, st + kTileBytes);
-      load_tile<KMajor>(X0, tt.n0, k0, st + 2 * kTileBytes);
-    } else {
-      const int k0 = (kt - nk0) * kBK;
-      load_tile<AMAJ>(A10, r0, k0, st);
-      load_tile<AMAJ>(A11, r1, k0, st + kTileBytes);
-      load_tile<KMajor>(X1, tt.n0, k0, st + 2 * kTileBytes);
+    if (kt == nk0) {  // switch to the second operand pair (chained K)
+      la0.init(A10, r0);
+      la1.init(A11, r1);
+      lx0.init(X1, tt.n0);
+      lx1.init(X1, tt.n0 + kTileRows);
     }
+    const int step = kt < nk0 ? kt : kt - nk0;
+    la0.load(step, st);
+    la1.load(step, st + kTileBytes);
+    lx0.load(step, st + 2 * kTileBytes);
+    lx1.load(step, st + 3 * kTileBytes);
   };
   const int w = threadIdx.x >> 6;
   const int wm = w >> 1, wn = w & 1;
-  auto mma = [&](const uint8_t* st) { mma_stage<AMAJ, KMajor>(acc0, acc1, st, wm, wn, two); };
-  run_pipeline(nk0 + nk1, load, mma, st0, st1, st2);
+  StageFrags fr;
+  auto read = [&](const uint8_t* st) { read_stage<AMAJ, KMajor>(fr, st, wm, wn); };
+  auto mma = [&]() { mma_frags(acc0, acc1, fr); };
+  (void)two;
+  run_pipeline(nk0 + nk1, load, read, mma, st0, st1, st2, st3);
   const TileCtx c{b, m0, wm, wn, mt, tt};
   Epi::apply(ea, acc0, acc1, c, two);
 }
 
 // ======================================================= weight gradients ==
 // out[b, e, x, y] = sum_{n in seg(b,e)} P[b, n, y] Q[b, n, x]; P [B, N, Y] and
-// Q [B, N, X] token-major.  A tile = 2 x 128 rows of y, B tile = 128 rows of
+// Q [B, N, X] token-major.  A tile = 2 x 128 rows of y, B tile = 256 rows of
 // x, so every lane holds four consecutive y of one x: 8-byte stores along the
 // contiguous y axis.  Up to two tasks share a launch.
 struct WgTask {
@@ -356,6 +365,7 @@ __global__ __launch_bounds__(kThreads) void wg_kernel(WgTask t0, WgTask t1,
   __shared__ __attribute__((aligned(16))) uint8_t st0[kStageBytes];
   __shared__ __attribute__((aligned(16))) uint8_t st1[kStageBytes];
   __shared__ __attribute__((aligned(16))) uint8_t st2[kStageBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t st3[kStageBytes];
 
   const int n0_tiles = t0.y_tiles * t0.x_tiles;
   const int per_group = n0_tiles + t1.y_tiles * t1.x_tiles;
@@ -367,7 +377,7 @@ __global__ __launch_bounds__(kThreads) void wg_kernel(WgTask t0, WgTask t1,
   const WgTask& tk = first ? t0 : t1;
   const int tl = first ? t : t - n0_tiles;
   const int y0 = (tl / tk.x_tiles) * 2 * kTileRows;
-  const int x0 = (tl % tk.x_tiles) * kTileRows;
+  const int x0 = (tl % tk.x_tiles) * kBRows;
   const int X = tk.X, Y = tk.Y;
 
   int start, size;
@@ -375,22 +385,29 @@ __global__ __launch_bounds__(kThreads) void wg_kernel(WgTask t0, WgTask t1,
   const Operand P{tk.p + ((int64_t)b * N + start) * Y, Y, Y, size};
   const Operand Q{tk.q + ((int64_t)b * N + start) * X, X, X, size};
 
-  f32x16 acc0[2][2], acc1[2][2];
+  f32x16 acc0[2][kNB], acc1[2][kNB];
   zero(acc0);
   zero(acc1);
+  TileLoader<RMajor> lp0, lp1, lq0, lq1;
+  lp0.init(P, y0);
+  lp1.init(P, y0 + kTileRows);
+  lq0.init(Q, x0);
+  lq1.init(Q, x0 + kTileRows);
   auto load = [&](int kt, uint8_t* st) {
-    const int k0 = kt * kBK;
-    load_tile<RMajor>(P, y0, k0, st);
-    load_tile<RMajor>(P, y0 + kTileRows, k0, st + kTileBytes);
-    load_tile<RMajor>(Q, x0, k0, st + 2 * kTileBytes);
+    lp0.load(kt, st);
+    lp1.load(kt, st + kTileBytes);
+    lq0.load(kt, st + 2 * kTileBytes);
+    lq1.load(kt, st + 3 * kTileBytes);
   };
   const int w = threadIdx.x >> 6;
   const int wm = w >> 1, wn = w & 1;
-  auto mma = [&](const uint8_t* st) { mma_stage<RMajor, RMajor>(acc0, acc1, st, wm, wn, true); };
-  run_pipeline((size + kBK - 1) / kBK, load, mma, st0, st1, st2);
+  StageFrags fr;
+  auto read = [&](const uint8_t* st) { read_stage<RMajor, RMajor>(fr, st, wm, wn); };
+  auto mma = [&]() { mma_frags(acc0, acc1, fr); };
+  run_pipeline((size + kBK - 1) / kBK, load, read, mma, st0, st1, st2, st3);
 
   uint16_t* ob = tk.out + ((int64_t)b * E + e) * X * Y;
-  for_quads(acc0, acc1, wm, wn, true, [&](int tt, int r, int n, const float* v) {
+  for_quads(acc0, acc1, wm, wn, true, [&](int tt, int r, int n, const float* v) __attribute__((always_inline)) {
     const int y = y0 + tt * kTileRows + r;
     const int x = x0 + n;
     if (y < Y && x < X) store4(ob, Y, x, y, v[0], v[1], v[2], v[3]);
@@ -485,7 +502,7 @@ TnArgs tn_args(const void* a0, const void* a1, const void* x, int K, int64_t lda
   t.row_end[1] = end1;
   t.m_step = m_step;
   t.m_tiles = (M_rows + m_step - 1) / m_step;
-  t.n_tiles_ub = (N + kTileRows - 1) / kTileRows + E;
+  t.n_tiles_ub = (N + kBRows - 1) / kBRows + E;
   t.E = E;
   t.N = N;
   t.two = 1;
@@ -528,7 +545,7 @@ WgTask wg_task(const void* p, const void* q, void* out, int X, int Y) {
   t.X = X;
   t.Y = Y;
   t.y_tiles = (Y + 2 * kTileRows - 1) / (2 * kTileRows);
-  t.x_tiles = (X + kTileRows - 1) / kTileRows;
+  t.x_tiles = (X + kBRows - 1) / kBRows;
   return t;
 }
 
