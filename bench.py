@@ -73,6 +73,22 @@ def _routing(T, E, k, seed, device, zipf=None):
     return mask, gates, g
 
 
+def _profile_traffic(summary, kernel):
+    """HBM bytes per launch of `kernel` as measured by the rocprofv3 PMC passes
+    (FETCH_SIZE and WRITE_SIZE, scaled by the copy calibration) recorded in
+    profiles/<summary> ("traffic_bytes <kernel> <bytes>"); None if absent."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", summary)
+    try:
+        with open(path) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) == 3 and parts[0] == "traffic_bytes" and parts[1] == kernel:
+                    return int(parts[2])
+    except OSError:
+        pass
+    return None
+
+
 def bench_permute(args):
     import torch
 
@@ -102,38 +118,50 @@ def bench_permute(args):
     stream = torch.cuda.current_stream(dev).cuda_stream
     BF16 = L.BF16
 
-    def step(s, ev=None):
-        p = s["gates"]
-        if ev is not None:
-            ev[0].record()
+    def rowmap(s):
         L.call("uttt_make_row_id_map", L.ptr(s["mask"]), 1, s["mask"].stride(0),
                s["mask"].stride(1), s["mask"].stride(2), B, T, E, L.ptr(s["rmap"]),
                L.ptr(s["gs"]), L.ptr(ws), ws_bytes, stream)
-        if ev is not None:
-            ev[1].record()
+
+    def permute(s):
+        p = s["gates"]
         L.call("uttt_permute_fwd", L.ptr(s["x"]), BF16, B, T, D, L.ptr(s["rmap"]), E,
                L.ptr(p), p.stride(0), p.stride(1), p.stride(2), L.ptr(s["xp"]), k * T,
                L.ptr(s["pp"]), stream)
-        if ev is not None:
-            ev[2].record()
+
+    def unpermute(s):
+        p = s["gates"]
         L.call("uttt_unpermute_fwd", L.ptr(s["xp"]), BF16, B, k * T, D, L.ptr(s["rmap"]), T, E,
                L.ptr(p), p.stride(0), p.stride(1), p.stride(2), L.ptr(s["y"]), stream)
-        if ev is not None:
-            ev[3].record()
+
+    def step(s):
+        rowmap(s)
+        permute(s)
+        unpermute(s)
+
+    def timed(fn, reps):
+        """Mean duration of `reps` back-to-back launches over the rotating
+        buffer sets, between two events on the launch stream."""
+        e0, e1 = _events(2)
+        e0.record()
+        for i in range(reps):
+            fn(sets[i % nsets])
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e-3 / reps
 
     for i in range(args.warmup):
         step(sets[i % nsets])
     torch.cuda.synchronize()
-    evs = [_events(4) for _ in range(args.steps)]
-    torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(sets[i % nsets], evs[i])
-    torch.cuda.synchronize()
+    t_step = timed(step, args.steps)
     wall = time.perf_counter() - t0
-    t_map = [e[0].elapsed_time(e[1]) * 1e-3 for e in evs]
-    t_perm = [e[1].elapsed_time(e[2]) * 1e-3 for e in evs]
-    t_unp = [e[2].elapsed_time(e[3]) * 1e-3 for e in evs]
+    reps = max(3 * args.steps, 30)
+    t_map = timed(rowmap, reps)
+    t_p = timed(permute, reps)
+    t_u = timed(unpermute, reps)
+    # practical streaming ceiling on the same buffers: a plain device copy
+    t_copy = timed(lambda s: s["y"].copy_(s["x"]), reps)
 
     # algorithmic bytes (each tensor once): permute reads x and the k row ids
     # per token and writes k copies; unpermute reads the k rows, their gates
@@ -143,9 +171,7 @@ def bench_permute(args):
     unp_bytes = k * T * row + k * T * (4 + 4) + T * row
     map_bytes = E * T * 1 + T * (2 * E + 1) * 4
     step_bytes = perm_bytes + unp_bytes
-    t_p = statistics.mean(t_perm)
-    t_u = statistics.mean(t_unp)
-    value = step_bytes / (t_p + t_u) / 1e9
+    value = (step_bytes + map_bytes) / t_step / 1e9
 
     # sanity: the HIP path ran and produced the unpermute∘permute invariant
     s = sets[(args.steps - 1) % nsets]
@@ -158,28 +184,32 @@ def bench_permute(args):
         metric="permute+unpermute GB/s (algorithmic bytes)",
         value=round(value, 2),
         unit="GB/s",
-        ms_per_step=round(wall / args.steps * 1e3, 4),
+        ms_per_step=round(t_step * 1e3, 4),
+        wall_ms_per_step=round(wall / args.steps * 1e3, 4),
         dtype="bf16",
         config={"workload": "uttt-moe permute/unpermute microbench (configs[2])", "T": T, "E": E,
                 "topk": k, "hidden": D, "payload": "bf16", "buffer_sets": nsets},
         roofline=dict(
-            bound="hbm", kernel="permute_fwd_kernel",
+            bound="hbm", kernel="permute_chunk_kernel",
             achieved=round(perm_bytes / t_p / 1e9, 2), peak=HBM_PEAK_GBS, unit="GB/s",
-            frac=round(perm_bytes / t_p / 1e9 / HBM_PEAK_GBS, 4), traffic=None,
+            frac=round(perm_bytes / t_p / 1e9 / HBM_PEAK_GBS, 4),
+            traffic=_profile_traffic("permute_unpermute_c2.txt", "permute_chunk_kernel"),
             algorithmic_bytes=perm_bytes, avg_launch_us=round(t_p * 1e6, 3),
         ),
         kernels={
-            "row_id_map(3 launches)": dict(us=round(statistics.mean(t_map) * 1e6, 3),
-                                           GBs=round(map_bytes / statistics.mean(t_map) / 1e9, 1)),
-            "permute_fwd_kernel": dict(us=round(t_p * 1e6, 3), GBs=round(perm_bytes / t_p / 1e9, 1),
+            "row_id_map(3 launches)": dict(us=round(t_map * 1e6, 3),
+                                           GBs=round(map_bytes / t_map / 1e9, 1)),
+            "permute_chunk_kernel": dict(us=round(t_p * 1e6, 3), GBs=round(perm_bytes / t_p / 1e9, 1),
                                        hbm_frac=round(perm_bytes / t_p / 1e9 / HBM_PEAK_GBS, 4)),
-            "unpermute_fwd_kernel": dict(us=round(t_u * 1e6, 3),
+            "device_copy(x -> y)": dict(us=round(t_copy * 1e6, 3),
+                                        GBs=round(2 * T * row / t_copy / 1e9, 1)),
+            "unpermute_chunk_kernel": dict(us=round(t_u * 1e6, 3),
                                          GBs=round(unp_bytes / t_u / 1e9, 1),
                                          hbm_frac=round(unp_bytes / t_u / 1e9 / HBM_PEAK_GBS, 4)),
         },
     )
     if not args.no_cpu_baseline:
-        res["cpu_baseline"] = cpu_baseline_permute(sets[0], B, T, E, k, D, step_bytes)
+        res["cpu_baseline"] = cpu_baseline_permute(sets[0], B, T, E, k, D, step_bytes + map_bytes)
     return res
 
 

@@ -129,6 +129,30 @@ def test_unpermute_fwd_bit_exact(dtype, H, T, E):
     assert torch.equal(bits(out), bits(ref))
 
 
+@pytest.mark.parametrize("dtype,H", [(torch.bfloat16, 256), (torch.float32, 36)])
+def test_permute_unpermute_topk4_ragged(dtype, H):
+    # top-4 with dropped slots: slots past the first two take the kernels'
+    # general loop, tokens with 0..4 slots mix within one wave
+    B, T, E, k = 2, 1537, 12, 4
+    g = torch.Generator().manual_seed(17)
+    scores = torch.rand(B, E, T, generator=g)
+    mask = torch.zeros(B, E, T, dtype=torch.bool).scatter_(1, scores.topk(k, 1).indices, True)
+    mask &= torch.rand(B, E, T, generator=g) > 0.25
+    probs = torch.rand(B, E, T, generator=g) * mask
+    probs[:, :, 3] = 0.0  # a token whose every gate is zero
+    x = torch.randn(B, T, H, generator=g).to(dtype)
+    out, pp, rm = TP.permute_with_expert_mask(x.to(DEV), mask.to(DEV), probs.to(DEV), k)
+    ref_rm = OP.make_row_id_map(mask)
+    assert torch.equal(rm.cpu(), ref_rm)
+    ref_out, ref_pp = OP.permute(x, ref_rm, probs, k * T)
+    wr = OP.written_rows(ref_rm, k * T)
+    assert torch.equal(bits(out)[wr], bits(ref_out)[wr])
+    assert torch.equal(pp.cpu()[wr], ref_pp[wr])
+    y = torch.randn(B, k * T, H, generator=g).to(dtype)
+    merged = TP.unpermute_and_merge_with_probs(y.to(DEV), rm, probs.to(DEV))
+    assert torch.equal(bits(merged), bits(OP.unpermute(y, ref_rm, probs, T)))
+
+
 def test_unpermute_strided_probs():
     # probs given as a [B, T, E] tensor viewed [B, E, T] (P:835-839)
     T, E, H, k = 1000, 8, 64, 2

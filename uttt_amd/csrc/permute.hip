@@ -14,9 +14,11 @@
 //           last, the reference's stale values in columns [n, E)).
 // No atomics are used, so the result is deterministic by construction.
 //
-// Payload kernels give one 64-lane wave to one token and move its row in
-// 16-byte vectors: permute reads the row once and writes it to each of the
-// token's slots; unpermute gathers the slots and reduces in fp32 registers.
+// Payload kernels move rows in 16-byte vectors: permute reads a token's row
+// once and writes it to each of the token's slots; unpermute gathers the slots
+// and reduces in fp32 registers.  The forward pair spreads (token, chunk)
+// pairs over all lanes; the backward and k/v/lr kernels give one 64-lane wave
+// to one token.
 #include "common.h"
 
 namespace uttt {
@@ -26,23 +28,53 @@ constexpr int kTile = 256;         // tokens per row-map workgroup
 constexpr int kMaxExperts = 128;   // row-map LDS tables are sized for this
 constexpr int kTokPerBlock = 4;    // payload kernels: 4 waves = 4 tokens
 
-__device__ __forceinline__ bool mask_bit(const void* map, int mask_bytes, int64_t idx) {
-  if (mask_bytes == 1) return reinterpret_cast<const uint8_t*>(map)[idx] != 0;
+template <int MB>
+__device__ __forceinline__ bool mask_bit(const void* map, int64_t idx) {
+  if constexpr (MB == 1) return reinterpret_cast<const uint8_t*>(map)[idx] != 0;
   return reinterpret_cast<const int32_t*>(map)[idx] != 0;
 }
 
+// Selection bits of one token (bit e of word e / 32).  All mask loads of a
+// 32-expert group are issued before any of them is used, so a tile pays one
+// memory latency per group rather than one per expert.
+template <int MB>
+__device__ __forceinline__ void load_mask_bits(const void* map, int64_t base, int64_t s_e, int E,
+                                               bool valid, uint32_t bits[kMaxExperts / 32]) {
+#pragma unroll
+  for (int g = 0; g < kMaxExperts / 32; ++g) {
+    bits[g] = 0u;
+    if (32 * g < E) {
+      bool bv[32];
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        const int e = 32 * g + i;
+        bv[i] = valid && e < E && mask_bit<MB>(map, base + (int64_t)e * s_e);
+      }
+#pragma unroll
+      for (int i = 0; i < 32; ++i) bits[g] |= (uint32_t)bv[i] << i;
+    }
+  }
+}
+
+__device__ __forceinline__ bool bit_of(const uint32_t bits[kMaxExperts / 32], int e) {
+  const uint32_t w = e < 32 ? bits[0] : e < 64 ? bits[1] : e < 96 ? bits[2] : bits[3];
+  return (w >> (e & 31)) & 1u;
+}
+
 // ------------------------------------------------------------ row map ------
+template <int MB>
 __global__ __launch_bounds__(kTile) void rowmap_count_kernel(
-    const void* map, int mask_bytes, int64_t s_b, int64_t s_e, int64_t s_t, int T, int E,
-    int ntiles, int32_t* counts) {
+    const void* map, int64_t s_b, int64_t s_e, int64_t s_t, int T, int E, int ntiles,
+    int32_t* counts) {
   __shared__ int wcnt[kTile / kWave][kMaxExperts];
   const int tile = blockIdx.x, b = blockIdx.y;
   const int t = tile * kTile + threadIdx.x;
   const int w = threadIdx.x / kWave;
   const int64_t base = (int64_t)b * s_b + (int64_t)t * s_t;
+  uint32_t bits[kMaxExperts / 32];
+  load_mask_bits<MB>(map, base, s_e, E, t < T, bits);
   for (int e = 0; e < E; ++e) {
-    bool bit = (t < T) && mask_bit(map, mask_bytes, base + (int64_t)e * s_e);
-    uint64_t bal = __ballot(bit);
+    const uint64_t bal = __ballot(bit_of(bits, e));
     if (lane_id() == 0) wcnt[w][e] = __popcll(bal);
   }
   __syncthreads();
@@ -114,20 +146,27 @@ __global__ __launch_bounds__(kScanThreads) void rowmap_scan_kernel(int32_t* coun
   }
 }
 
+// STAGE: the tile's packed entries (kTile x (2E+1) int32, contiguous in the
+// output) are assembled in LDS and written out with consecutive lanes on
+// consecutive words; without it each lane stores its own entry directly,
+// which strides the lanes 4 * (2E+1) bytes apart.
+constexpr int kStageMaxW = 63;  // STAGE needs kTile * (2E+1) * 4 <= 63 KiB of LDS
+
+template <int MB, bool STAGE>
 __global__ __launch_bounds__(kTile) void rowmap_emit_kernel(
-    const void* map, int mask_bytes, int64_t s_b, int64_t s_e, int64_t s_t, int T, int E,
-    int ntiles, const int32_t* offsets, int32_t* row_id_map) {
+    const void* map, int64_t s_b, int64_t s_e, int64_t s_t, int T, int E, int ntiles,
+    const int32_t* offsets, int32_t* row_id_map) {
+  extern __shared__ int32_t stage[];
   __shared__ int wcnt[kTile / kWave][kMaxExperts];
   __shared__ int toff[kMaxExperts];
   const int tile = blockIdx.x, b = blockIdx.y;
   const int t = tile * kTile + threadIdx.x;
   const int w = threadIdx.x / kWave;
   const int64_t base = (int64_t)b * s_b + (int64_t)t * s_t;
-  uint32_t bits[kMaxExperts / 32] = {0u, 0u, 0u, 0u};
+  uint32_t bits[kMaxExperts / 32];
+  load_mask_bits<MB>(map, base, s_e, E, t < T, bits);
   for (int e = 0; e < E; ++e) {
-    bool bit = (t < T) && mask_bit(map, mask_bytes, base + (int64_t)e * s_e);
-    bits[e >> 5] |= (uint32_t)bit << (e & 31);
-    uint64_t bal = __ballot(bit);
+    const uint64_t bal = __ballot(bit_of(bits, e));
     if (lane_id() == 0) wcnt[w][e] = __popcll(bal);
   }
   for (int e = threadIdx.x; e < E; e += kTile)
@@ -136,10 +175,10 @@ __global__ __launch_bounds__(kTile) void rowmap_emit_kernel(
 
   const int n = __popc(bits[0]) + __popc(bits[1]) + __popc(bits[2]) + __popc(bits[3]);
   const int W = 2 * E + 1;
-  int32_t* row = row_id_map + ((int64_t)b * T + t) * W;
+  int32_t* row = STAGE ? stage + threadIdx.x * W : row_id_map + ((int64_t)b * T + t) * W;
   int j = 0;
   for (int e = E - 1; e >= 0; --e) {
-    const bool bit = (bits[e >> 5] >> (e & 31)) & 1u;
+    const bool bit = bit_of(bits, e);
     const uint64_t bal = __ballot(bit);  // every lane of the wave takes part
     if (t < T) {
       int r = -1;
@@ -157,15 +196,23 @@ __global__ __launch_bounds__(kTile) void rowmap_emit_kernel(
     for (int c = E + n; c < 2 * E; ++c) row[c] = 0;
     row[2 * E] = n;
   }
+  if constexpr (STAGE) {
+    __syncthreads();
+    const int nt = min(kTile, T - tile * kTile);
+    int32_t* g = row_id_map + ((int64_t)b * T + (int64_t)tile * kTile) * W;
+    for (int i = threadIdx.x; i < nt * W; i += kTile) g[i] = stage[i];
+  }
 }
 
 // ---------------------------------------------------------- vector copy ----
 template <int VB>
 struct Vec;
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 template <>
-struct Vec<16> { using T = uint4; };
+struct Vec<16> { using T = u32x4_t; };
 template <>
-struct Vec<8> { using T = uint2; };
+struct Vec<8> { using T = u32x2_t; };
 template <>
 struct Vec<4> { using T = uint32_t; };
 template <>
@@ -182,6 +229,190 @@ inline int pick_vec_bytes(int64_t row_bytes, std::initializer_list<const void*> 
 }
 
 __device__ __forceinline__ int64_t tok_index(int b, int t, int T) { return (int64_t)b * T + t; }
+
+// ------------------------------------------------- chunked payload kernels --
+// The hot permute / unpermute kernels spread the flat (token, chunk) space of
+// the payload over all lanes: thread i handles the 16-byte chunks
+// base + u * 256 (u < CU) of the flattened B*T x CH grid, so every lane moves
+// full vectors whatever the row length.  A thread issues all its independent
+// loads first -- the payload chunk and the row-map entries of slots 0 and 1,
+// then the probs, then (unpermute) the gathered rows -- so the dependent chain
+// row map -> probs -> payload costs one memory latency per level rather than
+// one per slot.  Slots past the first two (top-k > 2) take a plain loop.  The
+// row-map entries of a token are re-read by its CH chunk threads and hit in
+// cache.  Outputs are written once and never re-read by the kernel, so they go
+// out as non-temporal stores.
+constexpr int kCT = 256;     // threads per workgroup
+constexpr int kCU = 2;       // chunks per thread
+constexpr bool kNT = true;   // non-temporal payload stores
+
+template <bool NT, class V>
+__device__ __forceinline__ void store_vec(V* p, const V& v) {
+  if constexpr (NT) {
+    __builtin_nontemporal_store(v, p);
+  } else {
+    *p = v;
+  }
+}
+
+// Row-map entries of slots 0 and 1.  Columns [n, E) of the expert half hold
+// 0 and, for E == 1, column E + 1 is the count: the expert index of a slot
+// that is not routed is forced to 0 so that it addresses a valid probs entry.
+struct Slots2 {
+  int n, r0, r1, e0, e1;
+};
+__device__ __forceinline__ Slots2 load_slots2(const int32_t* __restrict__ rm, int E) {
+  Slots2 s;
+  s.n = rm[2 * E];
+  s.r0 = rm[0];
+  s.r1 = rm[1];
+  s.e0 = rm[E];
+  s.e1 = rm[E + 1];
+  if (s.n < 1) s.e0 = 0;
+  if (s.n < 2) s.e1 = 0;
+  return s;
+}
+
+template <int VB, int CU, bool NT>
+__global__ __launch_bounds__(kCT) void permute_chunk_kernel(
+    const uint8_t* __restrict__ inp, int64_t row_bytes, int CH, int BT, int T,
+    const int32_t* __restrict__ rmap, int E, const float* __restrict__ probs, int64_t p_sb,
+    int64_t p_se, int64_t p_st, uint8_t* __restrict__ out, int num_out,
+    float* __restrict__ pprobs) {
+  using V = typename Vec<VB>::T;
+  const uint32_t total = (uint32_t)BT * (uint32_t)CH;
+  const uint32_t base = blockIdx.x * (kCT * CU) + threadIdx.x;
+  V v[CU];
+  Slots2 s[CU];
+  uint32_t bt[CU], c[CU];
+#pragma unroll
+  for (int u = 0; u < CU; ++u) {
+    const uint32_t idx = base + u * kCT;
+    const uint32_t q = idx < total ? idx : total - 1;  // dead lanes re-read the last chunk
+    bt[u] = q / (uint32_t)CH;
+    c[u] = q - bt[u] * (uint32_t)CH;
+    s[u] = load_slots2(rmap + (int64_t)bt[u] * (2 * E + 1), E);
+    v[u] = *reinterpret_cast<const V*>(inp + (int64_t)bt[u] * row_bytes + (int64_t)c[u] * VB);
+  }
+  float p0[CU], p1[CU];
+#pragma unroll
+  for (int u = 0; u < CU; ++u) {
+    p0[u] = p1[u] = 1.0f;
+    if (probs != nullptr) {
+      const int b = (int)(bt[u] / (uint32_t)T), t = (int)(bt[u] - (uint32_t)b * T);
+      const float* pb = probs + b * p_sb + (int64_t)t * p_st;
+      p0[u] = pb[(int64_t)s[u].e0 * p_se];
+      p1[u] = pb[(int64_t)s[u].e1 * p_se];
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < CU; ++u) {
+    if (base + u * kCT >= total) continue;
+    const int b = (int)(bt[u] / (uint32_t)T), t = (int)(bt[u] - (uint32_t)b * T);
+    uint8_t* dst_b = out + (int64_t)b * num_out * row_bytes + (int64_t)c[u] * VB;
+    auto put = [&](int row, float pr) __attribute__((always_inline)) {
+      if (row < 0 || row >= num_out) return;
+      V o = v[u];
+      if (probs != nullptr) {
+        if (pr == 0.0f) o = V{};
+        if (c[u] == 0) pprobs[(int64_t)b * num_out + row] = pr;
+      }
+      store_vec<NT>(reinterpret_cast<V*>(dst_b + (int64_t)row * row_bytes), o);
+    };
+    const int n = s[u].n;
+    if (n > 0) put(s[u].r0, p0[u]);
+    if (n > 1) put(s[u].r1, p1[u]);
+    const int32_t* rm = rmap + (int64_t)bt[u] * (2 * E + 1);
+    for (int j = 2; j < n; ++j) {
+      const float pr =
+          probs != nullptr ? probs[b * p_sb + (int64_t)rm[E + j] * p_se + (int64_t)t * p_st] : 1.0f;
+      put(rm[j], pr);
+    }
+  }
+}
+
+// out[t] = cast(sum_j fp32(y[row_j]) * p_j) in slot order (fma, one rounding
+// per slot); without probs the plain sum in slot order.
+template <class TT, int VE, int CU, bool NT>
+__global__ __launch_bounds__(kCT) void unpermute_chunk_kernel(
+    const typename TT::S* __restrict__ inp, int H, int CH, int BT, int T, int num_out,
+    const int32_t* __restrict__ rmap, int E, const float* __restrict__ probs, int64_t p_sb,
+    int64_t p_se, int64_t p_st, typename TT::S* __restrict__ out) {
+  using S = typename TT::S;
+  using VO = typename Vec<(int)sizeof(S) * VE>::T;
+  const uint32_t total = (uint32_t)BT * (uint32_t)CH;
+  const uint32_t base = blockIdx.x * (kCT * CU) + threadIdx.x;
+  Slots2 s[CU];
+  uint32_t bt[CU], c[CU];
+#pragma unroll
+  for (int u = 0; u < CU; ++u) {
+    const uint32_t idx = base + u * kCT;
+    const uint32_t q = idx < total ? idx : total - 1;
+    bt[u] = q / (uint32_t)CH;
+    c[u] = q - bt[u] * (uint32_t)CH;
+    s[u] = load_slots2(rmap + (int64_t)bt[u] * (2 * E + 1), E);
+  }
+  float p0[CU], p1[CU];
+  VO x0[CU], x1[CU];
+  bool ok0[CU], ok1[CU];
+#pragma unroll
+  for (int u = 0; u < CU; ++u) {
+    const int b = (int)(bt[u] / (uint32_t)T), t = (int)(bt[u] - (uint32_t)b * T);
+    p0[u] = p1[u] = 1.0f;
+    if (probs != nullptr) {
+      const float* pb = probs + b * p_sb + (int64_t)t * p_st;
+      p0[u] = pb[(int64_t)s[u].e0 * p_se];
+      p1[u] = pb[(int64_t)s[u].e1 * p_se];
+    }
+    const S* src_b = inp + (int64_t)b * num_out * H + (int64_t)c[u] * VE;
+    ok0[u] = s[u].n > 0 && s[u].r0 >= 0 && s[u].r0 < num_out;
+    ok1[u] = s[u].n > 1 && s[u].r1 >= 0 && s[u].r1 < num_out;
+    x0[u] = VO{};
+    x1[u] = VO{};
+    if (ok0[u]) x0[u] = *reinterpret_cast<const VO*>(src_b + (int64_t)s[u].r0 * H);
+    if (ok1[u]) x1[u] = *reinterpret_cast<const VO*>(src_b + (int64_t)s[u].r1 * H);
+  }
+#pragma unroll
+  for (int u = 0; u < CU; ++u) {
+    if (base + u * kCT >= total) continue;
+    float acc[VE];
+#pragma unroll
+    for (int i = 0; i < VE; ++i) acc[i] = 0.0f;
+    auto add = [&](const VO& raw, float pr) __attribute__((always_inline)) {
+      S e[VE];
+      __builtin_memcpy(e, &raw, sizeof(e));
+      if (probs != nullptr) {
+#pragma unroll
+        for (int i = 0; i < VE; ++i) acc[i] = __builtin_fmaf(TT::load(e[i]), pr, acc[i]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < VE; ++i) acc[i] += TT::load(e[i]);
+      }
+    };
+    if (ok0[u]) add(x0[u], p0[u]);
+    if (ok1[u]) add(x1[u], p1[u]);
+    const int n = s[u].n;
+    if (n > 2) {
+      const int b = (int)(bt[u] / (uint32_t)T), t = (int)(bt[u] - (uint32_t)b * T);
+      const int32_t* rm = rmap + (int64_t)bt[u] * (2 * E + 1);
+      const S* src_b = inp + (int64_t)b * num_out * H + (int64_t)c[u] * VE;
+      for (int j = 2; j < n; ++j) {
+        const int row = rm[j];
+        if (row < 0 || row >= num_out) continue;
+        const float pr =
+            probs != nullptr ? probs[b * p_sb + (int64_t)rm[E + j] * p_se + (int64_t)t * p_st]
+                             : 1.0f;
+        add(*reinterpret_cast<const VO*>(src_b + (int64_t)row * H), pr);
+      }
+    }
+    S o[VE];
+#pragma unroll
+    for (int i = 0; i < VE; ++i) o[i] = TT::store(acc[i]);
+    VO ov;
+    __builtin_memcpy(&ov, o, sizeof(ov));
+    store_vec<NT>(reinterpret_cast<VO*>(out + (int64_t)bt[u] * H + (int64_t)c[u] * VE), ov);
+  }
+}
 
 // --------------------------------------------------------------- permute ---
 template <int VB>
@@ -262,44 +493,6 @@ __global__ __launch_bounds__(kTokPerBlock* kWave) void permute_bwd_kernel(
 }
 
 // ------------------------------------------------------------- unpermute ---
-template <class TT, int VE>
-__global__ __launch_bounds__(kTokPerBlock* kWave) void unpermute_fwd_kernel(
-    const typename TT::S* __restrict__ inp, int H, int num_out, const int32_t* __restrict__ rmap,
-    int T, int E, const float* __restrict__ probs, int64_t p_sb, int64_t p_se, int64_t p_st,
-    typename TT::S* __restrict__ out) {
-  using S = typename TT::S;
-  const int t = blockIdx.x * kTokPerBlock + threadIdx.x / kWave;
-  const int b = blockIdx.y;
-  if (t >= T) return;
-  const int lane = lane_id();
-  const int32_t* rm = rmap + tok_index(b, t, T) * (2 * E + 1);
-  const int n = rm[2 * E];
-  for (int h0 = lane * VE; h0 < H; h0 += kWave * VE) {
-    float acc[VE];
-#pragma unroll
-    for (int i = 0; i < VE; ++i) acc[i] = 0.0f;
-    for (int j = 0; j < n; ++j) {
-      const int row = rm[j];
-      if (row < 0 || row >= num_out) continue;
-      const S* src = inp + ((int64_t)b * num_out + row) * H + h0;
-      S x[VE];
-#pragma unroll
-      for (int i = 0; i < VE; ++i) x[i] = src[i];
-      if (probs != nullptr) {
-        const float p = probs[b * p_sb + (int64_t)rm[E + j] * p_se + (int64_t)t * p_st];
-#pragma unroll
-        for (int i = 0; i < VE; ++i) acc[i] = __builtin_fmaf(TT::load(x[i]), p, acc[i]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < VE; ++i) acc[i] += TT::load(x[i]);
-      }
-    }
-    S* dst = out + tok_index(b, t, T) * H + h0;
-#pragma unroll
-    for (int i = 0; i < VE; ++i) dst[i] = TT::store(acc[i]);
-  }
-}
-
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int d = kWave / 2; d > 0; d >>= 1) v += __shfl_xor(v, d, kWave);
@@ -547,12 +740,26 @@ extern "C" int uttt_make_row_id_map(const void* routing_map, int mask_bytes, int
   UTTT_REQUIRE(routing_map != nullptr, "make_row_id_map: null routing_map");
   const int ntiles = (T + kTile - 1) / kTile;
   int32_t* counts = reinterpret_cast<int32_t*>(workspace);
-  hipLaunchKernelGGL(rowmap_count_kernel, dim3(ntiles, B), dim3(kTile), 0, st, routing_map,
-                     mask_bytes, s_b, s_e, s_t, T, E, ntiles, counts);
-  hipLaunchKernelGGL(rowmap_scan_kernel, dim3(B), dim3(kScanThreads), 0, st, counts, E, ntiles,
-                     group_sizes);
-  hipLaunchKernelGGL(rowmap_emit_kernel, dim3(ntiles, B), dim3(kTile), 0, st, routing_map,
-                     mask_bytes, s_b, s_e, s_t, T, E, ntiles, counts, row_id_map);
+  auto launch = [&](auto mb) {
+    constexpr int MB = decltype(mb)::value;
+    hipLaunchKernelGGL(rowmap_count_kernel<MB>, dim3(ntiles, B), dim3(kTile), 0, st, routing_map,
+                       s_b, s_e, s_t, T, E, ntiles, counts);
+    hipLaunchKernelGGL(rowmap_scan_kernel, dim3(B), dim3(kScanThreads), 0, st, counts, E, ntiles,
+                       group_sizes);
+    if (2 * E + 1 <= kStageMaxW) {
+      hipLaunchKernelGGL((rowmap_emit_kernel<MB, true>), dim3(ntiles, B), dim3(kTile),
+                         sizeof(int32_t) * kTile * (2 * E + 1), st, routing_map, s_b, s_e, s_t, T,
+                         E, ntiles, counts, row_id_map);
+    } else {
+      hipLaunchKernelGGL((rowmap_emit_kernel<MB, false>), dim3(ntiles, B), dim3(kTile), 0, st,
+                         routing_map, s_b, s_e, s_t, T, E, ntiles, counts, row_id_map);
+    }
+  };
+  if (mask_bytes == 1) {
+    launch(std::integral_constant<int, 1>{});
+  } else {
+    launch(std::integral_constant<int, 4>{});
+  }
   return check_launch("make_row_id_map");
 }
 
@@ -576,9 +783,24 @@ extern "C" int uttt_permute_fwd(const void* inp, int dtype, int B, int T, int H,
   const int vb = pick_vec_bytes(row_bytes > 0 ? row_bytes : 16, {inp, out});
   hipStream_t st = as_stream(stream);
 #define UTTT_LAUNCH_PERM(VBv)                                                                   \
-  hipLaunchKernelGGL(permute_fwd_kernel<VBv>, tok_grid(T, B), tok_block(), 0, st,              \
-                     reinterpret_cast<const uint8_t*>(inp), row_bytes, T, row_id_map, E, probs, \
-                     p_sb, p_se, p_st, reinterpret_cast<uint8_t*>(out), num_out, permuted_probs)
+  do {                                                                                          \
+    if (row_bytes > 0) {                                                                        \
+      const int CH = (int)(row_bytes / VBv);                                                    \
+      const int64_t chunks = (int64_t)B * T * CH;                                               \
+      UTTT_REQUIRE(chunks < (1ll << 31), "permute_fwd: payload too large (%lld chunks)",        \
+                   (long long)chunks);                                                          \
+      const unsigned grid = (unsigned)((chunks + kCT * kCU - 1) / (kCT * kCU));                 \
+      hipLaunchKernelGGL((permute_chunk_kernel<VBv, kCU, kNT>), dim3(grid), dim3(kCT), 0, st,               \
+                         reinterpret_cast<const uint8_t*>(inp), row_bytes, CH, B * T, T,        \
+                         row_id_map, E, probs, p_sb, p_se, p_st,                                \
+                         reinterpret_cast<uint8_t*>(out), num_out, permuted_probs);             \
+    } else {                                                                                    \
+      hipLaunchKernelGGL(permute_fwd_kernel<VBv>, tok_grid(T, B), tok_block(), 0, st,           \
+                         reinterpret_cast<const uint8_t*>(inp), row_bytes, T, row_id_map, E,    \
+                         probs, p_sb, p_se, p_st, reinterpret_cast<uint8_t*>(out), num_out,     \
+                         permuted_probs);                                                       \
+    }                                                                                           \
+  } while (0)
   switch (vb) {
     case 16: UTTT_LAUNCH_PERM(16); break;
     case 8: UTTT_LAUNCH_PERM(8); break;
@@ -619,10 +841,17 @@ extern "C" int uttt_unpermute_fwd(const void* inp, int dtype, int B, int num_out
   UTTT_DTYPE_SWITCH(dtype, TT, {
     using S = typename TT::S;
     const int ve = pick_ve<TT>(H, {inp, out});
-    UTTT_VE_SWITCH(ve, hipLaunchKernelGGL((unpermute_fwd_kernel<TT, VE>), tok_grid(T, B),
-                                          tok_block(), 0, st, reinterpret_cast<const S*>(inp), H,
-                                          num_out, row_id_map, T, E, probs, p_sb, p_se, p_st,
-                                          reinterpret_cast<S*>(out)));
+    const int CH = H / ve;
+    const int64_t chunks = (int64_t)B * T * CH;
+    UTTT_REQUIRE(chunks < (1ll << 31), "unpermute_fwd: payload too large (%lld chunks)",
+                 (long long)chunks);
+    const unsigned grid = (unsigned)((chunks + kCT * kCU - 1) / (kCT * kCU));
+    // pick_ve never yields a chunk above 16 bytes; those instantiations are skipped
+    UTTT_VE_SWITCH(ve, if constexpr (sizeof(S) * VE <= 16) {
+      hipLaunchKernelGGL((unpermute_chunk_kernel<TT, VE, kCU, kNT>), dim3(grid), dim3(kCT), 0, st,
+                         reinterpret_cast<const S*>(inp), H, CH, B * T, T, num_out, row_id_map, E,
+                         probs, p_sb, p_se, p_st, reinterpret_cast<S*>(out));
+    });
   });
   return check_launch("unpermute_fwd");
 }
