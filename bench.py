@@ -342,6 +342,9 @@ class MoeSweep:
                 st["gates_" + role] = (sm / sm.sum(1, keepdim=True)).contiguous()
                 st["gs_" + role] = mask.sum(-1).to(torch.int32).contiguous()
             self.sets.append(st)
+        # fp32 masters of the pool for the WRITE step (w0 and w2 rows stay
+        # concatenated: the norm-preserving write is per row)
+        self.M02, self.M1 = self.W02.float(), self.W1.float()
         if cfg["train"]:
             self.GW02 = randn(1, E, 2 * I, D, scale=0.02)
             self.GW1 = randn(1, E, D, I, scale=0.02)
@@ -437,6 +440,18 @@ class MoeSweep:
                L.ptr(p), p.stride(0), p.stride(1), p.stride(2), L.ptr(self.y), s)
         self._mark(None)
 
+    def write(self):
+        """The WRITE step on the pool: masters += lr_scale * dW, rows projected
+        back onto their pre-step norms, bf16 fast weights refreshed in place
+        (_apply_moe_update_dense, modeling_recurrent_lact.py:754-825)."""
+        L, E, D, I, s = self.L, self.E, self.D, self.I, self.stream
+        self._mark("write_step(2 launches)")
+        L.call("uttt_write_step", L.ptr(self.M02), None, L.ptr(self.dW02), L.BF16, None, None, 1.0,
+               1, E * 2 * I, D, D, 0, 1, L.ptr(self.M02), L.ptr(self.W02), None, s)
+        L.call("uttt_write_step", L.ptr(self.M1), None, L.ptr(self.dW1), L.BF16, None, None, 1.0,
+               1, E * D, I, I, 0, 1, L.ptr(self.M1), L.ptr(self.W1), None, s)
+        self._mark(None)
+
     def update(self, st):
         """One writer's UPDATE (the reference's per-layer call pattern)."""
         buf = dict(T=self.T, N=self.N, k=st["k"], v=st["v"], lr=st["lr"], mask=st["mask_u"],
@@ -513,6 +528,7 @@ class MoeSweep:
         timed("wgrad", lambda: L.call("uttt_grouped_wgrad_pair", L.ptr(dy), L.ptr(kp), L.ptr(hl),
                                       L.ptr(vp), L.ptr(gs), 1, E, I, D, Nu, L.ptr(self.dW02),
                                       L.ptr(self.dW1), s))
+        timed("write_step(2 launches)", self.write)
         return out
 
     def sweep(self, layers, chunks, batched):
@@ -522,11 +538,13 @@ class MoeSweep:
                 self.apply(self.sets[i % self.NSETS])
                 i += 1
             if c < chunks - 1:   # the last chunk is read but never written
-                if batched:
+                if batched:   # aggregate: all writers' gradients, one write
                     self.update_batched()
-                else:
+                    self.write()
+                else:         # chained: each writer updates and writes in turn
                     for l in range(layers):
                         self.update(self.sets[i % self.NSETS])
+                        self.write()
                         i += 1
 
 
@@ -592,7 +610,9 @@ def bench_moe(args, key):
     E, D, I, N = sw.E, sw.D, sw.I, sw.N
     by = {"gate_up": 2 * (E * 2 * I * D + N * D + N * I),
           "down_proj": 2 * (E * D * I + N * I + N * D),
-          "wgrad": 2 * (Nu * 2 * I + Nu * D + Nu * I + Nu * D + 3 * E * I * D)}
+          "wgrad": 2 * (Nu * 2 * I + Nu * D + Nu * I + Nu * D + 3 * E * I * D),
+          # fp32 master read + written, bf16 dW read, bf16 fast weight written
+          "write_step(2 launches)": (4 + 2 + 4 + 2) * 3 * E * I * D}
     for name, b in by.items():
         if name in kern:
             kern[name]["GBs"] = round(b / kern[name]["us"] / 1e3, 1)
@@ -618,11 +638,13 @@ def bench_moe(args, key):
                 "experts": cfg["E"], "topk": TOPK, "d": cfg["D"], "expert_hidden": cfg["I"],
                 "routing": "Zipf(1.1) prior" if cfg["zipf"] else "N(0,1) logits + N(0,0.5) bias",
                 "step": "one sweep: apply on 16 chunks x L layers, update on 15 chunks x L writers"
-                        + (" (+ update backward)" if cfg["train"] else ""),
+                        + (" (+ update backward)" if cfg["train"] else "") + " + write",
                 "update_schedule": ("batched: the L writers of a chunk in one grouped UPDATE "
                                     "call (aggregate write = sum of writer gradients)"
                                     if batched else "per-layer: one UPDATE call per writer"),
-                "excluded": "router logits/top-k (inputs precomputed); write step"},
+                "write": "norm-preserving write of the pool after every update "
+                         "(fp32 masters, bf16 fast weights)",
+                "excluded": "router logits/top-k (inputs precomputed)"},
         roofline=(dict(bound="hbm", kernel=dom, achieved=round(by[dom] / t_dom / 1e9, 1),
                        peak=HBM_PEAK_GBS, unit="GB/s",
                        frac=round(by[dom] / t_dom / 1e9 / HBM_PEAK_GBS, 4), traffic=None,

@@ -240,6 +240,27 @@ int uttt_grouped_update_bwd(const void* w0_w2, const void* w1, const void* k, co
  * [B, rows, N] intermediates): out[b, c, r] = in[b, r, c], 2-byte elements. */
 int uttt_transpose_2byte(const void* in, int B, int R, int C, void* out, void* stream);
 
+/* WRITE step of the fast weights.  Replaces the write of
+ * _apply_moe_update_dense (uttt_llm/flame/custom_models/uttt_moe/
+ * modeling_recurrent_lact.py:754-825; seg = C, norm_from_fast = 0,
+ * renorm_master = 1) and of uTTT-Dense's _apply_shared_update
+ * (uttt_llm/flame/custom_models/uttt_dense/modeling_recurrent_lact.py:1109-1240;
+ * seg = d, nu from the fast weight unless master renorm is on), without Muon.
+ * Tensors are [B, rows_per_batch, C] row-major; each row is cut into C / seg
+ * segments and for each segment, with nu = |segment of master (or of
+ * fast_in, bf16, when norm_from_fast)| taken before the step:
+ *   G = grad (+ mom_in * m_coeff[b] when mom_in; then mom_out = G)
+ *   U = master + G * lr_scale
+ *   P = U / (|U| + 1e-5) * nu
+ *   master_out = renorm_master ? P : U,   fast_out = bf16(P).
+ * grad: grad_dtype (fp32, bf16 or fp16); master, mom, master_out fp32;
+ * m_coeff fp32 [B].  master_out may be master and mom_out may be mom_in (in
+ * place).  seg must be a multiple of 4, at most 4096, and divide C. */
+int uttt_write_step(const float* master, const void* fast_in, const void* grad, int grad_dtype,
+                    const float* mom_in, const float* m_coeff, float lr_scale, int B,
+                    int64_t rows_per_batch, int C, int seg, int norm_from_fast, int renorm_master,
+                    float* master_out, void* fast_out, float* mom_out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

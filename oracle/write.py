@@ -1,0 +1,98 @@
+"""Oracle of the fast-weight WRITE step (checker only; see oracle/__init__.py).
+
+fp32 torch on the CPU, written from the two reference call sites:
+
+  moe_write    _apply_moe_update_dense,
+               uttt_llm/flame/custom_models/uttt_moe/modeling_recurrent_lact.py:754-825
+               (cited M:).  Row norms over the last dim of the fp32 masters,
+               taken before the step; optional momentum; W + s * G; the
+               masters are projected back onto the old norms; fast = bf16.
+  dense_write  _apply_shared_update and _wide_to_slices / _slices_to_wide,
+               uttt_llm/flame/custom_models/uttt_dense/modeling_recurrent_lact.py:1068-1240
+               (cited D:).  The same step on d x d slices: w0 / w2 rows are
+               whole slice rows, w1 rows are cut into r segments of d; the old
+               norms come from the fast (bf16) weights unless master renorm is
+               on, and the master keeps the unprojected value unless master
+               renorm is on.
+
+Muon (Newton-Schulz orthogonalisation of G) is not restated here: both call
+sites run it between the momentum and the step, and a caller that uses it
+passes the orthogonalised G with momentum off.
+
+Every operation follows the reference's operation order (separate multiply
+and add, divide then multiply) in fp32; only the norm reductions differ in
+summation order (the oracle sums in fp64), which the tests cover with a
+1e-5 relative tolerance.
+"""
+from __future__ import annotations
+
+import torch
+
+EPS = 1e-5
+
+
+def _norm(x: torch.Tensor, dim: int) -> torch.Tensor:
+    return x.double().pow(2).sum(dim=dim, keepdim=True).sqrt().float()
+
+
+def moe_write(grads, masterw, momentum_buf=None, m_coeff=None, lr_scale=1.0):
+    """M:754-825 without Muon.  grads, masterw: (w0, w1, w2), fp32 [B,E,R,C];
+    momentum_buf: same shapes or None; m_coeff: [B,1,1,1] or None.
+    Returns (fast bf16 tuple, new masters, new momentum or None)."""
+    new_master, new_mom, fast = [], [], []
+    use_mom = momentum_buf is not None and m_coeff is not None
+    for i, (g, w) in enumerate(zip(grads, masterw)):
+        w = w.float()
+        nu = _norm(w, 3)                                   # M:766-768
+        g = g.float()
+        if use_mom:
+            g = g + momentum_buf[i].float() * m_coeff      # M:772-774
+            new_mom.append(g.clone())                      # M:775-779
+        u = w + g * lr_scale                               # M:813-815
+        p = u / (_norm(u, 3) + EPS) * nu                   # M:817-819
+        new_master.append(p)
+        fast.append(p.to(torch.bfloat16))                  # M:822
+    return tuple(fast), tuple(new_master), (tuple(new_mom) if use_mom else momentum_buf)
+
+
+def wide_to_slices(weight: torch.Tensor, name: str, r: int) -> torch.Tensor:
+    """D:1068-1086: [b,h,r*d,d] (w0, w2) or [b,h,d,r*d] (w1) -> [b*h*r, d, d]."""
+    if name in ("w0", "w2"):
+        b, h, inter, d = weight.shape
+        return weight.reshape(b, h, r, d, d).reshape(b * h * r, d, d)
+    b, h, d, inter = weight.shape
+    return weight.reshape(b, h, d, r, d).permute(0, 1, 3, 2, 4).reshape(b * h * r, d, d)
+
+
+def slices_to_wide(slices: torch.Tensor, name: str, b: int, h: int, r: int) -> torch.Tensor:
+    """D:1088-1106, the inverse of wide_to_slices."""
+    _, d, _ = slices.shape
+    if name in ("w0", "w2"):
+        return slices.reshape(b, h, r * d, d)
+    return slices.reshape(b, h, r, d, d).permute(0, 1, 3, 2, 4).reshape(b, h, d, r * d)
+
+
+def dense_write(agg_grads, fastw, masterw, r, momentum_buf=None, coeff=None, lr_scale=1.0,
+                master_renorm=False):
+    """D:1109-1240 without Muon.  fastw bf16, masterw fp32, shapes w0/w2
+    [b,h,r*d,d], w1 [b,h,d,r*d]; coeff: [b,1,1,1] or None.
+    Returns (fast bf16 tuple, new masters, new momentum or None)."""
+    names = ("w0", "w1", "w2")
+    b, h = fastw[0].shape[:2]
+    fast_s = [wide_to_slices(w, n, r) for n, w in zip(names, fastw)]
+    master_s = [wide_to_slices(w.float(), n, r) for n, w in zip(names, masterw)]
+    src = master_s if master_renorm else fast_s
+    old = [_norm(s.float(), 2) for s in src]                           # D:1164-1167
+    deltas = [g.float() for g in agg_grads]
+    if momentum_buf is not None and coeff is not None:
+        deltas = [dl + m.float() * coeff for dl, m in zip(deltas, momentum_buf)]  # D:1175-1178
+        momentum_buf = tuple(deltas)
+    delta_s = [wide_to_slices(dl, n, r) for n, dl in zip(names, deltas)]
+    delta_s = [dl * lr_scale for dl in delta_s]                        # D:1206-1209
+    upd = [m + dl for m, dl in zip(master_s, delta_s)]                 # D:1210-1213
+    proj = [u / (_norm(u, 2) + EPS) * o for u, o in zip(upd, old)]     # D:1214-1222
+    if master_renorm:
+        upd = proj
+    new_master = tuple(slices_to_wide(s, n, b, h, r) for n, s in zip(names, upd))
+    fast = tuple(slices_to_wide(s, n, b, h, r).to(torch.bfloat16) for n, s in zip(names, proj))
+    return fast, new_master, momentum_buf

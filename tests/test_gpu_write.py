@@ -1,0 +1,112 @@
+"""GPU parity of the WRITE step (csrc/write_step.hip through
+uttt_amd.fast_weight_write) against oracle/write.py on the same seeded
+inputs.
+
+Bar: the fp32 masters within rtol 1e-5 (the norms are reduced in a different
+order than the oracle's fp64 sums); the momentum buffer and, without master
+renorm, the unprojected master are bit-exact (same fp32 operations in the
+same order); the bf16 fast weights within rtol 8e-3 (two bf16 ulps: an fp32
+difference in the last place can move a value across a bf16 rounding
+boundary).
+"""
+import pytest
+import torch
+
+from oracle import write as OW
+from uttt_amd import _lib as L
+from uttt_amd import fast_weight_write as FWW
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _rand(shape, seed, scale=1.0):
+    return torch.randn(*shape, generator=torch.Generator().manual_seed(seed)) * scale
+
+
+def _close_master(ours, ref):
+    torch.testing.assert_close(ours.cpu(), ref, rtol=1e-5, atol=1e-6)
+
+
+def _close_fast(ours, ref):
+    assert ours.dtype == torch.bfloat16
+    torch.testing.assert_close(ours.cpu().float(), ref.float(), rtol=8e-3, atol=1e-6)
+
+
+@pytest.mark.parametrize("B,E,I,D,grad_dtype,mom", [
+    (1, 4, 40, 96, torch.float32, False),       # w1 rows of 40: a partly filled wave
+    (2, 3, 384, 192, torch.bfloat16, True),
+    (1, 2, 3072, 1536, torch.bfloat16, False),  # the 760M expert shapes (rows of 1536 / 3072)
+    (1, 2, 768, 4096, torch.float32, True),     # the longest segment one wave holds
+])
+def test_moe_write_matches_oracle(B, E, I, D, grad_dtype, mom):
+    shapes = [(B, E, I, D), (B, E, D, I), (B, E, I, D)]
+    masters = [_rand(s, i) / D ** 0.5 for i, s in enumerate(shapes)]
+    grads = [_rand(s, 10 + i, 0.05).to(grad_dtype) for i, s in enumerate(shapes)]
+    moms = [_rand(s, 20 + i, 0.05) for i, s in enumerate(shapes)] if mom else None
+    m = torch.rand(B, 1, 1, 1, generator=torch.Generator().manual_seed(5)) if mom else None
+    rf, rm, rmom = OW.moe_write(tuple(g.float() for g in grads), masters, moms, m, lr_scale=0.8)
+    fast = tuple(w.to(torch.bfloat16).to(DEV) for w in masters)
+    of, om, omom = FWW.apply_moe_update_dense(
+        tuple(g.to(DEV) for g in grads), fast, tuple(w.to(DEV) for w in masters),
+        tuple(x.to(DEV) for x in moms) if mom else None, m.to(DEV) if mom else None, lr_scale=0.8)
+    for i in range(3):
+        _close_master(om[i], rm[i])
+        _close_fast(of[i], rf[i])
+        if mom:
+            assert torch.equal(omom[i].cpu(), rmom[i])
+    if not mom:
+        assert omom is None
+
+
+@pytest.mark.parametrize("master_renorm,mom", [(False, False), (True, False), (False, True)])
+def test_dense_write_matches_oracle(master_renorm, mom):
+    b, h, d, r = 1, 4, 96, 2   # configs[0] head shape: d = 96, d_h = 192
+    shapes = [(b, h, r * d, d), (b, h, d, r * d), (b, h, r * d, d)]
+    masters = [_rand(s, i) / d ** 0.5 for i, s in enumerate(shapes)]
+    fast = [(w * 1.003).to(torch.bfloat16) for w in masters]
+    grads = [_rand(s, 10 + i, 0.02) for i, s in enumerate(shapes)]
+    moms = [_rand(s, 20 + i, 0.02) for i, s in enumerate(shapes)] if mom else None
+    coeffs = [torch.full((b, 1, 1, 1), 0.4), torch.full((b, 1, 1, 1), 0.6)] if mom else None
+    coeff = torch.stack(coeffs).mean(0) if mom else None
+    rf, rm, rmom = OW.dense_write(grads, fast, masters, r, moms, coeff, lr_scale=0.5,
+                                  master_renorm=master_renorm)
+    of, om, omom = FWW.apply_shared_update(
+        tuple(g.to(DEV) for g in grads), tuple(f.to(DEV) for f in fast),
+        tuple(w.to(DEV) for w in masters), tuple(x.to(DEV) for x in moms) if mom else None,
+        [c.to(DEV) for c in coeffs] if mom else None, r=r, lr_scale=0.5,
+        master_renorm=master_renorm)
+    for i in range(3):
+        _close_fast(of[i], rf[i])
+        if master_renorm:
+            _close_master(om[i], rm[i])
+        else:
+            assert torch.equal(om[i].cpu(), rm[i])
+        if mom:
+            assert torch.equal(omom[i].cpu(), rmom[i])
+
+
+def test_write_in_place_equals_out_of_place():
+    B, E, R, C = 1, 3, 64, 1536
+    w = (_rand((B, E, R, C), 1) / C ** 0.5).to(DEV)
+    g = _rand((B, E, R, C), 2, 0.05).to(torch.bfloat16).to(DEV)
+    mom = _rand((B, E, R, C), 3, 0.05).to(DEV)
+    mc = torch.tensor([0.7], device=DEV)
+    outs = []
+    for in_place in (False, True):
+        master = w.clone()
+        mo = mom.clone()
+        m_out = master if in_place else torch.empty_like(master)
+        mo_out = mo if in_place else torch.empty_like(mo)
+        f_out = torch.empty(w.shape, dtype=torch.bfloat16, device=DEV)
+        L.call("uttt_write_step", L.ptr(master), None, L.ptr(g), L.BF16, L.ptr(mo), L.ptr(mc), 0.3,
+               B, E * R, C, C, 0, 1, L.ptr(m_out), L.ptr(f_out), L.ptr(mo_out), L.stream_of(w))
+        outs.append((m_out, f_out, mo_out))
+    for a, b_ in zip(*outs):
+        assert torch.equal(a, b_)
+
+
+def test_write_refuses_muon():
+    w = torch.zeros(1, 1, 4, 8, device=DEV)
+    with pytest.raises(NotImplementedError):
+        FWW.apply_moe_update_dense((w, w, w), (w, w, w), (w, w, w), use_moun=True)

@@ -35,3 +35,17 @@ def test_abi_rejects_bad_sizes_without_launch():
 def test_call_raises_runtime_error_with_message():
     with pytest.raises(RuntimeError, match="workspace"):
         _lib.call("uttt_make_row_id_map", None, 1, 0, 0, 0, 1, 16, 4, None, None, None, 0, None)
+
+
+@needs_lib
+def test_write_step_rejects_bad_segments_without_launch():
+    lib = _lib.lib()
+    rc = lib.uttt_write_step(None, None, None, 0, None, None, 1.0, 1, 4, 96, 40, 0, 1,
+                             None, None, None, None)
+    assert rc == -1 and b"segment 40" in lib.uttt_last_error()
+    rc = lib.uttt_write_step(None, None, None, 0, 8, None, 1.0, 1, 4, 96, 96, 0, 1,
+                             None, None, None, None)
+    assert rc == -1 and b"momentum" in lib.uttt_last_error()
+    rc = lib.uttt_write_step(None, None, None, 0, None, None, 1.0, 1, 4, 96, 96, 1, 1,
+                             None, None, None, None)
+    assert rc == -1 and b"norm_from_fast" in lib.uttt_last_error()

@@ -87,6 +87,11 @@ SIGNATURES = {
          c_int, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_sz, c_p],
     ),
     "uttt_transpose_2byte": (c_int, [c_p, c_int, c_int, c_int, c_p, c_p]),
+    "uttt_write_step": (
+        c_int,
+        [c_p, c_p, c_p, c_int, c_p, c_p, ctypes.c_float, c_int, c_i64, c_int, c_int, c_int, c_int,
+         c_p, c_p, c_p, c_p],
+    ),
 }
 
 _lib = None

@@ -1,0 +1,185 @@
+// Fast-weight WRITE step for gfx950: optional momentum, the step
+// U = W + s * G, and the norm-preserving projection P = U / (|U| + 1e-5) * nu
+// of every row segment, with nu the segment's norm before the step.
+//
+// reference: _apply_moe_update_dense,
+//   uttt_llm/flame/custom_models/uttt_moe/modeling_recurrent_lact.py:754-825
+//   (segment = whole row of the fp32 master, nu from the master, the master
+//   takes P), and _apply_shared_update,
+//   uttt_llm/flame/custom_models/uttt_dense/modeling_recurrent_lact.py:1109-1240
+//   (segment = d-wide piece of a row, nu from the bf16 fast weight, the master
+//   keeps U unless master renorm is on).
+//
+// One 64-lane wave owns one segment of S elements; lane l holds the 16-byte
+// chunks l, l + 64, ... of it in registers, so each tensor is read once and
+// written once (HBM-bound: 4 + |G| + 4 + 2 bytes per element, plus 8 with
+// momentum and 2 when nu comes from the fast weight).  The arithmetic keeps
+// the reference's operation order in fp32: G + M * m, W + G * s as a separate
+// multiply and add, U / (|U| + eps) * nu as divide then multiply.
+#include "common.h"
+
+namespace uttt {
+namespace {
+
+constexpr int kWS = 256;  // 4 waves = 4 segments per workgroup
+
+struct alignas(8) Half4 {
+  uint16_t h[4];
+};
+
+template <class GT>
+__device__ __forceinline__ float4 load_grad4(const typename GT::S* p) {
+  if constexpr (sizeof(typename GT::S) == 4) {
+    return *reinterpret_cast<const float4*>(p);
+  } else {
+    const Half4 v = *reinterpret_cast<const Half4*>(p);
+    return make_float4(GT::load(v.h[0]), GT::load(v.h[1]), GT::load(v.h[2]), GT::load(v.h[3]));
+  }
+}
+
+__device__ __forceinline__ float sumsq4(float4 v) {
+  float s = v.x * v.x;
+  s = __builtin_fmaf(v.y, v.y, s);
+  s = __builtin_fmaf(v.z, v.z, s);
+  return __builtin_fmaf(v.w, v.w, s);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int d = kWave / 2; d > 0; d >>= 1) v += __shfl_xor(v, d, kWave);
+  return v;
+}
+
+// master / master_out and mom_in / mom_out may alias (in-place write): every
+// element is read into registers before the same lane overwrites it.
+template <class GT, int NV, bool MOM, bool FASTNORM>
+__global__ __launch_bounds__(kWS) void write_step_kernel(
+    const float* master, const uint16_t* __restrict__ fast_in,
+    const typename GT::S* __restrict__ grad, const float* mom_in, const float* __restrict__ m_coeff,
+    float lr_scale, int64_t nseg, int64_t seg_per_batch, int S, int renorm_master,
+    float* master_out, uint16_t* __restrict__ fast_out, float* mom_out) {
+#pragma clang fp contract(off)
+  const int64_t seg = (int64_t)blockIdx.x * (kWS / kWave) + threadIdx.x / kWave;
+  if (seg >= nseg) return;  // whole wave leaves together
+  const int lane = lane_id();
+  const int64_t base = seg * S;
+  const float mc = MOM ? m_coeff[seg / seg_per_batch] : 0.0f;
+  float4 u[NV];
+  float ss_old = 0.0f, ss_new = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int e = 4 * (lane + kWave * i);
+    if (e < S) {
+      const float4 w = *reinterpret_cast<const float4*>(master + base + e);
+      float4 g = load_grad4<GT>(grad + base + e);
+      if constexpr (FASTNORM) {
+        const Half4 f = *reinterpret_cast<const Half4*>(fast_in + base + e);
+        ss_old += sumsq4(make_float4(bf16_to_f32(f.h[0]), bf16_to_f32(f.h[1]),
+                                     bf16_to_f32(f.h[2]), bf16_to_f32(f.h[3])));
+      } else {
+        ss_old += sumsq4(w);
+      }
+      if constexpr (MOM) {
+        const float4 m = *reinterpret_cast<const float4*>(mom_in + base + e);
+        g.x = g.x + m.x * mc;
+        g.y = g.y + m.y * mc;
+        g.z = g.z + m.z * mc;
+        g.w = g.w + m.w * mc;
+        *reinterpret_cast<float4*>(mom_out + base + e) = g;
+      }
+      u[i].x = w.x + g.x * lr_scale;
+      u[i].y = w.y + g.y * lr_scale;
+      u[i].z = w.z + g.z * lr_scale;
+      u[i].w = w.w + g.w * lr_scale;
+      ss_new += sumsq4(u[i]);
+    }
+  }
+  const float nu = sqrtf(wave_sum(ss_old));
+  const float den = sqrtf(wave_sum(ss_new)) + 1e-5f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int e = 4 * (lane + kWave * i);
+    if (e < S) {
+      float4 p;
+      p.x = u[i].x / den * nu;
+      p.y = u[i].y / den * nu;
+      p.z = u[i].z / den * nu;
+      p.w = u[i].w / den * nu;
+      *reinterpret_cast<float4*>(master_out + base + e) = renorm_master ? p : u[i];
+      Half4 f;
+      f.h[0] = f32_to_bf16(p.x);
+      f.h[1] = f32_to_bf16(p.y);
+      f.h[2] = f32_to_bf16(p.z);
+      f.h[3] = f32_to_bf16(p.w);
+      *reinterpret_cast<Half4*>(fast_out + base + e) = f;
+    }
+  }
+}
+
+inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+}  // namespace
+}  // namespace uttt
+
+using namespace uttt;
+
+extern "C" int uttt_write_step(const float* master, const void* fast_in, const void* grad,
+                               int grad_dtype, const float* mom_in, const float* m_coeff,
+                               float lr_scale, int B, int64_t rows_per_batch, int C, int seg,
+                               int norm_from_fast, int renorm_master, float* master_out,
+                               void* fast_out, float* mom_out, void* stream) {
+  UTTT_REQUIRE(B >= 0 && rows_per_batch >= 0 && C >= 0, "write_step: bad sizes");
+  UTTT_REQUIRE(seg > 0 && seg % 4 == 0 && seg <= 4096 && C % seg == 0,
+               "write_step: segment %d must be a multiple of 4, at most 4096, and divide C=%d",
+               seg, C);
+  UTTT_REQUIRE(grad_dtype == UTTT_F32 || grad_dtype == UTTT_BF16 || grad_dtype == UTTT_F16,
+               "write_step: unsupported grad dtype %d", grad_dtype);
+  UTTT_REQUIRE((mom_in == nullptr) == (mom_out == nullptr) &&
+                   (mom_in == nullptr || m_coeff != nullptr),
+               "write_step: momentum needs mom_in, mom_out and m_coeff together");
+  UTTT_REQUIRE(!norm_from_fast || fast_in != nullptr, "write_step: norm_from_fast needs fast_in");
+  const int64_t nseg = (int64_t)B * rows_per_batch * (C / seg);
+  if (nseg == 0) return UTTT_OK;
+  UTTT_REQUIRE(master && grad && master_out && fast_out, "write_step: null tensor");
+  UTTT_REQUIRE(aligned(master, 16) && aligned(master_out, 16) && aligned(mom_in, 16) &&
+                   aligned(mom_out, 16) && aligned(fast_out, 8) && aligned(fast_in, 8) &&
+                   aligned(grad, dtype_bytes(grad_dtype) * 4),
+               "write_step: tensors must be 16-byte (fp32) / 8-byte (bf16) aligned");
+  const int64_t seg_per_batch = rows_per_batch * (C / seg);
+  // the launch needs grid * 256 < 2^32 threads
+  UTTT_REQUIRE(nseg < (1ll << 26), "write_step: %lld segments exceed one launch", (long long)nseg);
+  const unsigned grid = (unsigned)((nseg + kWS / kWave - 1) / (kWS / kWave));
+  hipStream_t st = as_stream(stream);
+  const int nv = (seg + 4 * kWave - 1) / (4 * kWave);
+  const int nvp = nv <= 1 ? 1 : nv <= 2 ? 2 : nv <= 4 ? 4 : nv <= 8 ? 8 : nv <= 12 ? 12 : 16;
+  const bool mom = mom_in != nullptr;
+  const auto* fin = reinterpret_cast<const uint16_t*>(fast_in);
+  auto* fout = reinterpret_cast<uint16_t*>(fast_out);
+#define UTTT_WS_LAUNCH(NV, MOM, FN)                                                              \
+  hipLaunchKernelGGL((write_step_kernel<TT, NV, MOM, FN>), dim3(grid), dim3(kWS), 0, st, master, \
+                     fin, reinterpret_cast<const typename TT::S*>(grad), mom_in, m_coeff,        \
+                     lr_scale, nseg, seg_per_batch, seg, renorm_master, master_out, fout, mom_out)
+#define UTTT_WS_FLAGS(NV)                                     \
+  do {                                                        \
+    if (mom) {                                                \
+      if (norm_from_fast) UTTT_WS_LAUNCH(NV, true, true);     \
+      else UTTT_WS_LAUNCH(NV, true, false);                   \
+    } else {                                                  \
+      if (norm_from_fast) UTTT_WS_LAUNCH(NV, false, true);    \
+      else UTTT_WS_LAUNCH(NV, false, false);                  \
+    }                                                         \
+  } while (0)
+  UTTT_DTYPE_SWITCH_LR(grad_dtype, TT, {
+    switch (nvp) {
+      case 1: UTTT_WS_FLAGS(1); break;
+      case 2: UTTT_WS_FLAGS(2); break;
+      case 4: UTTT_WS_FLAGS(4); break;
+      case 8: UTTT_WS_FLAGS(8); break;
+      case 12: UTTT_WS_FLAGS(12); break;
+      default: UTTT_WS_FLAGS(16); break;
+    }
+  });
+#undef UTTT_WS_FLAGS
+#undef UTTT_WS_LAUNCH
+  return check_launch("write_step");
+}

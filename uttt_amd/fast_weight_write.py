@@ -1,0 +1,109 @@
+"""The fast-weight WRITE step on the gfx950 kernel of csrc/write_step.hip.
+
+Two functions with the argument meaning and return values of the reference's
+write methods (self's configuration becomes keyword arguments):
+
+  apply_moe_update_dense    _apply_moe_update_dense,
+                            uttt_llm/flame/custom_models/uttt_moe/modeling_recurrent_lact.py:754-825
+  apply_shared_update       _apply_shared_update,
+                            uttt_llm/flame/custom_models/uttt_dense/modeling_recurrent_lact.py:1109-1240
+
+Both return freshly allocated (fast bf16, master fp32, momentum) tuples and
+never modify their inputs, as the reference does.  Muon (Newton-Schulz
+orthogonalisation of the step) is not built: asking for it raises.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib as L
+
+_NAMES = ("w0", "w1", "w2")
+
+
+def _write_one(master, grad, mom, m_coeff_b, lr_scale, rows, C, seg, fast_in, renorm_master):
+    L.require_device(master, grad, mom, m_coeff_b, fast_in)
+    assert master.dtype == torch.float32 and master.is_contiguous(), "master must be fp32 contiguous"
+    assert grad.shape == master.shape and grad.is_contiguous(), "grad must match the master"
+    B = master.shape[0]
+    master_out = torch.empty_like(master)
+    fast_out = torch.empty(master.shape, dtype=torch.bfloat16, device=master.device)
+    mom_out = None
+    if mom is not None:
+        assert mom.dtype == torch.float32 and mom.shape == master.shape and mom.is_contiguous()
+        mom_out = torch.empty_like(mom)
+    if fast_in is not None:
+        assert fast_in.dtype == torch.bfloat16 and fast_in.shape == master.shape
+        fast_in = fast_in.contiguous()
+    L.call("uttt_write_step", L.ptr(master), L.ptr(fast_in), L.ptr(grad), L.dtype_code(grad.dtype),
+           L.ptr(mom), L.ptr(m_coeff_b), float(lr_scale), B, rows, C, seg,
+           int(fast_in is not None), int(renorm_master), L.ptr(master_out), L.ptr(fast_out),
+           L.ptr(mom_out), L.stream_of(master))
+    return fast_out, master_out, mom_out
+
+
+def _coeff_per_batch(m_coeff, B, device):
+    c = m_coeff.to(device=device, dtype=torch.float32).reshape(-1).contiguous()
+    assert c.numel() == B, f"momentum coefficient must hold one value per batch, got {c.numel()}"
+    return c
+
+
+def apply_moe_update_dense(grads, fastw, masterw, momentum_buf=None, m_coeff=None, lr_scale=1.0,
+                           use_momentum=True, use_moun=False):
+    """uTTT-MoE write (modeling_recurrent_lact.py:754-825).  grads, masterw:
+    (w0, w1, w2) [B,E,R,C] (grads fp32 or bf16, masters fp32); momentum_buf:
+    fp32 tuple or None; m_coeff: [B,1,1,1] or None.  `fastw` is accepted for
+    signature parity; the new fast weights are bf16 of the new masters.
+    Returns (fast, master, momentum_buf)."""
+    if use_moun:
+        raise NotImplementedError("the Muon (Newton-Schulz) write is not built on gfx950")
+    del fastw
+    use_mom = use_momentum and momentum_buf is not None and m_coeff is not None
+    B = masterw[0].shape[0]
+    coeff = _coeff_per_batch(m_coeff, B, masterw[0].device) if use_mom else None
+    fast, master, mom = [], [], []
+    for i, (g, w) in enumerate(zip(grads, masterw)):
+        assert w.dim() == 4, "masters are [B, E, R, C]"
+        _, E, R, C = w.shape
+        f, m, mo = _write_one(w.contiguous(), g.contiguous(), momentum_buf[i].contiguous() if use_mom else None,
+                              coeff, lr_scale, E * R, C, C, None, True)
+        fast.append(f)
+        master.append(m)
+        mom.append(mo)
+    return tuple(fast), tuple(master), (tuple(mom) if use_mom else momentum_buf)
+
+
+def apply_shared_update(agg_grads, fastw, masterw, momentum_buf=None, momentum_coeffs=None, *,
+                        r: int, lr_scale: float = 1.0, master_renorm: bool = False,
+                        use_momentum: bool = True, use_moun: bool = False):
+    """uTTT-Dense write (modeling_recurrent_lact.py:1109-1240).  Shapes: w0, w2
+    [b,h,r*d,d], w1 [b,h,d,r*d]; every d x d slice is written on its own, so a
+    w1 row is cut into r segments of d.  momentum_coeffs: a tensor, a list of
+    per-layer tensors (averaged) or None.  Returns (fast, master, momentum_buf)."""
+    if use_moun:
+        raise NotImplementedError("the Muon (Newton-Schulz) write is not built on gfx950")
+    if len(agg_grads) != 3 or len(fastw) != 3 or len(masterw) != 3:
+        raise ValueError("uTTT-Dense expects three fast-weight matrices")
+    b, h, inter, d = fastw[0].shape
+    if inter != r * d or tuple(fastw[1].shape) != (b, h, d, r * d) or fastw[2].shape != fastw[0].shape:
+        raise ValueError(f"invalid shared fast state shapes for r={r}: "
+                         f"{[tuple(w.shape) for w in fastw]}")
+    if torch.is_tensor(momentum_coeffs):
+        coeff = momentum_coeffs
+    elif momentum_coeffs:
+        coeff = torch.stack(list(momentum_coeffs), dim=0).mean(dim=0)
+    else:
+        coeff = None
+    use_mom = use_momentum and momentum_buf is not None and coeff is not None
+    cb = _coeff_per_batch(coeff, b, fastw[0].device) if use_mom else None
+    fast, master, mom = [], [], []
+    for i, name in enumerate(_NAMES):
+        w = masterw[i].contiguous()
+        rows, C = (h * r * d, d) if name != "w1" else (h * d, r * d)
+        f, m, mo = _write_one(w, agg_grads[i].contiguous(),
+                              momentum_buf[i].contiguous() if use_mom else None, cb, lr_scale,
+                              rows, C, d, None if master_renorm else fastw[i], master_renorm)
+        fast.append(f)
+        master.append(m)
+        mom.append(mo)
+    return tuple(fast), tuple(master), (tuple(mom) if use_mom else momentum_buf)
