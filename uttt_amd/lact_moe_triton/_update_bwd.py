@@ -8,7 +8,7 @@ from __future__ import annotations
 
 import torch
 
-from .. import _lib as L
+from uttt_amd import _lib as L  # absolute: the package also works mounted in the reference tree
 from . import _grouped
 
 

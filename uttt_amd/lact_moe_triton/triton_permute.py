@@ -12,7 +12,7 @@ from typing import Union
 
 import torch
 
-from .. import _lib as L
+from uttt_amd import _lib as L  # absolute: the package also works mounted in the reference tree
 
 
 def _mask_arg(routing_map: torch.Tensor):
