@@ -214,6 +214,36 @@ int uttt_grouped_wgrad_pair(const void* dy0_dy2_tok, const void* k, const void* 
 int uttt_grouped_wgrad(const void* a_tok, const void* b_tok, const int32_t* group_sizes, int B,
                        int E, int R, int C, int N, void* out, int transposed, void* stream);
 
+/* Two chained products in one pass (fp32 accumulation, one bf16 rounding):
+ *   nt2: y[b, n] = wa[b, e(n)] xa[b, n] + wb[b, e(n)] xb[b, n],  w [B,E,M,K]
+ *   tn2: y[b, n] = wa[b, e(n)]^T xa[b, n] + wb[b, e(n)]^T xb[b, n], w [B,E,K,M]
+ * x token-major [B, N, K], y [B, N, M], bf16.  Together they replace
+ * fused_grouped_grad_kv (L/triton_lact_bwd_grouped_grad_kv.py:227-340):
+ * grad_K = tn2(G_W0_W2, DY_lr, W0_W2, dY_02), grad_V = nt2(W1, dH, G_W1, H_lr). */
+int uttt_grouped_gemm_nt2(const void* wa, const void* xa, const void* wb, const void* xb,
+                          const int32_t* group_sizes, int B, int E, int M, int K, int N, void* y,
+                          void* stream);
+int uttt_grouped_gemm_tn2(const void* wa, const void* xa, const void* wb, const void* xb,
+                          const int32_t* group_sizes, int B, int E, int M, int K, int N, void* y,
+                          void* stream);
+
+/* Scratch bytes for uttt_swiglu_bwd_bwd at (B, D, L). */
+size_t uttt_swiglu_bwd_bwd_workspace_bytes(int B, int D, int L);
+
+/* Second-order SwiGLU pointwise pass.  Replaces
+ * triton_swiglu_bwd_bwd_fused_cat_inp_out / ref_pytorch_swiglu_bwd_bwd_fused_cat_inp_out
+ * (L/triton_pointwise_kernels.py:240-436).  dh, grad_hidden_lr1, grad_dh,
+ * hidden_lr1 [B, D, L]; x0_x2, grad_dx0_dx2, grad_x0_x2, dx0_x2 [B, 2D, L]
+ * (x_dtype); lr0/1/2 and grad_lr0/1/2 [B, L] (lr_dtype).  fp32 arithmetic;
+ * grad_lr* summed over D deterministically.  workspace:
+ * uttt_swiglu_bwd_bwd_workspace_bytes(B, D, L) bytes. */
+int uttt_swiglu_bwd_bwd(const void* dh, const void* x0_x2, int x_dtype, const void* lr0,
+                        const void* lr1, const void* lr2, int lr_dtype, const void* grad_dx0_dx2,
+                        const void* grad_hidden_lr1, int B, int D, int L, void* grad_dh,
+                        void* grad_x0_x2, void* grad_lr0, void* grad_lr1, void* grad_lr2,
+                        void* dx0_x2, void* hidden_lr1, void* workspace, size_t workspace_bytes,
+                        void* stream);
+
 /* Scratch bytes for uttt_grouped_update_bwd at (B, I, N). */
 size_t uttt_update_bwd_workspace_bytes(int B, int I, int N);
 

@@ -251,3 +251,76 @@ def fast_weight_grads_bwd(W0_W2, W1, K, V, lr0, lr1, lr2, group_sizes, G_W0_W2, 
     gw02, gw1 = two_gemm_fw_bwd(gx02, K, gdh, V, group_sizes, exact)
     glr = [t if exact else t.to(lr_dtype) for t in glr]
     return gw02, gw1, _r(gk, exact), _r(gv, exact), glr[0], glr[1], glr[2]
+
+
+# ------------------------------------------------ kernel-level backward pieces
+def four_grouped(W0_W2, G_W0_W2, W1, G_W1, K, V, group_sizes, exact=False):
+    """L/triton_lact_bwd_grouped_four_mm.py:443-501 (reference_four_grouped):
+    per segment Y0_Y2 = W0_W2 K^T, G_Y0_Y2 = G_W0_W2 K^T ([B,2I,N]),
+    DHidden = W1^T V^T, G_DHidden = G_W1^T V^T ([B,I,N]); fp32 accumulate, bf16."""
+    B, E, I2, D = W0_W2.shape
+    I = I2 // 2
+    N = K.shape[1]
+    outs = [torch.zeros(B, r, N, dtype=torch.float64) for r in (I2, I2, I, I)]
+    for b in range(B):
+        for e, s, g in segments(group_sizes[b]):
+            if g == 0:
+                continue
+            k = _f(K[b, s:s + g], exact)
+            v = _f(V[b, s:s + g], exact)
+            outs[0][b, :, s:s + g] = _f(W0_W2[b, e], exact) @ k.T
+            outs[1][b, :, s:s + g] = _f(G_W0_W2[b, e], exact) @ k.T
+            outs[2][b, :, s:s + g] = _f(W1[b, e], exact).T @ v.T
+            outs[3][b, :, s:s + g] = _f(G_W1[b, e], exact).T @ v.T
+    return tuple(_r(o, exact) for o in outs)
+
+
+def swiglu_bwd_bwd(dh, x0_x2, lr0, lr1, lr2, grad_dx0_dx2, grad_hidden_lr1, exact=False):
+    """L/triton_pointwise_kernels.py:354-436.  Inputs [B,I,L] / [B,2I,L] /
+    [B,L]; fp32 (fp64 when exact) arithmetic.  Returns (grad_dh, grad_x0_x2,
+    grad_lr0, grad_lr1, grad_lr2, dx0_x2, hidden_lr1) with element outputs in
+    the activations' dtype and the lr gradients in the lrs' dtype."""
+    xd, ld = x0_x2.dtype, lr0.dtype
+    acc = torch.float64 if exact else torch.float32
+    h = dh.to(acc)
+    x0, x2 = x0_x2.to(acc).chunk(2, dim=1)
+    g0, g2 = grad_dx0_dx2.to(acc).chunk(2, dim=1)
+    gh = grad_hidden_lr1.to(acc)
+    l0, l1, l2 = (x.to(acc).unsqueeze(1) for x in (lr0, lr1, lr2))
+    sg = torch.sigmoid(x0)
+    silu = x0 * sg
+    m = sg * (1 + x0 * (1 - sg))
+    grad_dh = g0 * l0 * x2 * m + g2 * l2 * silu
+    grad_x2 = g0 * l0 * h * m + gh * l1 * silu
+    grad_sig = g0 * l0 * h * x2 * (1 + x0 - 2 * sg * x0)
+    grad_x0 = (g2 * l2 * h + gh * l1 * x2) * m + g0 * l0 * h * x2 * sg * (1 - sg) \
+        + grad_sig * sg * (1 - sg)
+    glr0 = (g0 * h * x2 * m).sum(1)
+    glr1 = (gh * x2 * silu).sum(1)
+    glr2 = (g2 * h * silu).sum(1)
+    dx02 = torch.cat([h * x2 * m * l0, silu * h * l2], dim=1)
+    hl1 = l1 * x2 * silu
+    cx = (lambda t: t) if exact else (lambda t: t.to(xd))
+    cl = (lambda t: t) if exact else (lambda t: t.to(ld))
+    return (cx(grad_dh), cx(torch.cat([grad_x0, grad_x2], dim=1)), cl(glr0), cl(glr1), cl(glr2),
+            cx(dx02), cx(hl1))
+
+
+def grad_kv(G_W0_W2, W0_W2, DY_lr, dY_02, W1, G_W1, dH, H_lr, group_sizes, exact=False):
+    """L/triton_lact_bwd_grouped_grad_kv.py:344-396 (reference_grad_kv): per
+    segment grad_K = G_W0_W2^T DY_lr + W0_W2^T dY_02 and
+    grad_V = W1 dH + G_W1 H_lr, both [B,N,D]; fp32 accumulate, bf16."""
+    B, E, I2, D = W0_W2.shape
+    N = DY_lr.shape[2]
+    gk = torch.zeros(B, N, D, dtype=torch.float64)
+    gv = torch.zeros(B, N, D, dtype=torch.float64)
+    for b in range(B):
+        for e, s, g in segments(group_sizes[b]):
+            if g == 0:
+                continue
+            sl = slice(s, s + g)
+            gk[b, sl] = (_f(G_W0_W2[b, e], exact).T @ _f(DY_lr[b, :, sl], exact)
+                         + _f(W0_W2[b, e], exact).T @ _f(dY_02[b, :, sl], exact)).T
+            gv[b, sl] = (_f(W1[b, e], exact) @ _f(dH[b, :, sl], exact)
+                         + _f(G_W1[b, e], exact) @ _f(H_lr[b, :, sl], exact)).T
+    return _r(gk, exact), _r(gv, exact)

@@ -198,3 +198,60 @@ def test_update_backward_is_autograd_of_update():
                 assert torch.allclose(gl1[b, s:s + n], l1.grad, **tol)
                 assert torch.allclose(gl2[b, s:s + n], l2.grad, **tol)
             s += n
+
+
+def test_swiglu_bwd_bwd_is_vjp_of_first_order_map():
+    """The pointwise pass (exact mode) returns the first-order values and the
+    vector-Jacobian product of (dh, x0, x2, lr) -> (dx0, dx2, hidden_lr1)
+    with the given cotangents, as torch.autograd computes it."""
+    g = torch.Generator().manual_seed(21)
+    B, I, L = 2, 5, 7
+    dh = torch.randn(B, I, L, generator=g, dtype=torch.float64)
+    x02 = torch.randn(B, 2 * I, L, generator=g, dtype=torch.float64)
+    lr = [torch.rand(B, L, generator=g, dtype=torch.float64) for _ in range(3)]
+    gdx = torch.randn(B, 2 * I, L, generator=g, dtype=torch.float64)
+    ghl = torch.randn(B, I, L, generator=g, dtype=torch.float64)
+    out = FW.swiglu_bwd_bwd(dh, x02, *lr, gdx, ghl, exact=True)
+    h = dh.clone().requires_grad_()
+    x = x02.clone().requires_grad_()
+    ls = [t.clone().requires_grad_() for t in lr]
+    x0, x2 = x[:, :I], x[:, I:]
+    silu = F.silu(x0)
+    dsilu = torch.autograd.grad(silu.sum(), x0, create_graph=True)[0]   # silu'(x0) by autograd
+    dx0 = ls[0][:, None] * h * x2 * dsilu
+    dx2 = ls[2][:, None] * h * silu
+    hl1 = ls[1][:, None] * x2 * silu
+    loss = (dx0 * gdx[:, :I]).sum() + (dx2 * gdx[:, I:]).sum() + (hl1 * ghl).sum()
+    gh, gx, g0, g1, g2 = torch.autograd.grad(loss, [h, x, *ls])
+    tol = dict(rtol=1e-10, atol=1e-12)
+    assert torch.allclose(out[0], gh, **tol)
+    assert torch.allclose(out[1], gx, **tol)
+    for a, b_ in zip(out[2:5], (g0, g1, g2)):
+        assert torch.allclose(a, b_, **tol)
+    assert torch.allclose(out[5], torch.cat([dx0, dx2], 1).detach(), **tol)
+    assert torch.allclose(out[6], hl1.detach(), **tol)
+
+
+def test_backward_pieces_compose_to_update_backward():
+    """four_grouped -> swiglu_bwd_bwd -> grad_kv -> two_gemm_fw_bwd, composed
+    as the reference's backward does (L/lact_fw_grad.py:177-288), equals the
+    autograd-pinned UPDATE backward in exact mode."""
+    gs = [[4, 0, 6], [2, 5, 3]]
+    W02, W1, K, V, lr, gsz = _inputs(2, 3, 8, 12, gs, seed=9)
+    g = torch.Generator().manual_seed(10)
+    GW02 = torch.randn(W02.shape, generator=g).to(torch.bfloat16)
+    GW1 = torch.randn(W1.shape, generator=g).to(torch.bfloat16)
+    ref = FW.fast_weight_grads_bwd(W02, W1, K, V, *lr, gsz, GW02, GW1, exact=True)
+    y02, gy02, dh, gdh = FW.four_grouped(W02, GW02, W1, GW1, K, V, gsz, exact=True)
+    lr64 = [x.double() for x in lr]
+    g_dh, g_x02, gl0, gl1, gl2, dx02, hl1 = FW.swiglu_bwd_bwd(dh, y02, *lr64, gy02, gdh, exact=True)
+    gk, gv = FW.grad_kv(GW02, W02, dx02, g_x02, W1, GW1, g_dh, hl1, gsz, exact=True)
+    gw02, gw1 = FW.two_gemm_fw_bwd(g_x02, K, g_dh, V, gsz, exact=True)
+    N = K.shape[1]
+    cols = FW.written_columns(gsz, N)
+    tol = dict(rtol=1e-10, atol=1e-12)
+    assert torch.allclose(gw02, ref[0], **tol) and torch.allclose(gw1, ref[1], **tol)
+    assert torch.allclose(gk[cols], ref[2][cols], **tol)
+    assert torch.allclose(gv[cols], ref[3][cols], **tol)
+    for a, b_ in zip((gl0, gl1, gl2), ref[4:]):
+        assert torch.allclose(a[cols], b_[cols], **tol)

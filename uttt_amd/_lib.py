@@ -87,6 +87,16 @@ SIGNATURES = {
          c_int, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_sz, c_p],
     ),
     "uttt_transpose_2byte": (c_int, [c_p, c_int, c_int, c_int, c_p, c_p]),
+    "uttt_grouped_gemm_nt2": (c_int, [c_p, c_p, c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int,
+                                      c_p, c_p]),
+    "uttt_grouped_gemm_tn2": (c_int, [c_p, c_p, c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int,
+                                      c_p, c_p]),
+    "uttt_swiglu_bwd_bwd_workspace_bytes": (c_sz, [c_int, c_int, c_int]),
+    "uttt_swiglu_bwd_bwd": (
+        c_int,
+        [c_p, c_p, c_int, c_p, c_p, c_p, c_int, c_p, c_p, c_int, c_int, c_int, c_p, c_p, c_p, c_p,
+         c_p, c_p, c_p, c_p, c_sz, c_p],
+    ),
     "uttt_write_step": (
         c_int,
         [c_p, c_p, c_p, c_int, c_p, c_p, ctypes.c_float, c_int, c_i64, c_int, c_int, c_int, c_int,

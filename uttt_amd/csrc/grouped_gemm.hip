@@ -608,6 +608,34 @@ extern "C" int uttt_grouped_gemm_tn(const void* w, const void* x, const int32_t*
                              "grouped_gemm_tn");
 }
 
+extern "C" int uttt_grouped_gemm_nt2(const void* wa, const void* xa, const void* wb,
+                                     const void* xb, const int32_t* group_sizes, int B, int E,
+                                     int M, int K, int N, void* y, void* stream) {
+  UTTT_REQUIRE(B >= 0 && E >= 1 && M >= 0 && K >= 0 && N >= 0, "grouped_gemm_nt2: bad sizes");
+  UTTT_REQUIRE(M % 8 == 0 && K % 8 == 0, "grouped_gemm_nt2: M=%d and K=%d must be multiples of 8", M, K);
+  if (B == 0 || N == 0 || M == 0) return UTTT_OK;
+  UTTT_REQUIRE(wa && xa && wb && xb && group_sizes && y, "grouped_gemm_nt2: null pointer");
+  UTTT_REQUIRE(aligned16(wa) && aligned16(xa) && aligned16(wb) && aligned16(xb) && aligned16(y),
+               "grouped_gemm_nt2: tensors must be 16-byte aligned");
+  return launch_wide<KMajor>(wa, xa, K, wb, xb, K, M, K, (int64_t)M * K,
+                             static_cast<uint16_t*>(y), B, E, N, group_sizes, as_stream(stream),
+                             "grouped_gemm_nt2");
+}
+
+extern "C" int uttt_grouped_gemm_tn2(const void* wa, const void* xa, const void* wb,
+                                     const void* xb, const int32_t* group_sizes, int B, int E,
+                                     int M, int K, int N, void* y, void* stream) {
+  UTTT_REQUIRE(B >= 0 && E >= 1 && M >= 0 && K >= 0 && N >= 0, "grouped_gemm_tn2: bad sizes");
+  UTTT_REQUIRE(M % 8 == 0 && K % 8 == 0, "grouped_gemm_tn2: M=%d and K=%d must be multiples of 8", M, K);
+  if (B == 0 || N == 0 || M == 0) return UTTT_OK;
+  UTTT_REQUIRE(wa && xa && wb && xb && group_sizes && y, "grouped_gemm_tn2: null pointer");
+  UTTT_REQUIRE(aligned16(wa) && aligned16(xa) && aligned16(wb) && aligned16(xb) && aligned16(y),
+               "grouped_gemm_tn2: tensors must be 16-byte aligned");
+  return launch_wide<RMajor>(wa, xa, K, wb, xb, K, M, M, (int64_t)M * K,
+                             static_cast<uint16_t*>(y), B, E, N, group_sizes, as_stream(stream),
+                             "grouped_gemm_tn2");
+}
+
 extern "C" size_t uttt_update_stage1_workspace_bytes(int B, int I, int N) {
   if (B <= 0 || I <= 0 || N <= 0) return 0;
   return up256((size_t)B * N * I * sizeof(float));

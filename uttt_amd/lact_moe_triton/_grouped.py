@@ -155,3 +155,56 @@ def transpose_last2(X):
     out = torch.empty((B, C, R), dtype=X.dtype, device=X.device)
     L.call("uttt_transpose_2byte", L.ptr(X), B, R, C, L.ptr(out), L.stream_of(X))
     return out
+
+
+def _gemm2(name, Wa, Xa, Wb, Xb, group_sizes, rows_first: bool):
+    L.require_device(Wa, Xa, Wb, Xb, group_sizes)
+    _check_bf16(Wa, Xa, Wb, Xb)
+    assert Wa.shape == Wb.shape and Xa.shape == Xb.shape, "the two pairs must match in shape"
+    B, E, R, C = Wa.shape
+    M, K = (R, C) if rows_first else (C, R)
+    Bx, N, Kx = Xa.shape
+    assert Bx == B and Kx == K, "X must be [B, N, K] with matching B, K"
+    gs = group_sizes_i32(group_sizes)
+    assert gs.shape == (B, E)
+    Y = torch.empty((B, N, M), dtype=torch.bfloat16, device=Xa.device)
+    L.call(name, L.ptr(Wa), L.ptr(Xa), L.ptr(Wb), L.ptr(Xb), L.ptr(gs), B, E, M, K, N, L.ptr(Y),
+           L.stream_of(Xa))
+    return Y
+
+
+def gemm_nt2(Wa, Xa, Wb, Xb, group_sizes):
+    """Y[b, n] = Wa[b, e(n)] Xa[b, n] + Wb[b, e(n)] Xb[b, n]: W [B,E,M,K] -> [B,N,M]."""
+    return _gemm2("uttt_grouped_gemm_nt2", Wa, Xa, Wb, Xb, group_sizes, True)
+
+
+def gemm_tn2(Wa, Xa, Wb, Xb, group_sizes):
+    """Y[b, n] = Wa[b, e(n)]^T Xa[b, n] + Wb[b, e(n)]^T Xb[b, n]: W [B,E,K,M] -> [B,N,M]."""
+    return _gemm2("uttt_grouped_gemm_tn2", Wa, Xa, Wb, Xb, group_sizes, False)
+
+
+def swiglu_bwd_bwd(dh, x0_x2, lr0, lr1, lr2, grad_dx0_dx2, grad_hidden_lr1):
+    """Second-order SwiGLU pointwise pass on [B, I, L] / [B, 2I, L] tensors."""
+    L.require_device(dh, x0_x2, lr0, lr1, lr2, grad_dx0_dx2, grad_hidden_lr1)
+    B, I, Lt = dh.shape
+    assert x0_x2.shape == (B, 2 * I, Lt) and grad_dx0_dx2.shape == (B, 2 * I, Lt)
+    assert grad_hidden_lr1.shape == (B, I, Lt)
+    for t in (lr0, lr1, lr2):
+        assert t.shape == (B, Lt), "lr tensors must be [B, L]"
+    xd, ld = x0_x2.dtype, lr0.dtype
+    assert dh.dtype == xd and grad_dx0_dx2.dtype == xd and grad_hidden_lr1.dtype == xd
+    assert lr1.dtype == ld and lr2.dtype == ld
+    ins = [t.contiguous() for t in (dh, x0_x2, lr0, lr1, lr2, grad_dx0_dx2, grad_hidden_lr1)]
+    dev = dh.device
+    g_dh = torch.empty((B, I, Lt), dtype=xd, device=dev)
+    g_x = torch.empty((B, 2 * I, Lt), dtype=xd, device=dev)
+    glr = [torch.empty((B, Lt), dtype=ld, device=dev) for _ in range(3)]
+    dx = torch.empty((B, 2 * I, Lt), dtype=xd, device=dev)
+    hl = torch.empty((B, I, Lt), dtype=xd, device=dev)
+    ws_bytes = L.lib().uttt_swiglu_bwd_bwd_workspace_bytes(B, I, Lt)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    L.call("uttt_swiglu_bwd_bwd", L.ptr(ins[0]), L.ptr(ins[1]), L.dtype_code(xd), L.ptr(ins[2]),
+           L.ptr(ins[3]), L.ptr(ins[4]), L.dtype_code(ld), L.ptr(ins[5]), L.ptr(ins[6]), B, I, Lt,
+           L.ptr(g_dh), L.ptr(g_x), L.ptr(glr[0]), L.ptr(glr[1]), L.ptr(glr[2]), L.ptr(dx),
+           L.ptr(hl), L.ptr(ws), ws_bytes, L.stream_of(dh))
+    return g_dh, g_x, glr[0], glr[1], glr[2], dx, hl
