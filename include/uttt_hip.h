@@ -46,6 +46,42 @@ int uttt_abi_version(void);
 const char* uttt_last_error(void);
 
 /* ------------------------------------------------------------------------ */
+/* Router                                                                   */
+/* ------------------------------------------------------------------------ */
+
+/* Scratch bytes for uttt_router_select / uttt_route_tokens at (B, T, E). */
+size_t uttt_router_workspace_bytes(int B, int T, int E);
+
+/* Replaces create_router_mask_sizes_probs (M/moe_routing.py:7-75), M =
+ * uttt_llm/flame/custom_models/uttt_moe.  logits fp32 addressed
+ * logits[b*l_sb + e*l_se + t*l_st]; bias: optional fp32 [E] per batch
+ * (bias_sb = 0: shared), added to the selection scores only.
+ * router_type: 0 softmax, 1 norm_softmax, 2 norm_relu; combine_mode:
+ * 0 selected_prob, 1 topk_renorm; router_scale <= 0 means sqrt(E).
+ * Outputs (contiguous): mask [B,E,T] uint8 0/1 (torch.bool), group_sizes
+ * [B,E] int32 (optional), combine and balance [B,E,T] fp32, lb_loss fp32
+ * scalar (optional).  Top-k picks the lower expert index among equal scores.
+ * E <= 128, 1 <= topk <= E. */
+int uttt_router_select(const float* logits, int64_t l_sb, int64_t l_se, int64_t l_st,
+                       const float* bias, int64_t bias_sb, int B, int E, int T, int topk,
+                       int router_type, int combine_mode, float alpha, float router_scale,
+                       float norm_eps, void* mask, int32_t* group_sizes, float* combine,
+                       float* balance, float* lb_loss, void* workspace, size_t workspace_bytes,
+                       void* stream);
+
+/* Replaces FastWeightMLPSubNN._route_tokens (M/modeling_recurrent_lact.py:147-169):
+ * logits[b,e,t] = sum_d router_w[b,e,d] x[b,t,d] in fp32 (x [B,T,D]
+ * contiguous of x_dtype, router_w fp32 [E,D] with batch stride w_sb, 0 =
+ * shared), then the selection of uttt_router_select, in one launch plus a
+ * one-workgroup finalize.  logits_out: optional fp32 [B,E,T]. */
+int uttt_route_tokens(const void* x, int x_dtype, const float* router_w, int64_t w_sb, int B,
+                      int T, int D, int E, const float* bias, int64_t bias_sb, int topk,
+                      int router_type, int combine_mode, float alpha, float router_scale,
+                      float norm_eps, float* logits_out, void* mask, int32_t* group_sizes,
+                      float* combine, float* balance, float* lb_loss, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
 /* Routing map                                                              */
 /* ------------------------------------------------------------------------ */
 

@@ -12,11 +12,13 @@ import torch
 import torch.nn.functional as F
 
 
-def create_router_mask_sizes_probs(router_logits, topk, alpha=1.0, router_type="softmax",
-                                   combine_mode="selected_prob", router_scale=0.0,
-                                   norm_eps=1e-6, routing_bias=None):
+def create_router_mask_sizes_probs(router_logits, topk, alpha=1.0, use_sigmoid=False,
+                                   router_type="softmax", combine_mode="selected_prob",
+                                   router_scale=0.0, norm_eps=1e-6, routing_bias=None):
     """Returns (mask [B,E,T] bool, group_sizes [B,E] int32, combine [B,E,T],
     balance_probs [B,E,T], lb_loss)."""
+    if use_sigmoid:                                                 # R:19-22
+        raise NotImplementedError("sigmoid routing")
     E = router_logits.shape[-2]
     logits = router_logits.to(torch.float32)
     if router_type == "softmax":                                    # R:25-27
@@ -52,3 +54,12 @@ def create_router_mask_sizes_probs(router_logits, topk, alpha=1.0, router_type="
     gm = gs.to(torch.float32).mean(dim=0)
     lb = (pm * (gm / gm.sum())).sum() * E
     return mask, gs, comb, balance, lb
+
+
+def router_logits(x, router_w):
+    """_route_tokens' logits (modeling_recurrent_lact.py:153-157): R x^T with
+    fp32 operands; here accumulated in fp64 and returned as fp64 [B, E, T]."""
+    R = router_w.double()
+    if R.dim() == 2:
+        R = R.unsqueeze(0)
+    return torch.matmul(R, x.double().transpose(1, 2))

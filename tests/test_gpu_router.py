@@ -1,0 +1,120 @@
+"""GPU parity of the router (csrc/router.hip via uttt_amd.routing) against
+oracle/routing.py on the same seeded logits.
+
+Bar: mask and group_sizes bit-exact.  For the softmax router the routing
+scores are the logits themselves, so the selection must match exactly; the
+norm variants divide by a norm whose fp32 rounding can differ by an ulp from
+torch's, and norm_relu clamps negative scores to exactly 0 (true ties, whose
+order torch.topk leaves unspecified), so a token may only differ where its
+k-th and (k+1)-th routing scores are within 1e-5; lb_loss is then checked
+against the value implied by the kernel's own group sizes.  combine,
+balance and lb_loss within rtol 1e-5 (fp32; exp and the sums round
+differently).  The fused route (logits = R x^T in fp32) is compared with the
+fp64 product within 1e-4 relative to |R||x|, and its selection with the
+oracle's on the kernel's own logits.
+"""
+import pytest
+import torch
+
+from oracle import routing as OR
+from uttt_amd import routing as RT
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _cmp(ours, ref, k, logits_for_ties, bias=None):
+    mask, gs, comb, bal, lb = ours
+    rmask, rgs, rcomb, rbal, rlb = ref
+    mask = mask.cpu()
+    diff = (mask != rmask).any(1)                       # [B, T] tokens that differ
+    if diff.any():
+        sc = logits_for_ties if bias is None else logits_for_ties + bias
+        top = sc.topk(k + 1, dim=1).values
+        gap = (top[:, k - 1] - top[:, k])[diff]
+        assert (gap.abs() < 1e-5).all(), f"selection differs away from a near tie: {gap}"
+    else:
+        assert torch.equal(gs.cpu(), rgs)
+    torch.testing.assert_close(bal.cpu(), rbal, rtol=1e-5, atol=1e-7)
+    ok = ~diff.unsqueeze(1).expand_as(rcomb)
+    torch.testing.assert_close(comb.cpu()[ok], rcomb[ok], rtol=1e-5, atol=1e-7)
+    if diff.any():
+        # the counts differ at tied tokens: lb_loss from our group sizes
+        E = rbal.shape[1]
+        gm = gs.cpu().float().mean(0)
+        rlb = (rbal.mean(0).mean(-1) * (gm / gm.sum())).sum() * E
+    torch.testing.assert_close(lb.cpu(), rlb, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("E,k", [(16, 2), (32, 2), (7, 3), (128, 4)])
+@pytest.mark.parametrize("rt", ["softmax", "norm_softmax", "norm_relu"])
+@pytest.mark.parametrize("cm", ["selected_prob", "topk_renorm"])
+def test_router_select(E, k, rt, cm):
+    B, T = 2, 3001
+    g = torch.Generator().manual_seed(E * 7 + k)
+    logits = torch.randn(B, E, T, generator=g)
+    bias = (torch.randn(1, E, 1, generator=g) * 0.5) if E != 7 else None
+    kw = dict(alpha=0.8, router_type=rt, combine_mode=cm, routing_bias=bias)
+    ours = RT.create_router_mask_sizes_probs(logits.to(DEV), k,
+                                             **{**kw, "routing_bias": None if bias is None else bias.to(DEV)})
+    ref = OR.create_router_mask_sizes_probs(logits, k, **kw)
+    sel = logits if rt == "softmax" else None
+    if rt != "softmax":
+        n = logits.norm(dim=1, keepdim=True).clamp_min(1e-6)
+        z = logits / n * (E ** 0.5)
+        sel = z if rt == "norm_softmax" else z.clamp_min(0)
+    if rt == "softmax":
+        assert torch.equal(ours[0].cpu(), ref[0]) and torch.equal(ours[1].cpu(), ref[1])
+    _cmp(ours, ref, k, sel, bias)
+
+
+def test_router_select_strided_logits_and_batch_bias():
+    # logits given as a [B, T, E] tensor viewed [B, E, T]; a per-batch bias
+    B, T, E, k = 3, 700, 12, 2
+    g = torch.Generator().manual_seed(3)
+    lt = torch.randn(B, T, E, generator=g)
+    bias = torch.randn(B, E, 1, generator=g)
+    ours = RT.create_router_mask_sizes_probs(lt.to(DEV).transpose(1, 2), k, routing_bias=bias.to(DEV),
+                                             combine_mode="topk_renorm")
+    ref = OR.create_router_mask_sizes_probs(lt.transpose(1, 2), k, routing_bias=bias,
+                                            combine_mode="topk_renorm")
+    assert torch.equal(ours[0].cpu(), ref[0]) and torch.equal(ours[1].cpu(), ref[1])
+    _cmp(ours, ref, k, lt.transpose(1, 2), bias)
+
+
+@pytest.mark.parametrize("dtype,D,E,T", [(torch.bfloat16, 768, 16, 2048), (torch.bfloat16, 1536, 32, 1000),
+                                         (torch.float32, 100, 5, 333)])
+def test_route_tokens_fused(dtype, D, E, T):
+    B, k = 1, 2
+    g = torch.Generator().manual_seed(D + E)
+    x = torch.randn(B, T, D, generator=g)
+    x = (x / x.norm(dim=-1, keepdim=True)).to(dtype)
+    Rw = torch.randn(E, D, generator=g)
+    bias = torch.randn(1, E, 1, generator=g) * 0.5
+    mask, gs, comb, bal, lg = RT.route_tokens(x.to(DEV), Rw.to(DEV), k, routing_bias=bias.to(DEV),
+                                              combine_mode="topk_renorm", return_logits=True)
+    ref_lg = OR.router_logits(x, Rw)
+    scale = Rw.norm(dim=1).max().item() * x.float().norm(dim=-1).max().item()
+    assert (lg.cpu().double() - ref_lg).abs().max().item() < 1e-4 * scale
+    # the selection on the kernel's own logits is bit-exact
+    ref = OR.create_router_mask_sizes_probs(lg.cpu(), k, routing_bias=bias, combine_mode="topk_renorm")
+    assert torch.equal(mask.cpu(), ref[0]) and torch.equal(gs.cpu(), ref[1])
+    torch.testing.assert_close(comb.cpu(), ref[2], rtol=1e-5, atol=1e-7)
+    torch.testing.assert_close(bal.cpu(), ref[3], rtol=1e-5, atol=1e-7)
+    # and the fp64 logits select the same experts except at near ties
+    ref64 = OR.create_router_mask_sizes_probs(ref_lg.float(), k, routing_bias=bias,
+                                              combine_mode="topk_renorm")
+    diff = (mask.cpu() != ref64[0]).any(1)
+    if diff.any():
+        top = (ref_lg + bias).topk(k + 1, dim=1).values
+        assert ((top[:, k - 1] - top[:, k])[diff].abs() < 1e-4 * scale).all()
+
+
+def test_router_errors():
+    l = torch.randn(1, 4, 8, device=DEV)
+    with pytest.raises(NotImplementedError):
+        RT.create_router_mask_sizes_probs(l, 1, 1.0, True)
+    with pytest.raises(ValueError):
+        RT.create_router_mask_sizes_probs(l, 1, router_type="sigmoid")
+    with pytest.raises(RuntimeError, match="topk"):
+        RT.create_router_mask_sizes_probs(l, 5)

@@ -1,0 +1,118 @@
+"""MoE router on the gfx950 kernels of csrc/router.hip.
+
+  create_router_mask_sizes_probs  same signature, outputs and errors as
+      uttt_llm/flame/custom_models/uttt_moe/moe_routing.py:7-75
+  route_tokens                    FastWeightMLPSubNN._route_tokens,
+      uttt_llm/flame/custom_models/uttt_moe/modeling_recurrent_lact.py:147-169:
+      fp32 logits R x^T and the selection in one fused launch
+
+Outputs are freshly allocated on the inputs' device.  Top-k keeps the lower
+expert index among exactly equal routing scores (torch.topk leaves that
+order unspecified).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib as L
+
+ROUTER_TYPES = {"softmax": 0, "norm_softmax": 1, "norm_relu": 2}
+COMBINE_MODES = {"selected_prob": 0, "topk_renorm": 1}
+
+
+def _check_modes(use_sigmoid, router_type, combine_mode):
+    if use_sigmoid:
+        raise NotImplementedError("Sigmoid routing is not implemented for ttt_dense_base_moe.")
+    if router_type not in ROUTER_TYPES:
+        raise ValueError("`router_type` must be 'softmax', 'norm_softmax', or 'norm_relu', "
+                         f"got {router_type!r}.")
+    if combine_mode not in COMBINE_MODES:
+        raise ValueError("`combine_mode` must be 'selected_prob' or 'topk_renorm', "
+                         f"got {combine_mode!r}.")
+
+
+def _bias_arg(routing_bias, B, E, device):
+    """A selection bias broadcastable to [B, E, 1] as a contiguous fp32 [Bb, E]
+    tensor and its batch stride (0 when shared)."""
+    if routing_bias is None:
+        return None, 0
+    rb = routing_bias.to(device=device, dtype=torch.float32)
+    if rb.dim() == 3:
+        assert rb.shape[2] == 1 and rb.shape[1] == E, "routing_bias must broadcast to [B, E, 1]"
+        rb = rb[:, :, 0]
+    elif rb.dim() == 2:
+        assert rb.shape == (E, 1), "routing_bias must broadcast to [B, E, 1]"
+        rb = rb.reshape(1, E)
+    else:
+        assert rb.shape == (E,), "routing_bias must broadcast to [B, E, 1]"
+        rb = rb.reshape(1, E)
+    assert rb.shape[0] in (1, B), "routing_bias batch dimension must be 1 or B"
+    rb = rb.contiguous()
+    return rb, (E if rb.shape[0] > 1 else 0)
+
+
+def _outputs(B, E, T, device):
+    mask = torch.empty((B, E, T), dtype=torch.bool, device=device)
+    gs = torch.empty((B, E), dtype=torch.int32, device=device)
+    comb = torch.empty((B, E, T), dtype=torch.float32, device=device)
+    bal = torch.empty((B, E, T), dtype=torch.float32, device=device)
+    lb = torch.empty((), dtype=torch.float32, device=device)
+    nbytes = L.lib().uttt_router_workspace_bytes(B, T, E)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+    return mask, gs, comb, bal, lb, ws, nbytes
+
+
+def create_router_mask_sizes_probs(router_logits, topk, alpha=1.0, use_sigmoid=False,
+                                   router_type="softmax", combine_mode="selected_prob",
+                                   router_scale=0.0, norm_eps=1e-6, routing_bias=None):
+    """router_logits [B, E, T] (any strides) -> (router_mask bool [B,E,T],
+    group_sizes int32 [B,E], combine_weights [B,E,T], balance_probs [B,E,T],
+    lb_loss); combine and balance in router_logits' dtype."""
+    _check_modes(use_sigmoid, router_type, combine_mode)
+    L.require_device(router_logits)
+    assert router_logits.dim() == 3, "router_logits must be [B, E, T]"
+    B, E, T = router_logits.shape
+    logits = router_logits if router_logits.dtype == torch.float32 else router_logits.float()
+    bias, bias_sb = _bias_arg(routing_bias, B, E, logits.device)
+    mask, gs, comb, bal, lb, ws, nbytes = _outputs(B, E, T, logits.device)
+    L.call("uttt_router_select", L.ptr(logits), logits.stride(0), logits.stride(1),
+           logits.stride(2), L.ptr(bias), bias_sb, B, E, T, int(topk), ROUTER_TYPES[router_type],
+           COMBINE_MODES[combine_mode], float(alpha), float(router_scale), float(norm_eps),
+           L.ptr(mask), L.ptr(gs), L.ptr(comb), L.ptr(bal), L.ptr(lb), L.ptr(ws), nbytes,
+           L.stream_of(logits))
+    if router_logits.dtype != torch.float32:
+        comb, bal = comb.to(router_logits.dtype), bal.to(router_logits.dtype)
+    return mask, gs, comb, bal, lb
+
+
+def route_tokens(x, router_proj_weights, topk, alpha=1.0, use_sigmoid=False,
+                 router_type="softmax", combine_mode="selected_prob", router_scale=0.0,
+                 norm_eps=1e-6, routing_bias=None, return_logits=False):
+    """x [B, T, D] (bf16 / fp16 / fp32), router_proj_weights [E, D] or [B, E, D]
+    -> (expert_mask, group_sizes, router_probs, balance_probs) as _route_tokens
+    returns them (router_probs = the combine weights), plus the fp32 logits
+    [B, E, T] when return_logits."""
+    _check_modes(use_sigmoid, router_type, combine_mode)
+    L.require_device(x, router_proj_weights)
+    assert x.dim() == 3, "x must be [B, T, D]"
+    B, T, D = x.shape
+    x = x.contiguous()
+    R = router_proj_weights.to(torch.float32).contiguous()
+    if R.dim() == 2:
+        E = R.shape[0]
+        w_sb = 0
+    else:
+        assert R.dim() == 3 and R.shape[0] in (1, B), "router weights must be [E,D] or [B,E,D]"
+        E = R.shape[1]
+        w_sb = E * D if R.shape[0] > 1 else 0
+    assert R.shape[-1] == D, "router weights must have x's last dimension"
+    bias, bias_sb = _bias_arg(routing_bias, B, E, x.device)
+    mask, gs, comb, bal, lb, ws, nbytes = _outputs(B, E, T, x.device)
+    logits = torch.empty((B, E, T), dtype=torch.float32, device=x.device) if return_logits else None
+    L.call("uttt_route_tokens", L.ptr(x), L.dtype_code(x.dtype), L.ptr(R), w_sb, B, T, D, E,
+           L.ptr(bias), bias_sb, int(topk), ROUTER_TYPES[router_type],
+           COMBINE_MODES[combine_mode], float(alpha), float(router_scale), float(norm_eps),
+           L.ptr(logits), L.ptr(mask), L.ptr(gs), L.ptr(comb), L.ptr(bal), L.ptr(lb), L.ptr(ws),
+           nbytes, L.stream_of(x))
+    out = (mask, gs, comb, bal)
+    return out + (logits,) if return_logits else out
