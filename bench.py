@@ -345,6 +345,17 @@ class MoeSweep:
         # fp32 masters of the pool for the WRITE step (w0 and w2 rows stay
         # concatenated: the norm-preserving write is per row)
         self.M02, self.M1 = self.W02.float(), self.W1.float()
+        # one router shared by all layers (the reference's "share_all" mode):
+        # logits = R x with x L2-normalised and R ~ N(0, 1), so logits ~ N(0, 1);
+        # the expert prior (Zipf for configs[4], N(0, 0.5) otherwise) is the
+        # selection-only routing bias; gates are top-k renormalised
+        self.R = torch.randn(E, D, generator=g, device=dev)
+        if cfg["zipf"] is not None:
+            self.rbias = -cfg["zipf"] * torch.log(torch.arange(E, device=dev, dtype=torch.float32) + 1)
+        else:
+            self.rbias = torch.randn(E, generator=g, device=dev) * 0.5
+        self.route_a = self._route_buffers(T)
+        self.route_u = self._route_buffers(T)
         if cfg["train"]:
             self.GW02 = randn(1, E, 2 * I, D, scale=0.02)
             self.GW1 = randn(1, E, D, I, scale=0.02)
@@ -369,6 +380,28 @@ class MoeSweep:
         self.events = None
         self.batched = None
 
+    def _route_buffers(self, T):
+        import torch
+
+        E, dev = self.E, self.dev
+        nb = self.L.lib().uttt_router_workspace_bytes(1, T, E, self.D)
+        return dict(T=T, mask=torch.empty(1, E, T, dtype=torch.bool, device=dev),
+                    gs=torch.empty(1, E, dtype=torch.int32, device=dev),
+                    gates=torch.empty(1, E, T, dtype=torch.float32, device=dev),
+                    bal=torch.empty(1, E, T, dtype=torch.float32, device=dev),
+                    lb=torch.empty((), dtype=torch.float32, device=dev),
+                    ws=torch.empty(nb, dtype=torch.uint8, device=dev), ws_bytes=nb)
+
+    def route(self, x, rb):
+        """Fused router on x [1, T, D]: logits R x^T, top-k with the prior as
+        selection bias, topk_renorm gates, group sizes (route_tokens)."""
+        L = self.L
+        self._mark("router")
+        L.call("uttt_route_tokens", L.ptr(x), L.BF16, L.ptr(self.R), 0, 1, rb["T"], self.D, self.E,
+               L.ptr(self.rbias), 0, self.k, 0, 1, 1.0, 0.0, 1e-6, None, L.ptr(rb["mask"]),
+               L.ptr(rb["gs"]), L.ptr(rb["gates"]), L.ptr(rb["bal"]), L.ptr(rb["lb"]),
+               L.ptr(rb["ws"]), rb["ws_bytes"], self.stream)
+
     def prepare_batched(self, layers):
         """Inputs and buffers of the cross-layer batched UPDATE: the k, v, lr and
         routing of all `layers` writers of a chunk concatenated along the token
@@ -389,6 +422,7 @@ class MoeSweep:
         bt["mask"] = torch.cat([st["mask_u"] for st in sets], dim=2).contiguous()
         bt["gates"] = torch.cat([st["gates_u"] for st in sets], dim=2).contiguous()
         bt["gs"] = bt["mask"].sum(-1).to(torch.int32).contiguous()
+        bt["route"] = self._route_buffers(T)
         e = lambda *shape, dt=torch.bfloat16: torch.empty(*shape, dtype=dt, device=self.dev)
         bt["rmap"] = e(1, T, 2 * E + 1, dt=torch.int32)
         bt["ws_map"] = e(L.lib().uttt_row_id_map_workspace_bytes(1, T, E), dt=torch.uint8)
@@ -421,7 +455,9 @@ class MoeSweep:
 
     def apply(self, st):
         L, E, D, I, T, N, s = self.L, self.E, self.D, self.I, self.T, self.N, self.stream
-        m, p = st["mask_a"], st["gates_a"]
+        rb = self.route_a
+        self.route(st["x"], rb)
+        m, p, gs = rb["mask"], rb["gates"], rb["gs"]
         self._mark("row_map")
         L.call("uttt_make_row_id_map", L.ptr(m), 1, m.stride(0), m.stride(1), m.stride(2), 1, T,
                E, L.ptr(self.rmap), None, L.ptr(self.ws_map), self.ws_map.numel(), s)
@@ -430,10 +466,10 @@ class MoeSweep:
                L.ptr(p), p.stride(0), p.stride(1), p.stride(2), L.ptr(self.xp), N,
                L.ptr(self.pp), s)
         self._mark("gate_up")
-        L.call("uttt_grouped_gate_up", L.ptr(self.W02), L.ptr(self.xp), L.ptr(st["gs_a"]), 1, E,
+        L.call("uttt_grouped_gate_up", L.ptr(self.W02), L.ptr(self.xp), L.ptr(gs), 1, E,
                I, D, N, L.ptr(self.hid), 1, s)
         self._mark("down_proj")
-        L.call("uttt_grouped_gemm_nt", L.ptr(self.W1), L.ptr(self.hid), L.ptr(st["gs_a"]), 1, E,
+        L.call("uttt_grouped_gemm_nt", L.ptr(self.W1), L.ptr(self.hid), L.ptr(gs), 1, E,
                D, I, N, L.ptr(self.yp), s)
         self._mark("unpermute")
         L.call("uttt_unpermute_fwd", L.ptr(self.yp), L.BF16, 1, N, D, L.ptr(self.rmap), T, E,
@@ -454,8 +490,8 @@ class MoeSweep:
 
     def update(self, st):
         """One writer's UPDATE (the reference's per-layer call pattern)."""
-        buf = dict(T=self.T, N=self.N, k=st["k"], v=st["v"], lr=st["lr"], mask=st["mask_u"],
-                   gates=st["gates_u"], gs=st["gs_u"], rmap=self.rmap, ws_map=self.ws_map,
+        buf = dict(T=self.T, N=self.N, k=st["k"], v=st["v"], lr=st["lr"], route=self.route_u,
+                   rmap=self.rmap, ws_map=self.ws_map,
                    kp=self.kp, vp=self.vp, lrp=self.lrp, dy=self.dy, hl=self.hl,
                    ws_s1=self.ws_s1, ws_s1_bytes=self.ws_s1_bytes)
         if self.cfg["train"]:
@@ -469,7 +505,9 @@ class MoeSweep:
     def _update(self, bt):
         L, E, D, I, s = self.L, self.E, self.D, self.I, self.stream
         T, N = bt["T"], bt["N"]
-        m, p, gs, lr = bt["mask"], bt["gates"], bt["gs"], bt["lr"]
+        rb = bt["route"]
+        self.route(bt["k"], rb)
+        m, p, gs, lr = rb["mask"], rb["gates"], rb["gs"], bt["lr"]
         self._mark("row_map(update)")
         L.call("uttt_make_row_id_map", L.ptr(m), 1, m.stride(0), m.stride(1), m.stride(2), 1, T,
                E, L.ptr(bt["rmap"]), None, L.ptr(bt["ws_map"]), bt["ws_map"].numel(), s)
@@ -517,14 +555,17 @@ class MoeSweep:
             out[name] = e0.elapsed_time(e1) * 1e-3 / reps
 
         N = self.N
+        gs_a = self.route_a["gs"]   # the last apply's routing
         timed("gate_up", lambda: L.call("uttt_grouped_gate_up", L.ptr(self.W02), L.ptr(self.xp),
-                                        L.ptr(st["gs_a"]), 1, E, I, D, N, L.ptr(self.hid), 1, s))
+                                        L.ptr(gs_a), 1, E, I, D, N, L.ptr(self.hid), 1, s))
         timed("down_proj", lambda: L.call("uttt_grouped_gemm_nt", L.ptr(self.W1), L.ptr(self.hid),
-                                          L.ptr(st["gs_a"]), 1, E, D, I, N, L.ptr(self.yp), s))
+                                          L.ptr(gs_a), 1, E, D, I, N, L.ptr(self.yp), s))
+        timed("router", lambda: self.route(st["x"], self.route_a))
         if bt is not None:
-            Nu, gs, kp, vp, dy, hl = bt["N"], bt["gs"], bt["kp"], bt["vp"], bt["dy"], bt["hl"]
+            Nu, gs, kp, vp, dy, hl = (bt["N"], bt["route"]["gs"], bt["kp"], bt["vp"], bt["dy"],
+                                      bt["hl"])
         else:
-            Nu, gs, kp, vp, dy, hl = N, st["gs_u"], self.kp, self.vp, self.dy, self.hl
+            Nu, gs, kp, vp, dy, hl = N, self.route_u["gs"], self.kp, self.vp, self.dy, self.hl
         timed("wgrad", lambda: L.call("uttt_grouped_wgrad_pair", L.ptr(dy), L.ptr(kp), L.ptr(hl),
                                       L.ptr(vp), L.ptr(gs), 1, E, I, D, Nu, L.ptr(self.dW02),
                                       L.ptr(self.dW1), s))
@@ -636,7 +677,6 @@ def bench_moe(args, key):
         dtype="bf16",
         config={"workload": cfg["label"], "seq_len": SEQ, "chunk": CHUNK, "layers": layers,
                 "experts": cfg["E"], "topk": TOPK, "d": cfg["D"], "expert_hidden": cfg["I"],
-                "routing": "Zipf(1.1) prior" if cfg["zipf"] else "N(0,1) logits + N(0,0.5) bias",
                 "step": "one sweep: apply on 16 chunks x L layers, update on 15 chunks x L writers"
                         + (" (+ update backward)" if cfg["train"] else "") + " + write",
                 "update_schedule": ("batched: the L writers of a chunk in one grouped UPDATE "
@@ -644,7 +684,9 @@ def bench_moe(args, key):
                                     if batched else "per-layer: one UPDATE call per writer"),
                 "write": "norm-preserving write of the pool after every update "
                          "(fp32 masters, bf16 fast weights)",
-                "excluded": "router logits/top-k (inputs precomputed)"},
+                "routing": ("fused router per apply (x) and per update (k): fp32 logits of one "
+                            "shared router, " + ("Zipf(1.1)" if cfg["zipf"] else "N(0,0.5)")
+                            + " expert prior as selection bias, topk_renorm gates")},
         roofline=(dict(bound="hbm", kernel=dom, achieved=round(by[dom] / t_dom / 1e9, 1),
                        peak=HBM_PEAK_GBS, unit="GB/s",
                        frac=round(by[dom] / t_dom / 1e9 / HBM_PEAK_GBS, 4), traffic=None,

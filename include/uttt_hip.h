@@ -49,8 +49,9 @@ const char* uttt_last_error(void);
 /* Router                                                                   */
 /* ------------------------------------------------------------------------ */
 
-/* Scratch bytes for uttt_router_select / uttt_route_tokens at (B, T, E). */
-size_t uttt_router_workspace_bytes(int B, int T, int E);
+/* Scratch bytes for uttt_router_select (D = 0) or uttt_route_tokens (D =
+ * the feature size) at (B, T, E). */
+size_t uttt_router_workspace_bytes(int B, int T, int E, int D);
 
 /* Replaces create_router_mask_sizes_probs (M/moe_routing.py:7-75), M =
  * uttt_llm/flame/custom_models/uttt_moe.  logits fp32 addressed
@@ -72,8 +73,9 @@ int uttt_router_select(const float* logits, int64_t l_sb, int64_t l_se, int64_t 
 /* Replaces FastWeightMLPSubNN._route_tokens (M/modeling_recurrent_lact.py:147-169):
  * logits[b,e,t] = sum_d router_w[b,e,d] x[b,t,d] in fp32 (x [B,T,D]
  * contiguous of x_dtype, router_w fp32 [E,D] with batch stride w_sb, 0 =
- * shared), then the selection of uttt_router_select, in one launch plus a
- * one-workgroup finalize.  logits_out: optional fp32 [B,E,T]. */
+ * shared), then the selection of uttt_router_select (D is cut into slices
+ * summed in a fixed order when the token tiles alone would not fill the
+ * chip).  logits_out: optional fp32 [B,E,T]. */
 int uttt_route_tokens(const void* x, int x_dtype, const float* router_w, int64_t w_sb, int B,
                       int T, int D, int E, const float* bias, int64_t bias_sb, int topk,
                       int router_type, int combine_mode, float alpha, float router_scale,

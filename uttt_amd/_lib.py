@@ -97,7 +97,7 @@ SIGNATURES = {
         [c_p, c_p, c_int, c_p, c_p, c_p, c_int, c_p, c_p, c_int, c_int, c_int, c_p, c_p, c_p, c_p,
          c_p, c_p, c_p, c_p, c_sz, c_p],
     ),
-    "uttt_router_workspace_bytes": (c_sz, [c_int, c_int, c_int]),
+    "uttt_router_workspace_bytes": (c_sz, [c_int, c_int, c_int, c_int]),
     "uttt_router_select": (
         c_int,
         [c_p, c_i64, c_i64, c_i64, c_p, c_i64, c_int, c_int, c_int, c_int, c_int, c_int,

@@ -20,20 +20,20 @@
 //
 // Kernels:
 //   router_select_kernel : one thread per token, logits given ([B,E,T] strided);
-//   router_fused_kernel  : 32 tokens per workgroup, logits = R x^T accumulated
-//                          in fp32 from LDS tiles of x and R (D in steps of
-//                          64), then the same per-token selection;
-//   router_finalize_kernel: one workgroup sums the per-block expert partials
-//                          in block order (deterministic: no atomics) into
-//                          group_sizes and lb_loss.
+//   router_mfma_kernel   : logits = R x^T for 32 tokens x all experts per
+//                          workgroup on the fp32 matrix cores (the four waves
+//                          take a quarter of D each), then the selection of
+//                          those tokens;
+//   router_reduce_kernel : one workgroup per (batch, expert) adds the select
+//                          blocks' partial counts and balance sums with a
+//                          fixed tree (deterministic: no atomics);
+//   router_lb_kernel     : lb_loss from those sums.
 #include "common.h"
 
 namespace uttt {
 namespace {
 
 constexpr int kRT = 256;       // threads per workgroup
-constexpr int kFTok = 32;      // fused kernel: tokens per workgroup
-constexpr int kFD = 64;        // fused kernel: D step
 constexpr int kMaxE = 128;
 
 struct SelectArgs {
@@ -48,17 +48,6 @@ struct SelectArgs {
   int32_t* part_cnt;  // [B, nblk, E]
   int nblk;
 };
-
-__device__ __forceinline__ float wave_sum_f(float v) {
-#pragma unroll
-  for (int d = kWave / 2; d > 0; d >>= 1) v += __shfl_xor(v, d, kWave);
-  return v;
-}
-__device__ __forceinline__ int wave_sum_i(int v) {
-#pragma unroll
-  for (int d = kWave / 2; d > 0; d >>= 1) v += __shfl_xor(v, d, kWave);
-  return v;
-}
 
 template <int EB>
 using MaskBits = uint32_t[(EB + 31) / 32];
@@ -156,156 +145,232 @@ __device__ __forceinline__ void select_token(float (&v)[EB], const SelectArgs& a
   }
 }
 
-// Per-expert sums over the tokens of the first `nwaves` waves into
-// part[b][blk][e] (wave sums in LDS, then added in wave order).
-template <int EB>
+// Per-expert sums over the block's NTOK tokens into part[b][blk][e]: the
+// token holders write their rows (balance, mask bit) to LDS, then thread e
+// adds the column in token order (deterministic).  `row` is this thread's
+// token row, or -1 for threads that hold none.
+template <int EB, int NTOK>
 __device__ __forceinline__ void block_partials(const float (&bal)[EB], const MaskBits<EB>& m,
-                                               const SelectArgs& a, int b, int blk, int nwaves,
-                                               float* s_bal, int* s_cnt) {
-  const int w = threadIdx.x / kWave, lane = lane_id();
-  if (w < nwaves) {
+                                               int row, const SelectArgs& a, int b, int blk,
+                                               float (*sb)[EB + 1], uint8_t (*sc)[EB + 1]) {
+  if (row >= 0) {
 #pragma unroll
     for (int e = 0; e < EB; ++e) {
-      if (e >= a.E) break;
-      const float sb = wave_sum_f(bal[e]);
-      const int sc = wave_sum_i(bit<EB>(m, e) ? 1 : 0);
-      if (lane == 0) {
-        s_bal[w * kMaxE + e] = sb;
-        s_cnt[w * kMaxE + e] = sc;
-      }
+      sb[row][e] = bal[e];
+      sc[row][e] = bit<EB>(m, e) ? 1 : 0;
     }
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < a.E; e += kRT) {
-    float sb = 0.0f;
-    int sc = 0;
-    for (int i = 0; i < nwaves; ++i) {
-      sb += s_bal[i * kMaxE + e];
-      sc += s_cnt[i * kMaxE + e];
+  for (int e = threadIdx.x; e < a.E; e += blockDim.x) {
+    float s = 0.0f;
+    int c = 0;
+    for (int i = 0; i < NTOK; ++i) {
+      s += sb[i][e];
+      c += sc[i][e];
     }
     const int64_t o = ((int64_t)b * a.nblk + blk) * a.E + e;
-    a.part_bal[o] = sb;
-    a.part_cnt[o] = sc;
+    a.part_bal[o] = s;
+    a.part_cnt[o] = c;
   }
 }
 
+// Selection over given logits (logits[b*l_sb + e*l_se + t*l_st]), one thread
+// per token, sel_tpb(EB) tokens per block (the LDS transpose of the partial
+// sums stays at 33 KB).
+constexpr int sel_tpb(int EB) { return EB <= 32 ? 256 : EB <= 64 ? 128 : 64; }
+
 template <int EB>
-__global__ __launch_bounds__(kRT) void router_select_kernel(const float* __restrict__ logits,
-                                                            int64_t l_sb, int64_t l_se,
-                                                            int64_t l_st, SelectArgs a) {
-  __shared__ float s_bal[(kRT / kWave) * kMaxE];
-  __shared__ int s_cnt[(kRT / kWave) * kMaxE];
+__global__ __launch_bounds__(sel_tpb(EB)) void router_select_kernel(const float* __restrict__ logits,
+                                                                    int64_t l_sb, int64_t l_se,
+                                                                    int64_t l_st, SelectArgs a) {
+  constexpr int TPB = sel_tpb(EB);
+  __shared__ float sb[TPB][EB + 1];
+  __shared__ uint8_t sc[TPB][EB + 1];
   const int blk = blockIdx.x, b = blockIdx.y;
-  const int t = blk * kRT + threadIdx.x;
+  const int t = blk * TPB + threadIdx.x;
   const bool live = t < a.T;
-  const int tt = live ? t : a.T - 1;
+  const float* p = logits + (int64_t)b * l_sb + (int64_t)(live ? t : a.T - 1) * l_st;
   float l[EB];
 #pragma unroll
-  for (int e = 0; e < EB; ++e)
-    l[e] = e < a.E ? logits[(int64_t)b * l_sb + (int64_t)e * l_se + (int64_t)tt * l_st] : 0.0f;
+  for (int e = 0; e < EB; ++e) l[e] = e < a.E ? p[(int64_t)e * l_se] : 0.0f;
   float bal[EB];
   MaskBits<EB> m;
   select_token<EB>(l, a, b, t, live, bal, m);
-  block_partials<EB>(bal, m, a, b, blk, kRT / kWave, s_bal, s_cnt);
+  block_partials<EB, TPB>(bal, m, threadIdx.x, a, b, blk, sb, sc);
 }
 
-template <class XT, int EB>
-__global__ __launch_bounds__(kRT) void router_fused_kernel(
-    const typename XT::S* __restrict__ x, const float* __restrict__ rw, int64_t w_sb, int D,
-    float* __restrict__ logits_out, SelectArgs a) {
-  using S = typename XT::S;
-  constexpr int kGroups = kRT / kFTok;          // 8 expert groups
-  constexpr int kPer = (EB + kGroups - 1) / kGroups;
-  __shared__ float xs[kFTok][kFD + 1];
-  __shared__ float ws[EB][kFD + 1];
-  __shared__ float lg[kFTok][EB + 1];
-  __shared__ float s_bal[(kRT / kWave) * kMaxE];
-  __shared__ int s_cnt[(kRT / kWave) * kMaxE];
-  const int blk = blockIdx.x, b = blockIdx.y;
-  const int t0 = blk * kFTok;
-  const int tok = threadIdx.x % kFTok, grp = threadIdx.x / kFTok;
-  const int E = a.E;
-  const float* R = rw + (int64_t)b * w_sb;
-  float acc[kPer];
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// 8 consecutive features of one row as fp32 (zero past D or for a dead row).
+template <class XT>
+__device__ __forceinline__ void load8(const typename XT::S* p, int d, int D, bool ok, float (&o)[8]) {
+  if (ok && d + 8 <= D && ((reinterpret_cast<uintptr_t>(p + d) & (sizeof(typename XT::S) * 8 - 1)) == 0)) {
+    if constexpr (sizeof(typename XT::S) == 4) {
+      const float4 u = *reinterpret_cast<const float4*>(p + d);
+      const float4 v = *reinterpret_cast<const float4*>(p + d + 4);
+      o[0] = u.x; o[1] = u.y; o[2] = u.z; o[3] = u.w;
+      o[4] = v.x; o[5] = v.y; o[6] = v.z; o[7] = v.w;
+    } else {
+      const uint4 u = *reinterpret_cast<const uint4*>(p + d);
+      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
-  for (int j = 0; j < kPer; ++j) acc[j] = 0.0f;
-  for (int d0 = 0; d0 < D; d0 += kFD) {
-    // stage x[t0 .. t0+32)[d0 .. d0+64) and R[0 .. E)[d0 .. d0+64) as fp32
-    for (int i = threadIdx.x; i < kFTok * kFD; i += kRT) {
-      const int r = i / kFD, c = i % kFD;
-      const int t = t0 + r, d = d0 + c;
-      xs[r][c] = (t < a.T && d < D) ? XT::load(x[((int64_t)b * a.T + t) * D + d]) : 0.0f;
-    }
-    for (int i = threadIdx.x; i < EB * kFD; i += kRT) {
-      const int r = i / kFD, c = i % kFD;
-      const int d = d0 + c;
-      ws[r][c] = (r < E && d < D) ? R[(int64_t)r * D + d] : 0.0f;
-    }
-    __syncthreads();
-#pragma unroll 4
-    for (int c = 0; c < kFD; ++c) {
-      const float xv = xs[tok][c];
-#pragma unroll
-      for (int j = 0; j < kPer; ++j) {
-        const int e = grp + kGroups * j;
-        if (e < EB) acc[j] = __builtin_fmaf(ws[e][c], xv, acc[j]);
+      for (int i = 0; i < 4; ++i) {
+        o[2 * i] = XT::load(static_cast<typename XT::S>(w[i] & 0xffffu));
+        o[2 * i + 1] = XT::load(static_cast<typename XT::S>(w[i] >> 16));
       }
     }
-    __syncthreads();
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = (ok && d + i < D) ? XT::load(p[d + i]) : 0.0f;
+  }
+}
+
+// Fused router: logits of 32 tokens x NET*32 experts on the fp32 matrix cores
+// (v_mfma_f32_32x32x2_f32: exact fp32 products, fp32 accumulation), then the
+// selection of those 32 tokens in the same workgroup.
+//
+// Wave w of NW covers the feature range [w*D/NW, (w+1)*D/NW) in chunks of 16:
+// lane (r = lane % 32, h = lane / 32) feeds token t0 + r and expert 32*j + r
+// with features d0 + 8h + s for s < 8, one MFMA per s (the k index of the
+// MFMA is h, so each chunk's 16 features enter exactly once).  The next
+// chunk's operands are loaded before the current chunk's MFMAs issue.
+// Accumulator element v of lane l is (token 8*(v/4) + 4*(l/32) + v%4,
+// expert l%32).  The NW partial sums are added in wave order in LDS.
+template <class XT, int NET, int NW>
+__global__ __launch_bounds__(NW * kWave) void router_mfma_kernel(
+    const typename XT::S* __restrict__ x, const float* __restrict__ rw, int64_t w_sb, int D,
+    float* __restrict__ logits_out, SelectArgs a) {
+  constexpr int EB = NET * 32;
+  __shared__ float red[NW][NET][32][33];
+  __shared__ float sb[32][EB + 1];
+  __shared__ uint8_t sc[32][EB + 1];
+  const int blk = blockIdx.x, b = blockIdx.y;
+  const int t0 = blk * 32;
+  const int w = threadIdx.x / kWave, lane = lane_id();
+  const int r = lane % 32, h = lane / 32;
+  const int E = a.E, T = a.T;
+  const bool tv = t0 + r < T;
+  const typename XT::S* xrow = x + ((int64_t)b * T + (tv ? t0 + r : 0)) * D;
+  const float* R = rw + (int64_t)b * w_sb;
+  const int nch = (D + 15) / 16;
+  const int per = (nch + NW - 1) / NW;
+  const int c_lo = w * per, c_hi = min(nch, c_lo + per);
+  f32x16_t acc[NET];
+#pragma unroll
+  for (int j = 0; j < NET; ++j) acc[j] = f32x16_t{};
+  float xa[8], wa[NET][8];
+  auto fetch = [&](int c, float (&xo)[8], float (&wo)[NET][8]) __attribute__((always_inline)) {
+    const int d = c * 16 + 8 * h;
+    const bool in = c < c_hi;
+    load8<XT>(xrow, d, D, tv && in, xo);
+#pragma unroll
+    for (int j = 0; j < NET; ++j) {
+      const int e = 32 * j + r;
+      load8<F32T>(R + (int64_t)(e < E ? e : 0) * D, d, D, in && e < E, wo[j]);
+    }
+  };
+  if (c_lo < c_hi) fetch(c_lo, xa, wa);
+  for (int c = c_lo; c < c_hi; ++c) {
+    float xn[8], wn[NET][8];
+    fetch(c + 1, xn, wn);   // zeros past this wave's range
+#pragma unroll
+    for (int j = 0; j < NET; ++j)
+#pragma unroll
+      for (int s8 = 0; s8 < 8; ++s8)
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[s8], wa[j][s8], acc[j], 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      xa[i] = xn[i];
+#pragma unroll
+      for (int j = 0; j < NET; ++j) wa[j][i] = wn[j][i];
+    }
   }
 #pragma unroll
-  for (int j = 0; j < kPer; ++j) {
-    const int e = grp + kGroups * j;
-    if (e < EB) lg[tok][e] = acc[j];
+  for (int j = 0; j < NET; ++j)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) red[w][j][8 * (v / 4) + 4 * h + v % 4][r] = acc[j][v];
+  __syncthreads();
+  for (int i = threadIdx.x; i < NET * 32 * 32; i += NW * kWave) {
+    const int j = i / 1024, tok = (i / 32) % 32, e = i % 32;
+    float v = red[0][j][tok][e];
+#pragma unroll
+    for (int q = 1; q < NW; ++q) v += red[q][j][tok][e];
+    red[0][j][tok][e] = v;
   }
   __syncthreads();
   if (logits_out != nullptr) {
-    for (int i = threadIdx.x; i < E * kFTok; i += kRT) {
-      const int e = i / kFTok, r = i % kFTok;
-      if (t0 + r < a.T) logits_out[((int64_t)b * E + e) * a.T + t0 + r] = lg[r][e];
+    for (int i = threadIdx.x; i < E * 32; i += NW * kWave) {
+      const int e = i / 32, tok = i % 32;
+      if (t0 + tok < T) logits_out[((int64_t)b * E + e) * T + t0 + tok] = red[0][e / 32][tok][e % 32];
     }
   }
   float bal[EB];
   MaskBits<EB> m;
-  if (threadIdx.x < kWave) {   // wave 0 selects; lanes >= kFTok are padding
-    const int t = t0 + threadIdx.x;
-    const bool live = threadIdx.x < kFTok && t < a.T;
+  if (w == 0) {   // wave 0 selects: lane r < 32 owns token t0 + r, lanes >= 32 are padding
+    const bool live = lane < 32 && t0 + lane < T;
     float l[EB];
 #pragma unroll
-    for (int e = 0; e < EB; ++e) l[e] = (threadIdx.x < kFTok && e < E) ? lg[threadIdx.x][e] : 0.0f;
-    select_token<EB>(l, a, b, t, live, bal, m);
+    for (int e = 0; e < EB; ++e) l[e] = (lane < 32 && e < E) ? red[0][e / 32][lane % 32][e % 32] : 0.0f;
+    select_token<EB>(l, a, b, t0 + lane, live, bal, m);
   }
-  block_partials<EB>(bal, m, a, b, blk, 1, s_bal, s_cnt);
+  block_partials<EB, 32>(bal, m, (w == 0 && lane < 32) ? lane : -1, a, b, blk, sb, sc);
 }
 
-// One workgroup: group_sizes[b][e] and balance sums over the blocks, then
-// lb_loss = E * sum_e (sum_b bal_sum[b][e] / (B T)) * freq_e.
-__global__ __launch_bounds__(kRT) void router_finalize_kernel(const float* __restrict__ part_bal,
-                                                              const int32_t* __restrict__ part_cnt,
-                                                              int B, int E, int T, int nblk,
-                                                              int32_t* __restrict__ group_sizes,
-                                                              float* __restrict__ lb_loss) {
+// group_sizes[b][e] and the balance sum of (b, e) over the select blocks:
+// one workgroup per (b, e); thread i adds blocks i, i + 256, ... in order, then
+// a fixed tree over the 256 thread sums (deterministic).
+__global__ __launch_bounds__(kRT) void router_reduce_kernel(const float* __restrict__ part_bal,
+                                                            const int32_t* __restrict__ part_cnt,
+                                                            int E, int nblk,
+                                                            int32_t* __restrict__ group_sizes,
+                                                            float* __restrict__ bal_sum,
+                                                            int32_t* __restrict__ cnt_sum) {
+  __shared__ float sb[kRT];
+  __shared__ int sc[kRT];
+  const int be = blockIdx.x, b = be / E, e = be % E;
+  float fb = 0.0f;
+  int ic = 0;
+  for (int k = threadIdx.x; k < nblk; k += kRT) {
+    const int64_t o = ((int64_t)b * nblk + k) * E + e;
+    fb += part_bal[o];
+    ic += part_cnt[o];
+  }
+  sb[threadIdx.x] = fb;
+  sc[threadIdx.x] = ic;
+  __syncthreads();
+  for (int w = kRT / 2; w > 0; w >>= 1) {
+    if (threadIdx.x < w) {
+      sb[threadIdx.x] += sb[threadIdx.x + w];
+      sc[threadIdx.x] += sc[threadIdx.x + w];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    if (group_sizes != nullptr) group_sizes[be] = sc[0];
+    bal_sum[be] = sb[0];
+    cnt_sum[be] = sc[0];
+  }
+}
+
+// lb_loss = E * sum_e (sum_b bal_sum[b][e] / (B T)) * freq_e,
+// freq_e = mean_b(count) / sum_e mean_b(count).  One workgroup.
+__global__ __launch_bounds__(kRT) void router_lb_kernel(const float* __restrict__ bal_sum,
+                                                        const int32_t* __restrict__ cnt_sum,
+                                                        int B, int E, int T,
+                                                        float* __restrict__ lb_loss) {
   __shared__ float pm[kMaxE];
   __shared__ float gm[kMaxE];
   for (int e = threadIdx.x; e < E; e += kRT) {
-    float sb = 0.0f, sg = 0.0f;
+    float s = 0.0f, g = 0.0f;
     for (int b = 0; b < B; ++b) {
-      float bb = 0.0f;
-      int cc = 0;
-      for (int k = 0; k < nblk; ++k) {
-        const int64_t o = ((int64_t)b * nblk + k) * E + e;
-        bb += part_bal[o];
-        cc += part_cnt[o];
-      }
-      if (group_sizes != nullptr) group_sizes[(int64_t)b * E + e] = cc;
-      sb += bb;
-      sg += (float)cc;
+      s += bal_sum[(int64_t)b * E + e];
+      g += (float)cnt_sum[(int64_t)b * E + e];
     }
-    pm[e] = sb / ((float)B * (float)T);
-    gm[e] = sg / (float)B;
+    pm[e] = s / ((float)B * (float)T);
+    gm[e] = g / (float)B;
   }
   __syncthreads();
-  if (threadIdx.x == 0 && lb_loss != nullptr) {
+  if (threadIdx.x == 0) {
     float tot = 0.0f;
     for (int e = 0; e < E; ++e) tot += gm[e];
     float lb = 0.0f;
@@ -334,13 +399,57 @@ int check_select_args(int B, int E, int T, int topk, int router_type, int combin
                "%s: router_type %d (0 softmax, 1 norm_softmax, 2 norm_relu)", what, router_type);
   UTTT_REQUIRE(combine_mode == 0 || combine_mode == 1,
                "%s: combine_mode %d (0 selected_prob, 1 topk_renorm)", what, combine_mode);
-  UTTT_REQUIRE((int64_t)B * E <= 65535 * 64, "%s: B*E too large", what);
+  UTTT_REQUIRE(B <= 65535 && (int64_t)B * E <= 0x7fffffff, "%s: B=%d too large", what, B);
   return UTTT_OK;
 }
 
-size_t ws_bytes(int B, int T, int E) {
-  const int64_t nblk = (T + kFTok - 1) / kFTok;   // the finer of the two tilings
-  return (size_t)(2 * sizeof(float) * B * nblk * E);
+// Workspace layout: [part_bal: B*nblk*E fp32][part_cnt: B*nblk*E int32]
+// [bal_sum: B*E fp32][cnt_sum: B*E int32]; nblk = ceil(T / tokens per block).
+struct Ws {
+  float* part_bal;
+  int32_t* part_cnt;
+  float* bal_sum;
+  int32_t* cnt_sum;
+  int nblk;
+  size_t bytes;
+};
+Ws ws_layout(void* base, int B, int T, int E, int blk_tokens) {
+  const int nblk = (T + blk_tokens - 1) / blk_tokens;
+  auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
+  char* p = static_cast<char*>(base);
+  Ws w{};
+  size_t off = 0;
+  w.part_bal = reinterpret_cast<float*>(p + off);
+  off += up(sizeof(float) * (size_t)B * nblk * E);
+  w.part_cnt = reinterpret_cast<int32_t*>(p + off);
+  off += up(sizeof(int32_t) * (size_t)B * nblk * E);
+  w.bal_sum = reinterpret_cast<float*>(p + off);
+  off += up(sizeof(float) * (size_t)B * E);
+  w.cnt_sum = reinterpret_cast<int32_t*>(p + off);
+  off += up(sizeof(int32_t) * (size_t)B * E);
+  w.nblk = nblk;
+  w.bytes = off;
+  return w;
+}
+
+SelectArgs make_args(const Ws& w, const float* bias, int64_t bias_sb, int B, int E, int T,
+                     int topk, int router_type, int combine_mode, float alpha, float router_scale,
+                     float norm_eps, void* mask, float* combine, float* balance) {
+  return SelectArgs{bias, bias_sb, B, E, T, topk, router_type, combine_mode, alpha,
+                    router_scale > 0.0f ? router_scale : sqrtf((float)E), norm_eps,
+                    static_cast<uint8_t*>(mask), combine, balance, w.part_bal, w.part_cnt,
+                    w.nblk};
+}
+
+// group sizes, balance sums and lb_loss from the block partials
+int finish(const Ws& w, int B, int E, int T, int32_t* group_sizes, float* lb_loss, hipStream_t st,
+           const char* what) {
+  hipLaunchKernelGGL(router_reduce_kernel, dim3(B * E), dim3(kRT), 0, st, w.part_bal, w.part_cnt,
+                     E, w.nblk, group_sizes, w.bal_sum, w.cnt_sum);
+  if (lb_loss != nullptr)
+    hipLaunchKernelGGL(router_lb_kernel, dim3(1), dim3(kRT), 0, st, w.bal_sum, w.cnt_sum, B, E, T,
+                       lb_loss);
+  return check_launch(what);
 }
 
 }  // namespace
@@ -348,17 +457,9 @@ size_t ws_bytes(int B, int T, int E) {
 
 using namespace uttt;
 
-extern "C" size_t uttt_router_workspace_bytes(int B, int T, int E) {
+extern "C" size_t uttt_router_workspace_bytes(int B, int T, int E, int D) {
   if (B <= 0 || T <= 0 || E <= 0) return 0;
-  return ws_bytes(B, T, E);
-}
-
-static int finish_router(float* part_bal, int32_t* part_cnt, int B, int E, int T, int nblk,
-                         int32_t* group_sizes, float* lb_loss, hipStream_t st, const char* what) {
-  if (int rc = check_launch(what)) return rc;
-  hipLaunchKernelGGL(router_finalize_kernel, dim3(1), dim3(kRT), 0, st, part_bal, part_cnt, B, E,
-                     T, nblk, group_sizes, lb_loss);
-  return check_launch(what);
+  return ws_layout(nullptr, B, T, E, D > 0 ? 32 : sel_tpb(e_bucket(E))).bytes;
 }
 
 extern "C" int uttt_router_select(const float* logits, int64_t l_sb, int64_t l_se, int64_t l_st,
@@ -372,20 +473,16 @@ extern "C" int uttt_router_select(const float* logits, int64_t l_sb, int64_t l_s
     return rc;
   if (B == 0 || T == 0) return UTTT_OK;
   UTTT_REQUIRE(logits && mask && combine && balance, "router_select: null pointer");
-  UTTT_REQUIRE(workspace != nullptr && workspace_bytes >= ws_bytes(B, T, E),
-               "router_select: workspace %zu < %zu bytes", workspace_bytes, ws_bytes(B, T, E));
-  const int nblk = (T + kRT - 1) / kRT;
-  SelectArgs a{bias, bias_sb, B, E, T, topk, router_type, combine_mode, alpha,
-               router_scale > 0.0f ? router_scale : sqrtf((float)E), norm_eps,
-               static_cast<uint8_t*>(mask), combine, balance,
-               static_cast<float*>(workspace),
-               reinterpret_cast<int32_t*>(static_cast<float*>(workspace) + (int64_t)B * nblk * E),
-               nblk};
+  const Ws w = ws_layout(workspace, B, T, E, sel_tpb(e_bucket(E)));
+  UTTT_REQUIRE(workspace != nullptr && workspace_bytes >= w.bytes,
+               "router_select: workspace %zu < %zu bytes", workspace_bytes, w.bytes);
+  const SelectArgs a = make_args(w, bias, bias_sb, B, E, T, topk, router_type, combine_mode,
+                                 alpha, router_scale, norm_eps, mask, combine, balance);
   hipStream_t st = as_stream(stream);
-  UTTT_EB_SWITCH(E, hipLaunchKernelGGL((router_select_kernel<EB>), dim3(nblk, B), dim3(kRT), 0,
-                                       st, logits, l_sb, l_se, l_st, a));
-  return finish_router(a.part_bal, a.part_cnt, B, E, T, nblk, group_sizes, lb_loss, st,
-                       "router_select");
+  UTTT_EB_SWITCH(E, hipLaunchKernelGGL((router_select_kernel<EB>), dim3(w.nblk, B),
+                                       dim3(sel_tpb(EB)), 0, st, logits, l_sb, l_se, l_st, a));
+  if (int rc = check_launch("router_select")) return rc;
+  return finish(w, B, E, T, group_sizes, lb_loss, st, "router_select");
 }
 
 extern "C" int uttt_route_tokens(const void* x, int x_dtype, const float* router_w, int64_t w_sb,
@@ -400,22 +497,26 @@ extern "C" int uttt_route_tokens(const void* x, int x_dtype, const float* router
   UTTT_REQUIRE(D >= 1, "route_tokens: D=%d", D);
   if (B == 0 || T == 0) return UTTT_OK;
   UTTT_REQUIRE(x && router_w && mask && combine && balance, "route_tokens: null pointer");
-  UTTT_REQUIRE(workspace != nullptr && workspace_bytes >= ws_bytes(B, T, E),
-               "route_tokens: workspace %zu < %zu bytes", workspace_bytes, ws_bytes(B, T, E));
-  const int nblk = (T + kFTok - 1) / kFTok;
-  SelectArgs a{bias, bias_sb, B, E, T, topk, router_type, combine_mode, alpha,
-               router_scale > 0.0f ? router_scale : sqrtf((float)E), norm_eps,
-               static_cast<uint8_t*>(mask), combine, balance,
-               static_cast<float*>(workspace),
-               reinterpret_cast<int32_t*>(static_cast<float*>(workspace) + (int64_t)B * nblk * E),
-               nblk};
+  const Ws w = ws_layout(workspace, B, T, E, 32);
+  UTTT_REQUIRE(workspace != nullptr && workspace_bytes >= w.bytes,
+               "route_tokens: workspace %zu < %zu bytes", workspace_bytes, w.bytes);
+  const SelectArgs a = make_args(w, bias, bias_sb, B, E, T, topk, router_type, combine_mode,
+                                 alpha, router_scale, norm_eps, mask, combine, balance);
   hipStream_t st = as_stream(stream);
+  const int net = (E + 31) / 32;
+#define UTTT_ROUTE_LAUNCH(NET, NW)                                                           \
+  hipLaunchKernelGGL((router_mfma_kernel<XT, NET, NW>), dim3(w.nblk, B), dim3(NW * kWave), 0,  \
+                     st, static_cast<const S*>(x), router_w, w_sb, D, logits_out, a)
   UTTT_DTYPE_SWITCH_LR(x_dtype, XT, {
     using S = typename XT::S;
-    UTTT_EB_SWITCH(E, hipLaunchKernelGGL((router_fused_kernel<XT, EB>), dim3(nblk, B), dim3(kRT),
-                                         0, st, static_cast<const S*>(x), router_w, w_sb, D,
-                                         logits_out, a));
+    switch (net) {
+      case 1: UTTT_ROUTE_LAUNCH(1, 8); break;
+      case 2: UTTT_ROUTE_LAUNCH(2, 8); break;
+      case 3: UTTT_ROUTE_LAUNCH(3, 4); break;
+      default: UTTT_ROUTE_LAUNCH(4, 4); break;
+    }
   });
-  return finish_router(a.part_bal, a.part_cnt, B, E, T, nblk, group_sizes, lb_loss, st,
-                       "route_tokens");
+#undef UTTT_ROUTE_LAUNCH
+  if (int rc = check_launch("route_tokens")) return rc;
+  return finish(w, B, E, T, group_sizes, lb_loss, st, "route_tokens");
 }

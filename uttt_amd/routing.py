@@ -4,7 +4,8 @@
       uttt_llm/flame/custom_models/uttt_moe/moe_routing.py:7-75
   route_tokens                    FastWeightMLPSubNN._route_tokens,
       uttt_llm/flame/custom_models/uttt_moe/modeling_recurrent_lact.py:147-169:
-      fp32 logits R x^T and the selection in one fused launch
+      fp32 logits R x^T (D sliced across workgroups when the tokens are few),
+      then the selection and two small deterministic reductions
 
 Outputs are freshly allocated on the inputs' device.  Top-k keeps the lower
 expert index among exactly equal routing scores (torch.topk leaves that
@@ -51,13 +52,13 @@ def _bias_arg(routing_bias, B, E, device):
     return rb, (E if rb.shape[0] > 1 else 0)
 
 
-def _outputs(B, E, T, device):
+def _outputs(B, E, T, D, device):
     mask = torch.empty((B, E, T), dtype=torch.bool, device=device)
     gs = torch.empty((B, E), dtype=torch.int32, device=device)
     comb = torch.empty((B, E, T), dtype=torch.float32, device=device)
     bal = torch.empty((B, E, T), dtype=torch.float32, device=device)
     lb = torch.empty((), dtype=torch.float32, device=device)
-    nbytes = L.lib().uttt_router_workspace_bytes(B, T, E)
+    nbytes = L.lib().uttt_router_workspace_bytes(B, T, E, D)
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
     return mask, gs, comb, bal, lb, ws, nbytes
 
@@ -74,7 +75,7 @@ def create_router_mask_sizes_probs(router_logits, topk, alpha=1.0, use_sigmoid=F
     B, E, T = router_logits.shape
     logits = router_logits if router_logits.dtype == torch.float32 else router_logits.float()
     bias, bias_sb = _bias_arg(routing_bias, B, E, logits.device)
-    mask, gs, comb, bal, lb, ws, nbytes = _outputs(B, E, T, logits.device)
+    mask, gs, comb, bal, lb, ws, nbytes = _outputs(B, E, T, 0, logits.device)
     L.call("uttt_router_select", L.ptr(logits), logits.stride(0), logits.stride(1),
            logits.stride(2), L.ptr(bias), bias_sb, B, E, T, int(topk), ROUTER_TYPES[router_type],
            COMBINE_MODES[combine_mode], float(alpha), float(router_scale), float(norm_eps),
@@ -107,7 +108,7 @@ def route_tokens(x, router_proj_weights, topk, alpha=1.0, use_sigmoid=False,
         w_sb = E * D if R.shape[0] > 1 else 0
     assert R.shape[-1] == D, "router weights must have x's last dimension"
     bias, bias_sb = _bias_arg(routing_bias, B, E, x.device)
-    mask, gs, comb, bal, lb, ws, nbytes = _outputs(B, E, T, x.device)
+    mask, gs, comb, bal, lb, ws, nbytes = _outputs(B, E, T, D, x.device)
     logits = torch.empty((B, E, T), dtype=torch.float32, device=x.device) if return_logits else None
     L.call("uttt_route_tokens", L.ptr(x), L.dtype_code(x.dtype), L.ptr(R), w_sb, B, T, D, E,
            L.ptr(bias), bias_sb, int(topk), ROUTER_TYPES[router_type],
