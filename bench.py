@@ -11,9 +11,15 @@ in HBM before the timed region starts):
             layers sharing the pool, seq 32768 in chunks of 2048.  One step =
             one shifted block-causal sweep: APPLY (row map, permute, grouped
             SwiGLU apply, unpermute) on 16 chunks x 24 layers, UPDATE forward
-            and backward on 15 x 24; value = tokens/s of the sweep.
+            and backward on 15 x 24, the router in front of every APPLY and
+            UPDATE and the norm-preserving WRITE after every UPDATE; value =
+            tokens/s of the sweep.
   moe124m   configs[3]: uTTT-MoE 124M, E=16, d=768, hidden 1536, 12 layers,
-            APPLY + UPDATE forward.
+            APPLY + UPDATE forward + WRITE.
+  dense124m configs[1]: uTTT-Dense 124M, one shared SwiGLU fast weight per
+            head (H=4, d=192, hidden 384), 12 layers, aggregate write.
+  dense_c0  configs[0]'s single-layer shape (H=4, d=96, hidden 192, chunks of
+            512) on the GPU.
   permute   configs[2]: token permute + gate-weighted unpermute by expert,
             T=65536, E=16, top-2, payload bf16 [T, 768]; one step = row map +
             permute + unpermute of one batch; value = algorithmic GB/s.
@@ -745,9 +751,156 @@ def cpu_baseline_moe(sw, cfg, layers, chunks):
                 cpu=_cpu_model())
 
 
+# ------------------------------------------------------------- dense sweep --
+DENSE_CONFIGS = {
+    # uTTT-Dense 124M shape, one shared fast weight, 12 layers
+    "dense124m": dict(L=12, H=4, d=192, r=2, S=32768, chunk=2048,
+                      label="uTTT-Dense 124M shared fast-weight apply+update (configs[1])"),
+    # configs[0]'s single-layer shape, run on the GPU
+    "dense_c0": dict(L=1, H=4, d=96, r=2, S=4096, chunk=512,
+                     label="uTTT-Dense single layer, configs[0] shape, on the GPU"),
+}
+
+
+def bench_dense(args, key):
+    """One uTTT-Dense sweep: every layer reads every chunk with the chunk-start
+    fast weights (grouped APPLY, one head = one batch), and every chunk but
+    the last is written once from the layers' updates (aggregate mean: all
+    layers' tokens in one grouped UPDATE per head, then the per-slice
+    norm-preserving write).  Inputs: per layer q, k, v ~ N(0,1) L2-normalised
+    per head, lr = sigmoid(N(0,1)) * 0.1; weights N(0, 1/sqrt(d))."""
+    import torch
+
+    from uttt_amd import dense as DN
+
+    cfg = DENSE_CONFIGS[key]
+    L_, H, d, r, S, c = cfg["L"], cfg["H"], cfg["d"], cfg["r"], cfg["S"], cfg["chunk"]
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(0)
+    dh = r * d
+    w = [torch.randn(*s, generator=g, device=dev) / d ** 0.5
+         for s in ((1, H, dh, d), (1, H, d, dh), (1, H, dh, d))]
+    nsets = min(L_, 4)
+    sets = []
+    for _ in range(nsets):
+        qkv = [torch.nn.functional.normalize(torch.randn(1, S, H, d, generator=g, device=dev), dim=-1)
+               .reshape(1, S, H * d).to(torch.bfloat16) for _ in range(3)]
+        lr = torch.sigmoid(torch.randn(1, S, 3, generator=g, device=dev)) * 0.1
+        sets.append(qkv + [lr])
+
+    def sweep(bank, chunks):
+        for ci in range(chunks):
+            c0, c1 = ci * c, min(S, (ci + 1) * c)
+            for li in range(L_):
+                bank.read(sets[li % nsets][0][:, c0:c1])
+            if ci < chunks - 1:
+                st = [sets[li % nsets] for li in range(L_)]
+                bank.write([x[1][:, c0:c1] for x in st], [x[2][:, c0:c1] for x in st],
+                           [x[3][:, c0:c1] for x in st])
+
+    chunks = (S + c - 1) // c
+    for _ in range(max(args.warmup, 1)):
+        sweep(DN.SharedFastWeights(*w, r=r), min(chunks, 2))
+    torch.cuda.synchronize()
+    walls = []
+    for _ in range(args.steps):
+        bank = DN.SharedFastWeights(*w, r=r)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        sweep(bank, chunks)
+        torch.cuda.synchronize()
+        walls.append(time.perf_counter() - t0)
+    wall = statistics.mean(walls)
+    # isolated timings (events around back-to-back calls on the stream)
+    bank = DN.SharedFastWeights(*w, r=r)
+
+    def timed(fn, reps=10):
+        fn()
+        e0, e1 = _events(2)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e-3 / reps
+
+    q0 = sets[0][0][:, :c]
+    t_read = timed(lambda: bank.read(q0))
+    st = [sets[li % nsets] for li in range(L_)]
+    t_write = timed(lambda: bank.write([x[1][:, :c] for x in st], [x[2][:, :c] for x in st],
+                                       [x[3][:, :c] for x in st]))
+    nid = c * dh * d * H                                  # one layer-chunk, all heads
+    sweep_flops = L_ * (chunks * 6 + (chunks - 1) * 12) * nid
+    read_tf = 6 * nid / t_read / 1e12
+    write_tf = 12 * L_ * nid / t_write / 1e12
+    res = dict(
+        metric="fast-weight apply+update tokens/s",
+        value=round(S / wall, 1),
+        unit="tokens/s",
+        ms_per_step=round(wall * 1e3, 3),
+        dtype="bf16",
+        config={"workload": cfg["label"], "seq_len": S, "chunk": c, "layers": L_, "fw_heads": H,
+                "head_dim": d, "fw_hidden": dh, "r": r,
+                "schedule": "aggregate (the reference's uttt_dense): all layers read the "
+                            "chunk-start snapshot; one mean-reduced write per chunk",
+                "write": "per-slice norm-preserving, norms from the bf16 fast weights"},
+        roofline=dict(bound="mfma", kernel="aggregate write (UPDATE over all layers + write)",
+                      achieved=round(write_tf, 2), peak=BF16_PEAK_TFLOPS, unit="TFLOP/s",
+                      frac=round(write_tf / BF16_PEAK_TFLOPS, 4), traffic=None,
+                      algorithmic_flops=12 * L_ * nid, avg_launch_us=round(t_write * 1e6, 2)),
+        sweep=dict(algorithmic_flops=sweep_flops, TFLOPs=round(sweep_flops / wall / 1e12, 2),
+                   mfma_frac=round(sweep_flops / wall / 1e12 / BF16_PEAK_TFLOPS, 4)),
+        kernels={"read(one layer-chunk)": dict(us=round(t_read * 1e6, 2), TFLOPs=round(read_tf, 2)),
+                 "write(one chunk, all layers)": dict(us=round(t_write * 1e6, 2),
+                                                     TFLOPs=round(write_tf, 2))},
+    )
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline_dense(cfg, sets, w)
+    return res
+
+
+def cpu_baseline_dense(cfg, sets, w):
+    """The fp32 PyTorch restatement (oracle/dense.py, fp32 accumulation) on this
+    host's cores: configs[0]'s full single-layer sweep when L = 1, else one
+    layer-chunk read and one layer's update at full shape, extrapolated to the
+    sweep (L * (chunks reads + (chunks - 1) updates))."""
+    import torch
+
+    from oracle import dense as OD
+    from oracle import fastweight as FW
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    L_, r, S, c = cfg["L"], cfg["r"], cfg["S"], cfg["chunk"]
+    wc = [x.cpu() for x in w]
+    fast = tuple(x.to(torch.bfloat16) for x in wc)
+    q, k, v, lr = (x.cpu() for x in sets[0])
+    chunks = (S + c - 1) // c
+    with FW.fp32_accumulate():
+        if L_ == 1:
+            t0 = time.perf_counter()
+            OD.sweep([q], [k], [v], [lr], fast, wc, r, c)
+            t = time.perf_counter() - t0
+            sample = f"full single-layer sweep ({chunks} chunks of {c})"
+        else:
+            t0 = time.perf_counter()
+            OD.read(q[:, :c], *fast)
+            t_read = time.perf_counter() - t0
+            t0 = time.perf_counter()
+            OD.compute_update(k[:, :c], v[:, :c], lr[:, :c], fast)
+            t_upd = time.perf_counter() - t0
+            t = L_ * (chunks * t_read + (chunks - 1) * t_upd)
+            sample = (f"one layer-chunk: read {t_read:.3f} s, update {t_upd:.3f} s; sweep "
+                      f"extrapolated x{L_} layers x{chunks} chunks")
+    return dict(value=round(S / t, 2), unit="tokens/s", cores=threads, kind="port",
+                sample=sample + f" (fp32 torch, {threads} threads)", cpu=_cpu_model())
+
+
 WORKLOADS = {"permute": bench_permute,
              "moe124m": lambda a: bench_moe(a, "moe124m"),
-             "moe760m": lambda a: bench_moe(a, "moe760m")}
+             "moe760m": lambda a: bench_moe(a, "moe760m"),
+             "dense124m": lambda a: bench_dense(a, "dense124m"),
+             "dense_c0": lambda a: bench_dense(a, "dense_c0")}
 DEFAULT_WORKLOAD = "moe760m"
 
 
@@ -766,7 +919,7 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one plain 256 MiB device copy (PMC scaling)")
     args = ap.parse_args()
-    moe = args.workload.startswith("moe")
+    moe = args.workload.startswith(("moe", "dense"))
     if args.steps is None:
         args.steps = 2 if moe else 20
     if args.warmup is None:

@@ -1,0 +1,79 @@
+"""GPU parity of the uTTT-Dense path (uttt_amd.dense) against oracle/dense.py
+on the same seeded inputs at the configs[0] head shape (H = 4, d = 96,
+d_h = 192, chunks of 512) and the configs[1] shape (d = 192, d_h = 384).
+
+Bar: bf16 outputs and weights within rtol 2e-2 (tests.helpers.assert_bf16_close)
+of the oracle run with the reference's bf16 storage points; raw updates
+(bf16 stored, widened) the same; the fp32 masters of a multi-chunk sweep
+within rtol 2e-2 as well (each write consumes bf16 updates).
+"""
+import pytest
+import torch
+
+from oracle import dense as OD
+from tests.helpers import assert_bf16_close
+from uttt_amd import dense as DN
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _weights(b, H, d, r, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return tuple(torch.randn(*s, generator=g) / d ** 0.5
+                 for s in ((b, H, r * d, d), (b, H, d, r * d), (b, H, r * d, d)))
+
+
+def _layer(b, S, H, d, seed, per_head_lr=False):
+    g = torch.Generator().manual_seed(seed)
+    q, k, v = (torch.nn.functional.normalize(torch.randn(b, S, H, d, generator=g), dim=-1)
+               .reshape(b, S, H * d).to(torch.bfloat16) for _ in range(3))
+    lr = torch.sigmoid(torch.randn(b, S, 3 * H if per_head_lr else 3, generator=g)) * 0.1
+    return q, k, v, lr
+
+
+@pytest.mark.parametrize("H,d,r,l", [(4, 96, 2, 512), (4, 192, 2, 2048), (2, 64, 3, 300)])
+def test_dense_read_and_update(H, d, r, l):
+    b = 1
+    w = _weights(b, H, d, r)
+    fast = tuple(x.to(torch.bfloat16) for x in w)
+    q, k, v, lr = _layer(b, l, H, d, 1, per_head_lr=(r == 3))
+    out = DN.apply_fast_weights(q.to(DEV), *(x.to(DEV) for x in fast))
+    assert_bf16_close(out.cpu(), OD.read(q, *fast), name="read")
+    dws = DN.compute_update(k.to(DEV), v.to(DEV), lr.to(DEV), tuple(x.to(DEV) for x in fast))
+    refs = OD.compute_update(k, v, lr, fast)
+    for o, rr, n in zip(dws, refs, ("dw0", "dw1", "dw2")):
+        assert o.dtype == torch.float32
+        assert_bf16_close(o.cpu(), rr, name=n)
+
+
+@pytest.mark.parametrize("L,S,chunk,H,d,r,master_renorm", [
+    (1, 4096, 512, 4, 96, 2, False),     # configs[0]: one layer, 8 chunks
+    (3, 1536, 512, 4, 96, 2, True),      # aggregate over layers, master renorm
+])
+def test_dense_sweep(L, S, chunk, H, d, r, master_renorm):
+    b = 1
+    w = _weights(b, H, d, r, seed=5)
+    fast = tuple(x.to(torch.bfloat16) for x in w)
+    layers = [_layer(b, S, H, d, 100 + i) for i in range(L)]
+    qs, ks, vs, lrs = (list(t) for t in zip(*layers))
+    ref_out, ref_fast, ref_master = OD.sweep(qs, ks, vs, lrs, fast, w, r, chunk,
+                                             master_renorm=master_renorm)
+    bank = DN.SharedFastWeights(*(x.to(DEV) for x in fast), r=r,
+                                masters=tuple(x.to(DEV) for x in w), master_renorm=master_renorm)
+    outs = [[] for _ in range(L)]
+    for c0 in range(0, S, chunk):
+        c1 = min(S, c0 + chunk)
+        for li in range(L):
+            outs[li].append(bank.read(qs[li][:, c0:c1].to(DEV)))
+        if c1 < S:
+            bank.write([k[:, c0:c1].to(DEV) for k in ks], [v[:, c0:c1].to(DEV) for v in vs],
+                       [x[:, c0:c1].to(DEV) for x in lrs])
+    torch.cuda.synchronize()
+    for li in range(L):
+        assert_bf16_close(torch.cat(outs[li], 1).cpu(), ref_out[li], name=f"out{li}")
+    f, m = bank.weights()
+    for a, rr, n in zip(f, ref_fast, ("w0", "w1", "w2")):
+        assert_bf16_close(a.cpu(), rr, name="fast " + n)
+    for a, rr, n in zip(m, ref_master, ("w0", "w1", "w2")):
+        assert_bf16_close(a.cpu(), rr, name="master " + n)

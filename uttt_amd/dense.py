@@ -1,0 +1,157 @@
+"""uTTT-Dense fast-weight path on the gfx950 grouped kernels.
+
+uTTT-Dense keeps one SwiGLU fast weight per head (w0, w2 [b, H, d_h, d],
+w1 [b, H, d, d_h]) shared by all layers.  Each head is one batch of the
+grouped kernels with a single expert (group_sizes = [[N]]), so the read is
+the grouped APPLY and a layer's update the grouped UPDATE.  Reference:
+uttt_llm/flame/custom_models/uttt_dense/modeling_recurrent_lact.py (D:):
+
+  apply_fast_weights   _apply_fast_weights  D:241-268 (the output; the
+                       reference's intermediate views are not returned)
+  compute_update       compute_update       D:333-449 from the preprocessed
+                       k, v, lr (fp32 raw update, stored bf16 as under autocast)
+  SharedFastWeights    the shared bank of D:1801-1863: read() per layer and
+                       chunk, write() = _aggregate_memory_update D:1302-1386 +
+                       _apply_shared_update D:1109-1240
+
+SharedFastWeights keeps its state in the kernels' layout -- fast W0_W2
+[b*H, 1, 2 d_h, d] and W1 [b*H, 1, d, d_h] in bf16 with fp32 masters -- so a
+chunk needs no concatenation or copy of the weights.  Its write batches the L
+layers: their tokens are concatenated per head into one UPDATE call, whose
+fp32 accumulation gives sum_l dW_l (the reference adds the layers' bf16
+updates in fp32); the mean reduce is folded into the step size.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib as L
+from .lact_moe_triton import _grouped as G
+
+
+def _heads(x, H):
+    """[b, l, H*d] -> contiguous [b*H, l, d] bf16."""
+    b, l, hd = x.shape
+    return (x.reshape(b, l, H, hd // H).permute(0, 2, 1, 3).reshape(b * H, l, hd // H)
+            .to(torch.bfloat16).contiguous())
+
+
+def _unheads(y, b, H):
+    bh, l, d = y.shape
+    return y.reshape(b, H, l, d).permute(0, 2, 1, 3).reshape(b, l, H * d)
+
+
+def _lr_heads(lr, b, l, H):
+    """D:381-398: lr [b, l, 3] (shared by the heads) or [b, l, H*3] -> three
+    contiguous fp32 [b*H, l]."""
+    if lr.shape[2] == 3:
+        lr = lr.unsqueeze(2).expand(b, l, H, 3)
+    else:
+        lr = lr.reshape(b, l, H, 3)
+    lr = lr.permute(0, 2, 1, 3).reshape(b * H, l, 3).float()
+    return [lr[..., j].contiguous() for j in range(3)]
+
+
+def _gs(B, N, device):
+    return torch.full((B, 1), N, dtype=torch.int32, device=device)
+
+
+def apply_fast_weights(x, w0, w1, w2):
+    """D:241-268.  x [b, l, H*d] -> out [b, l, H*d] (bf16)."""
+    b, H, dh, d = w0.shape
+    W02 = torch.cat([w0, w2], dim=2).to(torch.bfloat16).reshape(b * H, 1, 2 * dh, d).contiguous()
+    W1 = w1.to(torch.bfloat16).reshape(b * H, 1, d, dh).contiguous()
+    return _read(x, W02, W1, b, H)
+
+
+def _read(x, W02, W1, b, H):
+    L.require_device(x)
+    xh = _heads(x, H)
+    gs = _gs(b * H, xh.shape[1], x.device)
+    hid = G.gate_up(W02, xh, gs, token_major=True)
+    return _unheads(G.gemm_nt(W1, hid, gs), b, H)
+
+
+def _update(W02, W1, ks, vs, lrs, b, H):
+    """The grouped UPDATE of several layers' tokens at once: per head the
+    tokens of all layers concatenated.  Returns bf16 (dW0_W2, dW1)."""
+    kh = torch.cat([_heads(k, H) for k in ks], dim=1).contiguous()
+    vh = torch.cat([_heads(v, H) for v in vs], dim=1).contiguous()
+    per = [_lr_heads(lr, b, k.shape[1], H) for lr, k in zip(lrs, ks)]
+    lr3 = [torch.cat([p[j] for p in per], dim=1).contiguous() for j in range(3)]
+    gs = _gs(b * H, kh.shape[1], kh.device)
+    dy, hl = G.update_stage1(W02, W1, kh, vh, lr3[0], lr3[1], lr3[2], gs, token_major=True)
+    return G.wgrad_pair(dy, kh, hl, vh, gs)
+
+
+def compute_update(k, v, lr, fastw):
+    """D:333-449 from the preprocessed k, v [b, l, H*d] and lr [b, l, 3] or
+    [b, l, H*3]: (dw0 [b,H,d_h,d], dw1 [b,H,d,d_h], dw2) in fp32."""
+    w0, w1, w2 = fastw
+    b, H, dh, d = w0.shape
+    L.require_device(k, v, lr, w0)
+    W02 = torch.cat([w0, w2], dim=2).to(torch.bfloat16).reshape(b * H, 1, 2 * dh, d).contiguous()
+    W1 = w1.to(torch.bfloat16).reshape(b * H, 1, d, dh).contiguous()
+    dW02, dW1 = _update(W02, W1, [k], [v], [lr], b, H)
+    dW02 = dW02.float().reshape(b, H, 2 * dh, d)
+    return dW02[:, :, :dh], dW1.float().reshape(b, H, d, dh), dW02[:, :, dh:]
+
+
+class SharedFastWeights:
+    """The shared fast-weight bank of uTTT-Dense (D:1801-1863), aggregate
+    schedule: read() every layer of a chunk with the chunk-start weights, then
+    write() once from the mean (or sum) of the layers' updates, projected per
+    d x d slice onto the old slice norms (_apply_shared_update).
+
+    w0, w2: [b, H, r*d, d]; w1: [b, H, d, r*d]; masters fp32 (default: the
+    given weights in fp32).  Momentum and Muon are not part of this write."""
+
+    def __init__(self, w0, w1, w2, r, masters=None, lr_scale=1.0, reduce="mean",
+                 master_renorm=False):
+        b, H, dh, d = w0.shape
+        if dh != r * d or tuple(w1.shape) != (b, H, d, r * d) or w2.shape != w0.shape:
+            raise ValueError(f"invalid shared fast state shapes for r={r}")
+        if reduce not in ("mean", "sum"):
+            raise ValueError(f"`uttt_agg_reduce` must be 'mean' or 'sum', got {reduce!r}.")
+        L.require_device(w0, w1, w2)
+        self.b, self.H, self.d, self.dh, self.r = b, H, d, dh, r
+        self.lr_scale, self.reduce, self.master_renorm = float(lr_scale), reduce, master_renorm
+        m0, m1, m2 = masters if masters is not None else (w0, w1, w2)
+        self.M02 = torch.cat([m0, m2], dim=2).float().reshape(b * H, 1, 2 * dh, d).contiguous()
+        self.M1 = m1.float().reshape(b * H, 1, d, dh).contiguous()
+        self.W02 = torch.cat([w0, w2], dim=2).to(torch.bfloat16).reshape(b * H, 1, 2 * dh, d).contiguous()
+        self.W1 = w1.to(torch.bfloat16).reshape(b * H, 1, d, dh).contiguous()
+        self._spare02 = torch.empty_like(self.W02)
+        self._spare1 = torch.empty_like(self.W1)
+
+    def read(self, q):
+        """One layer's read of a chunk: q [b, l, H*d] -> [b, l, H*d] bf16."""
+        return _read(q, self.W02, self.W1, self.b, self.H)
+
+    def write(self, ks, vs, lrs):
+        """The chunk's aggregate write from every layer's preprocessed k, v
+        [b, l, H*d] and lr ([b, l, 3] or [b, l, H*3])."""
+        dW02, dW1 = _update(self.W02, self.W1, ks, vs, lrs, self.b, self.H)
+        scale = self.lr_scale / (len(ks) if self.reduce == "mean" else 1)
+        st = L.stream_of(dW02)
+        nf = 0 if self.master_renorm else 1
+        B, d, dh = self.b * self.H, self.d, self.dh
+        # W0_W2 rows are whole d x d slice rows; W1 rows hold r slices of d
+        L.call("uttt_write_step", L.ptr(self.M02), L.ptr(self.W02), L.ptr(dW02), L.BF16, None,
+               None, scale, B, 2 * dh, d, d, nf, int(self.master_renorm), L.ptr(self.M02),
+               L.ptr(self._spare02), None, st)
+        L.call("uttt_write_step", L.ptr(self.M1), L.ptr(self.W1), L.ptr(dW1), L.BF16, None, None,
+               scale, B, d, dh, d, nf, int(self.master_renorm), L.ptr(self.M1),
+               L.ptr(self._spare1), None, st)
+        self.W02, self._spare02 = self._spare02, self.W02
+        self.W1, self._spare1 = self._spare1, self.W1
+
+    def weights(self):
+        """((w0, w1, w2) bf16, (w0, w1, w2) fp32 masters) in the reference layout."""
+        b, H, dh, d = self.b, self.H, self.dh, self.d
+
+        def split(W02, W1):
+            w02 = W02.reshape(b, H, 2 * dh, d)
+            return w02[:, :, :dh].contiguous(), W1.reshape(b, H, d, dh), w02[:, :, dh:].contiguous()
+
+        return split(self.W02, self.W1), split(self.M02, self.M1)
