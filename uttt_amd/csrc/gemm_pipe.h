@@ -153,14 +153,40 @@ struct TileLoader {
   }
 };
 
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// LDS byte address of a __shared__ pointer.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)((const __attribute__((address_space(3))) void*)p);
+}
+
+// The two LDS fragment reads as inline asm.  The compiler's wait-count pass
+// does not model these, so it can neither stall them behind in-flight LDS-DMA
+// loads nor insert the lgkmcnt wait their consumers need: run_pipeline<kAsm>
+// places every wait itself.  "memory" keeps them in program order with the
+// loads and barriers.
+__device__ __forceinline__ i16x4 ds_tr16_asm(const void* p) {
+  i32x2 v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(v) : "v"(lds_addr(p)) : "memory");
+  return __builtin_bit_cast(i16x4, v);
+}
+__device__ __forceinline__ bf16x8 ds_b128_asm(const void* p) {
+  i32x4 v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(lds_addr(p)) : "memory");
+  return __builtin_bit_cast(bf16x8, v);
+}
+
 // MFMA operand fragment of rows [rb, rb+32), k-substep ks (16 k) of an LDS tile.
-template <int MAJOR>
+template <int MAJOR, bool ASM = false>
 __device__ __forceinline__ bf16x8 frag(const uint8_t* tile, int rb, int ks) {
   const int lane = threadIdx.x & 63;
   if constexpr (MAJOR == KMajor) {
     const int r = rb + (lane & 31);
     const int c = 2 * ks + (lane >> 5);
-    return *reinterpret_cast<const bf16x8*>(tile + (r * 4 + (c ^ kswz(r))) * 16);
+    const uint8_t* p = tile + (r * 4 + (c ^ kswz(r))) * 16;
+    if constexpr (ASM) return ds_b128_asm(p);
+    return *reinterpret_cast<const bf16x8*>(p);
   } else {
     const int g = lane >> 4, s = lane & 15;
     const int j = s >> 2, q = s & 3;
@@ -170,94 +196,215 @@ __device__ __forceinline__ bf16x8 frag(const uint8_t* tile, int rb, int ks) {
     const int k0 = kb, k1 = kb + 4;
     const uint8_t* p0 = tile + (k0 * 16 + (c ^ rswz(k0))) * 16 + 8 * (q & 1);
     const uint8_t* p1 = tile + (k1 * 16 + (c ^ rswz(k1))) * 16 + 8 * (q & 1);
-    const i16x4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (__attribute__((address_space(3))) i16x4*)(p0));
-    const i16x4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (__attribute__((address_space(3))) i16x4*)(p1));
+    i16x4 x0, x1;
+    if constexpr (ASM) {
+      x0 = ds_tr16_asm(p0);
+      x1 = ds_tr16_asm(p1);
+    } else {
+      x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(p0));
+      x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(p1));
+    }
     const i16x8 x = __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7);
     return __builtin_bit_cast(bf16x8, x);
   }
 }
 
-// Fragments of one stage: both k-substeps of B (this wave's 4 column blocks)
-// and of A0 / A1 (this wave's 2 row blocks).
-struct StageFrags {
-  bf16x8 b[kBK / 16][kNB], a0[kBK / 16][2], a1[kBK / 16][2];
+// Fragments of one k-substep (16 k) of a stage: this wave's 4 column blocks of
+// B and its 2 row blocks of A0 / A1.
+struct HalfFrags {
+  bf16x8 b[kNB], a0[2], a1[2];
 };
 
-template <int AMAJ, int BMAJ>
-__device__ __forceinline__ void read_stage(StageFrags& f, const uint8_t* st, int wm, int wn) {
+template <int AMAJ, int BMAJ, bool ASM = false>
+__device__ __forceinline__ void read_half(HalfFrags& f, const uint8_t* st, int ks, int wm,
+                                          int wn) {
   const uint8_t* a0 = st;
   const uint8_t* a1 = st + kTileBytes;
   const uint8_t* b = st + (2 + wn) * kTileBytes;  // this wave's B half
 #pragma unroll
-  for (int ks = 0; ks < kBK / 16; ++ks) {
+  for (int j = 0; j < kNB; ++j) f.b[j] = frag<BMAJ, ASM>(b, j * 32, ks);
 #pragma unroll
-    for (int j = 0; j < kNB; ++j) f.b[ks][j] = frag<BMAJ>(b, j * 32, ks);
+  for (int i = 0; i < 2; ++i) f.a0[i] = frag<AMAJ, ASM>(a0, wm * 64 + i * 32, ks);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) f.a0[ks][i] = frag<AMAJ>(a0, wm * 64 + i * 32, ks);
-#pragma unroll
-    for (int i = 0; i < 2; ++i) f.a1[ks][i] = frag<AMAJ>(a1, wm * 64 + i * 32, ks);
-  }
+  for (int i = 0; i < 2; ++i) f.a1[i] = frag<AMAJ, ASM>(a1, wm * 64 + i * 32, ks);
 }
 
-// acc_a[i][j] += A_a(wave rows i) * B(wave cols j) over one stage, a = 0, 1.
-__device__ __forceinline__ void mma_frags(f32x16 (&acc0)[2][kNB], f32x16 (&acc1)[2][kNB],
-                                          const StageFrags& f) {
-#pragma unroll
-  for (int ks = 0; ks < kBK / 16; ++ks) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < kNB; ++j)
-        acc0[i][j] =
-            __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a0[ks][i], f.b[ks][j], acc0[i][j], 0, 0, 0);
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < kNB; ++j)
-        acc1[i][j] =
-            __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a1[ks][i], f.b[ks][j], acc1[i][j], 0, 0, 0);
-  }
+// LDS instructions of one read_half: a KMajor fragment is one ds_read_b128,
+// an RMajor one two ds_read_b64_tr_b16.
+template <int AMAJ, int BMAJ>
+constexpr int half_lds_ops() {
+  return kNB * (BMAJ == KMajor ? 1 : 2) + 4 * (AMAJ == KMajor ? 1 : 2);
 }
 
-// Four-stage ring: load(step, stage) issues kLoadsPerStage loads per wave;
-// read(stage) fetches the stage's MFMA fragments into registers and mma()
-// consumes them.  Step kt waits for its own loads while those of steps kt+1
-// and kt+2 are still in flight, reads its fragments, then issues step kt+3
-// into the stage step kt-1 used and runs the MFMAs.  Two rules keep the
-// compiler from inserting a wait for every outstanding load (vmcnt(0)) before
-// LDS reads, which would serialise the pipeline: the loads are issued
-// unconditionally (steps past the end read the zero block), since its
-// wait-count pass tracks LDS DMA per __shared__ array only along straight-line
-// paths; and the stage's fragment reads are issued before the step's new
-// loads (scheduling barriers keep that order).
-template <class LoadFn, class ReadFn, class MmaFn>
+// s_waitcnt on the LDS counter that the compiler must treat as redefining the
+// fragment registers, so no MFMA reading them can move above it.
+template <int N>
+__device__ __forceinline__ void lgkm_wait_tied(HalfFrags& f) {
+  i32x4 r[8] = {__builtin_bit_cast(i32x4, f.b[0]),  __builtin_bit_cast(i32x4, f.b[1]),
+                __builtin_bit_cast(i32x4, f.b[2]),  __builtin_bit_cast(i32x4, f.b[3]),
+                __builtin_bit_cast(i32x4, f.a0[0]), __builtin_bit_cast(i32x4, f.a0[1]),
+                __builtin_bit_cast(i32x4, f.a1[0]), __builtin_bit_cast(i32x4, f.a1[1])};
+  asm volatile("s_waitcnt lgkmcnt(%8)"
+               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]),
+                 "+v"(r[6]), "+v"(r[7])
+               : "i"(N)
+               : "memory");
+  f.b[0] = __builtin_bit_cast(bf16x8, r[0]);
+  f.b[1] = __builtin_bit_cast(bf16x8, r[1]);
+  f.b[2] = __builtin_bit_cast(bf16x8, r[2]);
+  f.b[3] = __builtin_bit_cast(bf16x8, r[3]);
+  f.a0[0] = __builtin_bit_cast(bf16x8, r[4]);
+  f.a0[1] = __builtin_bit_cast(bf16x8, r[5]);
+  f.a1[0] = __builtin_bit_cast(bf16x8, r[6]);
+  f.a1[1] = __builtin_bit_cast(bf16x8, r[7]);
+}
+
+// acc_a[i][j] += A_a(wave rows i) * B(wave cols j) over one k-substep, a = 0, 1.
+__device__ __forceinline__ void mma_half(f32x16 (&acc0)[2][kNB], f32x16 (&acc1)[2][kNB],
+                                         const HalfFrags& f) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < kNB; ++j)
+      acc0[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a0[i], f.b[j], acc0[i][j], 0, 0, 0);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < kNB; ++j)
+      acc1[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a1[i], f.b[j], acc1[i][j], 0, 0, 0);
+}
+
+// Four-stage ring with the fragment reads of one k-substep overlapping the
+// MFMAs of the previous one (kOverlap).  load(step, stage) issues
+// kLoadsPerStage loads per wave, read(stage, ks, frags) the fragments of
+// k-substep ks, mma(frags) their 16 MFMAs.  Stages kt+1..kt+3 are in flight
+// while step kt runs:
+//   read (kt, 1) -> f1      | MFMAs of f0 = (kt, 0)
+//   wait for stage kt+1, barrier (every wave is done reading stage kt)
+//   read (kt+1, 0) -> f0, then load stage kt+4 into stage kt's buffer
+//                           | MFMAs of f1 = (kt, 1)
+// so the matrix cores are fed while the next fragments arrive, with one wave
+// per SIMD.
+//
+// kSerial keeps every LDS read directly behind a wait and a barrier:
+//   wait for stage kt, barrier, read (kt, 0) and (kt, 1), load stage kt+3 into
+//   the buffer of stage kt-1, MFMAs of (kt, 0) and (kt, 1).
+// With the builtin transposing reads (ds_read_b64_tr_b16, RMajor operands)
+// neither order pipelines: the compiler's wait-count pass cannot tell those
+// reads apart from in-flight LDS-DMA loads and drains every outstanding load
+// (vmcnt(0)) in front of them.  kAsm (below) issues them as inline asm.
+//
+// In both, the compiler must not insert such drains for the plain reads: the
+// loads are issued unconditionally (steps past the end read the zero block),
+// each stage has its own __shared__ array, the loop is unrolled over the four
+// stages so every access names its array, and scheduling barriers keep the
+// order above.
+enum Sched { kSerial = 0, kOverlap = 1, kAsm = 2 };
+
+template <int SCHED, int NLDS = 0, class LoadFn, class ReadFn, class MmaFn>
 __device__ __forceinline__ void run_pipeline(int nk, LoadFn&& load, ReadFn&& read, MmaFn&& mma,
                                              uint8_t* s0, uint8_t* s1, uint8_t* s2,
                                              uint8_t* s3) {
-  load(0, s0);
-  load(1, s1);
-  load(2, s2);
-  auto step = [&](int kt, const uint8_t* cur, uint8_t* nxt) {
-    wait_vmcnt<2 * kLoadsPerStage>();
+  if (nk <= 0) return;
+  HalfFrags f0, f1;
+  if constexpr (SCHED == kAsm) {
+    // The overlapped order with the fragment reads in inline asm (read_half
+    // with ASM = true, NLDS instructions each): before the MFMAs of f0 the
+    // NLDS reads of f1 are the only younger LDS operations, so
+    // lgkmcnt(min(NLDS, 15)) leaves f0 complete; the barrier's lgkmcnt(0)
+    // completes f1; the reads of the stage past the end are drained at exit.
+    constexpr int kW = NLDS < 15 ? NLDS : 15;
+    load(0, s0);
+    load(1, s1);
+    load(2, s2);
+    load(3, s3);
+    wait_vmcnt<3 * kLoadsPerStage>();
     block_barrier();
-    read(cur);
-    __builtin_amdgcn_sched_barrier(0);
-    load(kt + 3, nxt);
-    __builtin_amdgcn_sched_barrier(0);
-    mma();
-  };
-  int kt = 0;
-  for (; kt + 4 <= nk; kt += 4) {
-    step(kt, s0, s3);
-    step(kt + 1, s1, s0);
-    step(kt + 2, s2, s1);
-    step(kt + 3, s3, s2);
+    read(s0, 0, f0);
+    auto step = [&](int kt, uint8_t* cur, const uint8_t* nxt) __attribute__((always_inline)) {
+      read(cur, 1, f1);
+      lgkm_wait_tied<kW>(f0);
+      mma(f0);
+      __builtin_amdgcn_sched_barrier(0);
+      wait_vmcnt<2 * kLoadsPerStage>();
+      lgkm_wait_tied<0>(f1);
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      read(nxt, 0, f0);
+      load(kt + 4, cur);
+      __builtin_amdgcn_sched_barrier(0);
+      mma(f1);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    int kt = 0;
+    for (; kt + 4 <= nk; kt += 4) {
+      step(kt, s0, s1);
+      step(kt + 1, s1, s2);
+      step(kt + 2, s2, s3);
+      step(kt + 3, s3, s0);
+    }
+    if (kt < nk) step(kt, s0, s1);
+    if (kt + 1 < nk) step(kt + 1, s1, s2);
+    if (kt + 2 < nk) step(kt + 2, s2, s3);
+    lgkm_wait_tied<0>(f0);
+  } else if constexpr (SCHED == kOverlap) {
+    load(0, s0);
+    load(1, s1);
+    load(2, s2);
+    load(3, s3);
+    wait_vmcnt<3 * kLoadsPerStage>();
+    block_barrier();
+    read(s0, 0, f0);
+    auto step = [&](int kt, uint8_t* cur, const uint8_t* nxt) __attribute__((always_inline)) {
+      read(cur, 1, f1);
+      __builtin_amdgcn_sched_barrier(0);
+      mma(f0);
+      __builtin_amdgcn_sched_barrier(0);
+      wait_vmcnt<2 * kLoadsPerStage>();
+      block_barrier();
+      read(nxt, 0, f0);
+      __builtin_amdgcn_sched_barrier(0);
+      load(kt + 4, cur);
+      __builtin_amdgcn_sched_barrier(0);
+      mma(f1);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    int kt = 0;
+    for (; kt + 4 <= nk; kt += 4) {
+      step(kt, s0, s1);
+      step(kt + 1, s1, s2);
+      step(kt + 2, s2, s3);
+      step(kt + 3, s3, s0);
+    }
+    if (kt < nk) step(kt, s0, s1);
+    if (kt + 1 < nk) step(kt + 1, s1, s2);
+    if (kt + 2 < nk) step(kt + 2, s2, s3);
+  } else {
+    load(0, s0);
+    load(1, s1);
+    load(2, s2);
+    auto step = [&](int kt, const uint8_t* cur, uint8_t* nxt) __attribute__((always_inline)) {
+      wait_vmcnt<2 * kLoadsPerStage>();
+      block_barrier();
+      read(cur, 0, f0);
+      read(cur, 1, f1);
+      __builtin_amdgcn_sched_barrier(0);
+      load(kt + 3, nxt);
+      __builtin_amdgcn_sched_barrier(0);
+      mma(f0);
+      mma(f1);
+    };
+    int kt = 0;
+    for (; kt + 4 <= nk; kt += 4) {
+      step(kt, s0, s3);
+      step(kt + 1, s1, s0);
+      step(kt + 2, s2, s1);
+      step(kt + 3, s3, s2);
+    }
+    if (kt < nk) step(kt, s0, s3);
+    if (kt + 1 < nk) step(kt + 1, s1, s0);
+    if (kt + 2 < nk) step(kt + 2, s2, s1);
   }
-  if (kt < nk) step(kt, s0, s3);
-  if (kt + 1 < nk) step(kt + 1, s1, s0);
-  if (kt + 2 < nk) step(kt + 2, s2, s1);
   wait_vmcnt<0>();  // drain the loads issued past the end
 }
 

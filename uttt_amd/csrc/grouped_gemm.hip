@@ -337,11 +337,16 @@ __global__ __launch_bounds__(kThreads) void tn_kernel(TnArgs a, typename Epi::Ar
   };
   const int w = threadIdx.x >> 6;
   const int wm = w >> 1, wn = w & 1;
-  StageFrags fr;
-  auto read = [&](const uint8_t* st) { read_stage<AMAJ, KMajor>(fr, st, wm, wn); };
-  auto mma = [&]() { mma_frags(acc0, acc1, fr); };
+  // K-major operands use the compiler's LDS reads; a row-major A needs the
+  // transposing reads, issued as inline asm (see run_pipeline)
+  constexpr bool kAsmReads = AMAJ == RMajor;
+  auto read = [&](const uint8_t* st, int ks, HalfFrags& f) __attribute__((always_inline)) {
+    read_half<AMAJ, KMajor, kAsmReads>(f, st, ks, wm, wn);
+  };
+  auto mma = [&](const HalfFrags& f) __attribute__((always_inline)) { mma_half(acc0, acc1, f); };
   (void)two;
-  run_pipeline(nk0 + nk1, load, read, mma, st0, st1, st2, st3);
+  run_pipeline<kAsmReads ? kAsm : kOverlap, half_lds_ops<AMAJ, KMajor>()>(
+      nk0 + nk1, load, read, mma, st0, st1, st2, st3);
   const TileCtx c{b, m0, wm, wn, mt, tt};
   Epi::apply(ea, acc0, acc1, c, two);
 }
@@ -401,10 +406,12 @@ __global__ __launch_bounds__(kThreads) void wg_kernel(WgTask t0, WgTask t1,
   };
   const int w = threadIdx.x >> 6;
   const int wm = w >> 1, wn = w & 1;
-  StageFrags fr;
-  auto read = [&](const uint8_t* st) { read_stage<RMajor, RMajor>(fr, st, wm, wn); };
-  auto mma = [&]() { mma_frags(acc0, acc1, fr); };
-  run_pipeline((size + kBK - 1) / kBK, load, read, mma, st0, st1, st2, st3);
+  auto read = [&](const uint8_t* st, int ks, HalfFrags& f) __attribute__((always_inline)) {
+    read_half<RMajor, RMajor, true>(f, st, ks, wm, wn);
+  };
+  auto mma = [&](const HalfFrags& f) __attribute__((always_inline)) { mma_half(acc0, acc1, f); };
+  run_pipeline<kAsm, half_lds_ops<RMajor, RMajor>()>((size + kBK - 1) / kBK, load, read, mma,
+                                                     st0, st1, st2, st3);
 
   uint16_t* ob = tk.out + ((int64_t)b * E + e) * X * Y;
   for_quads(acc0, acc1, wm, wn, true, [&](int tt, int r, int n, const float* v) __attribute__((always_inline)) {
