@@ -59,6 +59,22 @@ __device__ __attribute__((aligned(16))) uint4 g_zero16;
 
 #define UTTT_LDS(p) ((__attribute__((address_space(3))) void*)(p))
 
+// Wave index inside the workgroup as a wave-uniform (scalar) value.
+__device__ __forceinline__ int wave_id() {
+  return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+}
+
+// A pointer that is the same for every lane, marked wave-uniform so that it
+// stays in scalar registers (and addresses built from it use the scalar-base
+// form of the global loads).
+template <class T>
+__device__ __forceinline__ T* uniform_ptr(T* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return reinterpret_cast<T*>(((uint64_t)hi << 32) | lo);
+}
+
 // s_waitcnt vmcnt(N) leaving the export and LDS counters alone (gfx9
 // encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14).
 template <int N>
@@ -91,64 +107,88 @@ struct Operand {
 __device__ __forceinline__ int kswz(int r) { return (r >> 2) & 3; }
 __device__ __forceinline__ int rswz(int k) { return (k & 3) << 2; }
 
-// Per-lane state of the loads of one 128-row x kBK tile of an operand for a
-// whole K loop: the element offsets of this lane's kLoadsPerTile chunks
-// relative to the tile origin, their k position (for the k-range test) and
-// whether their row is valid (fixed for the workgroup).
+// Loads of one 128-row x kBK tile of an operand for a whole K loop.  The
+// tile origin and its per-step advance are wave-uniform (scalar registers);
+// each lane keeps only the 32-bit byte offsets of its kLoadsPerTile chunks, so
+// a load is one global_load_lds_dwordx4 with a scalar base and a vector
+// offset, and a whole step costs a few scalar instructions.  Rows past the
+// operand's end are clamped onto its last valid row (their products land in
+// output rows or token columns that are never stored); only the K tail (the
+// last step when k_end is not a multiple of kBK) reads zeros for k >= k_end,
+// through the masked form.  Steps past the last re-read the last step into a
+// stage that is never multiplied.
 template <int MAJOR>
 struct TileLoader {
-  const uint16_t* base;   // operand element (r0, 0)
-  int64_t kstep;          // elements advanced per K step
+  const uint8_t* base;    // wave-uniform: byte address of the tile origin at step 0
+  int64_t kstep;          // bytes advanced per K step
+  int last;               // last step holding data
   int k_end;
-  int off[kLoadsPerTile];
-  int kk[kLoadsPerTile];  // k of the lane's chunk inside the tile
-  bool rok[kLoadsPerTile];
+  uint32_t off[kLoadsPerTile];
 
   __device__ __forceinline__ void init(const Operand& op, int r0) {
     const int lane = threadIdx.x & 63;
-    const int w = threadIdx.x >> 6;
+    const int w = wave_id();
     k_end = op.k_end;
-    if constexpr (MAJOR == KMajor) {
-      base = op.base + (int64_t)r0 * op.ld;
-      kstep = kBK;
-    } else {
-      base = op.base + r0;
-      kstep = (int64_t)kBK * op.ld;
+    last = (op.k_end + kBK - 1) / kBK - 1;
+    int nrows = op.r_end - r0;
+    const uint16_t* org;
+    if (nrows > 0) {
+      org = MAJOR == KMajor ? op.base + (int64_t)r0 * op.ld : op.base + r0;
+    } else {  // no valid row: read the operand's first rows instead
+      org = op.base;
+      nrows = MAJOR == KMajor ? 1 : 8;
     }
+    base = uniform_ptr(reinterpret_cast<const uint8_t*>(org));
+    kstep = MAJOR == KMajor ? (int64_t)kBK * 2 : (int64_t)kBK * op.ld * 2;
 #pragma unroll
     for (int t = 0; t < kLoadsPerTile; ++t) {
       const int s = (t * 4 + w) * 64 + lane;
       if constexpr (MAJOR == KMajor) {
         const int r = s >> 2;
         const int c = (s & 3) ^ kswz(r);
-        off[t] = r * (int)op.ld + c * 8;
-        kk[t] = c * 8;
-        rok[t] = r0 + r < op.r_end;
+        const int rr = r < nrows ? r : nrows - 1;
+        off[t] = (uint32_t)(rr * (int)op.ld + c * 8) * 2u;
       } else {
         const int k = s >> 4;
         const int c = (s & 15) ^ rswz(k);
-        off[t] = k * (int)op.ld + c * 8;
-        kk[t] = k;
-        rok[t] = r0 + c * 8 < op.r_end;
+        const int cmax = (nrows >> 3) - 1;
+        const int cc = c < cmax ? c : cmax;
+        off[t] = (uint32_t)(k * (int)op.ld + cc * 8) * 2u;
       }
     }
   }
 
-  // Issue this wave's loads of K step `step` into the LDS tile at `dst`.
-  __device__ __forceinline__ void load(int step, uint8_t* dst) const {
-    const int w = threadIdx.x >> 6;
-    const int k0 = step * kBK;
-    const uint16_t* b = base + kstep * step;
-    const uintptr_t zero = reinterpret_cast<uintptr_t>(&g_zero16);
-#pragma unroll
-    for (int t = 0; t < kLoadsPerTile; ++t) {
-      // branch-free select (a branch here would split the straight-line path
-      // the wait-count pass needs, see run_pipeline)
-      const uintptr_t a = reinterpret_cast<uintptr_t>(b + off[t]);
-      const bool ok = rok[t] & (k0 + kk[t] < k_end);
-      const uintptr_t src = ok ? a : zero;
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
-                                       UTTT_LDS(dst + (t * 4 + w) * 64 * 16), 16, 0, 0);
+  __device__ __forceinline__ int clamp_step(int step) const { return step < last ? step : last; }
+  // Wave-uniform address of step `step`'s tile origin.
+  __device__ __forceinline__ const uint8_t* step_base(int step) const {
+    return uniform_ptr(base + (int64_t)clamp_step(step) * kstep);
+  }
+  // Whether the loads of `step` need the masked (K tail) form.
+  __device__ __forceinline__ bool tail(int step) const {
+    return clamp_step(step) == last && (k_end % kBK) != 0;
+  }
+
+  // Issue load t of this wave's share of the step at `sb` into LDS tile `dst`.
+  template <bool MASKED>
+  __device__ __forceinline__ void issue(const uint8_t* sb, int step, int t, uint8_t* dst) const {
+    uint8_t* d = dst + (t * 4 + wave_id()) * 64 * 16;
+    if constexpr (!MASKED) {
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(sb + off[t]), UTTT_LDS(d), 16,
+                                       0, 0);
+    } else {
+      const int lane = threadIdx.x & 63;
+      const int s = (t * 4 + wave_id()) * 64 + lane;
+      int kk;
+      if constexpr (MAJOR == KMajor) {
+        const int r = s >> 2;
+        kk = ((s & 3) ^ kswz(r)) * 8;
+      } else {
+        kk = s >> 4;
+      }
+      const bool ok = clamp_step(step) * kBK + kk < k_end;
+      const uintptr_t src =
+          ok ? reinterpret_cast<uintptr_t>(sb + off[t]) : reinterpret_cast<uintptr_t>(&g_zero16);
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src), UTTT_LDS(d), 16, 0, 0);
     }
   }
 };
@@ -259,6 +299,18 @@ __device__ __forceinline__ void lgkm_wait_tied(HalfFrags& f) {
   f.a1[1] = __builtin_bit_cast(bf16x8, r[7]);
 }
 
+// f(std::integral_constant<int, i>) for i = 0 .. N-1 with compile-time i, so
+// that accumulator indices stay constants whatever the unroller decides (a
+// runtime index would move the accumulator arrays to scratch memory).
+template <class F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 // acc_a[i][j] += A_a(wave rows i) * B(wave cols j) over one k-substep, a = 0, 1.
 __device__ __forceinline__ void mma_half(f32x16 (&acc0)[2][kNB], f32x16 (&acc1)[2][kNB],
                                          const HalfFrags& f) {
@@ -274,150 +326,111 @@ __device__ __forceinline__ void mma_half(f32x16 (&acc0)[2][kNB], f32x16 (&acc1)[
       acc1[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a1[i], f.b[j], acc1[i][j], 0, 0, 0);
 }
 
-// Four-stage ring with the fragment reads of one k-substep overlapping the
-// MFMAs of the previous one (kOverlap).  load(step, stage) issues
-// kLoadsPerStage loads per wave, read(stage, ks, frags) the fragments of
-// k-substep ks, mma(frags) their 16 MFMAs.  Stages kt+1..kt+3 are in flight
-// while step kt runs:
-//   read (kt, 1) -> f1      | MFMAs of f0 = (kt, 0)
-//   wait for stage kt+1, barrier (every wave is done reading stage kt)
-//   read (kt+1, 0) -> f0, then load stage kt+4 into stage kt's buffer
-//                           | MFMAs of f1 = (kt, 1)
-// so the matrix cores are fed while the next fragments arrive, with one wave
-// per SIMD.
-//
-// kSerial keeps every LDS read directly behind a wait and a barrier:
-//   wait for stage kt, barrier, read (kt, 0) and (kt, 1), load stage kt+3 into
-//   the buffer of stage kt-1, MFMAs of (kt, 0) and (kt, 1).
-// With the builtin transposing reads (ds_read_b64_tr_b16, RMajor operands)
-// neither order pipelines: the compiler's wait-count pass cannot tell those
-// reads apart from in-flight LDS-DMA loads and drains every outstanding load
-// (vmcnt(0)) in front of them.  kAsm (below) issues them as inline asm.
-//
-// In both, the compiler must not insert such drains for the plain reads: the
-// loads are issued unconditionally (steps past the end read the zero block),
-// each stage has its own __shared__ array, the loop is unrolled over the four
-// stages so every access names its array, and scheduling barriers keep the
-// order above.
-enum Sched { kSerial = 0, kOverlap = 1, kAsm = 2 };
+// The same 16 MFMAs with between(p) (p = 0 .. 7, a compile-time constant)
+// issued after MFMAs 2p and 2p+1, each in its own scheduling region: the wave
+// issues the work of `between` while the matrix core is busy.
+template <class Between>
+__device__ __forceinline__ void mma_half(f32x16 (&acc0)[2][kNB], f32x16 (&acc1)[2][kNB],
+                                         const HalfFrags& f, Between&& between) {
+  static_for<16>([&](auto I) __attribute__((always_inline)) {
+    constexpr int a = decltype(I)::value / 8;
+    constexpr int i = (decltype(I)::value / 4) % 2;
+    constexpr int j = decltype(I)::value % 4;
+    if constexpr (a == 0)
+      acc0[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a0[i], f.b[j], acc0[i][j], 0, 0, 0);
+    else
+      acc1[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a1[i], f.b[j], acc1[i][j], 0, 0, 0);
+    if constexpr (decltype(I)::value % 2 == 1) {
+      __builtin_amdgcn_sched_barrier(0);
+      between(std::integral_constant<int, decltype(I)::value / 2>{});
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  });
+}
 
-template <int SCHED, int NLDS = 0, class LoadFn, class ReadFn, class MmaFn>
-__device__ __forceinline__ void run_pipeline(int nk, LoadFn&& load, ReadFn&& read, MmaFn&& mma,
+// The K loop: a ring of four LDS stages; the loads of step kt+4 are issued
+// during step kt, so three steps are in flight while one is multiplied.
+//   prep(kt)                 readies the loads of step kt (operand switch,
+//                            per-step scalar bases) and returns whether they
+//                            need the masked (K tail) form
+//   issue(p, masked, stage)  issues load p (0 .. kLoadsPerStage-1, a constant)
+//                            of the prepared step into `stage`
+//   read(stage, ks, frags)   the fragment reads of k-substep ks, inline asm,
+//                            NLDS LDS instructions
+// Step kt (stage cur, next stage nxt):
+//   read (kt, 1) -> f1;  prep(kt + 4);  wait for f0;  MFMAs of f0
+//   wait for this wave's loads of stage kt+1 and for f1, barrier (stage kt+1
+//   has landed for every wave, and every wave is done reading stage kt)
+//   read (kt+1, 0) -> f0;  MFMAs of f1 with the loads of step kt+4 into
+//   stage cur interleaved between them
+// so with one wave per SIMD the matrix core is fed while the next fragments
+// and the next stage arrive.  The fragment reads are inline asm because the
+// compiler's wait-count pass cannot tell them from the in-flight LDS-DMA
+// writes and would drain every load (vmcnt(0)) or every read (lgkmcnt(0))
+// in front of them; every wait here is explicit.  Before the MFMAs of f0 the
+// NLDS reads of f1 are the only younger LDS operations, so lgkmcnt(min(NLDS,
+// 15)) leaves f0 complete (any other LGKM operation only makes it stricter).
+template <int NLDS, class PrepFn, class IssueFn, class ReadFn>
+__device__ __forceinline__ void run_pipeline(int nk, PrepFn&& prep, IssueFn&& issue, ReadFn&& read,
+                                             f32x16 (&acc0)[2][kNB], f32x16 (&acc1)[2][kNB],
                                              uint8_t* s0, uint8_t* s1, uint8_t* s2,
                                              uint8_t* s3) {
   if (nk <= 0) return;
+  constexpr int kW = NLDS < 15 ? NLDS : 15;
   HalfFrags f0, f1;
-  if constexpr (SCHED == kAsm) {
-    // The overlapped order with the fragment reads in inline asm (read_half
-    // with ASM = true, NLDS instructions each): before the MFMAs of f0 the
-    // NLDS reads of f1 are the only younger LDS operations, so
-    // lgkmcnt(min(NLDS, 15)) leaves f0 complete; the barrier's lgkmcnt(0)
-    // completes f1; the reads of the stage past the end are drained at exit.
-    constexpr int kW = NLDS < 15 ? NLDS : 15;
-    load(0, s0);
-    load(1, s1);
-    load(2, s2);
-    load(3, s3);
-    wait_vmcnt<3 * kLoadsPerStage>();
-    block_barrier();
-    read(s0, 0, f0);
-    auto step = [&](int kt, uint8_t* cur, const uint8_t* nxt) __attribute__((always_inline)) {
-      read(cur, 1, f1);
-      lgkm_wait_tied<kW>(f0);
-      mma(f0);
-      __builtin_amdgcn_sched_barrier(0);
-      wait_vmcnt<2 * kLoadsPerStage>();
-      lgkm_wait_tied<0>(f1);
-      __builtin_amdgcn_s_barrier();
-      __builtin_amdgcn_sched_barrier(0);
-      read(nxt, 0, f0);
-      load(kt + 4, cur);
-      __builtin_amdgcn_sched_barrier(0);
-      mma(f1);
-      __builtin_amdgcn_sched_barrier(0);
-    };
-    int kt = 0;
-    for (; kt + 4 <= nk; kt += 4) {
-      step(kt, s0, s1);
-      step(kt + 1, s1, s2);
-      step(kt + 2, s2, s3);
-      step(kt + 3, s3, s0);
-    }
-    if (kt < nk) step(kt, s0, s1);
-    if (kt + 1 < nk) step(kt + 1, s1, s2);
-    if (kt + 2 < nk) step(kt + 2, s2, s3);
-    lgkm_wait_tied<0>(f0);
-  } else if constexpr (SCHED == kOverlap) {
-    load(0, s0);
-    load(1, s1);
-    load(2, s2);
-    load(3, s3);
-    wait_vmcnt<3 * kLoadsPerStage>();
-    block_barrier();
-    read(s0, 0, f0);
-    auto step = [&](int kt, uint8_t* cur, const uint8_t* nxt) __attribute__((always_inline)) {
-      read(cur, 1, f1);
-      __builtin_amdgcn_sched_barrier(0);
-      mma(f0);
-      __builtin_amdgcn_sched_barrier(0);
-      wait_vmcnt<2 * kLoadsPerStage>();
-      block_barrier();
-      read(nxt, 0, f0);
-      __builtin_amdgcn_sched_barrier(0);
-      load(kt + 4, cur);
-      __builtin_amdgcn_sched_barrier(0);
-      mma(f1);
-      __builtin_amdgcn_sched_barrier(0);
-    };
-    int kt = 0;
-    for (; kt + 4 <= nk; kt += 4) {
-      step(kt, s0, s1);
-      step(kt + 1, s1, s2);
-      step(kt + 2, s2, s3);
-      step(kt + 3, s3, s0);
-    }
-    if (kt < nk) step(kt, s0, s1);
-    if (kt + 1 < nk) step(kt + 1, s1, s2);
-    if (kt + 2 < nk) step(kt + 2, s2, s3);
-  } else {
-    load(0, s0);
-    load(1, s1);
-    load(2, s2);
-    auto step = [&](int kt, const uint8_t* cur, uint8_t* nxt) __attribute__((always_inline)) {
-      wait_vmcnt<2 * kLoadsPerStage>();
-      block_barrier();
-      read(cur, 0, f0);
-      read(cur, 1, f1);
-      __builtin_amdgcn_sched_barrier(0);
-      load(kt + 3, nxt);
-      __builtin_amdgcn_sched_barrier(0);
-      mma(f0);
-      mma(f1);
-    };
-    int kt = 0;
-    for (; kt + 4 <= nk; kt += 4) {
-      step(kt, s0, s3);
-      step(kt + 1, s1, s0);
-      step(kt + 2, s2, s1);
-      step(kt + 3, s3, s2);
-    }
-    if (kt < nk) step(kt, s0, s3);
-    if (kt + 1 < nk) step(kt + 1, s1, s0);
-    if (kt + 2 < nk) step(kt + 2, s2, s1);
+  auto load_all = [&](int kt, uint8_t* st) __attribute__((always_inline)) {
+    if (prep(kt))
+      static_for<kLoadsPerStage>([&](auto p) __attribute__((always_inline)) {
+        issue(p, std::true_type{}, st);
+      });
+    else
+      static_for<kLoadsPerStage>([&](auto p) __attribute__((always_inline)) {
+        issue(p, std::false_type{}, st);
+      });
+  };
+  load_all(0, s0);
+  load_all(1, s1);
+  load_all(2, s2);
+  load_all(3, s3);
+  wait_vmcnt<3 * kLoadsPerStage>();
+  block_barrier();
+  read(s0, 0, f0);
+  auto step = [&](int kt, uint8_t* cur, const uint8_t* nxt) __attribute__((always_inline)) {
+    read(cur, 1, f1);
+    const bool masked = prep(kt + 4);
+    lgkm_wait_tied<kW>(f0);
+    mma_half(acc0, acc1, f0);
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vmcnt<2 * kLoadsPerStage>();
+    lgkm_wait_tied<0>(f1);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    read(nxt, 0, f0);
+    // the rare K-tail step issues its masked loads up front; otherwise the
+    // loads ride between the MFMAs (branches hold loads only, so the
+    // accumulators never meet at a join)
+    if (masked)
+      static_for<kLoadsPerStage>([&](auto p) __attribute__((always_inline)) {
+        issue(p, std::true_type{}, cur);
+      });
+    __builtin_amdgcn_sched_barrier(0);
+    mma_half(acc0, acc1, f1, [&](auto p) __attribute__((always_inline)) {
+      if (!masked) issue(p, std::false_type{}, cur);
+    });
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  int kt = 0;
+  for (; kt + 4 <= nk; kt += 4) {
+    step(kt, s0, s1);
+    step(kt + 1, s1, s2);
+    step(kt + 2, s2, s3);
+    step(kt + 3, s3, s0);
   }
-  wait_vmcnt<0>();  // drain the loads issued past the end
-}
-
-// f(std::integral_constant<int, i>) for i = 0 .. N-1 with compile-time i, so
-// that accumulator indices stay constants whatever the unroller decides (a
-// runtime index would move the accumulator arrays to scratch memory).
-template <class F, int... Is>
-__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
-  (f(std::integral_constant<int, Is>{}), ...);
-}
-template <int N, class F>
-__device__ __forceinline__ void static_for(F&& f) {
-  static_for_impl(f, std::make_integer_sequence<int, N>{});
+  if (kt < nk) step(kt, s0, s1);
+  if (kt + 1 < nk) step(kt + 1, s1, s2);
+  if (kt + 2 < nk) step(kt + 2, s2, s3);
+  lgkm_wait_tied<0>(f0);  // the reads of the stage past the end
+  wait_vmcnt<0>();        // and the loads issued past the end
 }
 
 template <int M, int N>
@@ -501,7 +514,11 @@ __device__ TokenTile find_token_tile(const int32_t* __restrict__ gs_b, int E, in
     }
   }
   __syncthreads();
-  return TokenTile{s_scratch[0], s_scratch[1], s_scratch[2], s_scratch[3]};
+  // wave-uniform: the tile origins built from these live in scalar registers
+  return TokenTile{__builtin_amdgcn_readfirstlane(s_scratch[0]),
+                   __builtin_amdgcn_readfirstlane(s_scratch[1]),
+                   __builtin_amdgcn_readfirstlane(s_scratch[2]),
+                   __builtin_amdgcn_readfirstlane(s_scratch[3])};
 }
 
 // Segment [start, start+size) of expert e in batch b, clamped to [0, N).

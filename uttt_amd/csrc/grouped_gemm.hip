@@ -78,7 +78,91 @@ __device__ __forceinline__ void for_pairs(const f32x16 (&acc0)[2][kNB], const f3
 struct TileCtx {
   int b, m0, wm, wn, mt;
   TokenTile tt;
+  float* lds0;  // two stage buffers (32 KiB each), free once the K loop is done
+  float* lds1;
 };
+
+// ------------------------------------------------ coalesced epilogue frame --
+// The accumulators hold, per lane, 4 consecutive rows of one token: written
+// straight to a token-major tensor every wave instruction touches 32 tokens.
+// The heavy epilogues instead go through LDS, one 64-token quarter of the
+// tile at a time: the two waves owning the quarter write acc0 / acc1 as
+// fp32 [token][128 rows] (16-byte chunks XOR-swizzled by token, conflict-free),
+// then thread t takes token (t / 16) and rows 8 (t % 16) .. +7, so 16 lanes
+// cover 128 contiguous rows of one token: 16-byte global loads and stores.
+template <int Q>
+__device__ __forceinline__ void stage_quarter(const f32x16 (&acc0)[2][kNB],
+                                              const f32x16 (&acc1)[2][kNB], const TileCtx& c) {
+  if (c.wn != Q / 2) return;
+  static_for<2 * 2 * 4>([&](auto idx) __attribute__((always_inline)) {
+    constexpr int i = idx / 8;
+    constexpr int jl = (idx / 4) % 2;
+    constexpr int q = idx % 4;
+    constexpr int jj = 2 * (Q % 2) + jl;
+    const int n = jl * 32 + acc_col();
+    const int r = c.wm * 64 + i * 32 + acc_row(q * 4);
+    const int off = n * 128 + (((r >> 2) ^ (n & 31)) << 2);
+    *reinterpret_cast<float4*>(c.lds0 + off) =
+        make_float4(acc0[i][jj][q * 4], acc0[i][jj][q * 4 + 1], acc0[i][jj][q * 4 + 2],
+                    acc0[i][jj][q * 4 + 3]);
+    *reinterpret_cast<float4*>(c.lds1 + off) =
+        make_float4(acc1[i][jj][q * 4], acc1[i][jj][q * 4 + 1], acc1[i][jj][q * 4 + 2],
+                    acc1[i][jj][q * 4 + 3]);
+  });
+}
+
+// Rows 8g .. 8g+7 of staged token n.
+__device__ __forceinline__ void staged8(const float* reg, int n, int g, float (&v)[8]) {
+  const float4 a = *reinterpret_cast<const float4*>(reg + n * 128 + (((2 * g) ^ (n & 31)) << 2));
+  const float4 b =
+      *reinterpret_cast<const float4*>(reg + n * 128 + (((2 * g + 1) ^ (n & 31)) << 2));
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+  v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+__device__ __forceinline__ void load8(const uint16_t* p, float (&v)[8]) {
+  const uint4 u = *reinterpret_cast<const uint4*>(p);
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    v[2 * k] = bf16_to_f32((uint16_t)(w[k] & 0xffffu));
+    v[2 * k + 1] = bf16_to_f32((uint16_t)(w[k] >> 16));
+  }
+}
+__device__ __forceinline__ void load8(const float* p, float (&v)[8]) {
+  const float4 a = *reinterpret_cast<const float4*>(p);
+  const float4 b = *reinterpret_cast<const float4*>(p + 4);
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+  v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+__device__ __forceinline__ void store8(uint16_t* p, const float (&v)[8]) {
+  uint4 u;
+  u.x = (uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
+  u.y = (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
+  u.z = (uint32_t)f32_to_bf16(v[4]) | ((uint32_t)f32_to_bf16(v[5]) << 16);
+  u.w = (uint32_t)f32_to_bf16(v[6]) | ((uint32_t)f32_to_bf16(v[7]) << 16);
+  *reinterpret_cast<uint4*>(p) = u;
+}
+
+// Runs body(n, g) for the 64 x 16 (token, row-group) items of every quarter
+// of the tile, n = token index inside the tile (0..255), g = row group.
+template <class Body>
+__device__ __forceinline__ void staged_epilogue(const f32x16 (&acc0)[2][kNB],
+                                                const f32x16 (&acc1)[2][kNB], const TileCtx& c,
+                                                Body&& body) {
+  __syncthreads();  // every wave is done reading the stage buffers
+  static_for<4>([&](auto QQ) __attribute__((always_inline)) {
+    constexpr int Q = QQ;
+    stage_quarter<Q>(acc0, acc1, c);
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int it = threadIdx.x + kThreads * k;
+      body(it >> 4, Q * 64 + (it >> 4), it & 15);
+    }
+    __syncthreads();
+  });
+}
 
 // --- epilogue: plain store of both tiles into a token-major [B, N, ld] buffer
 template <class OutT>
@@ -145,18 +229,20 @@ struct EpiS1 {
     const float* dhb = ea.dh + (int64_t)c.b * ea.N * I;
     uint16_t* dyb = ea.dy + (int64_t)c.b * ea.N * I2;
     uint16_t* hb = ea.hid + (int64_t)c.b * ea.N * I;
-    for_pairs(acc0, acc1, c.wm, c.wn, [&](int r, int n, const float* y0, const float* y2) __attribute__((always_inline)) {
-      const int m = c.m0 + r;
+    staged_epilogue(acc0, acc1, c, [&](int nl, int n, int g) __attribute__((always_inline)) {
+      const int m = c.m0 + 8 * g;
       if (c.tt.n0 + n >= c.tt.size || m >= I) return;
       const int tok = c.tt.start + c.tt.n0 + n;
       const int64_t li = (int64_t)c.b * ea.N + tok;
       const float l0 = ea.lr0 ? LR::load(ea.lr0[li]) : 1.0f;
       const float l1 = ea.lr1 ? LR::load(ea.lr1[li]) : 1.0f;
       const float l2 = ea.lr2 ? LR::load(ea.lr2[li]) : 1.0f;
-      float dh[4], d0[4], d2[4], hh[4];
-      load4(dhb, I, tok, m, dh);
+      float y0[8], y2[8], dh[8], d0[8], d2[8], hh[8];
+      staged8(c.lds0, nl, g, y0);
+      staged8(c.lds1, nl, g, y2);
+      load8(dhb + (int64_t)tok * I + m, dh);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < 8; ++u) {
         const float sg = sigmoidf_(y0[u]);
         const float sw = sg * y0[u];
         d0[u] = sg * y2[u] * dh[u] * (1.0f + y0[u] * (1.0f - sg)) * l0;
@@ -164,12 +250,12 @@ struct EpiS1 {
         hh[u] = sw * y2[u] * l1;
       }
       if (ea.token_major) {
-        store4(dyb, I2, tok, m, d0[0], d0[1], d0[2], d0[3]);
-        store4(dyb, I2, tok, I + m, d2[0], d2[1], d2[2], d2[3]);
-        store4(hb, I, tok, m, hh[0], hh[1], hh[2], hh[3]);
+        store8(dyb + (int64_t)tok * I2 + m, d0);
+        store8(dyb + (int64_t)tok * I2 + I + m, d2);
+        store8(hb + (int64_t)tok * I + m, hh);
       } else {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < 8; ++u) {
           dyb[(int64_t)(m + u) * ea.N + tok] = f32_to_bf16(d0[u]);
           dyb[(int64_t)(I + m + u) * ea.N + tok] = f32_to_bf16(d2[u]);
           hb[(int64_t)(m + u) * ea.N + tok] = f32_to_bf16(hh[u]);
@@ -198,90 +284,70 @@ struct EpiBwd {
   };
   __device__ __forceinline__ static void apply(const Args& ea, const f32x16 (&acc0)[2][kNB],
                                const f32x16 (&acc1)[2][kNB], const TileCtx& c, bool) {
-    __shared__ float red[3][2][kBRows];
     const int I = ea.I, I2 = 2 * I;
     const int64_t bo2 = (int64_t)c.b * ea.N * I2, bo1 = (int64_t)c.b * ea.N * I;
-    // per-lane partial lr sums for the two token columns j = 0, 1 of this lane
-    float s[3][kNB] = {};
-    float L[kNB][3];
-    int tokj[kNB];
-    bool nv[kNB];
-    static_for<kNB>([&](auto jj) __attribute__((always_inline)) {
-      constexpr int j = jj;
-      const int n = c.wn * 128 + j * 32 + acc_col();
-      nv[j] = c.tt.n0 + n < c.tt.size;
-      tokj[j] = c.tt.start + c.tt.n0 + n;
-      L[j][0] = L[j][1] = L[j][2] = 0.f;
-      if (nv[j]) {
-        const int64_t li = (int64_t)c.b * ea.N + tokj[j];
-        L[j][0] = LR::load(ea.lr0[li]);
-        L[j][1] = LR::load(ea.lr1[li]);
-        L[j][2] = LR::load(ea.lr2[li]);
+    const int64_t plane = (int64_t)ea.m_tiles * ea.B * ea.N;
+    staged_epilogue(acc0, acc1, c, [&](int nl, int n, int g) __attribute__((always_inline)) {
+      const int m = c.m0 + 8 * g;
+      const bool ok = c.tt.n0 + n < c.tt.size && m < I;
+      const int tok = c.tt.start + c.tt.n0 + n;
+      float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f;
+      if (ok) {
+        const int64_t li = (int64_t)c.b * ea.N + tok;
+        const float L0 = LR::load(ea.lr0[li]);
+        const float L1 = LR::load(ea.lr1[li]);
+        const float L2 = LR::load(ea.lr2[li]);
+        float x0[8], x2[8], gd0[8], gd2[8], dh[8], gd[8];
+        staged8(c.lds0, nl, g, x0);
+        staged8(c.lds1, nl, g, x2);
+        const int64_t r2 = bo2 + (int64_t)tok * I2, r1 = bo1 + (int64_t)tok * I;
+        load8(ea.gy + r2 + m, gd0);
+        load8(ea.gy + r2 + I + m, gd2);
+        load8(ea.dhg + r2 + m, dh);
+        load8(ea.dhg + r2 + I + m, gd);
+        float o_gdh[8], o_gx0[8], o_gx2[8], o_dx0[8], o_dx2[8], o_hl[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const float y0 = bf16r(x0[u]);
+          const float y2 = bf16r(x2[u]);
+          const float sg = sigmoidf_(y0);
+          const float silu = sg * y0;
+          const float mul = sg * (1.0f + y0 * (1.0f - sg));  // silu'(y0)
+          const float ds = sg * (1.0f - sg);                  // sigmoid'(y0)
+          o_gdh[u] = gd0[u] * L0 * y2 * mul + gd2[u] * L2 * silu;
+          o_gx2[u] = gd0[u] * L0 * dh[u] * mul + gd[u] * L1 * silu;
+          const float gsig = gd0[u] * L0 * dh[u] * y2 * (1.0f + y0 - 2.0f * sg * y0);
+          o_gx0[u] = (gd2[u] * L2 * dh[u] + gd[u] * L1 * y2) * mul +
+                     gd0[u] * L0 * dh[u] * y2 * ds + gsig * ds;
+          s0 += gd0[u] * dh[u] * y2 * mul;
+          s1 += gd[u] * y2 * silu;
+          s2 += gd2[u] * dh[u] * silu;
+          o_dx0[u] = dh[u] * y2 * mul * L0;
+          o_dx2[u] = silu * dh[u] * L2;
+          o_hl[u] = L1 * y2 * silu;
+        }
+        store8(ea.gdh + r1 + m, o_gdh);
+        store8(ea.gx + r2 + m, o_gx0);
+        store8(ea.gx + r2 + I + m, o_gx2);
+        store8(ea.dx + r2 + m, o_dx0);
+        store8(ea.dx + r2 + I + m, o_dx2);
+        store8(ea.hlr + r1 + m, o_hl);
+      }
+      // the 16 lanes of one token hold its 128 rows: sum them for this tile's
+      // lr-gradient partial
+#pragma unroll
+      for (int d = 8; d > 0; d >>= 1) {
+        s0 += __shfl_xor(s0, d, 16);
+        s1 += __shfl_xor(s1, d, 16);
+        s2 += __shfl_xor(s2, d, 16);
+      }
+      if (g == 0 && c.tt.n0 + n < c.tt.size) {
+        const int64_t o = ((int64_t)c.mt * ea.B + c.b) * ea.N + tok;
+        ea.lr_part[o] = s0;
+        ea.lr_part[plane + o] = s1;
+        ea.lr_part[2 * plane + o] = s2;
       }
     });
-    static_for<2 * kNB * 4>([&](auto idx) __attribute__((always_inline)) {
-      constexpr int i = idx / (kNB * 4);
-      constexpr int j = (idx / 4) % kNB;
-      constexpr int q = idx % 4;
-      const int m = c.m0 + c.wm * 64 + i * 32 + acc_row(q * 4);
-      if (!nv[j] || m >= I) return;
-      const int tok = tokj[j];
-      const float L0 = L[j][0], L1 = L[j][1], L2 = L[j][2];
-      float gd0[4], gd2[4], dh[4], gd[4];
-      load4(ea.gy + bo2, I2, tok, m, gd0);
-      load4(ea.gy + bo2, I2, tok, I + m, gd2);
-      load4(ea.dhg + bo2, I2, tok, m, dh);
-      load4(ea.dhg + bo2, I2, tok, I + m, gd);
-      float o_gdh[4], o_gx0[4], o_gx2[4], o_dx0[4], o_dx2[4], o_hl[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const float x0 = bf16r(acc0[i][j][q * 4 + u]);
-        const float x2 = bf16r(acc1[i][j][q * 4 + u]);
-        const float sg = sigmoidf_(x0);
-        const float silu = sg * x0;
-        const float mul = sg * (1.0f + x0 * (1.0f - sg));  // silu'(x0)
-        const float ds = sg * (1.0f - sg);                  // sigmoid'(x0)
-        o_gdh[u] = gd0[u] * L0 * x2 * mul + gd2[u] * L2 * silu;
-        o_gx2[u] = gd0[u] * L0 * dh[u] * mul + gd[u] * L1 * silu;
-        const float gsig = gd0[u] * L0 * dh[u] * x2 * (1.0f + x0 - 2.0f * sg * x0);
-        o_gx0[u] = (gd2[u] * L2 * dh[u] + gd[u] * L1 * x2) * mul +
-                   gd0[u] * L0 * dh[u] * x2 * ds + gsig * ds;
-        s[0][j] += gd0[u] * dh[u] * x2 * mul;
-        s[1][j] += gd[u] * x2 * silu;
-        s[2][j] += gd2[u] * dh[u] * silu;
-        o_dx0[u] = dh[u] * x2 * mul * L0;
-        o_dx2[u] = silu * dh[u] * L2;
-        o_hl[u] = L1 * x2 * silu;
-      }
-      store4(ea.gdh + bo1, I, tok, m, o_gdh[0], o_gdh[1], o_gdh[2], o_gdh[3]);
-      store4(ea.gx + bo2, I2, tok, m, o_gx0[0], o_gx0[1], o_gx0[2], o_gx0[3]);
-      store4(ea.gx + bo2, I2, tok, I + m, o_gx2[0], o_gx2[1], o_gx2[2], o_gx2[3]);
-      store4(ea.dx + bo2, I2, tok, m, o_dx0[0], o_dx0[1], o_dx0[2], o_dx0[3]);
-      store4(ea.dx + bo2, I2, tok, I + m, o_dx2[0], o_dx2[1], o_dx2[2], o_dx2[3]);
-      store4(ea.hlr + bo1, I, tok, m, o_hl[0], o_hl[1], o_hl[2], o_hl[3]);
-    });
-    // lanes l and l^32 hold the same token column (other rows); then the two
-    // waves of one column half (wm = 0, 1) meet in LDS
-#pragma unroll
-    for (int k = 0; k < 3; ++k)
-#pragma unroll
-      for (int j = 0; j < kNB; ++j) s[k][j] += __shfl_xor(s[k][j], 32, 64);
-    if ((threadIdx.x & 63) < 32) {
-#pragma unroll
-      for (int k = 0; k < 3; ++k)
-#pragma unroll
-        for (int j = 0; j < kNB; ++j) red[k][c.wm][c.wn * 128 + j * 32 + acc_col()] = s[k][j];
-    }
-    __syncthreads();
-    if (threadIdx.x < kBRows) {
-      const int n = threadIdx.x;
-      if (c.tt.n0 + n < c.tt.size) {
-        const int64_t plane = (int64_t)ea.m_tiles * ea.B * ea.N;
-        const int64_t o = ((int64_t)c.mt * ea.B + c.b) * ea.N + c.tt.start + c.tt.n0 + n;
-#pragma unroll
-        for (int k = 0; k < 3; ++k) ea.lr_part[k * plane + o] = red[k][0][n] + red[k][1][n];
-      }
-    }
   }
 };
 
@@ -322,32 +388,41 @@ __global__ __launch_bounds__(kThreads) void tn_kernel(TnArgs a, typename Epi::Ar
   la1.init(A01, r1);
   lx0.init(X0, tt.n0);
   lx1.init(X0, tt.n0 + kTileRows);
-  auto load = [&](int kt, uint8_t* st) {
-    if (kt == nk0) {  // switch to the second operand pair (chained K)
+  const uint8_t* sb[4];
+  int lstep = 0;
+  auto prep = [&](int kt) __attribute__((always_inline)) -> bool {
+    if (nk1 > 0 && kt == nk0) {  // switch to the second operand pair (chained K)
       la0.init(A10, r0);
       la1.init(A11, r1);
       lx0.init(X1, tt.n0);
       lx1.init(X1, tt.n0 + kTileRows);
     }
-    const int step = kt < nk0 ? kt : kt - nk0;
-    la0.load(step, st);
-    la1.load(step, st + kTileBytes);
-    lx0.load(step, st + 2 * kTileBytes);
-    lx1.load(step, st + 3 * kTileBytes);
+    lstep = nk1 > 0 && kt >= nk0 ? kt - nk0 : kt;
+    sb[0] = la0.step_base(lstep);
+    sb[1] = la1.step_base(lstep);
+    sb[2] = lx0.step_base(lstep);
+    sb[3] = lx1.step_base(lstep);
+    return la0.tail(lstep);  // A and X share the pair's K
+  };
+  auto issue = [&](auto p, auto masked, uint8_t* st) __attribute__((always_inline)) {
+    constexpr int tile = decltype(p)::value / kLoadsPerTile;
+    constexpr int t = decltype(p)::value % kLoadsPerTile;
+    constexpr bool M = decltype(masked)::value;
+    if constexpr (tile == 0) la0.template issue<M>(sb[0], lstep, t, st);
+    else if constexpr (tile == 1) la1.template issue<M>(sb[1], lstep, t, st + kTileBytes);
+    else if constexpr (tile == 2) lx0.template issue<M>(sb[2], lstep, t, st + 2 * kTileBytes);
+    else lx1.template issue<M>(sb[3], lstep, t, st + 3 * kTileBytes);
   };
   const int w = threadIdx.x >> 6;
   const int wm = w >> 1, wn = w & 1;
-  // K-major operands use the compiler's LDS reads; a row-major A needs the
-  // transposing reads, issued as inline asm (see run_pipeline)
-  constexpr bool kAsmReads = AMAJ == RMajor;
   auto read = [&](const uint8_t* st, int ks, HalfFrags& f) __attribute__((always_inline)) {
-    read_half<AMAJ, KMajor, kAsmReads>(f, st, ks, wm, wn);
+    read_half<AMAJ, KMajor, true>(f, st, ks, wm, wn);
   };
-  auto mma = [&](const HalfFrags& f) __attribute__((always_inline)) { mma_half(acc0, acc1, f); };
   (void)two;
-  run_pipeline<kAsmReads ? kAsm : kOverlap, half_lds_ops<AMAJ, KMajor>()>(
-      nk0 + nk1, load, read, mma, st0, st1, st2, st3);
-  const TileCtx c{b, m0, wm, wn, mt, tt};
+  run_pipeline<half_lds_ops<AMAJ, KMajor>()>(nk0 + nk1, prep, issue, read, acc0, acc1, st0, st1,
+                                              st2, st3);
+  const TileCtx c{b, m0, wm, wn, mt, tt, reinterpret_cast<float*>(st0),
+                  reinterpret_cast<float*>(st1)};
   Epi::apply(ea, acc0, acc1, c, two);
 }
 
@@ -398,20 +473,32 @@ __global__ __launch_bounds__(kThreads) void wg_kernel(WgTask t0, WgTask t1,
   lp1.init(P, y0 + kTileRows);
   lq0.init(Q, x0);
   lq1.init(Q, x0 + kTileRows);
-  auto load = [&](int kt, uint8_t* st) {
-    lp0.load(kt, st);
-    lp1.load(kt, st + kTileBytes);
-    lq0.load(kt, st + 2 * kTileBytes);
-    lq1.load(kt, st + 3 * kTileBytes);
+  const uint8_t* sb[4];
+  int lstep = 0;
+  auto prep = [&](int kt) __attribute__((always_inline)) -> bool {
+    lstep = kt;
+    sb[0] = lp0.step_base(kt);
+    sb[1] = lp1.step_base(kt);
+    sb[2] = lq0.step_base(kt);
+    sb[3] = lq1.step_base(kt);
+    return lp0.tail(kt);
+  };
+  auto issue = [&](auto p, auto masked, uint8_t* st) __attribute__((always_inline)) {
+    constexpr int tile = decltype(p)::value / kLoadsPerTile;
+    constexpr int t = decltype(p)::value % kLoadsPerTile;
+    constexpr bool M = decltype(masked)::value;
+    if constexpr (tile == 0) lp0.template issue<M>(sb[0], lstep, t, st);
+    else if constexpr (tile == 1) lp1.template issue<M>(sb[1], lstep, t, st + kTileBytes);
+    else if constexpr (tile == 2) lq0.template issue<M>(sb[2], lstep, t, st + 2 * kTileBytes);
+    else lq1.template issue<M>(sb[3], lstep, t, st + 3 * kTileBytes);
   };
   const int w = threadIdx.x >> 6;
   const int wm = w >> 1, wn = w & 1;
   auto read = [&](const uint8_t* st, int ks, HalfFrags& f) __attribute__((always_inline)) {
     read_half<RMajor, RMajor, true>(f, st, ks, wm, wn);
   };
-  auto mma = [&](const HalfFrags& f) __attribute__((always_inline)) { mma_half(acc0, acc1, f); };
-  run_pipeline<kAsm, half_lds_ops<RMajor, RMajor>()>((size + kBK - 1) / kBK, load, read, mma,
-                                                     st0, st1, st2, st3);
+  run_pipeline<half_lds_ops<RMajor, RMajor>()>((size + kBK - 1) / kBK, prep, issue, read, acc0,
+                                               acc1, st0, st1, st2, st3);
 
   uint16_t* ob = tk.out + ((int64_t)b * E + e) * X * Y;
   for_quads(acc0, acc1, wm, wn, true, [&](int tt, int r, int n, const float* v) __attribute__((always_inline)) {
