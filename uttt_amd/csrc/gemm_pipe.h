@@ -10,8 +10,8 @@
 // accumulate), i.e. 16 MFMAs per 8 fragment reads.
 //
 // Global -> LDS: global_load_lds_dwordx4 (16 bytes per lane straight into LDS,
-// no register staging) into a ring of four 32 KiB stages, so the loads of
-// steps k+1..k+3 are in flight while step k is multiplied; the only waits are
+// no register staging) into a ring of five 32 KiB stages (all 160 KiB of LDS),
+// so the loads of steps k+1..k+4 are in flight while step k is multiplied; the only waits are
 // explicit s_waitcnt vmcnt counts and one s_barrier per step.  Each stage lives
 // in its own __shared__ array so the compiler can tell the in-flight LDS
 // writes from the LDS reads of the current stage.
@@ -47,9 +47,11 @@ constexpr int kTileRows = 128;                                   // rows per LDS
 constexpr int kBRows = 2 * kTileRows;                            // B rows per workgroup
 constexpr int kTileBytes = kTileRows * kBK * 2;                  // 8 KiB
 constexpr int kStageBytes = 4 * kTileBytes;                      // A0 | A1 | B0 | B1
+constexpr int kStages = 5;                                       // LDS ring: 160 KiB
 constexpr int kLoadsPerTile = kTileBytes / 16 / kThreads;        // 2 per thread
 constexpr int kLoadsPerStage = 4 * kLoadsPerTile;                // 8 per wave
 constexpr int kNB = 4;                                           // 32-col blocks per wave
+constexpr int kXcds = 8;                                         // MI355X: 8 XCDs, 32 CUs each
 
 enum Major { KMajor = 0, RMajor = 1 };
 
@@ -348,8 +350,10 @@ __device__ __forceinline__ void mma_half(f32x16 (&acc0)[2][kNB], f32x16 (&acc1)[
   });
 }
 
-// The K loop: a ring of four LDS stages; the loads of step kt+4 are issued
-// during step kt, so three steps are in flight while one is multiplied.
+// The K loop: a ring of kStages LDS stages; the loads of step kt+kStages are
+// issued during step kt, so kStages-1 steps are in flight while one is
+// multiplied (four stages, 128 KiB, cover the L2-miss latency seen under
+// load; three did not).
 //   prep(kt)                 readies the loads of step kt (operand switch,
 //                            per-step scalar bases) and returns whether they
 //                            need the masked (K tail) form
@@ -358,11 +362,11 @@ __device__ __forceinline__ void mma_half(f32x16 (&acc0)[2][kNB], f32x16 (&acc1)[
 //   read(stage, ks, frags)   the fragment reads of k-substep ks, inline asm,
 //                            NLDS LDS instructions
 // Step kt (stage cur, next stage nxt):
-//   read (kt, 1) -> f1;  prep(kt + 4);  wait for f0;  MFMAs of f0
+//   read (kt, 1) -> f1;  prep(kt + kStages);  wait for f0;  MFMAs of f0
 //   wait for this wave's loads of stage kt+1 and for f1, barrier (stage kt+1
 //   has landed for every wave, and every wave is done reading stage kt)
-//   read (kt+1, 0) -> f0;  MFMAs of f1 with the loads of step kt+4 into
-//   stage cur interleaved between them
+//   read (kt+1, 0) -> f0;  MFMAs of f1 with the loads of step kt+kStages
+//   into stage cur interleaved between them
 // so with one wave per SIMD the matrix core is fed while the next fragments
 // and the next stage arrive.  The fragment reads are inline asm because the
 // compiler's wait-count pass cannot tell them from the in-flight LDS-DMA
@@ -373,8 +377,7 @@ __device__ __forceinline__ void mma_half(f32x16 (&acc0)[2][kNB], f32x16 (&acc1)[
 template <int NLDS, class PrepFn, class IssueFn, class ReadFn>
 __device__ __forceinline__ void run_pipeline(int nk, PrepFn&& prep, IssueFn&& issue, ReadFn&& read,
                                              f32x16 (&acc0)[2][kNB], f32x16 (&acc1)[2][kNB],
-                                             uint8_t* s0, uint8_t* s1, uint8_t* s2,
-                                             uint8_t* s3) {
+                                             uint8_t* const (&ring)[kStages]) {
   if (nk <= 0) return;
   constexpr int kW = NLDS < 15 ? NLDS : 15;
   HalfFrags f0, f1;
@@ -388,20 +391,17 @@ __device__ __forceinline__ void run_pipeline(int nk, PrepFn&& prep, IssueFn&& is
         issue(p, std::false_type{}, st);
       });
   };
-  load_all(0, s0);
-  load_all(1, s1);
-  load_all(2, s2);
-  load_all(3, s3);
-  wait_vmcnt<3 * kLoadsPerStage>();
+  static_for<kStages>([&](auto i) __attribute__((always_inline)) { load_all(i, ring[i]); });
+  wait_vmcnt<(kStages - 1) * kLoadsPerStage>();
   block_barrier();
-  read(s0, 0, f0);
+  read(ring[0], 0, f0);
   auto step = [&](int kt, uint8_t* cur, const uint8_t* nxt) __attribute__((always_inline)) {
     read(cur, 1, f1);
-    const bool masked = prep(kt + 4);
+    const bool masked = prep(kt + kStages);
     lgkm_wait_tied<kW>(f0);
     mma_half(acc0, acc1, f0);
     __builtin_amdgcn_sched_barrier(0);
-    wait_vmcnt<2 * kLoadsPerStage>();
+    wait_vmcnt<(kStages - 2) * kLoadsPerStage>();
     lgkm_wait_tied<0>(f1);
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
@@ -420,15 +420,13 @@ __device__ __forceinline__ void run_pipeline(int nk, PrepFn&& prep, IssueFn&& is
     __builtin_amdgcn_sched_barrier(0);
   };
   int kt = 0;
-  for (; kt + 4 <= nk; kt += 4) {
-    step(kt, s0, s1);
-    step(kt + 1, s1, s2);
-    step(kt + 2, s2, s3);
-    step(kt + 3, s3, s0);
-  }
-  if (kt < nk) step(kt, s0, s1);
-  if (kt + 1 < nk) step(kt + 1, s1, s2);
-  if (kt + 2 < nk) step(kt + 2, s2, s3);
+  for (; kt + kStages <= nk; kt += kStages)
+    static_for<kStages>([&](auto i) __attribute__((always_inline)) {
+      step(kt + i, ring[i], ring[(i + 1) % kStages]);
+    });
+  static_for<kStages - 1>([&](auto i) __attribute__((always_inline)) {
+    if (kt + i < nk) step(kt + i, ring[i], ring[(i + 1) % kStages]);
+  });
   lgkm_wait_tied<0>(f0);  // the reads of the stage past the end
   wait_vmcnt<0>();        // and the loads issued past the end
 }

@@ -36,7 +36,9 @@ struct TnArgs {
   int row_off[2];           // [tile] first A row of the tile = m0 + row_off
   int row_end[2];           // [tile] valid A rows are < row_end
   int m_step, m_tiles, n_tiles_ub;
-  int E, N;
+  int gm, gn, n_super_m;    // XCD super-tiles: gm m-tiles x gn n-tiles (see tn_kernel);
+                            // gm = 0: plain order (m-tile fastest)
+  int B, E, N;
   int two;                  // tile 1 multiplied
   const int32_t* gs;
 };
@@ -357,13 +359,34 @@ __global__ __launch_bounds__(kThreads) void tn_kernel(TnArgs a, typename Epi::Ar
   __shared__ __attribute__((aligned(16))) uint8_t st1[kStageBytes];
   __shared__ __attribute__((aligned(16))) uint8_t st2[kStageBytes];
   __shared__ __attribute__((aligned(16))) uint8_t st3[kStageBytes];
-  __shared__ int scratch[4];
+  __shared__ __attribute__((aligned(16))) uint8_t st4[kStageBytes];
+  // the tile lookup's 4 ints live in the last stage: it is done before any load
+  int* scratch = reinterpret_cast<int*>(st4);
 
+  // Tile order: workgroup i runs on XCD i % kXcds, each XCD with its own L2.
+  // The (m-tile, n-tile) plane (n-tiles of all batches in a row) is cut into
+  // gm x gn super-tiles and each XCD takes whole ones, so the ~32 workgroups
+  // an XCD runs at once share gm A slices and gn B slices per K step in its
+  // L2 instead of fetching the B tile once per XCD.
+  // Small grids (a few rounds of workgroups) keep the plain order, which
+  // spreads the work evenly over the XCDs.
   const int bid = blockIdx.x;
-  const int mt = bid % a.m_tiles;
-  const int nt = (bid / a.m_tiles) % a.n_tiles_ub;
-  const int b = bid / (a.m_tiles * a.n_tiles_ub);
+  int mt, ntg;
+  if (a.gm > 0) {
+    const int xcd = bid % kXcds, loc = bid / kXcds;
+    const int per = a.gm * a.gn;
+    const int sup = (loc / per) * kXcds + xcd;
+    const int p = loc % per;
+    mt = (sup % a.n_super_m) * a.gm + p % a.gm;
+    ntg = (sup / a.n_super_m) * a.gn + p / a.gm;
+  } else {
+    mt = bid % a.m_tiles;
+    ntg = bid / a.m_tiles;
+  }
+  if (mt >= a.m_tiles || ntg >= a.B * a.n_tiles_ub) return;  // padding of the super-tile grid
+  const int b = ntg / a.n_tiles_ub, nt = ntg % a.n_tiles_ub;
   const TokenTile tt = find_token_tile<kBRows>(a.gs + (int64_t)b * a.E, a.E, a.N, nt, scratch);
+  __syncthreads();  // every wave has read the lookup before stage 4 is loaded
   if (tt.e < 0) return;
   const int m0 = mt * a.m_step;
 
@@ -419,8 +442,8 @@ __global__ __launch_bounds__(kThreads) void tn_kernel(TnArgs a, typename Epi::Ar
     read_half<AMAJ, KMajor, true>(f, st, ks, wm, wn);
   };
   (void)two;
-  run_pipeline<half_lds_ops<AMAJ, KMajor>()>(nk0 + nk1, prep, issue, read, acc0, acc1, st0, st1,
-                                              st2, st3);
+  uint8_t* const ring[kStages] = {st0, st1, st2, st3, st4};
+  run_pipeline<half_lds_ops<AMAJ, KMajor>()>(nk0 + nk1, prep, issue, read, acc0, acc1, ring);
   const TileCtx c{b, m0, wm, wn, mt, tt, reinterpret_cast<float*>(st0),
                   reinterpret_cast<float*>(st1)};
   Epi::apply(ea, acc0, acc1, c, two);
@@ -446,6 +469,7 @@ __global__ __launch_bounds__(kThreads) void wg_kernel(WgTask t0, WgTask t1,
   __shared__ __attribute__((aligned(16))) uint8_t st1[kStageBytes];
   __shared__ __attribute__((aligned(16))) uint8_t st2[kStageBytes];
   __shared__ __attribute__((aligned(16))) uint8_t st3[kStageBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t st4[kStageBytes];
 
   const int n0_tiles = t0.y_tiles * t0.x_tiles;
   const int per_group = n0_tiles + t1.y_tiles * t1.x_tiles;
@@ -497,8 +521,9 @@ __global__ __launch_bounds__(kThreads) void wg_kernel(WgTask t0, WgTask t1,
   auto read = [&](const uint8_t* st, int ks, HalfFrags& f) __attribute__((always_inline)) {
     read_half<RMajor, RMajor, true>(f, st, ks, wm, wn);
   };
+  uint8_t* const ring[kStages] = {st0, st1, st2, st3, st4};
   run_pipeline<half_lds_ops<RMajor, RMajor>()>((size + kBK - 1) / kBK, prep, issue, read, acc0,
-                                               acc1, st0, st1, st2, st3);
+                                               acc1, ring);
 
   uint16_t* ob = tk.out + ((int64_t)b * E + e) * X * Y;
   for_quads(acc0, acc1, wm, wn, true, [&](int tt, int r, int n, const float* v) __attribute__((always_inline)) {
@@ -605,11 +630,44 @@ TnArgs tn_args(const void* a0, const void* a1, const void* x, int K, int64_t lda
   return t;
 }
 
+// Grids from this many tiles up (8 rounds of one workgroup per CU) take the
+// XCD super-tile order.
+constexpr int64_t kXcdMapMinTiles = 8 * 256;
+
+// Super-tile shape for m_tiles m-tiles: gm x gn with gm * gn <= 32 (one
+// workgroup per CU of an XCD), minimising the slices fetched per tile,
+// (gm + gn) / (gm gn), times the m padding.
+void super_tile(int m_tiles, int* gm, int* gn) {
+  double best = 1e30;
+  for (int m = 1; m <= 8 && m <= m_tiles; ++m) {
+    const int n = 32 / m;
+    const double pad = (double)((m_tiles + m - 1) / m * m) / m_tiles;
+    const double score = (double)(m + n) / (m * n) * pad;
+    if (score < best - 1e-9) {
+      best = score;
+      *gm = m;
+      *gn = n;
+    }
+  }
+}
+
 template <int AMAJ, class Epi>
-int launch_tn(const TnArgs& t, const typename Epi::Args& ea, int B, hipStream_t st,
+int launch_tn(TnArgs t, const typename Epi::Args& ea, int B, hipStream_t st,
               const char* what) {
-  const int64_t blocks = (int64_t)t.m_tiles * t.n_tiles_ub * B;
-  if (blocks == 0) return UTTT_OK;
+  const int64_t tiles = (int64_t)t.m_tiles * t.n_tiles_ub * B;
+  if (tiles == 0) return UTTT_OK;
+  t.B = B;
+  int64_t blocks = tiles;
+  if (tiles >= kXcdMapMinTiles) {
+    super_tile(t.m_tiles, &t.gm, &t.gn);
+    t.n_super_m = (t.m_tiles + t.gm - 1) / t.gm;
+    const int64_t n_super_n = ((int64_t)B * t.n_tiles_ub + t.gn - 1) / t.gn;
+    const int64_t supers = (t.n_super_m * n_super_n + kXcds - 1) / kXcds * kXcds;
+    blocks = supers * t.gm * t.gn;
+  } else {
+    t.gm = t.gn = 0;
+    t.n_super_m = 1;
+  }
   if (int rc = check_grid(blocks, what)) return rc;
   hipLaunchKernelGGL((tn_kernel<AMAJ, Epi>), dim3((unsigned)blocks), dim3(kThreads), 0, st, t, ea);
   return check_launch(what);
