@@ -531,7 +531,11 @@ __device__ __forceinline__ void expert_segment(const int32_t* __restrict__ gs_b,
   *size = g;
 }
 
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
+// Logistic sigmoid with the hardware exp and reciprocal (about 1 ulp of fp32
+// each, far below the bf16 resolution of every output built from it).
+__device__ __forceinline__ float sigmoidf_(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __expf(-x));
+}
 __device__ __forceinline__ float bf16r(float x) { return bf16_to_f32(f32_to_bf16(x)); }
 
 // Four consecutive-row results (rows m..m+3 of token column n) as one store
@@ -539,8 +543,8 @@ __device__ __forceinline__ float bf16r(float x) { return bf16_to_f32(f32_to_bf16
 __device__ __forceinline__ void store4(uint16_t* out, int64_t ld, int64_t n, int m, float a,
                                        float b, float c, float d) {
   uint2 w;
-  w.x = (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
-  w.y = (uint32_t)f32_to_bf16(c) | ((uint32_t)f32_to_bf16(d) << 16);
+  w.x = pack_bf16x2(a, b);
+  w.y = pack_bf16x2(c, d);
   *reinterpret_cast<uint2*>(out + n * ld + m) = w;
 }
 __device__ __forceinline__ void store4(float* out, int64_t ld, int64_t n, int m, float a, float b,
