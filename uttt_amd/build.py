@@ -11,6 +11,7 @@ from __future__ import annotations
 import concurrent.futures as cf
 import glob
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -33,13 +34,40 @@ COMMON_FLAGS = [
 ]
 
 
+# Sources whose kernels must not use scratch memory: the grouped GEMMs issue
+# their LDS fragment reads as inline asm with explicit waits, so a register
+# spill between a read and its wait would save the value from before the read.
+NO_SCRATCH = {"grouped_gemm.hip"}
+
+
+def _scratch_kernels(remarks: str) -> list:
+    """Kernels with a nonzero ScratchSize in hipcc's resource-usage remarks."""
+    bad, name = [], None
+    for line in remarks.splitlines():
+        m = re.search(r"Function Name: (\S+)", line)
+        if m:
+            name = m.group(1)
+            continue
+        m = re.search(r"ScratchSize \[bytes/lane\]: (\d+)", line)
+        if m and name and int(m.group(1)) > 0:
+            bad.append(f"{name} ({m.group(1)} bytes/lane)")
+    return bad
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD_DIR, os.path.basename(src).replace(".hip", ".o"))
     cmd = [HIPCC, *COMMON_FLAGS, "-c", src, "-o", obj]
+    guard = os.path.basename(src) in NO_SCRATCH
+    if guard:
+        cmd.append("-Rpass-analysis=kernel-resource-usage")
     proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     out = "\n".join(l for l in proc.stdout.splitlines() if "packed-fp32-ops" not in l)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{out}")
+    if guard:
+        bad = _scratch_kernels(proc.stdout)
+        if bad:
+            raise RuntimeError(f"{src}: kernels spill to scratch memory: {', '.join(bad)}")
     return obj
 
 

@@ -1,26 +1,26 @@
 // Asynchronous MFMA GEMM pipeline for gfx950 (the core of every grouped
 // fast-weight GEMM).
 //
-// Workgroup: 256 threads = 4 waves in a 2x2 grid.  Per K step of kBK = 32 a
+// Workgroup: 256 threads = 4 waves in a 2x2 grid.  Per K step of kBK = 64 a
 // workgroup multiplies two 128-row A tiles (A0, A1) by a 256-row B tile (two
 // 128-row halves B0, B1) into two fp32 accumulators acc0 = A0 B^T and
 // acc1 = A1 B^T (each 128 x 256).  Wave (wm, wn) owns rows [64 wm, 64 wm + 64)
 // of both accumulators and columns [128 wn, 128 wn + 128): 2 x 4 blocks of
 // 32x32 per accumulator, each fed by v_mfma_f32_32x32x16_bf16 (fp32
-// accumulate), i.e. 16 MFMAs per 8 fragment reads.
+// accumulate): per k-substep of 16, 16 MFMAs per 8 fragment reads.
 //
 // Global -> LDS: global_load_lds_dwordx4 (16 bytes per lane straight into LDS,
-// no register staging) into a ring of five 32 KiB stages (all 160 KiB of LDS),
-// so the loads of steps k+1..k+4 are in flight while step k is multiplied; the only waits are
+// no register staging) into two 64 KiB stages (kBK = 64), the loads of stage
+// k+1 in flight while stage k is multiplied; the only waits are
 // explicit s_waitcnt vmcnt counts and one s_barrier per step.  Each stage lives
 // in its own __shared__ array so the compiler can tell the in-flight LDS
 // writes from the LDS reads of the current stage.
 //
 // LDS tile layouts (16-byte chunks, XOR-swizzled against bank conflicts):
-//   KMajor tile (operand stored [rows][K], K contiguous): 128 rows x 4 chunks;
-//     chunk c of row r sits at slot r*4 + (c ^ kswz(r)).  Fragments are one
+//   KMajor tile (operand stored [rows][K], K contiguous): 128 rows x 8 chunks;
+//     chunk c of row r sits at slot r*8 + (c ^ kswz(r)).  Fragments are one
 //     ds_read_b128 (8 consecutive k of one row).
-//   RMajor tile (operand stored [K][rows], rows contiguous): 32 k-rows x 16
+//   RMajor tile (operand stored [K][rows], rows contiguous): 64 k-rows x 16
 //     chunks; chunk c of k-row k sits at slot k*16 + (c ^ rswz(k)).  Fragments
 //     are two ds_read_b64_tr_b16: within a group of 16 lanes, source lane
 //     s = 4j + q reads k-row j, rows 4q..4q+3, and the hardware hands lane i
@@ -42,18 +42,34 @@ typedef short i16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kThreads = 256;
-constexpr int kBK = 32;
+constexpr int kBK = 64;
 constexpr int kTileRows = 128;                                   // rows per LDS tile
 constexpr int kBRows = 2 * kTileRows;                            // B rows per workgroup
-constexpr int kTileBytes = kTileRows * kBK * 2;                  // 8 KiB
+constexpr int kTileBytes = kTileRows * kBK * 2;                  // 16 KiB
 constexpr int kStageBytes = 4 * kTileBytes;                      // A0 | A1 | B0 | B1
-constexpr int kStages = 5;                                       // LDS ring: 160 KiB
-constexpr int kLoadsPerTile = kTileBytes / 16 / kThreads;        // 2 per thread
-constexpr int kLoadsPerStage = 4 * kLoadsPerTile;                // 8 per wave
+constexpr int kStages = 2;                                       // LDS ring: 128 KiB
+constexpr int kChunks = kBK / 8;                                 // 16-byte chunks per KMajor row
+constexpr int kSubsteps = kBK / 16;                              // MFMA k-substeps per stage
+constexpr int kLoadsPerTile = kTileBytes / 16 / kThreads;        // 4 per thread
+constexpr int kLoadsPerStage = 4 * kLoadsPerTile;                // 16 per wave
 constexpr int kNB = 4;                                           // 32-col blocks per wave
 constexpr int kXcds = 8;                                         // MI355X: 8 XCDs, 32 CUs each
 
 enum Major { KMajor = 0, RMajor = 1 };
+
+// f(std::integral_constant<int, i>) for i = 0 .. N-1 with compile-time i, so
+// that accumulator indices stay constants whatever the unroller decides (a
+// runtime index would move the accumulator arrays to scratch memory).
+template <class F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+
 
 // 16 zero bytes (zero-initialised device memory, never written): the source
 // of every masked-off lane of a tile load.
@@ -100,13 +116,13 @@ struct Operand {
 };
 
 // Swizzles.  A 16-lane group of ds_read_b128 reads 16 consecutive rows of one
-// logical chunk; rows are 64 bytes, so row r sits in quarter (r & 3) of a
-// 256-byte bank line and the 4 rows sharing a quarter must use 4 different
-// chunk slots: slot = c ^ ((r >> 2) & 3).  A 32-lane half of
-// ds_read_b64_tr_b16 reads 4 k-rows x 4 chunks (a 64-byte aligned block) of
-// 256-byte rows; XOR with 4 * (k & 3) sends the 4 k-rows to 4 different
-// 64-byte blocks of the bank line.
-__device__ __forceinline__ int kswz(int r) { return (r >> 2) & 3; }
+// logical chunk; KMajor rows are 128 bytes (one cache line of the operand), so
+// row r sits in half (r & 1) of a 256-byte bank line and the 8 rows sharing a
+// half must use 8 different chunk slots: slot = c ^ ((r >> 1) & 7).  A 32-lane
+// half of ds_read_b64_tr_b16 reads 4 k-rows x 4 chunks (a 64-byte aligned
+// block) of 256-byte rows; XOR with 4 * (k & 3) sends the 4 k-rows to 4
+// different 64-byte blocks of the bank line.
+__device__ __forceinline__ int kswz(int r) { return (r >> 1) & 7; }
 __device__ __forceinline__ int rswz(int k) { return (k & 3) << 2; }
 
 // Loads of one 128-row x kBK tile of an operand for a whole K loop.  The
@@ -115,10 +131,10 @@ __device__ __forceinline__ int rswz(int k) { return (k & 3) << 2; }
 // a load is one global_load_lds_dwordx4 with a scalar base and a vector
 // offset, and a whole step costs a few scalar instructions.  Rows past the
 // operand's end are clamped onto its last valid row (their products land in
-// output rows or token columns that are never stored); only the K tail (the
-// last step when k_end is not a multiple of kBK) reads zeros for k >= k_end,
-// through the masked form.  Steps past the last re-read the last step into a
-// stage that is never multiplied.
+// output rows or token columns that are never stored); the K tail (the last
+// step when k_end is not a multiple of kBK) and every step past the last
+// (which the K loop runs to finish its ring, or issues ahead of the end) hold
+// zeros for k >= k_end, through the masked form.
 template <int MAJOR>
 struct TileLoader {
   const uint8_t* base;    // wave-uniform: byte address of the tile origin at step 0
@@ -146,8 +162,8 @@ struct TileLoader {
     for (int t = 0; t < kLoadsPerTile; ++t) {
       const int s = (t * 4 + w) * 64 + lane;
       if constexpr (MAJOR == KMajor) {
-        const int r = s >> 2;
-        const int c = (s & 3) ^ kswz(r);
+        const int r = s / kChunks;
+        const int c = (s % kChunks) ^ kswz(r);
         const int rr = r < nrows ? r : nrows - 1;
         off[t] = (uint32_t)(rr * (int)op.ld + c * 8) * 2u;
       } else {
@@ -157,6 +173,9 @@ struct TileLoader {
         const int cc = c < cmax ? c : cmax;
         off[t] = (uint32_t)(k * (int)op.ld + cc * 8) * 2u;
       }
+      // one 32-bit register per offset: left visible, the compiler folds the
+      // address's zero-extension into a 64-bit multiply-add and keeps pairs
+      asm volatile("" : "+v"(off[t]));
     }
   }
 
@@ -165,12 +184,17 @@ struct TileLoader {
   __device__ __forceinline__ const uint8_t* step_base(int step) const {
     return uniform_ptr(base + (int64_t)clamp_step(step) * kstep);
   }
-  // Whether the loads of `step` need the masked (K tail) form.
+  // Whether the loads of `step` need the masked form: the K tail (the last
+  // step when k_end is not a multiple of kBK) and every step past the last,
+  // which the K loop runs to finish its ring and which must multiply zeros.
   __device__ __forceinline__ bool tail(int step) const {
-    return clamp_step(step) == last && (k_end % kBK) != 0;
+    return step > last || (step == last && (k_end % kBK) != 0);
   }
 
   // Issue load t of this wave's share of the step at `sb` into LDS tile `dst`.
+  // The masked form loads the lanes whose chunk lies below k_end and writes 16
+  // zero bytes to the LDS slot of every other lane (a DMA lands lane i at
+  // M0 + 16 i); so it may issue no DMA instruction at all for this wave.
   template <bool MASKED>
   __device__ __forceinline__ void issue(const uint8_t* sb, int step, int t, uint8_t* dst) const {
     uint8_t* d = dst + (t * 4 + wave_id()) * 64 * 16;
@@ -182,15 +206,16 @@ struct TileLoader {
       const int s = (t * 4 + wave_id()) * 64 + lane;
       int kk;
       if constexpr (MAJOR == KMajor) {
-        const int r = s >> 2;
-        kk = ((s & 3) ^ kswz(r)) * 8;
+        const int r = s / kChunks;
+        kk = ((s % kChunks) ^ kswz(r)) * 8;
       } else {
         kk = s >> 4;
       }
-      const bool ok = clamp_step(step) * kBK + kk < k_end;
-      const uintptr_t src =
-          ok ? reinterpret_cast<uintptr_t>(sb + off[t]) : reinterpret_cast<uintptr_t>(&g_zero16);
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src), UTTT_LDS(d), 16, 0, 0);
+      if (step * kBK + kk < k_end)
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(sb + off[t]), UTTT_LDS(d),
+                                         16, 0, 0);
+      else
+        *reinterpret_cast<uint4*>(d + lane * 16) = make_uint4(0u, 0u, 0u, 0u);
     }
   }
 };
@@ -208,44 +233,55 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // loads nor insert the lgkmcnt wait their consumers need: run_pipeline<kAsm>
 // places every wait itself.  "memory" keeps them in program order with the
 // loads and barriers.
-__device__ __forceinline__ i16x4 ds_tr16_asm(const void* p) {
+template <int OFF>
+__device__ __forceinline__ i16x4 ds_tr16_asm(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
   i32x2 v;
-  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(v) : "v"(lds_addr(p)) : "memory");
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF) : "memory");
   return __builtin_bit_cast(i16x4, v);
 }
-__device__ __forceinline__ bf16x8 ds_b128_asm(const void* p) {
+template <int OFF>
+__device__ __forceinline__ bf16x8 ds_b128_asm(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
   i32x4 v;
-  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(lds_addr(p)) : "memory");
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF) : "memory");
   return __builtin_bit_cast(bf16x8, v);
 }
 
-// MFMA operand fragment of rows [rb, rb+32), k-substep ks (16 k) of an LDS tile.
-template <int MAJOR, bool ASM = false>
-__device__ __forceinline__ bf16x8 frag(const uint8_t* tile, int rb, int ks) {
+// Fragment addressing.  An MFMA operand fragment covers 32 rows (rb a
+// multiple of 32) and one k-substep KS (16 k) of an LDS tile.
+//   KMajor: lane l reads row rb + l%32, chunk 2 KS + l/32; the XOR key
+//     kswz(row) = kswz(l%32) does not depend on rb, so the fragments of all
+//     row blocks share one lane offset and differ by rb * 128 bytes (an
+//     immediate offset of the read).
+//   RMajor: the lane's two reads sit at k-rows k0 and k0 + 4 of the substep;
+//     rswz(k0) does not depend on KS, so substep KS adds KS * 16 k-rows
+//     (4096 bytes) and the second read 1024 bytes, both immediates.
+// So a substep's reads need one address register per tile (KMajor) or per
+// row block (RMajor) and everything else is an immediate offset.
+template <int KS>
+__device__ __forceinline__ uint32_t kmaj_lane() {
   const int lane = threadIdx.x & 63;
+  const int r = lane & 31;
+  const int c = 2 * KS + (lane >> 5);
+  return (uint32_t)((r * kChunks + (c ^ kswz(r))) * 16);
+}
+__device__ __forceinline__ uint32_t rmaj_lane(int rb) {
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4, s = lane & 15;
+  const int j = s >> 2, q = s & 3;
+  const int r = rb + 16 * (g & 1) + 4 * q;
+  const int c = r >> 3;
+  const int k0 = 8 * (g >> 1) + j;
+  return (uint32_t)((k0 * 16 + (c ^ rswz(k0))) * 16 + 8 * (q & 1));
+}
+template <int MAJOR, int KS, int OFF>
+__device__ __forceinline__ bf16x8 frag_at(uint32_t base) {
   if constexpr (MAJOR == KMajor) {
-    const int r = rb + (lane & 31);
-    const int c = 2 * ks + (lane >> 5);
-    const uint8_t* p = tile + (r * 4 + (c ^ kswz(r))) * 16;
-    if constexpr (ASM) return ds_b128_asm(p);
-    return *reinterpret_cast<const bf16x8*>(p);
+    return ds_b128_asm<OFF>(base);
   } else {
-    const int g = lane >> 4, s = lane & 15;
-    const int j = s >> 2, q = s & 3;
-    const int r = rb + 16 * (g & 1) + 4 * q;
-    const int c = r >> 3;
-    const int kb = 16 * ks + 8 * (g >> 1) + j;
-    const int k0 = kb, k1 = kb + 4;
-    const uint8_t* p0 = tile + (k0 * 16 + (c ^ rswz(k0))) * 16 + 8 * (q & 1);
-    const uint8_t* p1 = tile + (k1 * 16 + (c ^ rswz(k1))) * 16 + 8 * (q & 1);
-    i16x4 x0, x1;
-    if constexpr (ASM) {
-      x0 = ds_tr16_asm(p0);
-      x1 = ds_tr16_asm(p1);
-    } else {
-      x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(p0));
-      x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(p1));
-    }
+    const i16x4 x0 = ds_tr16_asm<OFF + KS * 4096>(base);
+    const i16x4 x1 = ds_tr16_asm<OFF + KS * 4096 + 1024>(base);
     const i16x8 x = __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7);
     return __builtin_bit_cast(bf16x8, x);
   }
@@ -257,18 +293,34 @@ struct HalfFrags {
   bf16x8 b[kNB], a0[2], a1[2];
 };
 
-template <int AMAJ, int BMAJ, bool ASM = false>
-__device__ __forceinline__ void read_half(HalfFrags& f, const uint8_t* st, int ks, int wm,
-                                          int wn) {
-  const uint8_t* a0 = st;
-  const uint8_t* a1 = st + kTileBytes;
-  const uint8_t* b = st + (2 + wn) * kTileBytes;  // this wave's B half
-#pragma unroll
-  for (int j = 0; j < kNB; ++j) f.b[j] = frag<BMAJ, ASM>(b, j * 32, ks);
-#pragma unroll
-  for (int i = 0; i < 2; ++i) f.a0[i] = frag<AMAJ, ASM>(a0, wm * 64 + i * 32, ks);
-#pragma unroll
-  for (int i = 0; i < 2; ++i) f.a1[i] = frag<AMAJ, ASM>(a1, wm * 64 + i * 32, ks);
+template <int AMAJ, int BMAJ, int KS>
+__device__ __forceinline__ void read_half(HalfFrags& f, const uint8_t* st, int wm, int wn) {
+  constexpr int kRow = kChunks * 16;  // bytes per KMajor tile row
+  const uint32_t s = lds_addr(st);
+  const uint32_t sb = s + (2 + wn) * kTileBytes;  // this wave's B half
+  if constexpr (BMAJ == KMajor) {
+    const uint32_t b = sb + kmaj_lane<KS>();
+    static_for<kNB>([&](auto J) __attribute__((always_inline)) {
+      f.b[J] = frag_at<KMajor, KS, decltype(J)::value * 32 * kRow>(b);
+    });
+  } else {
+    static_for<kNB>([&](auto J) __attribute__((always_inline)) {
+      f.b[J] = frag_at<RMajor, KS, 0>(sb + rmaj_lane(decltype(J)::value * 32));
+    });
+  }
+  if constexpr (AMAJ == KMajor) {
+    const uint32_t a = s + wm * 64 * kRow + kmaj_lane<KS>();
+    static_for<2>([&](auto I) __attribute__((always_inline)) {
+      f.a0[I] = frag_at<KMajor, KS, decltype(I)::value * 32 * kRow>(a);
+      f.a1[I] = frag_at<KMajor, KS, kTileBytes + decltype(I)::value * 32 * kRow>(a);
+    });
+  } else {
+    static_for<2>([&](auto I) __attribute__((always_inline)) {
+      const uint32_t a = s + rmaj_lane(wm * 64 + decltype(I)::value * 32);
+      f.a0[I] = frag_at<RMajor, KS, 0>(a);
+      f.a1[I] = frag_at<RMajor, KS, kTileBytes>(a);
+    });
+  }
 }
 
 // LDS instructions of one read_half: a KMajor fragment is one ds_read_b128,
@@ -301,18 +353,6 @@ __device__ __forceinline__ void lgkm_wait_tied(HalfFrags& f) {
   f.a1[1] = __builtin_bit_cast(bf16x8, r[7]);
 }
 
-// f(std::integral_constant<int, i>) for i = 0 .. N-1 with compile-time i, so
-// that accumulator indices stay constants whatever the unroller decides (a
-// runtime index would move the accumulator arrays to scratch memory).
-template <class F, int... Is>
-__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
-  (f(std::integral_constant<int, Is>{}), ...);
-}
-template <int N, class F>
-__device__ __forceinline__ void static_for(F&& f) {
-  static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
-
 // acc_a[i][j] += A_a(wave rows i) * B(wave cols j) over one k-substep, a = 0, 1.
 __device__ __forceinline__ void mma_half(f32x16 (&acc0)[2][kNB], f32x16 (&acc1)[2][kNB],
                                          const HalfFrags& f) {
@@ -328,9 +368,9 @@ __device__ __forceinline__ void mma_half(f32x16 (&acc0)[2][kNB], f32x16 (&acc1)[
       acc1[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a1[i], f.b[j], acc1[i][j], 0, 0, 0);
 }
 
-// The same 16 MFMAs with between(p) (p = 0 .. 7, a compile-time constant)
-// issued after MFMAs 2p and 2p+1, each in its own scheduling region: the wave
-// issues the work of `between` while the matrix core is busy.
+// The same 16 MFMAs with between(i) (a compile-time constant) issued after
+// MFMA i, each in its own scheduling region: the wave issues the work of
+// `between` while the matrix core is busy.
 template <class Between>
 __device__ __forceinline__ void mma_half(f32x16 (&acc0)[2][kNB], f32x16 (&acc1)[2][kNB],
                                          const HalfFrags& f, Between&& between) {
@@ -342,47 +382,50 @@ __device__ __forceinline__ void mma_half(f32x16 (&acc0)[2][kNB], f32x16 (&acc1)[
       acc0[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a0[i], f.b[j], acc0[i][j], 0, 0, 0);
     else
       acc1[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a1[i], f.b[j], acc1[i][j], 0, 0, 0);
-    if constexpr (decltype(I)::value % 2 == 1) {
-      __builtin_amdgcn_sched_barrier(0);
-      between(std::integral_constant<int, decltype(I)::value / 2>{});
-      __builtin_amdgcn_sched_barrier(0);
-    }
+    __builtin_amdgcn_sched_barrier(0);
+    between(I);
+    __builtin_amdgcn_sched_barrier(0);
   });
 }
 
-// The K loop: a ring of kStages LDS stages; the loads of step kt+kStages are
-// issued during step kt, so kStages-1 steps are in flight while one is
-// multiplied (four stages, 128 KiB, cover the L2-miss latency seen under
-// load; three did not).
-//   prep(kt)                 readies the loads of step kt (operand switch,
-//                            per-step scalar bases) and returns whether they
+// The K loop: two LDS stages of kBK = 64 (KMajor operand rows are then whole
+// 128-byte cache lines: an LDS-DMA instruction touches 8 lines instead of 16,
+// which doubles what a CU's L1 can stream from L2); the loads of stage kt+2
+// are issued during the last k-substep of stage kt and have the whole of stage
+// kt+1 to land.
+//   prep(kt)                 readies the loads of stage kt (operand switch,
+//                            per-stage scalar bases) and returns whether they
 //                            need the masked (K tail) form
 //   issue(p, masked, stage)  issues load p (0 .. kLoadsPerStage-1, a constant)
-//                            of the prepared step into `stage`
-//   read(stage, ks, frags)   the fragment reads of k-substep ks, inline asm,
+//                            of the prepared stage into `stage`
+//   read(stage, ks, frags)   the fragment reads of k-substep ks (a constant), inline asm,
 //                            NLDS LDS instructions
-// Step kt (stage cur, next stage nxt):
-//   read (kt, 1) -> f1;  prep(kt + kStages);  wait for f0;  MFMAs of f0
-//   wait for this wave's loads of stage kt+1 and for f1, barrier (stage kt+1
-//   has landed for every wave, and every wave is done reading stage kt)
-//   read (kt+1, 0) -> f0;  MFMAs of f1 with the loads of step kt+kStages
-//   into stage cur interleaved between them
+// Stage kt (buffer cur, next buffer nxt), fragments double-buffered in f[2]:
+//   substeps j < kSubsteps-1: read (kt, j+1) -> f[(j+1)&1];  wait for f[j&1];
+//     its MFMAs (prep(kt+2) rides on substep 0)
+//   last substep: wait for this wave's loads of stage kt+1 and for the last
+//     fragments, barrier (stage kt+1 has landed for every wave, and every wave
+//     is done reading stage kt), read (kt+1, 0) -> f[0], then the MFMAs of the
+//     last substep with the loads of stage kt+2 into cur, one after each MFMA
 // so with one wave per SIMD the matrix core is fed while the next fragments
 // and the next stage arrive.  The fragment reads are inline asm because the
 // compiler's wait-count pass cannot tell them from the in-flight LDS-DMA
 // writes and would drain every load (vmcnt(0)) or every read (lgkmcnt(0))
-// in front of them; every wait here is explicit.  Before the MFMAs of f0 the
-// NLDS reads of f1 are the only younger LDS operations, so lgkmcnt(min(NLDS,
-// 15)) leaves f0 complete (any other LGKM operation only makes it stricter).
+// in front of them; every wait here is explicit.  Before the MFMAs of
+// f[j&1] the NLDS reads of f[(j+1)&1] are the only younger LDS operations, so
+// lgkmcnt(min(NLDS, 15)) leaves f[j&1] complete (any other LGKM operation only
+// makes it stricter).
 template <int NLDS, class PrepFn, class IssueFn, class ReadFn>
 __device__ __forceinline__ void run_pipeline(int nk, PrepFn&& prep, IssueFn&& issue, ReadFn&& read,
                                              f32x16 (&acc0)[2][kNB], f32x16 (&acc1)[2][kNB],
                                              uint8_t* const (&ring)[kStages]) {
   if (nk <= 0) return;
   constexpr int kW = NLDS < 15 ? NLDS : 15;
-  HalfFrags f0, f1;
-  auto load_all = [&](int kt, uint8_t* st) __attribute__((always_inline)) {
-    if (prep(kt))
+  static_assert(kSubsteps % 2 == 0, "fragment double buffer parity");
+  HalfFrags f[2];
+  auto load_all = [&](int kt, uint8_t* st) __attribute__((always_inline)) -> bool {
+    const bool m = prep(kt);
+    if (m)
       static_for<kLoadsPerStage>([&](auto p) __attribute__((always_inline)) {
         issue(p, std::true_type{}, st);
       });
@@ -390,22 +433,37 @@ __device__ __forceinline__ void run_pipeline(int nk, PrepFn&& prep, IssueFn&& is
       static_for<kLoadsPerStage>([&](auto p) __attribute__((always_inline)) {
         issue(p, std::false_type{}, st);
       });
+    return m;
   };
-  static_for<kStages>([&](auto i) __attribute__((always_inline)) { load_all(i, ring[i]); });
-  wait_vmcnt<(kStages - 1) * kLoadsPerStage>();
+  // stage 0 landed: counted while stages 1.. issued their kLoadsPerStage DMAs
+  // each, a full drain when one of them took the masked form (fewer DMAs)
+  bool later_masked = false;
+  static_for<kStages>([&](auto i) __attribute__((always_inline)) {
+    const bool m = load_all(i, ring[i]);
+    if constexpr (decltype(i)::value > 0) later_masked |= m;
+  });
+  if (later_masked)
+    wait_vmcnt<0>();
+  else
+    wait_vmcnt<(kStages - 1) * kLoadsPerStage>();
   block_barrier();
-  read(ring[0], 0, f0);
+  read(ring[0], std::integral_constant<int, 0>{}, f[0]);
   auto step = [&](int kt, uint8_t* cur, const uint8_t* nxt) __attribute__((always_inline)) {
-    read(cur, 1, f1);
-    const bool masked = prep(kt + kStages);
-    lgkm_wait_tied<kW>(f0);
-    mma_half(acc0, acc1, f0);
-    __builtin_amdgcn_sched_barrier(0);
+    bool masked = false;
+    static_for<kSubsteps - 1>([&](auto J) __attribute__((always_inline)) {
+      constexpr int j = J;
+      read(cur, std::integral_constant<int, j + 1>{}, f[(j + 1) & 1]);
+      if constexpr (j == 0) masked = prep(kt + kStages);
+      lgkm_wait_tied<kW>(f[j & 1]);
+      mma_half(acc0, acc1, f[j & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    constexpr int jl = kSubsteps - 1;
     wait_vmcnt<(kStages - 2) * kLoadsPerStage>();
-    lgkm_wait_tied<0>(f1);
+    lgkm_wait_tied<0>(f[jl & 1]);
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    read(nxt, 0, f0);
+    read(nxt, std::integral_constant<int, 0>{}, f[(jl + 1) & 1]);
     // the rare K-tail step issues its masked loads up front; otherwise the
     // loads ride between the MFMAs (branches hold loads only, so the
     // accumulators never meet at a join)
@@ -414,21 +472,31 @@ __device__ __forceinline__ void run_pipeline(int nk, PrepFn&& prep, IssueFn&& is
         issue(p, std::true_type{}, cur);
       });
     __builtin_amdgcn_sched_barrier(0);
-    mma_half(acc0, acc1, f1, [&](auto p) __attribute__((always_inline)) {
-      if (!masked) issue(p, std::false_type{}, cur);
+    mma_half(acc0, acc1, f[jl & 1], [&](auto i) __attribute__((always_inline)) {
+      if constexpr (decltype(i)::value < kLoadsPerStage)
+        if (!masked) issue(i, std::false_type{}, cur);
     });
     __builtin_amdgcn_sched_barrier(0);
   };
-  int kt = 0;
-  for (; kt + kStages <= nk; kt += kStages)
+  // whole ring iterations only (one copy of the step code: a separate tail
+  // would keep its own addressing live across the loop); steps past nk
+  // multiply the zeros their masked loads wrote
+  for (int kt = 0; kt < nk; kt += kStages)
     static_for<kStages>([&](auto i) __attribute__((always_inline)) {
       step(kt + i, ring[i], ring[(i + 1) % kStages]);
     });
-  static_for<kStages - 1>([&](auto i) __attribute__((always_inline)) {
-    if (kt + i < nk) step(kt + i, ring[i], ring[(i + 1) % kStages]);
-  });
-  lgkm_wait_tied<0>(f0);  // the reads of the stage past the end
+  lgkm_wait_tied<0>(f[0]);  // the reads of the stage past the end
   wait_vmcnt<0>();        // and the loads issued past the end
+}
+
+// Opaque copies of the values an epilogue addresses with, taken after the K
+// loop: nothing computed from them can be hoisted above the loop, where it
+// would stay live across it (the loop needs every register: with the fragment
+// reads in asm, a spill of a fragment register between its read and its wait
+// would save the value from before the read).
+__device__ __forceinline__ int after_loop(int v) {
+  asm volatile("" : "+v"(v));
+  return v;
 }
 
 template <int M, int N>

@@ -357,11 +357,8 @@ template <int AMAJ, class Epi>
 __global__ __launch_bounds__(kThreads) void tn_kernel(TnArgs a, typename Epi::Args ea) {
   __shared__ __attribute__((aligned(16))) uint8_t st0[kStageBytes];
   __shared__ __attribute__((aligned(16))) uint8_t st1[kStageBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t st2[kStageBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t st3[kStageBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t st4[kStageBytes];
   // the tile lookup's 4 ints live in the last stage: it is done before any load
-  int* scratch = reinterpret_cast<int*>(st4);
+  int* scratch = reinterpret_cast<int*>(st1);
 
   // Tile order: workgroup i runs on XCD i % kXcds, each XCD with its own L2.
   // The (m-tile, n-tile) plane (n-tiles of all batches in a row) is cut into
@@ -386,7 +383,7 @@ __global__ __launch_bounds__(kThreads) void tn_kernel(TnArgs a, typename Epi::Ar
   if (mt >= a.m_tiles || ntg >= a.B * a.n_tiles_ub) return;  // padding of the super-tile grid
   const int b = ntg / a.n_tiles_ub, nt = ntg % a.n_tiles_ub;
   const TokenTile tt = find_token_tile<kBRows>(a.gs + (int64_t)b * a.E, a.E, a.N, nt, scratch);
-  __syncthreads();  // every wave has read the lookup before stage 4 is loaded
+  __syncthreads();  // every wave has read the lookup before stage 1 is loaded
   if (tt.e < 0) return;
   const int m0 = mt * a.m_step;
 
@@ -438,14 +435,15 @@ __global__ __launch_bounds__(kThreads) void tn_kernel(TnArgs a, typename Epi::Ar
   };
   const int w = threadIdx.x >> 6;
   const int wm = w >> 1, wn = w & 1;
-  auto read = [&](const uint8_t* st, int ks, HalfFrags& f) __attribute__((always_inline)) {
-    read_half<AMAJ, KMajor, true>(f, st, ks, wm, wn);
+  auto read = [&](const uint8_t* st, auto ks, HalfFrags& f) __attribute__((always_inline)) {
+    read_half<AMAJ, KMajor, decltype(ks)::value>(f, st, wm, wn);
   };
   (void)two;
-  uint8_t* const ring[kStages] = {st0, st1, st2, st3, st4};
+  uint8_t* const ring[kStages] = {st0, st1};
   run_pipeline<half_lds_ops<AMAJ, KMajor>()>(nk0 + nk1, prep, issue, read, acc0, acc1, ring);
-  const TileCtx c{b, m0, wm, wn, mt, tt, reinterpret_cast<float*>(st0),
-                  reinterpret_cast<float*>(st1)};
+  const TokenTile tte{tt.e, after_loop(tt.start), after_loop(tt.size), after_loop(tt.n0)};
+  const TileCtx c{after_loop(b), after_loop(m0), after_loop(wm), after_loop(wn), mt, tte,
+                  reinterpret_cast<float*>(st0), reinterpret_cast<float*>(st1)};
   Epi::apply(ea, acc0, acc1, c, two);
 }
 
@@ -467,9 +465,6 @@ __global__ __launch_bounds__(kThreads) void wg_kernel(WgTask t0, WgTask t1,
                                                       int N) {
   __shared__ __attribute__((aligned(16))) uint8_t st0[kStageBytes];
   __shared__ __attribute__((aligned(16))) uint8_t st1[kStageBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t st2[kStageBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t st3[kStageBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t st4[kStageBytes];
 
   const int n0_tiles = t0.y_tiles * t0.x_tiles;
   const int per_group = n0_tiles + t1.y_tiles * t1.x_tiles;
@@ -518,17 +513,18 @@ __global__ __launch_bounds__(kThreads) void wg_kernel(WgTask t0, WgTask t1,
   };
   const int w = threadIdx.x >> 6;
   const int wm = w >> 1, wn = w & 1;
-  auto read = [&](const uint8_t* st, int ks, HalfFrags& f) __attribute__((always_inline)) {
-    read_half<RMajor, RMajor, true>(f, st, ks, wm, wn);
+  auto read = [&](const uint8_t* st, auto ks, HalfFrags& f) __attribute__((always_inline)) {
+    read_half<RMajor, RMajor, decltype(ks)::value>(f, st, wm, wn);
   };
-  uint8_t* const ring[kStages] = {st0, st1, st2, st3, st4};
+  uint8_t* const ring[kStages] = {st0, st1};
   run_pipeline<half_lds_ops<RMajor, RMajor>()>((size + kBK - 1) / kBK, prep, issue, read, acc0,
                                                acc1, ring);
 
-  uint16_t* ob = tk.out + ((int64_t)b * E + e) * X * Y;
-  for_quads(acc0, acc1, wm, wn, true, [&](int tt, int r, int n, const float* v) __attribute__((always_inline)) {
-    const int y = y0 + tt * kTileRows + r;
-    const int x = x0 + n;
+  uint16_t* ob = tk.out + ((int64_t)after_loop(b) * E + after_loop(e)) * X * Y;
+  const int ye = after_loop(y0), xe = after_loop(x0);
+  for_quads(acc0, acc1, after_loop(wm), after_loop(wn), true, [&](int tt, int r, int n, const float* v) __attribute__((always_inline)) {
+    const int y = ye + tt * kTileRows + r;
+    const int x = xe + n;
     if (y < Y && x < X) store4(ob, Y, x, y, v[0], v[1], v[2], v[3]);
   });
 }
