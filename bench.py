@@ -540,9 +540,10 @@ class MoeSweep:
                    L.ptr(bt["glr"][2]), L.ptr(bt["ws_bwd"]), bt["ws_bwd_bytes"], s)
         self._mark(None)
 
-    def time_isolated(self, batched, reps=5):
+    def time_isolated(self, batched, reps=5, only=None):
         """Mean launch duration of each single-launch kernel of a sweep, timed
-        as `reps` back-to-back launches between two events on the stream."""
+        as `reps` back-to-back launches between two events on the stream (only
+        kernel `only` when given)."""
         import torch
 
         L, E, D, I, s = self.L, self.E, self.D, self.I, self.stream
@@ -551,6 +552,8 @@ class MoeSweep:
         out = {}
 
         def timed(name, fn):
+            if only is not None and name != only:
+                return
             fn()
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
@@ -695,14 +698,16 @@ def bench_moe(args, key):
                             + " expert prior as selection bias, topk_renorm gates")},
         roofline=(dict(bound="hbm", kernel=dom, achieved=round(by[dom] / t_dom / 1e9, 1),
                        peak=HBM_PEAK_GBS, unit="GB/s",
-                       frac=round(by[dom] / t_dom / 1e9 / HBM_PEAK_GBS, 4), traffic=None,
+                       frac=round(by[dom] / t_dom / 1e9 / HBM_PEAK_GBS, 4),
+                       traffic=_profile_traffic(f"{key}_sweep.txt", dom),
                        algorithmic_bytes=by[dom], algorithmic_flops=fl[dom],
                        arithmetic_intensity=round(ai, 1), avg_launch_us=round(t_dom * 1e6, 2),
                        mfma_frac=round(fl[dom] / t_dom / 1e12 / BF16_PEAK_TFLOPS, 4))
                   if ai < ridge else
                   dict(bound="mfma", kernel=dom, achieved=round(fl[dom] / t_dom / 1e12, 2),
                        peak=BF16_PEAK_TFLOPS, unit="TFLOP/s",
-                       frac=round(fl[dom] / t_dom / 1e12 / BF16_PEAK_TFLOPS, 4), traffic=None,
+                       frac=round(fl[dom] / t_dom / 1e12 / BF16_PEAK_TFLOPS, 4),
+                       traffic=_profile_traffic(f"{key}_sweep.txt", dom),
                        algorithmic_flops=fl[dom], avg_launch_us=round(t_dom * 1e6, 2))),
         sweep=dict(algorithmic_flops=sweep_flops,
                    TFLOPs=round(sweep_flops / wall / 1e12, 1),
@@ -712,6 +717,25 @@ def bench_moe(args, key):
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline_moe(sw, cfg, layers, chunks)
     return res
+
+
+def profile_kernel(args, key, name):
+    """One short sweep to set up the routing and buffers of workload `key`,
+    then the isolated launch loop of kernel `name` alone (for counter passes,
+    which profile every launch)."""
+    import torch
+
+    cfg = MOE_CONFIGS[key]
+    sw = MoeSweep(cfg, torch.device("cuda", 0))
+    batched = args.update_schedule == "batched"
+    if batched:
+        sw.prepare_batched(cfg["L"])
+    sw.sweep(cfg["L"], 2, batched)
+    torch.cuda.synchronize()
+    iso = sw.time_isolated(batched, reps=5, only=name)
+    if name not in iso:
+        raise SystemExit(f"bench.py: unknown kernel {name!r} (have {sorted(iso)})")
+    return dict(workload=cfg["label"], kernel=name, us=round(iso[name] * 1e6, 2), launches=6)
 
 
 def cpu_baseline_moe(sw, cfg, layers, chunks):
@@ -918,6 +942,10 @@ def main():
                     help="skip the CPU baseline leg (profiling runs)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one plain 256 MiB device copy (PMC scaling)")
+    ap.add_argument("--profile-kernel", default=None,
+                    help="MoE workloads: set up one sweep's state, then only run the isolated "
+                         "launch loop of this kernel (e.g. gate_up, down_proj, wgrad) and print "
+                         "its mean launch time; for rocprofv3 counter passes")
     args = ap.parse_args()
     moe = args.workload.startswith(("moe", "dense"))
     if args.steps is None:
@@ -939,6 +967,12 @@ def main():
     L.lib()  # fail loudly if the HIP library is not built
     if args.copy_calibration:
         copy_calibration()
+    if args.profile_kernel:
+        if not args.workload.startswith("moe"):
+            print("bench.py: --profile-kernel applies to the MoE workloads", file=sys.stderr)
+            sys.exit(2)
+        print(json.dumps(profile_kernel(args, args.workload, args.profile_kernel)), flush=True)
+        return
     res = WORKLOADS[args.workload](args)
     line = dict(metric=res.pop("metric"), value=res.pop("value"), unit=res.pop("unit"),
                 n_gpus=1, steps=args.steps, warmup=args.warmup,
