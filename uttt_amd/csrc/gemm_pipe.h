@@ -293,18 +293,18 @@ struct HalfFrags {
   bf16x8 b[kNB], a0[2], a1[2];
 };
 
-template <int AMAJ, int BMAJ, int KS>
+template <int AMAJ, int BMAJ, int KS, int NB = kNB>
 __device__ __forceinline__ void read_half(HalfFrags& f, const uint8_t* st, int wm, int wn) {
   constexpr int kRow = kChunks * 16;  // bytes per KMajor tile row
   const uint32_t s = lds_addr(st);
   const uint32_t sb = s + (2 + wn) * kTileBytes;  // this wave's B half
   if constexpr (BMAJ == KMajor) {
     const uint32_t b = sb + kmaj_lane<KS>();
-    static_for<kNB>([&](auto J) __attribute__((always_inline)) {
+    static_for<NB>([&](auto J) __attribute__((always_inline)) {
       f.b[J] = frag_at<KMajor, KS, decltype(J)::value * 32 * kRow>(b);
     });
   } else {
-    static_for<kNB>([&](auto J) __attribute__((always_inline)) {
+    static_for<NB>([&](auto J) __attribute__((always_inline)) {
       f.b[J] = frag_at<RMajor, KS, 0>(sb + rmaj_lane(decltype(J)::value * 32));
     });
   }
@@ -325,9 +325,9 @@ __device__ __forceinline__ void read_half(HalfFrags& f, const uint8_t* st, int w
 
 // LDS instructions of one read_half: a KMajor fragment is one ds_read_b128,
 // an RMajor one two ds_read_b64_tr_b16.
-template <int AMAJ, int BMAJ>
+template <int AMAJ, int BMAJ, int NB = kNB>
 constexpr int half_lds_ops() {
-  return kNB * (BMAJ == KMajor ? 1 : 2) + 4 * (AMAJ == KMajor ? 1 : 2);
+  return NB * (BMAJ == KMajor ? 1 : 2) + 4 * (AMAJ == KMajor ? 1 : 2);
 }
 
 // s_waitcnt on the LDS counter that the compiler must treat as redefining the
@@ -354,38 +354,61 @@ __device__ __forceinline__ void lgkm_wait_tied(HalfFrags& f) {
 }
 
 // acc_a[i][j] += A_a(wave rows i) * B(wave cols j) over one k-substep, a = 0, 1.
-__device__ __forceinline__ void mma_half(f32x16 (&acc0)[2][kNB], f32x16 (&acc1)[2][kNB],
-                                         const HalfFrags& f) {
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < kNB; ++j)
-      acc0[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a0[i], f.b[j], acc0[i][j], 0, 0, 0);
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < kNB; ++j)
-      acc1[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a1[i], f.b[j], acc1[i][j], 0, 0, 0);
+// MFMA q of a substep: the four of column block 0 first, then the other 12,
+// which a wave whose block 0 already covers every token of its columns skips
+// (`full` false: small experts' tiles under skewed routing).  The fragment
+// reads are the same either way, so every wait count holds on both paths.
+// (Without skipping, the order is accumulator-major: consecutive MFMAs share
+// their A fragment.)
+template <int Q, bool SKIP>
+__device__ __forceinline__ void mma_q(f32x16 (&acc0)[2][kNB], f32x16 (&acc1)[2][kNB],
+                                      const HalfFrags& f) {
+  constexpr int j = SKIP ? (Q < 4 ? 0 : 1 + (Q - 4) / 4) : Q % 4;
+  constexpr int a = SKIP ? (Q % 4) / 2 : Q / 8;
+  constexpr int i = SKIP ? Q % 2 : (Q / 4) % 2;
+  if constexpr (a == 0)
+    acc0[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a0[i], f.b[j], acc0[i][j], 0, 0, 0);
+  else
+    acc1[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a1[i], f.b[j], acc1[i][j], 0, 0, 0);
 }
 
-// The same 16 MFMAs with between(i) (a compile-time constant) issued after
-// MFMA i, each in its own scheduling region: the wave issues the work of
-// `between` while the matrix core is busy.
-template <class Between>
+template <bool SKIP>
 __device__ __forceinline__ void mma_half(f32x16 (&acc0)[2][kNB], f32x16 (&acc1)[2][kNB],
-                                         const HalfFrags& f, Between&& between) {
-  static_for<16>([&](auto I) __attribute__((always_inline)) {
-    constexpr int a = decltype(I)::value / 8;
-    constexpr int i = (decltype(I)::value / 4) % 2;
-    constexpr int j = decltype(I)::value % 4;
-    if constexpr (a == 0)
-      acc0[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a0[i], f.b[j], acc0[i][j], 0, 0, 0);
-    else
-      acc1[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a1[i], f.b[j], acc1[i][j], 0, 0, 0);
+                                         const HalfFrags& f, bool full) {
+  static_for<4>([&](auto Q) __attribute__((always_inline)) { mma_q<Q, SKIP>(acc0, acc1, f); });
+  if (!SKIP || full)
+    static_for<12>([&](auto Q) __attribute__((always_inline)) {
+      mma_q<4 + decltype(Q)::value, SKIP>(acc0, acc1, f);
+    });
+}
+
+// The same MFMAs with between(q) (a compile-time constant, 0 .. 15) issued
+// after MFMA q, each in its own scheduling region: the wave issues the work of
+// `between` while the matrix core is busy; without the 12 MFMAs, their slots'
+// work is issued back to back.
+template <bool SKIP, class Between>
+__device__ __forceinline__ void mma_half(f32x16 (&acc0)[2][kNB], f32x16 (&acc1)[2][kNB],
+                                         const HalfFrags& f, bool full, Between&& between) {
+  static_for<4>([&](auto Q) __attribute__((always_inline)) {
+    mma_q<Q, SKIP>(acc0, acc1, f);
     __builtin_amdgcn_sched_barrier(0);
-    between(I);
+    between(Q);
     __builtin_amdgcn_sched_barrier(0);
   });
+  if (!SKIP || full) {
+    static_for<12>([&](auto Q) __attribute__((always_inline)) {
+      constexpr int q = 4 + decltype(Q)::value;
+      mma_q<q, SKIP>(acc0, acc1, f);
+      __builtin_amdgcn_sched_barrier(0);
+      between(std::integral_constant<int, q>{});
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  } else {
+    static_for<12>([&](auto Q) __attribute__((always_inline)) {
+      between(std::integral_constant<int, 4 + decltype(Q)::value>{});
+    });
+  }
+  __builtin_amdgcn_sched_barrier(0);
 }
 
 // The K loop: two LDS stages of kBK = 64 (KMajor operand rows are then whole
@@ -415,8 +438,9 @@ __device__ __forceinline__ void mma_half(f32x16 (&acc0)[2][kNB], f32x16 (&acc1)[
 // f[j&1] the NLDS reads of f[(j+1)&1] are the only younger LDS operations, so
 // lgkmcnt(min(NLDS, 15)) leaves f[j&1] complete (any other LGKM operation only
 // makes it stricter).
-template <int NLDS, class PrepFn, class IssueFn, class ReadFn>
-__device__ __forceinline__ void run_pipeline(int nk, PrepFn&& prep, IssueFn&& issue, ReadFn&& read,
+template <int NLDS, bool SKIP, class PrepFn, class IssueFn, class ReadFn>
+__device__ __forceinline__ void run_pipeline(int nk, bool full, PrepFn&& prep, IssueFn&& issue,
+                                             ReadFn&& read,
                                              f32x16 (&acc0)[2][kNB], f32x16 (&acc1)[2][kNB],
                                              uint8_t* const (&ring)[kStages]) {
   if (nk <= 0) return;
@@ -455,7 +479,7 @@ __device__ __forceinline__ void run_pipeline(int nk, PrepFn&& prep, IssueFn&& is
       read(cur, std::integral_constant<int, j + 1>{}, f[(j + 1) & 1]);
       if constexpr (j == 0) masked = prep(kt + kStages);
       lgkm_wait_tied<kW>(f[j & 1]);
-      mma_half(acc0, acc1, f[j & 1]);
+      mma_half<SKIP>(acc0, acc1, f[j & 1], full);
       __builtin_amdgcn_sched_barrier(0);
     });
     constexpr int jl = kSubsteps - 1;
@@ -472,7 +496,7 @@ __device__ __forceinline__ void run_pipeline(int nk, PrepFn&& prep, IssueFn&& is
         issue(p, std::true_type{}, cur);
       });
     __builtin_amdgcn_sched_barrier(0);
-    mma_half(acc0, acc1, f[jl & 1], [&](auto i) __attribute__((always_inline)) {
+    mma_half<SKIP>(acc0, acc1, f[jl & 1], full, [&](auto i) __attribute__((always_inline)) {
       if constexpr (decltype(i)::value < kLoadsPerStage)
         if (!masked) issue(i, std::false_type{}, cur);
     });

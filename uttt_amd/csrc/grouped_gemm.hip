@@ -19,6 +19,8 @@
 //              read through the LDS transposing loads).
 // Intermediates are token-major ([B, N, rows]); the kernel-level compat entry
 // points can also write the reference's [B, rows, N] layout.
+#include <type_traits>
+
 #include "gemm_pipe.h"
 
 namespace uttt {
@@ -353,7 +355,7 @@ struct EpiBwd {
   }
 };
 
-template <int AMAJ, class Epi>
+template <int AMAJ, class Epi, bool SKIP>
 __global__ __launch_bounds__(kThreads) void tn_kernel(TnArgs a, typename Epi::Args ea) {
   __shared__ __attribute__((aligned(16))) uint8_t st0[kStageBytes];
   __shared__ __attribute__((aligned(16))) uint8_t st1[kStageBytes];
@@ -435,12 +437,20 @@ __global__ __launch_bounds__(kThreads) void tn_kernel(TnArgs a, typename Epi::Ar
   };
   const int w = threadIdx.x >> 6;
   const int wm = w >> 1, wn = w & 1;
+  (void)two;
+  uint8_t* const ring[kStages] = {st0, st1};
+  // SKIP: a wave whose first 32-token column block holds every token of its
+  // half of the tile skips the MFMAs of its other three blocks (small
+  // experts' tiles under skewed routing); loads, reads and barriers are the
+  // same.  Without SKIP the branch is gone at compile time.
+  const int vt = tt.size - tt.n0 - wn * (kBRows / 2);
+  const bool full = !SKIP || __builtin_amdgcn_readfirstlane(vt > 32 ? 1 : 0) != 0;
+  (void)vt;
   auto read = [&](const uint8_t* st, auto ks, HalfFrags& f) __attribute__((always_inline)) {
     read_half<AMAJ, KMajor, decltype(ks)::value>(f, st, wm, wn);
   };
-  (void)two;
-  uint8_t* const ring[kStages] = {st0, st1};
-  run_pipeline<half_lds_ops<AMAJ, KMajor>()>(nk0 + nk1, prep, issue, read, acc0, acc1, ring);
+  run_pipeline<half_lds_ops<AMAJ, KMajor>(), SKIP>(nk0 + nk1, full, prep, issue, read, acc0,
+                                                    acc1, ring);
   const TokenTile tte{tt.e, after_loop(tt.start), after_loop(tt.size), after_loop(tt.n0)};
   const TileCtx c{after_loop(b), after_loop(m0), after_loop(wm), after_loop(wn), mt, tte,
                   reinterpret_cast<float*>(st0), reinterpret_cast<float*>(st1)};
@@ -517,8 +527,8 @@ __global__ __launch_bounds__(kThreads) void wg_kernel(WgTask t0, WgTask t1,
     read_half<RMajor, RMajor, decltype(ks)::value>(f, st, wm, wn);
   };
   uint8_t* const ring[kStages] = {st0, st1};
-  run_pipeline<half_lds_ops<RMajor, RMajor>()>((size + kBK - 1) / kBK, prep, issue, read, acc0,
-                                               acc1, ring);
+  run_pipeline<half_lds_ops<RMajor, RMajor>(), false>((size + kBK - 1) / kBK, true, prep, issue,
+                                                      read, acc0, acc1, ring);
 
   uint16_t* ob = tk.out + ((int64_t)after_loop(b) * E + after_loop(e)) * X * Y;
   const int ye = after_loop(y0), xe = after_loop(x0);
@@ -647,6 +657,12 @@ void super_tile(int m_tiles, int* gm, int* gn) {
   }
 }
 
+// Epilogues whose launches take the MFMA-skipping variant when tokens per
+// expert are few (the per-layer APPLY): K-major gate/up and bf16 products.
+template <int AMAJ, class Epi>
+constexpr bool kSkippable =
+    AMAJ == KMajor && (std::is_same_v<Epi, EpiSwiGLU> || std::is_same_v<Epi, EpiStore<uint16_t>>);
+
 template <int AMAJ, class Epi>
 int launch_tn(TnArgs t, const typename Epi::Args& ea, int B, hipStream_t st,
               const char* what) {
@@ -665,7 +681,16 @@ int launch_tn(TnArgs t, const typename Epi::Args& ea, int B, hipStream_t st,
     t.n_super_m = 1;
   }
   if (int rc = check_grid(blocks, what)) return rc;
-  hipLaunchKernelGGL((tn_kernel<AMAJ, Epi>), dim3((unsigned)blocks), dim3(kThreads), 0, st, t, ea);
+  // fewer than 256 tokens per expert on average: many tiles at segment ends
+  if constexpr (kSkippable<AMAJ, Epi>) {
+    if ((int64_t)t.N < (int64_t)kBRows * t.E) {
+      hipLaunchKernelGGL((tn_kernel<AMAJ, Epi, true>), dim3((unsigned)blocks), dim3(kThreads), 0,
+                         st, t, ea);
+      return check_launch(what);
+    }
+  }
+  hipLaunchKernelGGL((tn_kernel<AMAJ, Epi, false>), dim3((unsigned)blocks), dim3(kThreads), 0, st,
+                     t, ea);
   return check_launch(what);
 }
 
