@@ -20,6 +20,9 @@ in HBM before the timed region starts):
             head (H=4, d=192, hidden 384), 12 layers, aggregate write.
   dense_c0  configs[0]'s single-layer shape (H=4, d=96, hidden 192, chunks of
             512) on the GPU.
+  muon760m  the Muon write of one chunk on the 760M pool (momentum,
+            Newton-Schulz5 of the 96 expert matrices, scaled add,
+            norm-preserving write); value = NS5 algorithmic TFLOP/s.
   permute   configs[2]: token permute + gate-weighted unpermute by expert,
             T=65536, E=16, top-2, payload bf16 [T, 768]; one step = row map +
             permute + unpermute of one batch; value = algorithmic GB/s.
@@ -920,11 +923,120 @@ def cpu_baseline_dense(cfg, sets, w):
                 sample=sample + f" (fp32 torch, {threads} threads)", cpu=_cpu_model())
 
 
+# ------------------------------------------------------------ Muon write --
+def _ns5_flops(R, C):
+    """Algorithmic FLOP of one Newton-Schulz5 of an R x C matrix (m = short
+    side, n = long side): per iteration A = X X^T (2 m^2 n), A @ A (2 m^3),
+    B @ X (2 m^2 n)."""
+    m, n = min(R, C), max(R, C)
+    return 5 * (4 * m * m * n + 2 * m ** 3)
+
+
+def bench_muon(args):
+    """The Muon write of one chunk on the 760M expert pool (E=32, W0/W2
+    [3072, 1536], W1 [1536, 3072]; fp32 masters and momentum, bf16 gradients):
+    momentum, Newton-Schulz5 per expert matrix, scaled add and the
+    norm-preserving projection (modeling_recurrent_lact.py:754-825 with
+    use_momentum and use_moun).  One step = the write of the three matrices;
+    value = NS5 algorithmic TFLOP/s of the step."""
+    import torch
+
+    from uttt_amd import fast_weight_write as FWW
+
+    dev = torch.device("cuda", 0)
+    B, E, I, D = 1, 32, 3072, 1536
+    g = torch.Generator().manual_seed(0)
+    shapes = [(B, E, I, D), (B, E, D, I), (B, E, I, D)]
+    masters = [(torch.randn(*s, generator=g) / D ** 0.5).to(dev) for s in shapes]
+    grads = [(torch.randn(*s, generator=g) * 0.05).to(torch.bfloat16).to(dev) for s in shapes]
+    moms = [(torch.randn(*s, generator=g) * 0.05).to(dev) for s in shapes]
+    coeff = torch.full((B, 1, 1, 1), 0.9, device=dev)
+
+    def step():
+        return FWW.apply_moe_update_dense(tuple(grads), None, tuple(masters), tuple(moms), coeff,
+                                          lr_scale=0.5, use_moun=True)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = _events(2)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        out = step()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    t_step = e0.elapsed_time(e1) * 1e-3 / args.steps
+    flops = sum(B * E * _ns5_flops(*s[2:]) for s in shapes)
+
+    # the NS5 chain of one matrix set alone (w0: 32 x [3072, 1536]), the
+    # dominant part of the step, between events on its launch stream
+    reps = max(3, args.steps)
+    G0 = grads[0].reshape(B * E, I, D)
+    FWW.newton_schulz5(G0, 0.5)
+    e0.record()
+    for _ in range(reps):
+        FWW.newton_schulz5(G0, 0.5)
+    e1.record()
+    torch.cuda.synchronize()
+    t_ns = e0.elapsed_time(e1) * 1e-3 / reps
+    f_ns = B * E * _ns5_flops(I, D)
+
+    # sanity: the write preserved the row norms of the masters
+    m0 = masters[0].norm(dim=-1)
+    m1 = out[1][0].norm(dim=-1)
+    assert torch.allclose(m1, m0, rtol=1e-4), "Muon write broke the norm-preserving projection"
+    res = dict(
+        metric="Muon write NS5 TFLOP/s (760M expert pool, one chunk's write)",
+        value=round(flops / t_step / 1e12, 2), unit="TFLOP/s",
+        ms_per_step=round(t_step * 1e3, 3), wall_ms_per_step=round(wall / args.steps * 1e3, 3),
+        dtype="bf16",
+        config={"workload": "uTTT-MoE 760M pool write with momentum + Muon",
+                "experts": E, "expert_hidden": I, "d": D,
+                "step": "momentum, NS5 of 96 expert matrices, scaled add, norm-preserving write"},
+        roofline=dict(bound="mfma", kernel="newton_schulz5 chain (w0: 32 x [3072,1536])",
+                      achieved=round(f_ns / t_ns / 1e12, 1), peak=BF16_PEAK_TFLOPS,
+                      unit="TFLOP/s", frac=round(f_ns / t_ns / 1e12 / BF16_PEAK_TFLOPS, 4),
+                      traffic=None, algorithmic_flops=f_ns, avg_call_us=round(t_ns * 1e6, 1)),
+        step_flops=flops, mfma_frac=round(flops / t_step / 1e12 / BF16_PEAK_TFLOPS, 4),
+    )
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline_muon(I, D)
+    return res
+
+
+def cpu_baseline_muon(I, D):
+    """oracle/write.newton_schulz5 (bf16 CPU torch, the reference's
+    arithmetic) on expert matrices of the pool (w0, w1, w2 in turn) until
+    about 10 s have passed, on this host's cores."""
+    import torch
+
+    from oracle import write as OW
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    gen = torch.Generator().manual_seed(1)
+    mats = [torch.randn(1, I, D, generator=gen), torch.randn(1, D, I, generator=gen)]
+    done, flops, t = 0, 0, 0.0
+    while t < 10.0 and done < 96:
+        G = mats[done % 3 == 1]
+        t0 = time.perf_counter()
+        OW.newton_schulz5(G)
+        t += time.perf_counter() - t0
+        flops += _ns5_flops(I, D)
+        done += 1
+    return dict(value=round(flops / t / 1e12, 4), unit="TFLOP/s", cores=threads, kind="port",
+                sample=f"NS5 of {done} of the 96 expert matrices ([{I}, {D}] / [{D}, {I}]) in "
+                       f"bf16 torch: {t:.2f} s ({threads} threads)", cpu=_cpu_model())
+
+
 WORKLOADS = {"permute": bench_permute,
              "moe124m": lambda a: bench_moe(a, "moe124m"),
              "moe760m": lambda a: bench_moe(a, "moe760m"),
              "dense124m": lambda a: bench_dense(a, "dense124m"),
-             "dense_c0": lambda a: bench_dense(a, "dense_c0")}
+             "dense_c0": lambda a: bench_dense(a, "dense_c0"),
+             "muon760m": bench_muon}
 DEFAULT_WORKLOAD = "moe760m"
 
 

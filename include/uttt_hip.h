@@ -329,6 +329,32 @@ int uttt_write_step(const float* master, const void* fast_in, const void* grad, 
                     int64_t rows_per_batch, int C, int seg, int norm_from_fast, int renorm_master,
                     float* master_out, void* fast_out, float* mom_out, void* stream);
 
+/* Momentum step of the Muon write on its own: out = raw + m_coeff[b] * mom
+ * (fp32; raw fp32 or bf16; B batches of per_batch elements).  Replaces the
+ * momentum lines of _apply_moe_update_dense (uttt_llm/flame/custom_models/
+ * uttt_moe/modeling_recurrent_lact.py:767-775) and of _apply_shared_update
+ * (uttt_llm/flame/custom_models/uttt_dense/modeling_recurrent_lact.py:1175-1185),
+ * whose result is both the new momentum buffer and the input of the
+ * Newton-Schulz step.  out may be mom (in place). */
+int uttt_momentum_add(const void* raw, int raw_dtype, const float* mom, const float* m_coeff,
+                      int B, int64_t per_batch, float* out, void* stream);
+
+/* Muon orthogonalisation: zeropower_via_newtonschulz5 (uttt_llm/flame/
+ * custom_models/uttt_moe/ttt_operation.py:19-46), called by the Muon writes
+ * (uttt_moe/modeling_recurrent_lact.py:777-810 with steps = 5;
+ * uttt_dense/modeling_recurrent_lact.py:1192-1203 per d x d slice).  For each
+ * of BE matrices G [rows, cols] (fp32 or bf16): X = bf16(G), transposed to
+ * [min, max] when rows > cols; X = X / (||X||_F + 1e-7); five steps of
+ * A = X X^T, B = b A + (c A) A (Python's `c * A @ A`), X = a X + B X with the reference's (a, b, c)
+ * table, every operation rounded to bf16 as the reference's bf16 tensors are;
+ * out = bf16(X * out_scale) [BE, rows, cols] bf16 (out_scale = the write's
+ * step size, which the reference applies to the bf16 result; 1 leaves X).
+ * rows and cols must be multiples of 8; the workspace is
+ * uttt_newton_schulz5_workspace_bytes(BE, rows, cols) bytes. */
+size_t uttt_newton_schulz5_workspace_bytes(int BE, int rows, int cols);
+int uttt_newton_schulz5(const void* g, int g_dtype, int BE, int rows, int cols, float out_scale,
+                        void* out, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

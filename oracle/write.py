@@ -15,9 +15,13 @@ fp32 torch on the CPU, written from the two reference call sites:
                on, and the master keeps the unprojected value unless master
                renorm is on.
 
-Muon (Newton-Schulz orthogonalisation of G) is not restated here: both call
-sites run it between the momentum and the step, and a caller that uses it
-passes the orthogonalised G with momentum off.
+newton_schulz5  zeropower_via_newtonschulz5,
+               uttt_llm/flame/custom_models/uttt_moe/ttt_operation.py:19-46 (cited N:),
+               the Muon orthogonalisation both writes run between the momentum
+               and the step when use_moun is on (M:781-810, D:1192-1203).  It
+               is bf16 tensor arithmetic in the reference, so it is restated in
+               bf16 torch on the CPU (bf16 matmuls accumulate in fp32 and round
+               their result, like the GPU's), operation by operation.
 
 Every operation follows the reference's operation order (separate multiply
 and add, divide then multiply) in fp32; only the norm reductions differ in
@@ -35,9 +39,36 @@ def _norm(x: torch.Tensor, dim: int) -> torch.Tensor:
     return x.double().pow(2).sum(dim=dim, keepdim=True).sqrt().float()
 
 
-def moe_write(grads, masterw, momentum_buf=None, m_coeff=None, lr_scale=1.0):
-    """M:754-825 without Muon.  grads, masterw: (w0, w1, w2), fp32 [B,E,R,C];
-    momentum_buf: same shapes or None; m_coeff: [B,1,1,1] or None.
+# N:34-40, the per-step (a, b, c) coefficients
+NS5_COEFFS = ((4.0848, -6.8946, 2.9270),
+              (3.9505, -6.3029, 2.6377),
+              (3.7418, -5.5913, 2.3037),
+              (2.8769, -3.1427, 1.2046),
+              (2.8366, -3.0525, 1.2012))
+
+
+def newton_schulz5(G: torch.Tensor) -> torch.Tensor:
+    """N:19-46.  G [n, R, C] (any float dtype) -> bf16 [n, R, C]."""
+    assert G.dim() == 3
+    X = G.to(torch.bfloat16)                               # N:31
+    tr = G.size(1) > G.size(2)
+    if tr:
+        X = X.transpose(1, 2)                              # N:32-33
+    X = X / (X.norm(dim=(1, 2), keepdim=True) + 1e-7)      # N:34
+    for a, b, c in NS5_COEFFS:                             # N:35-44
+        A = X @ X.transpose(1, 2)
+        B = b * A + c * A @ A                              # i.e. b A + (c A) @ A
+        X = a * X + B @ X
+    if tr:
+        X = X.transpose(1, 2)                              # N:45-46
+    return X
+
+
+def moe_write(grads, masterw, momentum_buf=None, m_coeff=None, lr_scale=1.0, use_moun=False):
+    """M:754-825.  grads, masterw: (w0, w1, w2), fp32 [B,E,R,C]; momentum_buf:
+    same shapes or None; m_coeff: [B,1,1,1] or None; use_moun: orthogonalise
+    each expert's step with newton_schulz5 (then the step is bf16 and
+    g * lr_scale is a bf16 product, as in the reference).
     Returns (fast bf16 tuple, new masters, new momentum or None)."""
     new_master, new_mom, fast = [], [], []
     use_mom = momentum_buf is not None and m_coeff is not None
@@ -48,6 +79,9 @@ def moe_write(grads, masterw, momentum_buf=None, m_coeff=None, lr_scale=1.0):
         if use_mom:
             g = g + momentum_buf[i].float() * m_coeff      # M:772-774
             new_mom.append(g.clone())                      # M:775-779
+        if use_moun:                                       # M:781-810
+            B, E, R, C = g.shape
+            g = newton_schulz5(g.reshape(B * E, R, C)).reshape(B, E, R, C)
         u = w + g * lr_scale                               # M:813-815
         p = u / (_norm(u, 3) + EPS) * nu                   # M:817-819
         new_master.append(p)
@@ -73,9 +107,10 @@ def slices_to_wide(slices: torch.Tensor, name: str, b: int, h: int, r: int) -> t
 
 
 def dense_write(agg_grads, fastw, masterw, r, momentum_buf=None, coeff=None, lr_scale=1.0,
-                master_renorm=False):
-    """D:1109-1240 without Muon.  fastw bf16, masterw fp32, shapes w0/w2
-    [b,h,r*d,d], w1 [b,h,d,r*d]; coeff: [b,1,1,1] or None.
+                master_renorm=False, use_moun=False):
+    """D:1109-1240.  fastw bf16, masterw fp32, shapes w0/w2 [b,h,r*d,d], w1
+    [b,h,d,r*d]; coeff: [b,1,1,1] or None; use_moun: orthogonalise each d x d
+    slice of the step with newton_schulz5 (D:1192-1203).
     Returns (fast bf16 tuple, new masters, new momentum or None)."""
     names = ("w0", "w1", "w2")
     b, h = fastw[0].shape[:2]
@@ -88,8 +123,10 @@ def dense_write(agg_grads, fastw, masterw, r, momentum_buf=None, coeff=None, lr_
         deltas = [dl + m.float() * coeff for dl, m in zip(deltas, momentum_buf)]  # D:1175-1178
         momentum_buf = tuple(deltas)
     delta_s = [wide_to_slices(dl, n, r) for n, dl in zip(names, deltas)]
+    if use_moun:
+        delta_s = [newton_schulz5(dl) for dl in delta_s]               # D:1192-1203
     delta_s = [dl * lr_scale for dl in delta_s]                        # D:1206-1209
-    upd = [m + dl for m, dl in zip(master_s, delta_s)]                 # D:1210-1213
+    upd = [m + dl.to(m.dtype) for m, dl in zip(master_s, delta_s)]     # D:1210-1213
     proj = [u / (_norm(u, 2) + EPS) * o for u, o in zip(upd, old)]     # D:1214-1222
     if master_renorm:
         upd = proj

@@ -106,7 +106,9 @@ def test_write_in_place_equals_out_of_place():
         assert torch.equal(a, b_)
 
 
-def test_write_refuses_muon():
+def test_muon_write_rejects_unaligned_shapes():
+    """The Newton-Schulz entry point needs rows and cols that are multiples
+    of 8 (16-byte bf16 rows); anything else is refused before any launch."""
     w = torch.zeros(1, 1, 4, 8, device=DEV)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(RuntimeError, match="multiples of 8"):
         FWW.apply_moe_update_dense((w, w, w), (w, w, w), (w, w, w), use_moun=True)

@@ -189,6 +189,44 @@ struct EpiStore {
   }
 };
 
+// --- epilogue: o = bf16(bf16(alpha * in) + bf16(beta * bf16(acc))) (no `in`:
+// o = bf16(beta * bf16(acc))), stored to `out`, and bf16(gamma * o) to `out2`
+// when given; all token-major [B, N, ld] at the product's position.  The
+// Newton-Schulz steps with the bf16 rounding after every operation that the
+// reference's bf16 tensor arithmetic has: A = X X^T (with c A as out2),
+// B = b A + (c A) A, X' = a X + B X.
+struct EpiLinComb {
+  struct Args {
+    uint16_t* out;
+    uint16_t* out2;
+    const uint16_t* in;
+    int64_t ld;
+    int col_end;
+    int N;
+    float alpha, beta, gamma;
+  };
+  __device__ __forceinline__ static void apply(const Args& ea, const f32x16 (&acc0)[2][kNB],
+                               const f32x16 (&acc1)[2][kNB], const TileCtx& c, bool two) {
+    const int64_t bo = (int64_t)c.b * ea.N * ea.ld;
+    for_quads(acc0, acc1, c.wm, c.wn, two, [&](int t, int r, int n, const float* v) __attribute__((always_inline)) {
+      const int col = c.m0 + t * kTileRows + r;
+      if (c.tt.n0 + n >= c.tt.size || col >= ea.col_end) return;
+      const int64_t tok = c.tt.start + c.tt.n0 + n;
+      float x[4] = {0.0f, 0.0f, 0.0f, 0.0f}, o[4];
+      if (ea.in != nullptr) load4(ea.in + bo, ea.ld, tok, col, x);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float p = bf16r(ea.beta * bf16r(v[u]));
+        o[u] = ea.in != nullptr ? bf16r(bf16r(ea.alpha * x[u]) + p) : p;
+      }
+      store4(ea.out + bo, ea.ld, tok, col, o[0], o[1], o[2], o[3]);
+      if (ea.out2 != nullptr)
+        store4(ea.out2 + bo, ea.ld, tok, col, ea.gamma * o[0], ea.gamma * o[1], ea.gamma * o[2],
+               ea.gamma * o[3]);
+    });
+  }
+};
+
 // --- epilogue: APPLY gate/up, h = y2 * silu(y0) (acc0 = w0 rows, acc1 = w2 rows)
 struct EpiSwiGLU {
   struct Args {
@@ -595,6 +633,84 @@ __global__ __launch_bounds__(256) void transpose16_kernel(const uint16_t* __rest
   }
 }
 
+// ============================================ Newton-Schulz orthogonalisation ==
+// Per matrix G [R, C] (BE of them): X = bf16(G) as [m, n] = [min, max] (G
+// transposed when R > C), X /= bf16(bf16(||X||_F) + 1e-7), five steps of
+// A = X X^T, B = b A + (c A) A, X = a X + B X, then bf16(X * scale) back in
+// G's orientation.  Reference: zeropower_via_newtonschulz5,
+// uttt_llm/flame/custom_models/uttt_moe/ttt_operation.py:19-46.
+constexpr int kNsParts = 64;   // partial sums of squares per matrix
+
+// part[be, p] = sum of bf16(g)^2 over the p-th of kNsParts equal slices of matrix be.
+template <class TT>
+__global__ __launch_bounds__(256) void ns_sumsq_kernel(const typename TT::S* __restrict__ g,
+                                                       int64_t elems, float* __restrict__ part) {
+  __shared__ float red[256];
+  const int be = blockIdx.y, p = blockIdx.x;
+  const int64_t per = (elems + kNsParts - 1) / kNsParts;
+  const int64_t lo = p * per, hi = lo + per < elems ? lo + per : elems;
+  const typename TT::S* gb = g + (int64_t)be * elems;
+  float acc = 0.0f;
+  for (int64_t i = lo + threadIdx.x; i < hi; i += 256) {
+    const float x = bf16r(TT::load(gb[i]));
+    acc = __builtin_fmaf(x, x, acc);
+  }
+  red[threadIdx.x] = acc;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) part[(int64_t)be * kNsParts + p] = red[0];
+}
+
+// denom[be] = bf16(bf16(sqrt(sum of parts)) + 1e-7) (fixed order); gs[be] = m.
+__global__ __launch_bounds__(256) void ns_norm_kernel(const float* __restrict__ part, int BE,
+                                                      int m, float* __restrict__ denom,
+                                                      int32_t* __restrict__ gs) {
+  const int be = blockIdx.x * 256 + threadIdx.x;
+  if (be >= BE) return;
+  float s = 0.0f;
+  for (int p = 0; p < kNsParts; ++p) s += part[(int64_t)be * kNsParts + p];
+  denom[be] = bf16r(bf16r(sqrtf(s)) + 1e-7f);
+  gs[be] = m;
+}
+
+// dst [BE, Rd, Cd] from src [BE, Rs, Cs] through 64x64 LDS tiles; TRANS: dst = src^T.
+//   PREP:  dst = bf16(bf16(src) / denom[be])
+//   FINAL: dst = bf16(src * scale)
+template <class TS, bool TRANS, bool PREP>
+__global__ __launch_bounds__(256) void ns_tile_kernel(const typename TS::S* __restrict__ src,
+                                                      int Rs, int Cs, const float* __restrict__ denom,
+                                                      float scale, uint16_t* __restrict__ dst,
+                                                      int rt, int ct) {
+  __shared__ float tile[64][65];
+  const int bid = blockIdx.x;
+  const int tc = bid % ct, tr = (bid / ct) % rt, be = bid / (ct * rt);
+  const int Rd = TRANS ? Cs : Rs, Cd = TRANS ? Rs : Cs;
+  const typename TS::S* sb = src + (int64_t)be * Rs * Cs;
+  uint16_t* db = dst + (int64_t)be * Rd * Cd;
+  const float mul = PREP ? 0.0f : scale;
+  const float dv = PREP ? denom[be] : 1.0f;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  // source tile rows/cols: the dst tile (tr, tc) maps to src tile (tc, tr) when transposing
+  const int sr0 = (TRANS ? tc : tr) * 64, sc0 = (TRANS ? tr : tc) * 64;
+  for (int yy = ty; yy < 64; yy += 4) {
+    const int r = sr0 + yy, cc = sc0 + tx;
+    float v = 0.0f;
+    if (r < Rs && cc < Cs) {
+      const float x = TS::load(sb[(int64_t)r * Cs + cc]);
+      v = PREP ? bf16r(bf16r(x) / dv) : bf16r(x * mul);
+    }
+    tile[yy][tx] = v;
+  }
+  __syncthreads();
+  for (int yy = ty; yy < 64; yy += 4) {
+    const int r = tr * 64 + yy, cc = tc * 64 + tx;
+    if (r < Rd && cc < Cd) db[(int64_t)r * Cd + cc] = f32_to_bf16(TRANS ? tile[tx][yy] : tile[yy][tx]);
+  }
+}
+
 // ------------------------------------------------------------- host side ----
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -708,6 +824,19 @@ int launch_wide(const void* a, const void* x, int K, const void* a_2, const void
   }
   typename EpiStore<OutT>::Args ea{y, M, {0, kTileRows}, {M, M}, N};
   return launch_tn<AMAJ, EpiStore<OutT>>(t, ea, B, st, what);
+}
+
+// y[b, n, m] = bf16(bf16(alpha in) + bf16(beta bf16(sum_k A(m, k) x[b, n, k]))) (and
+// y2 = bf16(gamma y) when y2), E = 1 group of N rows per batch, M rows in m-tiles of 256.
+template <int AMAJ>
+int launch_lincomb(const void* a, const void* x, int K, int M, int64_t lda, int64_t a_group,
+                   const uint16_t* in, float alpha, float beta, uint16_t* y, uint16_t* y2,
+                   float gamma, int B, int N, const int32_t* gs, hipStream_t st,
+                   const char* what) {
+  const TnArgs t = tn_args(a, a, x, K, lda, a_group, 0, kTileRows, M, M, 2 * kTileRows, M, B, 1,
+                           N, gs);
+  const EpiLinComb::Args ea{y, y2, in, M, M, N, alpha, beta, gamma};
+  return launch_tn<AMAJ, EpiLinComb>(t, ea, B, st, what);
 }
 
 WgTask wg_task(const void* p, const void* q, void* out, int X, int Y) {
@@ -1027,4 +1156,131 @@ extern "C" int uttt_transpose_2byte(const void* in, int B, int R, int C, void* o
   hipLaunchKernelGGL(transpose16_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream),
                      static_cast<const uint16_t*>(in), static_cast<uint16_t*>(out), R, C, rt, ct);
   return check_launch("transpose_2byte");
+}
+
+// ============================================================ Newton-Schulz ==
+namespace {
+struct NsWs {
+  size_t gs, denom, part, x0, x1, a, ac, bm, total;
+};
+NsWs ns_ws(int BE, int m, int n) {
+  NsWs w{};
+  size_t o = 0;
+  w.gs = o;
+  o += up256((size_t)BE * 4);
+  w.denom = o;
+  o += up256((size_t)BE * 4);
+  w.part = o;
+  o += up256((size_t)BE * kNsParts * 4);
+  w.x0 = o;
+  o += up256((size_t)BE * m * n * 2);
+  w.x1 = o;
+  o += up256((size_t)BE * m * n * 2);
+  w.a = o;
+  o += up256((size_t)BE * m * m * 2);
+  w.ac = o;
+  o += up256((size_t)BE * m * m * 2);
+  w.bm = o;
+  o += up256((size_t)BE * m * m * 2);
+  w.total = o;
+  return w;
+}
+}  // namespace
+
+extern "C" size_t uttt_newton_schulz5_workspace_bytes(int BE, int rows, int cols) {
+  if (BE <= 0 || rows <= 0 || cols <= 0) return 0;
+  const int m = rows < cols ? rows : cols, n = rows < cols ? cols : rows;
+  return ns_ws(BE, m, n).total;
+}
+
+extern "C" int uttt_newton_schulz5(const void* g, int g_dtype, int BE, int rows, int cols,
+                                   float out_scale, void* out, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+  UTTT_REQUIRE(BE >= 0 && rows >= 0 && cols >= 0, "newton_schulz5: bad sizes");
+  if (BE == 0 || rows == 0 || cols == 0) return UTTT_OK;
+  UTTT_REQUIRE(rows % 8 == 0 && cols % 8 == 0,
+               "newton_schulz5: rows=%d and cols=%d must be multiples of 8", rows, cols);
+  UTTT_REQUIRE(g && out && workspace, "newton_schulz5: null pointer");
+  UTTT_REQUIRE(aligned16(out) && aligned16(workspace), "newton_schulz5: tensors must be 16-byte aligned");
+  UTTT_REQUIRE(g_dtype == UTTT_F32 || g_dtype == UTTT_BF16,
+               "newton_schulz5: the update must be fp32 or bf16 (code %d)", g_dtype);
+  const bool trans = rows > cols;
+  const int m = trans ? cols : rows, n = trans ? rows : cols;
+  const NsWs w = ns_ws(BE, m, n);
+  UTTT_REQUIRE(workspace_bytes >= w.total, "newton_schulz5: workspace %zu < %zu bytes",
+               workspace_bytes, w.total);
+  hipStream_t st = as_stream(stream);
+  uint8_t* wb = static_cast<uint8_t*>(workspace);
+  int32_t* gs = reinterpret_cast<int32_t*>(wb + w.gs);
+  float* denom = reinterpret_cast<float*>(wb + w.denom);
+  float* part = reinterpret_cast<float*>(wb + w.part);
+  uint16_t* X = reinterpret_cast<uint16_t*>(wb + w.x0);
+  uint16_t* Xn = reinterpret_cast<uint16_t*>(wb + w.x1);
+  uint16_t* A = reinterpret_cast<uint16_t*>(wb + w.a);
+  uint16_t* Ac = reinterpret_cast<uint16_t*>(wb + w.ac);
+  uint16_t* Bm = reinterpret_cast<uint16_t*>(wb + w.bm);
+  const int64_t elems = (int64_t)m * n;
+  // 1. norm
+  UTTT_DTYPE_SWITCH_LR(g_dtype, TT, {
+    hipLaunchKernelGGL((ns_sumsq_kernel<TT>), dim3(kNsParts, BE), dim3(256), 0, st,
+                       static_cast<const typename TT::S*>(g), elems, part);
+  });
+  if (int rc = check_launch("newton_schulz5(norm)")) return rc;
+  hipLaunchKernelGGL(ns_norm_kernel, dim3((BE + 255) / 256), dim3(256), 0, st, part, BE, m, denom, gs);
+  if (int rc = check_launch("newton_schulz5(norm)")) return rc;
+  // 2. X = bf16(bf16(G') / denom), G' = G^T when rows > cols
+  {
+    const int rt = (m + 63) / 64, ct = (n + 63) / 64;
+    const int64_t blocks = (int64_t)rt * ct * BE;
+    if (int rc = check_grid(blocks, "newton_schulz5(prep)")) return rc;
+    UTTT_DTYPE_SWITCH_LR(g_dtype, TT, {
+      using S = typename TT::S;
+      if (trans)
+        hipLaunchKernelGGL((ns_tile_kernel<TT, true, true>), dim3((unsigned)blocks), dim3(256), 0,
+                           st, static_cast<const S*>(g), rows, cols, denom, 1.0f, X, rt, ct);
+      else
+        hipLaunchKernelGGL((ns_tile_kernel<TT, false, true>), dim3((unsigned)blocks), dim3(256),
+                           0, st, static_cast<const S*>(g), rows, cols, denom, 1.0f, X, rt, ct);
+    });
+    if (int rc = check_launch("newton_schulz5(prep)")) return rc;
+  }
+  // 3. five steps (the reference's coefficient table)
+  static const float kCoef[5][3] = {{4.0848f, -6.8946f, 2.9270f},
+                                    {3.9505f, -6.3029f, 2.6377f},
+                                    {3.7418f, -5.5913f, 2.3037f},
+                                    {2.8769f, -3.1427f, 1.2046f},
+                                    {2.8366f, -3.0525f, 1.2012f}};
+  for (int it = 0; it < 5; ++it) {
+    const float ca = kCoef[it][0], cb = kCoef[it][1], cc = kCoef[it][2];
+    // A = X X^T and Ac = c A  ([m, m]: x = X as m rows of K = n, A operand = X)
+    if (int rc = launch_lincomb<KMajor>(X, X, n, m, n, elems, nullptr, 0.0f, 1.0f, A, Ac, cc, BE, m,
+                                        gs, st, "newton_schulz5(X X^T)"))
+      return rc;
+    // B = b A + (c A) A  (x = Ac, A operand = A: A is symmetric, so row j of A is column j)
+    if (int rc = launch_lincomb<KMajor>(A, Ac, m, m, m, (int64_t)m * m, A, cb, 1.0f, Bm, nullptr,
+                                        0.0f, BE, m, gs, st, "newton_schulz5(B)"))
+      return rc;
+    // X' = a X + B X  ([m, n]: x = B, A operand = X read row-major: A(j, k) = X[k, j])
+    if (int rc = launch_lincomb<RMajor>(X, Bm, m, n, n, elems, X, ca, 1.0f, Xn, nullptr, 0.0f, BE,
+                                        m, gs, st, "newton_schulz5(B X)"))
+      return rc;
+    uint16_t* tmp = X;
+    X = Xn;
+    Xn = tmp;
+  }
+  // 4. out = bf16(X * scale) in G's orientation
+  {
+    const int Rd = rows, Cd = cols;
+    const int rt = (Rd + 63) / 64, ct = (Cd + 63) / 64;
+    const int64_t blocks = (int64_t)rt * ct * BE;
+    if (int rc = check_grid(blocks, "newton_schulz5(out)")) return rc;
+    if (trans)
+      hipLaunchKernelGGL((ns_tile_kernel<BF16T, true, false>), dim3((unsigned)blocks), dim3(256), 0,
+                         st, X, m, n, nullptr, out_scale, static_cast<uint16_t*>(out), rt, ct);
+    else
+      hipLaunchKernelGGL((ns_tile_kernel<BF16T, false, false>), dim3((unsigned)blocks), dim3(256),
+                         0, st, X, m, n, nullptr, out_scale, static_cast<uint16_t*>(out), rt, ct);
+    if (int rc = check_launch("newton_schulz5(out)")) return rc;
+  }
+  return UTTT_OK;
 }

@@ -118,6 +118,23 @@ __global__ __launch_bounds__(kWS) void write_step_kernel(
 
 inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
+// out = raw + m_coeff[b] * mom (fp32, the product rounded before the sum as the
+// reference's separate tensor ops do): the momentum step on its own, for the
+// Muon write, where the orthogonalisation sits between it and the write.
+template <class TT>
+__global__ __launch_bounds__(256) void momentum_add_kernel(const typename TT::S* __restrict__ raw,
+                                                           const float* __restrict__ mom,
+                                                           const float* __restrict__ m_coeff,
+                                                           int64_t per_batch, int64_t total,
+                                                           float* __restrict__ out) {
+#pragma clang fp contract(off)
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  const float c = m_coeff[i / per_batch];
+  const float p = mom[i] * c;
+  out[i] = TT::load(raw[i]) + p;
+}
+
 }  // namespace
 }  // namespace uttt
 
@@ -182,4 +199,24 @@ extern "C" int uttt_write_step(const float* master, const void* fast_in, const v
 #undef UTTT_WS_FLAGS
 #undef UTTT_WS_LAUNCH
   return check_launch("write_step");
+}
+
+extern "C" int uttt_momentum_add(const void* raw, int raw_dtype, const float* mom,
+                                 const float* m_coeff, int B, int64_t per_batch, float* out,
+                                 void* stream) {
+  UTTT_REQUIRE(B >= 0 && per_batch >= 0, "momentum_add: bad sizes");
+  const int64_t total = (int64_t)B * per_batch;
+  if (total == 0) return UTTT_OK;
+  UTTT_REQUIRE(raw && mom && m_coeff && out, "momentum_add: null pointer");
+  UTTT_REQUIRE(raw_dtype == UTTT_F32 || raw_dtype == UTTT_BF16,
+               "momentum_add: the update must be fp32 or bf16 (code %d)", raw_dtype);
+  const int64_t blocks = (total + 255) / 256;
+  UTTT_REQUIRE(blocks <= 0x7fffffffLL, "momentum_add: too many elements for one launch");
+  hipStream_t st = as_stream(stream);
+  UTTT_DTYPE_SWITCH_LR(raw_dtype, TT, {
+    hipLaunchKernelGGL((momentum_add_kernel<TT>), dim3((unsigned)blocks), dim3(256), 0, st,
+                       static_cast<const typename TT::S*>(raw), mom, m_coeff, per_batch, total,
+                       out);
+  });
+  return check_launch("momentum_add");
 }

@@ -9,8 +9,11 @@ write methods (self's configuration becomes keyword arguments):
                             uttt_llm/flame/custom_models/uttt_dense/modeling_recurrent_lact.py:1109-1240
 
 Both return freshly allocated (fast bf16, master fp32, momentum) tuples and
-never modify their inputs, as the reference does.  Muon (Newton-Schulz
-orthogonalisation of the step) is not built: asking for it raises.
+never modify their inputs, as the reference does.  With use_moun the step is
+orthogonalised between the momentum and the write (newton_schulz5 below):
+the momentum runs on its own kernel, Newton-Schulz on the grouped GEMMs, and
+the write takes the bf16 result with the step size already applied, as the
+reference's bf16 `g * lr_scale` is.
 """
 from __future__ import annotations
 
@@ -42,6 +45,35 @@ def _write_one(master, grad, mom, m_coeff_b, lr_scale, rows, C, seg, fast_in, re
     return fast_out, master_out, mom_out
 
 
+def newton_schulz5(G, out_scale=1.0):
+    """zeropower_via_newtonschulz5 (uttt_llm/flame/custom_models/uttt_moe/
+    ttt_operation.py:19-46) on the gfx950 kernels: G [n, R, C] fp32 or bf16 ->
+    bf16(NS5(G) * out_scale) [n, R, C]."""
+    L.require_device(G)
+    assert G.dim() == 3, "G must be [n, R, C]"
+    assert G.dtype in (torch.float32, torch.bfloat16), "G must be fp32 or bf16"
+    G = G.contiguous()
+    n, R, C = G.shape
+    out = torch.empty((n, R, C), dtype=torch.bfloat16, device=G.device)
+    nbytes = L.lib().uttt_newton_schulz5_workspace_bytes(n, R, C)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=G.device)
+    L.call("uttt_newton_schulz5", L.ptr(G), L.dtype_code(G.dtype), n, R, C, float(out_scale),
+           L.ptr(out), L.ptr(ws), nbytes, L.stream_of(G))
+    return out
+
+
+def _momentum(g, mom, coeff_b):
+    """g + mom * m_coeff[b] (fp32), the new momentum buffer."""
+    L.require_device(g, mom, coeff_b)
+    g, mom = g.contiguous(), mom.contiguous()
+    assert mom.dtype == torch.float32 and mom.shape == g.shape
+    out = torch.empty(g.shape, dtype=torch.float32, device=g.device)
+    B = g.shape[0]
+    L.call("uttt_momentum_add", L.ptr(g), L.dtype_code(g.dtype), L.ptr(mom), L.ptr(coeff_b), B,
+           g.numel() // max(B, 1), L.ptr(out), L.stream_of(g))
+    return out
+
+
 def _coeff_per_batch(m_coeff, B, device):
     c = m_coeff.to(device=device, dtype=torch.float32).reshape(-1).contiguous()
     assert c.numel() == B, f"momentum coefficient must hold one value per batch, got {c.numel()}"
@@ -55,8 +87,6 @@ def apply_moe_update_dense(grads, fastw, masterw, momentum_buf=None, m_coeff=Non
     fp32 tuple or None; m_coeff: [B,1,1,1] or None.  `fastw` is accepted for
     signature parity; the new fast weights are bf16 of the new masters.
     Returns (fast, master, momentum_buf)."""
-    if use_moun:
-        raise NotImplementedError("the Muon (Newton-Schulz) write is not built on gfx950")
     del fastw
     use_mom = use_momentum and momentum_buf is not None and m_coeff is not None
     B = masterw[0].shape[0]
@@ -65,11 +95,19 @@ def apply_moe_update_dense(grads, fastw, masterw, momentum_buf=None, m_coeff=Non
     for i, (g, w) in enumerate(zip(grads, masterw)):
         assert w.dim() == 4, "masters are [B, E, R, C]"
         _, E, R, C = w.shape
-        f, m, mo = _write_one(w.contiguous(), g.contiguous(), momentum_buf[i].contiguous() if use_mom else None,
-                              coeff, lr_scale, E * R, C, C, None, True)
+        if use_moun:                               # M:781-810, then M:813-815
+            if use_mom:
+                g = _momentum(g, momentum_buf[i], coeff)
+                mom.append(g)
+            step = newton_schulz5(g.reshape(B * E, R, C), lr_scale).reshape(g.shape)
+            f, m, _ = _write_one(w.contiguous(), step, None, None, 1.0, E * R, C, C, None, True)
+        else:
+            f, m, mo = _write_one(w.contiguous(), g.contiguous(),
+                                  momentum_buf[i].contiguous() if use_mom else None, coeff,
+                                  lr_scale, E * R, C, C, None, True)
+            mom.append(mo)
         fast.append(f)
         master.append(m)
-        mom.append(mo)
     return tuple(fast), tuple(master), (tuple(mom) if use_mom else momentum_buf)
 
 
@@ -80,8 +118,6 @@ def apply_shared_update(agg_grads, fastw, masterw, momentum_buf=None, momentum_c
     [b,h,r*d,d], w1 [b,h,d,r*d]; every d x d slice is written on its own, so a
     w1 row is cut into r segments of d.  momentum_coeffs: a tensor, a list of
     per-layer tensors (averaged) or None.  Returns (fast, master, momentum_buf)."""
-    if use_moun:
-        raise NotImplementedError("the Muon (Newton-Schulz) write is not built on gfx950")
     if len(agg_grads) != 3 or len(fastw) != 3 or len(masterw) != 3:
         raise ValueError("uTTT-Dense expects three fast-weight matrices")
     b, h, inter, d = fastw[0].shape
@@ -100,10 +136,38 @@ def apply_shared_update(agg_grads, fastw, masterw, momentum_buf=None, momentum_c
     for i, name in enumerate(_NAMES):
         w = masterw[i].contiguous()
         rows, C = (h * r * d, d) if name != "w1" else (h * d, r * d)
-        f, m, mo = _write_one(w, agg_grads[i].contiguous(),
-                              momentum_buf[i].contiguous() if use_mom else None, cb, lr_scale,
-                              rows, C, d, None if master_renorm else fastw[i], master_renorm)
+        norm_src = None if master_renorm else fastw[i]
+        if use_moun:                               # D:1175-1185, D:1192-1209
+            g = agg_grads[i]
+            if use_mom:
+                g = _momentum(g, momentum_buf[i], cb)
+                mom.append(g)
+            step = _slices_to_wide(newton_schulz5(_wide_to_slices(g, name, r), lr_scale),
+                                   name, b, h, r)
+            f, m, _ = _write_one(w, step, None, None, 1.0, rows, C, d, norm_src, master_renorm)
+        else:
+            f, m, mo = _write_one(w, agg_grads[i].contiguous(),
+                                  momentum_buf[i].contiguous() if use_mom else None, cb, lr_scale,
+                                  rows, C, d, norm_src, master_renorm)
+            mom.append(mo)
         fast.append(f)
         master.append(m)
-        mom.append(mo)
     return tuple(fast), tuple(master), (tuple(mom) if use_mom else momentum_buf)
+
+
+def _wide_to_slices(x, name, r):
+    """D:1068-1086 layout: [b,h,r*d,d] (w0, w2) or [b,h,d,r*d] (w1) -> [b*h*r, d, d]
+    (a copy for w1, whose slices are column blocks)."""
+    if name != "w1":
+        b, h, inter, d = x.shape
+        return x.reshape(b * h * r, d, d)
+    b, h, d, inter = x.shape
+    return x.reshape(b, h, d, r, d).permute(0, 1, 3, 2, 4).reshape(b * h * r, d, d)
+
+
+def _slices_to_wide(s, name, b, h, r):
+    """D:1088-1106, the inverse of _wide_to_slices (contiguous)."""
+    d = s.shape[-1]
+    if name != "w1":
+        return s.reshape(b, h, r * d, d)
+    return s.reshape(b, h, r, d, d).permute(0, 1, 3, 2, 4).reshape(b, h, d, r * d).contiguous()
