@@ -20,6 +20,9 @@ in HBM before the timed region starts):
             head (H=4, d=192, hidden 384), 12 layers, aggregate write.
   dense_c0  configs[0]'s single-layer shape (H=4, d=96, hidden 192, chunks of
             512) on the GPU.
+  decode760m generation-time read at the 760M shape: 8 sequences with their
+            own pools, one token each through 24 layers (router + routed
+            SwiGLU read); value = tokens/s.
   muon760m  the Muon write of one chunk on the 760M pool (momentum,
             Newton-Schulz5 of the 96 expert matrices, scaled add,
             norm-preserving write); value = NS5 algorithmic TFLOP/s.
@@ -923,6 +926,146 @@ def cpu_baseline_dense(cfg, sets, w):
                 sample=sample + f" (fp32 torch, {threads} threads)", cpu=_cpu_model())
 
 
+# ---------------------------------------------------------- decode read --
+def bench_decode(args):
+    """Generation-time fast-weight read at the 760M shape: B = 8 sequences,
+    each with its own expert pool (E=32, W0_W2 [6144, 1536], W1 [1536, 3072]),
+    one new token per sequence through 24 layers.  A step = per layer, the
+    fused router (shared router weights, Zipf(1.1) expert prior as selection
+    bias, top-2, topk_renorm gates) and the decode read; value = tokens/s.
+    The dominant cost is streaming each token's two experts' weights."""
+    import torch
+
+    from uttt_amd import _lib as L
+    from uttt_amd import decode as DEC
+    from uttt_amd.lact_moe_triton import lact_swiglu_ffn as SF
+    from uttt_amd.lact_moe_triton import triton_permute as TP
+    from uttt_amd.routing import route_tokens
+
+    dev = torch.device("cuda", 0)
+    B, T, E, k, D, I, layers = 8, 1, 32, 2, 1536, 3072, 24
+    g = torch.Generator(device=dev).manual_seed(0)
+    bf = torch.bfloat16
+    W02 = (torch.randn(B, E, 2 * I, D, generator=g, device=dev) * D ** -0.5).to(bf)
+    W1 = (torch.randn(B, E, D, I, generator=g, device=dev) * I ** -0.5).to(bf)
+    xs = []
+    for _ in range(layers):
+        t = torch.randn(B, T, D, generator=g, device=dev)
+        xs.append((t / (t.norm(dim=-1, keepdim=True) + 1e-5)).to(bf))
+    R = torch.randn(E, D, generator=g, device=dev)
+    rbias = -1.1 * torch.log(torch.arange(E, device=dev, dtype=torch.float32) + 1)
+    routed = [None] * layers
+
+    def step():
+        for l in range(layers):
+            mask, _, probs, _ = route_tokens(xs[l], R, k, combine_mode="topk_renorm",
+                                             routing_bias=rbias)
+            routed[l] = (mask, probs)
+            DEC.moe_decode_read(xs[l], W02, W1, mask, probs, k)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = _events(2)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    t_step = e0.elapsed_time(e1) * 1e-3 / args.steps
+
+    # the read alone (two launches per call), back to back over the layers'
+    # routings, and its algorithmic bytes: every selected (sequence, expert)
+    # pair's W0_W2 and W1 once, plus x, the mask, the gates and the output
+    reps = max(3, args.steps)
+    nsel = sum(int(m.any(dim=2).sum().item()) for m, _ in routed)
+    bytes_read = (nsel * 3 * I * D * 2 + layers * (2 * B * T * D * 2 + B * E * T * 5)) // layers
+    e0.record()
+    for _ in range(reps):
+        for l in range(layers):
+            DEC.moe_decode_read(xs[l], W02, W1, *routed[l], k)
+    e1.record()
+    torch.cuda.synchronize()
+    t_read = e0.elapsed_time(e1) * 1e-3 / (reps * layers)
+
+    # the same read through the grouped path (row map, permute, grouped
+    # SwiGLU apply, unpermute), for comparison
+    def grouped(l):
+        mask, probs = routed[l]
+        xp, _, rmap = TP.permute_with_expert_mask(xs[l], mask, probs, k)
+        y = SF.grouped_swiglu_ffn_fwd(W02, W1, xp, mask.sum(-1).to(torch.int32))
+        return TP.unpermute_and_merge_with_probs(y, rmap, probs)
+
+    ref = grouped(0)
+    ours = DEC.moe_decode_read(xs[0], W02, W1, *routed[0], k)
+    err = (ours.float() - ref.float()).abs().max().item()
+    assert err <= 2e-2 * ref.float().abs().max().item() + 1e-3, f"decode read diverged: {err}"
+    e0.record()
+    for _ in range(reps):
+        for l in range(layers):
+            grouped(l)
+    e1.record()
+    torch.cuda.synchronize()
+    t_grouped = e0.elapsed_time(e1) * 1e-3 / (reps * layers)
+
+    res = dict(
+        metric="fast-weight decode read tokens/s (760M pool per sequence)",
+        value=round(B * T / t_step, 1), unit="tokens/s",
+        ms_per_step=round(t_step * 1e3, 4), wall_ms_per_step=round(wall / args.steps * 1e3, 4),
+        dtype="bf16",
+        config={"workload": "uTTT-MoE 760M decode read: router + routed SwiGLU read, 24 layers",
+                "sequences": B, "tokens_per_step": T, "layers": layers, "experts": E, "topk": k,
+                "d": D, "expert_hidden": I, "routing": "shared router, Zipf(1.1) selection bias"},
+        roofline=dict(bound="hbm", kernel="moe_decode_read (gate/up + down launches)",
+                      achieved=round(bytes_read / t_read / 1e9, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                      frac=round(bytes_read / t_read / 1e9 / HBM_PEAK_GBS, 4),
+                      traffic=_profile_traffic("decode_read_760m.txt", "moe_decode_read"),
+                      algorithmic_bytes=bytes_read, avg_call_us=round(t_read * 1e6, 2)),
+        kernels={"decode read per layer": dict(us=round(t_read * 1e6, 2)),
+                 "router per layer": dict(us=round((t_step / layers - t_read) * 1e6, 2),
+                                          timing="step minus read"),
+                 "grouped path per layer (row map, permute, apply, unpermute)":
+                     dict(us=round(t_grouped * 1e6, 2))},
+    )
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline_decode(W02, W1, xs, routed, k, layers)
+    return res
+
+
+def cpu_baseline_decode(W02, W1, xs, routed, k, layers):
+    """oracle/moe_read.apply_moe_grouped (fp32 torch: permute, grouped apply,
+    unpermute) on this host's cores, layer by layer for about 10 s; the step
+    is extrapolated to all layers."""
+    import torch
+
+    from oracle import moe_read as MR
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    B = xs[0].shape[0]
+    t, done = 0.0, 0
+    while t < 10.0 and done < layers:
+        mask, probs = routed[done]
+        for b in range(B):
+            # only the sequence's selected experts travel to the host; their
+            # ascending order keeps the merge's slot order
+            sel = mask[b].any(dim=1).nonzero().flatten()
+            x = xs[done][b:b + 1].cpu()
+            w02, w1 = W02[b:b + 1, sel].cpu(), W1[b:b + 1, sel].cpu()
+            m, p = mask[b:b + 1, sel].cpu(), probs[b:b + 1, sel].cpu()
+            t0 = time.perf_counter()
+            MR.apply_moe_grouped(x, w02, w1, m, p, k, fast=True)
+            t += time.perf_counter() - t0
+        done += 1
+    per_layer = t / done
+    return dict(value=round(B / (per_layer * layers), 2), unit="tokens/s", cores=threads,
+                kind="port", sample=f"{done} of {layers} layers' reads in fp32 torch "
+                                    f"({per_layer * 1e3:.0f} ms each, {threads} threads); "
+                                    f"step extrapolated x{layers} layers", cpu=_cpu_model())
+
+
 # ------------------------------------------------------------ Muon write --
 def _ns5_flops(R, C):
     """Algorithmic FLOP of one Newton-Schulz5 of an R x C matrix (m = short
@@ -1036,7 +1179,8 @@ WORKLOADS = {"permute": bench_permute,
              "moe760m": lambda a: bench_moe(a, "moe760m"),
              "dense124m": lambda a: bench_dense(a, "dense124m"),
              "dense_c0": lambda a: bench_dense(a, "dense_c0"),
-             "muon760m": bench_muon}
+             "muon760m": bench_muon,
+             "decode760m": bench_decode}
 DEFAULT_WORKLOAD = "moe760m"
 
 

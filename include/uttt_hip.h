@@ -355,6 +355,26 @@ size_t uttt_newton_schulz5_workspace_bytes(int BE, int rows, int cols);
 int uttt_newton_schulz5(const void* g, int g_dtype, int BE, int rows, int cols, float out_scale,
                         void* out, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Routed SwiGLU read for a few tokens per sequence (generation): the part of
+ * FastWeightMLPSubNN._apply_moe_fast_weights_grouped (uttt_llm/flame/
+ * custom_models/uttt_moe/modeling_recurrent_lact.py:330-349) after routing --
+ * _permute_with_expert_mask, _grouped_swiglu_ffn_fwd (L/lact_swiglu_ffn.py:
+ * 37-61) and _unpermute_and_merge_with_probs -- fused for T <= 64 tokens per
+ * batch, with no row map or permuted copy.  x [B, T, D] bf16; w0_w2
+ * [B, E, 2I, D] and w1 [B, E, D, I] bf16 (contiguous); expert_mask [B, E, T]
+ * (element size mask_bytes = 1 or 4, any strides), probs [B, E, T] fp32 (any
+ * strides).  out[b, t] = bf16(sum over the token's experts in descending order
+ * of fma(bf16(w1 h), p)), h = bf16(silu(w0 x) * (w2 x)): the reference's
+ * rounding points.  E <= 64, T <= 64, D and I multiples of 8 and at most 4096;
+ * topk sets the launch width (any number of selected experts is handled).
+ * The workspace is uttt_moe_decode_read_workspace_bytes(B, T, E, I) bytes. */
+size_t uttt_moe_decode_read_workspace_bytes(int B, int T, int E, int I);
+int uttt_moe_decode_read(const void* x, int B, int T, int D, const void* w0_w2, const void* w1,
+                         int E, int I, const void* expert_mask, int mask_bytes, int64_t m_sb,
+                         int64_t m_se, int64_t m_st, const float* probs, int64_t p_sb,
+                         int64_t p_se, int64_t p_st, int topk, void* out, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -120,6 +120,12 @@ SIGNATURES = {
         c_int,
         [c_p, c_int, c_int, c_int, c_int, ctypes.c_float, c_p, c_p, ctypes.c_size_t, c_p],
     ),
+    "uttt_moe_decode_read_workspace_bytes": (c_sz, [c_int, c_int, c_int, c_int]),
+    "uttt_moe_decode_read": (
+        c_int,
+        [c_p, c_int, c_int, c_int, c_p, c_p, c_int, c_int, c_p, c_int, c_i64, c_i64, c_i64,
+         c_p, c_i64, c_i64, c_i64, c_int, c_p, c_p, c_sz, c_p],
+    ),
 }
 
 _lib = None

@@ -232,8 +232,7 @@ __device__ __forceinline__ void load8(const typename XT::S* p, int d, int D, boo
 // Wave w of NW covers the feature range [w*D/NW, (w+1)*D/NW) in chunks of 16:
 // lane (r = lane % 32, h = lane / 32) feeds token t0 + r and expert 32*j + r
 // with features d0 + 8h + s for s < 8, one MFMA per s (the k index of the
-// MFMA is h, so each chunk's 16 features enter exactly once).  The next
-// chunk's operands are loaded before the current chunk's MFMAs issue.
+// MFMA is h, so each chunk's 16 features enter exactly once).
 // Accumulator element v of lane l is (token 8*(v/4) + 4*(l/32) + v%4,
 // expert l%32).  The NW partial sums are added in wave order in LDS.
 template <class XT, int NET, int NW>
@@ -258,7 +257,6 @@ __global__ __launch_bounds__(NW * kWave) void router_mfma_kernel(
   f32x16_t acc[NET];
 #pragma unroll
   for (int j = 0; j < NET; ++j) acc[j] = f32x16_t{};
-  float xa[8], wa[NET][8];
   auto fetch = [&](int c, float (&xo)[8], float (&wo)[NET][8]) __attribute__((always_inline)) {
     const int d = c * 16 + 8 * h;
     const bool in = c < c_hi;
@@ -269,20 +267,23 @@ __global__ __launch_bounds__(NW * kWave) void router_mfma_kernel(
       load8<F32T>(R + (int64_t)(e < E ? e : 0) * D, d, D, in && e < E, wo[j]);
     }
   };
-  if (c_lo < c_hi) fetch(c_lo, xa, wa);
-  for (int c = c_lo; c < c_hi; ++c) {
-    float xn[8], wn[NET][8];
-    fetch(c + 1, xn, wn);   // zeros past this wave's range
+  // a ring of DEPTH chunks in flight: each chunk's slot is refilled with the
+  // chunk DEPTH ahead right after its MFMAs issue, so a wave waits on about
+  // (its chunks / DEPTH) load latencies; slots past the range hold zeros,
+  // whose MFMAs add nothing
+  constexpr int DEPTH = NET <= 2 ? 4 : 2;
+  float xr[DEPTH][8], wr[DEPTH][NET][8];
 #pragma unroll
-    for (int j = 0; j < NET; ++j)
+  for (int q = 0; q < DEPTH; ++q) fetch(c_lo + q, xr[q], wr[q]);
+  for (int c = c_lo; c < c_hi; c += DEPTH) {
 #pragma unroll
-      for (int s8 = 0; s8 < 8; ++s8)
-        acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[s8], wa[j][s8], acc[j], 0, 0, 0);
+    for (int q = 0; q < DEPTH; ++q) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      xa[i] = xn[i];
+      for (int j = 0; j < NET; ++j)
 #pragma unroll
-      for (int j = 0; j < NET; ++j) wa[j][i] = wn[j][i];
+        for (int s8 = 0; s8 < 8; ++s8)
+          acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(xr[q][s8], wr[q][j][s8], acc[j], 0, 0, 0);
+      fetch(c + q + DEPTH, xr[q], wr[q]);
     }
   }
 #pragma unroll
