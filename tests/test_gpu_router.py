@@ -110,6 +110,43 @@ def test_route_tokens_fused(dtype, D, E, T):
         assert ((top[:, k - 1] - top[:, k])[diff].abs() < 1e-4 * scale).all()
 
 
+@pytest.mark.parametrize("B,T,D,E,k,dtype", [
+    (8, 1, 1536, 32, 2, torch.bfloat16),   # the 760M decode step
+    (3, 5, 768, 16, 2, torch.bfloat16),
+    (2, 3, 100, 64, 4, torch.float32),     # two experts per lane, ragged D
+    (2, 7, 256, 128, 3, torch.bfloat16),   # matrix-core logits for E > 64
+    (2, 40, 128, 7, 2, torch.bfloat16),    # two blocks per batch
+])
+@pytest.mark.parametrize("rt", ["softmax", "norm_softmax", "norm_relu"])
+def test_route_tokens_few_tokens(B, T, D, E, k, dtype, rt):
+    """Generation-sized batches (the vector-ALU logits) and every router type:
+    the selection on the kernel's own logits against the oracle's."""
+    g = torch.Generator().manual_seed(B * 1000 + T * 10 + E)
+    x = torch.randn(B, T, D, generator=g)
+    x = (x / x.norm(dim=-1, keepdim=True)).to(dtype)
+    Rw = torch.randn(E, D, generator=g)
+    bias = torch.randn(B, E, 1, generator=g) * 0.5
+    mask, gs, comb, bal, lg = RT.route_tokens(x.to(DEV), Rw.to(DEV), k, routing_bias=bias.to(DEV),
+                                              router_type=rt, combine_mode="topk_renorm",
+                                              return_logits=True)
+    ref_lg = OR.router_logits(x, Rw)
+    scale = Rw.norm(dim=1).max().item() * x.float().norm(dim=-1).max().item()
+    assert (lg.cpu().double() - ref_lg).abs().max().item() < 1e-4 * scale
+    own = lg.cpu()
+    ref = OR.create_router_mask_sizes_probs(own, k, router_type=rt, routing_bias=bias,
+                                            combine_mode="topk_renorm")
+    # lb_loss of the same selection through the given-logits entry (one block per batch)
+    lb = RT.create_router_mask_sizes_probs(lg, k, router_type=rt, routing_bias=bias.to(DEV),
+                                           combine_mode="topk_renorm")[4]
+    sel = own
+    if rt != "softmax":
+        z = own / own.norm(dim=1, keepdim=True).clamp_min(1e-6) * (E ** 0.5)
+        sel = z if rt == "norm_softmax" else z.clamp_min(0)
+    else:
+        assert torch.equal(mask.cpu(), ref[0]) and torch.equal(gs.cpu(), ref[1])
+    _cmp((mask, gs, comb, bal, lb), ref, k, sel, bias)
+
+
 def test_router_errors():
     l = torch.randn(1, 4, 8, device=DEV)
     with pytest.raises(NotImplementedError):

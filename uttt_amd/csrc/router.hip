@@ -21,12 +21,14 @@
 // Kernels:
 //   router_select_kernel : one thread per token, logits given ([B,E,T] strided);
 //   router_mfma_kernel   : logits = R x^T for 32 tokens x all experts per
-//                          workgroup on the fp32 matrix cores (the four waves
-//                          take a quarter of D each), then the selection of
-//                          those tokens;
+//                          workgroup (fp32 matrix cores, the waves splitting
+//                          D; for batches of at most 8 tokens the vector ALU,
+//                          with no padded rows), then the selection of those
+//                          tokens with 32 lanes per token;
 //   router_reduce_kernel : one workgroup per (batch, expert) adds the select
 //                          blocks' partial counts and balance sums with a
-//                          fixed tree (deterministic: no atomics);
+//                          fixed tree (deterministic: no atomics); skipped
+//                          when a batch is one block, whose sums are final;
 //   router_lb_kernel     : lb_loss from those sums.
 #include "common.h"
 
@@ -47,7 +49,26 @@ struct SelectArgs {
   float* part_bal;    // [B, nblk, E]
   int32_t* part_cnt;  // [B, nblk, E]
   int nblk;
+  // with one block per batch the block's sums are final and go here directly
+  int32_t* group_sizes;  // [B, E] or null
+  float* bal_sum;        // [B, E]
+  int32_t* cnt_sum;      // [B, E]
 };
+
+// Where block blk of batch b leaves its per-expert sums for expert e.
+__device__ __forceinline__ void put_partial(const SelectArgs& a, int b, int blk, int e, float s,
+                                            int c) {
+  if (a.nblk == 1) {
+    const int64_t o = (int64_t)b * a.E + e;
+    a.bal_sum[o] = s;
+    a.cnt_sum[o] = c;
+    if (a.group_sizes != nullptr) a.group_sizes[o] = c;
+  } else {
+    const int64_t o = ((int64_t)b * a.nblk + blk) * a.E + e;
+    a.part_bal[o] = s;
+    a.part_cnt[o] = c;
+  }
+}
 
 template <int EB>
 using MaskBits = uint32_t[(EB + 31) / 32];
@@ -168,9 +189,7 @@ __device__ __forceinline__ void block_partials(const float (&bal)[EB], const Mas
       s += sb[i][e];
       c += sc[i][e];
     }
-    const int64_t o = ((int64_t)b * a.nblk + blk) * a.E + e;
-    a.part_bal[o] = s;
-    a.part_cnt[o] = c;
+    put_partial(a, b, blk, e, s, c);
   }
 }
 
@@ -225,96 +244,269 @@ __device__ __forceinline__ void load8(const typename XT::S* p, int d, int D, boo
   }
 }
 
-// Fused router: logits of 32 tokens x NET*32 experts on the fp32 matrix cores
-// (v_mfma_f32_32x32x2_f32: exact fp32 products, fp32 accumulation), then the
-// selection of those 32 tokens in the same workgroup.
+// Reductions over the 32 lanes of a half-wave (fixed xor butterflies).
+__device__ __forceinline__ float half_sum(float v) {
+#pragma unroll
+  for (int o = 16; o >= 1; o >>= 1) v += __shfl_xor(v, o, 32);
+  return v;
+}
+__device__ __forceinline__ float half_max(float v) {
+#pragma unroll
+  for (int o = 16; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 32));
+  return v;
+}
+// The larger score, equal scores resolved to the lower expert index.
+__device__ __forceinline__ void half_argmax(float& v, int& i) {
+#pragma unroll
+  for (int o = 16; o >= 1; o >>= 1) {
+    const float ov = __shfl_xor(v, o, 32);
+    const int oi = __shfl_xor(i, o, 32);
+    if (ov > v || (ov == v && oi < i)) {
+      v = ov;
+      i = oi;
+    }
+  }
+}
+
+// The selection of select_token for one token on the 32 lanes of a half-wave:
+// lane j holds experts j, j + 32, ... (lg[q] = logit of expert j + 32q).
+// Same scores, balance, top-k (k arg-max passes, equal scores to the lower
+// expert index) and combine weights; the sums over experts are butterflies.
+// Writes the token's mask / balance / combine entries when live, and its row
+// of the block partials (zeros when not live).
+template <int NET>
+__device__ __forceinline__ void select_lanes(const float (&lg)[NET], const SelectArgs& a, int b,
+                                             int t, bool live, int j, float* sb_row,
+                                             uint8_t* sc_row) {
+  const int E = a.E;
+  float v[NET];
+  bool ok[NET];
+#pragma unroll
+  for (int q = 0; q < NET; ++q) {
+    ok[q] = j + 32 * q < E;
+    v[q] = ok[q] ? lg[q] : 0.0f;
+  }
+  if (a.router_type != 0) {   // v <- selection scores
+    float ss = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NET; ++q) ss += v[q] * v[q];
+    const float n = fmaxf(sqrtf(half_sum(ss)), a.norm_eps);
+#pragma unroll
+    for (int q = 0; q < NET; ++q) {
+      const float z = v[q] / n;
+      v[q] = ok[q] ? (a.router_type == 1 ? z : fmaxf(z, 0.0f)) * a.scale : 0.0f;
+    }
+  }
+  float bal[NET];
+  if (a.router_type == 2) {
+    float s = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NET; ++q) s += v[q];
+    s = half_sum(s);
+    const float den = fmaxf(s, 1e-9f);
+#pragma unroll
+    for (int q = 0; q < NET; ++q) bal[q] = ok[q] ? (s > 0.0f ? v[q] / den : 1.0f / (float)E) : 0.0f;
+  } else {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < NET; ++q)
+      if (ok[q]) mx = fmaxf(mx, v[q]);
+    mx = half_max(mx);
+    float s = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NET; ++q) {
+      bal[q] = ok[q] ? expf(v[q] - mx) : 0.0f;
+      s += bal[q];
+    }
+    s = half_sum(s);
+#pragma unroll
+    for (int q = 0; q < NET; ++q) bal[q] = bal[q] / s;
+  }
+  const float* bias = a.bias != nullptr ? a.bias + (int64_t)b * a.bias_sb : nullptr;
+  float r[NET];
+  bool sel[NET];
+#pragma unroll
+  for (int q = 0; q < NET; ++q) {
+    r[q] = ok[q] ? (bias != nullptr ? v[q] + bias[j + 32 * q] : v[q]) : -INFINITY;
+    sel[q] = false;
+  }
+  for (int k = 0; k < a.topk; ++k) {
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;   // no candidate
+#pragma unroll
+    for (int q = 0; q < NET; ++q) {
+      const bool cand = ok[q] && !sel[q] && (bi == 0x7fffffff || r[q] > bv);
+      bv = cand ? r[q] : bv;
+      bi = cand ? j + 32 * q : bi;
+    }
+    half_argmax(bv, bi);
+#pragma unroll
+    for (int q = 0; q < NET; ++q) sel[q] = sel[q] || (j + 32 * q == bi);
+  }
+  float rsum = 0.0f;
+  if (a.combine_mode == 1) {
+#pragma unroll
+    for (int q = 0; q < NET; ++q) rsum += sel[q] ? bal[q] : 0.0f;
+    rsum = half_sum(rsum);
+  }
+  const float rden = fmaxf(rsum, 1e-9f);
+  const int64_t base = (int64_t)b * E * a.T + t;
+#pragma unroll
+  for (int q = 0; q < NET; ++q) {
+    if (!ok[q]) continue;
+    const int e = j + 32 * q;
+    if (live) {
+      const int64_t i = base + (int64_t)e * a.T;
+      a.mask[i] = sel[q] ? 1 : 0;
+      a.balance[i] = bal[q];
+      const float c = a.combine_mode == 1 ? (sel[q] ? bal[q] : 0.0f) / rden : bal[q];
+      a.combine[i] = c * a.alpha;
+    }
+    sb_row[e] = live ? bal[q] : 0.0f;
+    sc_row[e] = (live && sel[q]) ? 1 : 0;
+  }
+}
+
+// Fused router for a block of 32 tokens x NET*32 experts: logits, then the
+// selection of those tokens in the same workgroup.
 //
-// Wave w of NW covers the feature range [w*D/NW, (w+1)*D/NW) in chunks of 16:
-// lane (r = lane % 32, h = lane / 32) feeds token t0 + r and expert 32*j + r
-// with features d0 + 8h + s for s < 8, one MFMA per s (the k index of the
-// MFMA is h, so each chunk's 16 features enter exactly once).
-// Accumulator element v of lane l is (token 8*(v/4) + 4*(l/32) + v%4,
-// expert l%32).  The NW partial sums are added in wave order in LDS.
-template <class XT, int NET, int NW>
+// Logits, full blocks (SMALL = false): on the fp32 matrix cores
+// (v_mfma_f32_32x32x2_f32: exact fp32 products, fp32 accumulation).  Wave w
+// of NW covers the feature range [w*D/NW, (w+1)*D/NW) in chunks of 16: lane
+// (r = lane % 32, h = lane / 32) feeds token t0 + r and expert 32*j + r with
+// features d0 + 8h + s for s < 8, one MFMA per s (the k index of the MFMA is
+// h, so each chunk's 16 features enter exactly once).  Accumulator element v
+// of lane l is (token 8*(v/4) + 4*(l/32) + v%4, expert l%32).  The NW partial
+// sums are added in wave order in LDS.
+// Logits, batches of at most kSmallT tokens (SMALL, NET <= 2, NW = 8): on the
+// vector ALU, so no MFMA work is spent on padding rows; thread i takes expert
+// i / TPE and the 8-feature chunks i % TPE + TPE*m, and the TPE partial dot
+// products of an expert are summed with a butterfly.
+// Selection: 32 lanes per token (select_lanes), NW*2 tokens at a time.
+constexpr int kSmallT = 8;
+template <class XT, int NET, int NW, bool SMALL>
 __global__ __launch_bounds__(NW * kWave) void router_mfma_kernel(
     const typename XT::S* __restrict__ x, const float* __restrict__ rw, int64_t w_sb, int D,
     float* __restrict__ logits_out, SelectArgs a) {
   constexpr int EB = NET * 32;
-  __shared__ float red[NW][NET][32][33];
+  constexpr int NTH = NW * kWave;
+  __shared__ float red[SMALL ? 1 : NW][NET][32][33];
   __shared__ float sb[32][EB + 1];
   __shared__ uint8_t sc[32][EB + 1];
   const int blk = blockIdx.x, b = blockIdx.y;
   const int t0 = blk * 32;
   const int w = threadIdx.x / kWave, lane = lane_id();
-  const int r = lane % 32, h = lane / 32;
   const int E = a.E, T = a.T;
-  const bool tv = t0 + r < T;
-  const typename XT::S* xrow = x + ((int64_t)b * T + (tv ? t0 + r : 0)) * D;
   const float* R = rw + (int64_t)b * w_sb;
-  const int nch = (D + 15) / 16;
-  const int per = (nch + NW - 1) / NW;
-  const int c_lo = w * per, c_hi = min(nch, c_lo + per);
-  f32x16_t acc[NET];
+  if constexpr (SMALL) {
+    static_assert(NTH % EB == 0, "threads must split evenly over the experts");
+    constexpr int TPE = NTH / EB;
+    const int e = threadIdx.x / TPE, sl = threadIdx.x % TPE;
+    const int nt = min(T - t0, kSmallT);
+    const int nch = (D + 7) / 8;
+    float acc[kSmallT];
 #pragma unroll
-  for (int j = 0; j < NET; ++j) acc[j] = f32x16_t{};
-  auto fetch = [&](int c, float (&xo)[8], float (&wo)[NET][8]) __attribute__((always_inline)) {
-    const int d = c * 16 + 8 * h;
-    const bool in = c < c_hi;
-    load8<XT>(xrow, d, D, tv && in, xo);
+    for (int t = 0; t < kSmallT; ++t) acc[t] = 0.0f;
+    const float* Re = R + (int64_t)(e < E ? e : 0) * D;
+#pragma unroll 4
+    for (int c = sl; c < nch; c += TPE) {
+      float wv[8];
+      load8<F32T>(Re, c * 8, D, e < E, wv);
 #pragma unroll
-    for (int j = 0; j < NET; ++j) {
-      const int e = 32 * j + r;
-      load8<F32T>(R + (int64_t)(e < E ? e : 0) * D, d, D, in && e < E, wo[j]);
+      for (int t = 0; t < kSmallT; ++t) {
+        if (t >= nt) break;
+        float xv[8];
+        load8<XT>(x + ((int64_t)b * T + t0 + t) * D, c * 8, D, true, xv);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[t] = fmaf(xv[i], wv[i], acc[t]);
+      }
     }
-  };
-  // a ring of DEPTH chunks in flight: each chunk's slot is refilled with the
-  // chunk DEPTH ahead right after its MFMAs issue, so a wave waits on about
-  // (its chunks / DEPTH) load latencies; slots past the range hold zeros,
-  // whose MFMAs add nothing
-  constexpr int DEPTH = NET <= 2 ? 4 : 2;
-  float xr[DEPTH][8], wr[DEPTH][NET][8];
 #pragma unroll
-  for (int q = 0; q < DEPTH; ++q) fetch(c_lo + q, xr[q], wr[q]);
-  for (int c = c_lo; c < c_hi; c += DEPTH) {
+    for (int t = 0; t < kSmallT; ++t) {
 #pragma unroll
-    for (int q = 0; q < DEPTH; ++q) {
-#pragma unroll
-      for (int j = 0; j < NET; ++j)
-#pragma unroll
-        for (int s8 = 0; s8 < 8; ++s8)
-          acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(xr[q][s8], wr[q][j][s8], acc[j], 0, 0, 0);
-      fetch(c + q + DEPTH, xr[q], wr[q]);
+      for (int o = TPE / 2; o >= 1; o >>= 1) acc[t] += __shfl_xor(acc[t], o, TPE);
     }
+    for (int t = 0; t < 32; ++t)
+      if (sl == 0 && e < EB) red[0][e / 32][t][e % 32] = t < kSmallT ? acc[t < kSmallT ? t : 0] : 0.0f;
+    __syncthreads();
+  } else {
+    const int r = lane % 32, h = lane / 32;
+    const bool tv = t0 + r < T;
+    const typename XT::S* xrow = x + ((int64_t)b * T + (tv ? t0 + r : 0)) * D;
+    const int nch = (D + 15) / 16;
+    const int per = (nch + NW - 1) / NW;
+    const int c_lo = w * per, c_hi = min(nch, c_lo + per);
+    f32x16_t acc[NET];
+#pragma unroll
+    for (int j = 0; j < NET; ++j) acc[j] = f32x16_t{};
+    auto fetch = [&](int c, float (&xo)[8], float (&wo)[NET][8]) __attribute__((always_inline)) {
+      const int d = c * 16 + 8 * h;
+      const bool in = c < c_hi;
+      load8<XT>(xrow, d, D, tv && in, xo);
+#pragma unroll
+      for (int j = 0; j < NET; ++j) {
+        const int e = 32 * j + r;
+        load8<F32T>(R + (int64_t)(e < E ? e : 0) * D, d, D, in && e < E, wo[j]);
+      }
+    };
+    // a ring of DEPTH chunks in flight: each chunk's slot is refilled with the
+    // chunk DEPTH ahead right after its MFMAs issue; slots past the range
+    // hold zeros, whose MFMAs add nothing
+    constexpr int DEPTH = NET <= 2 ? 4 : 2;
+    float xr[DEPTH][8], wr[DEPTH][NET][8];
+#pragma unroll
+    for (int q = 0; q < DEPTH; ++q) fetch(c_lo + q, xr[q], wr[q]);
+    for (int c = c_lo; c < c_hi; c += DEPTH) {
+#pragma unroll
+      for (int q = 0; q < DEPTH; ++q) {
+#pragma unroll
+        for (int j = 0; j < NET; ++j)
+#pragma unroll
+          for (int s8 = 0; s8 < 8; ++s8)
+            acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(xr[q][s8], wr[q][j][s8], acc[j], 0, 0, 0);
+        fetch(c + q + DEPTH, xr[q], wr[q]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NET; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) red[w][j][8 * (v / 4) + 4 * h + v % 4][r] = acc[j][v];
+    __syncthreads();
+    for (int i = threadIdx.x; i < NET * 32 * 32; i += NTH) {
+      const int j = i / 1024, tok = (i / 32) % 32, e = i % 32;
+      float v = red[0][j][tok][e];
+#pragma unroll
+      for (int q = 1; q < NW; ++q) v += red[q][j][tok][e];
+      red[0][j][tok][e] = v;
+    }
+    __syncthreads();
   }
-#pragma unroll
-  for (int j = 0; j < NET; ++j)
-#pragma unroll
-    for (int v = 0; v < 16; ++v) red[w][j][8 * (v / 4) + 4 * h + v % 4][r] = acc[j][v];
-  __syncthreads();
-  for (int i = threadIdx.x; i < NET * 32 * 32; i += NW * kWave) {
-    const int j = i / 1024, tok = (i / 32) % 32, e = i % 32;
-    float v = red[0][j][tok][e];
-#pragma unroll
-    for (int q = 1; q < NW; ++q) v += red[q][j][tok][e];
-    red[0][j][tok][e] = v;
-  }
-  __syncthreads();
   if (logits_out != nullptr) {
-    for (int i = threadIdx.x; i < E * 32; i += NW * kWave) {
+    for (int i = threadIdx.x; i < E * 32; i += NTH) {
       const int e = i / 32, tok = i % 32;
       if (t0 + tok < T) logits_out[((int64_t)b * E + e) * T + t0 + tok] = red[0][e / 32][tok][e % 32];
     }
   }
-  float bal[EB];
-  MaskBits<EB> m;
-  if (w == 0) {   // wave 0 selects: lane r < 32 owns token t0 + r, lanes >= 32 are padding
-    const bool live = lane < 32 && t0 + lane < T;
-    float l[EB];
+  // selection: half-wave g of the block's 2*NW takes the live tokens g,
+  // g + 2*NW, ... (the block sums below read only live rows)
+  const int g = threadIdx.x / 32, jl = threadIdx.x % 32;
+  const int ntok = min(32, T - t0);
+  for (int tok = g; tok < ntok; tok += 2 * NW) {
+    float lg[NET];
 #pragma unroll
-    for (int e = 0; e < EB; ++e) l[e] = (lane < 32 && e < E) ? red[0][e / 32][lane % 32][e % 32] : 0.0f;
-    select_token<EB>(l, a, b, t0 + lane, live, bal, m);
+    for (int q = 0; q < NET; ++q) lg[q] = red[0][q][tok][jl];
+    select_lanes<NET>(lg, a, b, t0 + tok, true, jl, sb[tok], sc[tok]);
   }
-  block_partials<EB, 32>(bal, m, (w == 0 && lane < 32) ? lane : -1, a, b, blk, sb, sc);
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += NTH) {
+    float s = 0.0f;
+    int c = 0;
+    for (int i = 0; i < ntok; ++i) {
+      s += sb[i][e];
+      c += sc[i][e];
+    }
+    put_partial(a, b, blk, e, s, c);
+  }
 }
 
 // group_sizes[b][e] and the balance sum of (b, e) over the select blocks:
@@ -435,18 +627,20 @@ Ws ws_layout(void* base, int B, int T, int E, int blk_tokens) {
 
 SelectArgs make_args(const Ws& w, const float* bias, int64_t bias_sb, int B, int E, int T,
                      int topk, int router_type, int combine_mode, float alpha, float router_scale,
-                     float norm_eps, void* mask, float* combine, float* balance) {
+                     float norm_eps, void* mask, float* combine, float* balance,
+                     int32_t* group_sizes) {
   return SelectArgs{bias, bias_sb, B, E, T, topk, router_type, combine_mode, alpha,
                     router_scale > 0.0f ? router_scale : sqrtf((float)E), norm_eps,
                     static_cast<uint8_t*>(mask), combine, balance, w.part_bal, w.part_cnt,
-                    w.nblk};
+                    w.nblk, group_sizes, w.bal_sum, w.cnt_sum};
 }
 
 // group sizes, balance sums and lb_loss from the block partials
 int finish(const Ws& w, int B, int E, int T, int32_t* group_sizes, float* lb_loss, hipStream_t st,
            const char* what) {
-  hipLaunchKernelGGL(router_reduce_kernel, dim3(B * E), dim3(kRT), 0, st, w.part_bal, w.part_cnt,
-                     E, w.nblk, group_sizes, w.bal_sum, w.cnt_sum);
+  if (w.nblk > 1)   // one block per batch: the select kernel wrote the sums
+    hipLaunchKernelGGL(router_reduce_kernel, dim3(B * E), dim3(kRT), 0, st, w.part_bal,
+                       w.part_cnt, E, w.nblk, group_sizes, w.bal_sum, w.cnt_sum);
   if (lb_loss != nullptr)
     hipLaunchKernelGGL(router_lb_kernel, dim3(1), dim3(kRT), 0, st, w.bal_sum, w.cnt_sum, B, E, T,
                        lb_loss);
@@ -478,7 +672,8 @@ extern "C" int uttt_router_select(const float* logits, int64_t l_sb, int64_t l_s
   UTTT_REQUIRE(workspace != nullptr && workspace_bytes >= w.bytes,
                "router_select: workspace %zu < %zu bytes", workspace_bytes, w.bytes);
   const SelectArgs a = make_args(w, bias, bias_sb, B, E, T, topk, router_type, combine_mode,
-                                 alpha, router_scale, norm_eps, mask, combine, balance);
+                                 alpha, router_scale, norm_eps, mask, combine, balance,
+                                 group_sizes);
   hipStream_t st = as_stream(stream);
   UTTT_EB_SWITCH(E, hipLaunchKernelGGL((router_select_kernel<EB>), dim3(w.nblk, B),
                                        dim3(sel_tpb(EB)), 0, st, logits, l_sb, l_se, l_st, a));
@@ -502,19 +697,29 @@ extern "C" int uttt_route_tokens(const void* x, int x_dtype, const float* router
   UTTT_REQUIRE(workspace != nullptr && workspace_bytes >= w.bytes,
                "route_tokens: workspace %zu < %zu bytes", workspace_bytes, w.bytes);
   const SelectArgs a = make_args(w, bias, bias_sb, B, E, T, topk, router_type, combine_mode,
-                                 alpha, router_scale, norm_eps, mask, combine, balance);
+                                 alpha, router_scale, norm_eps, mask, combine, balance,
+                                 group_sizes);
   hipStream_t st = as_stream(stream);
   const int net = (E + 31) / 32;
-#define UTTT_ROUTE_LAUNCH(NET, NW)                                                           \
-  hipLaunchKernelGGL((router_mfma_kernel<XT, NET, NW>), dim3(w.nblk, B), dim3(NW * kWave), 0,  \
-                     st, static_cast<const S*>(x), router_w, w_sb, D, logits_out, a)
+#define UTTT_ROUTE_LAUNCH(NET, NW, SMALL)                                                   \
+  hipLaunchKernelGGL((router_mfma_kernel<XT, NET, NW, SMALL>), dim3(w.nblk, B),                \
+                     dim3(NW * kWave), 0, st, static_cast<const S*>(x), router_w, w_sb, D,      \
+                     logits_out, a)
+  // a few tokens per batch (generation): vector-ALU logits, no padded MFMA rows
+  const bool small = T <= kSmallT;
   UTTT_DTYPE_SWITCH_LR(x_dtype, XT, {
     using S = typename XT::S;
     switch (net) {
-      case 1: UTTT_ROUTE_LAUNCH(1, 8); break;
-      case 2: UTTT_ROUTE_LAUNCH(2, 8); break;
-      case 3: UTTT_ROUTE_LAUNCH(3, 4); break;
-      default: UTTT_ROUTE_LAUNCH(4, 4); break;
+      case 1:
+        if (small) UTTT_ROUTE_LAUNCH(1, 8, true);
+        else UTTT_ROUTE_LAUNCH(1, 8, false);
+        break;
+      case 2:
+        if (small) UTTT_ROUTE_LAUNCH(2, 8, true);
+        else UTTT_ROUTE_LAUNCH(2, 8, false);
+        break;
+      case 3: UTTT_ROUTE_LAUNCH(3, 4, false); break;
+      default: UTTT_ROUTE_LAUNCH(4, 4, false); break;
     }
   });
 #undef UTTT_ROUTE_LAUNCH
