@@ -47,6 +47,22 @@ def test_dense_read_and_update(H, d, r, l):
         assert_bf16_close(o.cpu(), rr, name=n)
 
 
+@pytest.mark.parametrize("H,d,r,l", [(4, 192, 2, 1), (4, 96, 2, 8), (2, 64, 3, 3)])
+def test_dense_read_few_tokens(H, d, r, l):
+    """Generation-sized reads take the decode kernels: against the oracle and
+    against the grouped path (one token more than the decode limit)."""
+    b = 2
+    fast = tuple(x.to(torch.bfloat16) for x in _weights(b, H, d, r, seed=3))
+    q = _layer(b, l, H, d, 4)[0]
+    out = DN.apply_fast_weights(q.to(DEV), *(x.to(DEV) for x in fast))
+    assert out.shape == (b, l, H * d)
+    assert_bf16_close(out.cpu(), OD.read(q, *fast), name="decode-size read")
+    q9 = _layer(b, DN.DECODE_TOKENS + 1, H, d, 5)[0]
+    q9[:, :l] = q
+    grouped = DN.apply_fast_weights(q9.to(DEV), *(x.to(DEV) for x in fast))[:, :l]
+    assert_bf16_close(out, grouped, name="decode kernels vs grouped path")
+
+
 @pytest.mark.parametrize("L,S,chunk,H,d,r,master_renorm", [
     (1, 4096, 512, 4, 96, 2, False),     # configs[0]: one layer, 8 chunks
     (3, 1536, 512, 4, 96, 2, True),      # aggregate over layers, master renorm

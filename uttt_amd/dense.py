@@ -26,7 +26,14 @@ from __future__ import annotations
 import torch
 
 from . import _lib as L
+from .decode import moe_decode_read
 from .lact_moe_triton import _grouped as G
+
+# Reads of at most this many tokens (generation) stream the weights with the
+# decode kernels (csrc/decode_read.hip, one "expert" per head, gate 1): the
+# grouped GEMM would spend a 256-token tile on them.  Same rounding points:
+# bf16 hidden, bf16 output (the gate-1 merge is exact).
+DECODE_TOKENS = 8
 
 
 def _heads(x, H):
@@ -67,6 +74,9 @@ def apply_fast_weights(x, w0, w1, w2):
 def _read(x, W02, W1, b, H):
     L.require_device(x)
     xh = _heads(x, H)
+    if xh.shape[1] <= DECODE_TOKENS:
+        ones = torch.ones((b * H, 1, xh.shape[1]), dtype=torch.float32, device=x.device)
+        return _unheads(moe_decode_read(xh, W02, W1, ones.to(torch.uint8), ones, 1), b, H)
     gs = _gs(b * H, xh.shape[1], x.device)
     hid = G.gate_up(W02, xh, gs, token_major=True)
     return _unheads(G.gemm_nt(W1, hid, gs), b, H)
