@@ -88,3 +88,23 @@ def test_lb_loss_uniform_and_brute_force():
 def test_sigmoid_routing_refused():
     with pytest.raises(NotImplementedError):
         R.create_router_mask_sizes_probs(_logits(1, 4, 3, 0), 1, 1.0, True)
+
+
+def test_router_logits_brute_force():
+    """router_logits (modeling_recurrent_lact.py:153-157) is R x^T per batch:
+    against explicit dot products, for shared [E, D] and per-batch [B, E, D]
+    weights; a transposed operand (x R^T laid out [B, T, E]) is caught."""
+    g = torch.Generator().manual_seed(9)
+    B, T, E, D = 2, 5, 3, 7
+    x = torch.randn(B, T, D, generator=g)
+    for W in (torch.randn(E, D, generator=g), torch.randn(B, E, D, generator=g)):
+        got = R.router_logits(x, W)
+        assert got.shape == (B, E, T)
+        for b in range(B):
+            Wb = W if W.dim() == 2 else W[b]
+            for e in range(E):
+                for t in range(T):
+                    ref = sum(float(Wb[e, d]) * float(x[b, t, d]) for d in range(D))
+                    assert abs(float(got[b, e, t]) - ref) < 1e-9
+    wrong = torch.matmul(x.double(), W.double().transpose(-1, -2))   # [B, T, E]
+    assert wrong.shape != got.shape or not torch.allclose(wrong, got)
