@@ -42,6 +42,7 @@ def _case(B, T, E, k, D, I, seed, ragged=True):
     (2, 5, 8, 3, 64, 96, torch.bool),          # partial chunks on both axes
     (1, 13, 16, 2, 128, 256, torch.int32),     # two token groups per expert
     (2, 64, 64, 4, 96, 192, torch.bool),       # the largest T and E
+    (1, 3, 8, 2, 2560, 4096, torch.bool),      # long rows: 5 and 8 chunks per lane, 2-token groups
 ])
 def test_decode_read_matches_oracle(B, T, E, k, D, I, mask_dtype):
     x, W02, W1, mask, probs = _case(B, T, E, k, D, I, seed=T * 31 + E)
