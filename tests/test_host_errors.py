@@ -49,3 +49,46 @@ def test_write_step_rejects_bad_segments_without_launch():
     rc = lib.uttt_write_step(None, None, None, 0, None, None, 1.0, 1, 4, 96, 96, 1, 1,
                              None, None, None, None)
     assert rc == -1 and b"norm_from_fast" in lib.uttt_last_error()
+
+
+@needs_lib
+def test_new_entry_points_reject_bad_arguments_without_launch():
+    """The decode read, Newton-Schulz, momentum and router entry points check
+    sizes, dtypes and pointers before any GPU call (fake, never-dereferenced
+    addresses stand in for device pointers where a check comes later)."""
+    lib = _lib.lib()
+    p = 1 << 20   # an aligned, non-null stand-in address
+
+    def decode(B=1, T=1, D=64, E=8, I=32, mb=1, topk=2, ptr=p, ws_bytes=1 << 30):
+        return lib.uttt_moe_decode_read(ptr, B, T, D, ptr, ptr, E, I, ptr, mb, 0, 0, 0, ptr, 0, 0,
+                                        0, topk, ptr, ptr, ws_bytes, None)
+
+    for kw, msg in ((dict(E=65), b"E=65 exceeds 64"), (dict(T=65), b"exceed 64"),
+                    (dict(D=12), b"multiples of 8"), (dict(D=8192), b"at most"),
+                    (dict(mb=2), b"mask element size"), (dict(topk=0), b"topk"),
+                    (dict(ptr=None), b"null pointer"), (dict(ws_bytes=16), b"workspace")):
+        assert decode(**kw) == -1, kw
+        assert msg in lib.uttt_last_error(), (kw, lib.uttt_last_error())
+    assert lib.uttt_newton_schulz5(p, 1, 2, 12, 16, 1.0, p, p, 1 << 30, None) == -1
+    assert b"multiples of 8" in lib.uttt_last_error()
+    assert lib.uttt_newton_schulz5(p, 2, 2, 16, 16, 1.0, p, p, 1 << 30, None) == -1
+    assert b"fp32 or bf16" in lib.uttt_last_error()
+    assert lib.uttt_momentum_add(p, 2, p, p, 1, 16, p, None) == -1
+    assert b"fp32 or bf16" in lib.uttt_last_error()
+    rc = lib.uttt_route_tokens(p, 1, p, 0, 1, 4, 64, 8, None, 0, 9, 0, 0, 1.0, 0.0, 1e-6, None,
+                               p, p, p, p, p, p, 1 << 20, None)
+    assert rc == -1 and b"topk" in lib.uttt_last_error()
+    rc = lib.uttt_route_tokens(p, 1, p, 0, 1, 4, 64, 8, None, 0, 2, 7, 0, 1.0, 0.0, 1e-6, None,
+                               p, p, p, p, p, p, 1 << 20, None)
+    assert rc == -1 and b"router_type" in lib.uttt_last_error()
+
+
+def test_new_wrappers_refuse_cpu_tensors():
+    from uttt_amd import decode as DEC
+    from uttt_amd import fast_weight_write as FWW
+
+    with pytest.raises(RuntimeError, match="GPU only"):
+        DEC.moe_decode_read(torch.zeros(1, 1, 8), torch.zeros(1, 2, 16, 8), torch.zeros(1, 2, 8, 8),
+                            torch.zeros(1, 2, 1, dtype=torch.bool), torch.zeros(1, 2, 1), 1)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        FWW.newton_schulz5(torch.zeros(1, 8, 8))
