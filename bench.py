@@ -382,6 +382,7 @@ class MoeSweep:
         self.dW02, self.dW1 = e(1, E, 2 * I, D), e(1, E, D, I)
         s1b = L.lib().uttt_update_stage1_workspace_bytes(1, I, N)
         self.ws_s1, self.ws_s1_bytes = e(s1b, dt=torch.uint8), s1b
+        self._wgrad_workspace(N)
         if cfg["train"]:
             self.gW02, self.gW1 = e(1, E, 2 * I, D), e(1, E, D, I)
             self.gK, self.gV = e(1, N, D), e(1, N, D)
@@ -391,6 +392,17 @@ class MoeSweep:
         self.stream = torch.cuda.current_stream(dev).cuda_stream
         self.events = None
         self.batched = None
+
+    def _wgrad_workspace(self, N):
+        """Split-K partials of the weight-gradient pair for N routed rows (none
+        at the MoE shapes: their tiles already fill the chip)."""
+        import torch
+
+        L, E, I, D = self.L, self.E, self.I, self.D
+        nb = L.lib().uttt_grouped_wgrad_pair_workspace_bytes(1, E, I, D, N)
+        if nb > getattr(self, "ws_wg_bytes", 0) or not hasattr(self, "ws_wg"):
+            self.ws_wg = torch.empty(nb, dtype=torch.uint8, device=self.dev) if nb else None
+            self.ws_wg_bytes = nb
 
     def _route_buffers(self, T):
         import torch
@@ -443,6 +455,7 @@ class MoeSweep:
         bt["dy"], bt["hl"] = e(1, N, 2 * I), e(1, N, I)
         s1b = L.lib().uttt_update_stage1_workspace_bytes(1, I, N)
         bt["ws_s1"], bt["ws_s1_bytes"] = e(s1b, dt=torch.uint8), s1b
+        self._wgrad_workspace(N)
         if self.cfg["train"]:
             bt["gK"], bt["gV"] = e(1, N, D), e(1, N, D)
             bt["glr"] = [e(1, N) for _ in range(3)]
@@ -535,7 +548,8 @@ class MoeSweep:
                L.ptr(bt["ws_s1"]), bt["ws_s1_bytes"], s)
         self._mark("wgrad")
         L.call("uttt_grouped_wgrad_pair", L.ptr(bt["dy"]), L.ptr(bt["kp"]), L.ptr(bt["hl"]),
-               L.ptr(bt["vp"]), L.ptr(gs), 1, E, I, D, N, L.ptr(self.dW02), L.ptr(self.dW1), s)
+               L.ptr(bt["vp"]), L.ptr(gs), 1, E, I, D, N, L.ptr(self.dW02), L.ptr(self.dW1),
+               L.ptr(self.ws_wg), self.ws_wg_bytes, s)
         if self.cfg["train"]:
             self._mark("update_bwd(5 launches)")
             L.call("uttt_grouped_update_bwd", L.ptr(self.W02), L.ptr(self.W1), L.ptr(bt["kp"]),
@@ -583,7 +597,7 @@ class MoeSweep:
             Nu, gs, kp, vp, dy, hl = N, self.route_u["gs"], self.kp, self.vp, self.dy, self.hl
         timed("wgrad", lambda: L.call("uttt_grouped_wgrad_pair", L.ptr(dy), L.ptr(kp), L.ptr(hl),
                                       L.ptr(vp), L.ptr(gs), 1, E, I, D, Nu, L.ptr(self.dW02),
-                                      L.ptr(self.dW1), s))
+                                      L.ptr(self.dW1), L.ptr(self.ws_wg), self.ws_wg_bytes, s))
         timed("write_step(2 launches)", self.write)
         return out
 

@@ -242,7 +242,12 @@ int uttt_grouped_update_stage1(const void* w0_w2, const void* w1, const void* k,
  * dw1 [B,E,D,I] = V[seg]^T Hid[seg], bf16; an empty expert gets zeros. */
 int uttt_grouped_wgrad_pair(const void* dy0_dy2_tok, const void* k, const void* hidden_tok,
                             const void* v, const int32_t* group_sizes, int B, int E, int I,
-                            int D, int N, void* dw0_w2, void* dw1, void* stream);
+                            int D, int N, void* dw0_w2, void* dw1, void* workspace,
+                            size_t workspace_bytes, void* stream);
+/* Workspace of uttt_grouped_wgrad_pair: fp32 split-K partials when the
+ * output tiles fill under half of the GPU (a single expert with small
+ * weights, as uTTT-Dense), else 0 (workspace may then be NULL). */
+size_t uttt_grouped_wgrad_pair_workspace_bytes(int B, int E, int I, int D, int N);
 
 /* One weight-gradient product.  Replaces grouped_gemm_bwd_triton
  * (L/triton_grouped_gemm.py:349-404; kernel :251-346) with token-major

@@ -40,3 +40,17 @@ def test_library_exports_every_declared_symbol():
     assert l.uttt_last_error() == b""
     # size queries are pure host arithmetic
     assert l.uttt_row_id_map_workspace_bytes(1, 65536, 16) == 16 * 256 * 4
+
+
+@pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="library not built")
+def test_wgrad_pair_split_rule():
+    """Split K only where the output tiles fill under half of the 256 CUs: the
+    dense 124M write (4 heads x 5 tiles) takes 12 runs of its 24576 tokens;
+    the MoE shapes and short segments take none."""
+    q = _lib.lib().uttt_grouped_wgrad_pair_workspace_bytes
+    I, D = 384, 192
+    assert q(4, 1, I, D, 24576) == 12 * 4 * 3 * I * D * 4
+    assert q(1, 32, 3072, 1536, 65536) == 0      # 6912 tiles
+    assert q(4, 1, 192, 96, 512) == 0            # 8 K steps per segment: one run
+    assert q(1, 1, 64, 64, 64 * 8 * 40) == 32 * 3 * 64 * 64 * 4  # capped at 32 runs
+    assert q(0, 1, I, D, 24576) == 0

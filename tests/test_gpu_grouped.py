@@ -136,6 +136,42 @@ def test_update_stage_compat(name):
     assert_bf16_close(wg, r1.transpose(2, 3), name="grouped_gemm_bwd")
 
 
+# Split K of the weight-gradient pair (few output tiles: the token segments
+# are cut into runs and fp32 partials summed in run order)
+SPLIT_CASES = {
+    # the uTTT-Dense 124M write: 4 heads of one shared weight, 12 layers x 2048 tokens
+    "dense124m": (4, 1, 192, 384, [[24576]] * 4),
+    # small tiles, ragged segments: an empty expert, a short one whose later runs are empty
+    "ragged_small": (2, 2, 64, 64, [[4000, 0], [100, 3300]]),
+}
+
+
+@pytest.mark.parametrize("name", list(SPLIT_CASES))
+def test_wgrad_pair_split_k(name):
+    from uttt_amd import _lib as L
+
+    B, E, D, I, gs = SPLIT_CASES[name]
+    gs = torch.tensor(gs, dtype=torch.int32)
+    N = int(gs.sum(1).max())
+    assert L.lib().uttt_grouped_wgrad_pair_workspace_bytes(B, E, I, D, N) > 0  # split path
+    g = torch.Generator().manual_seed(7)
+    dy = (torch.randn(B, 2 * I, N, generator=g) * 0.05).to(torch.bfloat16)
+    hid = (torch.randn(B, I, N, generator=g) * 0.05).to(torch.bfloat16)
+    K = F.normalize(torch.randn(B, N, D, generator=g), dim=-1).to(torch.bfloat16)
+    V = F.normalize(torch.randn(B, N, D, generator=g), dim=-1).to(torch.bfloat16)
+    args = (dy.to(DEV), K.to(DEV), hid.to(DEV), V.to(DEV), gs.to(DEV))
+    dw02, dw1 = U2.grouped_two_gemm_fw_bwd_triton(*args)
+    again02, again1 = U2.grouped_two_gemm_fw_bwd_triton(*args)
+    torch.cuda.synchronize()
+    r02, r1 = FW.two_gemm_fw_bwd(dy, K, hid, V, gs)
+    assert_bf16_close(dw02.cpu(), r02, name="dW0_W2 (split K)")
+    assert_bf16_close(dw1.cpu(), r1, name="dW1 (split K)")
+    # fixed summation order: bit-identical on a second call
+    assert torch.equal(dw02, again02) and torch.equal(dw1, again1)
+    for b, e in (gs == 0).nonzero().tolist():
+        assert torch.count_nonzero(dw02[b, e]) == 0 and torch.count_nonzero(dw1[b, e]) == 0
+
+
 @pytest.mark.parametrize("name", ["ragged", "slack", "c3_chunk"])
 def test_apply_backward(name):
     c = case(name)

@@ -74,8 +74,10 @@ SIGNATURES = {
         [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_int, c_p, c_int, c_int, c_int, c_int, c_int,
          c_p, c_p, c_int, c_p, c_sz, c_p],
     ),
+    "uttt_grouped_wgrad_pair_workspace_bytes": (c_sz, [c_int] * 5),
     "uttt_grouped_wgrad_pair": (
-        c_int, [c_p, c_p, c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int, c_p, c_p, c_p],
+        c_int,
+        [c_p, c_p, c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int, c_p, c_p, c_p, c_sz, c_p],
     ),
     "uttt_grouped_wgrad": (
         c_int, [c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int, c_p, c_int, c_p],

@@ -19,6 +19,7 @@
 //              read through the LDS transposing loads).
 // Intermediates are token-major ([B, N, rows]); the kernel-level compat entry
 // points can also write the reference's [B, rows, N] layout.
+#include <algorithm>
 #include <type_traits>
 
 #include "gemm_pipe.h"
@@ -500,25 +501,36 @@ __global__ __launch_bounds__(kThreads) void tn_kernel(TnArgs a, typename Epi::Ar
 // Q [B, N, X] token-major.  A tile = 2 x 128 rows of y, B tile = 256 rows of
 // x, so every lane holds four consecutive y of one x: 8-byte stores along the
 // contiguous y axis.  Up to two tasks share a launch.
+//
+// Split K: when the launch has too few output tiles to fill the chip (one
+// expert with small weights, the dense case), each tile's token segment is cut
+// into `splits` runs of whole K steps; workgroup (tile, s) writes its fp32
+// partial product to part[s][b, e] and wg_reduce_kernel sums the partials in
+// split order into the bf16 output (deterministic).
 struct WgTask {
   const uint16_t* p;
   const uint16_t* q;
   uint16_t* out;
+  float* part;  // [splits][B*E][X][Y] fp32 when splits > 1
   int X, Y;
   int y_tiles, x_tiles;
 };
 
+// SPLIT: fp32 partials (the two epilogues in one kernel do not fit the
+// register file: each alone does)
+template <bool SPLIT>
 __global__ __launch_bounds__(kThreads) void wg_kernel(WgTask t0, WgTask t1,
                                                       const int32_t* __restrict__ gs, int E,
-                                                      int N) {
+                                                      int N, int BE, int splits) {
   __shared__ __attribute__((aligned(16))) uint8_t st0[kStageBytes];
   __shared__ __attribute__((aligned(16))) uint8_t st1[kStageBytes];
 
   const int n0_tiles = t0.y_tiles * t0.x_tiles;
   const int per_group = n0_tiles + t1.y_tiles * t1.x_tiles;
   const int bid = blockIdx.x;
-  const int t = bid % per_group;
-  const int be = bid / per_group;
+  const int t = bid % per_group;  // tiles of one (split, b, e) are neighbours: shared rows in L2
+  const int be = (bid / per_group) % BE;
+  const int split = bid / per_group / BE;
   const int b = be / E, e = be % E;
   const bool first = t < n0_tiles;
   const WgTask& tk = first ? t0 : t1;
@@ -529,6 +541,11 @@ __global__ __launch_bounds__(kThreads) void wg_kernel(WgTask t0, WgTask t1,
 
   int start, size;
   expert_segment(gs + (int64_t)b * E, e, N, &start, &size);
+  // this split's run of the segment: whole K steps, the last run may be short or empty
+  const int run = ((size + kBK - 1) / kBK + splits - 1) / splits * kBK;
+  const int lo = min(size, split * run);
+  size = min(size - lo, run);
+  start += lo;
   const Operand P{tk.p + ((int64_t)b * N + start) * Y, Y, Y, size};
   const Operand Q{tk.q + ((int64_t)b * N + start) * X, X, X, size};
 
@@ -568,13 +585,61 @@ __global__ __launch_bounds__(kThreads) void wg_kernel(WgTask t0, WgTask t1,
   run_pipeline<half_lds_ops<RMajor, RMajor>(), false>((size + kBK - 1) / kBK, true, prep, issue,
                                                       read, acc0, acc1, ring);
 
-  uint16_t* ob = tk.out + ((int64_t)after_loop(b) * E + after_loop(e)) * X * Y;
-  const int ye = after_loop(y0), xe = after_loop(x0);
-  for_quads(acc0, acc1, after_loop(wm), after_loop(wn), true, [&](int tt, int r, int n, const float* v) __attribute__((always_inline)) {
-    const int y = ye + tt * kTileRows + r;
-    const int x = xe + n;
-    if (y < Y && x < X) store4(ob, Y, x, y, v[0], v[1], v[2], v[3]);
-  });
+  // the epilogue re-derives its indices from an opaque copy of the block id,
+  // so none of them is held across the K loop
+  const int bid2 = __builtin_amdgcn_readfirstlane(after_loop(bid));
+  const int t2 = bid2 % per_group;
+  const int be2 = (bid2 / per_group) % BE;
+  const bool first2 = t2 < n0_tiles;
+  const WgTask& tk2 = first2 ? t0 : t1;
+  const int tl2 = first2 ? t2 : t2 - n0_tiles;
+  const int ye = (tl2 / tk2.x_tiles) * 2 * kTileRows, xe = (tl2 % tk2.x_tiles) * kBRows;
+  const int X2 = tk2.X, Y2 = tk2.Y;
+  if constexpr (!SPLIT) {
+    uint16_t* ob = tk2.out + (int64_t)be2 * X2 * Y2;
+    for_quads(acc0, acc1, after_loop(wm), after_loop(wn), true, [&](int tt, int r, int n, const float* v) __attribute__((always_inline)) {
+      const int y = ye + tt * kTileRows + r;
+      const int x = xe + n;
+      if (y < Y2 && x < X2) store4(ob, Y2, x, y, v[0], v[1], v[2], v[3]);
+    });
+  } else {
+    float* pb = tk2.part + ((int64_t)(bid2 / per_group / BE) * BE + be2) * X2 * Y2;
+    for_quads(acc0, acc1, after_loop(wm), after_loop(wn), true, [&](int tt, int r, int n, const float* v) __attribute__((always_inline)) {
+      const int y = ye + tt * kTileRows + r;
+      const int x = xe + n;
+      if (y < Y2 && x < X2) store4(pb, Y2, x, y, v[0], v[1], v[2], v[3]);
+    });
+  }
+}
+
+typedef float nt_f32x4 __attribute__((ext_vector_type(4)));
+
+// out = bf16(sum_s part[s]) over both tasks' n0 and n1 elements (multiples of
+// 8), the splits added in order 0, 1, ...; partials are read once (non-temporal).
+__global__ __launch_bounds__(256) void wg_reduce_kernel(WgTask t0, WgTask t1, int64_t n0,
+                                                        int64_t n1, int splits) {
+  const int64_t g0 = n0 / 8, total = g0 + n1 / 8;
+  for (int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x; g < total;
+       g += (int64_t)gridDim.x * 256) {
+    const bool first = g < g0;
+    const float* part = first ? t0.part : t1.part;
+    uint16_t* out = first ? t0.out : t1.out;
+    const int64_t n = first ? n0 : n1;
+    const int64_t i = (first ? g : g - g0) * 8;
+    nt_f32x4 a = {0.f, 0.f, 0.f, 0.f}, c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+    for (int s = 0; s < splits; ++s) {
+      const nt_f32x4* src = reinterpret_cast<const nt_f32x4*>(part + s * n + i);
+      a += __builtin_nontemporal_load(src);
+      c += __builtin_nontemporal_load(src + 1);
+    }
+    uint4 w;
+    w.x = pack_bf16x2(a.x, a.y);
+    w.y = pack_bf16x2(a.z, a.w);
+    w.z = pack_bf16x2(c.x, c.y);
+    w.w = pack_bf16x2(c.z, c.w);
+    *reinterpret_cast<uint4*>(out + i) = w;
+  }
 }
 
 // grad_lr_j[b, tok] = sum over m-tiles of lr_part[j][mt][b][tok] (fixed
@@ -844,6 +909,7 @@ WgTask wg_task(const void* p, const void* q, void* out, int X, int Y) {
   t.p = static_cast<const uint16_t*>(p);
   t.q = static_cast<const uint16_t*>(q);
   t.out = static_cast<uint16_t*>(out);
+  t.part = nullptr;
   t.X = X;
   t.Y = Y;
   t.y_tiles = (Y + 2 * kTileRows - 1) / (2 * kTileRows);
@@ -851,13 +917,59 @@ WgTask wg_task(const void* p, const void* q, void* out, int X, int Y) {
   return t;
 }
 
-int launch_wg(const WgTask& t0, const WgTask& t1, const int32_t* gs, int B, int E, int N,
-              hipStream_t st, const char* what) {
+// Split K is used when the tiles fill under half of the chip's 256 CUs (one
+// 128 KiB-LDS workgroup per CU): as many splits as fit one pass over the CUs,
+// each at least kMinSplitSteps K steps of the mean segment N / E, at most
+// kMaxSplits.  A pure function of the sizes, so the workspace query and the
+// launch agree.
+constexpr int kCUs = 256;
+constexpr int kMinSplitSteps = 8;
+constexpr int kMaxSplits = 32;
+
+int wg_splits(const WgTask& t0, const WgTask& t1, int B, int E, int N) {
   const int64_t per = (int64_t)t0.y_tiles * t0.x_tiles + (int64_t)t1.y_tiles * t1.x_tiles;
   const int64_t blocks = per * E * B;
+  if (blocks == 0 || 2 * blocks > kCUs) return 1;
+  const int64_t mean_steps = ((int64_t)N / E + kBK - 1) / kBK;
+  const int64_t s = std::min<int64_t>({kCUs / blocks, mean_steps / kMinSplitSteps, kMaxSplits});
+  return (int)std::max<int64_t>(1, s);
+}
+
+// fp32 partials of both tasks, the second at a 256-byte boundary
+size_t wg_part_bytes(const WgTask& t0, const WgTask& t1, int B, int E, int splits,
+                     size_t* off1) {
+  const size_t be = (size_t)B * E;
+  *off1 = ((size_t)splits * be * t0.X * t0.Y * sizeof(float) + 255) & ~(size_t)255;
+  return splits > 1 ? *off1 + (size_t)splits * be * t1.X * t1.Y * sizeof(float) : 0;
+}
+
+// splits = 1: one pass, bf16 stores, no workspace
+int launch_wg(WgTask t0, WgTask t1, const int32_t* gs, int B, int E, int N, int splits,
+              void* workspace, size_t workspace_bytes, hipStream_t st, const char* what) {
+  const int64_t per = (int64_t)t0.y_tiles * t0.x_tiles + (int64_t)t1.y_tiles * t1.x_tiles;
+  const int64_t blocks = per * E * B * splits;
   if (blocks == 0) return UTTT_OK;
   if (int rc = check_grid(blocks, what)) return rc;
-  hipLaunchKernelGGL(wg_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, st, t0, t1, gs, E, N);
+  if (splits > 1) {
+    size_t off1;
+    const size_t need = wg_part_bytes(t0, t1, B, E, splits, &off1);
+    UTTT_REQUIRE(workspace && workspace_bytes >= need && aligned16(workspace),
+                 "%s: workspace of %zu bytes needed (got %zu)", what, need, workspace_bytes);
+    t0.part = static_cast<float*>(workspace);
+    t1.part = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + off1);
+  }
+  if (splits == 1)
+    hipLaunchKernelGGL(wg_kernel<false>, dim3((unsigned)blocks), dim3(kThreads), 0, st, t0, t1, gs,
+                       E, N, B * E, 1);
+  else
+    hipLaunchKernelGGL(wg_kernel<true>, dim3((unsigned)blocks), dim3(kThreads), 0, st, t0, t1, gs,
+                       E, N, B * E, splits);
+  if (int rc = check_launch(what)) return rc;
+  if (splits == 1) return UTTT_OK;
+  const int64_t n0 = (int64_t)B * E * t0.X * t0.Y, n1 = (int64_t)B * E * t1.X * t1.Y;
+  const int64_t groups = (n0 + n1) / 8;
+  const unsigned rblocks = (unsigned)std::min<int64_t>((groups + 255) / 256, 4096);
+  hipLaunchKernelGGL(wg_reduce_kernel, dim3(rblocks), dim3(256), 0, st, t0, t1, n0, n1, splits);
   return check_launch(what);
 }
 
@@ -988,10 +1100,19 @@ extern "C" int uttt_grouped_update_stage1(const void* w0_w2, const void* w1, con
   return UTTT_OK;
 }
 
+extern "C" size_t uttt_grouped_wgrad_pair_workspace_bytes(int B, int E, int I, int D, int N) {
+  if (B <= 0 || E <= 0 || I <= 0 || D <= 0 || N <= 0) return 0;
+  const WgTask t0 = wg_task(nullptr, nullptr, nullptr, 2 * I, D);
+  const WgTask t1 = wg_task(nullptr, nullptr, nullptr, D, I);
+  size_t off1;
+  return wg_part_bytes(t0, t1, B, E, wg_splits(t0, t1, B, E, N), &off1);
+}
+
 extern "C" int uttt_grouped_wgrad_pair(const void* dy0_dy2_tok, const void* k,
                                        const void* hidden_tok, const void* v,
                                        const int32_t* group_sizes, int B, int E, int I, int D,
-                                       int N, void* dw0_w2, void* dw1, void* stream) {
+                                       int N, void* dw0_w2, void* dw1, void* workspace,
+                                       size_t workspace_bytes, void* stream) {
   UTTT_REQUIRE(B >= 0 && E >= 1 && I >= 0 && D >= 0 && N >= 0, "grouped_wgrad_pair: bad sizes");
   UTTT_REQUIRE(I % 8 == 0 && D % 8 == 0,
                "grouped_wgrad_pair: I=%d and D=%d must be multiples of 8", I, D);
@@ -1004,7 +1125,8 @@ extern "C" int uttt_grouped_wgrad_pair(const void* dy0_dy2_tok, const void* k,
   // dW0_W2 [2I][D] = DY^T K;  dW1 [D][I] = V^T Hid
   const WgTask t0 = wg_task(k, dy0_dy2_tok, dw0_w2, 2 * I, D);
   const WgTask t1 = wg_task(hidden_tok, v, dw1, D, I);
-  return launch_wg(t0, t1, group_sizes, B, E, N, as_stream(stream), "grouped_wgrad_pair");
+  return launch_wg(t0, t1, group_sizes, B, E, N, wg_splits(t0, t1, B, E, N), workspace,
+                   workspace_bytes, as_stream(stream), "grouped_wgrad_pair");
 }
 
 extern "C" int uttt_grouped_wgrad(const void* a_tok, const void* b_tok,
@@ -1022,7 +1144,7 @@ extern "C" int uttt_grouped_wgrad(const void* a_tok, const void* b_tok,
   WgTask t1 = t0;
   t1.y_tiles = 0;
   t1.x_tiles = 0;
-  return launch_wg(t0, t1, group_sizes, B, E, N, as_stream(stream), "grouped_wgrad");
+  return launch_wg(t0, t1, group_sizes, B, E, N, 1, nullptr, 0, as_stream(stream), "grouped_wgrad");
 }
 
 namespace uttt {
@@ -1143,7 +1265,7 @@ extern "C" int uttt_grouped_update_bwd(
   // 7. grad_W0_W2 [2I][D] = grad_x0_x2^T K;  grad_W1 [D][I] = V^T grad_dh
   const WgTask t0 = wg_task(k, gx, grad_w0_w2, 2 * I, D);
   const WgTask t1 = wg_task(gdh, v, grad_w1, D, I);
-  return launch_wg(t0, t1, group_sizes, B, E, N, st, "grouped_update_bwd(weights)");
+  return launch_wg(t0, t1, group_sizes, B, E, N, 1, nullptr, 0, st, "grouped_update_bwd(weights)");
 }
 
 extern "C" int uttt_transpose_2byte(const void* in, int B, int R, int C, void* out, void* stream) {

@@ -125,8 +125,11 @@ def wgrad_pair(DY_tok, K, H_tok, V, group_sizes):
     dev = K.device
     dW02 = torch.empty((B, E, I2, D), dtype=torch.bfloat16, device=dev)
     dW1 = torch.empty((B, E, D, I), dtype=torch.bfloat16, device=dev)
+    # split-K partials when few output tiles (one expert, small weights)
+    nws = L.lib().uttt_grouped_wgrad_pair_workspace_bytes(B, E, I, D, N)
+    ws = torch.empty(nws, dtype=torch.uint8, device=dev) if nws else None
     L.call("uttt_grouped_wgrad_pair", L.ptr(DY_tok), L.ptr(K), L.ptr(H_tok), L.ptr(V), L.ptr(gs),
-           B, E, I, D, N, L.ptr(dW02), L.ptr(dW1), L.stream_of(K))
+           B, E, I, D, N, L.ptr(dW02), L.ptr(dW1), L.ptr(ws), nws, L.stream_of(K))
     return dW02, dW1
 
 
