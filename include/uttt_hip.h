@@ -380,6 +380,37 @@ int uttt_moe_decode_read(const void* x, int B, int T, int D, const void* w0_w2, 
                          int64_t p_se, int64_t p_st, int topk, void* out, void* workspace,
                          size_t workspace_bytes, void* stream);
 
+/* uTTT-Dense read, fused for small heads: out = W1 (silu(W0 x) * (W2 x))
+ * per head (_apply_fast_weights, uttt_dense/modeling_recurrent_lact.py:241-261,
+ * with the rearranges of :251 and :261 folded in).  x [b, l, H*D] bf16,
+ * w0_w2 [b*H, 2I, D] (w0 rows then w2 rows), w1 [b*H, D, I] bf16 ->
+ * out [b, l, H*D] bf16 (fp32 products, bf16 hidden, as the grouped APPLY).
+ * Shapes: uttt_dense_read_supported(D, I) != 0 (D in {64, 96, 128, 192, 256},
+ * I a multiple of 32 up to 512), b*H <= 65535, 16-byte aligned tensors. */
+int uttt_dense_read_supported(int D, int I);
+int uttt_dense_read(const void* x, int b, int l, int H, int D, const void* w0_w2, const void* w1,
+                    int I, void* out, void* stream);
+
+/* uTTT-Dense head layout (uttt_dense/modeling_recurrent_lact.py, D:).
+ * Gather: the head split 'b l (h d) -> (b h) l d' of k and v and
+ * 'b l h -> (b h) l 1' of the three lr columns in compute_update (D:370-398;
+ * of the read input at D:251), for L layers at once, the layers' tokens
+ * concatenated per head (the aggregate write's batching of
+ * _aggregate_memory_update, D:1302-1386):
+ *   kh [b*H, L*l, d] (bf16; vh likewise) from k_layers[li] [b, l, H*d] bf16,
+ *   lr0/1/2 [b*H, L*l] fp32 from lr_layers[li] [b, l, 3] (lr_per_head = 0,
+ *   shared by the heads) or [b, l, H*3] (lr_per_head = 1), dtype lr_dtype.
+ * k_layers, v_layers, lr_layers are HOST arrays of L device pointers
+ * (L <= 64); v_layers/vh and lr_layers/lr* may be NULL.  d % 8 == 0, k, v
+ * and the outputs 16-byte aligned. */
+int uttt_dense_gather_heads(const void* const* k_layers, const void* const* v_layers,
+                            const void* const* lr_layers, int lr_dtype, int lr_per_head, int L,
+                            int b, int l, int H, int d, void* kh, void* vh, float* lr0,
+                            float* lr1, float* lr2, void* stream);
+/* Scatter: '(b h) l hd -> b l (h hd)' of the read output (D:261):
+ * y [b*H, l, d] bf16 -> out [b, l, H*d] bf16; d % 8 == 0, 16-byte aligned. */
+int uttt_dense_scatter_heads(const void* y, int b, int l, int H, int d, void* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -93,3 +93,58 @@ def test_dense_sweep(L, S, chunk, H, d, r, master_renorm):
         assert_bf16_close(a.cpu(), rr, name="fast " + n)
     for a, rr, n in zip(m, ref_master, ("w0", "w1", "w2")):
         assert_bf16_close(a.cpu(), rr, name="master " + n)
+
+
+@pytest.mark.parametrize("b,l,H,d,per_head,lr_dtype", [
+    (2, 37, 4, 24, False, torch.float32),   # ragged token count, shared lr
+    (1, 2048, 4, 192, True, torch.bfloat16),  # the 124M head shape, per-head lr
+])
+def test_gather_and_scatter_heads_are_exact(b, l, H, d, per_head, lr_dtype):
+    """The head layout kernels move bytes: equal to torch's rearranges
+    (D:251, :261, :370-398) bit for bit, three layers gathered at once."""
+    g = torch.Generator().manual_seed(l)
+    ks = [torch.randn(b, l, H * d, generator=g).to(torch.bfloat16).to(DEV) for _ in range(3)]
+    vs = [torch.randn(b, l, H * d, generator=g).to(torch.bfloat16).to(DEV) for _ in range(3)]
+    lrs = [torch.rand(b, l, 3 * H if per_head else 3, generator=g).to(lr_dtype).to(DEV)
+           for _ in range(3)]
+    kh, vh, lr3 = DN._gather_heads(ks, vs, lrs, H)
+    split = lambda x: x.reshape(b, l, H, d).permute(0, 2, 1, 3).reshape(b * H, l, d)
+    assert torch.equal(kh, torch.cat([split(k) for k in ks], dim=1))
+    assert torch.equal(vh, torch.cat([split(v) for v in vs], dim=1))
+    for j in range(3):
+        cols = [(lr.reshape(b, l, H, 3)[..., j] if per_head else
+                 lr[..., j:j + 1].expand(b, l, H)).permute(0, 2, 1).reshape(b * H, l).float()
+                for lr in lrs]
+        assert torch.equal(lr3[j], torch.cat(cols, dim=1))
+    y = torch.randn(b * H, l, d, generator=g).to(torch.bfloat16).to(DEV)
+    out = DN._unheads(y, b, H)
+    assert torch.equal(out, y.reshape(b, H, l, d).permute(0, 2, 1, 3).reshape(b, l, H * d))
+
+
+@pytest.mark.parametrize("b,H,d,dh,l", [
+    (1, 4, 192, 384, 2048),   # 124M: 12 hidden blocks, 3 per wave
+    (2, 3, 128, 96, 77),      # 3 hidden blocks (one wave idle), ragged token tile
+    (1, 2, 256, 512, 64),     # 4 blocks per wave, the largest head
+    (3, 1, 64, 32, 9),        # one hidden block, one partial tile
+])
+def test_fused_dense_read(b, H, d, dh, l):
+    """csrc/dense_read.hip (fused read for small heads) against the oracle
+    and against the grouped route (head split, grouped APPLY, merge)."""
+    from uttt_amd import _lib as L
+    from uttt_amd.lact_moe_triton import _grouped as G
+
+    assert L.lib().uttt_dense_read_supported(d, dh)
+    g = torch.Generator().manual_seed(l + d)
+    w0, w2 = ((torch.randn(b, H, dh, d, generator=g) / d ** 0.5).to(torch.bfloat16)
+              for _ in range(2))
+    w1 = (torch.randn(b, H, d, dh, generator=g) / dh ** 0.5).to(torch.bfloat16)
+    q = torch.randn(b, l, H * d, generator=g).to(torch.bfloat16)
+    out = DN.apply_fast_weights(q.to(DEV), w0.to(DEV), w1.to(DEV), w2.to(DEV))
+    assert out.shape == (b, l, H * d) and out.dtype == torch.bfloat16
+    assert_bf16_close(out.cpu(), OD.read(q, w0, w1, w2), name="fused read")
+    W02 = torch.cat([w0, w2], dim=2).reshape(b * H, 1, 2 * dh, d).to(DEV)
+    W1 = w1.reshape(b * H, 1, d, dh).to(DEV)
+    xh = DN._heads(q.to(DEV), H)
+    gs = DN._gs(b * H, l, DEV)
+    grouped = DN._unheads(G.gemm_nt(W1, G.gate_up(W02, xh, gs, token_major=True), gs), b, H)
+    assert_bf16_close(out, grouped, name="fused read vs grouped route")

@@ -75,6 +75,16 @@ SIGNATURES = {
          c_p, c_p, c_int, c_p, c_sz, c_p],
     ),
     "uttt_grouped_wgrad_pair_workspace_bytes": (c_sz, [c_int] * 5),
+    "uttt_dense_gather_heads": (
+        c_int,
+        [c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_p, c_p, c_p, c_p,
+         c_p, c_p],
+    ),
+    "uttt_dense_scatter_heads": (c_int, [c_p, c_int, c_int, c_int, c_int, c_p, c_p]),
+    "uttt_dense_read_supported": (c_int, [c_int, c_int]),
+    "uttt_dense_read": (
+        c_int, [c_p, c_int, c_int, c_int, c_int, c_p, c_p, c_int, c_p, c_p],
+    ),
     "uttt_grouped_wgrad_pair": (
         c_int,
         [c_p, c_p, c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int, c_p, c_p, c_p, c_sz, c_p],

@@ -14,6 +14,11 @@ uttt_llm/flame/custom_models/uttt_dense/modeling_recurrent_lact.py (D:):
                        chunk, write() = _aggregate_memory_update D:1302-1386 +
                        _apply_shared_update D:1109-1240
 
+Reads of more than DECODE_TOKENS tokens with small heads (d in {64, 96, 128,
+192, 256}, d_h a multiple of 32 up to 512) run the fused read of
+csrc/dense_read.hip on the [b, l, H*d] activations directly; other shapes
+split the heads (csrc/dense_heads.hip) and run the grouped APPLY.
+
 SharedFastWeights keeps its state in the kernels' layout -- fast W0_W2
 [b*H, 1, 2 d_h, d] and W1 [b*H, 1, d, d_h] in bf16 with fp32 masters -- so a
 chunk needs no concatenation or copy of the weights.  Its write batches the L
@@ -22,6 +27,8 @@ fp32 accumulation gives sum_l dW_l (the reference adds the layers' bf16
 updates in fp32); the mean reduce is folded into the step size.
 """
 from __future__ import annotations
+
+import ctypes
 
 import torch
 
@@ -36,31 +43,72 @@ from .lact_moe_triton import _grouped as G
 DECODE_TOKENS = 8
 
 
+def _bf16_rows(x):
+    x = x.to(torch.bfloat16)
+    return x if x.is_contiguous() else x.contiguous()
+
+
+def _gather_heads(ks, vs, lrs, H):
+    """One launch (csrc/dense_heads.hip): the layers' k [b, l, H*d] (and v,
+    and lr [b, l, 3] or [b, l, H*3]) -> per head with the layers' tokens
+    concatenated: kh, vh [b*H, L*l, d] bf16 and lr0/1/2 [b*H, L*l] fp32
+    (D:370-398 per layer, the layers batched as the aggregate write needs)."""
+    ks = [_bf16_rows(k) for k in ks]
+    b, l, hd = ks[0].shape
+    n = len(ks)
+    for k in ks:
+        assert k.shape == (b, l, hd), "every layer's k, v: [b, l, H*d] of one shape"
+    d = hd // H
+    dev = ks[0].device
+    arr = lambda ts: (ctypes.c_void_p * n)(*[t.data_ptr() for t in ts])
+    kh = torch.empty((b * H, n * l, d), dtype=torch.bfloat16, device=dev)
+    vh = lr3 = None
+    vp = lp = None
+    if vs is not None:
+        vs = [_bf16_rows(v) for v in vs]
+        for v in vs:
+            assert v.shape == (b, l, hd), "every layer's k, v: [b, l, H*d] of one shape"
+        vh = torch.empty_like(kh)
+        vp = arr(vs)
+    per_head, code = 0, L.F32
+    if lrs is not None:
+        lrs = [lr.contiguous() for lr in lrs]
+        code = L.dtype_code(lrs[0].dtype)
+        per_head = int(lrs[0].shape[2] != 3)
+        for lr in lrs:
+            assert lr.dtype == lrs[0].dtype and lr.shape == (b, l, 3 * H if per_head else 3)
+        lr3 = [torch.empty((b * H, n * l), dtype=torch.float32, device=dev) for _ in range(3)]
+        lp = arr(lrs)
+    L.call("uttt_dense_gather_heads", arr(ks), vp, lp, code, per_head, n, b, l, H, d,
+           L.ptr(kh), L.ptr(vh), *(L.ptr(x) for x in (lr3 or [None] * 3)), L.stream_of(kh))
+    return kh, vh, lr3
+
+
 def _heads(x, H):
-    """[b, l, H*d] -> contiguous [b*H, l, d] bf16."""
-    b, l, hd = x.shape
-    return (x.reshape(b, l, H, hd // H).permute(0, 2, 1, 3).reshape(b * H, l, hd // H)
-            .to(torch.bfloat16).contiguous())
+    """D:251: [b, l, H*d] -> contiguous [b*H, l, d] bf16."""
+    return _gather_heads([x], None, None, H)[0]
 
 
 def _unheads(y, b, H):
+    """D:261: [b*H, l, d] bf16 -> [b, l, H*d]."""
     bh, l, d = y.shape
-    return y.reshape(b, H, l, d).permute(0, 2, 1, 3).reshape(b, l, H * d)
+    out = torch.empty((b, l, H * d), dtype=torch.bfloat16, device=y.device)
+    L.call("uttt_dense_scatter_heads", L.ptr(y.contiguous()), b, l, H, d, L.ptr(out),
+           L.stream_of(y))
+    return out
 
 
-def _lr_heads(lr, b, l, H):
-    """D:381-398: lr [b, l, 3] (shared by the heads) or [b, l, H*3] -> three
-    contiguous fp32 [b*H, l]."""
-    if lr.shape[2] == 3:
-        lr = lr.unsqueeze(2).expand(b, l, H, 3)
-    else:
-        lr = lr.reshape(b, l, H, 3)
-    lr = lr.permute(0, 2, 1, 3).reshape(b * H, l, 3).float()
-    return [lr[..., j].contiguous() for j in range(3)]
+_GS = {}
 
 
 def _gs(B, N, device):
-    return torch.full((B, 1), N, dtype=torch.int32, device=device)
+    """group_sizes [[N]] * B (one expert per head), kept per shape and device:
+    read-only for the kernels, so one tensor serves every call."""
+    key = (B, N, str(device))
+    gs = _GS.get(key)
+    if gs is None:
+        gs = _GS[key] = torch.full((B, 1), N, dtype=torch.int32, device=device)
+    return gs
 
 
 def apply_fast_weights(x, w0, w1, w2):
@@ -73,6 +121,15 @@ def apply_fast_weights(x, w0, w1, w2):
 
 def _read(x, W02, W1, b, H):
     L.require_device(x)
+    d, dh = W1.shape[-2], W1.shape[-1]
+    assert x.dim() == 3 and x.shape[2] == H * d, "x: [b, l, H*d]"
+    if x.shape[1] > DECODE_TOKENS and L.lib().uttt_dense_read_supported(d, dh):
+        # fused (csrc/dense_read.hip): x and out stay in the [b, l, H*d] layout
+        xb = _bf16_rows(x)
+        out = torch.empty_like(xb)
+        L.call("uttt_dense_read", L.ptr(xb), b, xb.shape[1], H, d, L.ptr(W02), L.ptr(W1), dh,
+               L.ptr(out), L.stream_of(xb))
+        return out
     xh = _heads(x, H)
     if xh.shape[1] <= DECODE_TOKENS:
         ones = torch.ones((b * H, 1, xh.shape[1]), dtype=torch.float32, device=x.device)
@@ -85,10 +142,7 @@ def _read(x, W02, W1, b, H):
 def _update(W02, W1, ks, vs, lrs, b, H):
     """The grouped UPDATE of several layers' tokens at once: per head the
     tokens of all layers concatenated.  Returns bf16 (dW0_W2, dW1)."""
-    kh = torch.cat([_heads(k, H) for k in ks], dim=1).contiguous()
-    vh = torch.cat([_heads(v, H) for v in vs], dim=1).contiguous()
-    per = [_lr_heads(lr, b, k.shape[1], H) for lr, k in zip(lrs, ks)]
-    lr3 = [torch.cat([p[j] for p in per], dim=1).contiguous() for j in range(3)]
+    kh, vh, lr3 = _gather_heads(ks, vs, lrs, H)
     gs = _gs(b * H, kh.shape[1], kh.device)
     dy, hl = G.update_stage1(W02, W1, kh, vh, lr3[0], lr3[1], lr3[2], gs, token_major=True)
     return G.wgrad_pair(dy, kh, hl, vh, gs)
