@@ -38,6 +38,15 @@ def test_row_id_map_kat_on_gpu():
         (1, 1, 1, 1, torch.bool, False),
         (1, 1000, 128, 4, torch.int32, True),
         (2, 300, 5, 5, torch.bool, False),      # every expert selected
+        # one-launch row map (contiguous bool mask, T % 16 == 0, T <= 4096, E <= 64)
+        (1, 2048, 32, 2, torch.bool, False),    # one apply's routing at the 760M shape
+        (2, 2048, 32, 2, torch.bool, True),
+        (1, 2048, 16, 2, torch.bool, True),     # the 124M shape
+        (2, 4096, 64, 3, torch.bool, True),     # largest one-launch case: 16 tiles, E = 64
+        (1, 1040, 7, 2, torch.bool, True),      # partial last tile and 64-token segment
+        (1, 16, 3, 1, torch.bool, False),
+        (1, 4096, 65, 2, torch.bool, False),    # E = 65 and T = 4112 take the three launches
+        (1, 4112, 8, 2, torch.bool, True),
     ],
 )
 def test_row_id_map_bit_exact(B, T, E, k, mask_dtype, ragged):

@@ -13,6 +13,9 @@
 //           reference format (rows and experts in descending order, n_routed
 //           last, the reference's stale values in columns [n, E)).
 // No atomics are used, so the result is deterministic by construction.
+// Short batches of a contiguous bool mask (T <= 4096, E <= 64: one apply's
+// routing) take one launch instead (rowmap_fused_kernel): each workgroup
+// counts the whole batch with 16-byte loads, then emits its own tile.
 //
 // Payload kernels move rows in 16-byte vectors: permute reads a token's row
 // once and writes it to each of the token's slots; unpermute gathers the slots
@@ -34,24 +37,28 @@ __device__ __forceinline__ bool mask_bit(const void* map, int64_t idx) {
   return reinterpret_cast<const int32_t*>(map)[idx] != 0;
 }
 
-// Selection bits of one token (bit e of word e / 32).  All mask loads of a
-// 32-expert group are issued before any of them is used, so a tile pays one
-// memory latency per group rather than one per expert.
+// Selection bits of one token (bit e of word e / 32).  `base` must address a
+// real token (callers clamp the token index; `valid` masks the result), and
+// experts past E re-read expert E-1: every load is then unconditional, so all
+// loads of a 32-expert group are in flight before the first is used and a
+// tile pays one memory latency per group.  (Loads under a per-lane condition
+// would each be followed by a wait before the merge of the two paths.)
 template <int MB>
 __device__ __forceinline__ void load_mask_bits(const void* map, int64_t base, int64_t s_e, int E,
                                                bool valid, uint32_t bits[kMaxExperts / 32]) {
 #pragma unroll
   for (int g = 0; g < kMaxExperts / 32; ++g) {
     bits[g] = 0u;
-    if (32 * g < E) {
+    if (32 * g < E) {  // wave-uniform
       bool bv[32];
 #pragma unroll
       for (int i = 0; i < 32; ++i) {
-        const int e = 32 * g + i;
-        bv[i] = valid && e < E && mask_bit<MB>(map, base + (int64_t)e * s_e);
+        const int e = min(32 * g + i, E - 1);
+        bv[i] = mask_bit<MB>(map, base + (int64_t)e * s_e);
       }
 #pragma unroll
-      for (int i = 0; i < 32; ++i) bits[g] |= (uint32_t)bv[i] << i;
+      for (int i = 0; i < 32; ++i)
+        bits[g] |= (uint32_t)(valid && 32 * g + i < E && bv[i]) << i;
     }
   }
 }
@@ -62,6 +69,21 @@ __device__ __forceinline__ bool bit_of(const uint32_t bits[kMaxExperts / 32], in
 }
 
 // ------------------------------------------------------------ row map ------
+// Per-wave expert counts of a tile (one ballot per expert), and the ballots
+// themselves when `wmask` is given.
+__device__ __forceinline__ void wave_counts(const uint32_t bits[kMaxExperts / 32], int E,
+                                            int (*wcnt)[kMaxExperts],
+                                            uint64_t (*wmask)[kMaxExperts] = nullptr) {
+  const int w = threadIdx.x / kWave;
+  for (int e = 0; e < E; ++e) {
+    const uint64_t bal = __ballot(bit_of(bits, e));
+    if (lane_id() == 0) {
+      wcnt[w][e] = __popcll(bal);
+      if (wmask != nullptr) wmask[w][e] = bal;
+    }
+  }
+}
+
 template <int MB>
 __global__ __launch_bounds__(kTile) void rowmap_count_kernel(
     const void* map, int64_t s_b, int64_t s_e, int64_t s_t, int T, int E, int ntiles,
@@ -69,14 +91,10 @@ __global__ __launch_bounds__(kTile) void rowmap_count_kernel(
   __shared__ int wcnt[kTile / kWave][kMaxExperts];
   const int tile = blockIdx.x, b = blockIdx.y;
   const int t = tile * kTile + threadIdx.x;
-  const int w = threadIdx.x / kWave;
-  const int64_t base = (int64_t)b * s_b + (int64_t)t * s_t;
+  const int64_t base = (int64_t)b * s_b + (int64_t)min(t, T - 1) * s_t;
   uint32_t bits[kMaxExperts / 32];
   load_mask_bits<MB>(map, base, s_e, E, t < T, bits);
-  for (int e = 0; e < E; ++e) {
-    const uint64_t bal = __ballot(bit_of(bits, e));
-    if (lane_id() == 0) wcnt[w][e] = __popcll(bal);
-  }
+  wave_counts(bits, E, wcnt);
   __syncthreads();
   for (int e = threadIdx.x; e < E; e += kTile) {
     int c = 0;
@@ -150,7 +168,56 @@ __global__ __launch_bounds__(kScanThreads) void rowmap_scan_kernel(int32_t* coun
 // output) are assembled in LDS and written out with consecutive lanes on
 // consecutive words; without it each lane stores its own entry directly,
 // which strides the lanes 4 * (2E+1) bytes apart.
-constexpr int kStageMaxW = 63;  // STAGE needs kTile * (2E+1) * 4 <= 63 KiB of LDS
+constexpr int kStageMaxW = 57;  // STAGE: kTile * (2E+1) * 4 bytes plus the 6.5 KiB of tables <= 64 KiB
+
+// Packed entries of one 256-token tile, given its tokens' selection bits, the
+// per-wave counts (wcnt) and selection ballots (wmask) of the tile and each
+// expert's first row for the tile (toff): rows and experts in descending
+// order, n_routed last, the reference's stale values in columns [n, E) (the
+// row where routed, else -1), zeros in [E + n, 2E).  Each lane walks only its
+// own experts, so the cost per token is its n_routed, not E.  STAGE assembles
+// the tile in LDS (`stage`, kTile * (2E+1) words) and writes it with
+// consecutive lanes on consecutive words; without it each lane stores its own
+// entry, which strides the lanes 4 * (2E+1) bytes apart.
+template <bool STAGE, bool COPY_OUT = STAGE>
+__device__ __forceinline__ void emit_tile(const uint32_t bits[kMaxExperts / 32], int T, int E,
+                                          int tile, int b, const int (*wcnt)[kMaxExperts],
+                                          const uint64_t (*wmask)[kMaxExperts], const int* toff,
+                                          int32_t* stage, int32_t* row_id_map) {
+  const int t = tile * kTile + threadIdx.x;
+  const int w = threadIdx.x / kWave;
+  const int n = __popc(bits[0]) + __popc(bits[1]) + __popc(bits[2]) + __popc(bits[3]);
+  const int W = 2 * E + 1;
+  int32_t* row = STAGE ? stage + threadIdx.x * W : row_id_map + ((int64_t)b * T + t) * W;
+  if (t < T) {
+    for (int c = n; c < E; ++c) row[c] = -1;  // stale columns; routed ones are set below
+    for (int c = E + n; c < 2 * E; ++c) row[c] = 0;
+    row[2 * E] = n;
+    const uint64_t below = (1ull << lane_id()) - 1ull;
+    int j = 0;
+#pragma unroll
+    for (int g = kMaxExperts / 32 - 1; g >= 0; --g) {
+      uint32_t m = bits[g];
+      while (m != 0u) {  // this token's experts, highest first
+        const int hb = 31 - __clz(m);
+        m &= ~(1u << hb);
+        const int e = 32 * g + hb;
+        int r = toff[e] + __popcll(wmask[w][e] & below);
+        for (int i = 0; i < w; ++i) r += wcnt[i][e];
+        row[j] = r;
+        row[E + j] = e;
+        ++j;
+        if (e >= n) row[e] = r;
+      }
+    }
+  }
+  if constexpr (STAGE && COPY_OUT) {
+    __syncthreads();
+    const int nt = min(kTile, T - tile * kTile);
+    int32_t* g = row_id_map + ((int64_t)b * T + (int64_t)tile * kTile) * W;
+    for (int i = threadIdx.x; i < nt * W; i += kTile) g[i] = stage[i];
+  }
+}
 
 template <int MB, bool STAGE>
 __global__ __launch_bounds__(kTile) void rowmap_emit_kernel(
@@ -158,50 +225,107 @@ __global__ __launch_bounds__(kTile) void rowmap_emit_kernel(
     const int32_t* offsets, int32_t* row_id_map) {
   extern __shared__ int32_t stage[];
   __shared__ int wcnt[kTile / kWave][kMaxExperts];
+  __shared__ uint64_t wmask[kTile / kWave][kMaxExperts];
   __shared__ int toff[kMaxExperts];
   const int tile = blockIdx.x, b = blockIdx.y;
   const int t = tile * kTile + threadIdx.x;
-  const int w = threadIdx.x / kWave;
-  const int64_t base = (int64_t)b * s_b + (int64_t)t * s_t;
+  const int64_t base = (int64_t)b * s_b + (int64_t)min(t, T - 1) * s_t;
   uint32_t bits[kMaxExperts / 32];
   load_mask_bits<MB>(map, base, s_e, E, t < T, bits);
-  for (int e = 0; e < E; ++e) {
-    const uint64_t bal = __ballot(bit_of(bits, e));
-    if (lane_id() == 0) wcnt[w][e] = __popcll(bal);
-  }
+  wave_counts(bits, E, wcnt, wmask);
   for (int e = threadIdx.x; e < E; e += kTile)
     toff[e] = offsets[((int64_t)b * E + e) * ntiles + tile];
   __syncthreads();
+  emit_tile<STAGE>(bits, T, E, tile, b, wcnt, wmask, toff, stage, row_id_map);
+}
 
-  const int n = __popc(bits[0]) + __popc(bits[1]) + __popc(bits[2]) + __popc(bits[3]);
-  const int W = 2 * E + 1;
-  int32_t* row = STAGE ? stage + threadIdx.x * W : row_id_map + ((int64_t)b * T + t) * W;
-  int j = 0;
-  for (int e = E - 1; e >= 0; --e) {
-    const bool bit = bit_of(bits, e);
-    const uint64_t bal = __ballot(bit);  // every lane of the wave takes part
-    if (t < T) {
-      int r = -1;
-      if (bit) {
-        r = toff[e] + lanes_below(bal);
-        for (int i = 0; i < w; ++i) r += wcnt[i][e];
-        row[j] = r;
-        row[E + j] = e;
-        ++j;
+// One-launch row map for short batches of a contiguous bool mask (s_t = 1,
+// T % 16 == 0, 16-byte aligned rows): T <= kFusedMaxTiles * kTile tokens and
+// E <= kFusedMaxE.  Every workgroup counts the whole batch itself -- the mask
+// is E * T bytes (64 KiB at T = 2048, E = 32) -- one (expert, 256-token tile)
+// count per thread from 16 independent 16-byte loads, so the count costs one
+// memory latency per 256 pairs; then it takes its tile's offsets from those
+// counts and emits the tile staged in LDS, written out in 16-byte vectors.
+// This replaces the count / scan / emit launches (and their workspace round
+// trip) where the three launches' fixed costs dominate.
+constexpr int kFusedMaxTiles = 16;
+constexpr int kFusedMaxE = 64;
+
+__device__ __forceinline__ int nonzero_bytes(uint32_t w) {
+  w |= w >> 4;
+  w |= w >> 2;
+  w |= w >> 1;
+  return __popc(w & 0x01010101u);
+}
+
+__global__ __launch_bounds__(kTile) void rowmap_fused_kernel(const uint8_t* __restrict__ map,
+                                                             int64_t s_b, int64_t s_e, int T,
+                                                             int E, int ntiles,
+                                                             int32_t* group_sizes,
+                                                             int32_t* row_id_map) {
+  __shared__ __attribute__((aligned(16))) int32_t stage[kTile * (2 * kFusedMaxE + 1)];
+  __shared__ int cnt[kFusedMaxE][kFusedMaxTiles];
+  __shared__ int wcnt[kTile / kWave][kMaxExperts];
+  __shared__ uint64_t wmask[kTile / kWave][kMaxExperts];
+  __shared__ int toff[kMaxExperts];
+  const int tile = blockIdx.x, b = blockIdx.y;
+  const int t = tile * kTile + threadIdx.x;
+  const uint8_t* mb = map + (int64_t)b * s_b;
+  // this tile's bits first: their loads overlap the whole-batch count
+  uint32_t bits[kMaxExperts / 32];
+  load_mask_bits<1>(mb, min(t, T - 1), s_e, E, t < T, bits);
+  // whole-batch counts: pair q = (expert, tile), 16 vectors of 16 tokens
+  constexpr int kVecPerTile = kTile / 16;
+  const int nvec = T / 16;
+  for (int q = threadIdx.x; q < E * ntiles; q += kTile) {
+    const int e = q / ntiles, i = q - e * ntiles;
+    const uint4* p = reinterpret_cast<const uint4*>(mb + (int64_t)e * s_e) + i * kVecPerTile;
+    const int nv = min(kVecPerTile, nvec - i * kVecPerTile);
+    uint4 v[kVecPerTile];
+#pragma unroll
+    for (int u = 0; u < kVecPerTile; ++u) v[u] = u < nv ? p[u] : make_uint4(0u, 0u, 0u, 0u);
+    int c = 0;
+#pragma unroll
+    for (int u = 0; u < kVecPerTile; ++u)
+      c += nonzero_bytes(v[u].x) + nonzero_bytes(v[u].y) + nonzero_bytes(v[u].z) +
+           nonzero_bytes(v[u].w);
+    cnt[e][i] = c;
+  }
+  wave_counts(bits, E, wcnt, wmask);
+  __syncthreads();
+  // offsets of this tile: exclusive scan over experts of the totals (wave 0,
+  // E <= 64 = one lane per expert) plus the expert's count in earlier tiles
+  if (threadIdx.x < kWave) {
+    const int e = threadIdx.x;
+    int total = 0, before = 0;
+    if (e < E)
+      for (int i = 0; i < ntiles; ++i) {
+        const int c = cnt[e][i];
+        total += c;
+        before += i < tile ? c : 0;
       }
-      if (e >= n) row[e] = r;  // stale column: row if routed, else -1
+    int incl = total;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const int o = __shfl_up(incl, d, kWave);
+      if (e >= d) incl += o;
+    }
+    if (e < E) {
+      toff[e] = incl - total + before;
+      if (group_sizes != nullptr && tile == 0) group_sizes[(int64_t)b * E + e] = total;
     }
   }
-  if (t < T) {
-    for (int c = E + n; c < 2 * E; ++c) row[c] = 0;
-    row[2 * E] = n;
-  }
-  if constexpr (STAGE) {
-    __syncthreads();
-    const int nt = min(kTile, T - tile * kTile);
-    int32_t* g = row_id_map + ((int64_t)b * T + (int64_t)tile * kTile) * W;
-    for (int i = threadIdx.x; i < nt * W; i += kTile) g[i] = stage[i];
-  }
+  __syncthreads();
+  emit_tile<true, false>(bits, T, E, tile, b, wcnt, wmask, toff, stage, nullptr);
+  __syncthreads();
+  // the tile's entries are nt * (2E+1) words, a multiple of 4 (nt % 16 == 0),
+  // and start 16-byte aligned (T % 16 == 0, aligned output)
+  const int nt = min(kTile, T - tile * kTile);
+  const int nw4 = nt * (2 * E + 1) / 4;
+  uint4* g = reinterpret_cast<uint4*>(row_id_map + ((int64_t)b * T + (int64_t)tile * kTile) *
+                                                       (2 * E + 1));
+  const uint4* sv = reinterpret_cast<const uint4*>(stage);
+  for (int i = threadIdx.x; i < nw4; i += kTile) g[i] = sv[i];
 }
 
 // ---------------------------------------------------------- vector copy ----
@@ -741,6 +865,15 @@ extern "C" int uttt_make_row_id_map(const void* routing_map, int mask_bytes, int
   }
   UTTT_REQUIRE(routing_map != nullptr, "make_row_id_map: null routing_map");
   const int ntiles = (T + kTile - 1) / kTile;
+  const bool vec_ok = ((reinterpret_cast<uintptr_t>(routing_map) |
+                        reinterpret_cast<uintptr_t>(row_id_map)) & 15u) == 0;
+  if (mask_bytes == 1 && s_t == 1 && T % 16 == 0 && s_e % 16 == 0 && s_b % 16 == 0 && vec_ok &&
+      ntiles <= kFusedMaxTiles && E <= kFusedMaxE) {
+    hipLaunchKernelGGL(rowmap_fused_kernel, dim3(ntiles, B), dim3(kTile), 0, st,
+                       static_cast<const uint8_t*>(routing_map), s_b, s_e, T, E, ntiles,
+                       group_sizes, row_id_map);
+    return check_launch("make_row_id_map");
+  }
   int32_t* counts = reinterpret_cast<int32_t*>(workspace);
   auto launch = [&](auto mb) {
     constexpr int MB = decltype(mb)::value;

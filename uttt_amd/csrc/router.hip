@@ -222,7 +222,34 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 // 8 consecutive features of one row as fp32 (zero past D or for a dead row).
 template <class XT>
-__device__ __forceinline__ void load8(const typename XT::S* p, int d, int D, bool ok, float (&o)[8]) {
+__device__ __forceinline__ void load8(const typename XT::S* p, int d, int D, bool ok, bool vec,
+                                     float (&o)[8]) {
+  if (vec) {  // wave-uniform: D % 8 == 0 and 16-byte aligned rows
+    // unconditional load (a lane that is off reads its row's first 8
+    // features and zeroes them), so the loads of consecutive calls stay in
+    // flight together; a load under a per-lane condition would be waited
+    // for where the two paths merge
+    const bool in = ok && d + 8 <= D;
+    const typename XT::S* q = p + (in ? d : 0);
+    float v[8];
+    if constexpr (sizeof(typename XT::S) == 4) {
+      const float4 u = *reinterpret_cast<const float4*>(q);
+      const float4 w = *reinterpret_cast<const float4*>(q + 4);
+      v[0] = u.x; v[1] = u.y; v[2] = u.z; v[3] = u.w;
+      v[4] = w.x; v[5] = w.y; v[6] = w.z; v[7] = w.w;
+    } else {
+      const uint4 u = *reinterpret_cast<const uint4*>(q);
+      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[2 * i] = XT::load(static_cast<typename XT::S>(w[i] & 0xffffu));
+        v[2 * i + 1] = XT::load(static_cast<typename XT::S>(w[i] >> 16));
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = in ? v[i] : 0.0f;
+    return;
+  }
   if (ok && d + 8 <= D && ((reinterpret_cast<uintptr_t>(p + d) & (sizeof(typename XT::S) * 8 - 1)) == 0)) {
     if constexpr (sizeof(typename XT::S) == 4) {
       const float4 u = *reinterpret_cast<const float4*>(p + d);
@@ -387,7 +414,7 @@ constexpr int kSmallT = 8;
 template <class XT, int NET, int NW, bool SMALL>
 __global__ __launch_bounds__(NW * kWave) void router_mfma_kernel(
     const typename XT::S* __restrict__ x, const float* __restrict__ rw, int64_t w_sb, int D,
-    float* __restrict__ logits_out, SelectArgs a) {
+    bool vec, float* __restrict__ logits_out, SelectArgs a) {
   constexpr int EB = NET * 32;
   constexpr int NTH = NW * kWave;
   __shared__ float red[SMALL ? 1 : NW][NET][32][33];
@@ -411,12 +438,12 @@ __global__ __launch_bounds__(NW * kWave) void router_mfma_kernel(
 #pragma unroll 4
     for (int c = sl; c < nch; c += TPE) {
       float wv[8];
-      load8<F32T>(Re, c * 8, D, e < E, wv);
+      load8<F32T>(Re, c * 8, D, e < E, vec, wv);
 #pragma unroll
       for (int t = 0; t < kSmallT; ++t) {
         if (t >= nt) break;
         float xv[8];
-        load8<XT>(x + ((int64_t)b * T + t0 + t) * D, c * 8, D, true, xv);
+        load8<XT>(x + ((int64_t)b * T + t0 + t) * D, c * 8, D, true, vec, xv);
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[t] = fmaf(xv[i], wv[i], acc[t]);
       }
@@ -442,11 +469,11 @@ __global__ __launch_bounds__(NW * kWave) void router_mfma_kernel(
     auto fetch = [&](int c, float (&xo)[8], float (&wo)[NET][8]) __attribute__((always_inline)) {
       const int d = c * 16 + 8 * h;
       const bool in = c < c_hi;
-      load8<XT>(xrow, d, D, tv && in, xo);
+      load8<XT>(xrow, d, D, tv && in, vec, xo);
 #pragma unroll
       for (int j = 0; j < NET; ++j) {
         const int e = 32 * j + r;
-        load8<F32T>(R + (int64_t)(e < E ? e : 0) * D, d, D, in && e < E, wo[j]);
+        load8<F32T>(R + (int64_t)(e < E ? e : 0) * D, d, D, in && e < E, vec, wo[j]);
       }
     };
     // a ring of DEPTH chunks in flight: each chunk's slot is refilled with the
@@ -703,10 +730,13 @@ extern "C" int uttt_route_tokens(const void* x, int x_dtype, const float* router
   const int net = (E + 31) / 32;
 #define UTTT_ROUTE_LAUNCH(NET, NW, SMALL)                                                   \
   hipLaunchKernelGGL((router_mfma_kernel<XT, NET, NW, SMALL>), dim3(w.nblk, B),                \
-                     dim3(NW * kWave), 0, st, static_cast<const S*>(x), router_w, w_sb, D,      \
+                     dim3(NW * kWave), 0, st, static_cast<const S*>(x), router_w, w_sb, D, vec, \
                      logits_out, a)
   // a few tokens per batch (generation): vector-ALU logits, no padded MFMA rows
   const bool small = T <= kSmallT;
+  // rows of whole 16-byte vectors: every feature load is one unconditional vector load
+  const bool vec = D % 8 == 0 && w_sb % 4 == 0 &&
+                   ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(router_w)) & 15u) == 0;
   UTTT_DTYPE_SWITCH_LR(x_dtype, XT, {
     using S = typename XT::S;
     switch (net) {
