@@ -141,6 +141,7 @@ struct TileLoader {
   int64_t kstep;          // bytes advanced per K step
   int last;               // last step holding data
   int k_end;
+  int nvalid;             // valid rows from the tile origin (KMajor: rows of 8 per load)
   uint32_t off[kLoadsPerTile];
 
   __device__ __forceinline__ void init(const Operand& op, int r0) {
@@ -149,6 +150,7 @@ struct TileLoader {
     k_end = op.k_end;
     last = (op.k_end + kBK - 1) / kBK - 1;
     int nrows = op.r_end - r0;
+    nvalid = nrows > 0 ? nrows : 0;
     const uint16_t* org;
     if (nrows > 0) {
       org = MAJOR == KMajor ? op.base + (int64_t)r0 * op.ld : op.base + r0;
@@ -195,9 +197,17 @@ struct TileLoader {
   // The masked form loads the lanes whose chunk lies below k_end and writes 16
   // zero bytes to the LDS slot of every other lane (a DMA lands lane i at
   // M0 + 16 i); so it may issue no DMA instruction at all for this wave.
-  template <bool MASKED>
+  // SKIP_ROWS (KMajor token tiles of the APPLY products): a load whose 8 rows
+  // all lie past the valid rows is not issued; its LDS slots keep stale
+  // values, which only reach the products of token columns that are never
+  // stored.  Fewer loads per stage than kLoadsPerStage: the pipeline then
+  // waits on vmcnt(0) wherever it would count loads.
+  template <bool MASKED, bool SKIP_ROWS = false>
   __device__ __forceinline__ void issue(const uint8_t* sb, int step, int t, uint8_t* dst) const {
     uint8_t* d = dst + (t * 4 + wave_id()) * 64 * 16;
+    if constexpr (SKIP_ROWS && !MASKED && MAJOR == KMajor) {
+      if ((t * 4 + wave_id()) * (64 / kChunks) >= nvalid) return;  // wave-uniform
+    }
     if constexpr (!MASKED) {
       __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(sb + off[t]), UTTT_LDS(d), 16,
                                        0, 0);
@@ -466,7 +476,7 @@ __device__ __forceinline__ void run_pipeline(int nk, bool full, PrepFn&& prep, I
     const bool m = load_all(i, ring[i]);
     if constexpr (decltype(i)::value > 0) later_masked |= m;
   });
-  if (later_masked)
+  if (SKIP || later_masked)  // SKIP: the token tiles may issue fewer loads per stage
     wait_vmcnt<0>();
   else
     wait_vmcnt<(kStages - 1) * kLoadsPerStage>();

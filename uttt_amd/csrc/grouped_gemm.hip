@@ -471,8 +471,8 @@ __global__ __launch_bounds__(kThreads) void tn_kernel(TnArgs a, typename Epi::Ar
     constexpr bool M = decltype(masked)::value;
     if constexpr (tile == 0) la0.template issue<M>(sb[0], lstep, t, st);
     else if constexpr (tile == 1) la1.template issue<M>(sb[1], lstep, t, st + kTileBytes);
-    else if constexpr (tile == 2) lx0.template issue<M>(sb[2], lstep, t, st + 2 * kTileBytes);
-    else lx1.template issue<M>(sb[3], lstep, t, st + 3 * kTileBytes);
+    else if constexpr (tile == 2) lx0.template issue<M, SKIP>(sb[2], lstep, t, st + 2 * kTileBytes);
+    else lx1.template issue<M, SKIP>(sb[3], lstep, t, st + 3 * kTileBytes);
   };
   const int w = threadIdx.x >> 6;
   const int wm = w >> 1, wn = w & 1;
