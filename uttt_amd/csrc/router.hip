@@ -30,6 +30,8 @@
 //                          fixed tree (deterministic: no atomics); skipped
 //                          when a batch is one block, whose sums are final;
 //   router_lb_kernel     : lb_loss from those sums.
+#include <type_traits>
+
 #include "common.h"
 
 namespace uttt {
@@ -219,6 +221,7 @@ __global__ __launch_bounds__(sel_tpb(EB)) void router_select_kernel(const float*
 }
 
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 
 // 8 consecutive features of one row as fp32 (zero past D or for a dead row).
 template <class XT>
@@ -486,11 +489,39 @@ __global__ __launch_bounds__(NW * kWave) void router_mfma_kernel(
     for (int c = c_lo; c < c_hi; c += DEPTH) {
 #pragma unroll
       for (int q = 0; q < DEPTH; ++q) {
+        if constexpr (std::is_same_v<XT, BF16T>) {
+          // bf16 x: each fp32 weight is split exactly into three bf16 parts
+          // (hi + mid + lo = w for normal w: 3 x 8 mantissa bits), so the
+          // products x*hi, x*mid, x*lo are exact and the fp32 accumulation
+          // gives fp32 logits on the bf16 matrix cores (one 32x32x16 MFMA
+          // per part covers the lane pair's 16 features; the f32 path needs 8
+          // 32x32x2 MFMAs of twice the cycles)
+          bf16x8_t xb;
 #pragma unroll
-        for (int j = 0; j < NET; ++j)
+          for (int i = 0; i < 8; ++i) xb[i] = static_cast<__bf16>(xr[q][i]);  // exact
 #pragma unroll
-          for (int s8 = 0; s8 < 8; ++s8)
-            acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(xr[q][s8], wr[q][j][s8], acc[j], 0, 0, 0);
+          for (int j = 0; j < NET; ++j) {
+            bf16x8_t hi, mid, lo;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              const float w = wr[q][j][i];
+              hi[i] = static_cast<__bf16>(w);
+              const float r1 = w - static_cast<float>(hi[i]);
+              mid[i] = static_cast<__bf16>(r1);
+              lo[i] = static_cast<__bf16>(r1 - static_cast<float>(mid[i]));
+            }
+            acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xb, hi, acc[j], 0, 0, 0);
+            acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xb, mid, acc[j], 0, 0, 0);
+            acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xb, lo, acc[j], 0, 0, 0);
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < NET; ++j)
+#pragma unroll
+            for (int s8 = 0; s8 < 8; ++s8)
+              acc[j] =
+                  __builtin_amdgcn_mfma_f32_32x32x2f32(xr[q][s8], wr[q][j][s8], acc[j], 0, 0, 0);
+        }
         fetch(c + q + DEPTH, xr[q], wr[q]);
       }
     }
