@@ -125,14 +125,16 @@ __device__ __forceinline__ void staged8(const float* reg, int n, int g, float (&
   v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
 
-__device__ __forceinline__ void load8(const uint16_t* p, float (&v)[8]) {
-  const uint4 u = *reinterpret_cast<const uint4*>(p);
+__device__ __forceinline__ void unpack8(const uint4& u, float (&v)[8]) {
   const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     v[2 * k] = bf16_to_f32((uint16_t)(w[k] & 0xffffu));
     v[2 * k + 1] = bf16_to_f32((uint16_t)(w[k] >> 16));
   }
+}
+__device__ __forceinline__ void load8(const uint16_t* p, float (&v)[8]) {
+  unpack8(*reinterpret_cast<const uint4*>(p), v);
 }
 __device__ __forceinline__ void load8(const float* p, float (&v)[8]) {
   const float4 a = *reinterpret_cast<const float4*>(p);
@@ -164,6 +166,37 @@ __device__ __forceinline__ void staged_epilogue(const f32x16 (&acc0)[2][kNB],
     for (int k = 0; k < 4; ++k) {
       const int it = threadIdx.x + kThreads * k;
       body(it >> 4, Q * 64 + (it >> 4), it & 15);
+    }
+    __syncthreads();
+  });
+}
+
+// The staged epilogue in two phases per quarter: fetch(n, g) for the thread's
+// four items first -- its global loads from clamped (always valid) addresses,
+// straight-line code issued before the quarter is staged, so all of them are
+// in flight together and overlap the staging -- then use(nl, n, g, raw) on
+// each.  (Loads inside a per-item `if (valid)` would each be waited for
+// before the next item's loads issue.)
+template <class FetchFn, class UseFn>
+__device__ __forceinline__ void staged_epilogue_prefetch(const f32x16 (&acc0)[2][kNB],
+                                                         const f32x16 (&acc1)[2][kNB],
+                                                         const TileCtx& c, FetchFn&& fetch,
+                                                         UseFn&& use) {
+  __syncthreads();  // every wave is done reading the stage buffers
+  static_for<4>([&](auto QQ) __attribute__((always_inline)) {
+    constexpr int Q = QQ;
+    decltype(fetch(0, 0)) raw[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int it = threadIdx.x + kThreads * k;
+      raw[k] = fetch(Q * 64 + (it >> 4), it & 15);
+    }
+    stage_quarter<Q>(acc0, acc1, c);
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int it = threadIdx.x + kThreads * k;
+      use(it >> 4, Q * 64 + (it >> 4), it & 15, raw[k]);
     }
     __syncthreads();
   });
@@ -272,18 +305,36 @@ struct EpiS1 {
     const float* dhb = ea.dh + (int64_t)c.b * ea.N * I;
     uint16_t* dyb = ea.dy + (int64_t)c.b * ea.N * I2;
     uint16_t* hb = ea.hid + (int64_t)c.b * ea.N * I;
-    staged_epilogue(acc0, acc1, c, [&](int nl, int n, int g) __attribute__((always_inline)) {
+    using S = typename LR::S;
+    struct Raw {
+      float4 dh0, dh1;
+      S l0, l1, l2;
+    };
+    auto fetch = [&](int n, int g) __attribute__((always_inline)) {
+      const int m = c.m0 + 8 * g;
+      const int tok = c.tt.start + min(c.tt.n0 + n, c.tt.size - 1);  // clamped: always valid
+      const float* p = dhb + (int64_t)tok * I + (m < I ? m : 0);
+      const int64_t li = (int64_t)c.b * ea.N + tok;
+      Raw r;
+      r.dh0 = *reinterpret_cast<const float4*>(p);
+      r.dh1 = *reinterpret_cast<const float4*>(p + 4);
+      r.l0 = ea.lr0 ? ea.lr0[li] : S(0);
+      r.l1 = ea.lr1 ? ea.lr1[li] : S(0);
+      r.l2 = ea.lr2 ? ea.lr2[li] : S(0);
+      return r;
+    };
+    staged_epilogue_prefetch(acc0, acc1, c, fetch, [&](int nl, int n, int g, const Raw& rw) __attribute__((always_inline)) {
       const int m = c.m0 + 8 * g;
       if (c.tt.n0 + n >= c.tt.size || m >= I) return;
       const int tok = c.tt.start + c.tt.n0 + n;
-      const int64_t li = (int64_t)c.b * ea.N + tok;
-      const float l0 = ea.lr0 ? LR::load(ea.lr0[li]) : 1.0f;
-      const float l1 = ea.lr1 ? LR::load(ea.lr1[li]) : 1.0f;
-      const float l2 = ea.lr2 ? LR::load(ea.lr2[li]) : 1.0f;
-      float y0[8], y2[8], dh[8], d0[8], d2[8], hh[8];
+      const float l0 = ea.lr0 ? LR::load(rw.l0) : 1.0f;
+      const float l1 = ea.lr1 ? LR::load(rw.l1) : 1.0f;
+      const float l2 = ea.lr2 ? LR::load(rw.l2) : 1.0f;
+      float y0[8], y2[8], d0[8], d2[8], hh[8];
+      const float dh[8] = {rw.dh0.x, rw.dh0.y, rw.dh0.z, rw.dh0.w,
+                           rw.dh1.x, rw.dh1.y, rw.dh1.z, rw.dh1.w};
       staged8(c.lds0, nl, g, y0);
       staged8(c.lds1, nl, g, y2);
-      load8(dhb + (int64_t)tok * I + m, dh);
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         const float sg = sigmoidf_(y0[u]);
@@ -330,24 +381,44 @@ struct EpiBwd {
     const int I = ea.I, I2 = 2 * I;
     const int64_t bo2 = (int64_t)c.b * ea.N * I2, bo1 = (int64_t)c.b * ea.N * I;
     const int64_t plane = (int64_t)ea.m_tiles * ea.B * ea.N;
-    staged_epilogue(acc0, acc1, c, [&](int nl, int n, int g) __attribute__((always_inline)) {
+    using S = typename LR::S;
+    struct Raw {
+      uint4 gd0, gd2, dh, gd;
+      S l0, l1, l2;
+    };
+    auto fetch = [&](int n, int g) __attribute__((always_inline)) {
+      const int m = c.m0 + 8 * g;
+      const int tok = c.tt.start + min(c.tt.n0 + n, c.tt.size - 1);  // clamped: always valid
+      const int mc = m < I ? m : 0;
+      const int64_t li = (int64_t)c.b * ea.N + tok;
+      const int64_t r2 = bo2 + (int64_t)tok * I2;
+      Raw r;
+      r.gd0 = *reinterpret_cast<const uint4*>(ea.gy + r2 + mc);
+      r.gd2 = *reinterpret_cast<const uint4*>(ea.gy + r2 + I + mc);
+      r.dh = *reinterpret_cast<const uint4*>(ea.dhg + r2 + mc);
+      r.gd = *reinterpret_cast<const uint4*>(ea.dhg + r2 + I + mc);
+      r.l0 = ea.lr0[li];
+      r.l1 = ea.lr1[li];
+      r.l2 = ea.lr2[li];
+      return r;
+    };
+    staged_epilogue_prefetch(acc0, acc1, c, fetch, [&](int nl, int n, int g, const Raw& rw) __attribute__((always_inline)) {
       const int m = c.m0 + 8 * g;
       const bool ok = c.tt.n0 + n < c.tt.size && m < I;
       const int tok = c.tt.start + c.tt.n0 + n;
       float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f;
       if (ok) {
-        const int64_t li = (int64_t)c.b * ea.N + tok;
-        const float L0 = LR::load(ea.lr0[li]);
-        const float L1 = LR::load(ea.lr1[li]);
-        const float L2 = LR::load(ea.lr2[li]);
+        const float L0 = LR::load(rw.l0);
+        const float L1 = LR::load(rw.l1);
+        const float L2 = LR::load(rw.l2);
         float x0[8], x2[8], gd0[8], gd2[8], dh[8], gd[8];
         staged8(c.lds0, nl, g, x0);
         staged8(c.lds1, nl, g, x2);
         const int64_t r2 = bo2 + (int64_t)tok * I2, r1 = bo1 + (int64_t)tok * I;
-        load8(ea.gy + r2 + m, gd0);
-        load8(ea.gy + r2 + I + m, gd2);
-        load8(ea.dhg + r2 + m, dh);
-        load8(ea.dhg + r2 + I + m, gd);
+        unpack8(rw.gd0, gd0);
+        unpack8(rw.gd2, gd2);
+        unpack8(rw.dh, dh);
+        unpack8(rw.gd, gd);
         float o_gdh[8], o_gx0[8], o_gx2[8], o_dx0[8], o_dx2[8], o_hl[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
