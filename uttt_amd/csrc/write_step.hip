@@ -91,33 +91,42 @@ __global__ __launch_bounds__(kWS) void write_step_kernel(
   const float mc = MOM ? m_coeff[seg / seg_per_batch] : 0.0f;
   float4 u[NV];
   float ss_old = 0.0f, ss_new = 0.0f;
+  // Every load is unconditional (a lane past the row end re-reads the row's
+  // first vector and zeroes it), so all NV vectors of a lane are in flight
+  // together; loads under the per-lane `e < S` would each be waited for
+  // before the next iteration's loads issue.
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int e = 4 * (lane + kWave * i);
-    if (e < S) {
-      const float4 w = nt_load4(master + base + e);
-      float4 g = load_grad4<GT>(grad + base + e);
-      if constexpr (FASTNORM) {
-        const Half4 f = nt_load_h4(fast_in + base + e);
-        ss_old += sumsq4(make_float4(bf16_to_f32(f.h[0]), bf16_to_f32(f.h[1]),
-                                     bf16_to_f32(f.h[2]), bf16_to_f32(f.h[3])));
-      } else {
-        ss_old += sumsq4(w);
-      }
-      if constexpr (MOM) {
-        const float4 m = nt_load4(mom_in + base + e);
-        g.x = g.x + m.x * mc;
-        g.y = g.y + m.y * mc;
-        g.z = g.z + m.z * mc;
-        g.w = g.w + m.w * mc;
-        nt_store4(mom_out + base + e, g);
-      }
-      u[i].x = w.x + g.x * lr_scale;
-      u[i].y = w.y + g.y * lr_scale;
-      u[i].z = w.z + g.z * lr_scale;
-      u[i].w = w.w + g.w * lr_scale;
-      ss_new += sumsq4(u[i]);
+    const bool ok = e < S;
+    const int ec = ok ? e : 0;
+    const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const float4 wl = nt_load4(master + base + ec);
+    const float4 gl = load_grad4<GT>(grad + base + ec);
+    const float4 w = ok ? wl : z;
+    float4 g = ok ? gl : z;
+    if constexpr (FASTNORM) {
+      const Half4 f = nt_load_h4(fast_in + base + ec);
+      const float4 fv = make_float4(bf16_to_f32(f.h[0]), bf16_to_f32(f.h[1]),
+                                    bf16_to_f32(f.h[2]), bf16_to_f32(f.h[3]));
+      ss_old += sumsq4(ok ? fv : z);
+    } else {
+      ss_old += sumsq4(w);
     }
+    if constexpr (MOM) {
+      const float4 ml = nt_load4(mom_in + base + ec);
+      const float4 m = ok ? ml : z;
+      g.x = g.x + m.x * mc;
+      g.y = g.y + m.y * mc;
+      g.z = g.z + m.z * mc;
+      g.w = g.w + m.w * mc;
+      if (ok) nt_store4(mom_out + base + e, g);
+    }
+    u[i].x = w.x + g.x * lr_scale;
+    u[i].y = w.y + g.y * lr_scale;
+    u[i].z = w.z + g.z * lr_scale;
+    u[i].w = w.w + g.w * lr_scale;
+    ss_new += sumsq4(u[i]);
   }
   const float nu = sqrtf(wave_sum(ss_old));
   const float den = sqrtf(wave_sum(ss_new)) + 1e-5f;
