@@ -102,6 +102,15 @@ __device__ __forceinline__ float sigmoid_(float x) {
 template <int CPL>
 constexpr int rows_k1() { return CPL <= 3 ? 2 : 1; }
 
+// p[ch] where `ok`, else zeros; the load itself is unconditional (a lane
+// that is off reads p[0], which every caller keeps valid), so a wave's loads
+// of a step are all in flight before the first is used -- a load under a
+// per-lane condition is waited for where the two paths merge.
+__device__ __forceinline__ uint4 load_or_zero(const uint4* p, int ch, bool ok) {
+  const uint4 v = p[ok ? ch : 0];
+  return ok ? v : make_uint4(0, 0, 0, 0);
+}
+
 template <int MB, int CPL, int MT>
 __global__ __launch_bounds__(kDecThreads) void decode_gate_up_kernel(
     const uint16_t* __restrict__ x, int T, int D, const uint16_t* __restrict__ w02,
@@ -131,8 +140,8 @@ __global__ __launch_bounds__(kDecThreads) void decode_gate_up_kernel(
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
           const int ch = lane + c * kWave;
-          w0[r][c] = ch < nch ? p0[ch] : make_uint4(0, 0, 0, 0);
-          w2[r][c] = ch < nch ? p2[ch] : make_uint4(0, 0, 0, 0);
+          w0[r][c] = load_or_zero(p0, ch, ch < nch);
+          w2[r][c] = load_or_zero(p2, ch, ch < nch);
         }
       }
     };
@@ -152,7 +161,7 @@ __global__ __launch_bounds__(kDecThreads) void decode_gate_up_kernel(
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
           const int ch = lane + c * kWave;
-          xv[j][c] = (j < nt && ch < nch) ? px[ch] : make_uint4(0, 0, 0, 0);
+          xv[j][c] = load_or_zero(px, ch, j < nt && ch < nch);
         }
       }
       auto compute = [&](int i0, const uint4 (&w0)[RP][CPL],
@@ -225,7 +234,7 @@ __device__ __forceinline__ void down_row(
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
           const int ch = lane + c * kWave;
-          w[q][c] = (ch < nch && ex[q] >= 0) ? pw[ch] : make_uint4(0, 0, 0, 0);
+          w[q][c] = load_or_zero(pw, ch, ch < nch && ex[q] >= 0);
         }
       }
 #pragma unroll
@@ -242,7 +251,7 @@ __device__ __forceinline__ void down_row(
 #pragma unroll
           for (int c = 0; c < CPL; ++c) {
             const int ch = lane + c * kWave;
-            if (ch < nch) a = dot8(w[q][c], ph[ch], a);
+            a = dot8(w[q][c], load_or_zero(ph, ch, ch < nch), a);  // w is 0 past nch
           }
           const float y = bf16_to_f32(f32_to_bf16(wave_sum(a)));
           const float p = probs[(int64_t)b * p_sb + (int64_t)e * p_se + (int64_t)t * p_st];
@@ -315,7 +324,7 @@ __global__ __launch_bounds__(kDecThreads) void decode_down_t1_kernel(
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
       const int ch = lane + c * kWave;
-      h[q][c] = (ex[q] >= 0 && ch < nch) ? ph[ch] : make_uint4(0, 0, 0, 0);
+      h[q][c] = load_or_zero(ph, ch, ex[q] >= 0 && ch < nch);
     }
   }
   auto load = [&](int d, uint4 (&w)[2][CPL]) __attribute__((always_inline)) {
@@ -326,7 +335,7 @@ __global__ __launch_bounds__(kDecThreads) void decode_down_t1_kernel(
 #pragma unroll
       for (int c = 0; c < CPL; ++c) {
         const int ch = lane + c * kWave;
-        w[q][c] = (ex[q] >= 0 && ch < nch) ? pw[ch] : make_uint4(0, 0, 0, 0);
+        w[q][c] = load_or_zero(pw, ch, ex[q] >= 0 && ch < nch);
       }
     }
   };
