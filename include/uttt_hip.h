@@ -313,6 +313,24 @@ int uttt_grouped_update_bwd(const void* w0_w2, const void* w1, const void* k, co
  * [B, rows, N] intermediates): out[b, c, r] = in[b, r, c], 2-byte elements. */
 int uttt_transpose_2byte(const void* in, int B, int R, int C, void* out, void* stream);
 
+/* Update-input preprocessing (replaces the qkv_silu / v_norm / qk_norm steps
+ * of _preprocess_update_inputs, uttt_llm/flame/custom_models/uttt_moe/
+ * modeling_recurrent_lact.py:641-648, with l2_norm of ref_base.py:182-186):
+ * for each of `rows` rows of D elements (row r at in + r * ld_in), optional
+ * y = silu(x) rounded to dtype, then optional y / (|y| + 1e-5) with the norm
+ * rounded to dtype and the eps added in dtype; written to out + r * ld_out
+ * (out may be in).  dtype: UTTT_BF16, UTTT_F16 or UTTT_F32; D and the strides
+ * multiples of 8, D <= 4096, 16-byte aligned tensors. */
+int uttt_rows_silu_l2norm(const void* in, int dtype, int64_t rows, int D, int64_t ld_in,
+                          int silu, int l2, void* out, int64_t ld_out, void* stream);
+
+/* Test hook (no reference counterpart): grids of the token-grouped GEMMs
+ * with at least `min_tiles` workgroup tiles take the XCD super-tile order
+ * (default 2048, one value per process; a negative value restores it).
+ * Returns the previous value.  Results do not depend on it: tests lower it
+ * to run small problems down the path the large ones take. */
+long long uttt_debug_set_supertile_min_tiles(long long min_tiles);
+
 /* WRITE step of the fast weights.  Replaces the write of
  * _apply_moe_update_dense (uttt_llm/flame/custom_models/uttt_moe/
  * modeling_recurrent_lact.py:754-825; seg = C, norm_from_fast = 0,

@@ -1,0 +1,142 @@
+"""GPU parity of the uTTT-MoE caller glue (uttt_amd/moe.py) against the
+oracle's compositions:
+  - the routed prefill read (route -> row map -> permute -> grouped APPLY ->
+    gate-weighted unpermute, modeling_recurrent_lact.py:296-349) at the
+    configs[4] chunk (T = 2048, E = 32, D = 1536, I = 3072) and with four
+    fast-weight heads, against oracle/moe_read.apply_moe_grouped on the
+    router's own mask and gates;
+  - one writer's gradients (M:453-518) and the aggregate of several writers
+    (M:2428-2445), forward and backward, against oracle/moe_update.py;
+  - the update-input preprocessing kernel (silu, l2 norm per head / per row)
+    against oracle/moe_update.silu_l2norm_rows.
+Bars: rtol 2e-2 in bf16 (tests.helpers.assert_bf16_close) for GEMM outputs;
+the preprocessing within one bf16 rounding (rtol 8e-3) or 1e-5 in fp32, since
+its fp32 sum of squares runs in another order than torch's and its sigmoid
+uses the hardware exp (about 1 ulp of fp32).
+"""
+import pytest
+import torch
+
+from oracle import moe_read as MR
+from oracle import moe_update as MU
+from tests.helpers import assert_bf16_close
+from uttt_amd import moe
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _close(ours, ref, rtol, name):
+    o, r = ours.detach().float().cpu(), ref.float()
+    bad = (o - r).abs() > rtol * r.abs() + 1e-6
+    assert not bad.any(), f"{name}: {int(bad.sum())} of {bad.numel()} elements off"
+
+
+@pytest.mark.parametrize("dtype,heads,hd", [(torch.bfloat16, 4, 96), (torch.float32, 2, 64),
+                                            (torch.bfloat16, 1, 1536)])
+def test_preprocess_update_inputs(dtype, heads, hd):
+    g = torch.Generator().manual_seed(heads)
+    B, Lx = 2, 37
+    k = (torch.randn(B, Lx, heads * hd, generator=g) * 2).to(dtype)
+    v = (torch.randn(B, Lx, heads * hd, generator=g) * 2).to(dtype)
+    lr = torch.sigmoid(torch.randn(B, Lx, 3, generator=g)) * 0.1
+    rtol = 8e-3 if dtype == torch.bfloat16 else 1e-5
+    kt, vt, lt = moe.preprocess_update_inputs(k.to(DEV), v.to(DEV), lr.to(DEV), heads,
+                                              qkv_silu=True, v_norm=True, qk_norm=True)
+    rk = MU.head_tokens(MU.silu_l2norm_rows(k, True, True, rows_of=hd), heads)
+    rv = MU.head_tokens(MU.silu_l2norm_rows(v, True, True), heads)
+    _close(kt, rk, rtol, "k")
+    _close(vt, rv, rtol, "v")
+    assert torch.equal(lt.cpu(), MU.lr_tokens(lr, heads))
+    # each switch alone
+    for silu, l2 in ((True, False), (False, True)):
+        out = moe.rows_silu_l2norm(k.to(DEV), silu, l2, rows_of=hd)
+        _close(out, MU.silu_l2norm_rows(k, silu, l2, rows_of=hd), rtol, f"silu={silu} l2={l2}")
+    with pytest.raises(AssertionError):
+        moe.rows_silu_l2norm(k.float().to(DEV).requires_grad_(), True, True)
+
+
+@pytest.mark.parametrize("T,E,D,I,heads,topk,combine", [
+    (2048, 32, 1536, 3072, 1, 2, "topk_renorm"),   # the configs[4] chunk read
+    (256, 16, 4 * 96, 192, 4, 2, "selected_prob"),  # four fast-weight heads
+])
+def test_routed_read_matches_oracle(T, E, D, I, heads, topk, combine):
+    g = torch.Generator().manual_seed(T + E)
+    hd = D // heads
+    x = torch.randn(1, T, D, generator=g).to(torch.bfloat16)
+    W02 = (torch.randn(1, E, 2 * I, hd, generator=g) / hd ** 0.5).to(torch.bfloat16)
+    W1 = (torch.randn(1, E, hd, I, generator=g) / I ** 0.5).to(torch.bfloat16)
+    R = torch.randn(E, hd, generator=g) / hd ** 0.5
+    bias = -1.1 * torch.log(torch.arange(E, dtype=torch.float32) + 1)
+    cfg = moe.RouterConfig(topk=topk, combine_mode=combine)
+    out, (bal_sum, gs) = moe.apply_moe_fast_weights_grouped(
+        x.to(DEV), W02[:, :, :I].to(DEV), W1.to(DEV), W02[:, :, I:].to(DEV), R.to(DEV), cfg,
+        heads, routing_bias=bias.to(DEV))
+    assert out.shape == x.shape and out.dtype == x.dtype
+    # the routing the read used (the router is deterministic)
+    xt = moe.reshape_head_tokens(x.to(DEV), heads)
+    mask, gs2, probs, bal = moe.route(xt, R.to(DEV), cfg, routing_bias=bias.to(DEV))
+    assert torch.equal(gs, gs2) and torch.equal(gs2, mask.sum(-1, dtype=torch.int32))
+    assert torch.equal(bal_sum, bal.sum(-1))
+    ref = MR.apply_moe_grouped(MU.head_tokens(x, heads), W02, W1, mask.cpu(), probs.cpu(), topk)
+    ref = ref.reshape(1, T, D)
+    assert_bf16_close(out, ref, name="routed read")
+    # precomputed w0_w2 gives the same launches
+    again, _ = moe.apply_moe_fast_weights_grouped(x.to(DEV), None, W1.to(DEV), None, R.to(DEV),
+                                                  cfg, heads, routing_bias=bias.to(DEV),
+                                                  precomputed_w0_w2=W02.to(DEV))
+    assert torch.equal(again, out)
+
+
+def _writer_inputs(T, E, D, k, seed):
+    g = torch.Generator().manual_seed(seed)
+    kk = torch.nn.functional.normalize(torch.randn(1, T, D, generator=g), dim=-1).to(torch.bfloat16)
+    vv = torch.nn.functional.normalize(torch.randn(1, T, D, generator=g), dim=-1).to(torch.bfloat16)
+    lr = torch.sigmoid(torch.randn(1, T, 3, generator=g)) * 0.1
+    s = torch.randn(1, E, T, generator=g)
+    idx = s.topk(k, dim=1).indices
+    mask = torch.zeros(1, E, T, dtype=torch.bool).scatter_(1, idx, True)
+    probs = (torch.softmax(s, dim=1) * mask).float()
+    return kk, vv, lr, mask, probs
+
+
+@pytest.mark.parametrize("n_writers", [1, 3])
+def test_update_glue_and_aggregate(n_writers):
+    E, D, I, k = 8, 128, 256, 2
+    Ts = [300, 257, 512][:n_writers]
+    g = torch.Generator().manual_seed(5)
+    W02 = (torch.randn(1, E, 2 * I, D, generator=g) / D ** 0.5).to(torch.bfloat16)
+    W1 = (torch.randn(1, E, D, I, generator=g) / D ** 0.5).to(torch.bfloat16)
+    G02 = (torch.randn(1, E, 2 * I, D, generator=g) * 0.02).to(torch.bfloat16)
+    G1 = (torch.randn(1, E, D, I, generator=g) * 0.02).to(torch.bfloat16)
+    cpu = [_writer_inputs(T, E, D, k, 10 + i) for i, T in enumerate(Ts)]
+    ws = [moe.WriterInputs(*(t.to(DEV).requires_grad_(t.is_floating_point()) if j != 3
+                             else t.to(DEV) for j, t in enumerate(c))) for c in cpu]
+    dw0, dw1, dw2 = moe.aggregate_moe_update_grads(ws, W02[:, :, :I].to(DEV), W1.to(DEV),
+                                                   W02[:, :, I:].to(DEV), k)
+    assert dw0.dtype == torch.float32 and dw0.shape == (1, E, I, D)
+    s02, s1 = MU.aggregate_grads(cpu, W02, W1, k)
+    assert_bf16_close(dw0, s02[:, :, :I], name="dW0")
+    assert_bf16_close(dw2, s02[:, :, I:], name="dW2")
+    assert_bf16_close(dw1, s1, name="dW1")
+    if n_writers == 1:
+        one = moe.compute_moe_update_grads_grouped(*(t.detach() for t in (ws[0].k_tokens,
+                                                                           ws[0].v_tokens,
+                                                                           ws[0].lr_tokens)),
+                                                   W02[:, :, :I].to(DEV), W1.to(DEV),
+                                                   W02[:, :, I:].to(DEV), ws[0].expert_mask,
+                                                   ws[0].expert_mask.sum(-1, dtype=torch.int32),
+                                                   ws[0].router_probs.detach(), k)
+        for a, b in zip(one, (dw0, dw1, dw2)):
+            assert torch.equal(a, b.detach())
+    # backward: upstream gradients of (dW0, dW1, dW2) in the master dtype
+    torch.autograd.backward([dw0, dw1, dw2], [G02[:, :, :I].float().to(DEV), G1.float().to(DEV),
+                                              G02[:, :, I:].float().to(DEV)])
+    torch.cuda.synchronize()
+    for i, (c, w) in enumerate(zip(cpu, ws)):
+        ref = MU.writer_grads_bwd(*c, k, W02, W1, G02, G1)
+        nm = f"writer {i}"
+        assert_bf16_close(w.k_tokens.grad, ref[2], name="grad_k " + nm)
+        assert_bf16_close(w.v_tokens.grad, ref[3], name="grad_v " + nm)
+        assert_bf16_close(w.lr_tokens.grad, ref[4].float(), name="grad_lr " + nm)
+        assert_bf16_close(w.router_probs.grad, ref[5], name="grad_probs " + nm)

@@ -17,6 +17,8 @@ namespace uttt {
 // ---------------------------------------------------------------- status ----
 void set_error(const char* fmt, ...);
 int check_launch(const char* what);
+// Zero `bytes` bytes at p on stream st with a fill kernel (graph-capture safe).
+int zero_fill_async(void* p, size_t bytes, hipStream_t st, const char* what);
 
 #define UTTT_REQUIRE(cond, ...)          \
   do {                                   \

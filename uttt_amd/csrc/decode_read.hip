@@ -448,11 +448,7 @@ extern "C" int uttt_moe_decode_read(const void* x, int B, int T, int D, const vo
   hipStream_t st = as_stream(stream);
   UTTT_REQUIRE(x && w0_w2 && w1 && expert_mask && probs && out, "moe_decode_read: null pointer");
   if (I == 0) {
-    if (hipMemsetAsync(out, 0, sizeof(uint16_t) * (size_t)B * T * D, st) != hipSuccess) {
-      set_error("moe_decode_read: memset failed");
-      return UTTT_ERR_HIP;
-    }
-    return UTTT_OK;
+    return zero_fill_async(out, sizeof(uint16_t) * (size_t)B * T * D, st, "moe_decode_read");
   }
   const size_t need = uttt_moe_decode_read_workspace_bytes(B, T, E, I);
   UTTT_REQUIRE(workspace != nullptr && workspace_bytes >= need,

@@ -203,8 +203,13 @@ __device__ __forceinline__ void staged_epilogue_prefetch(const f32x16 (&acc0)[2]
 }
 
 // --- epilogue: plain store of both tiles into a token-major [B, N, ld] buffer
+// Every epilogue states kStaleColumnsUnused: true only when it reads, stores
+// or reduces nothing of the token columns at or past its segment's end.  The
+// MFMA-skipping (SKIP) variant leaves stale LDS data in those columns'
+// products, so only such epilogues may take it.
 template <class OutT>
 struct EpiStore {
+  static constexpr bool kStaleColumnsUnused = true;  // per-column stores, masked by segment
   struct Args {
     OutT* out;
     int64_t ld;
@@ -230,6 +235,7 @@ struct EpiStore {
 // reference's bf16 tensor arithmetic has: A = X X^T (with c A as out2),
 // B = b A + (c A) A, X' = a X + B X.
 struct EpiLinComb {
+  static constexpr bool kStaleColumnsUnused = true;
   struct Args {
     uint16_t* out;
     uint16_t* out2;
@@ -263,6 +269,7 @@ struct EpiLinComb {
 
 // --- epilogue: APPLY gate/up, h = y2 * silu(y0) (acc0 = w0 rows, acc1 = w2 rows)
 struct EpiSwiGLU {
+  static constexpr bool kStaleColumnsUnused = true;  // per-column stores, masked by segment
   struct Args {
     uint16_t* out;
     int I, N, token_major;
@@ -292,6 +299,7 @@ struct EpiSwiGLU {
 //   Hid = lr1 silu(Y0) Y2; lr = 1 when the lr pointers are null.
 template <class LR>
 struct EpiS1 {
+  static constexpr bool kStaleColumnsUnused = false;  // not audited for the SKIP variant
   struct Args {
     const float* dh;  // [B, N, I]
     const typename LR::S *lr0, *lr1, *lr2;
@@ -368,6 +376,7 @@ struct EpiS1 {
 // tile's 128 hidden rows, lr_part[j][mt][b][tok].
 template <class LR>
 struct EpiBwd {
+  static constexpr bool kStaleColumnsUnused = false;  // reduces over tile rows per token
   struct Args {
     const uint16_t* gy;
     const uint16_t* dhg;
@@ -889,8 +898,10 @@ TnArgs tn_args(const void* a0, const void* a1, const void* x, int K, int64_t lda
 }
 
 // Grids from this many tiles up (8 rounds of one workgroup per CU) take the
-// XCD super-tile order.
+// XCD super-tile order.  A process-wide value so that tests can send small
+// grids down the same path (uttt_debug_set_supertile_min_tiles).
 constexpr int64_t kXcdMapMinTiles = 8 * 256;
+int64_t g_xcd_map_min_tiles = kXcdMapMinTiles;
 
 // Super-tile shape for m_tiles m-tiles: gm x gn with gm * gn <= 32 (one
 // workgroup per CU of an XCD), minimising the slices fetched per tile,
@@ -911,9 +922,16 @@ void super_tile(int m_tiles, int* gm, int* gn) {
 
 // Epilogues whose launches take the MFMA-skipping variant when tokens per
 // expert are few (the per-layer APPLY): K-major gate/up and bf16 products.
+// The variant leaves stale LDS contents (possibly NaN / Inf from an earlier
+// kernel) in the products of token columns past the segment, so an epilogue
+// may join only if it never touches those columns (kStaleColumnsUnused).
 template <int AMAJ, class Epi>
 constexpr bool kSkippable =
     AMAJ == KMajor && (std::is_same_v<Epi, EpiSwiGLU> || std::is_same_v<Epi, EpiStore<uint16_t>>);
+static_assert(kSkippable<KMajor, EpiSwiGLU> <= EpiSwiGLU::kStaleColumnsUnused &&
+                  kSkippable<KMajor, EpiStore<uint16_t>> <= EpiStore<uint16_t>::kStaleColumnsUnused &&
+                  !kSkippable<KMajor, EpiS1<BF16T>> && !kSkippable<KMajor, EpiBwd<BF16T>>,
+              "the SKIP variant needs an epilogue that ignores stale token columns");
 
 template <int AMAJ, class Epi>
 int launch_tn(TnArgs t, const typename Epi::Args& ea, int B, hipStream_t st,
@@ -922,7 +940,7 @@ int launch_tn(TnArgs t, const typename Epi::Args& ea, int B, hipStream_t st,
   if (tiles == 0) return UTTT_OK;
   t.B = B;
   int64_t blocks = tiles;
-  if (tiles >= kXcdMapMinTiles) {
+  if (tiles >= g_xcd_map_min_tiles) {
     super_tile(t.m_tiles, &t.gm, &t.gn);
     t.n_super_m = (t.m_tiles + t.gm - 1) / t.gm;
     const int64_t n_super_n = ((int64_t)B * t.n_tiles_ub + t.gn - 1) / t.gn;
@@ -935,6 +953,7 @@ int launch_tn(TnArgs t, const typename Epi::Args& ea, int B, hipStream_t st,
   if (int rc = check_grid(blocks, what)) return rc;
   // fewer than 256 tokens per expert on average: many tiles at segment ends
   if constexpr (kSkippable<AMAJ, Epi>) {
+    static_assert(Epi::kStaleColumnsUnused, "SKIP variant with an epilogue that reads stale columns");
     if ((int64_t)t.N < (int64_t)kBRows * t.E) {
       hipLaunchKernelGGL((tn_kernel<AMAJ, Epi, true>), dim3((unsigned)blocks), dim3(kThreads), 0,
                          st, t, ea);
@@ -1119,6 +1138,12 @@ extern "C" int uttt_grouped_gemm_tn2(const void* wa, const void* xa, const void*
   return launch_wide<RMajor>(wa, xa, K, wb, xb, K, M, M, (int64_t)M * K,
                              static_cast<uint16_t*>(y), B, E, N, group_sizes, as_stream(stream),
                              "grouped_gemm_tn2");
+}
+
+extern "C" long long uttt_debug_set_supertile_min_tiles(long long min_tiles) {
+  const long long prev = (long long)g_xcd_map_min_tiles;
+  g_xcd_map_min_tiles = min_tiles < 0 ? kXcdMapMinTiles : (int64_t)min_tiles;
+  return prev;
 }
 
 extern "C" size_t uttt_update_stage1_workspace_bytes(int B, int I, int N) {

@@ -856,10 +856,7 @@ extern "C" int uttt_make_row_id_map(const void* routing_map, int mask_bytes, int
   hipStream_t st = as_stream(stream);
   if (T == 0) {
     if (group_sizes != nullptr) {
-      if (hipMemsetAsync(group_sizes, 0, sizeof(int32_t) * B * E, st) != hipSuccess) {
-        set_error("make_row_id_map: memset failed");
-        return UTTT_ERR_HIP;
-      }
+      return zero_fill_async(group_sizes, sizeof(int32_t) * B * E, st, "make_row_id_map");
     }
     return UTTT_OK;
   }

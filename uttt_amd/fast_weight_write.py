@@ -111,6 +111,64 @@ def apply_moe_update_dense(grads, fastw, masterw, momentum_buf=None, m_coeff=Non
     return tuple(fast), tuple(master), (tuple(mom) if use_mom else momentum_buf)
 
 
+def apply_moe_update_packed(dW0_W2, dW1, M0_W2, M1, momentum_buf=None, m_coeff=None,
+                            lr_scale=1.0, use_momentum=True, use_moun=False, out=None):
+    """apply_moe_update_dense on the packed pool: dW0_W2 / M0_W2 [B,E,2I,D]
+    (w0 rows then w2 rows of each expert, the layout the grouped kernels
+    read), dW1 / M1 [B,E,D,I].  The write is per row and Newton-Schulz per
+    [I, D] matrix, so the result is the three-matrix write's (M:754-825)
+    without splitting or concatenating the pool.  momentum_buf: (mom0_w2,
+    mom1) fp32 or None.  Returns ((fast0_w2, fast1) bf16, (master0_w2,
+    master1) fp32, momentum_buf).  out: optional ((fast0_w2, fast1),
+    (master0_w2, master1)) to write in place of new tensors (masters may be
+    the inputs: each row is read before it is written)."""
+    use_mom = use_momentum and momentum_buf is not None and m_coeff is not None
+    B = M0_W2.shape[0]
+    coeff = _coeff_per_batch(m_coeff, B, M0_W2.device) if use_mom else None
+    fast, master, mom = [], [], []
+    for i, (g, w) in enumerate(((dW0_W2, M0_W2), (dW1, M1))):
+        assert w.dim() == 4 and w.dtype == torch.float32 and w.is_contiguous(), \
+            "masters are contiguous fp32 [B, E, R, C]"
+        assert g.shape == w.shape, "gradient must match the master"
+        _, E, R, C = w.shape
+        fo = mo_ = None
+        if out is not None:
+            fo, mo_ = out[0][i], out[1][i]
+            assert fo.dtype == torch.bfloat16 and fo.shape == w.shape and fo.is_contiguous()
+            assert mo_.dtype == torch.float32 and mo_.shape == w.shape and mo_.is_contiguous()
+        if use_moun:
+            if use_mom:
+                g = _momentum(g, momentum_buf[i], coeff)
+                mom.append(g)
+            nmat = B * E * (2 if i == 0 else 1)    # w0 and w2 are separate matrices
+            step = newton_schulz5(g.reshape(nmat, R * B * E // nmat, C), lr_scale).reshape(g.shape)
+            g_use, mom_in, cb, scale = step, None, None, 1.0
+        else:
+            g_use = g.contiguous()
+            mom_in, cb, scale = (momentum_buf[i].contiguous() if use_mom else None), coeff, lr_scale
+        f, m, mo = _write_into(w, g_use, mom_in, cb, scale, E * R, C, fo, mo_)
+        if not use_moun and use_mom:
+            mom.append(mo)
+        fast.append(f)
+        master.append(m)
+    return tuple(fast), tuple(master), (tuple(mom) if use_mom else momentum_buf)
+
+
+def _write_into(master, grad, mom, m_coeff_b, lr_scale, rows, C, fast_out=None, master_out=None):
+    """_write_one with optional caller-provided outputs (norm-preserving
+    master renorm, norms from the master)."""
+    L.require_device(master, grad, mom, m_coeff_b)
+    B = master.shape[0]
+    master_out = torch.empty_like(master) if master_out is None else master_out
+    fast_out = (torch.empty(master.shape, dtype=torch.bfloat16, device=master.device)
+                if fast_out is None else fast_out)
+    mom_out = torch.empty_like(mom) if mom is not None else None
+    L.call("uttt_write_step", L.ptr(master), None, L.ptr(grad), L.dtype_code(grad.dtype),
+           L.ptr(mom), L.ptr(m_coeff_b), float(lr_scale), B, rows, C, C, 0, 1,
+           L.ptr(master_out), L.ptr(fast_out), L.ptr(mom_out), L.stream_of(master))
+    return fast_out, master_out, mom_out
+
+
 def apply_shared_update(agg_grads, fastw, masterw, momentum_buf=None, momentum_coeffs=None, *,
                         r: int, lr_scale: float = 1.0, master_renorm: bool = False,
                         use_momentum: bool = True, use_moun: bool = False):

@@ -318,8 +318,8 @@ class PermuteKVAndLRs(torch.autograd.Function):
         k = k.contiguous()
         v = v.contiguous()
         lr0_2d, lr1_2d, lr2_2d = (x.contiguous() for x in (lr0_2d, lr1_2d, lr2_2d))
-        routing_map = expert_mask.to(torch.int32)
-        row_id_map = make_row_id_map(routing_map, B, T, E)
+        # bool / uint8 / int32 masks are read as stored (no int32 copy)
+        row_id_map = make_row_id_map(expert_mask, B, T, E)
         num_out = topk * T
         out_k = torch.empty((B, num_out, H), dtype=k.dtype, device=k.device)
         out_v = torch.empty_like(out_k)

@@ -1,0 +1,251 @@
+"""uTTT-MoE caller glue on the gfx950 ops: the routed fast-weight read, one
+writer's fast-weight gradients, and the gradients of all writers of a chunk
+summed in one grouped call (the aggregate write's input).
+
+Reference (cited M:line):
+uttt_llm/flame/custom_models/uttt_moe/modeling_recurrent_lact.py
+  reshape_head_tokens / merge_head_tokens   M:132-144
+  route, route_writers                      M:147-169 (_route_tokens; route_writers:
+                                            all writers of a chunk in one launch)
+  apply_moe_fast_weights_grouped            M:296-349
+  preprocess_update_inputs                  M:630-665 (silu, v norm, per-head k norm)
+  rows_silu_l2norm                          l2_norm of ref_base.py:182-186 (+ silu)
+  moe_update_grads_packed /
+  compute_moe_update_grads_grouped          M:453-518
+  aggregate_moe_update_grads                M:2381-2546 (the writers' raw
+                                            gradients summed at M:2444-2445)
+
+Every kernel call goes through the drop-in ops of uttt_amd.lact_moe_triton
+(autograd included), so gradients flow back to k, v, lr and the router
+probabilities as in the reference.  There is no CPU path.
+
+The aggregate update concatenates the writers' tokens and runs ONE grouped
+UPDATE over them: each expert's segment then holds every writer's rows, and
+the weight-gradient GEMM returns sum_l dW_l accumulated in fp32 and rounded
+to bf16 once, where the reference rounds each writer's dW_l to bf16 and sums
+the upcast terms in the master dtype.  Both are the same sum; the batched
+form is one MFMA-bound call instead of L HBM-bound ones.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Sequence
+
+import torch
+
+from . import _lib as L
+from .lact_moe_triton.lact_fw_grad import grouped_lact_swiglu_ffn_fast_weight_grads
+from .lact_moe_triton.lact_swiglu_ffn import grouped_swiglu_ffn_fwd
+from .lact_moe_triton.triton_permute import (permute_kv_and_lrs, permute_with_expert_mask,
+                                             unpermute_and_merge_with_probs)
+from .routing import route_tokens
+
+
+@dataclass(frozen=True)
+class RouterConfig:
+    """The router attributes _route_tokens reads (M:158-168)."""
+
+    topk: int
+    alpha: float = 1.0
+    use_sigmoid: bool = False
+    router_type: str = "softmax"
+    combine_mode: str = "selected_prob"
+    router_scale: float = 0.0
+    norm_eps: float = 1e-6
+
+    def kwargs(self):
+        return dict(alpha=self.alpha, use_sigmoid=self.use_sigmoid, router_type=self.router_type,
+                    combine_mode=self.combine_mode, router_scale=self.router_scale,
+                    norm_eps=self.norm_eps)
+
+
+def reshape_head_tokens(x: torch.Tensor, num_heads: int) -> torch.Tensor:
+    """b l (h hd) -> b (l h) hd (M:132-137): a view of a contiguous x."""
+    B, Lx, HD = x.shape
+    assert HD % num_heads == 0, "last dimension must split into num_heads heads"
+    return x.contiguous().view(B, Lx * num_heads, HD // num_heads)
+
+
+def merge_head_tokens(x: torch.Tensor, seq_len: int, num_heads: int) -> torch.Tensor:
+    """b (l h) hd -> b l (h hd) (M:139-144)."""
+    B, LH, hd = x.shape
+    assert LH == seq_len * num_heads, "token axis must be seq_len * num_heads"
+    return x.contiguous().view(B, seq_len, num_heads * hd)
+
+
+def route(x_tokens, router_proj_weights, cfg: RouterConfig, routing_bias=None):
+    """_route_tokens (M:147-169): fp32 logits R x^T and the top-k selection on
+    the fused router kernel.  Returns (expert_mask bool [B,E,T], group_sizes
+    int32 [B,E], router_probs fp32 [B,E,T], balance_probs fp32 [B,E,T])."""
+    return route_tokens(x_tokens, router_proj_weights, cfg.topk, routing_bias=routing_bias,
+                        **cfg.kwargs())
+
+
+def route_writers(k_cat, num_writers: int, router_proj_weights, cfg: RouterConfig,
+                  routing_bias=None):
+    """The routing of `num_writers` writers with equal token counts whose
+    tokens are concatenated writer-major in k_cat [1, L*T, D], in ONE router
+    launch: the writers are the router's batches, with one shared router
+    ([E, D]) or one per writer ([L, E, D], memory_router_share_mode
+    "per_layer"); routing_bias [E] or [L, E].  Each writer's routing is
+    _route_tokens of its own tokens (M:147-169).  Returns (expert_mask
+    [1,E,L*T], group_sizes [1,E] summed over the writers, router_probs
+    [1,E,L*T], balance_probs [L,E,T]) on the concatenated token axis."""
+    B1, LT, D = k_cat.shape
+    assert B1 == 1 and LT % num_writers == 0, "k_cat must be [1, L*T, D]"
+    T = LT // num_writers
+    mask, gs, probs, bal = route_tokens(k_cat.contiguous().view(num_writers, T, D),
+                                        router_proj_weights, cfg.topk, routing_bias=routing_bias,
+                                        **cfg.kwargs())
+    E = mask.shape[1]
+    m = mask.transpose(0, 1).reshape(1, E, LT)
+    p = probs.transpose(0, 1).reshape(1, E, LT)
+    return m, gs.sum(0, keepdim=True, dtype=torch.int32), p, bal
+
+
+def lb_info(balance_probs, group_sizes):
+    """_make_lb_info (M:171-176)."""
+    return balance_probs.sum(dim=-1), group_sizes
+
+
+def _w0_w2(w0, w2, precomputed_w0_w2):
+    if precomputed_w0_w2 is not None:
+        return precomputed_w0_w2
+    return torch.cat([w0, w2], dim=2).contiguous()
+
+
+def apply_moe_fast_weights_grouped(x, w0, w1, w2, router_proj_weights, cfg: RouterConfig,
+                                   num_heads: int, routing_bias=None, precomputed_w0_w2=None):
+    """_apply_moe_fast_weights_grouped (M:296-349): x [B, L, H*hd] is split into
+    head tokens, routed, permuted by expert, run through the grouped SwiGLU
+    APPLY (w0, w2 [B,E,I,hd], w1 [B,E,hd,I]) and merged back with the gates.
+    Returns (out [B, L, H*hd] in x's dtype, lb_info = (balance sums [B,E],
+    group_sizes [B,E]))."""
+    seq_len = x.shape[1]
+    input_dtype = x.dtype
+    xt = reshape_head_tokens(x, num_heads)
+    expert_mask, group_sizes, router_probs, balance_probs = route(
+        xt, router_proj_weights, cfg, routing_bias)
+    w0_w2 = _w0_w2(w0, w2, precomputed_w0_w2)
+    x_perm, _, row_id_map = permute_with_expert_mask(
+        xt.to(w0_w2.dtype).contiguous(), expert_mask, router_probs, cfg.topk)
+    y_perm = grouped_swiglu_ffn_fwd(w0_w2, w1.contiguous(), x_perm, group_sizes)
+    out = unpermute_and_merge_with_probs(y_perm, row_id_map, router_probs)
+    return (merge_head_tokens(out.to(input_dtype), seq_len, num_heads),
+            lb_info(balance_probs, group_sizes))
+
+
+def rows_silu_l2norm(x: torch.Tensor, silu: bool, l2: bool, rows_of: int | None = None):
+    """Optional silu, then optional l2 norm x / (|x| + 1e-5) (ref_base.py:182-186)
+    over rows of `rows_of` elements (default: the last dimension) on the HIP
+    kernel; rounding in x's dtype as the reference's tensor arithmetic.
+    Returns a new tensor of x's shape.  Forward only: a tensor that needs a
+    gradient is refused (the reference differentiates through these steps)."""
+    L.require_device(x)
+    assert not (x.requires_grad and torch.is_grad_enabled()), (
+        "rows_silu_l2norm has no backward; call it on detached inputs or under no_grad")
+    x = x.contiguous()
+    D = x.shape[-1] if rows_of is None else rows_of
+    assert x.numel() % D == 0, "rows must tile the tensor"
+    out = torch.empty_like(x)
+    L.call("uttt_rows_silu_l2norm", L.ptr(x), L.dtype_code(x.dtype), x.numel() // D, D, D,
+           int(silu), int(l2), L.ptr(out), D, L.stream_of(x))
+    return out
+
+
+def preprocess_update_inputs(k, v, lr, num_heads: int, *, qkv_silu: bool = False,
+                             v_norm: bool = False, qk_norm: bool = False):
+    """_preprocess_update_inputs (M:630-665) with the l2 norms
+    (memory_norm_type / memory_qk_norm_type "l2"): optional silu of k and v,
+    optional l2 norm of v over its last dimension, optional per-head l2 norm
+    of k (each on the row kernel), then head tokens, and lr [B, L, 3] (shared
+    by the heads) or [B, L, 3H] spread to [B, L*H, 3].  The learned qk
+    rescale and the rotary embedding belong to the model, not to this path:
+    apply them to k first."""
+    B, Lx, HD = k.shape
+    if qkv_silu or qk_norm:
+        k = rows_silu_l2norm(k, qkv_silu, qk_norm, rows_of=HD // num_heads)
+    if qkv_silu or v_norm:
+        v = rows_silu_l2norm(v, qkv_silu, v_norm)
+    k_tokens = reshape_head_tokens(k, num_heads)
+    v_tokens = reshape_head_tokens(v, num_heads)
+    if lr.shape[2] == 3:
+        lr_mh = lr.unsqueeze(2).expand(-1, -1, num_heads, -1)
+    else:
+        lr_mh = lr.view(B, Lx, num_heads, 3)
+    lr_tokens = lr_mh.reshape(B, Lx * num_heads, 3).contiguous()
+    return k_tokens, v_tokens, lr_tokens
+
+
+def moe_update_grads_packed(k_tokens, v_tokens, lr_tokens, w0_w2, w1, expert_mask, group_sizes,
+                            router_probs, topk: int):
+    """The grouped part of _compute_moe_update_grads_grouped (M:484-512): lr
+    split and cast to the fast-weight dtype, k / v*p / lr permuted by expert,
+    then the grouped UPDATE.  Returns (dW0_W2 [B,E,2I,D], dW1 [B,E,D,I]) in
+    bf16, differentiable with respect to k, v, lr and the router probs."""
+    target_dtype = w0_w2.dtype
+    lrs = [lr_tokens[:, :, j].contiguous().to(target_dtype) for j in range(3)]
+    k_perm, v_perm, lr0_p, lr1_p, lr2_p = permute_kv_and_lrs(
+        k_tokens.contiguous().to(target_dtype), v_tokens.contiguous(), *lrs, expert_mask,
+        router_probs, topk)
+    return grouped_lact_swiglu_ffn_fast_weight_grads(w0_w2, w1.contiguous(), k_perm, v_perm,
+                                                     lr0_p, lr1_p, lr2_p, group_sizes)
+
+
+def compute_moe_update_grads_grouped(k_tokens, v_tokens, lr_tokens, w0, w1, w2, expert_mask,
+                                     group_sizes, router_probs, topk: int,
+                                     master_dtype=torch.float32, precomputed_w0_w2=None):
+    """_compute_moe_update_grads_grouped (M:453-518): returns (dW0, dW1, dW2)
+    upcast to the master dtype (M:514-518)."""
+    dw0_w2, dw1 = moe_update_grads_packed(k_tokens, v_tokens, lr_tokens,
+                                          _w0_w2(w0, w2, precomputed_w0_w2), w1, expert_mask,
+                                          group_sizes, router_probs, topk)
+    inter_dim = w0.shape[2]
+    return (dw0_w2[:, :, :inter_dim, :].to(master_dtype), dw1.to(master_dtype),
+            dw0_w2[:, :, inter_dim:, :].to(master_dtype))
+
+
+@dataclass
+class WriterInputs:
+    """One writer layer's preprocessed update inputs and its routing."""
+
+    k_tokens: torch.Tensor      # [B, T, D]
+    v_tokens: torch.Tensor      # [B, T, D]
+    lr_tokens: torch.Tensor     # [B, T, 3]
+    expert_mask: torch.Tensor   # [B, E, T]
+    router_probs: torch.Tensor  # [B, E, T]
+
+
+def concat_writers(writers: Sequence[WriterInputs]):
+    """The writers' tokens one after another: (k, v, lr, mask, probs, group
+    sizes) of the concatenated token axis.  Row order inside each expert's
+    segment is then writer-major, token-ascending."""
+    assert len(writers) > 0, "at least one writer"
+    if len(writers) == 1:
+        w = writers[0]
+        m, p = w.expert_mask, w.router_probs
+    else:
+        m = torch.cat([w.expert_mask for w in writers], dim=2)
+        p = torch.cat([w.router_probs for w in writers], dim=2)
+    cat = (lambda ts: ts[0]) if len(writers) == 1 else (lambda ts: torch.cat(ts, dim=1))
+    k = cat([w.k_tokens for w in writers])
+    v = cat([w.v_tokens for w in writers])
+    lr = cat([w.lr_tokens for w in writers])
+    gs = m.sum(dim=-1, dtype=torch.int32)
+    return k, v, lr, m, p, gs
+
+
+def aggregate_moe_update_grads(writers: Sequence[WriterInputs], w0, w1, w2, topk: int,
+                               master_dtype=torch.float32, precomputed_w0_w2=None,
+                               packed: bool = False):
+    """The writers' raw gradients of one chunk summed (M:2428-2445), as one
+    grouped UPDATE over their concatenated tokens.  Returns (dW0, dW1, dW2)
+    in master_dtype, or (dW0_W2, dW1) in bf16 when `packed`."""
+    k, v, lr, m, p, gs = concat_writers(writers)
+    w0_w2 = _w0_w2(w0, w2, precomputed_w0_w2)
+    dw0_w2, dw1 = moe_update_grads_packed(k, v, lr, w0_w2, w1, m, gs, p, topk)
+    if packed:
+        return dw0_w2, dw1
+    inter_dim = w0_w2.shape[2] // 2
+    return (dw0_w2[:, :, :inter_dim, :].to(master_dtype), dw1.to(master_dtype),
+            dw0_w2[:, :, inter_dim:, :].to(master_dtype))
