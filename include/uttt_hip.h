@@ -398,6 +398,21 @@ int uttt_moe_decode_read(const void* x, int B, int T, int D, const void* w0_w2, 
                          int64_t p_se, int64_t p_st, int topk, void* out, void* workspace,
                          size_t workspace_bytes, void* stream);
 
+/* No counterpart in the reference: uttt_moe_decode_read for callers that
+ * cannot allocate (code under HIP graph capture, serving loops, harnesses
+ * that forbid hipMalloc).  Same arguments and results without the workspace:
+ * the hidden buffer lives in a file-scope device array of 8 MiB that each GPU
+ * the library runs on holds until the process ends, so B*E*T*I*2 must be at
+ * most 8 MiB (larger problems are refused with UTTT_ERR_ARG).  Calls no
+ * hipMalloc or hipFree.  The stream must belong to the current device.  Calls
+ * that overlap on one GPU (other streams or threads) share the array and
+ * race; calls ordered on one stream do not. */
+int uttt_moe_decode_read_noalloc(const void* x, int B, int T, int D, const void* w0_w2,
+                                 const void* w1, int E, int I, const void* expert_mask,
+                                 int mask_bytes, int64_t m_sb, int64_t m_se, int64_t m_st,
+                                 const float* probs, int64_t p_sb, int64_t p_se, int64_t p_st,
+                                 int topk, void* out, void* stream);
+
 /* uTTT-Dense read, fused for small heads: out = W1 (silu(W0 x) * (W2 x))
  * per head (_apply_fast_weights, uttt_dense/modeling_recurrent_lact.py:241-261,
  * with the rearranges of :251 and :261 folded in).  x [b, l, H*D] bf16,

@@ -141,6 +141,11 @@ SIGNATURES = {
         [c_p, c_int, c_int, c_int, c_p, c_p, c_int, c_int, c_p, c_int, c_i64, c_i64, c_i64,
          c_p, c_i64, c_i64, c_i64, c_int, c_p, c_p, c_sz, c_p],
     ),
+    "uttt_moe_decode_read_noalloc": (
+        c_int,
+        [c_p, c_int, c_int, c_int, c_p, c_p, c_int, c_int, c_p, c_int, c_i64, c_i64, c_i64,
+         c_p, c_i64, c_i64, c_i64, c_int, c_p, c_p],
+    ),
 }
 
 _lib = None

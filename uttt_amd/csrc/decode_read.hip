@@ -19,6 +19,8 @@
 // wave ballots (E <= 64, T <= 64).  Each wave streams whole 16-byte chunks of
 // its weight rows with every load of a row issued before the first FMA;
 // reductions are fixed butterflies, so results are deterministic.
+#include <mutex>
+
 #include "common.h"
 
 namespace uttt {
@@ -429,39 +431,139 @@ extern "C" size_t uttt_moe_decode_read_workspace_bytes(int B, int T, int E, int 
   return (size_t)B * E * T * I * sizeof(uint16_t);
 }
 
+namespace {
+
+// The read after argument checks, with the hidden buffer `hid` of at least
+// uttt_moe_decode_read_workspace_bytes(B, T, E, I) bytes.
+int decode_read_checked(const void* x, int B, int T, int D, const void* w0_w2, const void* w1,
+                        int E, int I, const void* expert_mask, int mask_bytes, int64_t m_sb,
+                        int64_t m_se, int64_t m_st, const float* probs, int64_t p_sb,
+                        int64_t p_se, int64_t p_st, int topk, void* out, void* hid,
+                        hipStream_t st) {
+  const int S = min(E, topk * T);
+  auto* xs = reinterpret_cast<const uint16_t*>(x);
+  auto* w02 = reinterpret_cast<const uint16_t*>(w0_w2);
+  auto* w1s = reinterpret_cast<const uint16_t*>(w1);
+  auto* o = reinterpret_cast<uint16_t*>(out);
+  auto* h = reinterpret_cast<uint16_t*>(hid);
+  if (mask_bytes == 1)
+    return launch_decode<1>(xs, B, T, D, w02, w1s, E, I, expert_mask, m_sb, m_se, m_st, probs,
+                            p_sb, p_se, p_st, S, o, h, st);
+  return launch_decode<4>(xs, B, T, D, w02, w1s, E, I, expert_mask, m_sb, m_se, m_st, probs, p_sb,
+                          p_se, p_st, S, o, h, st);
+}
+
+// Shape and pointer checks shared by both entry points; sets *done when
+// there is nothing to launch beyond what it did (an empty problem, or the
+// zero output of I = 0).
+int decode_read_args(const void* x, int B, int T, int D, const void* w0_w2, const void* w1,
+                     int E, int I, const void* expert_mask, int mask_bytes, const float* probs,
+                     int topk, void* out, hipStream_t st, const char* what, bool* done) {
+  *done = true;
+  UTTT_REQUIRE(B >= 0 && T >= 0 && D >= 0 && I >= 0 && E >= 1,
+               "%s: bad sizes B=%d T=%d D=%d I=%d E=%d", what, B, T, D, I, E);
+  UTTT_REQUIRE(E <= 64, "%s: E=%d exceeds 64", what, E);
+  UTTT_REQUIRE(T <= 64, "%s: T=%d tokens per batch exceed 64 (use the grouped apply)", what, T);
+  UTTT_REQUIRE(D % 8 == 0 && I % 8 == 0, "%s: D=%d and I=%d must be multiples of 8", what, D, I);
+  UTTT_REQUIRE(D <= 8 * kWave * kMaxChunks && I <= 8 * kWave * kMaxChunks,
+               "%s: D=%d and I=%d must be at most %d", what, D, I, 8 * kWave * kMaxChunks);
+  UTTT_REQUIRE(mask_bytes == 1 || mask_bytes == 4, "%s: mask element size %d", what, mask_bytes);
+  UTTT_REQUIRE(topk >= 1, "%s: topk=%d", what, topk);
+  if (B == 0 || T == 0 || D == 0) return UTTT_OK;
+  UTTT_REQUIRE(x && w0_w2 && w1 && expert_mask && probs && out, "%s: null pointer", what);
+  if (I == 0) return zero_fill_async(out, sizeof(uint16_t) * (size_t)B * T * D, st, what);
+  *done = false;
+  return UTTT_OK;
+}
+
+}  // namespace
+
 extern "C" int uttt_moe_decode_read(const void* x, int B, int T, int D, const void* w0_w2,
                                     const void* w1, int E, int I, const void* expert_mask,
                                     int mask_bytes, int64_t m_sb, int64_t m_se, int64_t m_st,
                                     const float* probs, int64_t p_sb, int64_t p_se, int64_t p_st,
                                     int topk, void* out, void* workspace, size_t workspace_bytes,
                                     void* stream) {
-  UTTT_REQUIRE(B >= 0 && T >= 0 && D >= 0 && I >= 0 && E >= 1,
-               "moe_decode_read: bad sizes B=%d T=%d D=%d I=%d E=%d", B, T, D, I, E);
-  UTTT_REQUIRE(E <= 64, "moe_decode_read: E=%d exceeds 64", E);
-  UTTT_REQUIRE(T <= 64, "moe_decode_read: T=%d tokens per batch exceed 64 (use the grouped apply)", T);
-  UTTT_REQUIRE(D % 8 == 0 && I % 8 == 0, "moe_decode_read: D=%d and I=%d must be multiples of 8", D, I);
-  UTTT_REQUIRE(D <= 8 * kWave * kMaxChunks && I <= 8 * kWave * kMaxChunks,
-               "moe_decode_read: D=%d and I=%d must be at most %d", D, I, 8 * kWave * kMaxChunks);
-  UTTT_REQUIRE(mask_bytes == 1 || mask_bytes == 4, "moe_decode_read: mask element size %d", mask_bytes);
-  UTTT_REQUIRE(topk >= 1, "moe_decode_read: topk=%d", topk);
-  if (B == 0 || T == 0 || D == 0) return UTTT_OK;
   hipStream_t st = as_stream(stream);
-  UTTT_REQUIRE(x && w0_w2 && w1 && expert_mask && probs && out, "moe_decode_read: null pointer");
-  if (I == 0) {
-    return zero_fill_async(out, sizeof(uint16_t) * (size_t)B * T * D, st, "moe_decode_read");
-  }
+  bool done = false;
+  if (int rc = decode_read_args(x, B, T, D, w0_w2, w1, E, I, expert_mask, mask_bytes, probs,
+                                topk, out, st, "moe_decode_read", &done))
+    return rc;
+  if (done) return UTTT_OK;
   const size_t need = uttt_moe_decode_read_workspace_bytes(B, T, E, I);
   UTTT_REQUIRE(workspace != nullptr && workspace_bytes >= need,
                "moe_decode_read: workspace %zu < %zu bytes", workspace_bytes, need);
-  const int S = min(E, topk * T);
-  auto* xs = reinterpret_cast<const uint16_t*>(x);
-  auto* w02 = reinterpret_cast<const uint16_t*>(w0_w2);
-  auto* w1s = reinterpret_cast<const uint16_t*>(w1);
-  auto* o = reinterpret_cast<uint16_t*>(out);
-  auto* hid = reinterpret_cast<uint16_t*>(workspace);
-  if (mask_bytes == 1)
-    return launch_decode<1>(xs, B, T, D, w02, w1s, E, I, expert_mask, m_sb, m_se, m_st, probs,
-                            p_sb, p_se, p_st, S, o, hid, st);
-  return launch_decode<4>(xs, B, T, D, w02, w1s, E, I, expert_mask, m_sb, m_se, m_st, probs, p_sb,
-                          p_se, p_st, S, o, hid, st);
+  return decode_read_checked(x, B, T, D, w0_w2, w1, E, I, expert_mask, mask_bytes, m_sb, m_se,
+                             m_st, probs, p_sb, p_se, p_st, topk, out, workspace, st);
+}
+
+// ------------------------------------------------- no-allocation variant ----
+// The same read with its hidden buffer in a file-scope device array instead
+// of a caller workspace, for callers that cannot allocate (code under HIP
+// graph capture, serving loops).  Each GPU the library runs on holds its own
+// copy of the array until the process ends.  The kernels address it through
+// the pointer hipGetSymbolAddress returns for the current device, taken once
+// per device on the first call there (the array's name is a host-side
+// stand-in, not a device address).  Calls that overlap on one GPU (other
+// streams, other threads) share the array and race; calls in stream order do
+// not.  The second kernel reads only hidden entries the first kernel wrote in
+// the same call, so the array needs no clearing between calls.
+constexpr size_t kNoAllocScratchBytes = (size_t)8 << 20;   // 8 MiB per GPU
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (looked up once per device).
+int scratch_on_current_device(void** ptr, const char* what) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("%s: no usable current device (%d)", what, dev);
+    return UTTT_ERR_HIP;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || p == nullptr) {
+      set_error("%s: hipGetSymbolAddress of the scratch array failed on device %d: %s", what,
+                dev, hipGetErrorString(err));
+      return UTTT_ERR_HIP;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return UTTT_OK;
+}
+}  // namespace
+
+extern "C" int uttt_moe_decode_read_noalloc(const void* x, int B, int T, int D,
+                                            const void* w0_w2, const void* w1, int E, int I,
+                                            const void* expert_mask, int mask_bytes,
+                                            int64_t m_sb, int64_t m_se, int64_t m_st,
+                                            const float* probs, int64_t p_sb, int64_t p_se,
+                                            int64_t p_st, int topk, void* out, void* stream) {
+  const char* what = "moe_decode_read_noalloc";
+  hipStream_t st = as_stream(stream);
+  bool done = false;
+  if (int rc = decode_read_args(x, B, T, D, w0_w2, w1, E, I, expert_mask, mask_bytes, probs,
+                                topk, out, st, what, &done))
+    return rc;
+  if (done) return UTTT_OK;
+  const size_t need = uttt_moe_decode_read_workspace_bytes(B, T, E, I);
+  UTTT_REQUIRE(need <= kNoAllocScratchBytes,
+               "%s: B*E*T*I*2 = %zu bytes of hidden state exceed the %zu-byte scratch array "
+               "(use uttt_moe_decode_read with a workspace)",
+               what, need, kNoAllocScratchBytes);
+  int dev_st = -1, dev_cur = -1;
+  if (st != nullptr && hipStreamGetDevice(st, &dev_st) == hipSuccess &&
+      hipGetDevice(&dev_cur) == hipSuccess)
+    UTTT_REQUIRE(dev_st == dev_cur, "%s: the stream belongs to device %d, the current device is %d",
+                 what, dev_st, dev_cur);
+  void* hid = nullptr;
+  if (int rc = scratch_on_current_device(&hid, what)) return rc;
+  return decode_read_checked(x, B, T, D, w0_w2, w1, E, I, expert_mask, mask_bytes, m_sb, m_se,
+                             m_st, probs, p_sb, p_se, p_st, topk, out, hid, st);
 }
