@@ -30,12 +30,17 @@ in HBM before the timed region starts):
             T=65536, E=16, top-2, payload bf16 [T, 768]; one step = row map +
             permute + unpermute of one batch; value = algorithmic GB/s.
 
-Timing: W untimed steps, then K steps bracketed by torch.cuda.synchronize();
-per-kernel durations come from HIP events recorded on the stream the kernels
-are launched on (torch's current stream, which the C-ABI calls receive).
-`roofline` reports the dominant kernel against MI355X's published peak;
-`cpu_baseline` times the CPU restatement under oracle/ on this host's cores
-(rank 0, N=1) on a bounded sample of the same workload.
+Timing: W untimed steps, then K steps bracketed by torch.cuda.synchronize().
+The MoE sweeps run through the product API (uttt_amd.moe, the compat ops
+under it, autograd for the UPDATE backward, uttt_amd.fast_weight_write).
+`kernels_by_symbol` groups one more sweep's GPU time by kernel symbol (from
+torch.profiler's device activity); `roofline` reports the symbol with the
+most time per sweep against MI355X's published peak, with its launch time
+measured by HIP events around back-to-back launches on the launch stream;
+`cpu_baseline` times the CPU restatement under oracle/ on all of this host's
+cores (rank 0, N=1; 1 warm-up, median of 3) on a bounded sample of the same
+workload.  The default line also carries `other_targets`: configs[2]'s
+permute / unpermute GB/s and configs[3]'s sweep.
 
 Only one GPU is used: --gpus N with N > 1 exits with a message.
 """
@@ -301,334 +306,344 @@ MOE_CONFIGS = {
 SEQ, CHUNK, TOPK = 32768, 2048, 2
 
 
+def norm_symbol(name):
+    """A kernel's symbol without namespaces, argument list or return type:
+    'tn_kernel<0, EpiSwiGLU, true>'."""
+    import re
+
+    s = name.replace("(anonymous namespace)::", "").replace("anon::", "").replace("uttt::", "")
+    s = re.sub(r"^void\s+", "", s)
+    depth, cut = 0, len(s)
+    for i, ch in enumerate(s):          # drop a trailing "(...)" parameter list
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0:
+            cut = i
+            break
+    return s[:cut].strip()
+
+
 class MoeSweep:
-    """Buffers and C-ABI launches of one shifted block-causal sweep over the
-    sequence: for every chunk and layer the APPLY (row map, permute, grouped
-    SwiGLU apply, gate-weighted unpermute), and for every chunk but the last
-    the UPDATE (row map, permute of k, v*p and the learning rates, grouped
-    update) plus, for the training slice, the UPDATE backward seeded with
-    fixed upstream weight gradients.  Each kernel launch is bracketed by HIP
-    events on the launch stream when `timed`."""
+    """One shifted block-causal sweep over the sequence through the product
+    API (uttt_amd.moe and uttt_amd.fast_weight_write), as a caller of the
+    reference's model would drive it:
+      - every (chunk, layer): the routed APPLY,
+        moe.apply_moe_fast_weights_grouped (router -> row map -> permute ->
+        grouped SwiGLU apply -> gate-weighted unpermute);
+      - every chunk but the last: the UPDATE of the chunk's writers -- batched
+        (the aggregate write: all L writers' tokens routed in one router launch,
+        moe.route_writers, and summed by one grouped UPDATE,
+        moe.aggregate_moe_update_grads) or per layer (one UPDATE per writer);
+        for the training slice, its backward through autograd seeded with fixed
+        upstream weight gradients (UPDATE backward and the permute's backward);
+        then the norm-preserving WRITE of the pool
+        (fast_weight_write.apply_moe_update_packed)."""
 
     NSETS = 4   # distinct per-layer input sets, cycled over (chunk, layer)
 
     def __init__(self, cfg, dev):
         import torch
 
-        from uttt_amd import _lib as L
+        from uttt_amd import moe
 
-        self.L, self.cfg, self.dev = L, cfg, dev
+        self.cfg, self.dev = cfg, dev
         E, D, I = cfg["E"], cfg["D"], cfg["I"]
         T, k = CHUNK, TOPK
-        N = k * T
-        self.E, self.D, self.I, self.T, self.k, self.N = E, D, I, T, k, N
+        self.E, self.D, self.I, self.T, self.k, self.N = E, D, I, T, k, k * T
         g = torch.Generator(device=dev).manual_seed(0)
         bf = torch.bfloat16
 
         def randn(*shape, scale=1.0):
             return (torch.randn(*shape, generator=g, device=dev) * scale).to(bf)
 
-        # the shared expert pool (W0_W2 = cat(w0, w2) rows, W1 = down proj)
+        # the shared expert pool (W0_W2 = w0 rows then w2 rows, W1 = down proj)
         self.W02 = randn(1, E, 2 * I, D, scale=D ** -0.5)
         self.W1 = randn(1, E, D, I, scale=D ** -0.5)
+        # fp32 masters of the pool for the WRITE step
+        self.M02, self.M1 = self.W02.float(), self.W1.float()
         self.sets = []
-        for s in range(self.NSETS):
+        for _ in range(self.NSETS):
             st = {}
             for name in ("x", "k", "v"):
                 t = torch.randn(1, T, D, generator=g, device=dev)
                 st[name] = (t / (t.norm(dim=-1, keepdim=True) + 1e-5)).to(bf)
-            st["lr"] = [(torch.sigmoid(torch.randn(1, T, generator=g, device=dev)) * 0.1).to(bf)
-                        for _ in range(3)]
-            for role in ("a", "u"):   # routing of the apply (x) and of the update (k)
-                logits = torch.randn(1, E, T, generator=g, device=dev)
-                if cfg["zipf"] is not None:
-                    prior = -cfg["zipf"] * torch.log(torch.arange(E, device=dev, dtype=torch.float32) + 1)
-                    logits = logits + prior.view(1, E, 1)
-                    bias = torch.zeros(1, E, 1, device=dev)
-                else:
-                    bias = (torch.randn(E, generator=g, device=dev) * 0.5).view(1, E, 1)
-                idx = torch.topk(logits + bias, k, dim=1).indices
-                mask = torch.zeros(1, E, T, dtype=torch.bool, device=dev).scatter_(1, idx, True)
-                sm = torch.softmax(logits, dim=1) * mask
-                st["mask_" + role] = mask
-                st["gates_" + role] = (sm / sm.sum(1, keepdim=True)).contiguous()
-                st["gs_" + role] = mask.sum(-1).to(torch.int32).contiguous()
+            st["lr"] = torch.sigmoid(torch.randn(1, T, 3, generator=g, device=dev)) * 0.1
             self.sets.append(st)
-        # fp32 masters of the pool for the WRITE step (w0 and w2 rows stay
-        # concatenated: the norm-preserving write is per row)
-        self.M02, self.M1 = self.W02.float(), self.W1.float()
-        # one router shared by all layers (the reference's "share_all" mode):
-        # logits = R x with x L2-normalised and R ~ N(0, 1), so logits ~ N(0, 1);
-        # the expert prior (Zipf for configs[4], N(0, 0.5) otherwise) is the
-        # selection-only routing bias; gates are top-k renormalised
+        # one router shared by all layers ("share_all"): logits = R x with x
+        # L2-normalised and R ~ N(0, 1), so logits ~ N(0, 1); the expert prior
+        # (Zipf for configs[4], N(0, 0.5) otherwise) is the selection-only
+        # routing bias; gates are top-k renormalised
         self.R = torch.randn(E, D, generator=g, device=dev)
         if cfg["zipf"] is not None:
             self.rbias = -cfg["zipf"] * torch.log(torch.arange(E, device=dev, dtype=torch.float32) + 1)
         else:
             self.rbias = torch.randn(E, generator=g, device=dev) * 0.5
-        self.route_a = self._route_buffers(T)
-        self.route_u = self._route_buffers(T)
+        self.rcfg = moe.RouterConfig(topk=k, combine_mode="topk_renorm")
         if cfg["train"]:
             self.GW02 = randn(1, E, 2 * I, D, scale=0.02)
             self.GW1 = randn(1, E, D, I, scale=0.02)
-        e = lambda *shape, dt=bf: torch.empty(*shape, dtype=dt, device=dev)
-        self.rmap = e(1, T, 2 * E + 1, dt=torch.int32)
-        self.ws_map = e(L.lib().uttt_row_id_map_workspace_bytes(1, T, E), dt=torch.uint8)
-        self.xp, self.pp = e(1, N, D), e(1, N, dt=torch.float32)
-        self.hid, self.yp, self.y = e(1, N, I), e(1, N, D), e(1, T, D)
-        self.kp, self.vp = e(1, N, D), e(1, N, D)
-        self.lrp = [e(1, N) for _ in range(3)]
-        self.dy, self.hl = e(1, N, 2 * I), e(1, N, I)
-        self.dW02, self.dW1 = e(1, E, 2 * I, D), e(1, E, D, I)
-        s1b = L.lib().uttt_update_stage1_workspace_bytes(1, I, N)
-        self.ws_s1, self.ws_s1_bytes = e(s1b, dt=torch.uint8), s1b
-        self._wgrad_workspace(N)
-        if cfg["train"]:
-            self.gW02, self.gW1 = e(1, E, 2 * I, D), e(1, E, D, I)
-            self.gK, self.gV = e(1, N, D), e(1, N, D)
-            self.glr = [e(1, N) for _ in range(3)]
-            wsb = L.lib().uttt_update_bwd_workspace_bytes(1, I, N)
-            self.ws_bwd, self.ws_bwd_bytes = e(wsb, dt=torch.uint8), wsb
-        self.stream = torch.cuda.current_stream(dev).cuda_stream
-        self.events = None
-        self.batched = None
-
-    def _wgrad_workspace(self, N):
-        """Split-K partials of the weight-gradient pair for N routed rows (none
-        at the MoE shapes: their tiles already fill the chip)."""
-        import torch
-
-        L, E, I, D = self.L, self.E, self.I, self.D
-        nb = L.lib().uttt_grouped_wgrad_pair_workspace_bytes(1, E, I, D, N)
-        if nb > getattr(self, "ws_wg_bytes", 0) or not hasattr(self, "ws_wg"):
-            self.ws_wg = torch.empty(nb, dtype=torch.uint8, device=self.dev) if nb else None
-            self.ws_wg_bytes = nb
-
-    def _route_buffers(self, T):
-        import torch
-
-        E, dev = self.E, self.dev
-        nb = self.L.lib().uttt_router_workspace_bytes(1, T, E, self.D)
-        return dict(T=T, mask=torch.empty(1, E, T, dtype=torch.bool, device=dev),
-                    gs=torch.empty(1, E, dtype=torch.int32, device=dev),
-                    gates=torch.empty(1, E, T, dtype=torch.float32, device=dev),
-                    bal=torch.empty(1, E, T, dtype=torch.float32, device=dev),
-                    lb=torch.empty((), dtype=torch.float32, device=dev),
-                    ws=torch.empty(nb, dtype=torch.uint8, device=dev), ws_bytes=nb)
-
-    def route(self, x, rb):
-        """Fused router on x [1, T, D]: logits R x^T, top-k with the prior as
-        selection bias, topk_renorm gates, group sizes (route_tokens)."""
-        L = self.L
-        self._mark("router")
-        L.call("uttt_route_tokens", L.ptr(x), L.BF16, L.ptr(self.R), 0, 1, rb["T"], self.D, self.E,
-               L.ptr(self.rbias), 0, self.k, 0, 1, 1.0, 0.0, 1e-6, None, L.ptr(rb["mask"]),
-               L.ptr(rb["gs"]), L.ptr(rb["gates"]), L.ptr(rb["bal"]), L.ptr(rb["lb"]),
-               L.ptr(rb["ws"]), rb["ws_bytes"], self.stream)
-
-    def prepare_batched(self, layers):
-        """Inputs and buffers of the cross-layer batched UPDATE: the k, v, lr and
-        routing of all `layers` writers of a chunk concatenated along the token
-        axis (writer l uses input set l % NSETS), so one grouped UPDATE call
-        produces sum_l dW_l -- the reference's aggregate write sums the
-        writers' raw gradients (modeling_recurrent_lact.py:2428-2445) -- and
-        its backward the per-writer k, v, lr gradients."""
-        import torch
-
-        L, E, D, I, k = self.L, self.E, self.D, self.I, self.k
-        sets = [self.sets[l % self.NSETS] for l in range(layers)]
-        T = self.T * layers
-        N = k * T
-        bt = dict(T=T, N=N, layers=layers)
-        bt["k"] = torch.cat([st["k"] for st in sets], dim=1).contiguous()
-        bt["v"] = torch.cat([st["v"] for st in sets], dim=1).contiguous()
-        bt["lr"] = [torch.cat([st["lr"][j] for st in sets], dim=1).contiguous() for j in range(3)]
-        bt["mask"] = torch.cat([st["mask_u"] for st in sets], dim=2).contiguous()
-        bt["gates"] = torch.cat([st["gates_u"] for st in sets], dim=2).contiguous()
-        bt["gs"] = bt["mask"].sum(-1).to(torch.int32).contiguous()
-        bt["route"] = self._route_buffers(T)
-        e = lambda *shape, dt=torch.bfloat16: torch.empty(*shape, dtype=dt, device=self.dev)
-        bt["rmap"] = e(1, T, 2 * E + 1, dt=torch.int32)
-        bt["ws_map"] = e(L.lib().uttt_row_id_map_workspace_bytes(1, T, E), dt=torch.uint8)
-        bt["kp"], bt["vp"] = e(1, N, D), e(1, N, D)
-        bt["lrp"] = [e(1, N) for _ in range(3)]
-        bt["dy"], bt["hl"] = e(1, N, 2 * I), e(1, N, I)
-        s1b = L.lib().uttt_update_stage1_workspace_bytes(1, I, N)
-        bt["ws_s1"], bt["ws_s1_bytes"] = e(s1b, dt=torch.uint8), s1b
-        self._wgrad_workspace(N)
-        if self.cfg["train"]:
-            bt["gK"], bt["gV"] = e(1, N, D), e(1, N, D)
-            bt["glr"] = [e(1, N) for _ in range(3)]
-            wsb = L.lib().uttt_update_bwd_workspace_bytes(1, I, N)
-            bt["ws_bwd"], bt["ws_bwd_bytes"] = e(wsb, dt=torch.uint8), wsb
-        self.batched = bt
-
-    # algorithmic FLOPs per launch, NID = N * I * D
-    def flops(self):
-        nid = self.N * self.I * self.D
-        return {"gate_up": 4 * nid, "down_proj": 2 * nid, "update_s1(2 launches)": 6 * nid,
-                "wgrad": 6 * nid, "update_bwd_s1": 12 * nid, "grad_k": 8 * nid, "grad_v": 4 * nid,
-                "wgrad_bwd": 6 * nid}
+        self.marks = None   # [(name, event)] when the stages are bracketed
 
     def _mark(self, name):
-        if self.events is not None:
+        if self.marks is not None:
             import torch
 
             ev = torch.cuda.Event(enable_timing=True)
             ev.record()
-            self.events.append((name, ev))
+            self.marks.append((name, ev))
 
     def apply(self, st):
-        L, E, D, I, T, N, s = self.L, self.E, self.D, self.I, self.T, self.N, self.stream
-        rb = self.route_a
-        self.route(st["x"], rb)
-        m, p, gs = rb["mask"], rb["gates"], rb["gs"]
-        self._mark("row_map")
-        L.call("uttt_make_row_id_map", L.ptr(m), 1, m.stride(0), m.stride(1), m.stride(2), 1, T,
-               E, L.ptr(self.rmap), None, L.ptr(self.ws_map), self.ws_map.numel(), s)
-        self._mark("permute")
-        L.call("uttt_permute_fwd", L.ptr(st["x"]), L.BF16, 1, T, D, L.ptr(self.rmap), E,
-               L.ptr(p), p.stride(0), p.stride(1), p.stride(2), L.ptr(self.xp), N,
-               L.ptr(self.pp), s)
-        self._mark("gate_up")
-        L.call("uttt_grouped_gate_up", L.ptr(self.W02), L.ptr(self.xp), L.ptr(gs), 1, E,
-               I, D, N, L.ptr(self.hid), 1, s)
-        self._mark("down_proj")
-        L.call("uttt_grouped_gemm_nt", L.ptr(self.W1), L.ptr(self.hid), L.ptr(gs), 1, E,
-               D, I, N, L.ptr(self.yp), s)
-        self._mark("unpermute")
-        L.call("uttt_unpermute_fwd", L.ptr(self.yp), L.BF16, 1, N, D, L.ptr(self.rmap), T, E,
-               L.ptr(p), p.stride(0), p.stride(1), p.stride(2), L.ptr(self.y), s)
-        self._mark(None)
-
-    def write(self):
-        """The WRITE step on the pool: masters += lr_scale * dW, rows projected
-        back onto their pre-step norms, bf16 fast weights refreshed in place
-        (_apply_moe_update_dense, modeling_recurrent_lact.py:754-825)."""
-        L, E, D, I, s = self.L, self.E, self.D, self.I, self.stream
-        self._mark("write_step(2 launches)")
-        L.call("uttt_write_step", L.ptr(self.M02), None, L.ptr(self.dW02), L.BF16, None, None, 1.0,
-               1, E * 2 * I, D, D, 0, 1, L.ptr(self.M02), L.ptr(self.W02), None, s)
-        L.call("uttt_write_step", L.ptr(self.M1), None, L.ptr(self.dW1), L.BF16, None, None, 1.0,
-               1, E * D, I, I, 0, 1, L.ptr(self.M1), L.ptr(self.W1), None, s)
-        self._mark(None)
-
-    def update(self, st):
-        """One writer's UPDATE (the reference's per-layer call pattern)."""
-        buf = dict(T=self.T, N=self.N, k=st["k"], v=st["v"], lr=st["lr"], route=self.route_u,
-                   rmap=self.rmap, ws_map=self.ws_map,
-                   kp=self.kp, vp=self.vp, lrp=self.lrp, dy=self.dy, hl=self.hl,
-                   ws_s1=self.ws_s1, ws_s1_bytes=self.ws_s1_bytes)
-        if self.cfg["train"]:
-            buf.update(gK=self.gK, gV=self.gV, glr=self.glr, ws_bwd=self.ws_bwd,
-                       ws_bwd_bytes=self.ws_bwd_bytes)
-        self._update(buf)
-
-    def update_batched(self):
-        self._update(self.batched)
-
-    def _update(self, bt):
-        L, E, D, I, s = self.L, self.E, self.D, self.I, self.stream
-        T, N = bt["T"], bt["N"]
-        rb = bt["route"]
-        self.route(bt["k"], rb)
-        m, p, gs, lr = rb["mask"], rb["gates"], rb["gs"], bt["lr"]
-        self._mark("row_map(update)")
-        L.call("uttt_make_row_id_map", L.ptr(m), 1, m.stride(0), m.stride(1), m.stride(2), 1, T,
-               E, L.ptr(bt["rmap"]), None, L.ptr(bt["ws_map"]), bt["ws_map"].numel(), s)
-        self._mark("permute_kv_lrs")
-        L.call("uttt_permute_kv_lrs_fwd", L.ptr(bt["k"]), L.BF16, L.ptr(bt["v"]), L.BF16,
-               L.ptr(lr[0]), L.ptr(lr[1]), L.ptr(lr[2]), 2, 1, T, D, L.ptr(bt["rmap"]), E,
-               L.ptr(p), p.stride(0), p.stride(1), p.stride(2), L.ptr(bt["kp"]), L.ptr(bt["vp"]),
-               L.ptr(bt["lrp"][0]), L.ptr(bt["lrp"][1]), L.ptr(bt["lrp"][2]), N, s)
-        self._mark("update_s1(2 launches)")
-        L.call("uttt_grouped_update_stage1", L.ptr(self.W02), L.ptr(self.W1), L.ptr(bt["kp"]),
-               L.ptr(bt["vp"]), L.ptr(bt["lrp"][0]), L.ptr(bt["lrp"][1]), L.ptr(bt["lrp"][2]),
-               L.BF16, L.ptr(gs), 1, E, I, D, N, L.ptr(bt["dy"]), L.ptr(bt["hl"]), 1,
-               L.ptr(bt["ws_s1"]), bt["ws_s1_bytes"], s)
-        self._mark("wgrad")
-        L.call("uttt_grouped_wgrad_pair", L.ptr(bt["dy"]), L.ptr(bt["kp"]), L.ptr(bt["hl"]),
-               L.ptr(bt["vp"]), L.ptr(gs), 1, E, I, D, N, L.ptr(self.dW02), L.ptr(self.dW1),
-               L.ptr(self.ws_wg), self.ws_wg_bytes, s)
-        if self.cfg["train"]:
-            self._mark("update_bwd(5 launches)")
-            L.call("uttt_grouped_update_bwd", L.ptr(self.W02), L.ptr(self.W1), L.ptr(bt["kp"]),
-                   L.ptr(bt["vp"]), L.ptr(bt["lrp"][0]), L.ptr(bt["lrp"][1]),
-                   L.ptr(bt["lrp"][2]), L.BF16, L.ptr(gs), L.ptr(self.GW02), L.ptr(self.GW1), 1,
-                   E, I, D, N, L.ptr(self.gW02), L.ptr(self.gW1), L.ptr(bt["gK"]),
-                   L.ptr(bt["gV"]), L.ptr(bt["glr"][0]), L.ptr(bt["glr"][1]),
-                   L.ptr(bt["glr"][2]), L.ptr(bt["ws_bwd"]), bt["ws_bwd_bytes"], s)
-        self._mark(None)
-
-    def time_isolated(self, batched, reps=5, only=None):
-        """Mean launch duration of each single-launch kernel of a sweep, timed
-        as `reps` back-to-back launches between two events on the stream (only
-        kernel `only` when given)."""
         import torch
 
-        L, E, D, I, s = self.L, self.E, self.D, self.I, self.stream
-        st = self.sets[0]
-        bt = self.batched if batched else None
-        out = {}
+        from uttt_amd import moe
 
-        def timed(name, fn):
-            if only is not None and name != only:
-                return
+        self._mark("apply")
+        with torch.no_grad():
+            out, _ = moe.apply_moe_fast_weights_grouped(
+                st["x"], None, self.W1, None, self.R, self.rcfg, 1, routing_bias=self.rbias,
+                precomputed_w0_w2=self.W02)
+        return out
+
+    def _grads(self, writers_k, writers_v, writers_lr, layers):
+        """UPDATE (+ backward) of `layers` writers given as lists; returns the
+        packed bf16 weight gradients."""
+        import torch
+
+        from uttt_amd import moe
+
+        train = self.cfg["train"]
+        self._mark("update_fwd")
+        cat = (lambda ts: ts[0]) if layers == 1 else (lambda ts: torch.cat(ts, dim=1))
+        K, V, LR = cat(writers_k), cat(writers_v), cat(writers_lr)
+        if train:
+            K, V, LR = (t.detach().requires_grad_() for t in (K, V, LR))
+        with torch.no_grad():
+            m, gs, p, _ = moe.route_writers(K.detach(), layers, self.R, self.rcfg,
+                                            routing_bias=self.rbias)
+        with torch.enable_grad() if train else torch.no_grad():
+            dW02, dW1 = moe.aggregate_moe_update_grads(
+                [moe.WriterInputs(K, V, LR, m, p)], None, self.W1, None, self.k,
+                precomputed_w0_w2=self.W02, packed=True)
+            if train:
+                self._mark("update_bwd")
+                torch.autograd.backward([dW02, dW1], [self.GW02, self.GW1])
+        return dW02.detach(), dW1.detach()
+
+    def write(self, dW02, dW1):
+        from uttt_amd import fast_weight_write as FWW
+
+        self._mark("write")
+        FWW.apply_moe_update_packed(dW02, dW1, self.M02, self.M1, lr_scale=1.0,
+                                    out=((self.W02, self.W1), (self.M02, self.M1)))
+
+    def update_batched(self, layers, first_set):
+        sets = [self.sets[(first_set + l) % self.NSETS] for l in range(layers)]
+        dW02, dW1 = self._grads([s["k"] for s in sets], [s["v"] for s in sets],
+                                [s["lr"] for s in sets], layers)
+        self.write(dW02, dW1)
+
+    def update_one(self, st):
+        dW02, dW1 = self._grads([st["k"]], [st["v"]], [st["lr"]], 1)
+        self.write(dW02, dW1)
+
+    def sweep(self, layers, chunks, batched):
+        i = 0
+        for c in range(chunks):
+            for _ in range(layers):
+                self.apply(self.sets[i % self.NSETS])
+                i += 1
+            if c < chunks - 1:   # the last chunk is read but never written
+                if batched:   # aggregate: all writers' gradients, one write
+                    self.update_batched(layers, i)
+                    i += layers
+                else:         # chained: each writer updates and writes in turn
+                    for _ in range(layers):
+                        self.update_one(self.sets[i % self.NSETS])
+                        i += 1
+        self._mark(None)
+
+    # ---------------------------------------------------------- accounting --
+    def apply_symbols(self):
+        """Kernel symbols of the APPLY's gate/up and down projection (the
+        MFMA-skipping variant when experts average under 256 rows)."""
+        skip = "true" if self.N < 256 * self.E else "false"
+        return (f"tn_kernel<0, EpiSwiGLU, {skip}>",
+                f"tn_kernel<0, EpiStore<unsigned short>, {skip}>")
+
+    def launch_table(self, layers, chunks, batched):
+        """Every kernel launch of one sweep that carries GEMM work, grouped by
+        kernel symbol: {symbol: [algorithmic FLOP per sweep, algorithmic HBM
+        bytes per sweep, launches per sweep]} (NID = rows * I * D of the call;
+        bytes count each tensor once: the pool, token rows in and out)."""
+        E, D, I = self.E, self.D, self.I
+        Na = self.N
+        Nu = self.N * (layers if batched else 1)
+        n_apply = layers * chunks
+        n_upd = (chunks - 1) * (1 if batched else layers)
+        skip_a = "true" if Na < 256 * E else "false"
+        skip_u = "true" if Nu < 256 * E else "false"
+        w_bytes = 2 * 3 * E * I * D
+        tab = {}
+
+        def add(sym, nid_mult, rows, n, bytes_):
+            t = tab.setdefault(sym, [0, 0, 0])
+            t[0] += nid_mult * rows * I * D * n
+            t[1] += bytes_ * n
+            t[2] += n
+
+        add(f"tn_kernel<0, EpiSwiGLU, {skip_a}>", 4, Na, n_apply,
+            2 * (E * 2 * I * D + Na * D + Na * I))
+        add(f"tn_kernel<0, EpiStore<unsigned short>, {skip_a}>", 2, Na, n_apply,
+            2 * (E * D * I + Na * I + Na * D))
+        add("tn_kernel<1, EpiStore<float>, false>", 2, Nu, n_upd,
+            2 * E * D * I + 2 * Nu * D + 4 * Nu * I)
+        add("tn_kernel<0, EpiS1<BF16T>, false>", 4, Nu, n_upd,
+            2 * E * 2 * I * D + 2 * Nu * D + 4 * Nu * I + 2 * 3 * Nu * I)
+        add("wg_kernel<false>", 6, Nu, n_upd, w_bytes + 2 * Nu * (3 * I + 2 * D))
+        if self.cfg["train"]:
+            add("tn_kernel<1, EpiStore<unsigned short>, false>", 4, Nu, n_upd,
+                2 * 2 * E * D * I + 2 * Nu * D + 2 * Nu * 2 * I)          # DHG
+            add(f"tn_kernel<0, EpiStore<unsigned short>, {skip_u}>", 4, Nu, n_upd,
+                2 * E * 2 * I * D + 2 * Nu * D + 2 * Nu * 2 * I)          # GY
+            add("tn_kernel<0, EpiBwd<BF16T>, false>", 4, Nu, n_upd,
+                2 * E * 2 * I * D + 2 * Nu * D + 2 * Nu * 14 * I)
+            add("tn_kernel<1, EpiStore<unsigned short>, false>", 8, Nu, n_upd,
+                2 * 2 * E * 2 * I * D + 2 * Nu * 4 * I + 2 * Nu * D)      # grad_K
+            add(f"tn_kernel<0, EpiStore<unsigned short>, {skip_u}>", 4, Nu, n_upd,
+                2 * 2 * E * D * I + 2 * Nu * 2 * I + 2 * Nu * D)          # grad_V
+            add("wg_kernel<false>", 6, Nu, n_upd, w_bytes + 2 * Nu * (3 * I + 2 * D))
+        return tab
+
+    def isolated(self, symbol, batched, reps=5):
+        """Mean duration of `reps` back-to-back launches of one kernel symbol at
+        the shape the sweep runs it, between two HIP events on the launch
+        stream; None when this symbol has no single-launch recipe."""
+        import torch
+
+        from uttt_amd import _lib as L
+        from uttt_amd import moe
+        from uttt_amd.lact_moe_triton import _grouped
+        from uttt_amd.lact_moe_triton.triton_permute import (permute_kv_and_lrs,
+                                                             permute_with_expert_mask)
+
+        E, D, I, s = self.E, self.D, self.I, torch.cuda.current_stream().cuda_stream
+        gate_sym, down_sym = self.apply_symbols()
+        upd = self.launch_table(self.cfg["L"], 2, batched)
+        with torch.no_grad():
+            if symbol == gate_sym or (symbol == down_sym and upd[down_sym][2] == 2 * self.cfg["L"]):
+                st = self.sets[0]
+                m, gs, p, _ = moe.route(st["x"], self.R, self.rcfg, routing_bias=self.rbias)
+                xp, _, _ = permute_with_expert_mask(st["x"], m, p, self.k)
+                N = xp.shape[1]
+                hid = torch.empty(1, N, I, dtype=torch.bfloat16, device=self.dev)
+                yp = torch.empty(1, N, D, dtype=torch.bfloat16, device=self.dev)
+                if "EpiSwiGLU" in symbol:
+                    fn = lambda: L.call("uttt_grouped_gate_up", L.ptr(self.W02), L.ptr(xp),
+                                        L.ptr(gs), 1, E, I, D, N, L.ptr(hid), 1, s)
+                else:
+                    L.call("uttt_grouped_gate_up", L.ptr(self.W02), L.ptr(xp), L.ptr(gs), 1, E,
+                           I, D, N, L.ptr(hid), 1, s)
+                    fn = lambda: L.call("uttt_grouped_gemm_nt", L.ptr(self.W1), L.ptr(hid),
+                                        L.ptr(gs), 1, E, D, I, N, L.ptr(yp), s)
+            elif symbol == "wg_kernel<false>":
+                layers = self.cfg["L"] if batched else 1
+                sets = [self.sets[l % self.NSETS] for l in range(layers)]
+                K = torch.cat([x["k"] for x in sets], 1)
+                V = torch.cat([x["v"] for x in sets], 1)
+                LR = torch.cat([x["lr"] for x in sets], 1)
+                m, gs, p, _ = moe.route_writers(K, layers, self.R, self.rcfg,
+                                                routing_bias=self.rbias)
+                lrs = [LR[:, :, j].contiguous().to(torch.bfloat16) for j in range(3)]
+                kp, vp, l0, l1, l2 = permute_kv_and_lrs(K, V, *lrs, m, p, self.k)
+                dy, hl = _grouped.update_stage1(self.W02, self.W1, kp, vp, l0, l1, l2, gs,
+                                                token_major=True)
+                N = kp.shape[1]
+                dW02 = torch.empty_like(self.W02)
+                dW1 = torch.empty_like(self.W1)
+                nws = L.lib().uttt_grouped_wgrad_pair_workspace_bytes(1, E, I, D, N)
+                ws = torch.empty(max(nws, 1), dtype=torch.uint8, device=self.dev)
+                fn = lambda: L.call("uttt_grouped_wgrad_pair", L.ptr(dy), L.ptr(kp), L.ptr(hl),
+                                    L.ptr(vp), L.ptr(gs), 1, E, I, D, N, L.ptr(dW02),
+                                    L.ptr(dW1), L.ptr(ws), nws, s)
+            else:
+                return None
             fn()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0, e1 = _events(2)
             e0.record()
             for _ in range(reps):
                 fn()
             e1.record()
             torch.cuda.synchronize()
-            out[name] = e0.elapsed_time(e1) * 1e-3 / reps
-
-        N = self.N
-        gs_a = self.route_a["gs"]   # the last apply's routing
-        timed("gate_up", lambda: L.call("uttt_grouped_gate_up", L.ptr(self.W02), L.ptr(self.xp),
-                                        L.ptr(gs_a), 1, E, I, D, N, L.ptr(self.hid), 1, s))
-        timed("down_proj", lambda: L.call("uttt_grouped_gemm_nt", L.ptr(self.W1), L.ptr(self.hid),
-                                          L.ptr(gs_a), 1, E, D, I, N, L.ptr(self.yp), s))
-        timed("router", lambda: self.route(st["x"], self.route_a))
-        if bt is not None:
-            Nu, gs, kp, vp, dy, hl = (bt["N"], bt["route"]["gs"], bt["kp"], bt["vp"], bt["dy"],
-                                      bt["hl"])
-        else:
-            Nu, gs, kp, vp, dy, hl = N, self.route_u["gs"], self.kp, self.vp, self.dy, self.hl
-        timed("wgrad", lambda: L.call("uttt_grouped_wgrad_pair", L.ptr(dy), L.ptr(kp), L.ptr(hl),
-                                      L.ptr(vp), L.ptr(gs), 1, E, I, D, Nu, L.ptr(self.dW02),
-                                      L.ptr(self.dW1), L.ptr(self.ws_wg), self.ws_wg_bytes, s))
-        timed("write_step(2 launches)", self.write)
-        return out
-
-    def sweep(self, layers, chunks, batched):
-        i = 0
-        for c in range(chunks):
-            for l in range(layers):
-                self.apply(self.sets[i % self.NSETS])
-                i += 1
-            if c < chunks - 1:   # the last chunk is read but never written
-                if batched:   # aggregate: all writers' gradients, one write
-                    self.update_batched()
-                    self.write()
-                else:         # chained: each writer updates and writes in turn
-                    for l in range(layers):
-                        self.update(self.sets[i % self.NSETS])
-                        self.write()
-                        i += 1
+        return e0.elapsed_time(e1) * 1e-3 / reps
 
 
-def _event_times(events):
-    """{name: [seconds]} from consecutive (name, event) marks."""
+def kernel_times_profiled(run):
+    """{symbol: [total us, launches]} of the GPU kernels `run()` launches,
+    from torch.profiler's device activity (the ROCm tracer's per-dispatch
+    start and end); None when the profiler records no device activity."""
+    import torch
+    from torch.profiler import ProfilerActivity, profile
+
+    with profile(activities=[ProfilerActivity.CUDA]) as prof:
+        run()
+        torch.cuda.synchronize()
     out = {}
-    for (name, ev), (_, ev2) in zip(events, events[1:]):
-        if name is None:
+    for ev in prof.events():
+        if getattr(ev, "device_type", None) != torch.autograd.DeviceType.CUDA:
             continue
-        out.setdefault(name, []).append(ev.elapsed_time(ev2) * 1e-3)
+        us = ev.time_range.end - ev.time_range.start
+        if us <= 0:
+            continue
+        d = out.setdefault(norm_symbol(ev.name), [0.0, 0])
+        d[0] += us
+        d[1] += 1
+    return out or None
+
+
+def kernel_times_from_profile(summary):
+    """Fallback: {symbol: [total us, launches]} per sweep from the committed
+    rocprofv3 summary profiles/<summary> ("<symbol> calls= n avg_us= t")."""
+    import re
+
+    path = os.path.join(ROOT, "profiles", summary)
+    out = {}
+    try:
+        with open(path) as f:
+            for line in f:
+                m = re.match(r"\s*(\S.*?)\s+calls=\s*(\d+)\s+avg_us=\s*([\d.]+)", line)
+                if m:
+                    out[norm_symbol(m.group(1))] = [float(m.group(3)) * int(m.group(2)),
+                                                    int(m.group(2))]
+    except OSError:
+        return None
+    return out or None
+
+
+def _profile_value(summary, key, symbol):
+    """A "<key> <symbol> <value>" line of profiles/<summary>, or None."""
+    path = os.path.join(ROOT, "profiles", summary)
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith(key + " ") and line[len(key) + 1:].rsplit(" ", 1)[0] == symbol:
+                    return float(line.rsplit(" ", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def _stage_times(marks):
+    """{stage: total seconds} from consecutive (name, event) marks."""
+    out = {}
+    for (name, ev), (_, ev2) in zip(marks, marks[1:]):
+        if name is not None:
+            out[name] = out.get(name, 0.0) + ev.elapsed_time(ev2) * 1e-3
     return out
 
 
-def bench_moe(args, key):
+def bench_moe(args, key, extras=True):
     import torch
 
     cfg = MOE_CONFIGS[key]
@@ -636,9 +651,6 @@ def bench_moe(args, key):
     sw = MoeSweep(cfg, dev)
     layers, chunks = cfg["L"], SEQ // CHUNK
     batched = args.update_schedule == "batched"
-    if batched:
-        sw.prepare_batched(layers)
-    # warmup: W sweeps untimed
     for _ in range(max(args.warmup, 1)):
         sw.sweep(layers, 2, batched)
     torch.cuda.synchronize()
@@ -650,57 +662,12 @@ def bench_moe(args, key):
         torch.cuda.synchronize()
         walls.append(time.perf_counter() - t0)
     wall = statistics.mean(walls)
-    # one more sweep with every launch bracketed by events (per-kernel table)
-    sw.events = []
-    sw.sweep(layers, chunks, batched)
-    torch.cuda.synchronize()
-    per = _event_times(sw.events)
-    sw.events = None
-
-    # launch durations of the main kernels, each timed back to back between two
-    # HIP events on the launch stream (no host gaps inside the interval)
-    iso = sw.time_isolated(batched, reps=5)
-
-    fl = sw.flops()
-    Nu = sw.batched["N"] if batched else sw.N   # routed rows per UPDATE call
-    nid_u = Nu * sw.I * sw.D
-    fl.update({"update_s1(2 launches)": 6 * nid_u, "wgrad": 6 * nid_u,
-               "update_bwd(5 launches)": 30 * nid_u})
-    kern = {}
-    for name, ts in per.items():
-        t = iso.get(name, statistics.mean(ts))
-        d = dict(us=round(t * 1e6, 2), launches_per_sweep=len(ts),
-                 timing="isolated loop" if name in iso else "in-sweep events")
-        if name in fl:
-            tf = fl[name] / t / 1e12
-            d.update(TFLOPs=round(tf, 1), mfma_frac=round(tf / BF16_PEAK_TFLOPS, 4))
-        kern[name] = d
-    # algorithmic HBM bytes per launch (each tensor once: the expert weights
-    # read, token activations read, outputs written; bf16)
-    E, D, I, N = sw.E, sw.D, sw.I, sw.N
-    by = {"gate_up": 2 * (E * 2 * I * D + N * D + N * I),
-          "down_proj": 2 * (E * D * I + N * I + N * D),
-          "wgrad": 2 * (Nu * 2 * I + Nu * D + Nu * I + Nu * D + 3 * E * I * D),
-          # fp32 master read + written, bf16 dW read, bf16 fast weight written
-          "write_step(2 launches)": (4 + 2 + 4 + 2) * 3 * E * I * D}
-    for name, b in by.items():
-        if name in kern:
-            kern[name]["GBs"] = round(b / kern[name]["us"] / 1e3, 1)
-            kern[name]["hbm_frac"] = round(b / kern[name]["us"] / 1e3 / HBM_PEAK_GBS, 4)
-    # dominant single-kernel launch by time per sweep; its roofline is HBM
-    # when its arithmetic intensity is below the ridge (2.5 PFLOP/s / 8 TB/s)
-    dom = max((n for n in kern if "TFLOPs" in kern[n] and "(" not in n),
-              key=lambda n: kern[n]["us"] * kern[n]["launches_per_sweep"])
-    t_dom = iso.get(dom, statistics.mean(per[dom]))
-    ridge = BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
-    ai = fl[dom] / by[dom] if dom in by else float("inf")
     tokens = SEQ  # B = 1
-    value = tokens / wall
     nid = sw.N * sw.I * sw.D
     sweep_flops = layers * (chunks * 6 + (chunks - 1) * (42 if cfg["train"] else 12)) * nid
     res = dict(
         metric="fast-weight apply+update tokens/s",
-        value=round(value, 1),
+        value=round(tokens / wall, 1),
         unit="tokens/s",
         ms_per_step=round(wall * 1e3, 3),
         dtype="bf16",
@@ -708,6 +675,8 @@ def bench_moe(args, key):
                 "experts": cfg["E"], "topk": TOPK, "d": cfg["D"], "expert_hidden": cfg["I"],
                 "step": "one sweep: apply on 16 chunks x L layers, update on 15 chunks x L writers"
                         + (" (+ update backward)" if cfg["train"] else "") + " + write",
+                "path": "product API: uttt_amd.moe (routed read, batched-writer routing and "
+                        "aggregate update, autograd backward) + fast_weight_write",
                 "update_schedule": ("batched: the L writers of a chunk in one grouped UPDATE "
                                     "call (aggregate write = sum of writer gradients)"
                                     if batched else "per-layer: one UPDATE call per writer"),
@@ -716,82 +685,140 @@ def bench_moe(args, key):
                 "routing": ("fused router per apply (x) and per update (k): fp32 logits of one "
                             "shared router, " + ("Zipf(1.1)" if cfg["zipf"] else "N(0,0.5)")
                             + " expert prior as selection bias, topk_renorm gates")},
-        roofline=(dict(bound="hbm", kernel=dom, achieved=round(by[dom] / t_dom / 1e9, 1),
-                       peak=HBM_PEAK_GBS, unit="GB/s",
-                       frac=round(by[dom] / t_dom / 1e9 / HBM_PEAK_GBS, 4),
-                       traffic=_profile_traffic(f"{key}_sweep.txt", dom),
-                       algorithmic_bytes=by[dom], algorithmic_flops=fl[dom],
-                       arithmetic_intensity=round(ai, 1), avg_launch_us=round(t_dom * 1e6, 2),
-                       mfma_frac=round(fl[dom] / t_dom / 1e12 / BF16_PEAK_TFLOPS, 4))
-                  if ai < ridge else
-                  dict(bound="mfma", kernel=dom, achieved=round(fl[dom] / t_dom / 1e12, 2),
-                       peak=BF16_PEAK_TFLOPS, unit="TFLOP/s",
-                       frac=round(fl[dom] / t_dom / 1e12 / BF16_PEAK_TFLOPS, 4),
-                       traffic=_profile_traffic(f"{key}_sweep.txt", dom),
-                       algorithmic_flops=fl[dom], avg_launch_us=round(t_dom * 1e6, 2))),
         sweep=dict(algorithmic_flops=sweep_flops,
                    TFLOPs=round(sweep_flops / wall / 1e12, 1),
                    mfma_frac=round(sweep_flops / wall / 1e12 / BF16_PEAK_TFLOPS, 4)),
-        kernels=kern,
     )
+    if not extras:
+        return res
+
+    # stage totals of one sweep (events around the product calls)
+    sw.marks = []
+    sw.sweep(layers, chunks, batched)
+    torch.cuda.synchronize()
+    res["stages_ms_per_sweep"] = {k: round(v * 1e3, 2) for k, v in _stage_times(sw.marks).items()}
+    sw.marks = None
+
+    # per-kernel device time of one sweep, grouped by kernel symbol
+    src = "torch.profiler device activity of one sweep"
+    try:
+        ktimes = kernel_times_profiled(lambda: sw.sweep(layers, chunks, batched))
+    except Exception as exc:  # the tracer may be unavailable
+        ktimes, src = None, f"profiler unavailable ({type(exc).__name__})"
+    if ktimes is None:
+        ktimes = kernel_times_from_profile(f"{key}_sweep.txt")
+        src = f"committed rocprofv3 summary profiles/{key}_sweep.txt (older run)"
+    tab = sw.launch_table(layers, chunks, batched)
+    kern = {}
+    for sym, (us, n) in sorted((ktimes or {}).items(), key=lambda kv: -kv[1][0]):
+        d = dict(ms_per_sweep=round(us * 1e-3, 3), launches=n, avg_us=round(us / n, 2))
+        if sym in tab:
+            fl, by, _ = tab[sym]
+            d.update(TFLOPs=round(fl / (us * 1e-6) / 1e12, 1),
+                     mfma_frac=round(fl / (us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                     hbm_frac=round(by / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4))
+        kern[sym] = d
+        if len(kern) >= 14:
+            break
+    res["kernels_by_symbol"] = dict(source=src, top=kern)
+
+    # roofline: the dominant kernel symbol by time per sweep
+    dom = next((s for s in kern if s in tab), None)
+    if dom is not None:
+        fl, by, n = tab[dom]
+        fl1, by1 = fl / n, by / n
+        t_iso = sw.isolated(dom, batched)
+        t_dom = t_iso if t_iso is not None else kern[dom]["avg_us"] * 1e-6
+        ridge = BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
+        ai = fl1 / by1
+        mfma = fl1 / t_dom / 1e12
+        hbm = by1 / t_dom / 1e9
+        common = dict(kernel=dom, avg_launch_us=round(t_dom * 1e6, 2),
+                      timing=("HIP events around back-to-back launches on the launch stream"
+                              if t_iso is not None else src),
+                      launches_per_sweep=n, share_of_sweep=round(kern[dom]["ms_per_sweep"]
+                                                                 * 1e-3 / wall, 4),
+                      algorithmic_flops=int(fl1), algorithmic_bytes=int(by1),
+                      arithmetic_intensity=round(ai, 1),
+                      mfma_frac=round(mfma / BF16_PEAK_TFLOPS, 4),
+                      hbm_frac=round(hbm / HBM_PEAK_GBS, 4),
+                      traffic=_profile_traffic(f"{key}_sweep.txt", dom),
+                      counter_mfma_util=_profile_value(f"{key}_sweep.txt", "mfma_util", dom))
+        if ai >= ridge:
+            res["roofline"] = dict(bound="mfma", achieved=round(mfma, 1), peak=BF16_PEAK_TFLOPS,
+                                   unit="TFLOP/s", frac=round(mfma / BF16_PEAK_TFLOPS, 4), **common)
+        else:
+            res["roofline"] = dict(bound="hbm", achieved=round(hbm, 1), peak=HBM_PEAK_GBS,
+                                   unit="GB/s", frac=round(hbm / HBM_PEAK_GBS, 4), **common)
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline_moe(sw, cfg, layers, chunks)
     return res
 
 
 def profile_kernel(args, key, name):
-    """One short sweep to set up the routing and buffers of workload `key`,
-    then the isolated launch loop of kernel `name` alone (for counter passes,
+    """One short sweep to set up the pool and inputs of workload `key`, then
+    only the isolated launch loop of kernel symbol `name` (for counter passes,
     which profile every launch)."""
     import torch
 
     cfg = MOE_CONFIGS[key]
     sw = MoeSweep(cfg, torch.device("cuda", 0))
     batched = args.update_schedule == "batched"
-    if batched:
-        sw.prepare_batched(cfg["L"])
     sw.sweep(cfg["L"], 2, batched)
     torch.cuda.synchronize()
-    iso = sw.time_isolated(batched, reps=5, only=name)
-    if name not in iso:
-        raise SystemExit(f"bench.py: unknown kernel {name!r} (have {sorted(iso)})")
-    return dict(workload=cfg["label"], kernel=name, us=round(iso[name] * 1e6, 2), launches=6)
+    t = sw.isolated(name, batched, reps=5)
+    if t is None:
+        raise SystemExit(f"bench.py: no isolated recipe for kernel {name!r}")
+    return dict(workload=cfg["label"], kernel=name, us=round(t * 1e6, 2), launches=6)
+
+
+def _median_time(fn, reps=3):
+    """1 untimed warm-up run, then the median of `reps` timed runs (s)."""
+    fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
 
 
 def cpu_baseline_moe(sw, cfg, layers, chunks):
     """The fp32 PyTorch restatement (oracle/fastweight.py, fp32 accumulation)
     of one layer-chunk's grouped APPLY, UPDATE (and UPDATE backward for the
-    training slice) at the full shape, on this host's cores; the sweep time is
-    extrapolated as layers * (chunks * t_apply + (chunks-1) * t_update)."""
+    training slice) at the full shape, on all of this host's cores (1 warm-up
+    run, median of 3); the sweep time is extrapolated as
+    layers * (chunks * t_apply + (chunks-1) * t_update)."""
     import torch
 
     from oracle import fastweight as FW
+    from uttt_amd import moe
 
-    threads = max(1, min(16, os.cpu_count() or 1))
-    torch.set_num_threads(threads)
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
     st = sw.sets[0]
-    gs_a, gs_u = st["gs_a"].cpu(), st["gs_u"].cpu()
+    with torch.no_grad():
+        _, gs_a, _, _ = moe.route(st["x"], sw.R, sw.rcfg, routing_bias=sw.rbias)
+        _, gs_u, _, _ = moe.route(st["k"], sw.R, sw.rcfg, routing_bias=sw.rbias)
+    gs_a, gs_u = gs_a.cpu(), gs_u.cpu()
     W02, W1 = sw.W02.cpu(), sw.W1.cpu()
-    x = torch.randn(1, sw.N, sw.D).to(torch.bfloat16)
-    kk = torch.randn(1, sw.N, sw.D).to(torch.bfloat16)
-    vv = torch.randn(1, sw.N, sw.D).to(torch.bfloat16)
+    g = torch.Generator().manual_seed(0)
+    x, kk, vv = (torch.randn(1, sw.N, sw.D, generator=g).to(torch.bfloat16) for _ in range(3))
     lr = [torch.full((1, sw.N), 0.05).to(torch.bfloat16) for _ in range(3)]
     with FW.fp32_accumulate():
-        t0 = time.perf_counter()
-        FW.swiglu_ffn_fwd(W02, W1, x, gs_a)
-        t_apply = time.perf_counter() - t0
-        t0 = time.perf_counter()
-        FW.fast_weight_grads(W02, W1, kk, vv, *lr, gs_u)
-        t_update = time.perf_counter() - t0
+        t_apply = _median_time(lambda: FW.swiglu_ffn_fwd(W02, W1, x, gs_a))
+        t_update = _median_time(lambda: FW.fast_weight_grads(W02, W1, kk, vv, *lr, gs_u))
         if cfg["train"]:
-            t0 = time.perf_counter()
-            FW.fast_weight_grads_bwd(W02, W1, kk, vv, *lr, gs_u, sw.GW02.cpu(), sw.GW1.cpu())
-            t_update += time.perf_counter() - t0
+            GW02, GW1 = sw.GW02.cpu(), sw.GW1.cpu()
+            t_update += _median_time(lambda: FW.fast_weight_grads_bwd(W02, W1, kk, vv, *lr, gs_u,
+                                                                      GW02, GW1))
     t_sweep = layers * (chunks * t_apply + (chunks - 1) * t_update)
-    return dict(value=round(SEQ / t_sweep, 2), unit="tokens/s", cores=threads, kind="port",
-                sample=f"one layer-chunk at full shape: apply {t_apply:.2f} s, update"
-                       f"{' fwd+bwd' if cfg['train'] else ''} {t_update:.2f} s (fp32 torch, "
-                       f"{threads} threads); sweep extrapolated x{layers} layers x{chunks} chunks",
+    return dict(value=round(SEQ / t_sweep, 2), unit="tokens/s", cores=cores,
+                threads=torch.get_num_threads(), kind="port",
+                sample=f"one layer-chunk at full shape (1 warm-up, median of 3): apply "
+                       f"{t_apply:.2f} s, update{' fwd+bwd' if cfg['train'] else ''} "
+                       f"{t_update:.2f} s (fp32 torch); sweep extrapolated x{layers} layers "
+                       f"x{chunks} chunks",
                 cpu=_cpu_model())
 
 
@@ -913,8 +940,9 @@ def cpu_baseline_dense(cfg, sets, w):
     from oracle import dense as OD
     from oracle import fastweight as FW
 
-    threads = max(1, min(16, os.cpu_count() or 1))
-    torch.set_num_threads(threads)
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
+    threads = torch.get_num_threads()
     L_, r, S, c = cfg["L"], cfg["r"], cfg["S"], cfg["chunk"]
     wc = [x.cpu() for x in w]
     fast = tuple(x.to(torch.bfloat16) for x in wc)
@@ -936,7 +964,7 @@ def cpu_baseline_dense(cfg, sets, w):
             t = L_ * (chunks * t_read + (chunks - 1) * t_upd)
             sample = (f"one layer-chunk: read {t_read:.3f} s, update {t_upd:.3f} s; sweep "
                       f"extrapolated x{L_} layers x{chunks} chunks")
-    return dict(value=round(S / t, 2), unit="tokens/s", cores=threads, kind="port",
+    return dict(value=round(S / t, 2), unit="tokens/s", cores=cores, threads=threads, kind="port",
                 sample=sample + f" (fp32 torch, {threads} threads)", cpu=_cpu_model())
 
 
@@ -1056,8 +1084,9 @@ def cpu_baseline_decode(W02, W1, xs, routed, k, layers):
 
     from oracle import moe_read as MR
 
-    threads = max(1, min(16, os.cpu_count() or 1))
-    torch.set_num_threads(threads)
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
+    threads = torch.get_num_threads()
     B = xs[0].shape[0]
     t, done = 0.0, 0
     while t < 10.0 and done < layers:
@@ -1074,7 +1103,8 @@ def cpu_baseline_decode(W02, W1, xs, routed, k, layers):
             t += time.perf_counter() - t0
         done += 1
     per_layer = t / done
-    return dict(value=round(B / (per_layer * layers), 2), unit="tokens/s", cores=threads,
+    return dict(value=round(B / (per_layer * layers), 2), unit="tokens/s", cores=cores,
+                threads=threads,
                 kind="port", sample=f"{done} of {layers} layers' reads in fp32 torch "
                                     f"({per_layer * 1e3:.0f} ms each, {threads} threads); "
                                     f"step extrapolated x{layers} layers", cpu=_cpu_model())
@@ -1171,8 +1201,9 @@ def cpu_baseline_muon(I, D):
 
     from oracle import write as OW
 
-    threads = max(1, min(16, os.cpu_count() or 1))
-    torch.set_num_threads(threads)
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
+    threads = torch.get_num_threads()
     gen = torch.Generator().manual_seed(1)
     mats = [torch.randn(1, I, D, generator=gen), torch.randn(1, D, I, generator=gen)]
     done, flops, t = 0, 0, 0.0
@@ -1183,9 +1214,36 @@ def cpu_baseline_muon(I, D):
         t += time.perf_counter() - t0
         flops += _ns5_flops(I, D)
         done += 1
-    return dict(value=round(flops / t / 1e12, 4), unit="TFLOP/s", cores=threads, kind="port",
+    return dict(value=round(flops / t / 1e12, 4), unit="TFLOP/s", cores=cores, threads=threads, kind="port",
                 sample=f"NS5 of {done} of the 96 expert matrices ([{I}, {D}] / [{D}, {I}]) in "
                        f"bf16 torch: {t:.2f} s ({threads} threads)", cpu=_cpu_model())
+
+
+def other_targets(args):
+    """The other BASELINE targets measured in the same run (no CPU legs):
+    configs[2] permute / unpermute GB/s against HBM peak, and the configs[3]
+    uTTT-MoE 124M sweep."""
+    import copy
+
+    a = copy.copy(args)
+    a.no_cpu_baseline = True
+    a.steps, a.warmup = 20, 5
+    p = bench_permute(a)
+    k = p["kernels"]
+    a.steps, a.warmup = 3, 1
+    m = bench_moe(a, "moe124m", extras=False)
+    return {
+        "configs[2]_permute": dict(
+            workload=p["config"]["workload"],
+            permute_GBs=k["permute_chunk_kernel"]["GBs"],
+            permute_hbm_frac=k["permute_chunk_kernel"]["hbm_frac"],
+            unpermute_GBs=k["unpermute_chunk_kernel"]["GBs"],
+            unpermute_hbm_frac=k["unpermute_chunk_kernel"]["hbm_frac"],
+            step_GBs=p["value"], target_hbm_frac=0.70),
+        "configs[3]_moe124m": dict(workload=m["config"]["workload"], value=m["value"],
+                                   unit=m["unit"], ms_per_step=m["ms_per_step"],
+                                   sweep_mfma_frac=m["sweep"]["mfma_frac"]),
+    }
 
 
 WORKLOADS = {"permute": bench_permute,
@@ -1210,6 +1268,9 @@ def main():
                          "(batched) or one per writer (per-layer)")
     ap.add_argument("--no-cpu-baseline", action="store_true",
                     help="skip the CPU baseline leg (profiling runs)")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="default workload: skip the configs[2] / configs[3] measurements "
+                         "that ride along in the line")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one plain 256 MiB device copy (PMC scaling)")
     ap.add_argument("--profile-kernel", default=None,
@@ -1244,6 +1305,8 @@ def main():
         print(json.dumps(profile_kernel(args, args.workload, args.profile_kernel)), flush=True)
         return
     res = WORKLOADS[args.workload](args)
+    if args.workload == DEFAULT_WORKLOAD and not args.no_extras:
+        res["other_targets"] = other_targets(args)
     line = dict(metric=res.pop("metric"), value=res.pop("value"), unit=res.pop("unit"),
                 n_gpus=1, steps=args.steps, warmup=args.warmup,
                 ms_per_step=res.pop("ms_per_step"), higher_is_better=True, scaling="weak",

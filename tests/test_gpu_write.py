@@ -112,3 +112,39 @@ def test_muon_write_rejects_unaligned_shapes():
     w = torch.zeros(1, 1, 4, 8, device=DEV)
     with pytest.raises(RuntimeError, match="multiples of 8"):
         FWW.apply_moe_update_dense((w, w, w), (w, w, w), (w, w, w), use_moun=True)
+
+
+@pytest.mark.parametrize("use_moun,mom", [(False, False), (False, True), (True, True)])
+def test_packed_pool_write_equals_three_matrix_write(use_moun, mom):
+    """apply_moe_update_packed on W0_W2 / W1 (w0 rows then w2 rows per
+    expert) gives bit for bit the three-matrix write (same row kernel, the
+    same Newton-Schulz per [I, D] matrix), in place when given outputs."""
+    from uttt_amd import fast_weight_write as FWW
+
+    B, E, I, D = 2, 3, 64, 48
+    g = torch.Generator().manual_seed(21)
+    rn = lambda *s, sc=1.0: (torch.randn(*s, generator=g) * sc).to(DEV)
+    M0, M2, M1 = rn(B, E, I, D, sc=0.2), rn(B, E, I, D, sc=0.2), rn(B, E, D, I, sc=0.2)
+    G0, G2, G1 = (rn(*t.shape, sc=0.05).to(torch.bfloat16) for t in (M0, M2, M1))
+    moms = (rn(B, E, I, D, sc=0.05), rn(B, E, D, I, sc=0.05), rn(B, E, I, D, sc=0.05)) if mom else None
+    coeff = torch.full((B, 1, 1, 1), 0.9, device=DEV) if mom else None
+    ref = FWW.apply_moe_update_dense((G0, G1, G2), None, (M0, M1, M2), moms, coeff, lr_scale=0.7,
+                                     use_moun=use_moun)
+    M02 = torch.cat([M0, M2], dim=2).contiguous()
+    G02 = torch.cat([G0, G2], dim=2).contiguous()
+    mom_p = (torch.cat([moms[0], moms[2]], dim=2).contiguous(), moms[1]) if mom else None
+    F02 = torch.empty(M02.shape, dtype=torch.bfloat16, device=DEV)
+    F1 = torch.empty(M1.shape, dtype=torch.bfloat16, device=DEV)
+    M1c = M1.clone()
+    fast, master, new_mom = FWW.apply_moe_update_packed(
+        G02, G1, M02, M1c, mom_p, coeff, lr_scale=0.7, use_moun=use_moun,
+        out=((F02, F1), (M02, M1c)))
+    torch.cuda.synchronize()
+    assert fast[0] is F02 and master[0] is M02 and master[1] is M1c
+    assert torch.equal(F02, torch.cat([ref[0][0], ref[0][2]], dim=2))
+    assert torch.equal(F1, ref[0][1])
+    assert torch.equal(M02, torch.cat([ref[1][0], ref[1][2]], dim=2))
+    assert torch.equal(M1c, ref[1][1])
+    if mom:
+        assert torch.equal(new_mom[0], torch.cat([ref[2][0], ref[2][2]], dim=2))
+        assert torch.equal(new_mom[1], ref[2][1])
