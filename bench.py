@@ -503,12 +503,11 @@ class MoeSweep:
             2 * E * 2 * I * D + 2 * Nu * D + 4 * Nu * I + 2 * 3 * Nu * I)
         add("wg_kernel<false>", 6, Nu, n_upd, w_bytes + 2 * Nu * (3 * I + 2 * D))
         if self.cfg["train"]:
-            add("tn_kernel<1, EpiStore<unsigned short>, false>", 4, Nu, n_upd,
-                2 * 2 * E * D * I + 2 * Nu * D + 2 * Nu * 2 * I)          # DHG
-            add(f"tn_kernel<0, EpiStore<unsigned short>, {skip_u}>", 4, Nu, n_upd,
-                2 * E * 2 * I * D + 2 * Nu * D + 2 * Nu * 2 * I)          # GY
-            add("tn_kernel<0, EpiBwd<BF16T>, false>", 4, Nu, n_upd,
-                2 * E * 2 * I * D + 2 * Nu * D + 2 * Nu * 14 * I)
+            # the backward from the forward's saved bf16 Y0 | Y2 and DH
+            add("tn_kernel<1, EpiStore<unsigned short>, false>", 2, Nu, n_upd,
+                2 * E * D * I + 2 * Nu * D + 2 * Nu * I)                  # GD
+            add("tn_kernel<0, EpiBwdSaved<BF16T>, false>", 4, Nu, n_upd,
+                2 * E * 2 * I * D + 2 * Nu * D + 2 * Nu * 16 * I)         # GY + 2nd order
             add("tn_kernel<1, EpiStore<unsigned short>, false>", 8, Nu, n_upd,
                 2 * 2 * E * 2 * I * D + 2 * Nu * 4 * I + 2 * Nu * D)      # grad_K
             add(f"tn_kernel<0, EpiStore<unsigned short>, {skip_u}>", 4, Nu, n_upd,
@@ -664,7 +663,10 @@ def bench_moe(args, key, extras=True):
     wall = statistics.mean(walls)
     tokens = SEQ  # B = 1
     nid = sw.N * sw.I * sw.D
+    # the reference's work per update (BASELINE: 12 NID, +30 NID backward) and
+    # what this build executes (its backward reuses the forward's Y0, Y2, DH)
     sweep_flops = layers * (chunks * 6 + (chunks - 1) * (42 if cfg["train"] else 12)) * nid
+    exec_flops = layers * (chunks * 6 + (chunks - 1) * (36 if cfg["train"] else 12)) * nid
     res = dict(
         metric="fast-weight apply+update tokens/s",
         value=round(tokens / wall, 1),
@@ -687,7 +689,9 @@ def bench_moe(args, key, extras=True):
                             + " expert prior as selection bias, topk_renorm gates")},
         sweep=dict(algorithmic_flops=sweep_flops,
                    TFLOPs=round(sweep_flops / wall / 1e12, 1),
-                   mfma_frac=round(sweep_flops / wall / 1e12 / BF16_PEAK_TFLOPS, 4)),
+                   mfma_frac=round(sweep_flops / wall / 1e12 / BF16_PEAK_TFLOPS, 4),
+                   executed_flops=exec_flops,
+                   executed_mfma_frac=round(exec_flops / wall / 1e12 / BF16_PEAK_TFLOPS, 4)),
     )
     if not extras:
         return res

@@ -228,12 +228,15 @@ size_t uttt_update_stage1_workspace_bytes(int B, int I, int N);
  * lr0 = lr1 = lr2 = NULL means lr = 1: the APPLY backward's three-GEMM pass
  * (swiglu_backward_three_bmm_grouped_triton,
  * L/triton_grouped_swiglu_bwd_kernels.py:49-320, with v = grad_out).
+ * y0_y2_save [B,N,2I] and dh_save [B,N,I] (optional, both or neither):
+ * bf16(Y0 | Y2) and bf16(DH), token-major, for uttt_grouped_update_bwd.
  * workspace: uttt_update_stage1_workspace_bytes(B, I, N) bytes (DH). */
 int uttt_grouped_update_stage1(const void* w0_w2, const void* w1, const void* k, const void* v,
                                const void* lr0, const void* lr1, const void* lr2, int lr_dtype,
                                const int32_t* group_sizes, int B, int E, int I, int D, int N,
-                               void* dy0_dy2, void* hidden, int token_major, void* workspace,
-                               size_t workspace_bytes, void* stream);
+                               void* dy0_dy2, void* hidden, int token_major, void* y0_y2_save,
+                               void* dh_save, void* workspace, size_t workspace_bytes,
+                               void* stream);
 
 /* UPDATE, stage 2 (weight gradients).  Replaces grouped_two_gemm_fw_bwd_triton
  * (L/triton_lact_bwd_grouped_two_mm_grad_fw.py:231-312; kernel :55-225) with
@@ -300,11 +303,18 @@ size_t uttt_update_bwd_workspace_bytes(int B, int I, int N);
  * the upstream gradients grad_dw0_w2 [B,E,2I,D], grad_dw1 [B,E,D,I] (bf16).
  * Outputs: grad_w0_w2 [B,E,2I,D], grad_w1 [B,E,D,I], grad_k, grad_v [B,N,D]
  * (bf16), grad_lr0/1/2 [B,N] (lr_dtype; zero past the routed tokens).
+ * y0_y2_saved / dh_saved (optional, both or neither): the forward's saved
+ * bf16(Y0 | Y2) and bf16(DH) (uttt_grouped_update_stage1); with them the
+ * backward does not recompute Y0, Y2 and DH, which the reference's backward
+ * recomputes and rounds to bf16 (L/lact_fw_grad.py:131-176): GD = gw1^T v
+ * runs alone and GY = gw0_w2 k carries the second-order pass in its
+ * epilogue (6 N*I*D FLOP in place of 12).
  * workspace: uttt_update_bwd_workspace_bytes(B, I, N) bytes. */
 int uttt_grouped_update_bwd(const void* w0_w2, const void* w1, const void* k, const void* v,
                             const void* lr0, const void* lr1, const void* lr2, int lr_dtype,
                             const int32_t* group_sizes, const void* grad_dw0_w2,
-                            const void* grad_dw1, int B, int E, int I, int D, int N,
+                            const void* grad_dw1, const void* y0_y2_saved, const void* dh_saved,
+                            int B, int E, int I, int D, int N,
                             void* grad_w0_w2, void* grad_w1, void* grad_k, void* grad_v,
                             void* grad_lr0, void* grad_lr1, void* grad_lr2, void* workspace,
                             size_t workspace_bytes, void* stream);

@@ -274,3 +274,13 @@ def test_update_backward(name, lr_dtype):
         if nm in ("grad_K", "grad_V", "grad_lr0", "grad_lr1", "grad_lr2"):
             got, r = got[m], r[m]
         assert_bf16_close(got, r, name=nm)
+    # the backward without the forward's saved Y0 | Y2 and DH (recomputing them,
+    # as a caller of the C ABI gets when it passes none): same bar
+    from uttt_amd.lact_moe_triton import _update_bwd
+    plain = _update_bwd.fast_weight_grads_backward(*(t.detach() for t in ins), gs, GW02.to(DEV),
+                                                   GW1.to(DEV))
+    for got, r, nm in zip(plain, ref, names):
+        got = got.cpu()
+        if nm in ("grad_K", "grad_V", "grad_lr0", "grad_lr1", "grad_lr2"):
+            got, r = got[m], r[m]
+        assert_bf16_close(got, r, name=nm + " (recomputing)")

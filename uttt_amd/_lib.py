@@ -72,7 +72,7 @@ SIGNATURES = {
     "uttt_grouped_update_stage1": (
         c_int,
         [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_int, c_p, c_int, c_int, c_int, c_int, c_int,
-         c_p, c_p, c_int, c_p, c_sz, c_p],
+         c_p, c_p, c_int, c_p, c_p, c_p, c_sz, c_p],
     ),
     "uttt_grouped_wgrad_pair_workspace_bytes": (c_sz, [c_int] * 5),
     "uttt_dense_gather_heads": (
@@ -95,8 +95,8 @@ SIGNATURES = {
     "uttt_update_bwd_workspace_bytes": (c_sz, [c_int, c_int, c_int]),
     "uttt_grouped_update_bwd": (
         c_int,
-        [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_int, c_p, c_p, c_p, c_int, c_int, c_int, c_int,
-         c_int, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_sz, c_p],
+        [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_int, c_p, c_p, c_p, c_p, c_p, c_int, c_int, c_int,
+         c_int, c_int, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_sz, c_p],
     ),
     "uttt_transpose_2byte": (c_int, [c_p, c_int, c_int, c_int, c_p, c_p]),
     "uttt_rows_silu_l2norm": (c_int, [c_p, c_int, c_i64, c_int, c_i64, c_int, c_int, c_p, c_i64,

@@ -305,6 +305,8 @@ struct EpiS1 {
     const typename LR::S *lr0, *lr1, *lr2;
     uint16_t* dy;     // [B, N, 2I] or [B, 2I, N]
     uint16_t* hid;    // [B, N, I] or [B, I, N]
+    uint16_t* y_save;   // optional [B, N, 2I]: bf16(Y0 | Y2) for the backward
+    uint16_t* dh_save;  // optional [B, N, I]: bf16(DH)
     int I, N, token_major;
   };
   __device__ __forceinline__ static void apply(const Args& ea, const f32x16 (&acc0)[2][kNB],
@@ -339,8 +341,8 @@ struct EpiS1 {
       const float l1 = ea.lr1 ? LR::load(rw.l1) : 1.0f;
       const float l2 = ea.lr2 ? LR::load(rw.l2) : 1.0f;
       float y0[8], y2[8], d0[8], d2[8], hh[8];
-      const float dh[8] = {rw.dh0.x, rw.dh0.y, rw.dh0.z, rw.dh0.w,
-                           rw.dh1.x, rw.dh1.y, rw.dh1.z, rw.dh1.w};
+      float dh[8] = {rw.dh0.x, rw.dh0.y, rw.dh0.z, rw.dh0.w,
+                     rw.dh1.x, rw.dh1.y, rw.dh1.z, rw.dh1.w};
       staged8(c.lds0, nl, g, y0);
       staged8(c.lds1, nl, g, y2);
 #pragma unroll
@@ -350,6 +352,11 @@ struct EpiS1 {
         d0[u] = sg * y2[u] * dh[u] * (1.0f + y0[u] * (1.0f - sg)) * l0;
         d2[u] = sw * dh[u] * l2;
         hh[u] = sw * y2[u] * l1;
+      }
+      if (ea.y_save != nullptr) {  // the values the backward would recompute, rounded as it does
+        store8(ea.y_save + (int64_t)c.b * ea.N * I2 + (int64_t)tok * I2 + m, y0);
+        store8(ea.y_save + (int64_t)c.b * ea.N * I2 + (int64_t)tok * I2 + I + m, y2);
+        store8(ea.dh_save + (int64_t)c.b * ea.N * I + (int64_t)tok * I + m, dh);
       }
       if (ea.token_major) {
         store8(dyb + (int64_t)tok * I2 + m, d0);
@@ -458,6 +465,111 @@ struct EpiBwd {
       }
       // the 16 lanes of one token hold its 128 rows: sum them for this tile's
       // lr-gradient partial
+#pragma unroll
+      for (int d = 8; d > 0; d >>= 1) {
+        s0 += __shfl_xor(s0, d, 16);
+        s1 += __shfl_xor(s1, d, 16);
+        s2 += __shfl_xor(s2, d, 16);
+      }
+      if (g == 0 && c.tt.n0 + n < c.tt.size) {
+        const int64_t o = ((int64_t)c.mt * ea.B + c.b) * ea.N + tok;
+        ea.lr_part[o] = s0;
+        ea.lr_part[plane + o] = s1;
+        ea.lr_part[2 * plane + o] = s2;
+      }
+    });
+  }
+};
+
+// --- epilogue: UPDATE backward from the forward's saved values (acc0 = GY0 =
+// gw0 k, acc1 = GY2 = gw2 k): the second-order pass of EpiBwd with Y0 | Y2 and
+// DH read from the forward's bf16 saves (the values the reference's backward
+// recomputes and stores bf16) and GD = gw1^T v from its own launch (bf16), so
+// Y0, Y2 and DH are not recomputed and GY is used from the registers, rounded
+// to bf16 where the reference stores it.  Outputs as EpiBwd.
+template <class LR>
+struct EpiBwdSaved {
+  static constexpr bool kStaleColumnsUnused = false;  // reduces over tile rows per token
+  struct Args {
+    const uint16_t* y_saved;   // [B, N, 2I]
+    const uint16_t* dh_saved;  // [B, N, I]
+    const uint16_t* gd;        // [B, N, I]
+    const typename LR::S *lr0, *lr1, *lr2;
+    uint16_t *gdh, *gx, *dx, *hlr;
+    float* lr_part;
+    int I, N, B, m_tiles;
+  };
+  __device__ __forceinline__ static void apply(const Args& ea, const f32x16 (&acc0)[2][kNB],
+                               const f32x16 (&acc1)[2][kNB], const TileCtx& c, bool) {
+    const int I = ea.I, I2 = 2 * I;
+    const int64_t bo2 = (int64_t)c.b * ea.N * I2, bo1 = (int64_t)c.b * ea.N * I;
+    const int64_t plane = (int64_t)ea.m_tiles * ea.B * ea.N;
+    using S = typename LR::S;
+    struct Raw {
+      uint4 y0, y2, dh, gd;
+      S l0, l1, l2;
+    };
+    auto fetch = [&](int n, int g) __attribute__((always_inline)) {
+      const int m = c.m0 + 8 * g;
+      const int tok = c.tt.start + min(c.tt.n0 + n, c.tt.size - 1);  // clamped: always valid
+      const int mc = m < I ? m : 0;
+      const int64_t li = (int64_t)c.b * ea.N + tok;
+      const int64_t r2 = bo2 + (int64_t)tok * I2, r1 = bo1 + (int64_t)tok * I;
+      Raw r;
+      r.y0 = *reinterpret_cast<const uint4*>(ea.y_saved + r2 + mc);
+      r.y2 = *reinterpret_cast<const uint4*>(ea.y_saved + r2 + I + mc);
+      r.dh = *reinterpret_cast<const uint4*>(ea.dh_saved + r1 + mc);
+      r.gd = *reinterpret_cast<const uint4*>(ea.gd + r1 + mc);
+      r.l0 = ea.lr0[li];
+      r.l1 = ea.lr1[li];
+      r.l2 = ea.lr2[li];
+      return r;
+    };
+    staged_epilogue_prefetch(acc0, acc1, c, fetch, [&](int nl, int n, int g, const Raw& rw) __attribute__((always_inline)) {
+      const int m = c.m0 + 8 * g;
+      const bool ok = c.tt.n0 + n < c.tt.size && m < I;
+      const int tok = c.tt.start + c.tt.n0 + n;
+      float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f;
+      if (ok) {
+        const float L0 = LR::load(rw.l0);
+        const float L1 = LR::load(rw.l1);
+        const float L2 = LR::load(rw.l2);
+        float gy0[8], gy2[8], y0v[8], y2v[8], dh[8], gd[8];
+        staged8(c.lds0, nl, g, gy0);
+        staged8(c.lds1, nl, g, gy2);
+        unpack8(rw.y0, y0v);
+        unpack8(rw.y2, y2v);
+        unpack8(rw.dh, dh);
+        unpack8(rw.gd, gd);
+        const int64_t r2 = bo2 + (int64_t)tok * I2, r1 = bo1 + (int64_t)tok * I;
+        float o_gdh[8], o_gx0[8], o_gx2[8], o_dx0[8], o_dx2[8], o_hl[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const float y0 = y0v[u], y2 = y2v[u];
+          const float gd0 = bf16r(gy0[u]), gd2 = bf16r(gy2[u]);
+          const float sg = sigmoidf_(y0);
+          const float silu = sg * y0;
+          const float mul = sg * (1.0f + y0 * (1.0f - sg));  // silu'(y0)
+          const float ds = sg * (1.0f - sg);                  // sigmoid'(y0)
+          o_gdh[u] = gd0 * L0 * y2 * mul + gd2 * L2 * silu;
+          o_gx2[u] = gd0 * L0 * dh[u] * mul + gd[u] * L1 * silu;
+          const float gsig = gd0 * L0 * dh[u] * y2 * (1.0f + y0 - 2.0f * sg * y0);
+          o_gx0[u] = (gd2 * L2 * dh[u] + gd[u] * L1 * y2) * mul + gd0 * L0 * dh[u] * y2 * ds +
+                     gsig * ds;
+          s0 += gd0 * dh[u] * y2 * mul;
+          s1 += gd[u] * y2 * silu;
+          s2 += gd2 * dh[u] * silu;
+          o_dx0[u] = dh[u] * y2 * mul * L0;
+          o_dx2[u] = silu * dh[u] * L2;
+          o_hl[u] = L1 * y2 * silu;
+        }
+        store8(ea.gdh + r1 + m, o_gdh);
+        store8(ea.gx + r2 + m, o_gx0);
+        store8(ea.gx + r2 + I + m, o_gx2);
+        store8(ea.dx + r2 + m, o_dx0);
+        store8(ea.dx + r2 + I + m, o_dx2);
+        store8(ea.hlr + r1 + m, o_hl);
+      }
 #pragma unroll
       for (int d = 8; d > 0; d >>= 1) {
         s0 += __shfl_xor(s0, d, 16);
@@ -930,7 +1042,8 @@ constexpr bool kSkippable =
     AMAJ == KMajor && (std::is_same_v<Epi, EpiSwiGLU> || std::is_same_v<Epi, EpiStore<uint16_t>>);
 static_assert(kSkippable<KMajor, EpiSwiGLU> <= EpiSwiGLU::kStaleColumnsUnused &&
                   kSkippable<KMajor, EpiStore<uint16_t>> <= EpiStore<uint16_t>::kStaleColumnsUnused &&
-                  !kSkippable<KMajor, EpiS1<BF16T>> && !kSkippable<KMajor, EpiBwd<BF16T>>,
+                  !kSkippable<KMajor, EpiS1<BF16T>> && !kSkippable<KMajor, EpiBwd<BF16T>> &&
+                  !kSkippable<KMajor, EpiBwdSaved<BF16T>>,
               "the SKIP variant needs an epilogue that ignores stale token columns");
 
 template <int AMAJ, class Epi>
@@ -1156,8 +1269,8 @@ extern "C" int uttt_grouped_update_stage1(const void* w0_w2, const void* w1, con
                                           const void* lr2, int lr_dtype,
                                           const int32_t* group_sizes, int B, int E, int I, int D,
                                           int N, void* dy0_dy2, void* hidden, int token_major,
-                                          void* workspace, size_t workspace_bytes,
-                                          void* stream) {
+                                          void* y0_y2_save, void* dh_save, void* workspace,
+                                          size_t workspace_bytes, void* stream) {
   UTTT_REQUIRE(B >= 0 && E >= 1 && I >= 0 && D >= 0 && N >= 0, "grouped_update_stage1: bad sizes");
   UTTT_REQUIRE(I % 8 == 0 && D % 8 == 0,
                "grouped_update_stage1: I=%d and D=%d must be multiples of 8", I, D);
@@ -1166,8 +1279,11 @@ extern "C" int uttt_grouped_update_stage1(const void* w0_w2, const void* w1, con
                "grouped_update_stage1: null pointer");
   UTTT_REQUIRE((lr0 == nullptr) == (lr1 == nullptr) && (lr1 == nullptr) == (lr2 == nullptr),
                "grouped_update_stage1: pass all three lr vectors or none");
+  UTTT_REQUIRE((y0_y2_save == nullptr) == (dh_save == nullptr),
+               "grouped_update_stage1: pass both saved tensors or none");
   UTTT_REQUIRE(aligned16(w0_w2) && aligned16(w1) && aligned16(k) && aligned16(v) &&
-                   aligned16(dy0_dy2) && aligned16(hidden) && aligned16(workspace),
+                   aligned16(dy0_dy2) && aligned16(hidden) && aligned16(workspace) &&
+                   (y0_y2_save == nullptr || (aligned16(y0_y2_save) && aligned16(dh_save))),
                "grouped_update_stage1: tensors must be 16-byte aligned");
   const size_t need = uttt_update_stage1_workspace_bytes(B, I, N);
   UTTT_REQUIRE(workspace_bytes >= need, "grouped_update_stage1: workspace %zu < %zu bytes",
@@ -1188,6 +1304,8 @@ extern "C" int uttt_grouped_update_stage1(const void* w0_w2, const void* w1, con
                                       static_cast<const S*>(lr2),
                                       static_cast<uint16_t*>(dy0_dy2),
                                       static_cast<uint16_t*>(hidden),
+                                      static_cast<uint16_t*>(y0_y2_save),
+                                      static_cast<uint16_t*>(dh_save),
                                       I,
                                       N,
                                       token_major};
@@ -1273,7 +1391,8 @@ extern "C" size_t uttt_update_bwd_workspace_bytes(int B, int I, int N) {
 extern "C" int uttt_grouped_update_bwd(
     const void* w0_w2, const void* w1, const void* k, const void* v, const void* lr0,
     const void* lr1, const void* lr2, int lr_dtype, const int32_t* group_sizes,
-    const void* grad_dw0_w2, const void* grad_dw1, int B, int E, int I, int D, int N,
+    const void* grad_dw0_w2, const void* grad_dw1, const void* y0_y2_saved,
+    const void* dh_saved, int B, int E, int I, int D, int N,
     void* grad_w0_w2, void* grad_w1, void* grad_k, void* grad_v, void* grad_lr0, void* grad_lr1,
     void* grad_lr2, void* workspace, size_t workspace_bytes, void* stream) {
   UTTT_REQUIRE(B >= 0 && E >= 1 && I >= 0 && D >= 0 && N >= 0, "grouped_update_bwd: bad sizes");
@@ -1287,8 +1406,11 @@ extern "C" int uttt_grouped_update_bwd(
   UTTT_REQUIRE(aligned16(w0_w2) && aligned16(w1) && aligned16(k) && aligned16(v) &&
                    aligned16(grad_dw0_w2) && aligned16(grad_dw1) && aligned16(grad_w0_w2) &&
                    aligned16(grad_w1) && aligned16(grad_k) && aligned16(grad_v) &&
-                   aligned16(workspace),
+                   aligned16(workspace) &&
+                   (y0_y2_saved == nullptr || (aligned16(y0_y2_saved) && aligned16(dh_saved))),
                "grouped_update_bwd: tensors must be 16-byte aligned");
+  UTTT_REQUIRE((y0_y2_saved == nullptr) == (dh_saved == nullptr),
+               "grouped_update_bwd: pass both saved tensors or none");
   const UpdateBwdWs ws = update_bwd_ws(B, I, N);
   UTTT_REQUIRE(workspace_bytes >= ws.total, "grouped_update_bwd: workspace %zu < %zu bytes",
                workspace_bytes, ws.total);
@@ -1304,6 +1426,40 @@ extern "C" int uttt_grouped_update_bwd(
   const int64_t g02 = (int64_t)2 * I * D, g1 = (int64_t)D * I;
   const int m_tiles = (I + kTileRows - 1) / kTileRows;
 
+  if (y0_y2_saved != nullptr) {
+    // from the forward's saved bf16 Y0 | Y2 and DH: GD = gw1^T v (bf16 [N, I]),
+    // then GY0 | GY2 = gw0_w2 k with the second-order pass on the registers
+    uint16_t* gd = dhg;
+    if (int rc = launch_wide<RMajor>(grad_dw1, v, D, nullptr, nullptr, 0, I, I, g1, gd, B, E, N,
+                                     group_sizes, st, "grouped_update_bwd(GD)"))
+      return rc;
+    const TnArgs t = tn_args(grad_dw0_w2, grad_dw0_w2, k, D, D, g02, 0, I, I, 2 * I, kTileRows, I,
+                             B, E, N, group_sizes);
+    UTTT_DTYPE_SWITCH_LR(lr_dtype, LR, {
+      using S = typename LR::S;
+      const typename EpiBwdSaved<LR>::Args ea{static_cast<const uint16_t*>(y0_y2_saved),
+                                              static_cast<const uint16_t*>(dh_saved),
+                                              gd,
+                                              static_cast<const S*>(lr0),
+                                              static_cast<const S*>(lr1),
+                                              static_cast<const S*>(lr2),
+                                              gdh,
+                                              gx,
+                                              dx,
+                                              hlr,
+                                              part,
+                                              I,
+                                              N,
+                                              B,
+                                              m_tiles};
+      if (int rc = launch_tn<KMajor, EpiBwdSaved<LR>>(t, ea, B, st, "grouped_update_bwd(GY)"))
+        return rc;
+      hipLaunchKernelGGL((lr_grad_reduce_kernel<LR>), dim3((N + 255) / 256, B), dim3(256), 0, st,
+                         part, group_sizes, B, E, N, m_tiles, static_cast<S*>(grad_lr0),
+                         static_cast<S*>(grad_lr1), static_cast<S*>(grad_lr2));
+      if (int rc = check_launch("grouped_update_bwd(lr grads)")) return rc;
+    });
+  } else {
   // 1. DHG = [w1^T v | gw1^T v]  (bf16 [N, 2I])
   {
     const TnArgs t = tn_args(w1, grad_dw1, v, D, I, g1, 0, 0, I, I, kTileRows, I, B, E, N,
@@ -1347,6 +1503,7 @@ extern "C" int uttt_grouped_update_bwd(
                          static_cast<S*>(grad_lr1), static_cast<S*>(grad_lr2));
       if (int rc = check_launch("grouped_update_bwd(lr grads)")) return rc;
     });
+  }
   }
   // 5. grad_K = GW0_W2^T dx0_x2 + W0_W2^T grad_x0_x2 (K = 2I, chained)
   if (int rc = launch_wide<RMajor>(grad_dw0_w2, dx, 2 * I, w0_w2, gx, 2 * I, D, D, g02,

@@ -71,10 +71,13 @@ def gemm_tn(W, X_tok, group_sizes):
     return Y
 
 
-def update_stage1(W0_W2, W1, K, V, lr0, lr1, lr2, group_sizes, token_major: bool):
+def update_stage1(W0_W2, W1, K, V, lr0, lr1, lr2, group_sizes, token_major: bool,
+                  save: bool = False):
     """(DY0_DY2, Hidden) of the UPDATE, token-major ([B,N,2I], [B,N,I]) or the
     reference layout ([B,2I,N], [B,I,N]).  lr0 = lr1 = lr2 = None means lr = 1
-    (the APPLY backward's pass with V = grad_out)."""
+    (the APPLY backward's pass with V = grad_out).  save: also return the
+    bf16 (Y0 | Y2) [B,N,2I] and DH [B,N,I] the backward takes instead of
+    recomputing them."""
     L.require_device(W0_W2, W1, K, V, lr0, lr1, lr2, group_sizes)
     _check_bf16(W0_W2, W1, K, V)
     B, E, I2, D = W0_W2.shape
@@ -103,13 +106,17 @@ def update_stage1(W0_W2, W1, K, V, lr0, lr1, lr2, group_sizes, token_major: bool
     else:
         DY = torch.empty((B, I2, N), dtype=torch.bfloat16, device=dev)
         H = torch.empty((B, I, N), dtype=torch.bfloat16, device=dev)
+    Ys = DHs = None
+    if save:
+        Ys = torch.empty((B, N, I2), dtype=torch.bfloat16, device=dev)
+        DHs = torch.empty((B, N, I), dtype=torch.bfloat16, device=dev)
     ws_bytes = L.lib().uttt_update_stage1_workspace_bytes(B, I, N)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     L.call("uttt_grouped_update_stage1", L.ptr(W0_W2), L.ptr(W1), L.ptr(K), L.ptr(V),
            L.ptr(lrs[0]), L.ptr(lrs[1]), L.ptr(lrs[2]), lr_code, L.ptr(gs),
-           B, E, I, D, N, L.ptr(DY), L.ptr(H), int(token_major), L.ptr(ws), ws_bytes,
-           L.stream_of(K))
-    return DY, H
+           B, E, I, D, N, L.ptr(DY), L.ptr(H), int(token_major), L.ptr(Ys), L.ptr(DHs),
+           L.ptr(ws), ws_bytes, L.stream_of(K))
+    return (DY, H, Ys, DHs) if save else (DY, H)
 
 
 def wgrad_pair(DY_tok, K, H_tok, V, group_sizes):

@@ -13,9 +13,10 @@ from . import _grouped
 
 
 def fast_weight_grads_backward(W0_W2, W1, K, V, lr0, lr1, lr2, group_sizes, grad_dw0_dw2,
-                               grad_dw1):
+                               grad_dw1, y0_y2_saved=None, dh_saved=None):
     """Returns (grad_W0_W2, grad_W1, grad_K, grad_V, grad_lr0, grad_lr1, grad_lr2, None)
-    with the grad_lr* in the lr dtype and the lr tensors' shape."""
+    with the grad_lr* in the lr dtype and the lr tensors' shape.  y0_y2_saved /
+    dh_saved: the forward's bf16 (Y0 | Y2) and DH (both or neither)."""
     B, E, I2, D = W0_W2.shape
     I = I2 // 2
     N = K.shape[1]
@@ -39,7 +40,8 @@ def fast_weight_grads_backward(W0_W2, W1, K, V, lr0, lr1, lr2, group_sizes, grad
     L.call(
         "uttt_grouped_update_bwd",
         L.ptr(W0_W2), L.ptr(W1), L.ptr(K), L.ptr(V), L.ptr(lrs[0]), L.ptr(lrs[1]), L.ptr(lrs[2]),
-        L.dtype_code(lr_dtype), L.ptr(gs), L.ptr(gw02), L.ptr(gw1), B, E, I, D, N,
+        L.dtype_code(lr_dtype), L.ptr(gs), L.ptr(gw02), L.ptr(gw1), L.ptr(y0_y2_saved),
+        L.ptr(dh_saved), B, E, I, D, N,
         L.ptr(grad_W0_W2), L.ptr(grad_W1), L.ptr(grad_K), L.ptr(grad_V),
         L.ptr(glr[0]), L.ptr(glr[1]), L.ptr(glr[2]), L.ptr(ws), ws_bytes, L.stream_of(K),
     )
