@@ -205,9 +205,11 @@ def stream_of(t: torch.Tensor) -> int:
 
 
 def require_device(*tensors) -> None:
-    """The HIP path only: CPU tensors are a caller error, never a fallback."""
+    """The HIP path only: CPU tensors are a caller error, never a fallback.
+    Meta tensors pass: they only carry shapes through tracing (the registered
+    ops' fake implementations), and no kernel ever receives them."""
     for t in tensors:
-        if t is not None and t.device.type != "cuda":
+        if t is not None and t.device.type not in ("cuda", "meta"):
             raise RuntimeError(
                 f"uttt_amd ops run on the GPU only; got a tensor on {t.device}"
             )

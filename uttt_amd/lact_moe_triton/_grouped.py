@@ -4,12 +4,18 @@ launch on torch's current stream.  No CPU path: CPU tensors raise.
 
 Token-major intermediates ("_tok" suffix) are [B, N, rows] with rows
 contiguous; the reference's kernel-level functions exchange [B, rows, N].
+Every launch helper is registered as a torch.ops.uttt_hip op with a fake
+implementation (uttt_amd._ops), so torch.compile traces it.
 """
 from __future__ import annotations
 
+from typing import Optional
+
 import torch
+from torch import Tensor
 
 from uttt_amd import _lib as L  # absolute: the package also works mounted in the reference tree
+from uttt_amd._ops import traced_op
 
 
 def _check_bf16(*ts):
@@ -23,7 +29,13 @@ def group_sizes_i32(group_sizes: torch.Tensor) -> torch.Tensor:
     return gs.contiguous()
 
 
-def gate_up(W0_W2, X, group_sizes, token_major: bool):
+def _gate_up_fake(W0_W2, X, group_sizes, token_major):
+    B, N, I = X.shape[0], X.shape[1], W0_W2.shape[2] // 2
+    return X.new_empty((B, N, I) if token_major else (B, I, N))
+
+
+@traced_op("grouped_gate_up", _gate_up_fake)
+def gate_up(W0_W2: Tensor, X: Tensor, group_sizes: Tensor, token_major: bool) -> Tensor:
     """silu(w0 x) * (w2 x) per routed token: [B, N, I] (token_major) or [B, I, N]."""
     L.require_device(W0_W2, X, group_sizes)
     _check_bf16(W0_W2, X)
@@ -41,7 +53,12 @@ def gate_up(W0_W2, X, group_sizes, token_major: bool):
     return H
 
 
-def gemm_nt(W, X_tok, group_sizes):
+def _gemm_nt_fake(W, X_tok, group_sizes):
+    return X_tok.new_empty((X_tok.shape[0], X_tok.shape[1], W.shape[2]))
+
+
+@traced_op("grouped_gemm_nt", _gemm_nt_fake)
+def gemm_nt(W: Tensor, X_tok: Tensor, group_sizes: Tensor) -> Tensor:
     """Y[b, n] = W[b, e(n)] @ X_tok[b, n]: W [B, E, M, K], X_tok [B, N, K] -> [B, N, M]."""
     L.require_device(W, X_tok, group_sizes)
     _check_bf16(W, X_tok)
@@ -56,7 +73,12 @@ def gemm_nt(W, X_tok, group_sizes):
     return Y
 
 
-def gemm_tn(W, X_tok, group_sizes):
+def _gemm_tn_fake(W, X_tok, group_sizes):
+    return X_tok.new_empty((X_tok.shape[0], X_tok.shape[1], W.shape[3]))
+
+
+@traced_op("grouped_gemm_tn", _gemm_tn_fake)
+def gemm_tn(W: Tensor, X_tok: Tensor, group_sizes: Tensor) -> Tensor:
     """Y[b, n] = W[b, e(n)]^T @ X_tok[b, n]: W [B, E, K, M], X_tok [B, N, K] -> [B, N, M]."""
     L.require_device(W, X_tok, group_sizes)
     _check_bf16(W, X_tok)
@@ -73,6 +95,27 @@ def gemm_tn(W, X_tok, group_sizes):
 
 def update_stage1(W0_W2, W1, K, V, lr0, lr1, lr2, group_sizes, token_major: bool,
                   save: bool = False):
+    """See _update_stage1 (the registered op, which returns 0-element saves
+    when save is False)."""
+    out = _update_stage1(W0_W2, W1, K, V, lr0, lr1, lr2, group_sizes, token_major, save)
+    return out if save else out[:2]
+
+
+def _update_stage1_fake(W0_W2, W1, K, V, lr0, lr1, lr2, group_sizes, token_major, save):
+    B, N = K.shape[0], K.shape[1]
+    I2 = W0_W2.shape[2]
+    I = I2 // 2
+    dy = K.new_empty((B, N, I2) if token_major else (B, I2, N))
+    h = K.new_empty((B, N, I) if token_major else (B, I, N))
+    ys = K.new_empty((B, N, I2) if save else (0,))
+    dhs = K.new_empty((B, N, I) if save else (0,))
+    return dy, h, ys, dhs
+
+
+@traced_op("grouped_update_stage1", _update_stage1_fake)
+def _update_stage1(W0_W2: Tensor, W1: Tensor, K: Tensor, V: Tensor, lr0: Optional[Tensor],
+                   lr1: Optional[Tensor], lr2: Optional[Tensor], group_sizes: Tensor,
+                   token_major: bool, save: bool) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """(DY0_DY2, Hidden) of the UPDATE, token-major ([B,N,2I], [B,N,I]) or the
     reference layout ([B,2I,N], [B,I,N]).  lr0 = lr1 = lr2 = None means lr = 1
     (the APPLY backward's pass with V = grad_out).  save: also return the
@@ -110,16 +153,27 @@ def update_stage1(W0_W2, W1, K, V, lr0, lr1, lr2, group_sizes, token_major: bool
     if save:
         Ys = torch.empty((B, N, I2), dtype=torch.bfloat16, device=dev)
         DHs = torch.empty((B, N, I), dtype=torch.bfloat16, device=dev)
+    else:
+        Ys = torch.empty((0,), dtype=torch.bfloat16, device=dev)
+        DHs = torch.empty((0,), dtype=torch.bfloat16, device=dev)
     ws_bytes = L.lib().uttt_update_stage1_workspace_bytes(B, I, N)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     L.call("uttt_grouped_update_stage1", L.ptr(W0_W2), L.ptr(W1), L.ptr(K), L.ptr(V),
            L.ptr(lrs[0]), L.ptr(lrs[1]), L.ptr(lrs[2]), lr_code, L.ptr(gs),
-           B, E, I, D, N, L.ptr(DY), L.ptr(H), int(token_major), L.ptr(Ys), L.ptr(DHs),
-           L.ptr(ws), ws_bytes, L.stream_of(K))
-    return (DY, H, Ys, DHs) if save else (DY, H)
+           B, E, I, D, N, L.ptr(DY), L.ptr(H), int(token_major), L.ptr(Ys) if save else None,
+           L.ptr(DHs) if save else None, L.ptr(ws), ws_bytes, L.stream_of(K))
+    return DY, H, Ys, DHs
 
 
-def wgrad_pair(DY_tok, K, H_tok, V, group_sizes):
+def _wgrad_pair_fake(DY_tok, K, H_tok, V, group_sizes):
+    B, N, I2 = DY_tok.shape
+    E, D = group_sizes.shape[1], K.shape[2]
+    return K.new_empty((B, E, I2, D)), K.new_empty((B, E, D, I2 // 2))
+
+
+@traced_op("grouped_wgrad_pair", _wgrad_pair_fake)
+def wgrad_pair(DY_tok: Tensor, K: Tensor, H_tok: Tensor, V: Tensor,
+               group_sizes: Tensor) -> tuple[Tensor, Tensor]:
     """dW0_W2 [B,E,2I,D] = DY[seg]^T K[seg]; dW1 [B,E,D,I] = V[seg]^T H[seg]."""
     L.require_device(DY_tok, K, H_tok, V, group_sizes)
     _check_bf16(DY_tok, K, H_tok, V)
@@ -140,7 +194,13 @@ def wgrad_pair(DY_tok, K, H_tok, V, group_sizes):
     return dW02, dW1
 
 
-def wgrad(A_tok, B_tok, group_sizes, transposed: bool):
+def _wgrad_fake(A_tok, B_tok, group_sizes, transposed):
+    B, R, C, E = A_tok.shape[0], A_tok.shape[2], B_tok.shape[2], group_sizes.shape[1]
+    return A_tok.new_empty((B, E, C, R) if transposed else (B, E, R, C))
+
+
+@traced_op("grouped_wgrad", _wgrad_fake)
+def wgrad(A_tok: Tensor, B_tok: Tensor, group_sizes: Tensor, transposed: bool) -> Tensor:
     """out[b,e] = A[seg]^T B[seg] as [B,E,R,C] (or [B,E,C,R] when transposed)."""
     L.require_device(A_tok, B_tok, group_sizes)
     _check_bf16(A_tok, B_tok)
@@ -156,7 +216,12 @@ def wgrad(A_tok, B_tok, group_sizes, transposed: bool):
     return out
 
 
-def transpose_last2(X):
+def _transpose_fake(X):
+    return X.new_empty((X.shape[0], X.shape[2], X.shape[1]))
+
+
+@traced_op("transpose_2byte", _transpose_fake)
+def transpose_last2(X: Tensor) -> Tensor:
     """[B, R, C] -> [B, C, R] (2-byte elements) on the GPU."""
     L.require_device(X)
     assert X.element_size() == 2
@@ -183,17 +248,43 @@ def _gemm2(name, Wa, Xa, Wb, Xb, group_sizes, rows_first: bool):
     return Y
 
 
-def gemm_nt2(Wa, Xa, Wb, Xb, group_sizes):
+def _gemm2_fake(Wa, Xa, Wb, Xb, group_sizes, rows_first):
+    M = Wa.shape[2] if rows_first else Wa.shape[3]
+    return Xa.new_empty((Xa.shape[0], Xa.shape[1], M))
+
+
+def _gemm_nt2_fake(Wa, Xa, Wb, Xb, group_sizes):
+    return _gemm2_fake(Wa, Xa, Wb, Xb, group_sizes, True)
+
+
+def _gemm_tn2_fake(Wa, Xa, Wb, Xb, group_sizes):
+    return _gemm2_fake(Wa, Xa, Wb, Xb, group_sizes, False)
+
+
+@traced_op("grouped_gemm_nt2", _gemm_nt2_fake)
+def gemm_nt2(Wa: Tensor, Xa: Tensor, Wb: Tensor, Xb: Tensor, group_sizes: Tensor) -> Tensor:
     """Y[b, n] = Wa[b, e(n)] Xa[b, n] + Wb[b, e(n)] Xb[b, n]: W [B,E,M,K] -> [B,N,M]."""
     return _gemm2("uttt_grouped_gemm_nt2", Wa, Xa, Wb, Xb, group_sizes, True)
 
 
-def gemm_tn2(Wa, Xa, Wb, Xb, group_sizes):
+@traced_op("grouped_gemm_tn2", _gemm_tn2_fake)
+def gemm_tn2(Wa: Tensor, Xa: Tensor, Wb: Tensor, Xb: Tensor, group_sizes: Tensor) -> Tensor:
     """Y[b, n] = Wa[b, e(n)]^T Xa[b, n] + Wb[b, e(n)]^T Xb[b, n]: W [B,E,K,M] -> [B,N,M]."""
     return _gemm2("uttt_grouped_gemm_tn2", Wa, Xa, Wb, Xb, group_sizes, False)
 
 
-def swiglu_bwd_bwd(dh, x0_x2, lr0, lr1, lr2, grad_dx0_dx2, grad_hidden_lr1):
+def _swiglu_bwd_bwd_fake(dh, x0_x2, lr0, lr1, lr2, grad_dx0_dx2, grad_hidden_lr1):
+    B, I, Lt = dh.shape
+    xd, ld = x0_x2.dtype, lr0.dtype
+    e = lambda *sh, dt: dh.new_empty(sh, dtype=dt)
+    return (e(B, I, Lt, dt=xd), e(B, 2 * I, Lt, dt=xd), e(B, Lt, dt=ld), e(B, Lt, dt=ld),
+            e(B, Lt, dt=ld), e(B, 2 * I, Lt, dt=xd), e(B, I, Lt, dt=xd))
+
+
+@traced_op("swiglu_bwd_bwd", _swiglu_bwd_bwd_fake)
+def swiglu_bwd_bwd(dh: Tensor, x0_x2: Tensor, lr0: Tensor, lr1: Tensor, lr2: Tensor,
+                   grad_dx0_dx2: Tensor, grad_hidden_lr1: Tensor
+                   ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
     """Second-order SwiGLU pointwise pass on [B, I, L] / [B, 2I, L] tensors."""
     L.require_device(dh, x0_x2, lr0, lr1, lr2, grad_dx0_dx2, grad_hidden_lr1)
     B, I, Lt = dh.shape

@@ -13,9 +13,13 @@ order unspecified).
 """
 from __future__ import annotations
 
+from typing import Optional
+
 import torch
+from torch import Tensor
 
 from . import _lib as L
+from ._ops import none_if_empty, traced_op
 
 ROUTER_TYPES = {"softmax": 0, "norm_softmax": 1, "norm_relu": 2}
 COMBINE_MODES = {"selected_prob": 0, "topk_renorm": 1}
@@ -70,6 +74,23 @@ def create_router_mask_sizes_probs(router_logits, topk, alpha=1.0, use_sigmoid=F
     group_sizes int32 [B,E], combine_weights [B,E,T], balance_probs [B,E,T],
     lb_loss); combine and balance in router_logits' dtype."""
     _check_modes(use_sigmoid, router_type, combine_mode)
+    return _select(router_logits, int(topk), float(alpha), router_type, combine_mode,
+                   float(router_scale), float(norm_eps), routing_bias)
+
+
+def _select_fake(router_logits, topk, alpha, router_type, combine_mode, router_scale, norm_eps,
+                 routing_bias):
+    B, E, T = router_logits.shape
+    dt = router_logits.dtype
+    e = router_logits.new_empty
+    return (e((B, E, T), dtype=torch.bool), e((B, E), dtype=torch.int32), e((B, E, T), dtype=dt),
+            e((B, E, T), dtype=dt), e((), dtype=torch.float32))
+
+
+@traced_op("router_select", _select_fake)
+def _select(router_logits: Tensor, topk: int, alpha: float, router_type: str, combine_mode: str,
+            router_scale: float, norm_eps: float, routing_bias: Optional[Tensor]
+            ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     L.require_device(router_logits)
     assert router_logits.dim() == 3, "router_logits must be [B, E, T]"
     B, E, T = router_logits.shape
@@ -94,6 +115,26 @@ def route_tokens(x, router_proj_weights, topk, alpha=1.0, use_sigmoid=False,
     returns them (router_probs = the combine weights), plus the fp32 logits
     [B, E, T] when return_logits."""
     _check_modes(use_sigmoid, router_type, combine_mode)
+    out = _route(x, router_proj_weights, int(topk), float(alpha), router_type, combine_mode,
+                 float(router_scale), float(norm_eps), routing_bias, bool(return_logits))
+    return out if return_logits else out[:4]
+
+
+def _route_fake(x, router_proj_weights, topk, alpha, router_type, combine_mode, router_scale,
+                norm_eps, routing_bias, return_logits):
+    B, T, _ = x.shape
+    E = router_proj_weights.shape[-2]
+    e = x.new_empty
+    return (e((B, E, T), dtype=torch.bool), e((B, E), dtype=torch.int32),
+            e((B, E, T), dtype=torch.float32), e((B, E, T), dtype=torch.float32),
+            e((B, E, T) if return_logits else (0,), dtype=torch.float32))
+
+
+@traced_op("route_tokens", _route_fake)
+def _route(x: Tensor, router_proj_weights: Tensor, topk: int, alpha: float, router_type: str,
+           combine_mode: str, router_scale: float, norm_eps: float,
+           routing_bias: Optional[Tensor], return_logits: bool
+           ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     L.require_device(x, router_proj_weights)
     assert x.dim() == 3, "x must be [B, T, D]"
     B, T, D = x.shape
@@ -109,11 +150,11 @@ def route_tokens(x, router_proj_weights, topk, alpha=1.0, use_sigmoid=False,
     assert R.shape[-1] == D, "router weights must have x's last dimension"
     bias, bias_sb = _bias_arg(routing_bias, B, E, x.device)
     mask, gs, comb, bal, lb, ws, nbytes = _outputs(B, E, T, D, x.device)
-    logits = torch.empty((B, E, T), dtype=torch.float32, device=x.device) if return_logits else None
+    logits = torch.empty((B, E, T) if return_logits else (0,), dtype=torch.float32,
+                         device=x.device)
     L.call("uttt_route_tokens", L.ptr(x), L.dtype_code(x.dtype), L.ptr(R), w_sb, B, T, D, E,
            L.ptr(bias), bias_sb, int(topk), ROUTER_TYPES[router_type],
            COMBINE_MODES[combine_mode], float(alpha), float(router_scale), float(norm_eps),
-           L.ptr(logits), L.ptr(mask), L.ptr(gs), L.ptr(comb), L.ptr(bal), L.ptr(lb), L.ptr(ws),
-           nbytes, L.stream_of(x))
-    out = (mask, gs, comb, bal)
-    return out + (logits,) if return_logits else out
+           L.ptr(logits) if return_logits else None, L.ptr(mask), L.ptr(gs), L.ptr(comb),
+           L.ptr(bal), L.ptr(lb), L.ptr(ws), nbytes, L.stream_of(x))
+    return mask, gs, comb, bal, logits
