@@ -83,6 +83,27 @@ int uttt_route_tokens(const void* x, int x_dtype, const float* router_w, int64_t
                       float* combine, float* balance, float* lb_loss, void* workspace,
                       size_t workspace_bytes, void* stream);
 
+/* Loss-free balancing counts.  Replaces _store_loss_free_counts with
+ * _loss_free_counts_for_scope (M/modeling_recurrent_lact.py:1646-1654,
+ * 1695-1712) on one GPU (the all-reduce of :1657-1660 is the caller's):
+ * apply_freqs, update_freqs fp32 [L, B, E] (per-layer row counts);
+ * pending_counts fp32 [L, E] (pool = 0) or [E] (pool = 1) +=
+ * sum over b (and over l when pool) of apply + update; *steps += 1 (int64). */
+int uttt_loss_free_store_counts(const float* apply_freqs, const float* update_freqs, int L, int B,
+                                int E, int pool, float* pending_counts, long long* steps,
+                                void* stream);
+
+/* Loss-free bias step.  Replaces the tensor part of _maybe_update_loss_free_bias
+ * (M/modeling_recurrent_lact.py:1662-1693); the caller keeps the step
+ * counter's warm-up / interval logic.  bias, counts fp32 [rows, E] (rows = 1
+ * for the pool scope).  When the counts sum to > 0: mode 1 clears them (warm-up);
+ * mode 2 does, per row, bias += rate * sign(mean(counts) - counts),
+ * bias -= mean(bias), clamp to [-bias_max, bias_max] if bias_max >= 0,
+ * then clears the counts and adds 1 to *num_updates (int64).  Means are the
+ * fp32 sum times fp32(1 / E), as torch's GPU mean computes them. */
+int uttt_loss_free_bias_step(float* bias, float* counts, int rows, int E, int mode, float rate,
+                             float bias_max, long long* num_updates, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Routing map                                                              */
 /* ------------------------------------------------------------------------ */
@@ -361,6 +382,20 @@ int uttt_write_step(const float* master, const void* fast_in, const void* grad, 
                     const float* mom_in, const float* m_coeff, float lr_scale, int B,
                     int64_t rows_per_batch, int C, int seg, int norm_from_fast, int renorm_master,
                     float* master_out, void* fast_out, float* mom_out, void* stream);
+
+/* Unit-row WRITE of the NVS block.  Replaces the write of apply_raw_update
+ * (uttt_nvs/models/uttt_moe_block.py:665-714; Muon, when on, runs before it
+ * through uttt_newton_schulz5):
+ *   U = master + grad              (fp32; grad fp32, bf16 or fp16)
+ *   master_out = U,   fast_out = bf16(U / max(|U|, 1e-5))   (F.normalize)
+ * per row of C elements.  The tensors hold `groups` groups of R rows; row r
+ * of group g starts at g * <tensor>_gs + r * C elements, so the w0 / w2
+ * halves of a packed [B, E, 2I, D] gradient or fast weight are addressed in
+ * place (gs = 2I * D, offset 0 or I * D).  master_out may be master (same
+ * strides).  C must be a multiple of 4, at most 4096; strides multiples of 4. */
+int uttt_write_unit_rows(const float* master, int64_t master_gs, const void* grad, int grad_dtype,
+                         int64_t grad_gs, int64_t groups, int R, int C, float* master_out,
+                         int64_t master_out_gs, void* fast_out, int64_t fast_gs, void* stream);
 
 /* Momentum step of the Muon write on its own: out = raw + m_coeff[b] * mom
  * (fp32; raw fp32 or bf16; B batches of per_batch elements).  Replaces the

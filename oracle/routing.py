@@ -1,8 +1,11 @@
 """Oracle of the router (checker only; see oracle/__init__.py).
 
-Restates create_router_mask_sizes_probs
-(uttt_llm/flame/custom_models/uttt_moe/moe_routing.py:7-75, cited R:line) in
-fp32 torch on the CPU.
+Restates, in fp32 torch on the CPU:
+  create_router_mask_sizes_probs       uttt_llm/flame/custom_models/uttt_moe/
+                                       moe_routing.py:7-75 (cited R:line)
+  nvs_create_router_mask_sizes_probs   uttt_nvs/models/routing.py:4-44 (V:)
+  LossFree                             the loss-free balancing bias of
+                                       uttt_moe/modeling_recurrent_lact.py:1646-1712 (M:)
 """
 from __future__ import annotations
 
@@ -63,3 +66,67 @@ def router_logits(x, router_w):
     if R.dim() == 2:
         R = R.unsqueeze(0)
     return torch.matmul(R, x.double().transpose(1, 2))
+
+
+def nvs_create_router_mask_sizes_probs(router_logits, topk, alpha=1.0):
+    """uttt_nvs/models/routing.py:4-44 (cited V:).  Returns (mask, group_sizes,
+    router_probs, lb_loss)."""
+    E = router_logits.shape[-2]
+    _, idx = torch.topk(router_logits, k=topk, dim=-2)                 # V:16
+    mask = torch.zeros_like(router_logits, dtype=torch.bool)
+    mask.scatter_(-2, idx, True)                                       # V:17-18
+    gs = mask.sum(dim=-1).to(torch.int32)                              # V:21
+    probs = torch.softmax(router_logits.to(torch.float32), dim=-2).to(router_logits.dtype) * alpha
+    pm = probs.mean(dim=0).mean(dim=-1)                                # V:38-42
+    gm = gs.to(torch.float32).mean(dim=0)
+    lb = (pm * (gm / gm.sum())).sum() * E
+    return mask, gs, probs, lb
+
+
+def _gpu_mean(x, dim=None):
+    """torch's GPU mean: the fp32 sum times the fp32 reciprocal of the count
+    (the sums here are of small integers or are compared with a tolerance)."""
+    n = x.numel() if dim is None else x.shape[dim]
+    s = x.double().sum() if dim is None else x.double().sum(dim=dim, keepdim=True)
+    return (s.float() * torch.tensor(1.0 / n, dtype=torch.float32)).float()
+
+
+class LossFree:
+    """The loss-free balancing state, restating modeling_recurrent_lact.py
+    (cited M:) _loss_free_counts_for_scope :1646-1654, _store_loss_free_counts
+    :1695-1712 and _maybe_update_loss_free_bias :1662-1693 on fp32 CPU
+    tensors, one process (no all-reduce)."""
+
+    def __init__(self, num_layers, num_experts, scope, rate, bias_max, warmup, interval):
+        shape = (num_experts,) if scope == "pool" else (num_layers, num_experts)
+        self.scope, self.rate, self.bias_max = scope, rate, bias_max
+        self.warmup, self.interval = warmup, interval
+        self.bias = torch.zeros(shape)
+        self.counts = torch.zeros(shape)
+        self.steps = 0
+        self.num_updates = 0
+
+    def store(self, apply_freqs, update_freqs):
+        c = apply_freqs.float().sum(dim=1) + update_freqs.float().sum(dim=1)   # M:1651
+        if self.scope == "pool":
+            c = c.sum(dim=0)                                                    # M:1652-1653
+        self.counts = self.counts + c                                           # M:1711
+        self.steps += 1                                                         # M:1712
+
+    def maybe_update(self):
+        if self.counts.sum() <= 0:                                              # M:1667-1668
+            return
+        if self.steps <= self.warmup:                                           # M:1670-1672
+            self.counts = torch.zeros_like(self.counts)
+            return
+        if (self.steps - self.warmup) % self.interval != 0:                     # M:1673-1678
+            return
+        dim = None if self.scope == "pool" else -1
+        target = _gpu_mean(self.counts, dim)                                    # M:1681
+        step = torch.tensor(self.rate, dtype=torch.float32) * torch.sign(target - self.counts)
+        self.bias = self.bias + step                                            # M:1682
+        self.bias = self.bias - _gpu_mean(self.bias, dim)                       # M:1683-1686
+        if self.bias_max >= 0:                                                  # M:1687-1691
+            self.bias = self.bias.clamp(min=-self.bias_max, max=self.bias_max)
+        self.counts = torch.zeros_like(self.counts)                             # M:1692
+        self.num_updates += 1                                                   # M:1693

@@ -15,6 +15,11 @@ fp32 torch on the CPU, written from the two reference call sites:
                on, and the master keeps the unprojected value unless master
                renorm is on.
 
+  nvs_write    apply_raw_update, uttt_nvs/models/uttt_moe_block.py:665-714
+               (cited V:).  master + raw gradient (no momentum, no step
+               size), the master kept unprojected, fast = bf16 unit rows of
+               the new master (F.normalize, clamped at 1e-5).
+
 newton_schulz5  zeropower_via_newtonschulz5,
                uttt_llm/flame/custom_models/uttt_moe/ttt_operation.py:19-46 (cited N:),
                the Muon orthogonalisation both writes run between the momentum
@@ -87,6 +92,39 @@ def moe_write(grads, masterw, momentum_buf=None, m_coeff=None, lr_scale=1.0, use
         new_master.append(p)
         fast.append(p.to(torch.bfloat16))                  # M:822
     return tuple(fast), tuple(new_master), (tuple(new_mom) if use_mom else momentum_buf)
+
+
+def _unit_rows(u: torch.Tensor) -> torch.Tensor:
+    """u / max(|u|, eps) over the last dim (F.normalize's clamped divide),
+    the norm summed in fp64."""
+    n = _norm(u, u.dim() - 1)
+    return u / torch.where(n < EPS, torch.full_like(n, EPS), n)
+
+
+def nvs_write(raw_grads, masterw, inter_dim, use_muon=False):
+    """apply_raw_update, uttt_nvs/models/uttt_moe_block.py:665-714 (cited V:).
+    raw_grads: (dw0_w2 [b,e,2I,D], dw1) packed (V:669-693) or (dw0, dw1, dw2)
+    (V:695-714), fp32; masterw (w0, w1, w2) fp32.  No momentum and no step
+    size: the masters take the raw (or orthogonalised) gradient and keep the
+    unprojected sum; the fast weights are bf16 unit rows of the new masters.
+    Returns (new fast, new masters): fast = (bf16 cat[w0, w2] rows, bf16 w1)
+    for packed grads, else the three bf16 matrices."""
+    if len(raw_grads) == 2:
+        dw0_w2, dw1 = raw_grads
+        dws = [dw0_w2[:, :, :inter_dim], dw1, dw0_w2[:, :, inter_dim:]]   # V:672-673
+    else:
+        dws = list(raw_grads)
+    if use_muon:                                                           # V:674-678
+        out = []
+        for g in dws:
+            b, e, r, c = g.shape
+            out.append(newton_schulz5(g.reshape(b * e, r, c)).reshape(b, e, r, c))
+        dws = out
+    new_master = [w.float() + g.float() for w, g in zip(masterw, dws)]     # V:679-681
+    unit = [_unit_rows(m).to(torch.bfloat16) for m in new_master]          # V:683-691
+    if len(raw_grads) == 2:
+        return (torch.cat([unit[0], unit[2]], dim=2), unit[1]), tuple(new_master)
+    return tuple(unit), tuple(new_master)
 
 
 def wide_to_slices(weight: torch.Tensor, name: str, r: int) -> torch.Tensor:

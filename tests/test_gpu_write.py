@@ -148,3 +148,53 @@ def test_packed_pool_write_equals_three_matrix_write(use_moun, mom):
     if mom:
         assert torch.equal(new_mom[0], torch.cat([ref[2][0], ref[2][2]], dim=2))
         assert torch.equal(new_mom[1], ref[2][1])
+
+
+@pytest.mark.parametrize("packed,grad_dtype,b,e,I,D", [
+    (True, torch.float32, 2, 3, 40, 96),       # rows of 40: a partly filled wave
+    (True, torch.bfloat16, 1, 4, 3072, 1536),  # the 760M expert shapes
+    (False, torch.float32, 1, 2, 384, 192),
+])
+def test_nvs_unit_row_write_matches_oracle(packed, grad_dtype, b, e, I, D):
+    """apply_raw_update (uttt_nvs/models/uttt_moe_block.py:665-714): masters
+    bit-exact (one fp32 add), fast weights within two bf16 ulps; a zero row
+    and a row of norm 3e-6 cover the clamp of F.normalize."""
+    ms = [_rand(s, 30 + i) / D ** 0.5 for i, s in enumerate([(b, e, I, D), (b, e, D, I), (b, e, I, D)])]
+    g02 = _rand((b, e, 2 * I, D), 40, 0.05).to(grad_dtype)
+    g1 = _rand((b, e, D, I), 41, 0.05).to(grad_dtype)
+    ms[0][0, 0, 0] = 0.0
+    g02[0, 0, 0] = 0.0
+    ms[0][0, 0, 1] = 0.0
+    g02[0, 0, 1] = (torch.ones(D) * (3e-6 / D ** 0.5)).to(grad_dtype)
+    grads = (g02, g1) if packed else (g02[:, :, :I].contiguous(), g1, g02[:, :, I:].contiguous())
+    rf, rm = OW.nvs_write(tuple(g.float() for g in grads), ms, I)
+    of, om = FWW.apply_raw_update(tuple(g.to(DEV) for g in grads), tuple(w.to(DEV) for w in ms),
+                                  inter_dim=I)
+    assert len(of) == len(rf)
+    for a, r in zip(om, rm):
+        assert torch.equal(a.cpu(), r)
+    for a, r in zip(of, rf):
+        assert a.shape == r.shape
+        _close_fast(a, r)
+    assert torch.equal(of[0][0, 0, 0].cpu().float(), torch.zeros(D))
+
+
+def test_nvs_unit_row_write_muon():
+    """With Muon the step is this library's Newton-Schulz (checked on its own
+    in the Muon tests); the write after it matches the oracle's write of that
+    same step, packed and as three matrices."""
+    b, e, I, D = 1, 2, 64, 32
+    ms = [_rand(s, 50 + i).to(DEV) for i, s in enumerate([(b, e, I, D), (b, e, D, I), (b, e, I, D)])]
+    g02 = _rand((b, e, 2 * I, D), 60, 0.05).to(DEV)
+    g1 = _rand((b, e, D, I), 61, 0.05).to(DEV)
+    of, om = FWW.apply_raw_update((g02, g1), ms, inter_dim=I, use_muon=True)
+    s02 = FWW.newton_schulz5(g02.reshape(b * e * 2, I, D)).reshape(g02.shape)
+    s1 = FWW.newton_schulz5(g1.reshape(b * e, D, I)).reshape(g1.shape)
+    rf, rm = OW.nvs_write((s02.float().cpu(), s1.float().cpu()), [w.cpu() for w in ms], I)
+    for a, r in zip(om, rm):
+        assert torch.equal(a.cpu(), r)
+    for a, r in zip(of, rf):
+        _close_fast(a, r)
+    of3, om3 = FWW.apply_raw_update((g02[:, :, :I], g1, g02[:, :, I:]), ms, inter_dim=I,
+                                    use_muon=True)
+    assert torch.equal(torch.cat([of3[0], of3[2]], dim=2), of[0]) and torch.equal(of3[1], of[1])

@@ -118,3 +118,71 @@ def test_dense_write_segment_norms(master_renorm):
             assert torch.equal(nf[i], nm[i].to(torch.bfloat16))
         else:
             assert torch.equal(nm[i], master[i] + grads[i] * 0.9)
+
+
+# ---- NVS unit-row write (oracle/write.nvs_write) ----
+
+def _nvs_inputs(b=2, e=3, I=8, D=12, seed=0):
+    ms = (_rand(b, e, I, D, seed=seed), _rand(b, e, D, I, seed=seed + 1),
+          _rand(b, e, I, D, seed=seed + 2))
+    g02 = _rand(b, e, 2 * I, D, seed=seed + 3) * 0.1
+    g1 = _rand(b, e, D, I, seed=seed + 4) * 0.1
+    return ms, g02, g1
+
+
+def test_nvs_write_unit_rows_and_unprojected_master():
+    ms, g02, g1 = _nvs_inputs()
+    I = 8
+    (f02, f1), (m0, m1, m2) = OW.nvs_write((g02, g1), ms, I)
+    # the masters keep the plain sum: (master' - master) is the gradient
+    torch.testing.assert_close(m0 - ms[0], g02[:, :, :I], rtol=0, atol=1e-6)
+    torch.testing.assert_close(m2 - ms[2], g02[:, :, I:], rtol=0, atol=1e-6)
+    torch.testing.assert_close(m1 - ms[1], g1, rtol=0, atol=1e-6)
+    # fast rows: unit length along the last dim, parallel to the masters
+    for f in (f02, f1):
+        n = _rownorm(f.float())
+        assert ((n - 1).abs() < 8e-3).all()
+    torch.testing.assert_close(f02[:, :, :I].float(), (m0 / _rownorm(m0)[..., None]).float(),
+                               rtol=8e-3, atol=1e-6)
+    torch.testing.assert_close(f02[:, :, I:].float(), (m2 / _rownorm(m2)[..., None]).float(),
+                               rtol=8e-3, atol=1e-6)
+    # the library routine the reference calls
+    ref = torch.nn.functional.normalize(m1, dim=3, eps=1e-5).to(torch.bfloat16)
+    assert (f1.float() - ref.float()).abs().max() <= 8e-3
+
+
+def test_nvs_write_clamps_tiny_rows():
+    """F.normalize divides by max(|u|, eps): a row of norm 3e-6 comes out with
+    norm 0.3 (a "+ eps" form would give 0.23), a zero row stays zero."""
+    ms, g02, g1 = _nvs_inputs(b=1, e=1, I=4, D=8)
+    w0 = ms[0].clone()
+    w0[0, 0, 0] = 0.0
+    w0[0, 0, 1] = 0.0
+    g02 = g02.clone()
+    g02[0, 0, 0] = 0.0
+    v = torch.randn(8, generator=torch.Generator().manual_seed(9))
+    g02[0, 0, 1] = v / v.norm() * 3e-6
+    (f02, _), _ = OW.nvs_write((g02, g1), (w0, ms[1], ms[2]), 4)
+    assert torch.equal(f02[0, 0, 0].float(), torch.zeros(8))
+    assert abs(float(f02[0, 0, 1].float().norm()) - 0.3) < 3e-3
+
+
+def test_nvs_write_packed_equals_three_matrices():
+    ms, g02, g1 = _nvs_inputs(seed=4)
+    I = 8
+    (f02, f1), m = OW.nvs_write((g02, g1), ms, I)
+    f3, m3 = OW.nvs_write((g02[:, :, :I], g1, g02[:, :, I:]), ms, I)
+    assert torch.equal(f02, torch.cat([f3[0], f3[2]], dim=2)) and torch.equal(f1, f3[1])
+    for a, b in zip(m, m3):
+        assert torch.equal(a, b)
+
+
+def test_nvs_write_muon_step_is_orthogonalised():
+    """With Muon the masters move by NS5 of each expert matrix: the step's
+    singular values sit near 1 (the quintic's band), so its Frobenius norm
+    is about sqrt(min(R, C))."""
+    ms, g02, g1 = _nvs_inputs(b=1, e=2, I=16, D=32, seed=6)
+    _, m = OW.nvs_write((g02, g1), ms, 16, use_muon=True)
+    step = m[0] - ms[0]
+    sv = torch.linalg.svdvals(step[0, 0].double())
+    assert (sv > 0.5).all() and (sv < 1.3).all()

@@ -129,6 +129,15 @@ SIGNATURES = {
         [c_p, c_p, c_p, c_int, c_p, c_p, ctypes.c_float, c_int, c_i64, c_int, c_int, c_int, c_int,
          c_p, c_p, c_p, c_p],
     ),
+    "uttt_loss_free_store_counts": (c_int, [c_p, c_p, c_int, c_int, c_int, c_int, c_p, c_p, c_p]),
+    "uttt_loss_free_bias_step": (
+        c_int,
+        [c_p, c_p, c_int, c_int, c_int, ctypes.c_float, ctypes.c_float, c_p, c_p],
+    ),
+    "uttt_write_unit_rows": (
+        c_int,
+        [c_p, c_i64, c_p, c_int, c_i64, c_i64, c_int, c_int, c_p, c_i64, c_p, c_i64, c_p],
+    ),
     "uttt_momentum_add": (c_int, [c_p, c_int, c_p, c_p, c_int, c_i64, c_p, c_p]),
     "uttt_newton_schulz5_workspace_bytes": (ctypes.c_size_t, [c_int, c_int, c_int]),
     "uttt_newton_schulz5": (

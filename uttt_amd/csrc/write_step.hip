@@ -150,6 +150,58 @@ __global__ __launch_bounds__(kWS) void write_step_kernel(
   }
 }
 
+// Unit-row write: U = master + grad (one fp32 add), master_out = U and
+// fast_out = bf16(U / max(|U|, 1e-5)), the clamped divide of F.normalize.
+// Rows are addressed by group, row r of group g at g * group_stride + r * C
+// (per tensor), so the w0 and w2 halves of a packed [B, E, 2I, D] tensor are
+// read and written in place as B*E groups of I rows.  One wave per row, as in
+// write_step_kernel; master_out may alias master (same strides).
+template <class GT, int NV>
+__global__ __launch_bounds__(kWS) void write_unit_rows_kernel(
+    const float* master, int64_t master_gs, const typename GT::S* __restrict__ grad,
+    int64_t grad_gs, int64_t nrows, int R, int C, float* master_out, int64_t master_out_gs,
+    uint16_t* __restrict__ fast_out, int64_t fast_gs) {
+#pragma clang fp contract(off)
+  const int64_t row = (int64_t)blockIdx.x * (kWS / kWave) + threadIdx.x / kWave;
+  if (row >= nrows) return;  // whole wave leaves together
+  const int lane = lane_id();
+  const int64_t g = row / R, r = row - g * R;
+  const float* w_row = master + g * master_gs + r * C;
+  const typename GT::S* g_row = grad + g * grad_gs + r * C;
+  float4 u[NV];
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int e = 4 * (lane + kWave * i);
+    const bool ok = e < C;
+    const int ec = ok ? e : 0;
+    const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const float4 wl = nt_load4(w_row + ec);
+    const float4 gl = load_grad4<GT>(g_row + ec);
+    const float4 w = ok ? wl : z;
+    const float4 gv = ok ? gl : z;
+    u[i] = make_float4(w.x + gv.x, w.y + gv.y, w.z + gv.z, w.w + gv.w);
+    ss += sumsq4(u[i]);
+  }
+  const float nrm = sqrtf(wave_sum(ss));
+  const float den = nrm < 1e-5f ? 1e-5f : nrm;  // clamp_min: a NaN norm stays NaN
+  float* mo_row = master_out + g * master_out_gs + r * C;
+  uint16_t* f_row = fast_out + g * fast_gs + r * C;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int e = 4 * (lane + kWave * i);
+    if (e < C) {
+      nt_store4(mo_row + e, u[i]);
+      Half4 f;
+      f.h[0] = f32_to_bf16(u[i].x / den);
+      f.h[1] = f32_to_bf16(u[i].y / den);
+      f.h[2] = f32_to_bf16(u[i].z / den);
+      f.h[3] = f32_to_bf16(u[i].w / den);
+      nt_store_h4(f_row + e, f);
+    }
+  }
+}
+
 inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 // out = raw + m_coeff[b] * mom (fp32, the product rounded before the sum as the
@@ -253,4 +305,49 @@ extern "C" int uttt_momentum_add(const void* raw, int raw_dtype, const float* mo
                        out);
   });
   return check_launch("momentum_add");
+}
+
+extern "C" int uttt_write_unit_rows(const float* master, int64_t master_gs, const void* grad,
+                                    int grad_dtype, int64_t grad_gs, int64_t groups, int R, int C,
+                                    float* master_out, int64_t master_out_gs, void* fast_out,
+                                    int64_t fast_gs, void* stream) {
+  UTTT_REQUIRE(groups >= 0 && R >= 0 && C >= 0, "write_unit_rows: bad sizes");
+  UTTT_REQUIRE(C % 4 == 0 && C <= 4096,
+               "write_unit_rows: rows of %d elements (must be a multiple of 4, at most 4096)", C);
+  UTTT_REQUIRE(grad_dtype == UTTT_F32 || grad_dtype == UTTT_BF16 || grad_dtype == UTTT_F16,
+               "write_unit_rows: unsupported grad dtype %d", grad_dtype);
+  const int64_t nrows = groups * R;
+  if (nrows == 0 || C == 0) return UTTT_OK;
+  UTTT_REQUIRE(master && grad && master_out && fast_out, "write_unit_rows: null tensor");
+  const int64_t rc = (int64_t)R * C;
+  UTTT_REQUIRE(master_gs >= rc && grad_gs >= rc && master_out_gs >= rc && fast_gs >= rc &&
+                   master_gs % 4 == 0 && grad_gs % 4 == 0 && master_out_gs % 4 == 0 &&
+                   fast_gs % 4 == 0,
+               "write_unit_rows: group strides must hold R*C elements and be multiples of 4");
+  UTTT_REQUIRE(aligned(master, 16) && aligned(master_out, 16) && aligned(fast_out, 8) &&
+                   aligned(grad, dtype_bytes(grad_dtype) * 4),
+               "write_unit_rows: tensors must be 16-byte (fp32) / 8-byte (bf16) aligned");
+  UTTT_REQUIRE(nrows < (1ll << 26), "write_unit_rows: %lld rows exceed one launch",
+               (long long)nrows);
+  const unsigned grid = (unsigned)((nrows + kWS / kWave - 1) / (kWS / kWave));
+  hipStream_t st = as_stream(stream);
+  const int nv = (C + 4 * kWave - 1) / (4 * kWave);
+  const int nvp = nv <= 1 ? 1 : nv <= 2 ? 2 : nv <= 4 ? 4 : nv <= 8 ? 8 : nv <= 12 ? 12 : 16;
+  auto* fout = reinterpret_cast<uint16_t*>(fast_out);
+#define UTTT_WU_LAUNCH(NV)                                                                       \
+  hipLaunchKernelGGL((write_unit_rows_kernel<TT, NV>), dim3(grid), dim3(kWS), 0, st, master,     \
+                     master_gs, reinterpret_cast<const typename TT::S*>(grad), grad_gs, nrows, R, \
+                     C, master_out, master_out_gs, fout, fast_gs)
+  UTTT_DTYPE_SWITCH_LR(grad_dtype, TT, {
+    switch (nvp) {
+      case 1: UTTT_WU_LAUNCH(1); break;
+      case 2: UTTT_WU_LAUNCH(2); break;
+      case 4: UTTT_WU_LAUNCH(4); break;
+      case 8: UTTT_WU_LAUNCH(8); break;
+      case 12: UTTT_WU_LAUNCH(12); break;
+      default: UTTT_WU_LAUNCH(16); break;
+    }
+  });
+#undef UTTT_WU_LAUNCH
+  return check_launch("write_unit_rows");
 }

@@ -1,14 +1,17 @@
 """The fast-weight WRITE step on the gfx950 kernel of csrc/write_step.hip.
 
-Two functions with the argument meaning and return values of the reference's
+Functions with the argument meaning and return values of the reference's
 write methods (self's configuration becomes keyword arguments):
 
   apply_moe_update_dense    _apply_moe_update_dense,
                             uttt_llm/flame/custom_models/uttt_moe/modeling_recurrent_lact.py:754-825
+  apply_moe_update_packed   the same write on the packed [B,E,2I,D] pool
   apply_shared_update       _apply_shared_update,
                             uttt_llm/flame/custom_models/uttt_dense/modeling_recurrent_lact.py:1109-1240
+  apply_raw_update          the NVS block's write, apply_raw_update,
+                            uttt_nvs/models/uttt_moe_block.py:665-714 (unit rows)
 
-Both return freshly allocated (fast bf16, master fp32, momentum) tuples and
+They return freshly allocated (fast bf16, master fp32, momentum) tuples and
 never modify their inputs, as the reference does.  With use_moun the step is
 orthogonalised between the momentum and the write (newton_schulz5 below):
 the momentum runs on its own kernel, Newton-Schulz on the grouped GEMMs, and
@@ -229,3 +232,70 @@ def _slices_to_wide(s, name, b, h, r):
     if name != "w1":
         return s.reshape(b, h, r * d, d)
     return s.reshape(b, h, r, d, d).permute(0, 1, 3, 2, 4).reshape(b, h, d, r * d).contiguous()
+
+
+def _group_stride(t, name):
+    """Group stride of a [b, e, R, C] tensor whose rows are contiguous and
+    whose b*e groups sit at one stride (a whole tensor, or the w0 / w2 half
+    of a packed [b, e, 2I, C] tensor)."""
+    assert t.dim() == 4, f"{name} must be [b, e, R, C]"
+    b, e, R, C = t.shape
+    assert t.stride(3) == 1 and (R <= 1 or t.stride(2) == C), f"{name}: rows must be contiguous"
+    assert b <= 1 or t.stride(0) == e * t.stride(1), f"{name}: groups must sit at one stride"
+    return t.stride(1) if e > 1 else (t.stride(0) if b > 1 else R * C)
+
+
+def _unit_rows_into(master, grad, fast_view):
+    """master + grad -> (new master, unit rows written into fast_view)."""
+    L.require_device(master, grad, fast_view)
+    assert master.dtype == torch.float32 and master.is_contiguous(), "masters must be contiguous fp32"
+    assert grad.shape == master.shape and fast_view.shape == master.shape, "shape mismatch"
+    assert fast_view.dtype == torch.bfloat16
+    b, e, R, C = master.shape
+    out = torch.empty_like(master)
+    L.call("uttt_write_unit_rows", L.ptr(master), R * C, L.ptr(grad), L.dtype_code(grad.dtype),
+           _group_stride(grad, "grad"), b * e, R, C, L.ptr(out), R * C, L.ptr(fast_view),
+           _group_stride(fast_view, "fast"), L.stream_of(master))
+    return out
+
+
+def apply_raw_update(raw_grads, masterw, *, inter_dim, use_muon=False):
+    """NVS write, apply_raw_update (uttt_nvs/models/uttt_moe_block.py:665-714),
+    with self.inter_dim and self.use_muon as keyword arguments.
+
+    raw_grads: (dw0_w2 [b,e,2I,D], dw1 [b,e,D,I]) packed, or (dw0, dw1, dw2);
+    fp32 (or bf16) gradients, summed over writers, with the step size already
+    in them.  masterw: (w0, w1, w2) fp32 masters.  No momentum and no
+    norm-preserving projection: master' = master + step (step = the gradient,
+    or its Newton-Schulz orthogonalisation per expert matrix when use_muon),
+    and the fast weights are bf16 unit rows of master' (F.normalize over the
+    last dim, clamped at 1e-5).  Returns (new_fastw, new_masterw):
+    new_fastw = (fast0_w2 [b,e,2I,D], fast1) for packed gradients (the
+    reference's torch.cat, written in place here), else three matrices."""
+    w0, w1, w2 = masterw
+    if len(raw_grads) == 2:
+        dw0_w2, dw1 = raw_grads
+        b, e, two_i, D = dw0_w2.shape
+        assert two_i == 2 * inter_dim, "dw0_w2 must hold 2 * inter_dim rows"
+        if use_muon:                               # uttt_moe_block.py:674-678, w0 and w2 apart
+            dw0_w2 = newton_schulz5(dw0_w2.contiguous().reshape(b * e * 2, inter_dim, D)
+                                    ).reshape(b, e, two_i, D)
+            dw1 = newton_schulz5(dw1.contiguous().reshape(b * e, *dw1.shape[2:])
+                                 ).reshape(dw1.shape)
+        fast02 = torch.empty((b, e, two_i, D), dtype=torch.bfloat16, device=w0.device)
+        fast1 = torch.empty(w1.shape, dtype=torch.bfloat16, device=w1.device)
+        m0 = _unit_rows_into(w0, dw0_w2[:, :, :inter_dim], fast02[:, :, :inter_dim])
+        m2 = _unit_rows_into(w2, dw0_w2[:, :, inter_dim:], fast02[:, :, inter_dim:])
+        m1 = _unit_rows_into(w1, dw1.contiguous(), fast1)
+        return (fast02, fast1), (m0, m1, m2)
+    if len(raw_grads) != 3:
+        raise ValueError("raw_grads must be (dw0_w2, dw1) or (dw0, dw1, dw2)")
+    fast, master = [], []
+    for g, w in zip(raw_grads, masterw):
+        g = g.contiguous()
+        if use_muon:                               # uttt_moe_block.py:697-701
+            g = newton_schulz5(g.reshape(-1, *g.shape[2:])).reshape(g.shape)
+        f = torch.empty(w.shape, dtype=torch.bfloat16, device=w.device)
+        master.append(_unit_rows_into(w, g, f))
+        fast.append(f)
+    return tuple(fast), tuple(master)
