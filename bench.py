@@ -467,10 +467,10 @@ class MoeSweep:
     # ---------------------------------------------------------- accounting --
     def apply_symbols(self):
         """Kernel symbols of the APPLY's gate/up and down projection (the
-        MFMA-skipping variant when experts average under 256 rows)."""
-        skip = "true" if self.N < 256 * self.E else "false"
-        return (f"tn_kernel<0, EpiSwiGLU, {skip}>",
-                f"tn_kernel<0, EpiStore<unsigned short>, {skip}>")
+        skinny-tile kernel when experts average under 256 rows)."""
+        if self.N < 256 * self.E:
+            return ("apply_kernel<ApSwiGLU, true>", "apply_kernel<ApStore, false>")
+        return ("tn_kernel<0, EpiSwiGLU, false>", "tn_kernel<0, EpiStore<unsigned short>, false>")
 
     def launch_table(self, layers, chunks, batched):
         """Every kernel launch of one sweep that carries GEMM work, grouped by
@@ -482,7 +482,6 @@ class MoeSweep:
         Nu = self.N * (layers if batched else 1)
         n_apply = layers * chunks
         n_upd = (chunks - 1) * (1 if batched else layers)
-        skip_a = "true" if Na < 256 * E else "false"
         skip_u = "true" if Nu < 256 * E else "false"
         w_bytes = 2 * 3 * E * I * D
         tab = {}
@@ -493,10 +492,9 @@ class MoeSweep:
             t[1] += bytes_ * n
             t[2] += n
 
-        add(f"tn_kernel<0, EpiSwiGLU, {skip_a}>", 4, Na, n_apply,
-            2 * (E * 2 * I * D + Na * D + Na * I))
-        add(f"tn_kernel<0, EpiStore<unsigned short>, {skip_a}>", 2, Na, n_apply,
-            2 * (E * D * I + Na * I + Na * D))
+        gate_sym, down_sym = self.apply_symbols()
+        add(gate_sym, 4, Na, n_apply, 2 * (E * 2 * I * D + Na * D + Na * I))
+        add(down_sym, 2, Na, n_apply, 2 * (E * D * I + Na * I + Na * D))
         add("tn_kernel<1, EpiStore<float>, false>", 2, Nu, n_upd,
             2 * E * D * I + 2 * Nu * D + 4 * Nu * I)
         add("tn_kernel<0, EpiS1<BF16T>, false>", 4, Nu, n_upd,

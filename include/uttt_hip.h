@@ -362,6 +362,14 @@ int uttt_rows_silu_l2norm(const void* in, int dtype, int64_t rows, int D, int64_
  * to run small problems down the path the large ones take. */
 long long uttt_debug_set_supertile_min_tiles(long long min_tiles);
 
+/* Test hook: which kernel runs the weight-streaming APPLY products
+ * (uttt_grouped_gate_up with token_major, uttt_grouped_gemm_nt): -1 by the
+ * sizes (the skinny-tile three-stage kernel when N < 256 * E), 0 the general
+ * tiles, 1 the skinny tiles (128-row down-projection tiles), 2 the skinny
+ * tiles with 256-row down-projection tiles.  Results are identical on every
+ * path.  Returns the previous value. */
+int uttt_debug_set_apply_path(int path);
+
 /* WRITE step of the fast weights.  Replaces the write of
  * _apply_moe_update_dense (uttt_llm/flame/custom_models/uttt_moe/
  * modeling_recurrent_lact.py:754-825; seg = C, norm_from_fast = 0,

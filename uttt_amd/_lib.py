@@ -102,6 +102,7 @@ SIGNATURES = {
     "uttt_rows_silu_l2norm": (c_int, [c_p, c_int, c_i64, c_int, c_i64, c_int, c_int, c_p, c_i64,
                                       c_p]),
     "uttt_debug_set_supertile_min_tiles": (ctypes.c_longlong, [ctypes.c_longlong]),
+    "uttt_debug_set_apply_path": (c_int, [c_int]),
     "uttt_grouped_gemm_nt2": (c_int, [c_p, c_p, c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int,
                                       c_p, c_p]),
     "uttt_grouped_gemm_tn2": (c_int, [c_p, c_p, c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int,

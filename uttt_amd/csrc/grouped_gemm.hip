@@ -688,6 +688,245 @@ __global__ __launch_bounds__(kThreads) void tn_kernel(TnArgs a, typename Epi::Ar
   Epi::apply(ea, acc0, acc1, c, two);
 }
 
+// ==================================================== APPLY: skinny tiles ==
+// The per-layer APPLY routes a few thousand rows over the experts, most of
+// them few rows each under a skewed router, so its products stream every
+// expert's weights once per token tile with little arithmetic per byte: they
+// are bound by the bytes each CU keeps in flight.  tn_kernel keeps one 64 KiB
+// stage in flight, half of it the token tile that is mostly clamped
+// duplicates here.  This variant pairs the 256-row weight tile (A0 | A1 as in
+// tn_kernel; A0 alone when !TWO) with 128-token tiles in a three-stage ring of
+// 48 KiB stages, so two stages (96 KiB) are in flight while one is
+// multiplied.  Wave w owns rows [32 w, 32 w + 32) of A0 and A1 and all four
+// 32-column token blocks; the blocks past the segment end are not multiplied
+// (JN blocks, the same for every wave).  Token rows past the segment are
+// clamped copies of its last row (TileLoader), so no stale LDS data reaches
+// any product.  The accumulation runs in the same k order with the same MFMA
+// as tn_kernel, so both give identical results.
+// Tile order: XCD x runs tiles [x * per_xcd, (x + 1) * per_xcd) of the
+// (batch, m-tile, token tile) order, token tile fastest: the token tiles of
+// one expert and m-tile run together on one XCD and share the weight slice
+// through its L2.
+constexpr int kApTok = 128;
+constexpr int kApStageBytes = 3 * kTileBytes;  // A0 | A1 | X: 48 KiB, three of them
+
+struct ApArgs {
+  const uint16_t* a;  // weights of (b, e) at a + (b * E + e) * a_group, K-major rows
+  const uint16_t* x;  // tokens [B, N, K]
+  int64_t lda, a_group;
+  int K;
+  int row_off1;       // A1 row of tile row r: m0 + row_off1 + r
+  int row_end0, row_end1;
+  int m_step, m_tiles, n_tiles_ub;
+  int64_t tiles, per_xcd;
+  int B, E, N;
+  const int32_t* gs;
+};
+
+// Per-wave accumulators: acc[t][j] = rows [32 w, 32 w + 32) of tile t x token block j.
+struct ApCtx {
+  int b, m0, w;
+  TokenTile tt;
+};
+
+// APPLY gate/up: h = y2 * silu(y0), token-major [B, N, I] (EpiSwiGLU's formula)
+struct ApSwiGLU {
+  struct Args {
+    uint16_t* out;
+    int I, N;
+  };
+  template <bool TWO>
+  __device__ __forceinline__ static void apply(const Args& ea, const f32x16 (&acc)[2][4],
+                                               const ApCtx& c) {
+    static_assert(TWO, "gate/up pairs the w0 and w2 tiles");
+    uint16_t* hb = ea.out + (int64_t)c.b * ea.N * ea.I;
+    static_for<16>([&](auto idx) __attribute__((always_inline)) {
+      constexpr int j = idx / 4, q = idx % 4;
+      const int n = j * 32 + acc_col();
+      const int m = c.m0 + c.w * 32 + acc_row(q * 4);
+      if (c.tt.n0 + n >= c.tt.size || m >= ea.I) return;
+      float h[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float y0 = acc[0][j][q * 4 + u], y2 = acc[1][j][q * 4 + u];
+        h[u] = y2 * (y0 * sigmoidf_(y0));
+      }
+      store4(hb, ea.I, c.tt.start + c.tt.n0 + n, m, h[0], h[1], h[2], h[3]);
+    });
+  }
+};
+
+// Plain bf16 store of the tiles (both when TWO), token-major [B, N, ld]:
+// tile t row r is column m0 + t * 128 + r, stored while below col_end.
+struct ApStore {
+  struct Args {
+    uint16_t* out;
+    int64_t ld;
+    int col_end, N;
+  };
+  template <bool TWO>
+  __device__ __forceinline__ static void apply(const Args& ea, const f32x16 (&acc)[2][4],
+                                               const ApCtx& c) {
+    uint16_t* ob = ea.out + (int64_t)c.b * ea.N * ea.ld;
+    static_for<(TWO ? 2 : 1) * 16>([&](auto idx) __attribute__((always_inline)) {
+      constexpr int t = idx / 16, j = (idx / 4) % 4, q = idx % 4;
+      const int n = j * 32 + acc_col();
+      const int col = c.m0 + t * kTileRows + c.w * 32 + acc_row(q * 4);
+      if (c.tt.n0 + n >= c.tt.size || col >= ea.col_end) return;
+      store4(ob, ea.ld, c.tt.start + c.tt.n0 + n, col, acc[t][j][q * 4], acc[t][j][q * 4 + 1],
+             acc[t][j][q * 4 + 2], acc[t][j][q * 4 + 3]);
+    });
+  }
+};
+
+struct ApFrags {
+  bf16x8 a[2], b[4];
+};
+
+// s_waitcnt lgkmcnt(N) that redefines the fragment registers (no MFMA that
+// reads them can move above it).
+template <int N>
+__device__ __forceinline__ void ap_lgkm_wait(ApFrags& f) {
+  i32x4 r[6] = {__builtin_bit_cast(i32x4, f.a[0]), __builtin_bit_cast(i32x4, f.a[1]),
+                __builtin_bit_cast(i32x4, f.b[0]), __builtin_bit_cast(i32x4, f.b[1]),
+                __builtin_bit_cast(i32x4, f.b[2]), __builtin_bit_cast(i32x4, f.b[3])};
+  asm volatile("s_waitcnt lgkmcnt(%6)"
+               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5])
+               : "i"(N)
+               : "memory");
+  f.a[0] = __builtin_bit_cast(bf16x8, r[0]);
+  f.a[1] = __builtin_bit_cast(bf16x8, r[1]);
+  f.b[0] = __builtin_bit_cast(bf16x8, r[2]);
+  f.b[1] = __builtin_bit_cast(bf16x8, r[3]);
+  f.b[2] = __builtin_bit_cast(bf16x8, r[4]);
+  f.b[3] = __builtin_bit_cast(bf16x8, r[5]);
+}
+
+// Fragment reads of k-substep KS of the stage at LDS byte address s: A rows
+// of this wave (A1 when TWO) and the JN token blocks.  LDS ops: TWO + 1 + JN.
+template <bool TWO, int JN, int KS>
+__device__ __forceinline__ void ap_read(ApFrags& f, uint32_t s, uint32_t a_lane) {
+  constexpr int kRow = kChunks * 16;
+  const uint32_t l = s + kmaj_lane<KS>();
+  f.a[0] = ds_b128_asm<0>(l + a_lane);
+  if constexpr (TWO) f.a[1] = ds_b128_asm<kTileBytes>(l + a_lane);
+  static_for<JN>([&](auto J) __attribute__((always_inline)) {
+    f.b[J] = ds_b128_asm<2 * kTileBytes + decltype(J)::value * 32 * kRow>(l);
+  });
+}
+
+template <bool TWO, int JN>
+__device__ __forceinline__ void ap_mma(f32x16 (&acc)[2][4], const ApFrags& f) {
+  static_for<JN>([&](auto J) __attribute__((always_inline)) {
+    constexpr int j = J;
+    acc[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[0], f.b[j], acc[0][j], 0, 0, 0);
+    if constexpr (TWO)
+      acc[1][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[1], f.b[j], acc[1][j], 0, 0, 0);
+  });
+}
+
+// The K loop.  Step k: wait for stage k's loads (stage k+1's may stay in
+// flight unless it is the masked K tail, which may issue fewer DMAs), barrier
+// (stage k visible to every wave; every wave done reading the buffer of stage
+// k-1), issue stage k+2 into that buffer, then the four k-substeps of stage k
+// with the fragments of substep s+1 read while substep s multiplies.
+template <bool TWO, int JN>
+__device__ __forceinline__ void ap_loop(TileLoader<KMajor>& la0, TileLoader<KMajor>& la1,
+                                        TileLoader<KMajor>& lx, int nk, uint8_t* ring,
+                                        f32x16 (&acc)[2][4]) {
+  constexpr int kLPS = (TWO ? 3 : 2) * kLoadsPerTile;
+  constexpr int kOps = (TWO ? 2 : 1) + JN;
+  auto issue_stage = [&](int k, uint8_t* st) __attribute__((always_inline)) {
+    const uint8_t* s0 = la0.step_base(k);
+    const uint8_t* s1 = la1.step_base(k);
+    const uint8_t* sx = lx.step_base(k);
+    if (la0.tail(k)) {
+      static_for<kLoadsPerTile>([&](auto T) __attribute__((always_inline)) {
+        la0.template issue<true>(s0, k, T, st);
+        if constexpr (TWO) la1.template issue<true>(s1, k, T, st + kTileBytes);
+        lx.template issue<true>(sx, k, T, st + 2 * kTileBytes);
+      });
+    } else {
+      static_for<kLoadsPerTile>([&](auto T) __attribute__((always_inline)) {
+        la0.template issue<false>(s0, k, T, st);
+        if constexpr (TWO) la1.template issue<false>(s1, k, T, st + kTileBytes);
+        lx.template issue<false>(sx, k, T, st + 2 * kTileBytes);
+      });
+    }
+  };
+  const uint32_t a_lane = (uint32_t)(wave_id() * 32 * kChunks * 16);
+  uint8_t* p0 = ring;
+  uint8_t* p1 = ring + kApStageBytes;
+  uint8_t* p2 = ring + 2 * kApStageBytes;
+  issue_stage(0, p0);
+  if (nk > 1) issue_stage(1, p1);
+  ApFrags f[2];
+  for (int k = 0; k < nk; ++k) {
+    if (k + 1 < nk && !la0.tail(k + 1))
+      wait_vmcnt<kLPS>();
+    else
+      wait_vmcnt<0>();
+    block_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    if (k + 2 < nk) issue_stage(k + 2, p2);
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t s = lds_addr(p0);
+    ap_read<TWO, JN, 0>(f[0], s, a_lane);
+    static_for<kSubsteps>([&](auto KS) __attribute__((always_inline)) {
+      constexpr int ks = KS;
+      if constexpr (ks + 1 < kSubsteps) {
+        ap_read<TWO, JN, ks + 1>(f[(ks + 1) & 1], s, a_lane);
+        ap_lgkm_wait<kOps>(f[ks & 1]);
+      } else {
+        ap_lgkm_wait<0>(f[ks & 1]);
+      }
+      ap_mma<TWO, JN>(acc, f[ks & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    uint8_t* t = p0;
+    p0 = p1;
+    p1 = p2;
+    p2 = t;
+  }
+}
+
+template <class Epi, bool TWO>
+__global__ __launch_bounds__(kThreads) void apply_kernel(ApArgs a, typename Epi::Args ea) {
+  __shared__ __attribute__((aligned(16))) uint8_t ring[3 * kApStageBytes];
+  // the tile lookup's 4 ints live in the third stage, loaded last
+  int* scratch = reinterpret_cast<int*>(ring + 2 * kApStageBytes);
+  const int bid = blockIdx.x;
+  const int64_t t = (int64_t)(bid % kXcds) * a.per_xcd + bid / kXcds;
+  if (t >= a.tiles) return;
+  const int nt = (int)(t % a.n_tiles_ub);
+  const int64_t rest = t / a.n_tiles_ub;
+  const int mt = (int)(rest % a.m_tiles), b = (int)(rest / a.m_tiles);
+  const TokenTile tt = find_token_tile<kApTok>(a.gs + (int64_t)b * a.E, a.E, a.N, nt, scratch);
+  __syncthreads();  // every wave has read the lookup before the third stage is loaded
+  if (tt.e < 0) return;
+  const int m0 = mt * a.m_step;
+  const int64_t ag = ((int64_t)b * a.E + tt.e) * a.a_group;
+  const Operand A0{a.a + ag, a.lda, a.row_end0, a.K};
+  const Operand A1{a.a + ag, a.lda, a.row_end1, a.K};
+  const Operand X{a.x + ((int64_t)b * a.N + tt.start) * a.K, a.K, tt.size, a.K};
+  TileLoader<KMajor> la0, la1, lx;
+  la0.init(A0, m0);
+  la1.init(A1, m0 + a.row_off1);
+  lx.init(X, tt.n0);
+  const int nk = (a.K + kBK - 1) / kBK;
+  f32x16 acc[2][4];
+  zero(acc);
+  const int valid = tt.size - tt.n0;  // >= 1
+  const int jn = valid >= 3 * 32 + 1 ? 4 : (valid + 31) / 32;
+  if (jn == 4) ap_loop<TWO, 4>(la0, la1, lx, nk, ring, acc);
+  else if (jn == 3) ap_loop<TWO, 3>(la0, la1, lx, nk, ring, acc);
+  else if (jn == 2) ap_loop<TWO, 2>(la0, la1, lx, nk, ring, acc);
+  else ap_loop<TWO, 1>(la0, la1, lx, nk, ring, acc);
+  const TokenTile tte{tt.e, after_loop(tt.start), after_loop(tt.size), after_loop(tt.n0)};
+  const ApCtx c{after_loop(b), after_loop(m0), after_loop((int)(threadIdx.x >> 6)), tte};
+  Epi::template apply<TWO>(ea, acc, c);
+}
+
 // ======================================================= weight gradients ==
 // out[b, e, x, y] = sum_{n in seg(b,e)} P[b, n, y] Q[b, n, x]; P [B, N, Y] and
 // Q [B, N, X] token-major.  A tile = 2 x 128 rows of y, B tile = 256 rows of
@@ -1078,6 +1317,53 @@ int launch_tn(TnArgs t, const typename Epi::Args& ea, int B, hipStream_t st,
   return check_launch(what);
 }
 
+// APPLY path: 0 = tn_kernel, 1 = apply_kernel, -1 = by the sizes (apply_kernel
+// when the experts average under 256 routed rows, as the per-layer APPLY does).
+// Both give identical results; a process-wide value so that tests can run
+// either path (uttt_debug_set_apply_path).
+int g_apply_path = -1;
+bool g_apply_down_two = false;  // down products on 256-row tiles (default 128: twice the tiles)
+
+bool use_apply_kernel(int64_t N, int E) {
+  return g_apply_path == 1 || (g_apply_path < 0 && N < (int64_t)kBRows * E);
+}
+
+template <class Epi, bool TWO>
+int launch_apply(ApArgs a, int M_rows, const typename Epi::Args& ea, hipStream_t st,
+                 const char* what) {
+  a.m_tiles = (M_rows + a.m_step - 1) / a.m_step;
+  a.n_tiles_ub = (a.N + kApTok - 1) / kApTok + a.E;
+  a.tiles = (int64_t)a.B * a.m_tiles * a.n_tiles_ub;
+  if (a.tiles == 0) return UTTT_OK;
+  a.per_xcd = (a.tiles + kXcds - 1) / kXcds;
+  const int64_t blocks = a.per_xcd * kXcds;
+  if (int rc = check_grid(blocks, what)) return rc;
+  hipLaunchKernelGGL((apply_kernel<Epi, TWO>), dim3((unsigned)blocks), dim3(kThreads), 0, st, a,
+                     ea);
+  return check_launch(what);
+}
+
+// The weight-streaming APPLY products on apply_kernel: w [B, E, M, K] K-major,
+// x [B, N, K]; A1 rows at row_off1 (TWO).
+ApArgs apply_args(const void* w, const void* x, int K, int64_t a_group, int row_off1, int end0,
+                  int end1, int m_step, int B, int E, int N, const int32_t* gs) {
+  ApArgs a{};
+  a.a = static_cast<const uint16_t*>(w);
+  a.x = static_cast<const uint16_t*>(x);
+  a.lda = K;
+  a.a_group = a_group;
+  a.K = K;
+  a.row_off1 = row_off1;
+  a.row_end0 = end0;
+  a.row_end1 = end1;
+  a.m_step = m_step;
+  a.B = B;
+  a.E = E;
+  a.N = N;
+  a.gs = gs;
+  return a;
+}
+
 // Wide single product: y[b, n, m] = sum_k A(m, k) x[b, n, k] with M rows in
 // m-tiles of 256 (tile 1 = rows +128).  Optional second pair chained on K.
 template <int AMAJ, class OutT>
@@ -1193,6 +1479,12 @@ extern "C" int uttt_grouped_gate_up(const void* w0_w2, const void* x, const int3
   UTTT_REQUIRE(w0_w2 && x && group_sizes && hidden, "grouped_gate_up: null pointer");
   UTTT_REQUIRE(aligned16(w0_w2) && aligned16(x) && aligned16(hidden),
                "grouped_gate_up: tensors must be 16-byte aligned");
+  if (token_major && use_apply_kernel(N, E)) {
+    const ApArgs a = apply_args(w0_w2, x, D, (int64_t)2 * I * D, I, I, 2 * I, kTileRows, B, E, N,
+                                group_sizes);
+    const ApSwiGLU::Args ea{static_cast<uint16_t*>(hidden), I, N};
+    return launch_apply<ApSwiGLU, true>(a, I, ea, as_stream(stream), "grouped_gate_up");
+  }
   const TnArgs t = tn_args(w0_w2, w0_w2, x, D, D, (int64_t)2 * I * D, 0, I, I, 2 * I, kTileRows,
                            I, B, E, N, group_sizes);
   const EpiSwiGLU::Args ea{static_cast<uint16_t*>(hidden), I, N, token_major};
@@ -1207,6 +1499,17 @@ extern "C" int uttt_grouped_gemm_nt(const void* w, const void* x, const int32_t*
   UTTT_REQUIRE(w && x && group_sizes && y, "grouped_gemm_nt: null pointer");
   UTTT_REQUIRE(aligned16(w) && aligned16(x) && aligned16(y),
                "grouped_gemm_nt: tensors must be 16-byte aligned");
+  if (use_apply_kernel(N, E)) {
+    const ApStore::Args ea{static_cast<uint16_t*>(y), M, M, N};
+    if (g_apply_down_two) {
+      const ApArgs a = apply_args(w, x, K, (int64_t)M * K, kTileRows, M, M, 2 * kTileRows, B, E, N,
+                                  group_sizes);
+      return launch_apply<ApStore, true>(a, M, ea, as_stream(stream), "grouped_gemm_nt");
+    }
+    const ApArgs a = apply_args(w, x, K, (int64_t)M * K, kTileRows, M, M, kTileRows, B, E, N,
+                                group_sizes);
+    return launch_apply<ApStore, false>(a, M, ea, as_stream(stream), "grouped_gemm_nt");
+  }
   return launch_wide<KMajor>(w, x, K, nullptr, nullptr, 0, M, K, (int64_t)M * K,
                              static_cast<uint16_t*>(y), B, E, N, group_sizes, as_stream(stream),
                              "grouped_gemm_nt");
@@ -1251,6 +1554,13 @@ extern "C" int uttt_grouped_gemm_tn2(const void* wa, const void* xa, const void*
   return launch_wide<RMajor>(wa, xa, K, wb, xb, K, M, M, (int64_t)M * K,
                              static_cast<uint16_t*>(y), B, E, N, group_sizes, as_stream(stream),
                              "grouped_gemm_tn2");
+}
+
+extern "C" int uttt_debug_set_apply_path(int path) {
+  const int prev = g_apply_path;
+  g_apply_path = path < 0 ? -1 : path > 0 ? 1 : 0;
+  g_apply_down_two = path == 2;
+  return prev;
 }
 
 extern "C" long long uttt_debug_set_supertile_min_tiles(long long min_tiles) {
