@@ -704,9 +704,11 @@ __global__ __launch_bounds__(kThreads) void tn_kernel(TnArgs a, typename Epi::Ar
 // any product.  The accumulation runs in the same k order with the same MFMA
 // as tn_kernel, so both give identical results.
 // Tile order: XCD x runs tiles [x * per_xcd, (x + 1) * per_xcd) of the
-// (batch, m-tile, token tile) order, token tile fastest: the token tiles of
-// one expert and m-tile run together on one XCD and share the weight slice
-// through its L2.
+// (batch, m-tile, token tile) upper-bound order, token tile fastest: the
+// token tiles of one expert and m-tile run together on one XCD and share the
+// weight slice through its L2.  The down projection of one batch (em) instead
+// cuts the real (token tile, m-tile) pairs into 8 equal XCD ranges in
+// expert-major order (see apply_kernel).
 constexpr int kApTok = 128;
 constexpr int kApStageBytes = 3 * kTileBytes;  // A0 | A1 | X: 48 KiB, three of them
 
@@ -720,6 +722,7 @@ struct ApArgs {
   int m_step, m_tiles, n_tiles_ub;
   int64_t tiles, per_xcd;
   int B, E, N;
+  int em;             // one batch: expert-major order over the real pairs (else upper-bound order)
   const int32_t* gs;
 };
 
@@ -896,12 +899,33 @@ __global__ __launch_bounds__(kThreads) void apply_kernel(ApArgs a, typename Epi:
   // the tile lookup's 4 ints live in the third stage, loaded last
   int* scratch = reinterpret_cast<int*>(ring + 2 * kApStageBytes);
   const int bid = blockIdx.x;
-  const int64_t t = (int64_t)(bid % kXcds) * a.per_xcd + bid / kXcds;
-  if (t >= a.tiles) return;
-  const int nt = (int)(t % a.n_tiles_ub);
-  const int64_t rest = t / a.n_tiles_ub;
-  const int mt = (int)(rest % a.m_tiles), b = (int)(rest / a.m_tiles);
-  const TokenTile tt = find_token_tile<kApTok>(a.gs + (int64_t)b * a.E, a.E, a.N, nt, scratch);
+  int mt, b;
+  TokenTile tt;
+  if (a.em) {
+    // One batch: the real pair count R * m_tiles is known on the device, so
+    // the pairs are cut into 8 equal XCD ranges in expert-major order (token
+    // tile fastest inside an expert): an XCD streams each of its experts'
+    // weight slices once and reuses it from L2 for that expert's token tiles,
+    // and reads a small expert's tokens once for all its m-tiles.  Workgroups
+    // past their XCD's range leave at once.
+    const int R = count_token_tiles<kApTok>(a.gs, a.E, a.N, scratch);
+    const int64_t total = (int64_t)R * a.m_tiles;
+    const int64_t per = (total + kXcds - 1) / kXcds;
+    const int64_t loc = bid / kXcds;
+    const int64_t t = (int64_t)(bid % kXcds) * per + loc;
+    if (loc >= per || t >= total) return;  // uniform over the workgroup
+    __syncthreads();                        // the count is read before the scratch is reused
+    tt = find_pair_em<kApTok>(a.gs, a.E, a.N, t, a.m_tiles, &mt, scratch);
+    b = 0;
+  } else {
+    const int64_t t = (int64_t)(bid % kXcds) * a.per_xcd + bid / kXcds;
+    if (t >= a.tiles) return;
+    const int nt = (int)(t % a.n_tiles_ub);
+    const int64_t rest = t / a.n_tiles_ub;
+    mt = (int)(rest % a.m_tiles);
+    b = (int)(rest / a.m_tiles);
+    tt = find_token_tile<kApTok>(a.gs + (int64_t)b * a.E, a.E, a.N, nt, scratch);
+  }
   __syncthreads();  // every wave has read the lookup before the third stage is loaded
   if (tt.e < 0) return;
   const int m0 = mt * a.m_step;
@@ -1335,6 +1359,9 @@ int launch_apply(ApArgs a, int M_rows, const typename Epi::Args& ea, hipStream_t
   a.n_tiles_ub = (a.N + kApTok - 1) / kApTok + a.E;
   a.tiles = (int64_t)a.B * a.m_tiles * a.n_tiles_ub;
   if (a.tiles == 0) return UTTT_OK;
+  // the expert-major order measured 5% faster for the down projection and 4%
+  // slower for gate/up (whose 256-row weight tiles are read by more m-tiles)
+  a.em = a.B == 1 && std::is_same_v<Epi, ApStore>;
   a.per_xcd = (a.tiles + kXcds - 1) / kXcds;
   const int64_t blocks = a.per_xcd * kXcds;
   if (int rc = check_grid(blocks, what)) return rc;
