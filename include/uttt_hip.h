@@ -61,27 +61,30 @@ size_t uttt_router_workspace_bytes(int B, int T, int E, int D);
  * 0 selected_prob, 1 topk_renorm; router_scale <= 0 means sqrt(E).
  * Outputs (contiguous): mask [B,E,T] uint8 0/1 (torch.bool), group_sizes
  * [B,E] int32 (optional), combine and balance [B,E,T] fp32, lb_loss fp32
- * scalar (optional).  Top-k picks the lower expert index among equal scores.
- * E <= 128, 1 <= topk <= E. */
+ * scalar (optional; its kernel is skipped when NULL), balance_sum [B,E] fp32
+ * = sum over t of balance (optional: the sums of _make_lb_info,
+ * M/modeling_recurrent_lact.py:171-176, added in a fixed order).  Top-k picks
+ * the lower expert index among equal scores.  E <= 128, 1 <= topk <= E. */
 int uttt_router_select(const float* logits, int64_t l_sb, int64_t l_se, int64_t l_st,
                        const float* bias, int64_t bias_sb, int B, int E, int T, int topk,
                        int router_type, int combine_mode, float alpha, float router_scale,
                        float norm_eps, void* mask, int32_t* group_sizes, float* combine,
-                       float* balance, float* lb_loss, void* workspace, size_t workspace_bytes,
-                       void* stream);
+                       float* balance, float* lb_loss, float* balance_sum, void* workspace,
+                       size_t workspace_bytes, void* stream);
 
 /* Replaces FastWeightMLPSubNN._route_tokens (M/modeling_recurrent_lact.py:147-169):
  * logits[b,e,t] = sum_d router_w[b,e,d] x[b,t,d] in fp32 (x [B,T,D]
  * contiguous of x_dtype, router_w fp32 [E,D] with batch stride w_sb, 0 =
  * shared), then the selection of uttt_router_select (D is cut into slices
  * summed in a fixed order when the token tiles alone would not fill the
- * chip).  logits_out: optional fp32 [B,E,T]. */
+ * chip).  logits_out: optional fp32 [B,E,T]; lb_loss and balance_sum as in
+ * uttt_router_select. */
 int uttt_route_tokens(const void* x, int x_dtype, const float* router_w, int64_t w_sb, int B,
                       int T, int D, int E, const float* bias, int64_t bias_sb, int topk,
                       int router_type, int combine_mode, float alpha, float router_scale,
                       float norm_eps, float* logits_out, void* mask, int32_t* group_sizes,
-                      float* combine, float* balance, float* lb_loss, void* workspace,
-                      size_t workspace_bytes, void* stream);
+                      float* combine, float* balance, float* lb_loss, float* balance_sum,
+                      void* workspace, size_t workspace_bytes, void* stream);
 
 /* Loss-free balancing counts.  Replaces _store_loss_free_counts with
  * _loss_free_counts_for_scope (M/modeling_recurrent_lact.py:1646-1654,

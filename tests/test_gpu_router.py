@@ -108,6 +108,16 @@ def test_route_tokens_fused(dtype, D, E, T):
     if diff.any():
         top = (ref_lg + bias).topk(k + 1, dim=1).values
         assert ((top[:, k - 1] - top[:, k])[diff].abs() < 1e-4 * scale).all()
+    _check_balance_sums(x, Rw, k, bias, mask, bal)
+
+
+def _check_balance_sums(x, Rw, k, bias, mask, bal, **kw):
+    """route_tokens_lb: the same routing plus the per-expert balance sums
+    (the router's fixed-order reductions against torch's sum)."""
+    m2, _, _, bal2, bsum = RT.route_tokens_lb(x.to(DEV), Rw.to(DEV), k, routing_bias=bias.to(DEV),
+                                              combine_mode="topk_renorm", **kw)
+    assert torch.equal(m2, mask) and torch.equal(bal2, bal)
+    torch.testing.assert_close(bsum.cpu(), bal.cpu().sum(-1), rtol=1e-5, atol=1e-5)
 
 
 @pytest.mark.parametrize("B,T,D,E,k,dtype", [
@@ -132,6 +142,7 @@ def test_route_tokens_few_tokens(B, T, D, E, k, dtype, rt):
     ref_lg = OR.router_logits(x, Rw)
     scale = Rw.norm(dim=1).max().item() * x.float().norm(dim=-1).max().item()
     assert (lg.cpu().double() - ref_lg).abs().max().item() < 1e-4 * scale
+    _check_balance_sums(x, Rw, k, bias, mask, bal, router_type=rt)
     own = lg.cpu()
     ref = OR.create_router_mask_sizes_probs(own, k, router_type=rt, routing_bias=bias,
                                             combine_mode="topk_renorm")

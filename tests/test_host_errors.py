@@ -76,10 +76,10 @@ def test_new_entry_points_reject_bad_arguments_without_launch():
     assert lib.uttt_momentum_add(p, 2, p, p, 1, 16, p, None) == -1
     assert b"fp32 or bf16" in lib.uttt_last_error()
     rc = lib.uttt_route_tokens(p, 1, p, 0, 1, 4, 64, 8, None, 0, 9, 0, 0, 1.0, 0.0, 1e-6, None,
-                               p, p, p, p, p, p, 1 << 20, None)
+                               p, p, p, p, p, None, p, 1 << 20, None)
     assert rc == -1 and b"topk" in lib.uttt_last_error()
     rc = lib.uttt_route_tokens(p, 1, p, 0, 1, 4, 64, 8, None, 0, 2, 7, 0, 1.0, 0.0, 1e-6, None,
-                               p, p, p, p, p, p, 1 << 20, None)
+                               p, p, p, p, p, None, p, 1 << 20, None)
     assert rc == -1 and b"router_type" in lib.uttt_last_error()
 
 

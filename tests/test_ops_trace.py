@@ -75,3 +75,4 @@ def test_fake_shapes(token_major):
     r = ops.route_tokens(_t(B, T, D), _t(E, D, dtype=torch.float32), 2, 1.0, "softmax",
                          "selected_prob", 0.0, 1e-6, None, False)
     assert r[0].shape == (B, E, T) and r[0].dtype == torch.bool and r[4].numel() == 0
+    assert r[5].shape == (B, E) and r[5].dtype == torch.float32

@@ -117,13 +117,14 @@ SIGNATURES = {
     "uttt_router_select": (
         c_int,
         [c_p, c_i64, c_i64, c_i64, c_p, c_i64, c_int, c_int, c_int, c_int, c_int, c_int,
-         ctypes.c_float, ctypes.c_float, ctypes.c_float, c_p, c_p, c_p, c_p, c_p, c_p, c_sz, c_p],
+         ctypes.c_float, ctypes.c_float, ctypes.c_float, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_sz,
+         c_p],
     ),
     "uttt_route_tokens": (
         c_int,
         [c_p, c_int, c_p, c_i64, c_int, c_int, c_int, c_int, c_p, c_i64, c_int, c_int, c_int,
-         ctypes.c_float, ctypes.c_float, ctypes.c_float, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_sz,
-         c_p],
+         ctypes.c_float, ctypes.c_float, ctypes.c_float, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p,
+         c_sz, c_p],
     ),
     "uttt_write_step": (
         c_int,

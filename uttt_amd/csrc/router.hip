@@ -720,15 +720,16 @@ extern "C" int uttt_router_select(const float* logits, int64_t l_sb, int64_t l_s
                                   int topk, int router_type, int combine_mode, float alpha,
                                   float router_scale, float norm_eps, void* mask,
                                   int32_t* group_sizes, float* combine, float* balance,
-                                  float* lb_loss, void* workspace, size_t workspace_bytes,
-                                  void* stream) {
+                                  float* lb_loss, float* balance_sum, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
   if (int rc = check_select_args(B, E, T, topk, router_type, combine_mode, "router_select"))
     return rc;
   if (B == 0 || T == 0) return UTTT_OK;
   UTTT_REQUIRE(logits && mask && combine && balance, "router_select: null pointer");
-  const Ws w = ws_layout(workspace, B, T, E, sel_tpb(e_bucket(E)));
+  Ws w = ws_layout(workspace, B, T, E, sel_tpb(e_bucket(E)));
   UTTT_REQUIRE(workspace != nullptr && workspace_bytes >= w.bytes,
                "router_select: workspace %zu < %zu bytes", workspace_bytes, w.bytes);
+  if (balance_sum != nullptr) w.bal_sum = balance_sum;
   const SelectArgs a = make_args(w, bias, bias_sb, B, E, T, topk, router_type, combine_mode,
                                  alpha, router_scale, norm_eps, mask, combine, balance,
                                  group_sizes);
@@ -744,16 +745,17 @@ extern "C" int uttt_route_tokens(const void* x, int x_dtype, const float* router
                                  int topk, int router_type, int combine_mode, float alpha,
                                  float router_scale, float norm_eps, float* logits_out,
                                  void* mask, int32_t* group_sizes, float* combine,
-                                 float* balance, float* lb_loss, void* workspace,
-                                 size_t workspace_bytes, void* stream) {
+                                 float* balance, float* lb_loss, float* balance_sum,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
   if (int rc = check_select_args(B, E, T, topk, router_type, combine_mode, "route_tokens"))
     return rc;
   UTTT_REQUIRE(D >= 1, "route_tokens: D=%d", D);
   if (B == 0 || T == 0) return UTTT_OK;
   UTTT_REQUIRE(x && router_w && mask && combine && balance, "route_tokens: null pointer");
-  const Ws w = ws_layout(workspace, B, T, E, 32);
+  Ws w = ws_layout(workspace, B, T, E, 32);
   UTTT_REQUIRE(workspace != nullptr && workspace_bytes >= w.bytes,
                "route_tokens: workspace %zu < %zu bytes", workspace_bytes, w.bytes);
+  if (balance_sum != nullptr) w.bal_sum = balance_sum;
   const SelectArgs a = make_args(w, bias, bias_sb, B, E, T, topk, router_type, combine_mode,
                                  alpha, router_scale, norm_eps, mask, combine, balance,
                                  group_sizes);

@@ -38,7 +38,7 @@ from .lact_moe_triton.lact_fw_grad import grouped_lact_swiglu_ffn_fast_weight_gr
 from .lact_moe_triton.lact_swiglu_ffn import grouped_swiglu_ffn_fwd
 from .lact_moe_triton.triton_permute import (permute_kv_and_lrs, permute_with_expert_mask,
                                              unpermute_and_merge_with_probs)
-from .routing import route_tokens
+from .routing import route_tokens, route_tokens_lb
 
 
 @dataclass(frozen=True)
@@ -124,15 +124,15 @@ def apply_moe_fast_weights_grouped(x, w0, w1, w2, router_proj_weights, cfg: Rout
     seq_len = x.shape[1]
     input_dtype = x.dtype
     xt = reshape_head_tokens(x, num_heads)
-    expert_mask, group_sizes, router_probs, balance_probs = route(
-        xt, router_proj_weights, cfg, routing_bias)
+    expert_mask, group_sizes, router_probs, _, balance_sums = route_tokens_lb(
+        xt, router_proj_weights, cfg.topk, routing_bias=routing_bias, **cfg.kwargs())
     w0_w2 = _w0_w2(w0, w2, precomputed_w0_w2)
     x_perm, _, row_id_map = permute_with_expert_mask(
         xt.to(w0_w2.dtype).contiguous(), expert_mask, router_probs, cfg.topk)
     y_perm = grouped_swiglu_ffn_fwd(w0_w2, w1.contiguous(), x_perm, group_sizes)
     out = unpermute_and_merge_with_probs(y_perm, row_id_map, router_probs)
-    return (merge_head_tokens(out.to(input_dtype), seq_len, num_heads),
-            lb_info(balance_probs, group_sizes))
+    # _make_lb_info (M:171-176): the balance sums come from the router kernel
+    return merge_head_tokens(out.to(input_dtype), seq_len, num_heads), (balance_sums, group_sizes)
 
 
 def rows_silu_l2norm(x: torch.Tensor, silu: bool, l2: bool, rows_of: int | None = None):

@@ -100,7 +100,7 @@ def _select(router_logits: Tensor, topk: int, alpha: float, router_type: str, co
     L.call("uttt_router_select", L.ptr(logits), logits.stride(0), logits.stride(1),
            logits.stride(2), L.ptr(bias), bias_sb, B, E, T, int(topk), ROUTER_TYPES[router_type],
            COMBINE_MODES[combine_mode], float(alpha), float(router_scale), float(norm_eps),
-           L.ptr(mask), L.ptr(gs), L.ptr(comb), L.ptr(bal), L.ptr(lb), L.ptr(ws), nbytes,
+           L.ptr(mask), L.ptr(gs), L.ptr(comb), L.ptr(bal), L.ptr(lb), None, L.ptr(ws), nbytes,
            L.stream_of(logits))
     if router_logits.dtype != torch.float32:
         comb, bal = comb.to(router_logits.dtype), bal.to(router_logits.dtype)
@@ -117,7 +117,20 @@ def route_tokens(x, router_proj_weights, topk, alpha=1.0, use_sigmoid=False,
     _check_modes(use_sigmoid, router_type, combine_mode)
     out = _route(x, router_proj_weights, int(topk), float(alpha), router_type, combine_mode,
                  float(router_scale), float(norm_eps), routing_bias, bool(return_logits))
-    return out if return_logits else out[:4]
+    return out[:5] if return_logits else out[:4]
+
+
+def route_tokens_lb(x, router_proj_weights, topk, alpha=1.0, use_sigmoid=False,
+                    router_type="softmax", combine_mode="selected_prob", router_scale=0.0,
+                    norm_eps=1e-6, routing_bias=None):
+    """route_tokens plus the balance sums over the tokens [B, E] fp32 (the
+    first half of _make_lb_info, M:171-176), added by the router's own
+    reductions in a fixed order: (expert_mask, group_sizes, router_probs,
+    balance_probs, balance_sums)."""
+    _check_modes(use_sigmoid, router_type, combine_mode)
+    out = _route(x, router_proj_weights, int(topk), float(alpha), router_type, combine_mode,
+                 float(router_scale), float(norm_eps), routing_bias, False)
+    return out[:4] + (out[5],)
 
 
 def _route_fake(x, router_proj_weights, topk, alpha, router_type, combine_mode, router_scale,
@@ -127,14 +140,15 @@ def _route_fake(x, router_proj_weights, topk, alpha, router_type, combine_mode, 
     e = x.new_empty
     return (e((B, E, T), dtype=torch.bool), e((B, E), dtype=torch.int32),
             e((B, E, T), dtype=torch.float32), e((B, E, T), dtype=torch.float32),
-            e((B, E, T) if return_logits else (0,), dtype=torch.float32))
+            e((B, E, T) if return_logits else (0,), dtype=torch.float32),
+            e((B, E), dtype=torch.float32))
 
 
 @traced_op("route_tokens", _route_fake)
 def _route(x: Tensor, router_proj_weights: Tensor, topk: int, alpha: float, router_type: str,
            combine_mode: str, router_scale: float, norm_eps: float,
            routing_bias: Optional[Tensor], return_logits: bool
-           ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+           ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
     L.require_device(x, router_proj_weights)
     assert x.dim() == 3, "x must be [B, T, D]"
     B, T, D = x.shape
@@ -149,12 +163,14 @@ def _route(x: Tensor, router_proj_weights: Tensor, topk: int, alpha: float, rout
         w_sb = E * D if R.shape[0] > 1 else 0
     assert R.shape[-1] == D, "router weights must have x's last dimension"
     bias, bias_sb = _bias_arg(routing_bias, B, E, x.device)
-    mask, gs, comb, bal, lb, ws, nbytes = _outputs(B, E, T, D, x.device)
+    mask, gs, comb, bal, _, ws, nbytes = _outputs(B, E, T, D, x.device)
     logits = torch.empty((B, E, T) if return_logits else (0,), dtype=torch.float32,
                          device=x.device)
+    bal_sum = torch.empty((B, E), dtype=torch.float32, device=x.device)
+    # no lb_loss here (_route_tokens returns none): its kernel is skipped
     L.call("uttt_route_tokens", L.ptr(x), L.dtype_code(x.dtype), L.ptr(R), w_sb, B, T, D, E,
            L.ptr(bias), bias_sb, int(topk), ROUTER_TYPES[router_type],
            COMBINE_MODES[combine_mode], float(alpha), float(router_scale), float(norm_eps),
            L.ptr(logits) if return_logits else None, L.ptr(mask), L.ptr(gs), L.ptr(comb),
-           L.ptr(bal), L.ptr(lb), L.ptr(ws), nbytes, L.stream_of(x))
-    return mask, gs, comb, bal, logits
+           L.ptr(bal), None, L.ptr(bal_sum), L.ptr(ws), nbytes, L.stream_of(x))
+    return mask, gs, comb, bal, logits, bal_sum
