@@ -135,6 +135,9 @@ __device__ __forceinline__ int rswz(int k) { return (k & 3) << 2; }
 // step when k_end is not a multiple of kBK) and every step past the last
 // (which the K loop runs to finish its ring, or issues ahead of the end) hold
 // zeros for k >= k_end, through the masked form.
+// Word 3 of a raw buffer descriptor on gfx9 (32-bit data format, no swizzle).
+constexpr int kBufferWord3 = 0x00020000;
+
 template <int MAJOR>
 struct TileLoader {
   const uint8_t* base;    // wave-uniform: byte address of the tile origin at step 0
@@ -143,6 +146,7 @@ struct TileLoader {
   int k_end;
   int nvalid;             // valid rows from the tile origin (KMajor: rows of 8 per load)
   uint32_t off[kLoadsPerTile];
+  int wofs;               // wave-uniform: this wave's LDS byte offset inside a tile
 
   __device__ __forceinline__ void init(const Operand& op, int r0) {
     const int lane = threadIdx.x & 63;
@@ -151,6 +155,10 @@ struct TileLoader {
     last = (op.k_end + kBK - 1) / kBK - 1;
     int nrows = op.r_end - r0;
     nvalid = nrows > 0 ? nrows : 0;
+    // kept in a scalar register for the whole loop (opaque, so not re-derived
+    // from the thread id before every load)
+    wofs = w * 64 * 16;
+    asm volatile("" : "+s"(wofs));
     const uint16_t* org;
     if (nrows > 0) {
       org = MAJOR == KMajor ? op.base + (int64_t)r0 * op.ld : op.base + r0;
@@ -204,13 +212,16 @@ struct TileLoader {
   // waits on vmcnt(0) wherever it would count loads.
   template <bool MASKED, bool SKIP_ROWS = false>
   __device__ __forceinline__ void issue(const uint8_t* sb, int step, int t, uint8_t* dst) const {
-    uint8_t* d = dst + (t * 4 + wave_id()) * 64 * 16;
+    uint8_t* d = dst + t * 4 * 64 * 16 + wofs;
     if constexpr (SKIP_ROWS && !MASKED && MAJOR == KMajor) {
-      if ((t * 4 + wave_id()) * (64 / kChunks) >= nvalid) return;  // wave-uniform
+      if (t * 4 * (64 / kChunks) + (wofs >> 7) >= nvalid) return;  // wave-uniform
     }
     if constexpr (!MASKED) {
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(sb + off[t]), UTTT_LDS(d), 16,
-                                       0, 0);
+      // buffer form: the step's tile origin as a scalar descriptor and the
+      // lane's 32-bit offset, so the address costs no vector instruction
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint8_t*>(sb), (short)0, -1, kBufferWord3);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, UTTT_LDS(d), 16, off[t], 0, 0, 0);
     } else {
       const int lane = threadIdx.x & 63;
       const int s = (t * 4 + wave_id()) * 64 + lane;
@@ -303,7 +314,8 @@ struct HalfFrags {
   bf16x8 b[kNB], a0[2], a1[2];
 };
 
-template <int AMAJ, int BMAJ, int KS, int NB = kNB>
+// ONLY >= 0: fragment ONLY alone (0 .. NB-1: B blocks, then a0[0], a1[0], a0[1], a1[1]).
+template <int AMAJ, int BMAJ, int KS, int NB = kNB, int ONLY = -1>
 __device__ __forceinline__ void read_half(HalfFrags& f, const uint8_t* st, int wm, int wn) {
   constexpr int kRow = kChunks * 16;  // bytes per KMajor tile row
   const uint32_t s = lds_addr(st);
@@ -311,24 +323,33 @@ __device__ __forceinline__ void read_half(HalfFrags& f, const uint8_t* st, int w
   if constexpr (BMAJ == KMajor) {
     const uint32_t b = sb + kmaj_lane<KS>();
     static_for<NB>([&](auto J) __attribute__((always_inline)) {
-      f.b[J] = frag_at<KMajor, KS, decltype(J)::value * 32 * kRow>(b);
+      if constexpr (ONLY < 0 || ONLY == decltype(J)::value)
+        f.b[J] = frag_at<KMajor, KS, decltype(J)::value * 32 * kRow>(b);
     });
   } else {
     static_for<NB>([&](auto J) __attribute__((always_inline)) {
-      f.b[J] = frag_at<RMajor, KS, 0>(sb + rmaj_lane(decltype(J)::value * 32));
+      if constexpr (ONLY < 0 || ONLY == decltype(J)::value)
+        f.b[J] = frag_at<RMajor, KS, 0>(sb + rmaj_lane(decltype(J)::value * 32));
     });
   }
   if constexpr (AMAJ == KMajor) {
     const uint32_t a = s + wm * 64 * kRow + kmaj_lane<KS>();
     static_for<2>([&](auto I) __attribute__((always_inline)) {
-      f.a0[I] = frag_at<KMajor, KS, decltype(I)::value * 32 * kRow>(a);
-      f.a1[I] = frag_at<KMajor, KS, kTileBytes + decltype(I)::value * 32 * kRow>(a);
+      constexpr int i = decltype(I)::value;
+      if constexpr (ONLY < 0 || ONLY == NB + 2 * i)
+        f.a0[I] = frag_at<KMajor, KS, i * 32 * kRow>(a);
+      if constexpr (ONLY < 0 || ONLY == NB + 2 * i + 1)
+        f.a1[I] = frag_at<KMajor, KS, kTileBytes + i * 32 * kRow>(a);
     });
   } else {
     static_for<2>([&](auto I) __attribute__((always_inline)) {
-      const uint32_t a = s + rmaj_lane(wm * 64 + decltype(I)::value * 32);
-      f.a0[I] = frag_at<RMajor, KS, 0>(a);
-      f.a1[I] = frag_at<RMajor, KS, kTileBytes>(a);
+      constexpr int i = decltype(I)::value;
+      if constexpr (ONLY < 0 || ONLY == NB + 2 * i || ONLY == NB + 2 * i + 1) {
+        const uint32_t a = s + rmaj_lane(wm * 64 + i * 32);
+        if constexpr (ONLY < 0 || ONLY == NB + 2 * i) f.a0[I] = frag_at<RMajor, KS, 0>(a);
+        if constexpr (ONLY < 0 || ONLY == NB + 2 * i + 1)
+          f.a1[I] = frag_at<RMajor, KS, kTileBytes>(a);
+      }
     });
   }
 }
@@ -423,39 +444,70 @@ __device__ __forceinline__ void mma_half(f32x16 (&acc0)[2][kNB], f32x16 (&acc1)[
 
 // The K loop: two LDS stages of kBK = 64 (KMajor operand rows are then whole
 // 128-byte cache lines: an LDS-DMA instruction touches 8 lines instead of 16,
-// which doubles what a CU's L1 can stream from L2); the loads of stage kt+2
-// are issued during the last k-substep of stage kt and have the whole of stage
-// kt+1 to land.
+// which doubles what a CU's L1 can stream from L2).
 //   prep(kt)                 readies the loads of stage kt (operand switch,
 //                            per-stage scalar bases) and returns whether they
 //                            need the masked (K tail) form
 //   issue(p, masked, stage)  issues load p (0 .. kLoadsPerStage-1, a constant)
 //                            of the prepared stage into `stage`
-//   read(stage, ks, frags)   the fragment reads of k-substep ks (a constant), inline asm,
-//                            NLDS LDS instructions
+//   read(stage, ks, frags, only)  the fragment reads of k-substep ks (a
+//                            constant), inline asm: fragment `only` (0 .. 7:
+//                            B blocks 0-3, then A0/A1 of row block 0, then of
+//                            row block 1) or, for only = -1, all of them
 // Stage kt (buffer cur, next buffer nxt), fragments double-buffered in f[2]:
-//   substeps j < kSubsteps-1: read (kt, j+1) -> f[(j+1)&1];  wait for f[j&1];
-//     its MFMAs (prep(kt+2) rides on substep 0)
+//   substeps j < kSubsteps-1: wait for f[j&1]; its 16 MFMAs, with the reads of
+//     (kt, j+1) -> f[(j+1)&1] one fragment after each of the first 8 MFMAs,
+//     and the loads of stage kt+1 that the previous stage left over (below);
+//     prep(kt+2) after substep kSubsteps-2
 //   last substep: wait for this wave's loads of stage kt+1 and for the last
 //     fragments, barrier (stage kt+1 has landed for every wave, and every wave
 //     is done reading stage kt), read (kt+1, 0) -> f[0], then the MFMAs of the
-//     last substep with the loads of stage kt+2 into cur, one after each MFMA
-// so with one wave per SIMD the matrix core is fed while the next fragments
-// and the next stage arrive.  The fragment reads are inline asm because the
-// compiler's wait-count pass cannot tell them from the in-flight LDS-DMA
-// writes and would drain every load (vmcnt(0)) or every read (lgkmcnt(0))
-// in front of them; every wait here is explicit.  Before the MFMAs of
-// f[j&1] the NLDS reads of f[(j+1)&1] are the only younger LDS operations, so
-// lgkmcnt(min(NLDS, 15)) leaves f[j&1] complete (any other LGKM operation only
-// makes it stricter).
+//     last substep with the first loads of stage kt+2 into cur between them.
+// The loads of one stage are spread over the last substep of stage kt and the
+// first substeps of stage kt+1 (kLdSplit), because a CU's vector memory path
+// takes one 64-lane, 16-byte-per-lane LDS-DMA instruction in about 16 clocks:
+// the 64 of a stage (4 waves x 16) need ~1000 clocks, twice the 16 MFMAs of
+// one substep, and a wave whose load cannot issue stops issuing MFMAs too.
+// The ones issued in stage kt+1 still have its last substeps to land.
+// Reads ride on the MFMAs for the same reason at a smaller scale: issued as a
+// block, 8 to 16 reads and the wait for the first of them leave the matrix
+// core idle for about a hundred clocks per substep.
+// The fragment reads are inline asm because the compiler's wait-count pass
+// cannot tell them from the in-flight LDS-DMA writes and would drain every
+// load (vmcnt(0)) or every read (lgkmcnt(0)) in front of them; every wait
+// here is explicit.  At the start of a substep the only LDS reads in flight
+// are those of its own fragments, so lgkmcnt(0) costs nothing there.
+#ifndef UTTT_LD_SPLIT
+#define UTTT_LD_SPLIT 10, 6, 0, 0
+#endif
+// Loads of a stage issued in: the last substep of the stage before, then
+// substeps 0, 1, 2 of the stage before the one they fill.
+constexpr int kLdSplit[4] = {UTTT_LD_SPLIT};
+static_assert(kLdSplit[0] + kLdSplit[1] + kLdSplit[2] + kLdSplit[3] == kLoadsPerStage,
+              "every load of a stage has a slot");
+
+// The load (0 .. kLoadsPerStage-1) issued after MFMA q of phase ph (0 = last
+// substep, 1..3 = substeps 0..2 of the next stage), or -1: phase ph's n loads
+// sit after MFMAs 0, 16/n, 2*16/n, ...
+template <int PH, int Q>
+constexpr int load_slot() {
+  int lo = 0;
+  for (int i = 0; i < PH; ++i) lo += kLdSplit[i];
+  const int n = kLdSplit[PH];
+  for (int i = 0; i < n; ++i)
+    if (i * 16 / n == Q) return lo + i;
+  return -1;
+}
+
 template <int NLDS, bool SKIP, class PrepFn, class IssueFn, class ReadFn>
 __device__ __forceinline__ void run_pipeline(int nk, bool full, PrepFn&& prep, IssueFn&& issue,
                                              ReadFn&& read,
                                              f32x16 (&acc0)[2][kNB], f32x16 (&acc1)[2][kNB],
                                              uint8_t* const (&ring)[kStages]) {
   if (nk <= 0) return;
-  constexpr int kW = NLDS < 15 ? NLDS : 15;
-  static_assert(kSubsteps % 2 == 0, "fragment double buffer parity");
+  static_assert(kSubsteps % 2 == 0 && kSubsteps == 4, "fragment double buffer parity");
+  static_assert(NLDS <= 16, "two LDS reads per MFMA slot at most");
+  using All = std::integral_constant<int, -1>;
   HalfFrags f[2];
   auto load_all = [&](int kt, uint8_t* st) __attribute__((always_inline)) -> bool {
     const bool m = prep(kt);
@@ -481,15 +533,25 @@ __device__ __forceinline__ void run_pipeline(int nk, bool full, PrepFn&& prep, I
   else
     wait_vmcnt<(kStages - 1) * kLoadsPerStage>();
   block_barrier();
-  read(ring[0], std::integral_constant<int, 0>{}, f[0]);
-  auto step = [&](int kt, uint8_t* cur, const uint8_t* nxt) __attribute__((always_inline)) {
-    bool masked = false;
+  read(ring[0], std::integral_constant<int, 0>{}, f[0], All{});
+  // whether the stage whose loads are being issued takes the masked form (all
+  // its loads then go out at once, in the last substep); stage 1 was loaded
+  // whole before the loop, so stage 0 has no leftover loads either
+  bool masked = true;
+  auto step = [&](int kt, uint8_t* cur, uint8_t* nxt) __attribute__((always_inline)) {
     static_for<kSubsteps - 1>([&](auto J) __attribute__((always_inline)) {
       constexpr int j = J;
-      read(cur, std::integral_constant<int, j + 1>{}, f[(j + 1) & 1]);
-      if constexpr (j == 0) masked = prep(kt + kStages);
-      lgkm_wait_tied<kW>(f[j & 1]);
-      mma_half<SKIP>(acc0, acc1, f[j & 1], full);
+      lgkm_wait_tied<0>(f[j & 1]);
+      mma_half<SKIP>(acc0, acc1, f[j & 1], full, [&](auto q) __attribute__((always_inline)) {
+        constexpr int Q = decltype(q)::value;
+        if constexpr (Q < 8)
+          read(cur, std::integral_constant<int, j + 1>{}, f[(j + 1) & 1],
+               std::integral_constant<int, Q>{});
+        constexpr int p = load_slot<j + 1, Q>();
+        if constexpr (p >= 0)
+          if (!masked) issue(std::integral_constant<int, p>{}, std::false_type{}, nxt);
+      });
+      if constexpr (j == kSubsteps - 2) masked = prep(kt + kStages);
       __builtin_amdgcn_sched_barrier(0);
     });
     constexpr int jl = kSubsteps - 1;
@@ -497,7 +559,7 @@ __device__ __forceinline__ void run_pipeline(int nk, bool full, PrepFn&& prep, I
     lgkm_wait_tied<0>(f[jl & 1]);
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    read(nxt, std::integral_constant<int, 0>{}, f[(jl + 1) & 1]);
+    read(nxt, std::integral_constant<int, 0>{}, f[(jl + 1) & 1], All{});
     // the rare K-tail step issues its masked loads up front; otherwise the
     // loads ride between the MFMAs (branches hold loads only, so the
     // accumulators never meet at a join)
@@ -506,9 +568,10 @@ __device__ __forceinline__ void run_pipeline(int nk, bool full, PrepFn&& prep, I
         issue(p, std::true_type{}, cur);
       });
     __builtin_amdgcn_sched_barrier(0);
-    mma_half<SKIP>(acc0, acc1, f[jl & 1], full, [&](auto i) __attribute__((always_inline)) {
-      if constexpr (decltype(i)::value < kLoadsPerStage)
-        if (!masked) issue(i, std::false_type{}, cur);
+    mma_half<SKIP>(acc0, acc1, f[jl & 1], full, [&](auto q) __attribute__((always_inline)) {
+      constexpr int p = load_slot<0, decltype(q)::value>();
+      if constexpr (p >= 0)
+        if (!masked) issue(std::integral_constant<int, p>{}, std::false_type{}, cur);
     });
     __builtin_amdgcn_sched_barrier(0);
   };

@@ -677,8 +677,9 @@ __global__ __launch_bounds__(kThreads) void tn_kernel(TnArgs a, typename Epi::Ar
   const int vt = tt.size - tt.n0 - wn * (kBRows / 2);
   const bool full = !SKIP || __builtin_amdgcn_readfirstlane(vt > 32 ? 1 : 0) != 0;
   (void)vt;
-  auto read = [&](const uint8_t* st, auto ks, HalfFrags& f) __attribute__((always_inline)) {
-    read_half<AMAJ, KMajor, decltype(ks)::value>(f, st, wm, wn);
+  auto read = [&](const uint8_t* st, auto ks, HalfFrags& f, auto only)
+                  __attribute__((always_inline)) {
+    read_half<AMAJ, KMajor, decltype(ks)::value, kNB, decltype(only)::value>(f, st, wm, wn);
   };
   run_pipeline<half_lds_ops<AMAJ, KMajor>(), SKIP>(nk0 + nk1, full, prep, issue, read, acc0,
                                                     acc1, ring);
@@ -1033,8 +1034,9 @@ __global__ __launch_bounds__(kThreads) void wg_kernel(WgTask t0, WgTask t1,
   };
   const int w = threadIdx.x >> 6;
   const int wm = w >> 1, wn = w & 1;
-  auto read = [&](const uint8_t* st, auto ks, HalfFrags& f) __attribute__((always_inline)) {
-    read_half<RMajor, RMajor, decltype(ks)::value>(f, st, wm, wn);
+  auto read = [&](const uint8_t* st, auto ks, HalfFrags& f, auto only)
+                  __attribute__((always_inline)) {
+    read_half<RMajor, RMajor, decltype(ks)::value, kNB, decltype(only)::value>(f, st, wm, wn);
   };
   uint8_t* const ring[kStages] = {st0, st1};
   run_pipeline<half_lds_ops<RMajor, RMajor>(), false>((size + kBK - 1) / kBK, true, prep, issue,
