@@ -25,8 +25,9 @@
 //     are two ds_read_b64_tr_b16: within a group of 16 lanes, source lane
 //     s = 4j + q reads k-row j, rows 4q..4q+3, and the hardware hands lane i
 //     the column i of that 4x16 block, i.e. 4 consecutive k of row i.
-// Lanes whose chunk lies outside the operand read a 16-byte zero block, so
-// partial tiles need no special casing in the MFMA loop.
+// Lanes whose chunk lies at or past the operand's K end load zeros (the
+// buffer descriptor's record bound), so partial tiles need no special casing
+// in the MFMA loop.
 #pragma once
 
 #include <utility>
@@ -70,10 +71,6 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 
-
-// 16 zero bytes (zero-initialised device memory, never written): the source
-// of every masked-off lane of a tile load.
-__device__ __attribute__((aligned(16))) uint4 g_zero16;
 
 #define UTTT_LDS(p) ((__attribute__((address_space(3))) void*)(p))
 
@@ -125,18 +122,28 @@ struct Operand {
 __device__ __forceinline__ int kswz(int r) { return (r >> 1) & 7; }
 __device__ __forceinline__ int rswz(int k) { return (k & 3) << 2; }
 
-// Loads of one 128-row x kBK tile of an operand for a whole K loop.  The
-// tile origin and its per-step advance are wave-uniform (scalar registers);
-// each lane keeps only the 32-bit byte offsets of its kLoadsPerTile chunks, so
-// a load is one global_load_lds_dwordx4 with a scalar base and a vector
-// offset, and a whole step costs a few scalar instructions.  Rows past the
+// Loads of one 128-row x kBK tile of an operand for a whole K loop, as
+// buffer-form LDS-DMA (buffer_load_dwordx4 ... lds: 16 bytes per lane from a
+// scalar descriptor plus the lane's 32-bit offset, straight into LDS at
+// M0 + 16 * lane).  The tile origin and its per-step advance are wave-uniform;
+// each lane keeps only the byte offsets of its kLoadsPerTile chunks, so a load
+// costs a few scalar instructions and no vector ones.  Rows past the
 // operand's end are clamped onto its last valid row (their products land in
-// output rows or token columns that are never stored); the K tail (the last
-// step when k_end is not a multiple of kBK) and every step past the last
-// (which the K loop runs to finish its ring, or issues ahead of the end) hold
-// zeros for k >= k_end, through the masked form.
+// output rows or token columns that are never stored).  Every k >= k_end reads
+// as zero through the descriptor's record bound (out-of-range lanes of a
+// buffer load return zeros and touch no memory), so every step issues the
+// same loads:
+//   - each step past the last (the K loop runs whole ring iterations and
+//     issues ahead of the end): no records at all;
+//   - the K tail of an RMajor operand (k-rows contiguous): the bound ends at
+//     the first k-row past k_end;
+//   - the K tail of a KMajor operand (k contiguous inside a row): the lanes
+//     whose chunk lies at or past k_end get bit 31 set in their offset and
+//     the bound is 2^31 (offsets of valid chunks stay below it: rows of at
+//     most 2^23 elements).
 // Word 3 of a raw buffer descriptor on gfx9 (32-bit data format, no swizzle).
 constexpr int kBufferWord3 = 0x00020000;
+typedef __amdgpu_buffer_rsrc_t Rsrc;
 
 template <int MAJOR>
 struct TileLoader {
@@ -145,6 +152,8 @@ struct TileLoader {
   int last;               // last step holding data
   int k_end;
   int nvalid;             // valid rows from the tile origin (KMajor: rows of 8 per load)
+  int ld2;                // RMajor: bytes per k-row of the operand
+  int col2;               // RMajor: byte offset of the tile origin inside its k-row
   uint32_t off[kLoadsPerTile];
   int wofs;               // wave-uniform: this wave's LDS byte offset inside a tile
 
@@ -159,12 +168,15 @@ struct TileLoader {
     // from the thread id before every load)
     wofs = w * 64 * 16;
     asm volatile("" : "+s"(wofs));
+    ld2 = (int)op.ld * 2;
     const uint16_t* org;
     if (nrows > 0) {
       org = MAJOR == KMajor ? op.base + (int64_t)r0 * op.ld : op.base + r0;
+      col2 = r0 * 2;
     } else {  // no valid row: read the operand's first rows instead
       org = op.base;
       nrows = MAJOR == KMajor ? 1 : 8;
+      col2 = 0;
     }
     base = uniform_ptr(reinterpret_cast<const uint8_t*>(org));
     kstep = MAJOR == KMajor ? (int64_t)kBK * 2 : (int64_t)kBK * op.ld * 2;
@@ -183,61 +195,52 @@ struct TileLoader {
         const int cc = c < cmax ? c : cmax;
         off[t] = (uint32_t)(k * (int)op.ld + cc * 8) * 2u;
       }
-      // one 32-bit register per offset: left visible, the compiler folds the
-      // address's zero-extension into a 64-bit multiply-add and keeps pairs
       asm volatile("" : "+v"(off[t]));
     }
   }
 
   __device__ __forceinline__ int clamp_step(int step) const { return step < last ? step : last; }
-  // Wave-uniform address of step `step`'s tile origin.
-  __device__ __forceinline__ const uint8_t* step_base(int step) const {
-    return uniform_ptr(base + (int64_t)clamp_step(step) * kstep);
-  }
-  // Whether the loads of `step` need the masked form: the K tail (the last
-  // step when k_end is not a multiple of kBK) and every step past the last,
-  // which the K loop runs to finish its ring and which must multiply zeros.
-  __device__ __forceinline__ bool tail(int step) const {
-    return step > last || (step == last && (k_end % kBK) != 0);
+
+  // The descriptor of step `step` (call once per step, in step order: the
+  // KMajor K tail marks its out-of-range lanes for the steps after it too,
+  // which have no records anyway).
+  __device__ __forceinline__ Rsrc rsrc(int step) {
+    const uint8_t* sb = uniform_ptr(base + (int64_t)clamp_step(step) * kstep);
+    uint32_t recs = 0xFFFFFFFFu;
+    if (step > last) {
+      recs = 0;
+    } else if (step == last && (k_end % kBK) != 0) {
+      if constexpr (MAJOR == RMajor) {
+        recs = (uint32_t)((k_end - step * kBK) * ld2 - col2);
+      } else {
+        recs = 0x80000000u;
+        const int lane = threadIdx.x & 63, w = wofs >> 10, kt = k_end % kBK;
+#pragma unroll
+        for (int t = 0; t < kLoadsPerTile; ++t) {
+          const int sl = (t * 4 + w) * 64 + lane;
+          const int r = sl / kChunks;
+          const int c = (sl % kChunks) ^ kswz(r);
+          if (c * 8 >= kt) off[t] |= 0x80000000u;
+        }
+      }
+    }
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(sb), (short)0, (int)recs,
+                                             kBufferWord3);
   }
 
-  // Issue load t of this wave's share of the step at `sb` into LDS tile `dst`.
-  // The masked form loads the lanes whose chunk lies below k_end and writes 16
-  // zero bytes to the LDS slot of every other lane (a DMA lands lane i at
-  // M0 + 16 i); so it may issue no DMA instruction at all for this wave.
-  // SKIP_ROWS (KMajor token tiles of the APPLY products): a load whose 8 rows
-  // all lie past the valid rows is not issued; its LDS slots keep stale
+  // Issue load t of this wave's share of a step (descriptor rs) into LDS tile
+  // `dst`.  SKIP_ROWS (KMajor token tiles of the APPLY products): a load whose
+  // 8 rows all lie past the valid rows is not issued; its LDS slots keep stale
   // values, which only reach the products of token columns that are never
   // stored.  Fewer loads per stage than kLoadsPerStage: the pipeline then
   // waits on vmcnt(0) wherever it would count loads.
-  template <bool MASKED, bool SKIP_ROWS = false>
-  __device__ __forceinline__ void issue(const uint8_t* sb, int step, int t, uint8_t* dst) const {
+  template <bool SKIP_ROWS = false>
+  __device__ __forceinline__ void issue(const Rsrc& rs, int t, uint8_t* dst) const {
     uint8_t* d = dst + t * 4 * 64 * 16 + wofs;
-    if constexpr (SKIP_ROWS && !MASKED && MAJOR == KMajor) {
+    if constexpr (SKIP_ROWS && MAJOR == KMajor) {
       if (t * 4 * (64 / kChunks) + (wofs >> 7) >= nvalid) return;  // wave-uniform
     }
-    if constexpr (!MASKED) {
-      // buffer form: the step's tile origin as a scalar descriptor and the
-      // lane's 32-bit offset, so the address costs no vector instruction
-      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<uint8_t*>(sb), (short)0, -1, kBufferWord3);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, UTTT_LDS(d), 16, off[t], 0, 0, 0);
-    } else {
-      const int lane = threadIdx.x & 63;
-      const int s = (t * 4 + wave_id()) * 64 + lane;
-      int kk;
-      if constexpr (MAJOR == KMajor) {
-        const int r = s / kChunks;
-        kk = ((s % kChunks) ^ kswz(r)) * 8;
-      } else {
-        kk = s >> 4;
-      }
-      if (step * kBK + kk < k_end)
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(sb + off[t]), UTTT_LDS(d),
-                                         16, 0, 0);
-      else
-        *reinterpret_cast<uint4*>(d + lane * 16) = make_uint4(0u, 0u, 0u, 0u);
-    }
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, UTTT_LDS(d), 16, off[t], 0, 0, 0);
   }
 };
 
@@ -446,9 +449,8 @@ __device__ __forceinline__ void mma_half(f32x16 (&acc0)[2][kNB], f32x16 (&acc1)[
 // 128-byte cache lines: an LDS-DMA instruction touches 8 lines instead of 16,
 // which doubles what a CU's L1 can stream from L2).
 //   prep(kt)                 readies the loads of stage kt (operand switch,
-//                            per-stage scalar bases) and returns whether they
-//                            need the masked (K tail) form
-//   issue(p, masked, stage)  issues load p (0 .. kLoadsPerStage-1, a constant)
+//                            per-stage descriptors)
+//   issue(p, stage)          issues load p (0 .. kLoadsPerStage-1, a constant)
 //                            of the prepared stage into `stage`
 //   read(stage, ks, frags, only)  the fragment reads of k-substep ks (a
 //                            constant), inline asm: fragment `only` (0 .. 7:
@@ -509,35 +511,21 @@ __device__ __forceinline__ void run_pipeline(int nk, bool full, PrepFn&& prep, I
   static_assert(NLDS <= 16, "two LDS reads per MFMA slot at most");
   using All = std::integral_constant<int, -1>;
   HalfFrags f[2];
-  auto load_all = [&](int kt, uint8_t* st) __attribute__((always_inline)) -> bool {
-    const bool m = prep(kt);
-    if (m)
-      static_for<kLoadsPerStage>([&](auto p) __attribute__((always_inline)) {
-        issue(p, std::true_type{}, st);
-      });
-    else
-      static_for<kLoadsPerStage>([&](auto p) __attribute__((always_inline)) {
-        issue(p, std::false_type{}, st);
-      });
-    return m;
-  };
-  // stage 0 landed: counted while stages 1.. issued their kLoadsPerStage DMAs
-  // each, a full drain when one of them took the masked form (fewer DMAs)
-  bool later_masked = false;
   static_for<kStages>([&](auto i) __attribute__((always_inline)) {
-    const bool m = load_all(i, ring[i]);
-    if constexpr (decltype(i)::value > 0) later_masked |= m;
+    prep(decltype(i)::value);
+    static_for<kLoadsPerStage>([&](auto p) __attribute__((always_inline)) {
+      issue(p, ring[decltype(i)::value]);
+    });
   });
-  if (SKIP || later_masked)  // SKIP: the token tiles may issue fewer loads per stage
+  // stage 0 landed: counted while stage 1 issued its kLoadsPerStage DMAs
+  if (SKIP)  // the token tiles may issue fewer loads per stage
     wait_vmcnt<0>();
   else
     wait_vmcnt<(kStages - 1) * kLoadsPerStage>();
   block_barrier();
   read(ring[0], std::integral_constant<int, 0>{}, f[0], All{});
-  // whether the stage whose loads are being issued takes the masked form (all
-  // its loads then go out at once, in the last substep); stage 1 was loaded
-  // whole before the loop, so stage 0 has no leftover loads either
-  bool masked = true;
+  // stage 1 was loaded whole before the loop: stage 0 has no leftover loads
+  bool leftovers = false;
   auto step = [&](int kt, uint8_t* cur, uint8_t* nxt) __attribute__((always_inline)) {
     static_for<kSubsteps - 1>([&](auto J) __attribute__((always_inline)) {
       constexpr int j = J;
@@ -549,9 +537,9 @@ __device__ __forceinline__ void run_pipeline(int nk, bool full, PrepFn&& prep, I
                std::integral_constant<int, Q>{});
         constexpr int p = load_slot<j + 1, Q>();
         if constexpr (p >= 0)
-          if (!masked) issue(std::integral_constant<int, p>{}, std::false_type{}, nxt);
+          if (leftovers) issue(std::integral_constant<int, p>{}, nxt);
       });
-      if constexpr (j == kSubsteps - 2) masked = prep(kt + kStages);
+      if constexpr (j == kSubsteps - 2) prep(kt + kStages);
       __builtin_amdgcn_sched_barrier(0);
     });
     constexpr int jl = kSubsteps - 1;
@@ -560,24 +548,17 @@ __device__ __forceinline__ void run_pipeline(int nk, bool full, PrepFn&& prep, I
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
     read(nxt, std::integral_constant<int, 0>{}, f[(jl + 1) & 1], All{});
-    // the rare K-tail step issues its masked loads up front; otherwise the
-    // loads ride between the MFMAs (branches hold loads only, so the
-    // accumulators never meet at a join)
-    if (masked)
-      static_for<kLoadsPerStage>([&](auto p) __attribute__((always_inline)) {
-        issue(p, std::true_type{}, cur);
-      });
     __builtin_amdgcn_sched_barrier(0);
     mma_half<SKIP>(acc0, acc1, f[jl & 1], full, [&](auto q) __attribute__((always_inline)) {
       constexpr int p = load_slot<0, decltype(q)::value>();
-      if constexpr (p >= 0)
-        if (!masked) issue(std::integral_constant<int, p>{}, std::false_type{}, cur);
+      if constexpr (p >= 0) issue(std::integral_constant<int, p>{}, cur);
     });
+    leftovers = true;
     __builtin_amdgcn_sched_barrier(0);
   };
   // whole ring iterations only (one copy of the step code: a separate tail
   // would keep its own addressing live across the loop); steps past nk
-  // multiply the zeros their masked loads wrote
+  // multiply the zeros their loads wrote (no records)
   for (int kt = 0; kt < nk; kt += kStages)
     static_for<kStages>([&](auto i) __attribute__((always_inline)) {
       step(kt + i, ring[i], ring[(i + 1) % kStages]);

@@ -641,30 +641,27 @@ __global__ __launch_bounds__(kThreads) void tn_kernel(TnArgs a, typename Epi::Ar
   la1.init(A01, r1);
   lx0.init(X0, tt.n0);
   lx1.init(X0, tt.n0 + kTileRows);
-  const uint8_t* sb[4];
-  int lstep = 0;
-  auto prep = [&](int kt) __attribute__((always_inline)) -> bool {
+  Rsrc rs[4];
+  auto prep = [&](int kt) __attribute__((always_inline)) {
     if (nk1 > 0 && kt == nk0) {  // switch to the second operand pair (chained K)
       la0.init(A10, r0);
       la1.init(A11, r1);
       lx0.init(X1, tt.n0);
       lx1.init(X1, tt.n0 + kTileRows);
     }
-    lstep = nk1 > 0 && kt >= nk0 ? kt - nk0 : kt;
-    sb[0] = la0.step_base(lstep);
-    sb[1] = la1.step_base(lstep);
-    sb[2] = lx0.step_base(lstep);
-    sb[3] = lx1.step_base(lstep);
-    return la0.tail(lstep);  // A and X share the pair's K
+    const int lstep = nk1 > 0 && kt >= nk0 ? kt - nk0 : kt;
+    rs[0] = la0.rsrc(lstep);
+    rs[1] = la1.rsrc(lstep);
+    rs[2] = lx0.rsrc(lstep);
+    rs[3] = lx1.rsrc(lstep);
   };
-  auto issue = [&](auto p, auto masked, uint8_t* st) __attribute__((always_inline)) {
+  auto issue = [&](auto p, uint8_t* st) __attribute__((always_inline)) {
     constexpr int tile = decltype(p)::value / kLoadsPerTile;
     constexpr int t = decltype(p)::value % kLoadsPerTile;
-    constexpr bool M = decltype(masked)::value;
-    if constexpr (tile == 0) la0.template issue<M>(sb[0], lstep, t, st);
-    else if constexpr (tile == 1) la1.template issue<M>(sb[1], lstep, t, st + kTileBytes);
-    else if constexpr (tile == 2) lx0.template issue<M, SKIP>(sb[2], lstep, t, st + 2 * kTileBytes);
-    else lx1.template issue<M, SKIP>(sb[3], lstep, t, st + 3 * kTileBytes);
+    if constexpr (tile == 0) la0.issue(rs[0], t, st);
+    else if constexpr (tile == 1) la1.issue(rs[1], t, st + kTileBytes);
+    else if constexpr (tile == 2) lx0.template issue<SKIP>(rs[2], t, st + 2 * kTileBytes);
+    else lx1.template issue<SKIP>(rs[3], t, st + 3 * kTileBytes);
   };
   const int w = threadIdx.x >> 6;
   const int wm = w >> 1, wn = w & 1;
@@ -830,7 +827,7 @@ __device__ __forceinline__ void ap_mma(f32x16 (&acc)[2][4], const ApFrags& f) {
 }
 
 // The K loop.  Step k: wait for stage k's loads (stage k+1's may stay in
-// flight unless it is the masked K tail, which may issue fewer DMAs), barrier
+// flight), barrier
 // (stage k visible to every wave; every wave done reading the buffer of stage
 // k-1), issue stage k+2 into that buffer, then the four k-substeps of stage k
 // with the fragments of substep s+1 read while substep s multiplies.
@@ -841,22 +838,14 @@ __device__ __forceinline__ void ap_loop(TileLoader<KMajor>& la0, TileLoader<KMaj
   constexpr int kLPS = (TWO ? 3 : 2) * kLoadsPerTile;
   constexpr int kOps = (TWO ? 2 : 1) + JN;
   auto issue_stage = [&](int k, uint8_t* st) __attribute__((always_inline)) {
-    const uint8_t* s0 = la0.step_base(k);
-    const uint8_t* s1 = la1.step_base(k);
-    const uint8_t* sx = lx.step_base(k);
-    if (la0.tail(k)) {
-      static_for<kLoadsPerTile>([&](auto T) __attribute__((always_inline)) {
-        la0.template issue<true>(s0, k, T, st);
-        if constexpr (TWO) la1.template issue<true>(s1, k, T, st + kTileBytes);
-        lx.template issue<true>(sx, k, T, st + 2 * kTileBytes);
-      });
-    } else {
-      static_for<kLoadsPerTile>([&](auto T) __attribute__((always_inline)) {
-        la0.template issue<false>(s0, k, T, st);
-        if constexpr (TWO) la1.template issue<false>(s1, k, T, st + kTileBytes);
-        lx.template issue<false>(sx, k, T, st + 2 * kTileBytes);
-      });
-    }
+    const Rsrc r0 = la0.rsrc(k);
+    const Rsrc r1 = TWO ? la1.rsrc(k) : r0;
+    const Rsrc rx = lx.rsrc(k);
+    static_for<kLoadsPerTile>([&](auto T) __attribute__((always_inline)) {
+      la0.issue(r0, T, st);
+      if constexpr (TWO) la1.issue(r1, T, st + kTileBytes);
+      lx.issue(rx, T, st + 2 * kTileBytes);
+    });
   };
   const uint32_t a_lane = (uint32_t)(wave_id() * 32 * kChunks * 16);
   uint8_t* p0 = ring;
@@ -866,7 +855,7 @@ __device__ __forceinline__ void ap_loop(TileLoader<KMajor>& la0, TileLoader<KMaj
   if (nk > 1) issue_stage(1, p1);
   ApFrags f[2];
   for (int k = 0; k < nk; ++k) {
-    if (k + 1 < nk && !la0.tail(k + 1))
+    if (k + 1 < nk)
       wait_vmcnt<kLPS>();
     else
       wait_vmcnt<0>();
@@ -1013,24 +1002,20 @@ __global__ __launch_bounds__(kThreads) void wg_kernel(WgTask t0, WgTask t1,
   lp1.init(P, y0 + kTileRows);
   lq0.init(Q, x0);
   lq1.init(Q, x0 + kTileRows);
-  const uint8_t* sb[4];
-  int lstep = 0;
-  auto prep = [&](int kt) __attribute__((always_inline)) -> bool {
-    lstep = kt;
-    sb[0] = lp0.step_base(kt);
-    sb[1] = lp1.step_base(kt);
-    sb[2] = lq0.step_base(kt);
-    sb[3] = lq1.step_base(kt);
-    return lp0.tail(kt);
+  Rsrc rs[4];
+  auto prep = [&](int kt) __attribute__((always_inline)) {
+    rs[0] = lp0.rsrc(kt);
+    rs[1] = lp1.rsrc(kt);
+    rs[2] = lq0.rsrc(kt);
+    rs[3] = lq1.rsrc(kt);
   };
-  auto issue = [&](auto p, auto masked, uint8_t* st) __attribute__((always_inline)) {
+  auto issue = [&](auto p, uint8_t* st) __attribute__((always_inline)) {
     constexpr int tile = decltype(p)::value / kLoadsPerTile;
     constexpr int t = decltype(p)::value % kLoadsPerTile;
-    constexpr bool M = decltype(masked)::value;
-    if constexpr (tile == 0) lp0.template issue<M>(sb[0], lstep, t, st);
-    else if constexpr (tile == 1) lp1.template issue<M>(sb[1], lstep, t, st + kTileBytes);
-    else if constexpr (tile == 2) lq0.template issue<M>(sb[2], lstep, t, st + 2 * kTileBytes);
-    else lq1.template issue<M>(sb[3], lstep, t, st + 3 * kTileBytes);
+    if constexpr (tile == 0) lp0.issue(rs[0], t, st);
+    else if constexpr (tile == 1) lp1.issue(rs[1], t, st + kTileBytes);
+    else if constexpr (tile == 2) lq0.issue(rs[2], t, st + 2 * kTileBytes);
+    else lq1.issue(rs[3], t, st + 3 * kTileBytes);
   };
   const int w = threadIdx.x >> 6;
   const int wm = w >> 1, wn = w & 1;
