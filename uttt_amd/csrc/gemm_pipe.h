@@ -463,24 +463,27 @@ __device__ __forceinline__ void mma_half(f32x16 (&acc0)[2][kNB], f32x16 (&acc1)[
 //     prep(kt+2) after substep kSubsteps-2
 //   last substep: wait for this wave's loads of stage kt+1 and for the last
 //     fragments, barrier (stage kt+1 has landed for every wave, and every wave
-//     is done reading stage kt), read (kt+1, 0) -> f[0], then the MFMAs of the
-//     last substep with the first loads of stage kt+2 into cur between them.
-// The loads of one stage are spread over the last substep of stage kt and the
-// first substeps of stage kt+1 (kLdSplit), because a CU's vector memory path
-// takes one 64-lane, 16-byte-per-lane LDS-DMA instruction in about 16 clocks:
-// the 64 of a stage (4 waves x 16) need ~1000 clocks, twice the 16 MFMAs of
-// one substep, and a wave whose load cannot issue stops issuing MFMAs too.
-// The ones issued in stage kt+1 still have its last substeps to land.
-// Reads ride on the MFMAs for the same reason at a smaller scale: issued as a
-// block, 8 to 16 reads and the wait for the first of them leave the matrix
-// core idle for about a hundred clocks per substep.
+//     is done reading stage kt), then the MFMAs of the last substep with the
+//     reads of (kt+1, 0) -> f[0] and the first loads of stage kt+2 into cur
+//     between them.
+// With one wave per SIMD the matrix core only stays busy if the wave issues
+// its next MFMA as soon as the previous one leaves the pipe (32 clocks for
+// 32x32x16), so everything else rides between MFMAs in small pieces:
+// measured with clock stamps around each phase, the 16 loads of a stage issued
+// back to back cost ~1000 clocks of idle matrix core per stage, and 8 to 16
+// reads issued as a block plus the wait for the first of them ~100 clocks per
+// substep.  Hence one fragment read after each of 8 MFMAs, loads of 3 scalar
+// instructions each (buffer descriptor and M0 prepared per stage, no branch),
+// and the loads of one stage spread over the last substep of stage kt and the
+// first substeps of stage kt+1 (kLdSplit); those issued in stage kt+1 still
+// have its last substeps to land.
 // The fragment reads are inline asm because the compiler's wait-count pass
 // cannot tell them from the in-flight LDS-DMA writes and would drain every
 // load (vmcnt(0)) or every read (lgkmcnt(0)) in front of them; every wait
 // here is explicit.  At the start of a substep the only LDS reads in flight
 // are those of its own fragments, so lgkmcnt(0) costs nothing there.
 #ifndef UTTT_LD_SPLIT
-#define UTTT_LD_SPLIT 10, 6, 0, 0
+#define UTTT_LD_SPLIT 8, 8, 0, 0
 #endif
 // Loads of a stage issued in: the last substep of the stage before, then
 // substeps 0, 1, 2 of the stage before the one they fill.
@@ -547,9 +550,11 @@ __device__ __forceinline__ void run_pipeline(int nk, bool full, PrepFn&& prep, I
     lgkm_wait_tied<0>(f[jl & 1]);
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    read(nxt, std::integral_constant<int, 0>{}, f[(jl + 1) & 1], All{});
     __builtin_amdgcn_sched_barrier(0);
     mma_half<SKIP>(acc0, acc1, f[jl & 1], full, [&](auto q) __attribute__((always_inline)) {
+      if constexpr (decltype(q)::value < 8)
+        read(nxt, std::integral_constant<int, 0>{}, f[(jl + 1) & 1],
+             std::integral_constant<int, decltype(q)::value>{});
       constexpr int p = load_slot<0, decltype(q)::value>();
       if constexpr (p >= 0) issue(std::integral_constant<int, p>{}, cur);
     });
