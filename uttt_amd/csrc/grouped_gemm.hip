@@ -153,21 +153,25 @@ __device__ __forceinline__ void store8(uint16_t* p, const float (&v)[8]) {
 
 // Runs body(n, g) for the 64 x 16 (token, row-group) items of every quarter
 // of the tile, n = token index inside the tile (0..255), g = row group.
+// The barriers order only the LDS staging buffer (s_waitcnt lgkmcnt(0) +
+// s_barrier): a __syncthreads() would also wait for every global store of the
+// quarter to complete (its workgroup-scope fence), four store drains per tile
+// with the matrix core idle.
 template <class Body>
 __device__ __forceinline__ void staged_epilogue(const f32x16 (&acc0)[2][kNB],
                                                 const f32x16 (&acc1)[2][kNB], const TileCtx& c,
                                                 Body&& body) {
-  __syncthreads();  // every wave is done reading the stage buffers
+  block_barrier();  // every wave is done reading the stage buffers
   static_for<4>([&](auto QQ) __attribute__((always_inline)) {
     constexpr int Q = QQ;
     stage_quarter<Q>(acc0, acc1, c);
-    __syncthreads();
+    block_barrier();
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int it = threadIdx.x + kThreads * k;
       body(it >> 4, Q * 64 + (it >> 4), it & 15);
     }
-    __syncthreads();
+    block_barrier();
   });
 }
 
@@ -182,7 +186,7 @@ __device__ __forceinline__ void staged_epilogue_prefetch(const f32x16 (&acc0)[2]
                                                          const f32x16 (&acc1)[2][kNB],
                                                          const TileCtx& c, FetchFn&& fetch,
                                                          UseFn&& use) {
-  __syncthreads();  // every wave is done reading the stage buffers
+  block_barrier();  // every wave is done reading the stage buffers
   static_for<4>([&](auto QQ) __attribute__((always_inline)) {
     constexpr int Q = QQ;
     decltype(fetch(0, 0)) raw[4];
@@ -192,13 +196,13 @@ __device__ __forceinline__ void staged_epilogue_prefetch(const f32x16 (&acc0)[2]
       raw[k] = fetch(Q * 64 + (it >> 4), it & 15);
     }
     stage_quarter<Q>(acc0, acc1, c);
-    __syncthreads();
+    block_barrier();
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int it = threadIdx.x + kThreads * k;
       use(it >> 4, Q * 64 + (it >> 4), it & 15, raw[k]);
     }
-    __syncthreads();
+    block_barrier();
   });
 }
 
