@@ -150,6 +150,10 @@ __device__ __forceinline__ void store8(uint16_t* p, const float (&v)[8]) {
   u.w = pack_bf16x2(v[6], v[7]);
   *reinterpret_cast<uint4*>(p) = u;
 }
+__device__ __forceinline__ void store8(float* p, const float (&v)[8]) {
+  *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+}
 
 // Runs body(n, g) for the 64 x 16 (token, row-group) items of every quarter
 // of the tile, n = token index inside the tile (0..255), g = row group.
@@ -212,23 +216,46 @@ __device__ __forceinline__ void staged_epilogue_prefetch(const f32x16 (&acc0)[2]
 // MFMA-skipping (SKIP) variant leaves stale LDS data in those columns'
 // products, so only such epilogues may take it.
 template <class OutT>
+struct EpiStoreArgs {
+  OutT* out;
+  int64_t ld;
+  int col_off[2];  // tile t, row r -> column m0 + col_off[t] + r
+  int col_end[2];  // stored while that column < col_end[t]
+  int N;
+};
+
+// STAGED (the launcher's choice when the output is 16-byte aligned; ld and
+// the column offsets are multiples of 8): through the LDS frame, so every
+// store instruction writes 4 tokens x 256 contiguous bytes (bf16) instead of
+// 32 tokens x 16 bytes; otherwise straight from the accumulators.
+template <class OutT, bool STAGED = false>
 struct EpiStore {
   static constexpr bool kStaleColumnsUnused = true;  // per-column stores, masked by segment
-  struct Args {
-    OutT* out;
-    int64_t ld;
-    int col_off[2];  // tile t, row r -> column m0 + col_off[t] + r
-    int col_end[2];  // stored while that column < col_end[t]
-    int N;
-  };
+  using Args = EpiStoreArgs<OutT>;
   __device__ __forceinline__ static void apply(const Args& ea, const f32x16 (&acc0)[2][kNB],
                                const f32x16 (&acc1)[2][kNB], const TileCtx& c, bool two) {
     OutT* ob = ea.out + (int64_t)c.b * ea.N * ea.ld;
-    for_quads(acc0, acc1, c.wm, c.wn, two, [&](int t, int r, int n, const float* v) __attribute__((always_inline)) {
-      const int col = c.m0 + ea.col_off[t] + r;
-      if (c.tt.n0 + n < c.tt.size && col < ea.col_end[t])
-        store4(ob, ea.ld, c.tt.start + c.tt.n0 + n, col, v[0], v[1], v[2], v[3]);
-    });
+    if constexpr (STAGED) {
+      staged_epilogue(acc0, acc1, c, [&](int nl, int n, int g) __attribute__((always_inline)) {
+        if (c.tt.n0 + n >= c.tt.size) return;
+        OutT* row = ob + (int64_t)(c.tt.start + c.tt.n0 + n) * ea.ld;
+        static_for<2>([&](auto T) __attribute__((always_inline)) {
+          constexpr int t = T;
+          if (t == 1 && !two) return;
+          const int col = c.m0 + ea.col_off[t] + 8 * g;
+          if (col >= ea.col_end[t]) return;  // col_end is a multiple of 8
+          float v[8];
+          staged8(t == 0 ? c.lds0 : c.lds1, nl, g, v);
+          store8(row + col, v);
+        });
+      });
+    } else {
+      for_quads(acc0, acc1, c.wm, c.wn, two, [&](int t, int r, int n, const float* v) __attribute__((always_inline)) {
+        const int col = c.m0 + ea.col_off[t] + r;
+        if (c.tt.n0 + n < c.tt.size && col < ea.col_end[t])
+          store4(ob, ea.ld, c.tt.start + c.tt.n0 + n, col, v[0], v[1], v[2], v[3]);
+      });
+    }
   }
 };
 
@@ -1293,9 +1320,12 @@ void super_tile(int m_tiles, int* gm, int* gn) {
 // may join only if it never touches those columns (kStaleColumnsUnused).
 template <int AMAJ, class Epi>
 constexpr bool kSkippable =
-    AMAJ == KMajor && (std::is_same_v<Epi, EpiSwiGLU> || std::is_same_v<Epi, EpiStore<uint16_t>>);
+    AMAJ == KMajor && (std::is_same_v<Epi, EpiSwiGLU> || std::is_same_v<Epi, EpiStore<uint16_t>> ||
+                       std::is_same_v<Epi, EpiStore<uint16_t, true>>);
 static_assert(kSkippable<KMajor, EpiSwiGLU> <= EpiSwiGLU::kStaleColumnsUnused &&
                   kSkippable<KMajor, EpiStore<uint16_t>> <= EpiStore<uint16_t>::kStaleColumnsUnused &&
+                  kSkippable<KMajor, EpiStore<uint16_t, true>> <=
+                      EpiStore<uint16_t, true>::kStaleColumnsUnused &&
                   !kSkippable<KMajor, EpiS1<BF16T>> && !kSkippable<KMajor, EpiBwd<BF16T>> &&
                   !kSkippable<KMajor, EpiBwdSaved<BF16T>>,
               "the SKIP variant needs an epilogue that ignores stale token columns");
@@ -1394,7 +1424,8 @@ int launch_wide(const void* a, const void* x, int K, const void* a_2, const void
     t.x[1] = static_cast<const uint16_t*>(x_2);
     t.K[1] = K_2;
   }
-  typename EpiStore<OutT>::Args ea{y, M, {0, kTileRows}, {M, M}, N};
+  const EpiStoreArgs<OutT> ea{y, M, {0, kTileRows}, {M, M}, N};
+  if (aligned16(y)) return launch_tn<AMAJ, EpiStore<OutT, true>>(t, ea, B, st, what);
   return launch_tn<AMAJ, EpiStore<OutT>>(t, ea, B, st, what);
 }
 
@@ -1792,16 +1823,22 @@ extern "C" int uttt_grouped_update_bwd(
   {
     const TnArgs t = tn_args(w1, grad_dw1, v, D, I, g1, 0, 0, I, I, kTileRows, I, B, E, N,
                              group_sizes);
-    const EpiStore<uint16_t>::Args ea{dhg, 2 * I, {0, I}, {I, 2 * I}, N};
-    if (int rc = launch_tn<RMajor, EpiStore<uint16_t>>(t, ea, B, st, "grouped_update_bwd(DH)"))
+    const EpiStoreArgs<uint16_t> ea{dhg, 2 * I, {0, I}, {I, 2 * I}, N};
+    if (int rc = aligned16(dhg)
+                     ? launch_tn<RMajor, EpiStore<uint16_t, true>>(t, ea, B, st,
+                                                                   "grouped_update_bwd(DH)")
+                     : launch_tn<RMajor, EpiStore<uint16_t>>(t, ea, B, st, "grouped_update_bwd(DH)"))
       return rc;
   }
   // 2. GY = [gw0 k | gw2 k]  (bf16 [N, 2I])
   {
     const TnArgs t = tn_args(grad_dw0_w2, grad_dw0_w2, k, D, D, g02, 0, I, I, 2 * I, kTileRows, I,
                              B, E, N, group_sizes);
-    const EpiStore<uint16_t>::Args ea{gy, 2 * I, {0, I}, {I, 2 * I}, N};
-    if (int rc = launch_tn<KMajor, EpiStore<uint16_t>>(t, ea, B, st, "grouped_update_bwd(GY)"))
+    const EpiStoreArgs<uint16_t> ea{gy, 2 * I, {0, I}, {I, 2 * I}, N};
+    if (int rc = aligned16(gy)
+                     ? launch_tn<KMajor, EpiStore<uint16_t, true>>(t, ea, B, st,
+                                                                   "grouped_update_bwd(GY)")
+                     : launch_tn<KMajor, EpiStore<uint16_t>>(t, ea, B, st, "grouped_update_bwd(GY)"))
       return rc;
   }
   // 3. Y0, Y2 = w0 k, w2 k with the second-order pointwise pass; 4. lr grads
