@@ -866,7 +866,10 @@ template <bool TWO, int JN>
 __device__ __forceinline__ void ap_loop(TileLoader<KMajor>& la0, TileLoader<KMajor>& la1,
                                         TileLoader<KMajor>& lx, int nk, uint8_t* ring,
                                         f32x16 (&acc)[2][4]) {
-  constexpr int kLPS = (TWO ? 3 : 2) * kLoadsPerTile;
+  // load T of a wave covers token rows 32 T .. 32 T + 31 of the tile (8 per
+  // wave), so only the JN blocks that are multiplied are loaded; the LDS rows
+  // of the others keep stale data that no fragment read touches
+  constexpr int kLPS = (TWO ? 2 : 1) * kLoadsPerTile + JN;
   constexpr int kOps = (TWO ? 2 : 1) + JN;
   auto issue_stage = [&](int k, uint8_t* st) __attribute__((always_inline)) {
     const Rsrc r0 = la0.rsrc(k);
@@ -875,7 +878,7 @@ __device__ __forceinline__ void ap_loop(TileLoader<KMajor>& la0, TileLoader<KMaj
     static_for<kLoadsPerTile>([&](auto T) __attribute__((always_inline)) {
       la0.issue(r0, T, st);
       if constexpr (TWO) la1.issue(r1, T, st + kTileBytes);
-      lx.issue(rx, T, st + 2 * kTileBytes);
+      if constexpr (decltype(T)::value < JN) lx.issue(rx, T, st + 2 * kTileBytes);
     });
   };
   const uint32_t a_lane = (uint32_t)(wave_id() * 32 * kChunks * 16);
