@@ -43,6 +43,8 @@ struct TnArgs {
                             // gm = 0: plain order (m-tile fastest)
   int B, E, N;
   int two;                  // tile 1 multiplied
+  int sym;                  // symmetric output (one square group per batch, m_step equal to
+                            // the token tile): only tiles on or below the diagonal are computed
   const int32_t* gs;
 };
 
@@ -265,36 +267,95 @@ struct EpiStore {
 // Newton-Schulz steps with the bf16 rounding after every operation that the
 // reference's bf16 tensor arithmetic has: A = X X^T (with c A as out2),
 // B = b A + (c A) A, X' = a X + B X.
+// Through the LDS frame (16-byte accesses along the token rows; the arrays
+// are 16-byte aligned workspace with ld a multiple of 8).
+// SYM: the product is symmetric and only tiles on or below the diagonal run
+// (TnArgs::sym); a tile strictly below the diagonal also stores its
+// transpose, every thread 8 consecutive tokens of one output row (`in` is
+// symmetric too, so the transposed element is read from the transposed
+// position).
+struct EpiLinCombArgs {
+  uint16_t* out;
+  uint16_t* out2;
+  const uint16_t* in;
+  int64_t ld;
+  int col_end;
+  int N;
+  float alpha, beta, gamma;
+};
+
+// 8 consecutive elements at offset `at` of every array.
+__device__ __forceinline__ void lincomb8(const EpiLinCombArgs& ea, const float (&v)[8], int64_t at) {
+  float x[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f}, o[8];
+  if (ea.in != nullptr) load8(ea.in + at, x);
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const float p = bf16r(ea.beta * bf16r(v[u]));
+    o[u] = ea.in != nullptr ? bf16r(bf16r(ea.alpha * x[u]) + p) : p;
+  }
+  store8(ea.out + at, o);
+  if (ea.out2 != nullptr) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) o[u] *= ea.gamma;
+    store8(ea.out2 + at, o);
+  }
+}
+
+template <bool SYM = false>
 struct EpiLinComb {
   static constexpr bool kStaleColumnsUnused = true;
-  struct Args {
-    uint16_t* out;
-    uint16_t* out2;
-    const uint16_t* in;
-    int64_t ld;
-    int col_end;
-    int N;
-    float alpha, beta, gamma;
-  };
+  using Args = EpiLinCombArgs;
   __device__ __forceinline__ static void apply(const Args& ea, const f32x16 (&acc0)[2][kNB],
                                const f32x16 (&acc1)[2][kNB], const TileCtx& c, bool two) {
     const int64_t bo = (int64_t)c.b * ea.N * ea.ld;
-    for_quads(acc0, acc1, c.wm, c.wn, two, [&](int t, int r, int n, const float* v) __attribute__((always_inline)) {
-      const int col = c.m0 + t * kTileRows + r;
-      if (c.tt.n0 + n >= c.tt.size || col >= ea.col_end) return;
-      const int64_t tok = c.tt.start + c.tt.n0 + n;
-      float x[4] = {0.0f, 0.0f, 0.0f, 0.0f}, o[4];
-      if (ea.in != nullptr) load4(ea.in + bo, ea.ld, tok, col, x);
+    (void)two;  // past col_end when tile 1 is not multiplied
+    {
+      const bool mirror = SYM && c.m0 < c.tt.n0;  // uniform: a tile strictly below the diagonal
+      block_barrier();                     // every wave is done reading the stage buffers
+      static_for<4>([&](auto QQ) __attribute__((always_inline)) {
+        constexpr int Q = QQ;
+        stage_quarter<Q>(acc0, acc1, c);
+        block_barrier();
+        // the tile itself: token nl of the quarter, rows 8 g .. 8 g + 7 of each part
+#pragma unroll 1
+        for (int k = 0; k < 4; ++k) {
+          const int it = threadIdx.x + kThreads * k;
+          const int nl = it >> 4, g = it & 15;
+          if (c.tt.n0 + Q * 64 + nl >= c.tt.size) continue;
+          const int64_t tok = c.tt.start + c.tt.n0 + Q * 64 + nl;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const float p = bf16r(ea.beta * bf16r(v[u]));
-        o[u] = ea.in != nullptr ? bf16r(bf16r(ea.alpha * x[u]) + p) : p;
-      }
-      store4(ea.out + bo, ea.ld, tok, col, o[0], o[1], o[2], o[3]);
-      if (ea.out2 != nullptr)
-        store4(ea.out2 + bo, ea.ld, tok, col, ea.gamma * o[0], ea.gamma * o[1], ea.gamma * o[2],
-               ea.gamma * o[3]);
-    });
+          for (int part = 0; part < 2; ++part) {
+            const int col = c.m0 + part * kTileRows + 8 * g;
+            if (col >= ea.col_end) continue;  // col_end is a multiple of 8
+            float v[8];
+            staged8(part == 0 ? c.lds0 : c.lds1, nl, g, v);
+            const int64_t at = bo + tok * ea.ld + col;
+            lincomb8(ea, v, at);
+          }
+        }
+        // its transpose: row `col` of the output, 8 consecutive tokens
+        if (mirror) {
+#pragma unroll 1
+          for (int k = 0; k < 8; ++k) {
+            const int it = threadIdx.x + kThreads * k;
+            const int r = it & 127, part = (it >> 7) & 1, g8 = it >> 8;
+            const int nq = Q * 64 + 8 * g8;
+            const int col = c.m0 + part * kTileRows + r;
+            if (c.tt.n0 + nq >= c.tt.size || col >= ea.col_end) continue;  // multiples of 8
+            const float* lds = part == 0 ? c.lds0 : c.lds1;
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+              const int nl = 8 * g8 + u;
+              v[u] = lds[nl * 128 + (((r >> 2) ^ (nl & 31)) << 2) + (r & 3)];
+            }
+            const int64_t at = bo + (int64_t)col * ea.ld + c.tt.start + c.tt.n0 + nq;
+            lincomb8(ea, v, at);
+          }
+        }
+        block_barrier();
+      });
+    }
   }
 };
 
@@ -648,7 +709,7 @@ __global__ __launch_bounds__(kThreads) void tn_kernel(TnArgs a, typename Epi::Ar
   const int b = ntg / a.n_tiles_ub, nt = ntg % a.n_tiles_ub;
   const TokenTile tt = find_token_tile<kBRows>(a.gs + (int64_t)b * a.E, a.E, a.N, nt, scratch);
   __syncthreads();  // every wave has read the lookup before stage 1 is loaded
-  if (tt.e < 0) return;
+  if (tt.e < 0 || (a.sym && mt * a.m_step > tt.n0)) return;
   const int m0 = mt * a.m_step;
 
   const int64_t ag = ((int64_t)b * a.E + tt.e) * a.a_group;
@@ -1263,6 +1324,8 @@ int check_grid(int64_t blocks, const char* what) {
   return UTTT_OK;
 }
 
+
+
 // TnArgs of one token-grouped product family.
 TnArgs tn_args(const void* a0, const void* a1, const void* x, int K, int64_t lda, int64_t a_group,
                int off0, int off1, int end0, int end1, int m_step, int M_rows, int B, int E,
@@ -1288,6 +1351,7 @@ TnArgs tn_args(const void* a0, const void* a1, const void* x, int K, int64_t lda
   t.E = E;
   t.N = N;
   t.two = 1;
+  t.sym = 0;
   t.gs = gs;
   (void)B;
   return t;
@@ -1438,11 +1502,12 @@ template <int AMAJ>
 int launch_lincomb(const void* a, const void* x, int K, int M, int64_t lda, int64_t a_group,
                    const uint16_t* in, float alpha, float beta, uint16_t* y, uint16_t* y2,
                    float gamma, int B, int N, const int32_t* gs, hipStream_t st,
-                   const char* what) {
-  const TnArgs t = tn_args(a, a, x, K, lda, a_group, 0, kTileRows, M, M, 2 * kTileRows, M, B, 1,
-                           N, gs);
-  const EpiLinComb::Args ea{y, y2, in, M, M, N, alpha, beta, gamma};
-  return launch_tn<AMAJ, EpiLinComb>(t, ea, B, st, what);
+                   const char* what, bool sym = false) {
+  TnArgs t = tn_args(a, a, x, K, lda, a_group, 0, kTileRows, M, M, 2 * kTileRows, M, B, 1, N, gs);
+  t.sym = sym ? 1 : 0;
+  const EpiLinCombArgs ea{y, y2, in, M, M, N, alpha, beta, gamma};
+  if (sym) return launch_tn<AMAJ, EpiLinComb<true>>(t, ea, B, st, what);
+  return launch_tn<AMAJ, EpiLinComb<>>(t, ea, B, st, what);
 }
 
 WgTask wg_task(const void* p, const void* q, void* out, int X, int Y) {
@@ -1995,13 +2060,16 @@ extern "C" int uttt_newton_schulz5(const void* g, int g_dtype, int BE, int rows,
                                     {2.8366f, -3.0525f, 1.2012f}};
   for (int it = 0; it < 5; ++it) {
     const float ca = kCoef[it][0], cb = kCoef[it][1], cc = kCoef[it][2];
-    // A = X X^T and Ac = c A  ([m, m]: x = X as m rows of K = n, A operand = X)
+    // A = X X^T and Ac = c A  ([m, m]: x = X as m rows of K = n, A operand = X).
+    // A and B are symmetric: only the 256-tiles on or below the diagonal are
+    // multiplied and those below it also store their transposes (EpiLinComb),
+    // which takes 15 of the 36 tiles of a 1536-wide matrix off the matrix cores
     if (int rc = launch_lincomb<KMajor>(X, X, n, m, n, elems, nullptr, 0.0f, 1.0f, A, Ac, cc, BE, m,
-                                        gs, st, "newton_schulz5(X X^T)"))
+                                        gs, st, "newton_schulz5(X X^T)", true))
       return rc;
     // B = b A + (c A) A  (x = Ac, A operand = A: A is symmetric, so row j of A is column j)
     if (int rc = launch_lincomb<KMajor>(A, Ac, m, m, m, (int64_t)m * m, A, cb, 1.0f, Bm, nullptr,
-                                        0.0f, BE, m, gs, st, "newton_schulz5(B)"))
+                                        0.0f, BE, m, gs, st, "newton_schulz5(B)", true))
       return rc;
     // X' = a X + B X  ([m, n]: x = B, A operand = X read row-major: A(j, k) = X[k, j])
     if (int rc = launch_lincomb<RMajor>(X, Bm, m, n, n, elems, X, ca, 1.0f, Xn, nullptr, 0.0f, BE,
