@@ -1133,11 +1133,22 @@ __global__ __launch_bounds__(kThreads) void wg_kernel(WgTask t0, WgTask t1,
   const int ye = (tl2 / tk2.x_tiles) * 2 * kTileRows, xe = (tl2 % tk2.x_tiles) * kBRows;
   const int X2 = tk2.X, Y2 = tk2.Y;
   if constexpr (!SPLIT) {
+    // through the LDS frame (16-byte stores, 256 contiguous bytes per x row);
+    // the launcher passes 16-byte-aligned outputs only (Y is a multiple of 8)
     uint16_t* ob = tk2.out + (int64_t)be2 * X2 * Y2;
-    for_quads(acc0, acc1, after_loop(wm), after_loop(wn), true, [&](int tt, int r, int n, const float* v) __attribute__((always_inline)) {
-      const int y = ye + tt * kTileRows + r;
+    const TileCtx c{0, 0, after_loop(wm), after_loop(wn), 0, TokenTile{0, 0, 0, 0},
+                    reinterpret_cast<float*>(st0), reinterpret_cast<float*>(st1)};
+    staged_epilogue(acc0, acc1, c, [&](int nl, int n, int g) __attribute__((always_inline)) {
       const int x = xe + n;
-      if (y < Y2 && x < X2) store4(ob, Y2, x, y, v[0], v[1], v[2], v[3]);
+      if (x >= X2) return;
+      uint16_t* row = ob + (int64_t)x * Y2;
+      static_for<2>([&](auto T) __attribute__((always_inline)) {
+        const int y = ye + decltype(T)::value * kTileRows + 8 * g;
+        if (y >= Y2) return;
+        float v[8];
+        staged8(decltype(T)::value == 0 ? c.lds0 : c.lds1, nl, g, v);
+        store8(row + y, v);
+      });
     });
   } else {
     float* pb = tk2.part + ((int64_t)(bid2 / per_group / BE) * BE + be2) * X2 * Y2;
@@ -1564,6 +1575,9 @@ int launch_wg(WgTask t0, WgTask t1, const int32_t* gs, int B, int E, int N, int 
     t0.part = static_cast<float*>(workspace);
     t1.part = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + off1);
   }
+  // the plain epilogue stores 16 bytes at a time
+  UTTT_REQUIRE(splits > 1 || (aligned16(t0.out) && (t1.y_tiles * t1.x_tiles == 0 || aligned16(t1.out))),
+               "%s: outputs must be 16-byte aligned", what);
   if (splits == 1)
     hipLaunchKernelGGL(wg_kernel<false>, dim3((unsigned)blocks), dim3(kThreads), 0, st, t0, t1, gs,
                        E, N, B * E, 1);
