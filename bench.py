@@ -470,7 +470,7 @@ class MoeSweep:
         skinny-tile kernel when experts average under 256 rows)."""
         if self.N < 256 * self.E:
             return ("apply_kernel<ApSwiGLU, true>", "apply_kernel<ApStore, false>")
-        return ("tn_kernel<0, EpiSwiGLU, false>", "tn_kernel<0, EpiStore<unsigned short>, false>")
+        return ("tn_kernel<0, EpiSwiGLU, false>", "tn_kernel<0, EpiStore<unsigned short, true>, false>")
 
     def launch_table(self, layers, chunks, batched):
         """Every kernel launch of one sweep that carries GEMM work, grouped by
@@ -495,20 +495,20 @@ class MoeSweep:
         gate_sym, down_sym = self.apply_symbols()
         add(gate_sym, 4, Na, n_apply, 2 * (E * 2 * I * D + Na * D + Na * I))
         add(down_sym, 2, Na, n_apply, 2 * (E * D * I + Na * I + Na * D))
-        add("tn_kernel<1, EpiStore<float>, false>", 2, Nu, n_upd,
+        add("tn_kernel<1, EpiStore<float, true>, false>", 2, Nu, n_upd,
             2 * E * D * I + 2 * Nu * D + 4 * Nu * I)
         add("tn_kernel<0, EpiS1<BF16T>, false>", 4, Nu, n_upd,
             2 * E * 2 * I * D + 2 * Nu * D + 4 * Nu * I + 2 * 3 * Nu * I)
         add("wg_kernel<false>", 6, Nu, n_upd, w_bytes + 2 * Nu * (3 * I + 2 * D))
         if self.cfg["train"]:
             # the backward from the forward's saved bf16 Y0 | Y2 and DH
-            add("tn_kernel<1, EpiStore<unsigned short>, false>", 2, Nu, n_upd,
+            add("tn_kernel<1, EpiStore<unsigned short, true>, false>", 2, Nu, n_upd,
                 2 * E * D * I + 2 * Nu * D + 2 * Nu * I)                  # GD
             add("tn_kernel<0, EpiBwdSaved<BF16T>, false>", 4, Nu, n_upd,
                 2 * E * 2 * I * D + 2 * Nu * D + 2 * Nu * 16 * I)         # GY + 2nd order
-            add("tn_kernel<1, EpiStore<unsigned short>, false>", 8, Nu, n_upd,
+            add("tn_kernel<1, EpiStore<unsigned short, true>, false>", 8, Nu, n_upd,
                 2 * 2 * E * 2 * I * D + 2 * Nu * 4 * I + 2 * Nu * D)      # grad_K
-            add(f"tn_kernel<0, EpiStore<unsigned short>, {skip_u}>", 4, Nu, n_upd,
+            add(f"tn_kernel<0, EpiStore<unsigned short, true>, {skip_u}>", 4, Nu, n_upd,
                 2 * 2 * E * D * I + 2 * Nu * 2 * I + 2 * Nu * D)          # grad_V
             add("wg_kernel<false>", 6, Nu, n_upd, w_bytes + 2 * Nu * (3 * I + 2 * D))
         return tab
