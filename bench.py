@@ -98,9 +98,11 @@ def _profile_traffic(summary, kernel):
     try:
         with open(path) as f:
             for line in f:
-                parts = line.split()
-                if len(parts) == 3 and parts[0] == "traffic_bytes" and parts[1] == kernel:
-                    return int(parts[2])
+                if not line.startswith("traffic_bytes "):
+                    continue
+                name, value = line[len("traffic_bytes "):].rstrip().rsplit(None, 1)
+                if name == kernel:  # kernel names may hold spaces
+                    return int(value)
     except OSError:
         pass
     return None
@@ -536,7 +538,7 @@ class MoeSweep:
                 N = xp.shape[1]
                 hid = torch.empty(1, N, I, dtype=torch.bfloat16, device=self.dev)
                 yp = torch.empty(1, N, D, dtype=torch.bfloat16, device=self.dev)
-                if "EpiSwiGLU" in symbol:
+                if symbol == gate_sym:
                     fn = lambda: L.call("uttt_grouped_gate_up", L.ptr(self.W02), L.ptr(xp),
                                         L.ptr(gs), 1, E, I, D, N, L.ptr(hid), 1, s)
                 else:
