@@ -672,13 +672,19 @@ __device__ TokenTile find_token_tile(const int32_t* __restrict__ gs_b, int E, in
 
 // Number of BN-token tiles over all experts of one batch (the count
 // find_token_tile enumerates), with the same clamping of segments to [0, N).
-// Wave 0 scans; every thread gets the count.
+// The expert-major pair of workgroup `bid` when the real pairs (token tiles x
+// M m-tiles, counted here) are cut into kXcds equal ranges, workgroup bid
+// taking the (bid / kXcds)-th pair of range bid % kXcds: one wave counts the
+// token tiles and finds the pair in registers (one read of group_sizes, one
+// barrier); e = -1 for a workgroup past its range.
 template <int BN>
-__device__ int count_token_tiles(const int32_t* __restrict__ gs_b, int E, int N,
-                                 int* s_scratch /* >= 1 int */) {
+__device__ TokenTile find_pair_em_xcd(const int32_t* __restrict__ gs_b, int E, int N, int M,
+                                      int bid, int* mt, int* s_scratch /* >= 5 ints */) {
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
-    int tok_base = 0, tiles = 0;
+    int found_e = -1, found_start = 0, found_size = 0, found_n0 = 0, found_mt = 0;
+    // pass 1: total token tiles R
+    int tok_base = 0, R = 0;
     for (int e0 = 0; e0 < E; e0 += 64) {
       const int e = e0 + lane;
       const int graw = e < E ? gs_b[e] : 0;
@@ -695,64 +701,54 @@ __device__ int count_token_tiles(const int32_t* __restrict__ gs_b, int E, int N,
       int nt = (gc + BN - 1) / BN;
 #pragma unroll
       for (int d = 32; d >= 1; d >>= 1) nt += __shfl_xor(nt, d, 64);
-      tiles += nt;
+      R += nt;
       tok_base += __shfl(tok_incl, 63, 64);
     }
-    if (lane == 0) s_scratch[0] = tiles;
-  }
-  __syncthreads();
-  return __builtin_amdgcn_readfirstlane(s_scratch[0]);
-}
-
-// Expert-major enumeration of (token tile, m-tile) pairs: pair g belongs to
-// the expert e whose pairs [M * off_e, M * (off_e + n_e)) contain it (off_e
-// = token tiles before e, n_e its token tiles, M = m_tiles); inside an
-// expert the token tile runs fastest.  Returns the token tile (as
-// find_token_tile does) and the m-tile in *mt; e = -1 past the last pair.
-template <int BN>
-__device__ TokenTile find_pair_em(const int32_t* __restrict__ gs_b, int E, int N, int64_t g,
-                                  int M, int* mt, int* s_scratch /* >= 5 ints */) {
-  if (threadIdx.x < 64) {
-    const int lane = threadIdx.x;
-    int tok_base = 0;
-    int64_t pair_base = 0;
-    int found_e = -1, found_start = 0, found_size = 0, found_n0 = 0, found_mt = 0;
-    for (int e0 = 0; e0 < E; e0 += 64) {
-      const int e = e0 + lane;
-      const int graw = e < E ? gs_b[e] : 0;
-      const int gg = graw > 0 ? graw : 0;
-      int tok_incl = gg;
+    const int64_t total = (int64_t)R * M;
+    const int64_t per = (total + kXcds - 1) / kXcds;
+    const int64_t loc = bid / kXcds;
+    const int64_t t = (int64_t)(bid % kXcds) * per + loc;
+    if (loc < per && t < total) {
+      // pass 2: the expert whose pairs hold t (group_sizes are in L1 now)
+      tok_base = 0;
+      int64_t pair_base = 0;
+      for (int e0 = 0; e0 < E; e0 += 64) {
+        const int e = e0 + lane;
+        const int graw = e < E ? gs_b[e] : 0;
+        const int gg = graw > 0 ? graw : 0;
+        int tok_incl = gg;
 #pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const int a = __shfl_up(tok_incl, d, 64);
-        if (lane >= d) tok_incl += a;
-      }
-      const int start = tok_base + tok_incl - gg;
-      const int avail = start < N ? N - start : 0;
-      const int gc = gg < avail ? gg : avail;
-      const int nt = (gc + BN - 1) / BN;
-      int64_t pairs_incl = (int64_t)nt * M;
+        for (int d = 1; d < 64; d <<= 1) {
+          const int a = __shfl_up(tok_incl, d, 64);
+          if (lane >= d) tok_incl += a;
+        }
+        const int start = tok_base + tok_incl - gg;
+        const int avail = start < N ? N - start : 0;
+        const int gc = gg < avail ? gg : avail;
+        const int nt = (gc + BN - 1) / BN;
+        int64_t pairs_incl = (int64_t)nt * M;
 #pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const int64_t b = __shfl_up(pairs_incl, d, 64);
-        if (lane >= d) pairs_incl += b;
+        for (int d = 1; d < 64; d <<= 1) {
+          const int64_t b = __shfl_up(pairs_incl, d, 64);
+          if (lane >= d) pairs_incl += b;
+        }
+        const int64_t pairs_excl = pair_base + pairs_incl - (int64_t)nt * M;
+        const bool hit = e < E && nt > 0 && t >= pairs_excl && t < pairs_excl + (int64_t)nt * M;
+        const uint64_t bal = __ballot(hit);
+        if (bal != 0ull) {
+          const int src = __ffsll((unsigned long long)bal) - 1;
+          const int ntb = __shfl(nt, src, 64);
+          const int64_t local = t - __shfl(pairs_excl, src, 64);
+          found_e = e0 + src;
+          found_start = __shfl(start, src, 64);
+          found_size = __shfl(gc, src, 64);
+          found_n0 = (int)(local % ntb) * BN;
+          found_mt = (int)(local / ntb);
+          break;
+        }
+        tok_base += __shfl(tok_incl, 63, 64);
+        pair_base += __shfl(pairs_incl, 63, 64);
       }
-      const int64_t pairs_excl = pair_base + pairs_incl - (int64_t)nt * M;
-      const bool hit = e < E && nt > 0 && g >= pairs_excl && g < pairs_excl + (int64_t)nt * M;
-      const uint64_t bal = __ballot(hit);
-      if (bal != 0ull) {
-        const int src = __ffsll((unsigned long long)bal) - 1;
-        const int ntb = __shfl(nt, src, 64);
-        const int64_t local = g - __shfl(pairs_excl, src, 64);
-        found_e = e0 + src;
-        found_start = __shfl(start, src, 64);
-        found_size = __shfl(gc, src, 64);
-        found_n0 = (int)(local % ntb) * BN;
-        found_mt = (int)(local / ntb);
-        break;
-      }
-      tok_base += __shfl(tok_incl, 63, 64);
-      pair_base += __shfl(pairs_incl, 63, 64);
     }
     if (lane == 0) {
       s_scratch[0] = found_e;
@@ -769,6 +765,7 @@ __device__ TokenTile find_pair_em(const int32_t* __restrict__ gs_b, int E, int N
                    __builtin_amdgcn_readfirstlane(s_scratch[2]),
                    __builtin_amdgcn_readfirstlane(s_scratch[3])};
 }
+
 
 // Segment [start, start+size) of expert e in batch b, clamped to [0, N).
 __device__ __forceinline__ void expert_segment(const int32_t* __restrict__ gs_b, int e, int N,

@@ -993,14 +993,7 @@ __global__ __launch_bounds__(kThreads) void apply_kernel(ApArgs a, typename Epi:
     // weight slices once and reuses it from L2 for that expert's token tiles,
     // and reads a small expert's tokens once for all its m-tiles.  Workgroups
     // past their XCD's range leave at once.
-    const int R = count_token_tiles<kApTok>(a.gs, a.E, a.N, scratch);
-    const int64_t total = (int64_t)R * a.m_tiles;
-    const int64_t per = (total + kXcds - 1) / kXcds;
-    const int64_t loc = bid / kXcds;
-    const int64_t t = (int64_t)(bid % kXcds) * per + loc;
-    if (loc >= per || t >= total) return;  // uniform over the workgroup
-    __syncthreads();                        // the count is read before the scratch is reused
-    tt = find_pair_em<kApTok>(a.gs, a.E, a.N, t, a.m_tiles, &mt, scratch);
+    tt = find_pair_em_xcd<kApTok>(a.gs, a.E, a.N, a.m_tiles, bid, &mt, scratch);
     b = 0;
   } else {
     const int64_t t = (int64_t)(bid % kXcds) * a.per_xcd + bid / kXcds;
