@@ -92,3 +92,19 @@ def test_new_wrappers_refuse_cpu_tensors():
                             torch.zeros(1, 2, 1, dtype=torch.bool), torch.zeros(1, 2, 1), 1)
     with pytest.raises(RuntimeError, match="GPU only"):
         FWW.newton_schulz5(torch.zeros(1, 8, 8))
+
+
+@needs_lib
+def test_gemm_rejects_rows_past_2_pow_23_without_launch():
+    """The GEMM tile loads keep per-lane 32-bit offsets below 2^31 (bit 31
+    marks the K tail), so operand rows of 2^23 or more elements are refused
+    before any launch (stand-in addresses are never dereferenced)."""
+    lib = _lib.lib()
+    p = 1 << 20
+    K = 1 << 23
+    # grouped_gemm_nt: M rows of K = 2^23 features
+    rc = lib.uttt_grouped_gemm_nt(p, p, p, 1, 1, 256, K, 256, p, None)
+    assert rc == -1 and b"2^23" in lib.uttt_last_error()
+    # grouped_wgrad: R x C output with C = 2^23
+    rc = lib.uttt_grouped_wgrad(p, p, p, 1, 1, 256, K, 256, p, 0, None)
+    assert rc == -1 and b"2^23" in lib.uttt_last_error()

@@ -1406,6 +1406,10 @@ int launch_tn(TnArgs t, const typename Epi::Args& ea, int B, hipStream_t st,
               const char* what) {
   const int64_t tiles = (int64_t)t.m_tiles * t.n_tiles_ub * B;
   if (tiles == 0) return UTTT_OK;
+  // the tile loads keep 32-bit lane offsets below 2^31 (bit 31 marks the K
+  // tail): 128 rows of at most 2^23 elements
+  UTTT_REQUIRE(t.lda < (1 << 23) && t.K[0] < (1 << 23) && t.K[1] < (1 << 23),
+               "%s: operand rows of 2^23 or more elements are not supported", what);
   t.B = B;
   int64_t blocks = tiles;
   if (tiles >= g_xcd_map_min_tiles) {
@@ -1451,6 +1455,8 @@ int launch_apply(ApArgs a, int M_rows, const typename Epi::Args& ea, hipStream_t
   a.n_tiles_ub = (a.N + kApTok - 1) / kApTok + a.E;
   a.tiles = (int64_t)a.B * a.m_tiles * a.n_tiles_ub;
   if (a.tiles == 0) return UTTT_OK;
+  UTTT_REQUIRE(a.lda < (1 << 23) && a.K < (1 << 23),
+               "%s: operand rows of 2^23 or more elements are not supported", what);
   // the expert-major order measured 5% faster for the down projection and 4%
   // slower for gate/up (whose 256-row weight tiles are read by more m-tiles)
   a.em = a.B == 1 && std::is_same_v<Epi, ApStore>;
@@ -1560,6 +1566,8 @@ int launch_wg(WgTask t0, WgTask t1, const int32_t* gs, int B, int E, int N, int 
   const int64_t blocks = per * E * B * splits;
   if (blocks == 0) return UTTT_OK;
   if (int rc = check_grid(blocks, what)) return rc;
+  UTTT_REQUIRE(t0.X < (1 << 23) && t0.Y < (1 << 23) && t1.X < (1 << 23) && t1.Y < (1 << 23),
+               "%s: operand rows of 2^23 or more elements are not supported", what);
   if (splits > 1) {
     size_t off1;
     const size_t need = wg_part_bytes(t0, t1, B, E, splits, &off1);
