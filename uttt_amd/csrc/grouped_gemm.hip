@@ -152,6 +152,14 @@ __device__ __forceinline__ void store8(uint16_t* p, const float (&v)[8]) {
   u.w = pack_bf16x2(v[6], v[7]);
   *reinterpret_cast<uint4*>(p) = u;
 }
+// The same store with a non-temporal hint, for outputs read back only much
+// later (the saved tensors of the UPDATE's backward).
+typedef unsigned int nt_store_u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void store8_nt(uint16_t* p, const float (&v)[8]) {
+  const nt_store_u32x4 u = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                            pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
+  __builtin_nontemporal_store(u, reinterpret_cast<nt_store_u32x4*>(p));
+}
 __device__ __forceinline__ void store8(float* p, const float (&v)[8]) {
   *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
   *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
@@ -446,9 +454,9 @@ struct EpiS1 {
         hh[u] = sw * y2[u] * l1;
       }
       if (ea.y_save != nullptr) {  // the values the backward would recompute, rounded as it does
-        store8(ea.y_save + (int64_t)c.b * ea.N * I2 + (int64_t)tok * I2 + m, y0);
-        store8(ea.y_save + (int64_t)c.b * ea.N * I2 + (int64_t)tok * I2 + I + m, y2);
-        store8(ea.dh_save + (int64_t)c.b * ea.N * I + (int64_t)tok * I + m, dh);
+        store8_nt(ea.y_save + (int64_t)c.b * ea.N * I2 + (int64_t)tok * I2 + m, y0);
+        store8_nt(ea.y_save + (int64_t)c.b * ea.N * I2 + (int64_t)tok * I2 + I + m, y2);
+        store8_nt(ea.dh_save + (int64_t)c.b * ea.N * I + (int64_t)tok * I + m, dh);
       }
       if (ea.token_major) {
         store8(dyb + (int64_t)tok * I2 + m, d0);
