@@ -292,10 +292,12 @@ struct EpiLinCombArgs {
   float alpha, beta, gamma;
 };
 
-// 8 consecutive elements at offset `at` of every array.
-__device__ __forceinline__ void lincomb8(const EpiLinCombArgs& ea, const float (&v)[8], int64_t at) {
-  float x[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f}, o[8];
-  if (ea.in != nullptr) load8(ea.in + at, x);
+// 8 consecutive elements at offset `at` of every array; xin = in[at .. at + 7]
+// as loaded (ignored without `in`).
+__device__ __forceinline__ void lincomb8(const EpiLinCombArgs& ea, const float (&v)[8],
+                                         const uint4& xin, int64_t at) {
+  float x[8], o[8];
+  unpack8(xin, x);
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
     const float p = bf16r(ea.beta * bf16r(v[u]));
@@ -317,53 +319,80 @@ struct EpiLinComb {
                                const f32x16 (&acc1)[2][kNB], const TileCtx& c, bool two) {
     const int64_t bo = (int64_t)c.b * ea.N * ea.ld;
     (void)two;  // past col_end when tile 1 is not multiplied
-    {
-      const bool mirror = SYM && c.m0 < c.tt.n0;  // uniform: a tile strictly below the diagonal
-      block_barrier();                     // every wave is done reading the stage buffers
-      static_for<4>([&](auto QQ) __attribute__((always_inline)) {
-        constexpr int Q = QQ;
-        stage_quarter<Q>(acc0, acc1, c);
-        block_barrier();
-        // the tile itself: token nl of the quarter, rows 8 g .. 8 g + 7 of each part
-#pragma unroll 1
-        for (int k = 0; k < 4; ++k) {
+    // `in` is read from valid addresses whether or not it is given (out's,
+    // ignored then), all of a quarter's loads before any is used: a load
+    // under a branch, or one used at once, waits for every store in flight
+    const uint16_t* src = ea.in != nullptr ? ea.in : ea.out;
+    const bool mirror = SYM && c.m0 < c.tt.n0;  // uniform: a tile strictly below the diagonal
+    block_barrier();                             // every wave is done reading the stage buffers
+    static_for<4>([&](auto QQ) __attribute__((always_inline)) {
+      constexpr int Q = QQ;
+      // the tile itself: token nl of the quarter, rows 8 g .. 8 g + 7 of each part
+      uint4 xt[4][2];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int it = threadIdx.x + kThreads * k;
+        const int nl = it >> 4, g = it & 15;
+        const bool tok_ok = c.tt.n0 + Q * 64 + nl < c.tt.size;
+        const int64_t tok = c.tt.start + c.tt.n0 + Q * 64 + nl;
+#pragma unroll
+        for (int part = 0; part < 2; ++part) {
+          const int col = c.m0 + part * kTileRows + 8 * g;
+          const int64_t at = tok_ok && col < ea.col_end ? bo + tok * ea.ld + col : bo;
+          xt[k][part] = *reinterpret_cast<const uint4*>(src + at);
+        }
+      }
+      // its transpose: row `col` of the output, 8 consecutive tokens
+      uint4 xm[8];
+      if (mirror) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
           const int it = threadIdx.x + kThreads * k;
-          const int nl = it >> 4, g = it & 15;
-          if (c.tt.n0 + Q * 64 + nl >= c.tt.size) continue;
-          const int64_t tok = c.tt.start + c.tt.n0 + Q * 64 + nl;
-#pragma unroll
-          for (int part = 0; part < 2; ++part) {
-            const int col = c.m0 + part * kTileRows + 8 * g;
-            if (col >= ea.col_end) continue;  // col_end is a multiple of 8
-            float v[8];
-            staged8(part == 0 ? c.lds0 : c.lds1, nl, g, v);
-            const int64_t at = bo + tok * ea.ld + col;
-            lincomb8(ea, v, at);
-          }
+          const int r = it & 127, part = (it >> 7) & 1, g8 = it >> 8;
+          const int nq = Q * 64 + 8 * g8;
+          const int col = c.m0 + part * kTileRows + r;
+          const bool ok = c.tt.n0 + nq < c.tt.size && col < ea.col_end;  // multiples of 8
+          const int64_t at = ok ? bo + (int64_t)col * ea.ld + c.tt.start + c.tt.n0 + nq : bo;
+          xm[k] = *reinterpret_cast<const uint4*>(src + at);
         }
-        // its transpose: row `col` of the output, 8 consecutive tokens
-        if (mirror) {
-#pragma unroll 1
-          for (int k = 0; k < 8; ++k) {
-            const int it = threadIdx.x + kThreads * k;
-            const int r = it & 127, part = (it >> 7) & 1, g8 = it >> 8;
-            const int nq = Q * 64 + 8 * g8;
-            const int col = c.m0 + part * kTileRows + r;
-            if (c.tt.n0 + nq >= c.tt.size || col >= ea.col_end) continue;  // multiples of 8
-            const float* lds = part == 0 ? c.lds0 : c.lds1;
-            float v[8];
+      }
+      stage_quarter<Q>(acc0, acc1, c);
+      block_barrier();
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-              const int nl = 8 * g8 + u;
-              v[u] = lds[nl * 128 + (((r >> 2) ^ (nl & 31)) << 2) + (r & 3)];
-            }
-            const int64_t at = bo + (int64_t)col * ea.ld + c.tt.start + c.tt.n0 + nq;
-            lincomb8(ea, v, at);
-          }
+      for (int k = 0; k < 4; ++k) {
+        const int it = threadIdx.x + kThreads * k;
+        const int nl = it >> 4, g = it & 15;
+        if (c.tt.n0 + Q * 64 + nl >= c.tt.size) continue;
+        const int64_t tok = c.tt.start + c.tt.n0 + Q * 64 + nl;
+#pragma unroll
+        for (int part = 0; part < 2; ++part) {
+          const int col = c.m0 + part * kTileRows + 8 * g;
+          if (col >= ea.col_end) continue;  // col_end is a multiple of 8
+          float v[8];
+          staged8(part == 0 ? c.lds0 : c.lds1, nl, g, v);
+          lincomb8(ea, v, xt[k][part], bo + tok * ea.ld + col);
         }
-        block_barrier();
-      });
-    }
+      }
+      if (mirror) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const int it = threadIdx.x + kThreads * k;
+          const int r = it & 127, part = (it >> 7) & 1, g8 = it >> 8;
+          const int nq = Q * 64 + 8 * g8;
+          const int col = c.m0 + part * kTileRows + r;
+          if (c.tt.n0 + nq >= c.tt.size || col >= ea.col_end) continue;
+          const float* lds = part == 0 ? c.lds0 : c.lds1;
+          float v[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const int nl = 8 * g8 + u;
+            v[u] = lds[nl * 128 + (((r >> 2) ^ (nl & 31)) << 2) + (r & 3)];
+          }
+          lincomb8(ea, v, xm[k], bo + (int64_t)col * ea.ld + c.tt.start + c.tt.n0 + nq);
+        }
+      }
+      block_barrier();
+    });
   }
 };
 
@@ -425,12 +454,19 @@ struct EpiS1 {
       const int tok = c.tt.start + min(c.tt.n0 + n, c.tt.size - 1);  // clamped: always valid
       const float* p = dhb + (int64_t)tok * I + (m < I ? m : 0);
       const int64_t li = (int64_t)c.b * ea.N + tok;
+      // every load from a valid address (a missing lr reads the first element
+      // of dh, which the use ignores): a load under a branch is followed by a
+      // wait on every access in flight, the last quarter's stores included
+      const S* fb = reinterpret_cast<const S*>(ea.dh);
+      const S* q0 = ea.lr0 ? ea.lr0 + li : fb;
+      const S* q1 = ea.lr1 ? ea.lr1 + li : fb;
+      const S* q2 = ea.lr2 ? ea.lr2 + li : fb;
       Raw r;
       r.dh0 = *reinterpret_cast<const float4*>(p);
       r.dh1 = *reinterpret_cast<const float4*>(p + 4);
-      r.l0 = ea.lr0 ? ea.lr0[li] : S(0);
-      r.l1 = ea.lr1 ? ea.lr1[li] : S(0);
-      r.l2 = ea.lr2 ? ea.lr2[li] : S(0);
+      r.l0 = *q0;
+      r.l1 = *q1;
+      r.l2 = *q2;
       return r;
     };
     staged_epilogue_prefetch(acc0, acc1, c, fetch, [&](int nl, int n, int g, const Raw& rw) __attribute__((always_inline)) {
