@@ -438,18 +438,34 @@ __global__ __launch_bounds__(NW * kWave) void router_mfma_kernel(
 #pragma unroll
     for (int t = 0; t < kSmallT; ++t) acc[t] = 0.0f;
     const float* Re = R + (int64_t)(e < E ? e : 0) * D;
-#pragma unroll 4
-    for (int c = sl; c < nch; c += TPE) {
-      float wv[8];
-      load8<F32T>(Re, c * 8, D, e < E, vec, wv);
+    // the batch's nt live tokens as a compile-time count (uniform per block):
+    // every load unconditional, all of a chunk's in flight together (a load
+    // under a per-token branch would be waited for before the next issues)
+    auto logits = [&](auto NTC) __attribute__((always_inline)) {
+      constexpr int NT = decltype(NTC)::value;
+#pragma unroll 2
+      for (int c = sl; c < nch; c += TPE) {
+        float wv[8], xv[NT][8];
+        load8<F32T>(Re, c * 8, D, e < E, vec, wv);
 #pragma unroll
-      for (int t = 0; t < kSmallT; ++t) {
-        if (t >= nt) break;
-        float xv[8];
-        load8<XT>(x + ((int64_t)b * T + t0 + t) * D, c * 8, D, true, vec, xv);
+        for (int t = 0; t < NT; ++t)
+          load8<XT>(x + ((int64_t)b * T + t0 + t) * D, c * 8, D, true, vec, xv[t]);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[t] = fmaf(xv[i], wv[i], acc[t]);
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[t] = fmaf(xv[t][i], wv[i], acc[t]);
       }
+    };
+    static_assert(kSmallT == 8, "one case per token count");
+    switch (nt) {
+      case 1: logits(std::integral_constant<int, 1>{}); break;
+      case 2: logits(std::integral_constant<int, 2>{}); break;
+      case 3: logits(std::integral_constant<int, 3>{}); break;
+      case 4: logits(std::integral_constant<int, 4>{}); break;
+      case 5: logits(std::integral_constant<int, 5>{}); break;
+      case 6: logits(std::integral_constant<int, 6>{}); break;
+      case 7: logits(std::integral_constant<int, 7>{}); break;
+      default: logits(std::integral_constant<int, 8>{}); break;
     }
 #pragma unroll
     for (int t = 0; t < kSmallT; ++t) {
