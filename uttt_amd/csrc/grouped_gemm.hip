@@ -127,6 +127,23 @@ __device__ __forceinline__ void staged8(const float* reg, int n, int g, float (&
   v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
 
+// Sum over each aligned group of 16 lanes, the total in every lane: four
+// DPP adds (swap neighbours, swap pairs, mirror the 8-lane halves, mirror
+// the 16-lane row), no LDS round trip.  Every lane adds the same operands in
+// a commutated order, so all 16 hold the same bits.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float sum16(float v) {
+  v += dpp_f32<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v += dpp_f32<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v += dpp_f32<0x141>(v);  // row_half_mirror
+  v += dpp_f32<0x140>(v);  // row_mirror
+  return v;
+}
+
 __device__ __forceinline__ void unpack8(const uint4& u, float (&v)[8]) {
   const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
@@ -601,12 +618,9 @@ struct EpiBwd {
       }
       // the 16 lanes of one token hold its 128 rows: sum them for this tile's
       // lr-gradient partial
-#pragma unroll
-      for (int d = 8; d > 0; d >>= 1) {
-        s0 += __shfl_xor(s0, d, 16);
-        s1 += __shfl_xor(s1, d, 16);
-        s2 += __shfl_xor(s2, d, 16);
-      }
+      s0 = sum16(s0);
+      s1 = sum16(s1);
+      s2 = sum16(s2);
       if (g == 0 && c.tt.n0 + n < c.tt.size) {
         const int64_t o = ((int64_t)c.mt * ea.B + c.b) * ea.N + tok;
         ea.lr_part[o] = s0;
@@ -706,12 +720,9 @@ struct EpiBwdSaved {
         store8(ea.dx + r2 + I + m, o_dx2);
         store8(ea.hlr + r1 + m, o_hl);
       }
-#pragma unroll
-      for (int d = 8; d > 0; d >>= 1) {
-        s0 += __shfl_xor(s0, d, 16);
-        s1 += __shfl_xor(s1, d, 16);
-        s2 += __shfl_xor(s2, d, 16);
-      }
+      s0 = sum16(s0);
+      s1 = sum16(s1);
+      s2 = sum16(s2);
       if (g == 0 && c.tt.n0 + n < c.tt.size) {
         const int64_t o = ((int64_t)c.mt * ea.B + c.b) * ea.N + tok;
         ea.lr_part[o] = s0;
