@@ -383,19 +383,52 @@ __device__ __forceinline__ void store_vec(V* p, const V& v) {
 // Row-map entries of slots 0 and 1.  Columns [n, E) of the expert half hold
 // 0 and, for E == 1, column E + 1 is the count: the expert index of a slot
 // that is not routed is forced to 0 so that it addresses a valid probs entry.
+// The raw words are loaded first and decoded after every chunk's loads are
+// issued: a decode next to its load would wait for it there.
 struct Slots2 {
   int n, r0, r1, e0, e1;
 };
-__device__ __forceinline__ Slots2 load_slots2(const int32_t* __restrict__ rm, int E) {
+struct SlotsRaw {
+  int4 w;  // {row 0, row 1, expert 0, n}
+  int e1;  // expert of slot 1
+};
+__device__ __forceinline__ SlotsRaw load_slots_raw(const int32_t* __restrict__ rm, int E) {
+  SlotsRaw r;
+  r.w = make_int4(rm[0], rm[1], rm[E], rm[2 * E]);
+  r.e1 = rm[E + 1];
+  return r;
+}
+__device__ __forceinline__ Slots2 decode_slots(const SlotsRaw& r) {
   Slots2 s;
-  s.n = rm[2 * E];
-  s.r0 = rm[0];
-  s.r1 = rm[1];
-  s.e0 = rm[E];
-  s.e1 = rm[E + 1];
-  if (s.n < 1) s.e0 = 0;
-  if (s.n < 2) s.e1 = 0;
+  s.r0 = r.w.x;
+  s.r1 = r.w.y;
+  s.n = r.w.w;
+  s.e0 = s.n < 1 ? 0 : r.w.z;
+  s.e1 = s.n < 2 ? 0 : r.e1;
   return s;
+}
+
+// The gates of slots 0 and 1 (1 without probs), loaded unconditionally: a
+// missing probs tensor reads word 0 of the row map and the value is replaced,
+// so no load sits under a branch (the compiler waits for a load under a branch
+// where the paths join, and with it for every access in flight).
+template <int CU>
+__device__ __forceinline__ void gate_pair(const float* __restrict__ probs,
+                                          const int32_t* __restrict__ rmap, int64_t p_sb,
+                                          int64_t p_se, int64_t p_st, int T, const uint32_t (&bt)[CU],
+                                          const Slots2 (&s)[CU], float (&p0)[CU], float (&p1)[CU]) {
+  const bool has = probs != nullptr;
+  const float* pbase = has ? probs : reinterpret_cast<const float*>(rmap);
+  const int64_t sb = has ? p_sb : 0, se = has ? p_se : 0, stt = has ? p_st : 0;
+#pragma unroll
+  for (int u = 0; u < CU; ++u) {
+    const int b = (int)(bt[u] / (uint32_t)T), t = (int)(bt[u] - (uint32_t)b * T);
+    const float* pb = pbase + b * sb + (int64_t)t * stt;
+    const float a0 = pb[(int64_t)s[u].e0 * se];
+    const float a1 = pb[(int64_t)s[u].e1 * se];
+    p0[u] = has ? a0 : 1.0f;
+    p1[u] = has ? a1 : 1.0f;
+  }
 }
 
 template <int VB, int CU, bool NT>
@@ -408,6 +441,7 @@ __global__ __launch_bounds__(kCT) void permute_chunk_kernel(
   const uint32_t total = (uint32_t)BT * (uint32_t)CH;
   const uint32_t base = blockIdx.x * (kCT * CU) + threadIdx.x;
   V v[CU];
+  SlotsRaw raw[CU];
   Slots2 s[CU];
   uint32_t bt[CU], c[CU];
 #pragma unroll
@@ -416,43 +450,46 @@ __global__ __launch_bounds__(kCT) void permute_chunk_kernel(
     const uint32_t q = idx < total ? idx : total - 1;  // dead lanes re-read the last chunk
     bt[u] = q / (uint32_t)CH;
     c[u] = q - bt[u] * (uint32_t)CH;
-    s[u] = load_slots2(rmap + (int64_t)bt[u] * (2 * E + 1), E);
+    raw[u] = load_slots_raw(rmap + (int64_t)bt[u] * (2 * E + 1), E);
     v[u] = __builtin_nontemporal_load(
         reinterpret_cast<const V*>(inp + (int64_t)bt[u] * row_bytes + (int64_t)c[u] * VB));
   }
+  // every chunk's first-level loads issue before any of their values is used
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int u = 0; u < CU; ++u) s[u] = decode_slots(raw[u]);
   float p0[CU], p1[CU];
+  gate_pair<CU>(probs, rmap, p_sb, p_se, p_st, T, bt, s, p0, p1);
+  // The rows of slots 0 and 1, taken in straight-line code once every load is
+  // in flight: the empty asm defines them here, so neither they nor their
+  // loads can sink into the per-lane store branches below (a load sunk there
+  // would issue only after the previous chunk's stores).
+  const bool has = probs != nullptr;
+  V o0[CU], o1[CU];
 #pragma unroll
   for (int u = 0; u < CU; ++u) {
-    p0[u] = p1[u] = 1.0f;
-    if (probs != nullptr) {
-      const int b = (int)(bt[u] / (uint32_t)T), t = (int)(bt[u] - (uint32_t)b * T);
-      const float* pb = probs + b * p_sb + (int64_t)t * p_st;
-      p0[u] = pb[(int64_t)s[u].e0 * p_se];
-      p1[u] = pb[(int64_t)s[u].e1 * p_se];
-    }
+    o0[u] = has && p0[u] == 0.0f ? V{} : v[u];
+    o1[u] = has && p1[u] == 0.0f ? V{} : v[u];
+    asm volatile("" : "+v"(o0[u]), "+v"(o1[u]));
   }
 #pragma unroll
   for (int u = 0; u < CU; ++u) {
     if (base + u * kCT >= total) continue;
     const int b = (int)(bt[u] / (uint32_t)T), t = (int)(bt[u] - (uint32_t)b * T);
     uint8_t* dst_b = out + (int64_t)b * num_out * row_bytes + (int64_t)c[u] * VB;
-    auto put = [&](int row, float pr) __attribute__((always_inline)) {
+    auto put = [&](int row, float pr, const V& o) __attribute__((always_inline)) {
       if (row < 0 || row >= num_out) return;
-      V o = v[u];
-      if (probs != nullptr) {
-        if (pr == 0.0f) o = V{};
-        if (c[u] == 0) pprobs[(int64_t)b * num_out + row] = pr;
-      }
+      if (has && c[u] == 0) pprobs[(int64_t)b * num_out + row] = pr;
       store_vec<NT>(reinterpret_cast<V*>(dst_b + (int64_t)row * row_bytes), o);
     };
     const int n = s[u].n;
-    if (n > 0) put(s[u].r0, p0[u]);
-    if (n > 1) put(s[u].r1, p1[u]);
+    if (n > 0) put(s[u].r0, p0[u], o0[u]);
+    if (n > 1) put(s[u].r1, p1[u], o1[u]);
     const int32_t* rm = rmap + (int64_t)bt[u] * (2 * E + 1);
     for (int j = 2; j < n; ++j) {
       const float pr =
-          probs != nullptr ? probs[b * p_sb + (int64_t)rm[E + j] * p_se + (int64_t)t * p_st] : 1.0f;
-      put(rm[j], pr);
+          has ? probs[b * p_sb + (int64_t)rm[E + j] * p_se + (int64_t)t * p_st] : 1.0f;
+      put(rm[j], pr, has && pr == 0.0f ? V{} : v[u]);
     }
   }
 }
@@ -468,6 +505,7 @@ __global__ __launch_bounds__(kCT) void unpermute_chunk_kernel(
   using VO = typename Vec<(int)sizeof(S) * VE>::T;
   const uint32_t total = (uint32_t)BT * (uint32_t)CH;
   const uint32_t base = blockIdx.x * (kCT * CU) + threadIdx.x;
+  SlotsRaw raw[CU];
   Slots2 s[CU];
   uint32_t bt[CU], c[CU];
 #pragma unroll
@@ -476,27 +514,28 @@ __global__ __launch_bounds__(kCT) void unpermute_chunk_kernel(
     const uint32_t q = idx < total ? idx : total - 1;
     bt[u] = q / (uint32_t)CH;
     c[u] = q - bt[u] * (uint32_t)CH;
-    s[u] = load_slots2(rmap + (int64_t)bt[u] * (2 * E + 1), E);
+    raw[u] = load_slots_raw(rmap + (int64_t)bt[u] * (2 * E + 1), E);
   }
+  // every chunk's slot loads issue before any is used
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int u = 0; u < CU; ++u) s[u] = decode_slots(raw[u]);
   float p0[CU], p1[CU];
   VO x0[CU], x1[CU];
   bool ok0[CU], ok1[CU];
+  gate_pair<CU>(probs, rmap, p_sb, p_se, p_st, T, bt, s, p0, p1);
 #pragma unroll
   for (int u = 0; u < CU; ++u) {
-    const int b = (int)(bt[u] / (uint32_t)T), t = (int)(bt[u] - (uint32_t)b * T);
-    p0[u] = p1[u] = 1.0f;
-    if (probs != nullptr) {
-      const float* pb = probs + b * p_sb + (int64_t)t * p_st;
-      p0[u] = pb[(int64_t)s[u].e0 * p_se];
-      p1[u] = pb[(int64_t)s[u].e1 * p_se];
-    }
+    const int b = (int)(bt[u] / (uint32_t)T);
     const S* src_b = inp + (int64_t)b * num_out * H + (int64_t)c[u] * VE;
     ok0[u] = s[u].n > 0 && s[u].r0 >= 0 && s[u].r0 < num_out;
     ok1[u] = s[u].n > 1 && s[u].r1 >= 0 && s[u].r1 < num_out;
-    x0[u] = VO{};
-    x1[u] = VO{};
-    if (ok0[u]) x0[u] = __builtin_nontemporal_load(reinterpret_cast<const VO*>(src_b + (int64_t)s[u].r0 * H));
-    if (ok1[u]) x1[u] = __builtin_nontemporal_load(reinterpret_cast<const VO*>(src_b + (int64_t)s[u].r1 * H));
+    // both gathers from valid rows (row 0 for an empty slot; num_out >= 1 is
+    // checked on the host) and unconditional, so they are in flight together
+    x0[u] = __builtin_nontemporal_load(
+        reinterpret_cast<const VO*>(src_b + (int64_t)(ok0[u] ? s[u].r0 : 0) * H));
+    x1[u] = __builtin_nontemporal_load(
+        reinterpret_cast<const VO*>(src_b + (int64_t)(ok1[u] ? s[u].r1 : 0) * H));
   }
 #pragma unroll
   for (int u = 0; u < CU; ++u) {
@@ -922,7 +961,7 @@ extern "C" int uttt_permute_fwd(const void* inp, int dtype, int B, int T, int H,
       UTTT_REQUIRE(chunks < (1ll << 31), "permute_fwd: payload too large (%lld chunks)",        \
                    (long long)chunks);                                                          \
       const unsigned grid = (unsigned)((chunks + kCT * kCU - 1) / (kCT * kCU));                 \
-      hipLaunchKernelGGL((permute_chunk_kernel<VBv, kCU, kNT>), dim3(grid), dim3(kCT), 0, st,               \
+      hipLaunchKernelGGL((permute_chunk_kernel<VBv, kCU, kNT>), dim3(grid), dim3(kCT), 0, st,   \
                          reinterpret_cast<const uint8_t*>(inp), row_bytes, CH, B * T, T,        \
                          row_id_map, E, probs, p_sb, p_se, p_st,                                \
                          reinterpret_cast<uint8_t*>(out), num_out, permuted_probs);             \
@@ -970,6 +1009,11 @@ extern "C" int uttt_unpermute_fwd(const void* inp, int dtype, int B, int num_out
   UTTT_REQUIRE(B >= 0 && T >= 0 && H >= 0 && E >= 1 && num_out >= 0, "unpermute_fwd: bad sizes");
   if (B == 0 || T == 0 || H == 0) return UTTT_OK;
   hipStream_t st = as_stream(stream);
+  if (num_out == 0) {  // no slot holds a row: every output row is the empty sum
+    const int eb = dtype_bytes(dtype);
+    UTTT_REQUIRE(eb > 0, "unpermute_fwd: unsupported dtype %d", dtype);
+    return zero_fill_async(out, (size_t)B * T * H * eb, st, "unpermute_fwd");
+  }
   UTTT_DTYPE_SWITCH(dtype, TT, {
     using S = typename TT::S;
     const int ve = pick_ve<TT>(H, {inp, out});
