@@ -614,156 +614,114 @@ struct TokenTile {
   int n0;      // first token of this tile, relative to the segment
 };
 
-template <int BN>
-__device__ TokenTile find_token_tile(const int32_t* __restrict__ gs_b, int E, int N, int tile,
-                                     int* s_scratch /* >= 4 ints */) {
-  if (threadIdx.x < 64) {
-    const int lane = threadIdx.x;
-    int tok_base = 0, tile_base = 0;
-    int found_e = -1, found_start = 0, found_size = 0, found_n0 = 0;
-    for (int e0 = 0; e0 < E; e0 += 64) {
-      const int e = e0 + lane;
-      const int graw = e < E ? gs_b[e] : 0;
-      const int g = graw > 0 ? graw : 0;
-      int tok_incl = g;
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const int a = __shfl_up(tok_incl, d, 64);
-        if (lane >= d) tok_incl += a;
-      }
-      const int start = tok_base + tok_incl - g;
-      const int avail = start < N ? N - start : 0;
-      const int gc = g < avail ? g : avail;
-      const int nt = (gc + BN - 1) / BN;
-      int tile_incl = nt;
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const int b = __shfl_up(tile_incl, d, 64);
-        if (lane >= d) tile_incl += b;
-      }
-      const int tile_excl = tile_base + tile_incl - nt;
-      const bool hit = e < E && tile >= tile_excl && tile < tile_excl + nt;
-      const uint64_t bal = __ballot(hit);
-      if (bal != 0ull) {
-        const int src = __ffsll((unsigned long long)bal) - 1;
-        found_e = e0 + src;
-        found_start = __shfl(start, src, 64);
-        found_size = __shfl(gc, src, 64);
-        found_n0 = (tile - __shfl(tile_excl, src, 64)) * BN;
-        break;
-      }
-      tok_base += __shfl(tok_incl, 63, 64);
-      tile_base += __shfl(tile_incl, 63, 64);
-    }
-    if (lane == 0) {
-      s_scratch[0] = found_e;
-      s_scratch[1] = found_start;
-      s_scratch[2] = found_size;
-      s_scratch[3] = found_n0;
-    }
-  }
-  __syncthreads();
-  // wave-uniform: the tile origins built from these live in scalar registers
-  return TokenTile{__builtin_amdgcn_readfirstlane(s_scratch[0]),
-                   __builtin_amdgcn_readfirstlane(s_scratch[1]),
-                   __builtin_amdgcn_readfirstlane(s_scratch[2]),
-                   __builtin_amdgcn_readfirstlane(s_scratch[3])};
+// Wave-wide sums with DPP adds (no LDS round trip): the inclusive prefix
+// sum over the 64 lanes (row shifts by 1, 2, 4, 8 inside each 16-lane row,
+// then row 15 and lane 31 broadcast into the later rows), and a lane's value
+// read by every lane.  Lanes outside a shift's row take the added 0.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ int dpp_add_src(int x) {
+  return __builtin_amdgcn_update_dpp(0, x, CTRL, ROWS, 0xf, false);
+}
+__device__ __forceinline__ int wave_incl_scan(int x) {
+  x += dpp_add_src<0x111, 0xf>(x);  // row_shr:1
+  x += dpp_add_src<0x112, 0xf>(x);  // row_shr:2
+  x += dpp_add_src<0x114, 0xf>(x);  // row_shr:4
+  x += dpp_add_src<0x118, 0xf>(x);  // row_shr:8
+  x += dpp_add_src<0x142, 0xa>(x);  // row_bcast:15 into rows 1 and 3
+  x += dpp_add_src<0x143, 0xc>(x);  // row_bcast:31 into rows 2 and 3
+  return x;
+}
+__device__ __forceinline__ int lane_value(int x, int lane) {
+  return __builtin_amdgcn_readlane(x, lane);
 }
 
-// Number of BN-token tiles over all experts of one batch (the count
-// find_token_tile enumerates), with the same clamping of segments to [0, N).
+// The token tile of one workgroup.  Every wave scans group_sizes itself (the
+// same result in each: no LDS broadcast and no barrier before the first
+// loads).
+template <int BN>
+__device__ TokenTile find_token_tile(const int32_t* __restrict__ gs_b, int E, int N, int tile) {
+  const int lane = threadIdx.x & 63;
+  int tok_base = 0, tile_base = 0;
+  for (int e0 = 0; e0 < E; e0 += 64) {
+    const int e = e0 + lane;
+    const int graw = e < E ? gs_b[e] : 0;
+    const int g = graw > 0 ? graw : 0;
+    const int tok_incl = wave_incl_scan(g);
+    const int start = min(tok_base + tok_incl - g, N);
+    const int gc = min(g, N - start);
+    const int nt = (gc + BN - 1) / BN;
+    const int tile_incl = wave_incl_scan(nt);
+    const int tile_excl = tile_base + tile_incl - nt;
+    const bool hit = e < E && tile >= tile_excl && tile < tile_excl + nt;
+    const uint64_t bal = __ballot(hit);
+    if (bal != 0ull) {
+      const int src = __ffsll((unsigned long long)bal) - 1;
+      return TokenTile{__builtin_amdgcn_readfirstlane(e0 + src), lane_value(start, src),
+                       lane_value(gc, src), (tile - lane_value(tile_excl, src)) * BN};
+    }
+    tok_base += lane_value(tok_incl, 63);
+    tile_base += lane_value(tile_incl, 63);
+  }
+  return TokenTile{-1, 0, 0, 0};
+}
+
 // The expert-major pair of workgroup `bid` when the real pairs (token tiles x
-// M m-tiles, counted here) are cut into kXcds equal ranges, workgroup bid
-// taking the (bid / kXcds)-th pair of range bid % kXcds: one wave counts the
-// token tiles and finds the pair in registers (one read of group_sizes, one
-// barrier); e = -1 for a workgroup past its range.
+// M m-tiles, the tiles counted with find_token_tile's clamping of segments to
+// [0, N)) are cut into kXcds equal ranges, workgroup bid taking the
+// (bid / kXcds)-th pair of range bid % kXcds: every wave counts the token
+// tiles and finds the pair in registers (no LDS, no barrier); e = -1 for a
+// workgroup past its range.
 template <int BN>
 __device__ TokenTile find_pair_em_xcd(const int32_t* __restrict__ gs_b, int E, int N, int M,
-                                      int bid, int* mt, int* s_scratch /* >= 5 ints */) {
-  if (threadIdx.x < 64) {
-    const int lane = threadIdx.x;
-    int found_e = -1, found_start = 0, found_size = 0, found_n0 = 0, found_mt = 0;
-    // pass 1: total token tiles R
-    int tok_base = 0, R = 0;
-    for (int e0 = 0; e0 < E; e0 += 64) {
-      const int e = e0 + lane;
-      const int graw = e < E ? gs_b[e] : 0;
-      const int g = graw > 0 ? graw : 0;
-      int tok_incl = g;
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const int a = __shfl_up(tok_incl, d, 64);
-        if (lane >= d) tok_incl += a;
-      }
-      const int start = tok_base + tok_incl - g;
-      const int avail = start < N ? N - start : 0;
-      const int gc = g < avail ? g : avail;
-      int nt = (gc + BN - 1) / BN;
-#pragma unroll
-      for (int d = 32; d >= 1; d >>= 1) nt += __shfl_xor(nt, d, 64);
-      R += nt;
-      tok_base += __shfl(tok_incl, 63, 64);
-    }
-    const int64_t total = (int64_t)R * M;
-    const int64_t per = (total + kXcds - 1) / kXcds;
-    const int64_t loc = bid / kXcds;
-    const int64_t t = (int64_t)(bid % kXcds) * per + loc;
-    if (loc < per && t < total) {
-      // pass 2: the expert whose pairs hold t (group_sizes are in L1 now)
-      tok_base = 0;
-      int64_t pair_base = 0;
-      for (int e0 = 0; e0 < E; e0 += 64) {
-        const int e = e0 + lane;
-        const int graw = e < E ? gs_b[e] : 0;
-        const int gg = graw > 0 ? graw : 0;
-        int tok_incl = gg;
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-          const int a = __shfl_up(tok_incl, d, 64);
-          if (lane >= d) tok_incl += a;
-        }
-        const int start = tok_base + tok_incl - gg;
-        const int avail = start < N ? N - start : 0;
-        const int gc = gg < avail ? gg : avail;
-        const int nt = (gc + BN - 1) / BN;
-        int64_t pairs_incl = (int64_t)nt * M;
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-          const int64_t b = __shfl_up(pairs_incl, d, 64);
-          if (lane >= d) pairs_incl += b;
-        }
-        const int64_t pairs_excl = pair_base + pairs_incl - (int64_t)nt * M;
-        const bool hit = e < E && nt > 0 && t >= pairs_excl && t < pairs_excl + (int64_t)nt * M;
-        const uint64_t bal = __ballot(hit);
-        if (bal != 0ull) {
-          const int src = __ffsll((unsigned long long)bal) - 1;
-          const int ntb = __shfl(nt, src, 64);
-          const int64_t local = t - __shfl(pairs_excl, src, 64);
-          found_e = e0 + src;
-          found_start = __shfl(start, src, 64);
-          found_size = __shfl(gc, src, 64);
-          found_n0 = (int)(local % ntb) * BN;
-          found_mt = (int)(local / ntb);
-          break;
-        }
-        tok_base += __shfl(tok_incl, 63, 64);
-        pair_base += __shfl(pairs_incl, 63, 64);
-      }
-    }
-    if (lane == 0) {
-      s_scratch[0] = found_e;
-      s_scratch[1] = found_start;
-      s_scratch[2] = found_size;
-      s_scratch[3] = found_n0;
-      s_scratch[4] = found_mt;
-    }
+                                      int bid, int* mt) {
+  const int lane = threadIdx.x & 63;
+  // pass 1: total token tiles R
+  int tok_base = 0, R = 0;
+  for (int e0 = 0; e0 < E; e0 += 64) {
+    const int e = e0 + lane;
+    const int graw = e < E ? gs_b[e] : 0;
+    const int g = graw > 0 ? graw : 0;
+    const int tok_incl = wave_incl_scan(g);
+    const int start = min(tok_base + tok_incl - g, N);
+    const int gc = min(g, N - start);
+    R += lane_value(wave_incl_scan((gc + BN - 1) / BN), 63);
+    tok_base += lane_value(tok_incl, 63);
   }
-  __syncthreads();
-  *mt = __builtin_amdgcn_readfirstlane(s_scratch[4]);
-  return TokenTile{__builtin_amdgcn_readfirstlane(s_scratch[0]),
-                   __builtin_amdgcn_readfirstlane(s_scratch[1]),
-                   __builtin_amdgcn_readfirstlane(s_scratch[2]),
-                   __builtin_amdgcn_readfirstlane(s_scratch[3])};
+  const int64_t total = (int64_t)R * M;
+  const int64_t per = (total + kXcds - 1) / kXcds;
+  const int64_t loc = bid / kXcds;
+  const int64_t t = (int64_t)(bid % kXcds) * per + loc;
+  *mt = 0;
+  if (loc >= per || t >= total) return TokenTile{-1, 0, 0, 0};
+  // pass 2: the expert whose pairs hold t (group_sizes are in L1 now); the
+  // pair counts fit in 32 bits (tiles of a batch times the m-tiles)
+  tok_base = 0;
+  int pair_base = 0;
+  const int ti = (int)t;
+  for (int e0 = 0; e0 < E; e0 += 64) {
+    const int e = e0 + lane;
+    const int graw = e < E ? gs_b[e] : 0;
+    const int gg = graw > 0 ? graw : 0;
+    const int tok_incl = wave_incl_scan(gg);
+    const int start = min(tok_base + tok_incl - gg, N);
+    const int gc = min(gg, N - start);
+    const int nt = (gc + BN - 1) / BN;
+    const int pairs_incl = wave_incl_scan(nt * M);
+    const int pairs_excl = pair_base + pairs_incl - nt * M;
+    const bool hit = e < E && nt > 0 && ti >= pairs_excl && ti < pairs_excl + nt * M;
+    const uint64_t bal = __ballot(hit);
+    if (bal != 0ull) {
+      const int src = __ffsll((unsigned long long)bal) - 1;
+      const int ntb = lane_value(nt, src);
+      const int local = ti - lane_value(pairs_excl, src);
+      *mt = local / ntb;
+      return TokenTile{__builtin_amdgcn_readfirstlane(e0 + src), lane_value(start, src),
+                       lane_value(gc, src), (local % ntb) * BN};
+    }
+    tok_base += lane_value(tok_incl, 63);
+    pair_base += lane_value(pairs_incl, 63);
+  }
+  return TokenTile{-1, 0, 0, 0};
 }
 
 

@@ -737,8 +737,6 @@ template <int AMAJ, class Epi, bool SKIP>
 __global__ __launch_bounds__(kThreads) void tn_kernel(TnArgs a, typename Epi::Args ea) {
   __shared__ __attribute__((aligned(16))) uint8_t st0[kStageBytes];
   __shared__ __attribute__((aligned(16))) uint8_t st1[kStageBytes];
-  // the tile lookup's 4 ints live in the last stage: it is done before any load
-  int* scratch = reinterpret_cast<int*>(st1);
 
   // Tile order: workgroup i runs on XCD i % kXcds, each XCD with its own L2.
   // The (m-tile, n-tile) plane (n-tiles of all batches in a row) is cut into
@@ -762,8 +760,7 @@ __global__ __launch_bounds__(kThreads) void tn_kernel(TnArgs a, typename Epi::Ar
   }
   if (mt >= a.m_tiles || ntg >= a.B * a.n_tiles_ub) return;  // padding of the super-tile grid
   const int b = ntg / a.n_tiles_ub, nt = ntg % a.n_tiles_ub;
-  const TokenTile tt = find_token_tile<kBRows>(a.gs + (int64_t)b * a.E, a.E, a.N, nt, scratch);
-  __syncthreads();  // every wave has read the lookup before stage 1 is loaded
+  const TokenTile tt = find_token_tile<kBRows>(a.gs + (int64_t)b * a.E, a.E, a.N, nt);
   if (tt.e < 0 || (a.sym && mt * a.m_step > tt.n0)) return;
   const int m0 = mt * a.m_step;
 
@@ -1065,8 +1062,6 @@ __device__ __forceinline__ void ap_loop(TileLoader<KMajor>& la0, TileLoader<KMaj
 template <class Epi, bool TWO>
 __global__ __launch_bounds__(kThreads) void apply_kernel(ApArgs a, typename Epi::Args ea) {
   __shared__ __attribute__((aligned(16))) uint8_t ring[3 * kApStageBytes];
-  // the tile lookup's 4 ints live in the third stage, loaded last
-  int* scratch = reinterpret_cast<int*>(ring + 2 * kApStageBytes);
   const int bid = blockIdx.x;
   int mt, b;
   TokenTile tt;
@@ -1077,7 +1072,7 @@ __global__ __launch_bounds__(kThreads) void apply_kernel(ApArgs a, typename Epi:
     // weight slices once and reuses it from L2 for that expert's token tiles,
     // and reads a small expert's tokens once for all its m-tiles.  Workgroups
     // past their XCD's range leave at once.
-    tt = find_pair_em_xcd<kApTok>(a.gs, a.E, a.N, a.m_tiles, bid, &mt, scratch);
+    tt = find_pair_em_xcd<kApTok>(a.gs, a.E, a.N, a.m_tiles, bid, &mt);
     b = 0;
   } else {
     const int64_t t = (int64_t)(bid % kXcds) * a.per_xcd + bid / kXcds;
@@ -1086,9 +1081,8 @@ __global__ __launch_bounds__(kThreads) void apply_kernel(ApArgs a, typename Epi:
     const int64_t rest = t / a.n_tiles_ub;
     mt = (int)(rest % a.m_tiles);
     b = (int)(rest / a.m_tiles);
-    tt = find_token_tile<kApTok>(a.gs + (int64_t)b * a.E, a.E, a.N, nt, scratch);
+    tt = find_token_tile<kApTok>(a.gs + (int64_t)b * a.E, a.E, a.N, nt);
   }
-  __syncthreads();  // every wave has read the lookup before the third stage is loaded
   if (tt.e < 0) return;
   const int m0 = mt * a.m_step;
   const int64_t ag = ((int64_t)b * a.E + tt.e) * a.a_group;
