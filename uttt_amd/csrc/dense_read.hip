@@ -84,16 +84,34 @@ __global__ __launch_bounds__(kReadWaves * 64) void dense_read_kernel(
   for (int u = 0; u < UB; ++u) {
     const int blk = w + kReadWaves * u;
     if (blk >= nblk) break;  // wave-uniform
-    // 1. Y0, Y2 for hidden units blk*32 .. +32 (A = weight rows, B = x^T)
+    // every weight fragment of the block is requested before the first
+    // product: the L2 latency is paid once per block, not once per k step
     const uint16_t* a0 = w0h + (int64_t)(blk * 32 + r) * D + 8 * g;
     const uint16_t* a2 = a0 + (int64_t)I * D;
+    bf16x8_t a0f[KS], a2f[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      a0f[s] = ld16(a0 + 16 * s);
+      a2f[s] = ld16(a2 + 16 * s);
+    }
+    bf16x4_t w1f[2][DB][2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const uint16_t* b1 = w1h + (int64_t)(db * 32 + r) * I + blk * 32 + 16 * q + 4 * g;
+        w1f[q][db][0] = ld8(b1);
+        w1f[q][db][1] = ld8(b1 + 8);
+      }
+    __builtin_amdgcn_sched_barrier(0);
+    // 1. Y0, Y2 for hidden units blk*32 .. +32 (A = weight rows, B = x^T)
     f32x16_t y0, y2;
 #pragma unroll
     for (int v = 0; v < 16; ++v) y0[v] = y2[v] = 0.0f;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      y0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld16(a0 + 16 * s), xf[s], y0, 0, 0, 0);
-      y2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld16(a2 + 16 * s), xf[s], y2, 0, 0, 0);
+      y0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0f[s], xf[s], y0, 0, 0, 0);
+      y2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2f[s], xf[s], y2, 0, 0, 0);
     }
     // 2. h: element v of this lane is hidden unit 8 (v / 4) + 4 g + v % 4 of
     //    the block, token t0 + r
@@ -114,8 +132,8 @@ __global__ __launch_bounds__(kReadWaves * 64) void dense_read_kernel(
     for (int q = 0; q < 2; ++q) {
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        const uint16_t* b1 = w1h + (int64_t)(db * 32 + r) * I + blk * 32 + 16 * q + 4 * g;
-        const bf16x8_t a = __builtin_shufflevector(ld8(b1), ld8(b1 + 8), 0, 1, 2, 3, 4, 5, 6, 7);
+        const bf16x8_t a =
+            __builtin_shufflevector(w1f[q][db][0], w1f[q][db][1], 0, 1, 2, 3, 4, 5, 6, 7);
         acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, hq[q], acc[db], 0, 0, 0);
       }
     }
