@@ -479,6 +479,18 @@ int uttt_moe_decode_read_noalloc(const void* x, int B, int T, int D, const void*
 int uttt_dense_read_supported(int D, int I);
 int uttt_dense_read(const void* x, int b, int l, int H, int D, const void* w0_w2, const void* w1,
                     int I, void* out, void* stream);
+/* The same read from a fragment-ordered copy of the weights (no reference
+ * counterpart: a layout of this build for the shared fast-weight bank, whose
+ * twelve reads per chunk share one copy).  uttt_dense_pack_weights writes
+ * packed [BH, 3 I D] bf16 (the bytes of w0_w2 [BH, 2I, D] and w1 [BH, D, I]
+ * regrouped so that each fragment load of the read is 64 lanes x 16
+ * consecutive bytes); uttt_dense_read_packed(x, b, l, H, D, packed, I, out)
+ * gives bit-identical results to uttt_dense_read on the weights packed.
+ * Shapes and alignment as uttt_dense_read, BH = b*H. */
+int uttt_dense_pack_weights(const void* w0_w2, const void* w1, int BH, int D, int I, void* packed,
+                            void* stream);
+int uttt_dense_read_packed(const void* x, int b, int l, int H, int D, const void* packed, int I,
+                           void* out, void* stream);
 
 /* uTTT-Dense head layout (uttt_dense/modeling_recurrent_lact.py, D:).
  * Gather: the head split 'b l (h d) -> (b h) l d' of k and v and

@@ -148,3 +148,43 @@ def test_fused_dense_read(b, H, d, dh, l):
     gs = DN._gs(b * H, l, DEV)
     grouped = DN._unheads(G.gemm_nt(W1, G.gate_up(W02, xh, gs, token_major=True), gs), b, H)
     assert_bf16_close(out, grouped, name="fused read vs grouped route")
+
+
+@pytest.mark.parametrize("b,H,d,dh,l", [
+    (1, 4, 96, 192, 512),     # configs[0]
+    (1, 4, 192, 384, 2048),   # configs[1]
+    (2, 3, 128, 96, 77),
+    (1, 2, 256, 512, 64),
+    (3, 1, 64, 32, 9),
+])
+def test_packed_dense_read_is_bit_identical(b, H, d, dh, l):
+    """The read from the fragment-ordered weight copy (uttt_dense_pack_weights
+    + uttt_dense_read_packed) against the read from the weights as stored:
+    the same operands in the same MFMAs, so the same bits; and the shared
+    bank's reads after a write (the copy is rebuilt) against a fresh read."""
+    g = torch.Generator().manual_seed(3 * l + d)
+    w0, w2 = ((torch.randn(b, H, dh, d, generator=g) / d ** 0.5).to(torch.bfloat16)
+              for _ in range(2))
+    w1 = (torch.randn(b, H, d, dh, generator=g) / dh ** 0.5).to(torch.bfloat16)
+    q = torch.randn(b, l, H * d, generator=g).to(torch.bfloat16).to(DEV)
+    W02 = torch.cat([w0, w2], dim=2).reshape(b * H, 1, 2 * dh, d).contiguous().to(DEV)
+    W1 = w1.reshape(b * H, 1, d, dh).contiguous().to(DEV)
+    ref = DN._read(q, W02, W1, b, H)
+    P = DN._pack(W02, W1)
+    assert P is not None and P.numel() == b * H * 3 * dh * d
+    got = DN._read_packed(q, P, W02, W1, b, H)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    if dh % d == 0:
+        # one-layer write: the first read uses W02/W1, the second the copy
+        # packed then; two-layer write: the copy is packed at the write
+        bank = DN.SharedFastWeights(w0.to(DEV), w1.to(DEV), w2.to(DEV), dh // d)
+        for n_layers in (1, 2, 1):
+            lay = [_layer(b, l, H, d, 5 + i) for i in range(n_layers)]
+            bank.write([x[1].to(DEV) for x in lay], [x[2].to(DEV) for x in lay],
+                       [x[3].to(DEV) for x in lay])
+            ref2 = DN._read(q, bank.W02, bank.W1, b, H)
+            for _ in range(2):
+                got2 = bank.read(q)
+                torch.cuda.synchronize()
+                assert torch.equal(got2.view(torch.int16), ref2.view(torch.int16)), n_layers

@@ -85,6 +85,10 @@ SIGNATURES = {
     "uttt_dense_read": (
         c_int, [c_p, c_int, c_int, c_int, c_int, c_p, c_p, c_int, c_p, c_p],
     ),
+    "uttt_dense_pack_weights": (c_int, [c_p, c_p, c_int, c_int, c_int, c_p, c_p]),
+    "uttt_dense_read_packed": (
+        c_int, [c_p, c_int, c_int, c_int, c_int, c_p, c_int, c_p, c_p],
+    ),
     "uttt_grouped_wgrad_pair": (
         c_int,
         [c_p, c_p, c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int, c_p, c_p, c_p, c_sz, c_p],

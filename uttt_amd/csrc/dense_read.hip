@@ -49,7 +49,51 @@ __device__ __forceinline__ float silu_mul(float y0, float y2) {
   return y2 * (y0 * __builtin_amdgcn_rcpf(1.0f + __expf(-y0)));
 }
 
-template <int D, int UB>
+// Fragment-ordered copy of one head's weights (uttt_dense_pack_weights), the
+// same bytes as W0_W2 [2I, D] and W1 [D, I] regrouped so that each of the
+// read's fragment loads is 64 lanes x 16 consecutive bytes (8 cache lines)
+// instead of 16 bytes from each of 32 weight rows:
+//   W0 / W2 part m (0 / 1): [I/32 blocks][D/16 k steps][64 lanes][8], lane
+//     (r, g) holding row 32 blk + r, columns 16 s + 8 g .. + 8 of W_m;
+//   W1 part: [I/32 blocks][2 halves q][D/32 column blocks db][64 lanes][8],
+//     lane (r, g) holding W1[32 db + r][32 blk + 16 q + 4 g .. + 4] then
+//     W1[32 db + r][32 blk + 16 q + 8 + 4 g .. + 4].
+__host__ __device__ constexpr int64_t packed_head_elems(int D, int I) { return (int64_t)3 * I * D; }
+
+__global__ __launch_bounds__(256) void dense_pack_kernel(const uint16_t* __restrict__ w02,
+                                                         const uint16_t* __restrict__ w1, int D,
+                                                         int I, uint16_t* __restrict__ packed) {
+  // 32-bit index math: a head holds at most 3 * 512 * 256 / 8 = 49152 chunks
+  const int bh = blockIdx.y;
+  const int nch = 3 * I * D / 8;  // 16-byte chunks per head
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= nch) return;
+  const int KS = D / 16, DB = D / 32;
+  const int per_mat = I * D / 8;
+  const int lane = c & 63, r = lane & 31, g = lane >> 5;
+  uint4 v;
+  if (c < 2 * per_mat) {
+    const int m = c >= per_mat;
+    const int q = (c - m * per_mat) >> 6;  // blk * KS + s
+    const int blk = q / KS, s = q - blk * KS;
+    const uint16_t* src = w02 + (int64_t)bh * 2 * I * D + (m * I + blk * 32 + r) * D + 16 * s +
+                          8 * g;
+    v = *reinterpret_cast<const uint4*>(src);
+  } else {
+    const int q = (c - 2 * per_mat) >> 6;  // (blk * 2 + half) * DB + db
+    const int qd = q / DB, db = q - qd * DB, half = qd & 1, blk = qd >> 1;
+    const uint16_t* row =
+        w1 + (int64_t)bh * D * I + (db * 32 + r) * I + blk * 32 + 16 * half + 4 * g;
+    const uint2 lo = *reinterpret_cast<const uint2*>(row);
+    const uint2 hi = *reinterpret_cast<const uint2*>(row + 8);
+    v = make_uint4(lo.x, lo.y, hi.x, hi.y);
+  }
+  *reinterpret_cast<uint4*>(packed + (int64_t)bh * packed_head_elems(D, I) + 8 * c) = v;
+}
+
+// PACKED: the weights come from the fragment-ordered copy (w02 = the packed
+// copy, w1 unused).
+template <int D, int UB, bool PACKED>
 __global__ __launch_bounds__(kReadWaves * 64) void dense_read_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w02,
     const uint16_t* __restrict__ w1, int l, int H, int I, uint16_t* __restrict__ out) {
@@ -86,23 +130,38 @@ __global__ __launch_bounds__(kReadWaves * 64) void dense_read_kernel(
     if (blk >= nblk) break;  // wave-uniform
     // every weight fragment of the block is requested before the first
     // product: the L2 latency is paid once per block, not once per k step
-    const uint16_t* a0 = w0h + (int64_t)(blk * 32 + r) * D + 8 * g;
-    const uint16_t* a2 = a0 + (int64_t)I * D;
     bf16x8_t a0f[KS], a2f[KS];
+    bf16x8_t w1f[2][DB];
+    if constexpr (PACKED) {
+      const uint16_t* ph = w02 + (int64_t)bh * packed_head_elems(D, I);
+      const uint16_t* p0 = ph + ((int64_t)blk * KS * 64 + lane) * 8;
+      const uint16_t* p2 = p0 + (int64_t)I * D;
+      const uint16_t* p1 = ph + 2 * (int64_t)I * D + ((int64_t)blk * 2 * DB * 64 + lane) * 8;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      a0f[s] = ld16(a0 + 16 * s);
-      a2f[s] = ld16(a2 + 16 * s);
-    }
-    bf16x4_t w1f[2][DB][2];
-#pragma unroll
-    for (int q = 0; q < 2; ++q)
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const uint16_t* b1 = w1h + (int64_t)(db * 32 + r) * I + blk * 32 + 16 * q + 4 * g;
-        w1f[q][db][0] = ld8(b1);
-        w1f[q][db][1] = ld8(b1 + 8);
+      for (int s = 0; s < KS; ++s) {
+        a0f[s] = ld16(p0 + s * 64 * 8);
+        a2f[s] = ld16(p2 + s * 64 * 8);
       }
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int db = 0; db < DB; ++db) w1f[q][db] = ld16(p1 + (q * DB + db) * 64 * 8);
+    } else {
+      const uint16_t* a0 = w0h + (int64_t)(blk * 32 + r) * D + 8 * g;
+      const uint16_t* a2 = a0 + (int64_t)I * D;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        a0f[s] = ld16(a0 + 16 * s);
+        a2f[s] = ld16(a2 + 16 * s);
+      }
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          const uint16_t* b1 = w1h + (int64_t)(db * 32 + r) * I + blk * 32 + 16 * q + 4 * g;
+          w1f[q][db] = __builtin_shufflevector(ld8(b1), ld8(b1 + 8), 0, 1, 2, 3, 4, 5, 6, 7);
+        }
+    }
     __builtin_amdgcn_sched_barrier(0);
     // 1. Y0, Y2 for hidden units blk*32 .. +32 (A = weight rows, B = x^T)
     f32x16_t y0, y2;
@@ -132,9 +191,7 @@ __global__ __launch_bounds__(kReadWaves * 64) void dense_read_kernel(
     for (int q = 0; q < 2; ++q) {
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        const bf16x8_t a =
-            __builtin_shufflevector(w1f[q][db][0], w1f[q][db][1], 0, 1, 2, 3, 4, 5, 6, 7);
-        acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, hq[q], acc[db], 0, 0, 0);
+        acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w1f[q][db], hq[q], acc[db], 0, 0, 0);
       }
     }
   }
@@ -173,17 +230,30 @@ __global__ __launch_bounds__(kReadWaves * 64) void dense_read_kernel(
   }
 }
 
-template <int D>
+template <int D, bool PACKED>
 int launch_dense_read(int ub, dim3 grid, hipStream_t st, const uint16_t* x, const uint16_t* w02,
                       const uint16_t* w1, int l, int H, int I, uint16_t* out) {
   const dim3 block(kReadWaves * 64);
   switch (ub) {
-    case 1: hipLaunchKernelGGL((dense_read_kernel<D, 1>), grid, block, 0, st, x, w02, w1, l, H, I, out); break;
-    case 2: hipLaunchKernelGGL((dense_read_kernel<D, 2>), grid, block, 0, st, x, w02, w1, l, H, I, out); break;
-    case 3: hipLaunchKernelGGL((dense_read_kernel<D, 3>), grid, block, 0, st, x, w02, w1, l, H, I, out); break;
-    default: hipLaunchKernelGGL((dense_read_kernel<D, 4>), grid, block, 0, st, x, w02, w1, l, H, I, out); break;
+    case 1: hipLaunchKernelGGL((dense_read_kernel<D, 1, PACKED>), grid, block, 0, st, x, w02, w1, l, H, I, out); break;
+    case 2: hipLaunchKernelGGL((dense_read_kernel<D, 2, PACKED>), grid, block, 0, st, x, w02, w1, l, H, I, out); break;
+    case 3: hipLaunchKernelGGL((dense_read_kernel<D, 3, PACKED>), grid, block, 0, st, x, w02, w1, l, H, I, out); break;
+    default: hipLaunchKernelGGL((dense_read_kernel<D, 4, PACKED>), grid, block, 0, st, x, w02, w1, l, H, I, out); break;
   }
   return check_launch("dense_read");
+}
+
+template <bool PACKED>
+int dense_read_dispatch(int D, int ub, dim3 grid, hipStream_t st, const uint16_t* x,
+                        const uint16_t* w02, const uint16_t* w1, int l, int H, int I,
+                        uint16_t* out) {
+  switch (D) {
+    case 64: return launch_dense_read<64, PACKED>(ub, grid, st, x, w02, w1, l, H, I, out);
+    case 96: return launch_dense_read<96, PACKED>(ub, grid, st, x, w02, w1, l, H, I, out);
+    case 128: return launch_dense_read<128, PACKED>(ub, grid, st, x, w02, w1, l, H, I, out);
+    case 192: return launch_dense_read<192, PACKED>(ub, grid, st, x, w02, w1, l, H, I, out);
+    default: return launch_dense_read<256, PACKED>(ub, grid, st, x, w02, w1, l, H, I, out);
+  }
 }
 
 }  // namespace
@@ -210,15 +280,47 @@ extern "C" int uttt_dense_read(const void* x, int b, int l, int H, int D, const 
   const int ub = (I / 32 + kReadWaves - 1) / kReadWaves;
   const dim3 grid((unsigned)((l + kReadTok - 1) / kReadTok), (unsigned)(b * H));
   hipStream_t st = as_stream(stream);
-  const auto* xp = static_cast<const uint16_t*>(x);
-  const auto* wp = static_cast<const uint16_t*>(w0_w2);
-  const auto* w1p = static_cast<const uint16_t*>(w1);
-  auto* op = static_cast<uint16_t*>(out);
-  switch (D) {
-    case 64: return launch_dense_read<64>(ub, grid, st, xp, wp, w1p, l, H, I, op);
-    case 96: return launch_dense_read<96>(ub, grid, st, xp, wp, w1p, l, H, I, op);
-    case 128: return launch_dense_read<128>(ub, grid, st, xp, wp, w1p, l, H, I, op);
-    case 192: return launch_dense_read<192>(ub, grid, st, xp, wp, w1p, l, H, I, op);
-    default: return launch_dense_read<256>(ub, grid, st, xp, wp, w1p, l, H, I, op);
-  }
+  return dense_read_dispatch<false>(D, ub, grid, st, static_cast<const uint16_t*>(x),
+                                    static_cast<const uint16_t*>(w0_w2),
+                                    static_cast<const uint16_t*>(w1), l, H, I,
+                                    static_cast<uint16_t*>(out));
+}
+
+extern "C" int uttt_dense_pack_weights(const void* w0_w2, const void* w1, int BH, int D, int I,
+                                       void* packed, void* stream) {
+  UTTT_REQUIRE(BH >= 0, "dense_pack_weights: bad sizes");
+  UTTT_REQUIRE(uttt_dense_read_supported(D, I),
+               "dense_pack_weights: D=%d must be 64, 96, 128, 192 or 256 and I=%d a multiple of "
+               "32 in [32, 512]", D, I);
+  if (BH == 0) return UTTT_OK;
+  UTTT_REQUIRE(BH <= 65535, "dense_pack_weights: BH=%d exceeds 65535", BH);
+  UTTT_REQUIRE(w0_w2 && w1 && packed, "dense_pack_weights: null pointer");
+  UTTT_REQUIRE(aligned16(w0_w2) && aligned16(w1) && aligned16(packed),
+               "dense_pack_weights: tensors must be 16-byte aligned");
+  const int64_t nch = (int64_t)3 * I * D / 8;
+  const dim3 grid((unsigned)((nch + 255) / 256), (unsigned)BH);
+  hipLaunchKernelGGL(dense_pack_kernel, grid, dim3(256), 0, as_stream(stream),
+                     static_cast<const uint16_t*>(w0_w2), static_cast<const uint16_t*>(w1), D, I,
+                     static_cast<uint16_t*>(packed));
+  return check_launch("dense_pack_weights");
+}
+
+extern "C" int uttt_dense_read_packed(const void* x, int b, int l, int H, int D,
+                                      const void* packed, int I, void* out, void* stream) {
+  UTTT_REQUIRE(b >= 0 && l >= 0 && H >= 1, "dense_read_packed: bad sizes");
+  UTTT_REQUIRE(uttt_dense_read_supported(D, I),
+               "dense_read_packed: D=%d must be 64, 96, 128, 192 or 256 and I=%d a multiple of "
+               "32 in [32, 512]", D, I);
+  if (b == 0 || l == 0) return UTTT_OK;
+  UTTT_REQUIRE((int64_t)b * H <= 65535, "dense_read_packed: b*H=%lld exceeds 65535",
+               (long long)b * H);
+  UTTT_REQUIRE(x && packed && out, "dense_read_packed: null pointer");
+  UTTT_REQUIRE(aligned16(x) && aligned16(packed) && aligned16(out),
+               "dense_read_packed: tensors must be 16-byte aligned");
+  const int ub = (I / 32 + kReadWaves - 1) / kReadWaves;
+  const dim3 grid((unsigned)((l + kReadTok - 1) / kReadTok), (unsigned)(b * H));
+  return dense_read_dispatch<true>(D, ub, grid, as_stream(stream),
+                                   static_cast<const uint16_t*>(x),
+                                   static_cast<const uint16_t*>(packed), nullptr, l, H, I,
+                                   static_cast<uint16_t*>(out));
 }

@@ -139,6 +139,33 @@ def _read(x, W02, W1, b, H):
     return _unheads(G.gemm_nt(W1, hid, gs), b, H)
 
 
+def _pack(W02, W1, packed=None):
+    """The fragment-ordered copy of the weights that uttt_dense_read_packed
+    reads (csrc/dense_read.hip), or None where the fused read does not apply."""
+    BH, d, dh = W02.shape[0], W1.shape[-2], W1.shape[-1]
+    if not L.lib().uttt_dense_read_supported(d, dh):
+        return None
+    if packed is None:
+        packed = torch.empty(BH * 3 * dh * d, dtype=torch.bfloat16, device=W02.device)
+    L.call("uttt_dense_pack_weights", L.ptr(W02), L.ptr(W1), BH, d, dh, L.ptr(packed),
+           L.stream_of(W02))
+    return packed
+
+
+def _read_packed(x, packed, W02, W1, b, H):
+    """_read with the weights' packed copy for the fused read."""
+    d, dh = W1.shape[-2], W1.shape[-1]
+    if packed is None or x.shape[1] <= DECODE_TOKENS:
+        return _read(x, W02, W1, b, H)
+    L.require_device(x)
+    assert x.dim() == 3 and x.shape[2] == H * d, "x: [b, l, H*d]"
+    xb = _bf16_rows(x)
+    out = torch.empty_like(xb)
+    L.call("uttt_dense_read_packed", L.ptr(xb), b, xb.shape[1], H, d, L.ptr(packed), dh,
+           L.ptr(out), L.stream_of(xb))
+    return out
+
+
 def _update(W02, W1, ks, vs, lrs, b, H):
     """The grouped UPDATE of several layers' tokens at once: per head the
     tokens of all layers concatenated.  Returns bf16 (dW0_W2, dW1)."""
@@ -187,10 +214,23 @@ class SharedFastWeights:
         self.W1 = w1.to(torch.bfloat16).reshape(b * H, 1, d, dh).contiguous()
         self._spare02 = torch.empty_like(self.W02)
         self._spare1 = torch.empty_like(self.W1)
+        # The read's fragment-ordered copy of W02/W1 (one extra pass over the
+        # weights) pays off only when the same weights are read more than once:
+        # it is rebuilt at a write that aggregated several layers (the next
+        # chunk's reads are as many), else at the second read after a write.
+        supported = L.lib().uttt_dense_read_supported(d, dh)
+        self.P = (torch.empty(b * H * 3 * dh * d, dtype=torch.bfloat16, device=w0.device)
+                  if supported else None)
+        self._packed, self._reads = False, 0
 
     def read(self, q):
         """One layer's read of a chunk: q [b, l, H*d] -> [b, l, H*d] bf16."""
-        return _read(q, self.W02, self.W1, self.b, self.H)
+        self._reads += 1
+        if self.P is not None and not self._packed and self._reads >= 2:
+            _pack(self.W02, self.W1, self.P)
+            self._packed = True
+        return _read_packed(q, self.P if self._packed else None, self.W02, self.W1, self.b,
+                            self.H)
 
     def write(self, ks, vs, lrs):
         """The chunk's aggregate write from every layer's preprocessed k, v
@@ -209,6 +249,10 @@ class SharedFastWeights:
                L.ptr(self._spare1), None, st)
         self.W02, self._spare02 = self._spare02, self.W02
         self.W1, self._spare1 = self._spare1, self.W1
+        self._reads, self._packed = 0, False
+        if self.P is not None and len(ks) > 1:
+            _pack(self.W02, self.W1, self.P)
+            self._packed = True
 
     def weights(self):
         """((w0, w1, w2) bf16, (w0, w1, w2) fp32 masters) in the reference layout."""
