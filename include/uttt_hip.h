@@ -492,6 +492,25 @@ int uttt_dense_pack_weights(const void* w0_w2, const void* w1, int BH, int D, in
 int uttt_dense_read_packed(const void* x, int b, int l, int H, int D, const void* packed, int I,
                            void* out, void* stream);
 
+/* uTTT-Dense UPDATE stage 1, fused for small heads (replaces the two grouped
+ * products of uttt_grouped_update_stage1 with E = 1 for the dense write:
+ * uttt_dense/modeling_recurrent_lact.py:409-432, gate_before_act,
+ * hidden_before_mul, dhidden and silu_backprop, the lr factors of :425-432
+ * applied to DY0 / Hid / DY2).  k, v [BH, N, D] bf16 (one head per BH, the
+ * layers' tokens concatenated), lr0/1/2 [BH, N] fp32 (all three or none:
+ * none means 1), dy [BH, N, 2I] and hid [BH, N, I] bf16, token-major as
+ * uttt_grouped_update_stage1's token_major output.  The weights come as a
+ * fragment-ordered copy [BH, 3 I D] bf16 written by
+ * uttt_dense_pack_update_weights from w0_w2 [BH, 2I, D] and w1 [BH, D, I]
+ * (a layout of this build, no reference counterpart).  D in {64, 96, 128,
+ * 192, 256}, I a multiple of 32 in [32, 512] (uttt_dense_update_supported). */
+int uttt_dense_update_supported(int D, int I);
+int uttt_dense_pack_update_weights(const void* w0_w2, const void* w1, int BH, int D, int I,
+                                   void* packed, void* stream);
+int uttt_dense_update_stage1(const void* k, const void* v, const void* lr0, const void* lr1,
+                             const void* lr2, int BH, int N, int D, int I, const void* packed,
+                             void* dy, void* hid, void* stream);
+
 /* uTTT-Dense head layout (uttt_dense/modeling_recurrent_lact.py, D:).
  * Gather: the head split 'b l (h d) -> (b h) l d' of k and v and
  * 'b l h -> (b h) l 1' of the three lr columns in compute_update (D:370-398;

@@ -188,3 +188,45 @@ def test_packed_dense_read_is_bit_identical(b, H, d, dh, l):
                 got2 = bank.read(q)
                 torch.cuda.synchronize()
                 assert torch.equal(got2.view(torch.int16), ref2.view(torch.int16)), n_layers
+
+
+@pytest.mark.parametrize("BH,N,d,dh,with_lr", [
+    (4, 3000, 192, 384, True),   # configs[1] head, ragged token tiles
+    (4, 1024, 96, 192, True),    # configs[0] head
+    (2, 77, 128, 96, True),      # one partial tile
+    (3, 128, 64, 32, False),     # one hidden block, lr = 1
+    (1, 513, 256, 512, True),    # the largest head
+])
+def test_fused_dense_update_stage1(BH, N, d, dh, with_lr):
+    """csrc/dense_update.hip (fused stage 1 for small heads: Y0, Y2, DH on
+    MFMA, the SwiGLU-derivative epilogue in registers) against the grouped
+    stage 1 with one expert (the same rounding points: fp32 Y and DH, one
+    bf16 rounding of each output)."""
+    from uttt_amd import _lib as L
+    from uttt_amd.lact_moe_triton import _grouped as G
+
+    assert L.lib().uttt_dense_update_supported(d, dh)
+    g = torch.Generator().manual_seed(N + d)
+    W02 = (torch.randn(BH, 1, 2 * dh, d, generator=g) / d ** 0.5).to(torch.bfloat16).to(DEV)
+    W1 = (torch.randn(BH, 1, d, dh, generator=g) / dh ** 0.5).to(torch.bfloat16).to(DEV)
+    kh, vh = (torch.nn.functional.normalize(torch.randn(BH, N, d, generator=g), dim=-1)
+              .to(torch.bfloat16).to(DEV) for _ in range(2))
+    lr3 = ([(torch.sigmoid(torch.randn(BH, N, generator=g)) * 0.1).to(DEV) for _ in range(3)]
+           if with_lr else None)
+    gs = DN._gs(BH, N, DEV)
+    dy, hl = DN._update_stage1(W02, W1, kh, vh, lr3, gs)
+    ref_dy, ref_hl = G.update_stage1(W02, W1, kh, vh, *(lr3 or (None,) * 3), gs,
+                                     token_major=True)
+    torch.cuda.synchronize()
+    assert dy.shape == (BH, N, 2 * dh) and hl.shape == (BH, N, dh)
+    assert_bf16_close(dy.cpu(), ref_dy.cpu(), name="DY0_DY2")
+    assert_bf16_close(hl.cpu(), ref_hl.cpu(), name="Hid")
+    # same products in the same k order on the same MFMA, same epilogue: the
+    # two routes agree bit for bit (measured at the configs[0] and [1] heads)
+    if (d, dh) in ((192, 384), (96, 192)):
+        assert torch.equal(dy.view(torch.int16), ref_dy.view(torch.int16))
+        assert torch.equal(hl.view(torch.int16), ref_hl.view(torch.int16))
+    # a second call into the same weight copy: same bits
+    dy2, hl2 = DN._update_stage1(W02, W1, kh, vh, lr3, gs, DN._pack_update(W02, W1))
+    torch.cuda.synchronize()
+    assert torch.equal(dy2, dy) and torch.equal(hl2, hl)

@@ -89,6 +89,11 @@ SIGNATURES = {
     "uttt_dense_read_packed": (
         c_int, [c_p, c_int, c_int, c_int, c_int, c_p, c_int, c_p, c_p],
     ),
+    "uttt_dense_update_supported": (c_int, [c_int, c_int]),
+    "uttt_dense_pack_update_weights": (c_int, [c_p, c_p, c_int, c_int, c_int, c_p, c_p]),
+    "uttt_dense_update_stage1": (
+        c_int, [c_p, c_p, c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_p, c_p, c_p, c_p],
+    ),
     "uttt_grouped_wgrad_pair": (
         c_int,
         [c_p, c_p, c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int, c_p, c_p, c_p, c_sz, c_p],

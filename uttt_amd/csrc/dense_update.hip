@@ -1,0 +1,232 @@
+// uTTT-Dense UPDATE stage 1 for small heads, fused: per head and token
+//   Y0 = W0 k, Y2 = W2 k, DH = W1^T v            (fp32, K = D)
+//   DY0 = sigmoid(Y0) Y2 DH (1 + Y0 (1 - sigmoid(Y0))) lr0
+//   DY2 = silu(Y0) DH lr2,   Hid = silu(Y0) Y2 lr1   (stored bf16)
+// Reference: compute_update, uttt_dense/modeling_recurrent_lact.py:409-432
+// (gate_before_act, hidden_before_mul, dhidden, silu_backprop; the lr factors
+// of dw0 / dw1 / dw2 at :425-432 are applied here to the token-side operands'
+// partners, DY0 / Hid / DY2, so the weight gradients that follow are plain
+// products DY^T k and v^T Hid).  The values and rounding points are those of
+// the grouped stage 1 (a DH product to fp32, then the SwiGLU-derivative
+// epilogue on fp32 Y0 / Y2 / DH).
+//
+// One workgroup = 4 waves; each wave owns 32 tokens of one head and keeps
+// their k^T and v^T fragments in registers for the whole kernel.  It walks
+// the head's 32-unit hidden blocks: Y0, Y2 and DH of a block land in the same
+// accumulator layout (lane = token, 16 hidden units per lane), so the
+// epilogue is lane-local and DH never leaves the registers.  The weights come
+// from a fragment-ordered copy (uttt_dense_pack_update_weights) in which the
+// A-operand rows of every block are permuted so that each lane's 16
+// accumulator rows are 16 consecutive hidden units: every output row segment
+// is two 16-byte stores.  The 4 waves of a workgroup stream the same weight
+// fragments at about the same time (L2 / vector-cache reuse).
+#include <stdint.h>
+
+#include "common.h"
+
+namespace uttt {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+constexpr int kUpdWaves = 4;
+constexpr int kUpdTok = 32 * kUpdWaves;  // tokens per workgroup
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+__device__ __forceinline__ bf16x8_t ld16(const uint16_t* p) {
+  return *reinterpret_cast<const bf16x8_t*>(p);
+}
+
+// Logistic sigmoid with the hardware exp and reciprocal (the grouped stage
+// 1's formula).
+__device__ __forceinline__ float sigm(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __expf(-x));
+}
+
+// Hidden offset (within a 32-unit block) of A-operand row slot rho of
+// v_mfma_f32_32x32x16: accumulator element j of lane half g is row
+// 8 (j / 4) + 4 g + j % 4, so this makes it hidden unit 16 g + j.
+__host__ __device__ constexpr int upd_row_hidden(int rho) {
+  return 16 * ((rho >> 2) & 1) + 4 * (rho >> 3) + (rho & 3);
+}
+
+// Fragment-ordered copy for the update, per head three parts of I*D bf16,
+// each [I/32 blocks][D/16 k steps][64 lanes][8]; lane (r, g) of block blk,
+// step s holds, with h = 32 blk + upd_row_hidden(r):
+//   part 0: W0[h][16 s + 8 g .. + 8]      part 1: W2[h][16 s + 8 g .. + 8]
+//   part 2: W1[16 s + 8 g + j][h], j = 0 .. 7  (a column of W1: W1^T row h)
+__global__ __launch_bounds__(256) void dense_pack_update_kernel(
+    const uint16_t* __restrict__ w02, const uint16_t* __restrict__ w1, int D, int I,
+    uint16_t* __restrict__ packed) {
+  const int bh = blockIdx.y;
+  const int per_mat = I * D / 8;  // 16-byte chunks per part (<= 16384)
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= 3 * per_mat) return;
+  const int KS = D / 16;
+  const int m = c / per_mat;
+  const int q = (c - m * per_mat) >> 6;  // blk * KS + s
+  const int blk = q / KS, s = q - blk * KS;
+  const int lane = c & 63, r = lane & 31, g = lane >> 5;
+  const int h = 32 * blk + upd_row_hidden(r);
+  uint4 v;
+  if (m < 2) {
+    v = *reinterpret_cast<const uint4*>(w02 + (int64_t)bh * 2 * I * D + (m * I + h) * D + 16 * s +
+                                        8 * g);
+  } else {
+    const uint16_t* col = w1 + (int64_t)bh * D * I + (16 * s + 8 * g) * I + h;
+    uint16_t e[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) e[j] = col[j * I];
+    v = make_uint4(e[0] | (uint32_t)e[1] << 16, e[2] | (uint32_t)e[3] << 16,
+                   e[4] | (uint32_t)e[5] << 16, e[6] | (uint32_t)e[7] << 16);
+  }
+  *reinterpret_cast<uint4*>(packed + (int64_t)bh * 3 * I * D + 8 * (int64_t)c) = v;
+}
+
+__device__ __forceinline__ void store16(uint16_t* p, const float* f) {
+  uint4 v;
+  v.x = pack_bf16x2(f[0], f[1]);
+  v.y = pack_bf16x2(f[2], f[3]);
+  v.z = pack_bf16x2(f[4], f[5]);
+  v.w = pack_bf16x2(f[6], f[7]);
+  *reinterpret_cast<uint4*>(p) = v;
+}
+
+template <int D>
+__global__ __launch_bounds__(kUpdWaves * 64) void dense_update_s1_kernel(
+    const uint16_t* __restrict__ kh, const uint16_t* __restrict__ vh,
+    const float* __restrict__ lr0, const float* __restrict__ lr1, const float* __restrict__ lr2,
+    int N, int I, const uint16_t* __restrict__ packed, uint16_t* __restrict__ dy,
+    uint16_t* __restrict__ hid) {
+  constexpr int KS = D / 16;
+  const int bh = blockIdx.y;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int r = lane & 31, g = lane >> 5;
+  const int t = blockIdx.x * kUpdTok + 32 * w + r;
+  const bool valid = t < N;
+  const int64_t row = (int64_t)bh * N + min(t, N - 1);  // clamped: always a valid address
+
+  // k^T / v^T fragments of this lane's token, k = 16 s + 8 g .. + 8
+  bf16x8_t kf[KS], vf[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    kf[s] = ld16(kh + row * D + 16 * s + 8 * g);
+    vf[s] = ld16(vh + row * D + 16 * s + 8 * g);
+  }
+  // a missing lr reads the first k element (a valid address) and is ignored
+  const float* fb = reinterpret_cast<const float*>(kh);
+  const float l0r = *(lr0 ? lr0 + row : fb), l1r = *(lr1 ? lr1 + row : fb),
+              l2r = *(lr2 ? lr2 + row : fb);
+  const float l0 = lr0 ? l0r : 1.0f, l1 = lr1 ? l1r : 1.0f, l2 = lr2 ? l2r : 1.0f;
+
+  const uint16_t* ph = packed + (int64_t)bh * 3 * I * D + lane * 8;
+  const int64_t part = (int64_t)I * D;
+  uint16_t* dyr = dy + row * 2 * I + 16 * g;
+  uint16_t* hr = hid + row * I + 16 * g;
+  const int nblk = I / 32;
+  for (int blk = 0; blk < nblk; ++blk) {
+    const uint16_t* p0 = ph + (int64_t)blk * KS * 64 * 8;
+    bf16x8_t a0[KS], a2[KS], a1[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      a0[s] = ld16(p0 + s * 64 * 8);
+      a2[s] = ld16(p0 + part + s * 64 * 8);
+      a1[s] = ld16(p0 + 2 * part + s * 64 * 8);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    f32x16_t y0, y2, dh;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) y0[v] = y2[v] = dh[v] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      y0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0[s], kf[s], y0, 0, 0, 0);
+      y2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2[s], kf[s], y2, 0, 0, 0);
+      dh = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1[s], vf[s], dh, 0, 0, 0);
+    }
+    float d0[16], d2[16], hh[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const float sg = sigm(y0[u]);
+      const float sw = sg * y0[u];
+      d0[u] = sg * y2[u] * dh[u] * (1.0f + y0[u] * (1.0f - sg)) * l0;
+      d2[u] = sw * dh[u] * l2;
+      hh[u] = sw * y2[u] * l1;
+    }
+    if (valid) {
+      uint16_t* o = dyr + 32 * blk;
+      store16(o, d0);
+      store16(o + 8, d0 + 8);
+      store16(o + I, d2);
+      store16(o + I + 8, d2 + 8);
+      store16(hr + 32 * blk, hh);
+      store16(hr + 32 * blk + 8, hh + 8);
+    }
+  }
+}
+
+}  // namespace
+}  // namespace uttt
+
+using namespace uttt;
+
+extern "C" int uttt_dense_update_supported(int D, int I) {
+  return (D == 64 || D == 96 || D == 128 || D == 192 || D == 256) && I >= 32 && I <= 512 &&
+         I % 32 == 0;
+}
+
+extern "C" int uttt_dense_pack_update_weights(const void* w0_w2, const void* w1, int BH, int D,
+                                              int I, void* packed, void* stream) {
+  UTTT_REQUIRE(BH >= 0, "dense_pack_update_weights: bad sizes");
+  UTTT_REQUIRE(uttt_dense_update_supported(D, I),
+               "dense_pack_update_weights: D=%d must be 64, 96, 128, 192 or 256 and I=%d a "
+               "multiple of 32 in [32, 512]", D, I);
+  if (BH == 0) return UTTT_OK;
+  UTTT_REQUIRE(BH <= 65535, "dense_pack_update_weights: BH=%d exceeds 65535", BH);
+  UTTT_REQUIRE(w0_w2 && w1 && packed, "dense_pack_update_weights: null pointer");
+  UTTT_REQUIRE(aligned16(w0_w2) && aligned16(packed),
+               "dense_pack_update_weights: w0_w2 and packed must be 16-byte aligned");
+  const int nch = 3 * I * D / 8;
+  hipLaunchKernelGGL(dense_pack_update_kernel, dim3((unsigned)((nch + 255) / 256), (unsigned)BH),
+                     dim3(256), 0, as_stream(stream), static_cast<const uint16_t*>(w0_w2),
+                     static_cast<const uint16_t*>(w1), D, I, static_cast<uint16_t*>(packed));
+  return check_launch("dense_pack_update_weights");
+}
+
+extern "C" int uttt_dense_update_stage1(const void* kh, const void* vh, const void* lr0,
+                                        const void* lr1, const void* lr2, int BH, int N, int D,
+                                        int I, const void* packed, void* dy, void* hid,
+                                        void* stream) {
+  UTTT_REQUIRE(BH >= 0 && N >= 0, "dense_update_stage1: bad sizes");
+  UTTT_REQUIRE(uttt_dense_update_supported(D, I),
+               "dense_update_stage1: D=%d must be 64, 96, 128, 192 or 256 and I=%d a multiple "
+               "of 32 in [32, 512]", D, I);
+  if (BH == 0 || N == 0) return UTTT_OK;
+  UTTT_REQUIRE(BH <= 65535, "dense_update_stage1: BH=%d exceeds 65535", BH);
+  UTTT_REQUIRE(kh && vh && packed && dy && hid, "dense_update_stage1: null pointer");
+  UTTT_REQUIRE(aligned16(kh) && aligned16(vh) && aligned16(packed) && aligned16(dy) &&
+                   aligned16(hid),
+               "dense_update_stage1: k, v, packed, dy and hid must be 16-byte aligned");
+  UTTT_REQUIRE((lr0 == nullptr) == (lr1 == nullptr) && (lr0 == nullptr) == (lr2 == nullptr),
+               "dense_update_stage1: give all three lr or none");
+  const dim3 grid((unsigned)((N + kUpdTok - 1) / kUpdTok), (unsigned)BH);
+  const dim3 block(kUpdWaves * 64);
+  hipStream_t st = as_stream(stream);
+  const auto* k = static_cast<const uint16_t*>(kh);
+  const auto* v = static_cast<const uint16_t*>(vh);
+  const auto* a = static_cast<const float*>(lr0);
+  const auto* b = static_cast<const float*>(lr1);
+  const auto* c = static_cast<const float*>(lr2);
+  const auto* p = static_cast<const uint16_t*>(packed);
+  auto* o = static_cast<uint16_t*>(dy);
+  auto* h = static_cast<uint16_t*>(hid);
+  switch (D) {
+    case 64: hipLaunchKernelGGL(dense_update_s1_kernel<64>, grid, block, 0, st, k, v, a, b, c, N, I, p, o, h); break;
+    case 96: hipLaunchKernelGGL(dense_update_s1_kernel<96>, grid, block, 0, st, k, v, a, b, c, N, I, p, o, h); break;
+    case 128: hipLaunchKernelGGL(dense_update_s1_kernel<128>, grid, block, 0, st, k, v, a, b, c, N, I, p, o, h); break;
+    case 192: hipLaunchKernelGGL(dense_update_s1_kernel<192>, grid, block, 0, st, k, v, a, b, c, N, I, p, o, h); break;
+    default: hipLaunchKernelGGL(dense_update_s1_kernel<256>, grid, block, 0, st, k, v, a, b, c, N, I, p, o, h); break;
+  }
+  return check_launch("dense_update_stage1");
+}

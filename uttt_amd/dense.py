@@ -166,12 +166,39 @@ def _read_packed(x, packed, W02, W1, b, H):
     return out
 
 
-def _update(W02, W1, ks, vs, lrs, b, H):
-    """The grouped UPDATE of several layers' tokens at once: per head the
-    tokens of all layers concatenated.  Returns bf16 (dW0_W2, dW1)."""
+def _pack_update(W02, W1, packed=None):
+    """The fragment-ordered copy of the weights that uttt_dense_update_stage1
+    reads (csrc/dense_update.hip)."""
+    BH, d, dh = W02.shape[0], W1.shape[-2], W1.shape[-1]
+    if packed is None:
+        packed = torch.empty(BH * 3 * dh * d, dtype=torch.bfloat16, device=W02.device)
+    L.call("uttt_dense_pack_update_weights", L.ptr(W02), L.ptr(W1), BH, d, dh, L.ptr(packed),
+           L.stream_of(W02))
+    return packed
+
+
+def _update_stage1(W02, W1, kh, vh, lr3, gs, upacked=None):
+    """(DY0_DY2 [BH, N, 2I], Hid [BH, N, I]) bf16 token-major: the fused
+    kernel for small heads, else the grouped stage 1 (E = 1)."""
+    d, dh = W1.shape[-2], W1.shape[-1]
+    if not L.lib().uttt_dense_update_supported(d, dh):
+        return G.update_stage1(W02, W1, kh, vh, *(lr3 or (None,) * 3), gs, token_major=True)
+    upacked = _pack_update(W02, W1, upacked)
+    BH, N = kh.shape[0], kh.shape[1]
+    dy = torch.empty((BH, N, 2 * dh), dtype=torch.bfloat16, device=kh.device)
+    hl = torch.empty((BH, N, dh), dtype=torch.bfloat16, device=kh.device)
+    L.call("uttt_dense_update_stage1", L.ptr(kh), L.ptr(vh), *(L.ptr(x) for x in (lr3 or (None,) * 3)),
+           BH, N, d, dh, L.ptr(upacked), L.ptr(dy), L.ptr(hl), L.stream_of(kh))
+    return dy, hl
+
+
+def _update(W02, W1, ks, vs, lrs, b, H, upacked=None):
+    """The UPDATE of several layers' tokens at once: per head the tokens of
+    all layers concatenated.  Returns bf16 (dW0_W2, dW1).  upacked: a buffer
+    of BH * 3 * d_h * d bf16 for the fused stage 1's weight copy."""
     kh, vh, lr3 = _gather_heads(ks, vs, lrs, H)
     gs = _gs(b * H, kh.shape[1], kh.device)
-    dy, hl = G.update_stage1(W02, W1, kh, vh, lr3[0], lr3[1], lr3[2], gs, token_major=True)
+    dy, hl = _update_stage1(W02, W1, kh, vh, lr3, gs, upacked)
     return G.wgrad_pair(dy, kh, hl, vh, gs)
 
 
@@ -222,6 +249,8 @@ class SharedFastWeights:
         self.P = (torch.empty(b * H * 3 * dh * d, dtype=torch.bfloat16, device=w0.device)
                   if supported else None)
         self._packed, self._reads = False, 0
+        self._upacked = (torch.empty(b * H * 3 * dh * d, dtype=torch.bfloat16, device=w0.device)
+                         if L.lib().uttt_dense_update_supported(d, dh) else None)
 
     def read(self, q):
         """One layer's read of a chunk: q [b, l, H*d] -> [b, l, H*d] bf16."""
@@ -235,7 +264,7 @@ class SharedFastWeights:
     def write(self, ks, vs, lrs):
         """The chunk's aggregate write from every layer's preprocessed k, v
         [b, l, H*d] and lr ([b, l, 3] or [b, l, H*3])."""
-        dW02, dW1 = _update(self.W02, self.W1, ks, vs, lrs, self.b, self.H)
+        dW02, dW1 = _update(self.W02, self.W1, ks, vs, lrs, self.b, self.H, self._upacked)
         scale = self.lr_scale / (len(ks) if self.reduce == "mean" else 1)
         st = L.stream_of(dW02)
         nf = 0 if self.master_renorm else 1
