@@ -33,6 +33,7 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 constexpr int kUpdWaves = 4;
 constexpr int kUpdTok = 32 * kUpdWaves;  // tokens per workgroup
 
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 __device__ __forceinline__ bf16x8_t ld16(const uint16_t* p) {
@@ -94,7 +95,11 @@ __device__ __forceinline__ void store16(uint16_t* p, const float* f) {
   *reinterpret_cast<uint4*>(p) = v;
 }
 
-template <int D>
+// PIPE: two register sets of weight fragments, block b + 1's loads in flight
+// while block b is multiplied and its epilogue runs (the last prefetch
+// re-reads the last block: unconditional loads keep the wait counts exact).
+// It needs 2 x 3 D/16 fragments of registers: D <= 192 only.
+template <int D, bool PIPE>
 __global__ __launch_bounds__(kUpdWaves * 64) void dense_update_s1_kernel(
     const uint16_t* __restrict__ kh, const uint16_t* __restrict__ vh,
     const float* __restrict__ lr0, const float* __restrict__ lr1, const float* __restrict__ lr2,
@@ -126,16 +131,19 @@ __global__ __launch_bounds__(kUpdWaves * 64) void dense_update_s1_kernel(
   uint16_t* dyr = dy + row * 2 * I + 16 * g;
   uint16_t* hr = hid + row * I + 16 * g;
   const int nblk = I / 32;
-  for (int blk = 0; blk < nblk; ++blk) {
+
+  auto load_blk = [&](bf16x8_t (&a0)[KS], bf16x8_t (&a2)[KS], bf16x8_t (&a1)[KS], int blk)
+      __attribute__((always_inline)) {
     const uint16_t* p0 = ph + (int64_t)blk * KS * 64 * 8;
-    bf16x8_t a0[KS], a2[KS], a1[KS];
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       a0[s] = ld16(p0 + s * 64 * 8);
       a2[s] = ld16(p0 + part + s * 64 * 8);
       a1[s] = ld16(p0 + 2 * part + s * 64 * 8);
     }
-    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto compute_blk = [&](const bf16x8_t (&a0)[KS], const bf16x8_t (&a2)[KS],
+                         const bf16x8_t (&a1)[KS], int blk) __attribute__((always_inline)) {
     f32x16_t y0, y2, dh;
 #pragma unroll
     for (int v = 0; v < 16; ++v) y0[v] = y2[v] = dh[v] = 0.0f;
@@ -163,7 +171,35 @@ __global__ __launch_bounds__(kUpdWaves * 64) void dense_update_s1_kernel(
       store16(hr + 32 * blk, hh);
       store16(hr + 32 * blk + 8, hh + 8);
     }
+  };
+
+  if constexpr (PIPE) {
+    bf16x8_t A0[KS], A2[KS], A1[KS], B0[KS], B2[KS], B1[KS];
+    load_blk(A0, A2, A1, 0);
+    for (int blk = 0; blk < nblk; blk += 2) {
+      load_blk(B0, B2, B1, min(blk + 1, nblk - 1));
+      compute_blk(A0, A2, A1, blk);
+      if (blk + 1 >= nblk) break;
+      load_blk(A0, A2, A1, min(blk + 2, nblk - 1));
+      compute_blk(B0, B2, B1, blk + 1);
+    }
+  } else {
+    for (int blk = 0; blk < nblk; ++blk) {
+      bf16x8_t a0[KS], a2[KS], a1[KS];
+      load_blk(a0, a2, a1, blk);
+      __builtin_amdgcn_sched_barrier(0);
+      compute_blk(a0, a2, a1, blk);
+    }
   }
+}
+
+template <int D>
+void launch_update_s1(int BH, int N, int I, hipStream_t st, const uint16_t* k, const uint16_t* v,
+                      const float* a, const float* b, const float* c, const uint16_t* p,
+                      uint16_t* o, uint16_t* h) {
+  const dim3 grid((unsigned)((N + kUpdTok - 1) / kUpdTok), (unsigned)BH);
+  hipLaunchKernelGGL((dense_update_s1_kernel<D, (D <= 192)>), grid, dim3(kUpdWaves * 64), 0, st,
+                     k, v, a, b, c, N, I, p, o, h);
 }
 
 }  // namespace
@@ -210,8 +246,6 @@ extern "C" int uttt_dense_update_stage1(const void* kh, const void* vh, const vo
                "dense_update_stage1: k, v, packed, dy and hid must be 16-byte aligned");
   UTTT_REQUIRE((lr0 == nullptr) == (lr1 == nullptr) && (lr0 == nullptr) == (lr2 == nullptr),
                "dense_update_stage1: give all three lr or none");
-  const dim3 grid((unsigned)((N + kUpdTok - 1) / kUpdTok), (unsigned)BH);
-  const dim3 block(kUpdWaves * 64);
   hipStream_t st = as_stream(stream);
   const auto* k = static_cast<const uint16_t*>(kh);
   const auto* v = static_cast<const uint16_t*>(vh);
@@ -222,11 +256,11 @@ extern "C" int uttt_dense_update_stage1(const void* kh, const void* vh, const vo
   auto* o = static_cast<uint16_t*>(dy);
   auto* h = static_cast<uint16_t*>(hid);
   switch (D) {
-    case 64: hipLaunchKernelGGL(dense_update_s1_kernel<64>, grid, block, 0, st, k, v, a, b, c, N, I, p, o, h); break;
-    case 96: hipLaunchKernelGGL(dense_update_s1_kernel<96>, grid, block, 0, st, k, v, a, b, c, N, I, p, o, h); break;
-    case 128: hipLaunchKernelGGL(dense_update_s1_kernel<128>, grid, block, 0, st, k, v, a, b, c, N, I, p, o, h); break;
-    case 192: hipLaunchKernelGGL(dense_update_s1_kernel<192>, grid, block, 0, st, k, v, a, b, c, N, I, p, o, h); break;
-    default: hipLaunchKernelGGL(dense_update_s1_kernel<256>, grid, block, 0, st, k, v, a, b, c, N, I, p, o, h); break;
+    case 64: launch_update_s1<64>(BH, N, I, st, k, v, a, b, c, p, o, h); break;
+    case 96: launch_update_s1<96>(BH, N, I, st, k, v, a, b, c, p, o, h); break;
+    case 128: launch_update_s1<128>(BH, N, I, st, k, v, a, b, c, p, o, h); break;
+    case 192: launch_update_s1<192>(BH, N, I, st, k, v, a, b, c, p, o, h); break;
+    default: launch_update_s1<256>(BH, N, I, st, k, v, a, b, c, p, o, h); break;
   }
   return check_launch("dense_update_stage1");
 }
