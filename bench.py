@@ -40,7 +40,8 @@ measured by HIP events around back-to-back launches on the launch stream;
 `cpu_baseline` times the CPU restatement under oracle/ on all of this host's
 cores (rank 0, N=1; 1 warm-up, median of 3) on a bounded sample of the same
 workload.  The default line also carries `other_targets`: configs[2]'s
-permute / unpermute GB/s and configs[3]'s sweep.
+permute / unpermute GB/s, configs[3]'s sweep, and the uTTT-Dense sweeps of
+configs[1] and configs[0]'s shape.
 
 Only one GPU is used: --gpus N with N > 1 exits with a message.
 """
@@ -1281,8 +1282,9 @@ def cpu_baseline_muon(I, D):
 
 def other_targets(args):
     """The other BASELINE targets measured in the same run (no CPU legs):
-    configs[2] permute / unpermute GB/s against HBM peak, and the configs[3]
-    uTTT-MoE 124M sweep."""
+    configs[2] permute / unpermute GB/s against HBM peak, the configs[3]
+    uTTT-MoE 124M sweep, and the uTTT-Dense sweeps of configs[1] (124M) and
+    configs[0]'s shape."""
     import copy
 
     a = copy.copy(args)
@@ -1292,6 +1294,12 @@ def other_targets(args):
     k = p["kernels"]
     a.steps, a.warmup = 3, 1
     m = bench_moe(a, "moe124m", extras=False)
+    a.steps, a.warmup = 3, 1
+    d1 = bench_dense(a, "dense124m")
+    d0 = bench_dense(a, "dense_c0")
+    dense = lambda r: dict(workload=r["config"]["workload"], value=r["value"], unit=r["unit"],
+                           ms_per_step=r["ms_per_step"], kernels_us={
+                               n: v["us"] for n, v in r["kernels"].items()})
     return {
         "configs[2]_permute": dict(
             workload=p["config"]["workload"],
@@ -1303,6 +1311,8 @@ def other_targets(args):
         "configs[3]_moe124m": dict(workload=m["config"]["workload"], value=m["value"],
                                    unit=m["unit"], ms_per_step=m["ms_per_step"],
                                    sweep_mfma_frac=m["sweep"]["mfma_frac"]),
+        "configs[1]_dense124m": dense(d1),
+        "configs[0]_dense": dense(d0),
     }
 
 
