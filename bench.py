@@ -325,7 +325,10 @@ def norm_symbol(name):
         elif ch == "(" and depth == 0:
             cut = i
             break
-    return s[:cut].strip()
+    s = s[:cut].strip()
+    # the GEMM kernels' last template argument is the wave layout (4 or 8
+    # waves): one symbol per product family whichever layout it runs
+    return re.sub(r"^((?:tn|wg)_kernel<.*), [12]>$", r"\1>", s)
 
 
 class MoeSweep:

@@ -347,16 +347,38 @@ int uttt_grouped_update_bwd(const void* w0_w2, const void* w1, const void* k, co
  * [B, rows, N] intermediates): out[b, c, r] = in[b, r, c], 2-byte elements. */
 int uttt_transpose_2byte(const void* in, int B, int R, int C, void* out, void* stream);
 
-/* Update-input preprocessing (replaces the qkv_silu / v_norm / qk_norm steps
- * of _preprocess_update_inputs, uttt_llm/flame/custom_models/uttt_moe/
- * modeling_recurrent_lact.py:641-648, with l2_norm of ref_base.py:182-186):
- * for each of `rows` rows of D elements (row r at in + r * ld_in), optional
- * y = silu(x) rounded to dtype, then optional y / (|y| + 1e-5) with the norm
- * rounded to dtype and the eps added in dtype; written to out + r * ld_out
- * (out may be in).  dtype: UTTT_BF16, UTTT_F16 or UTTT_F32; D and the strides
- * multiples of 8, D <= 4096, 16-byte aligned tensors. */
-int uttt_rows_silu_l2norm(const void* in, int dtype, int64_t rows, int D, int64_t ld_in,
-                          int silu, int l2, void* out, int64_t ld_out, void* stream);
+/* Row preprocessing of the fast-weight inputs, forward.  Replaces the steps
+ * of _preprocess_update_inputs (uttt_llm/flame/custom_models/uttt_moe/
+ * modeling_recurrent_lact.py:630-657) and of the read's q path (ibid.
+ * :588-601): optional F.silu (silu = 1), then an optional parameter-free norm
+ * over each row of D elements (norm = 0 none, 1 l2_norm x / (|x| + 1e-5),
+ * 2 rms_norm x * rsqrt(mean(x^2) + 1e-5); ref_base.py:181-195, fp32 inside,
+ * the result rounded to dtype), then, when rope_dim > 0, the rotary
+ * embedding of ref_base.py:342-355 (rotary.py:83-104, non-interleaved): the
+ * value cast to bf16 and each pair (j, j + rope_dim / 2) of every rope_dim
+ * block of the token's features rotated with the bf16 tables
+ * rope_cos / rope_sin [table_rows, rope_dim / 2] at position
+ * (token % seq_len) + pos_offset, token = row / rows_per_token.  Output:
+ * bf16 with the rotary, else dtype; row r at out + r * ld_out.  dtype:
+ * UTTT_BF16, UTTT_F16 or UTTT_F32; D and the strides multiples of 8,
+ * D <= 4096, rope_dim one of 16 .. 256 (a power of two) dividing D, rows a
+ * multiple of rows_per_token * seq_len, 16-byte aligned tensors. */
+int uttt_rows_preprocess(const void* in, int dtype, int64_t rows, int D, int64_t ld_in,
+                         int silu, int norm, const void* rope_cos, const void* rope_sin,
+                         int rope_dim, int rows_per_token, int seq_len, int pos_offset,
+                         int table_rows, void* out, int64_t ld_out, void* stream);
+
+/* Backward of uttt_rows_preprocess: grad_in [rows, ld_in] (dtype) from the
+ * forward's input `in` and grad_out [rows, ld_out] (the forward output's
+ * dtype), with the reference autograd's rounding points: the conjugate
+ * rotation (RotaryEmbeddingFunction.backward, rotary.py:244-266) stored bf16,
+ * the compiled norm's backward and F.silu's backward stored in dtype.
+ * Same arguments and limits as the forward. */
+int uttt_rows_preprocess_bwd(const void* in, int dtype, const void* grad_out, int64_t rows,
+                             int D, int64_t ld_in, int64_t ld_out, int silu, int norm,
+                             const void* rope_cos, const void* rope_sin, int rope_dim,
+                             int rows_per_token, int seq_len, int pos_offset, int table_rows,
+                             void* grad_in, void* stream);
 
 /* Test hook (no reference counterpart): grids of the token-grouped GEMMs
  * with at least `min_tiles` workgroup tiles take the XCD super-tile order
@@ -372,6 +394,15 @@ long long uttt_debug_set_supertile_min_tiles(long long min_tiles);
  * tiles with 256-row down-projection tiles.  Results are identical on every
  * path.  Returns the previous value. */
 int uttt_debug_set_apply_path(int path);
+
+/* Test hook (no reference counterpart): the wave layout of the token-grouped
+ * and weight-gradient GEMM kernels, process-wide.  0: each product family's
+ * default; 2: four waves per 256x256 tile (one per SIMD, 128x128 per wave);
+ * 1: eight waves (two per SIMD, 64x128 per wave; families whose eight-wave
+ * kernel does not fit the register file keep four).  Both layouts
+ * accumulate every output in the same k order with the same MFMA, so
+ * results are identical.  Returns the previous value. */
+int uttt_debug_set_gemm_layout(int na);
 
 /* WRITE step of the fast weights.  Replaces the write of
  * _apply_moe_update_dense (uttt_llm/flame/custom_models/uttt_moe/

@@ -1,11 +1,20 @@
 """Oracle of the uTTT-MoE update glue (checker only; see oracle/__init__.py).
 
-Reference (M:) uttt_llm/flame/custom_models/uttt_moe/modeling_recurrent_lact.py
-and (RB:) uttt_llm/flame/custom_models/uttt_moe/ref_base.py:
+Reference (M:) uttt_llm/flame/custom_models/uttt_moe/modeling_recurrent_lact.py,
+(RB:) uttt_llm/flame/custom_models/uttt_moe/ref_base.py and
+(RO:) uttt_llm/flame/custom_models/uttt_moe/rotary.py:
 
-  silu_l2norm_rows   the qkv_silu / v_norm / qk_norm steps of
-                     _preprocess_update_inputs (M:641-648) with l2_norm
-                     (RB:182-186): x / (|x| + 1e-5) in the tensor's dtype
+  preprocess_rows    the qkv_silu / v_norm / qk_norm / rotary steps of
+                     _preprocess_update_inputs (M:641-654) and of the read's
+                     q path (M:588-601): F.silu, then l2_norm or rms_norm
+                     (RB:181-195, torch.compile'd: fp32 inside, the result
+                     rounded to the dtype), then the rotary embedding
+                     (RB:342-355; RO: rotary.py:83-104 non-interleaved, bf16
+                     cos / sin tables of RO:394-433)
+  preprocess_rows_bwd  its backward with the reference autograd's rounding
+                     points (the conjugate rotation RO:245-266 stored bf16,
+                     the norm's and silu's backward stored in the dtype)
+  rope_tables        the cos / sin cache of RO:385-433
   head_tokens, lr_tokens   M:132-137 and M:659-664
   writer_grads       _compute_moe_update_grads_grouped (M:484-512): lr cast
                      to bf16, k / v*p / lr permuted by expert, then the
@@ -27,21 +36,96 @@ from . import fastweight as FW
 from . import permute as P
 
 
-def silu_l2norm_rows(x: torch.Tensor, silu: bool, l2: bool, rows_of: int | None = None):
-    """Rows of `rows_of` elements (default: the last dimension): y = silu(x)
-    rounded to x's dtype (F.silu), then y / (|y| + 1e-5) with torch's rounding
-    in x's dtype (RB:182-186): |y| is an fp32 sum rounded to the dtype, the
-    eps is added in the dtype and the quotient rounded to the dtype."""
+def rope_tables(dim: int, base: float, max_len: int, dtype=torch.bfloat16):
+    """RO:385-433 without the xpos scale: inv_freq = 1 / base^(2i / dim) in
+    fp32, fp32 positions, freqs = outer(t, inv_freq), cos / sin rounded to
+    dtype.  Returns (cos, sin) [max_len, dim / 2]."""
+    inv_freq = 1.0 / (float(base) ** (torch.arange(0, dim, 2, dtype=torch.float32) / dim))
+    freqs = torch.outer(torch.arange(max_len, dtype=torch.float32), inv_freq)
+    return torch.cos(freqs).to(dtype), torch.sin(freqs).to(dtype)
+
+
+def _rope_fp32(y, cos, sin, offset, conj=False):
+    """The non-interleaved rotary of RO:86-104 in fp32 on y [B, L, F] (F a
+    multiple of rope_dim): pair (j, j + R) of every rope_dim block rotated by
+    the bf16 table values at position l + offset; conj: the backward's
+    conjugate rotation (RO:263)."""
+    B, Lx, Fdim = y.shape
+    R = cos.shape[-1]
+    c = cos[offset:offset + Lx].float().view(1, Lx, 1, R)
+    s = sin[offset:offset + Lx].float().view(1, Lx, 1, R)
+    if conj:
+        s = -s
+    blk = y.reshape(B, Lx, Fdim // (2 * R), 2 * R)
+    x0, x1 = blk[..., :R], blk[..., R:]
+    o0 = x0 * c - x1 * s
+    o1 = x0 * s + x1 * c
+    return torch.cat([o0, o1], dim=-1).reshape(B, Lx, Fdim)
+
+
+def _norm_fp32(y, norm):
+    if norm == "l2":
+        return y / (y.double().pow(2).sum(-1, keepdim=True).sqrt().float() + 1e-5)
+    if norm == "rms":
+        return y * torch.rsqrt(y.double().pow(2).mean(-1, keepdim=True).float() + 1e-5)
+    return y
+
+
+def preprocess_rows(x, silu=False, norm=None, rows_of=None, rope=None):
+    """x [B, L, F] -> [silu] -> [norm over rows of `rows_of` features] ->
+    [rotary], each step rounded as the reference: F.silu to x's dtype; the
+    compiled norm in fp32, its result to x's dtype (RB:181-195); the rotary
+    input cast to the tables' bf16, rotated in fp32, stored bf16.
+    rope = (cos, sin, seqlen_offset) or None."""
     dt = x.dtype
-    D = x.shape[-1] if rows_of is None else rows_of
-    y = x.reshape(-1, D).float()
+    B, Lx, Fdim = x.shape
+    D = Fdim if rows_of is None else rows_of
+    y = x.float()
     if silu:
         y = (y * torch.sigmoid(y)).to(dt).float()
-    if l2:
-        nrm = y.double().pow(2).sum(-1, keepdim=True).sqrt().float().to(dt).float()
-        den = (nrm + 1e-5).to(dt).float()
-        y = y / den
-    return y.to(dt).reshape(x.shape)
+    y = _norm_fp32(y.reshape(B, Lx, Fdim // D, D), norm).reshape(B, Lx, Fdim).to(dt).float()
+    if rope is None:
+        return y.to(dt)
+    cos, sin, offset = rope
+    y = y.to(torch.bfloat16).float()
+    return _rope_fp32(y, cos, sin, offset).to(torch.bfloat16)
+
+
+def preprocess_rows_bwd(x, g, silu=False, norm=None, rows_of=None, rope=None):
+    """grad_x of preprocess_rows given its output's gradient g, with the
+    reference autograd's rounding points: the conjugate rotation stored bf16
+    (then cast to x's dtype), the norm's backward (fp32, stored in x's
+    dtype), F.silu's backward (fp32, stored in x's dtype).  The formulas:
+    l2  y = s / (n + e):  g_s = g / (n + e) - s (s . g) / (n (n + e)^2);
+    rms y = s r, r = (mean s^2 + e)^-1/2:  g_s = r g - s (s . g) r^3 / D;
+    silu:  g_x = g_s sig(x) (1 + x (1 - sig(x)))."""
+    dt = x.dtype
+    B, Lx, Fdim = x.shape
+    D = Fdim if rows_of is None else rows_of
+    gg = g.float()
+    if rope is not None:
+        cos, sin, offset = rope
+        gg = _rope_fp32(gg, cos, sin, offset, conj=True).to(torch.bfloat16).to(dt).float()
+    xf = x.float()
+    s = (xf * torch.sigmoid(xf)).to(dt).float() if silu else xf
+    if norm is not None:
+        sr = s.reshape(B, Lx, Fdim // D, D)
+        gr = gg.reshape(B, Lx, Fdim // D, D)
+        dot = (sr.double() * gr.double()).sum(-1, keepdim=True).float()
+        ss = sr.double().pow(2).sum(-1, keepdim=True).float()
+        if norm == "l2":
+            n = ss.sqrt()
+            den = n + 1e-5
+            coef = torch.where(n > 0, dot / (n * den * den), torch.zeros_like(n))
+            gs = gr / den - sr * coef
+        else:
+            r = torch.rsqrt(ss / D + 1e-5)
+            gs = r * gr - sr * (dot * r * r * r / D)
+        gg = gs.reshape(B, Lx, Fdim).to(dt).float()
+    if silu:
+        sg = torch.sigmoid(xf)
+        gg = gg * (sg * (1 + xf * (1 - sg)))
+    return gg.to(dt)
 
 
 def head_tokens(x: torch.Tensor, num_heads: int) -> torch.Tensor:

@@ -7,8 +7,9 @@ oracle's compositions:
     router's own mask and gates;
   - one writer's gradients (M:453-518) and the aggregate of several writers
     (M:2428-2445), forward and backward, against oracle/moe_update.py;
-  - the update-input preprocessing kernel (silu, l2 norm per head / per row)
-    against oracle/moe_update.silu_l2norm_rows.
+  - the row preprocessing kernel (silu, l2 / rms norm per head or per row,
+    the rotary embedding; forward and backward) against
+    oracle/moe_update.preprocess_rows / preprocess_rows_bwd.
 Bars: rtol 2e-2 in bf16 (tests.helpers.assert_bf16_close) for GEMM outputs;
 the preprocessing within one bf16 rounding (rtol 8e-3) or 1e-5 in fp32, since
 its fp32 sum of squares runs in another order than torch's and its sigmoid
@@ -32,28 +33,86 @@ def _close(ours, ref, rtol, name):
     assert not bad.any(), f"{name}: {int(bad.sum())} of {bad.numel()} elements off"
 
 
-@pytest.mark.parametrize("dtype,heads,hd", [(torch.bfloat16, 4, 96), (torch.float32, 2, 64),
-                                            (torch.bfloat16, 1, 1536)])
-def test_preprocess_update_inputs(dtype, heads, hd):
-    g = torch.Generator().manual_seed(heads)
+PREP_CASES = [
+    # dtype, heads, hd, qk norm type, v norm type, rope (dim, base, offset) or None
+    (torch.bfloat16, 4, 96, "l2", "rms", None),
+    (torch.float32, 2, 64, "rms", "l2", None),
+    (torch.bfloat16, 1, 1536, "l2", "l2", (64, 1e6, 0)),    # the 760M config: same_rope, l2
+    (torch.bfloat16, 4, 384, "l2", "rms", (64, 1e6, 300)),  # four fast-weight heads, offset
+    (torch.float32, 2, 256, "l2", "rms", (128, 1e4, 7)),
+]
+
+
+@pytest.mark.parametrize("dtype,heads,hd,qk_type,v_type,rope", PREP_CASES)
+def test_preprocess_update_inputs(dtype, heads, hd, qk_type, v_type, rope):
+    g = torch.Generator().manual_seed(heads + hd)
     B, Lx = 2, 37
     k = (torch.randn(B, Lx, heads * hd, generator=g) * 2).to(dtype)
     v = (torch.randn(B, Lx, heads * hd, generator=g) * 2).to(dtype)
     lr = torch.sigmoid(torch.randn(B, Lx, 3, generator=g)) * 0.1
-    rtol = 8e-3 if dtype == torch.bfloat16 else 1e-5
-    kt, vt, lt = moe.preprocess_update_inputs(k.to(DEV), v.to(DEV), lr.to(DEV), heads,
-                                              qkv_silu=True, v_norm=True, qk_norm=True)
-    rk = MU.head_tokens(MU.silu_l2norm_rows(k, True, True, rows_of=hd), heads)
-    rv = MU.head_tokens(MU.silu_l2norm_rows(v, True, True), heads)
-    _close(kt, rk, rtol, "k")
-    _close(vt, rv, rtol, "v")
+    rp = orp = None
+    if rope is not None:
+        dim, base, off = rope
+        cos, sin = MU.rope_tables(dim, base, off + Lx + 5)
+        rp = moe.Rope(cos.to(DEV), sin.to(DEV), off)
+        orp = (cos, sin, off)
+    kd, vd = k.to(DEV).requires_grad_(), v.to(DEV).requires_grad_()
+    kt, vt, lt = moe.preprocess_update_inputs(kd, vd, lr.to(DEV), heads, qkv_silu=True,
+                                              v_norm=True, qk_norm=True, norm_type=v_type,
+                                              qk_norm_type=qk_type, rope=rp)
+    rk = MU.preprocess_rows(k, silu=True, norm=qk_type, rows_of=hd, rope=orp)
+    rv = MU.preprocess_rows(v, silu=True, norm=v_type)
+    # forward: within one rounding of the output dtype (the fp32 sums run in
+    # another order than the oracle's; silu uses the hardware exp)
+    out_bf16 = dtype == torch.bfloat16 or rope is not None
+    _close(kt, MU.head_tokens(rk, heads), 8e-3 if out_bf16 else 1e-5, "k")
+    _close(vt, MU.head_tokens(rv, heads), 8e-3 if dtype == torch.bfloat16 else 1e-5, "v")
+    assert kt.dtype == (torch.bfloat16 if rope is not None else dtype) and vt.dtype == dtype
     assert torch.equal(lt.cpu(), MU.lr_tokens(lr, heads))
-    # each switch alone
-    for silu, l2 in ((True, False), (False, True)):
-        out = moe.rows_silu_l2norm(k.to(DEV), silu, l2, rows_of=hd)
-        _close(out, MU.silu_l2norm_rows(k, silu, l2, rows_of=hd), rtol, f"silu={silu} l2={l2}")
-    with pytest.raises(AssertionError):
-        moe.rows_silu_l2norm(k.float().to(DEV).requires_grad_(), True, True)
+    # backward through the head tokens
+    gk = torch.randn(kt.shape, generator=g).to(kt.dtype)
+    gv = torch.randn(vt.shape, generator=g).to(vt.dtype)
+    torch.autograd.backward([kt, vt], [gk.to(DEV), gv.to(DEV)])
+    rgk = MU.preprocess_rows_bwd(k, gk.reshape(B, Lx, heads * hd), silu=True, norm=qk_type,
+                                 rows_of=hd, rope=orp)
+    rgv = MU.preprocess_rows_bwd(v, gv.reshape(B, Lx, heads * hd), silu=True, norm=v_type)
+    assert kd.grad.dtype == dtype and vd.grad.dtype == dtype
+    assert_bf16_close(kd.grad.cpu(), rgk, name="grad k")
+    assert_bf16_close(vd.grad.cpu(), rgv, name="grad v")
+
+
+@pytest.mark.parametrize("silu,norm,rows_of,rope", [
+    (True, None, None, None), (False, "l2", 64, None), (False, "rms", None, None),
+    (False, None, None, (32, 1e4, 2)), (True, None, 64, (64, 1e6, 0)),
+])
+def test_rows_preprocess_each_switch(silu, norm, rows_of, rope):
+    g = torch.Generator().manual_seed(17)
+    x = (torch.randn(3, 11, 256, generator=g) * 2).to(torch.bfloat16)
+    rp = orp = None
+    if rope is not None:
+        dim, base, off = rope
+        cos, sin = MU.rope_tables(dim, base, off + 11)
+        rp, orp = moe.Rope(cos.to(DEV), sin.to(DEV), off), (cos, sin, off)
+    xd = x.to(DEV).requires_grad_()
+    y = moe.rows_preprocess(xd, silu=silu, norm=norm, rows_of=rows_of, rope=rp)
+    _close(y, MU.preprocess_rows(x, silu=silu, norm=norm, rows_of=rows_of, rope=orp), 8e-3,
+           "forward")
+    gy = torch.randn(y.shape, generator=g).to(y.dtype)
+    y.backward(gy.to(DEV))
+    ref = MU.preprocess_rows_bwd(x, gy, silu=silu, norm=norm, rows_of=rows_of, rope=orp)
+    assert_bf16_close(xd.grad.cpu(), ref, name="backward")
+
+
+def test_read_query_path():
+    # q -> silu -> l2 per head -> rotary, as the MoE read (M:588-601)
+    g = torch.Generator().manual_seed(3)
+    q = (torch.randn(1, 40, 4 * 96, generator=g) * 2).to(torch.bfloat16)
+    cos, sin = MU.rope_tables(32, 1e4, 64)
+    out = moe.preprocess_read_query(q.to(DEV), 4, qkv_silu=True, qk_norm=True,
+                                    rope=moe.Rope(cos.to(DEV), sin.to(DEV), 9))
+    ref = MU.preprocess_rows(q, silu=True, norm="l2", rows_of=96, rope=(cos, sin, 9))
+    _close(out, ref, 8e-3, "q")
+    assert moe.preprocess_read_query(q, 4) is q
 
 
 @pytest.mark.parametrize("T,E,D,I,heads,topk,combine", [

@@ -8,48 +8,180 @@ from oracle import fastweight as FW
 from oracle import moe_update as MU
 
 
+def _pre(x, silu=False, norm=None, rows_of=None, rope=None):
+    """preprocess_rows on [rows, F] or [B, L, F]."""
+    y = x if x.dim() == 3 else x.unsqueeze(0)
+    out = MU.preprocess_rows(y, silu=silu, norm=norm, rows_of=rows_of, rope=rope)
+    return out if x.dim() == 3 else out[0]
+
+
 def test_l2_norm_rows_unit_norm_and_eps_placement():
     g = torch.Generator().manual_seed(0)
     x = (torch.randn(64, 96, generator=g) * 3).to(torch.bfloat16)
-    y = MU.silu_l2norm_rows(x, silu=False, l2=True)
+    y = _pre(x, norm="l2")
     n = y.double().norm(dim=-1)
     assert (n - 1).abs().max() < 2e-2
     # eps outside the norm and added, not max(|x|, eps) (F.normalize) or
     # inside the square root: |x| = 1e-5 gives 1e-5 / (1e-5 + 1e-5) = 0.5
     t = torch.zeros(1, 8)
     t[0, 3] = 1e-5
-    y = MU.silu_l2norm_rows(t, silu=False, l2=True)
+    y = _pre(t, norm="l2")
     assert abs(float(y[0, 3]) - 0.5) < 1e-6
     assert abs(float(torch.nn.functional.normalize(t, dim=-1)[0, 3]) - 0.5) > 0.4
+
+
+def test_norms_round_once_in_fp32():
+    # torch.compile'd l2_norm / rms_norm (ref_base.py:181-195) keep the norm in
+    # fp32 and round only the quotient: the result equals the exact value
+    # rounded to bf16 once (not the bf16-rounded norm of eager arithmetic)
+    g = torch.Generator().manual_seed(5)
+    x = (torch.randn(256, 384, generator=g) * 2).to(torch.bfloat16)
+    xd = x.double()
+    exact_l2 = xd / (xd.norm(dim=-1, keepdim=True) + 1e-5)
+    exact_rms = xd / (xd.pow(2).mean(-1, keepdim=True) + 1e-5).sqrt()
+    for norm, exact in (("l2", exact_l2), ("rms", exact_rms)):
+        y = _pre(x, norm=norm)
+        once = exact.to(torch.bfloat16)
+        # at most one bf16 ulp from the once-rounded exact value, nearly always equal
+        diff = (y.float() - once.float()).abs()
+        assert (diff <= once.float().abs() * 2 ** -8 + 1e-30).all(), norm
+        assert (diff > 0).float().mean() < 0.01, norm
+    # rms: unit mean square; l2 and rms differ by sqrt(D)
+    y = _pre(x.float(), norm="rms")
+    assert (y.double().pow(2).mean(-1) - 1).abs().max() < 1e-5
+    assert torch.allclose(_pre(x.float(), norm="l2") * 384 ** 0.5, y, rtol=1e-4, atol=1e-6)
 
 
 def test_l2_norm_rows_scale_invariance_and_rows():
     g = torch.Generator().manual_seed(1)
     x = (torch.randn(4, 6, 4 * 32, generator=g) + 0.5).to(torch.bfloat16)
     # powers of two scale exactly in bf16 and the eps is below the norm's ulp
-    assert torch.equal(MU.silu_l2norm_rows(2 * x, False, True),
-                       MU.silu_l2norm_rows(x, False, True))
+    assert torch.equal(_pre(2 * x, norm="l2"), _pre(x, norm="l2"))
     # per-head rows equal the norm of each head taken alone
-    per_head = MU.silu_l2norm_rows(x, False, True, rows_of=32)
+    per_head = _pre(x, norm="l2", rows_of=32)
     for h in range(4):
         sl = slice(32 * h, 32 * h + 32)
-        assert torch.equal(per_head[..., sl], MU.silu_l2norm_rows(x[..., sl].contiguous(), False,
-                                                                   True))
-    assert not torch.equal(per_head, MU.silu_l2norm_rows(x, False, True))
+        assert torch.equal(per_head[..., sl], _pre(x[..., sl].contiguous(), norm="l2"))
+    assert not torch.equal(per_head, _pre(x, norm="l2"))
 
 
 def test_silu_closed_forms():
     x = torch.tensor([[0.0, 1.0, 20.0, -20.0, -1.0, 2.0, 0.5, -0.5]])
-    y = MU.silu_l2norm_rows(x, silu=True, l2=False)
+    y = _pre(x, silu=True)
     assert float(y[0, 0]) == 0.0
     assert abs(float(y[0, 1]) - 0.7310585786) < 1e-6
     assert abs(float(y[0, 2]) - 20.0) < 1e-6
     assert abs(float(y[0, 3])) < 1e-6
     assert abs(float(y[0, 4]) + 0.2689414214) < 1e-6
     # bf16 input: silu rounds to bf16 before the norm
-    yb = MU.silu_l2norm_rows(x.to(torch.bfloat16), silu=True, l2=False)
+    yb = _pre(x.to(torch.bfloat16), silu=True)
     assert yb.dtype == torch.bfloat16
     assert torch.equal(yb, y.to(torch.bfloat16))
+
+
+def _rope_complex(y, dim, base, offset):
+    """The rotary as complex multiplication, angles in fp64 from the formula
+    theta_i(p) = p / base^(2i/dim): pair (j, j + dim/2) of each block is the
+    complex number y_j + i y_(j+dim/2), multiplied by exp(i theta_j(p))."""
+    B, Lx, F = y.shape
+    R = dim // 2
+    blk = y.double().reshape(B, Lx, F // dim, 2, R)
+    z = torch.complex(blk[..., 0, :], blk[..., 1, :])
+    p = torch.arange(offset, offset + Lx, dtype=torch.float64).view(1, Lx, 1, 1)
+    theta = p / (float(base) ** (torch.arange(0, dim, 2, dtype=torch.float64) / dim))
+    w = z * torch.exp(1j * theta)
+    return torch.stack([w.real, w.imag], dim=3).reshape(B, Lx, F)
+
+
+@pytest.mark.parametrize("dim,base,offset", [(64, 1e6, 0), (64, 1e4, 37), (128, 500.0, 5)])
+def test_rope_is_the_complex_rotation(dim, base, offset):
+    g = torch.Generator().manual_seed(dim + offset)
+    B, Lx, F = 2, 21, 3 * dim
+    x = torch.randn(B, Lx, F, generator=g).to(torch.bfloat16)
+    cos, sin = MU.rope_tables(dim, base, offset + Lx)
+    assert cos.dtype == torch.bfloat16 and cos.shape == (offset + Lx, dim // 2)
+    y = MU.preprocess_rows(x, rope=(cos, sin, offset))
+    ref = _rope_complex(x.float(), dim, base, offset)
+    # cos / sin are bf16 table values: a few bf16 ulps of |x|
+    assert (y.double() - ref).abs().max() < 3 * 2 ** -8 * x.float().abs().max()
+    # pair norms are kept (a rotation), position 0 is the identity
+    blk = y.float().reshape(B, Lx, F // dim, 2, dim // 2).pow(2).sum(3)
+    bx = x.float().reshape(B, Lx, F // dim, 2, dim // 2).pow(2).sum(3)
+    assert torch.allclose(blk, bx, rtol=2e-2, atol=1e-3)
+    if offset == 0:
+        assert torch.equal(y[:, 0], x[:, 0])
+    # the conjugate rotation undoes it (in fp32, before any rounding)
+    yf = MU._rope_fp32(x.float(), cos, sin, offset)
+    back = MU._rope_fp32(yf, cos, sin, offset, conj=True)
+    c2s2 = (cos.float() ** 2 + sin.float() ** 2)[offset:offset + Lx]  # bf16 tables: ~1
+    assert torch.allclose(back, x.float() * torch.cat([c2s2, c2s2], -1).repeat(1, F // dim)
+                          .unsqueeze(0), rtol=1e-5, atol=1e-6)
+    # a planted mistake fails: pairs of neighbours (the interleaved layout)
+    inter = x.float().reshape(B, Lx, F // 2, 2).transpose(2, 3).reshape(B, Lx, F)
+    assert (MU._rope_fp32(inter, cos, sin, offset).double() - ref).abs().max() > 0.1
+
+
+def _pre_fp64(x, silu, norm, rows_of, rope):
+    """The same map in fp64 without any rounding (for autograd)."""
+    B, Lx, F = x.shape
+    D = F if rows_of is None else rows_of
+    y = x * torch.sigmoid(x) if silu else x
+    yr = y.reshape(B, Lx, F // D, D)
+    if norm == "l2":
+        yr = yr / (yr.pow(2).sum(-1, keepdim=True).sqrt() + 1e-5)
+    elif norm == "rms":
+        yr = yr * torch.rsqrt(yr.pow(2).mean(-1, keepdim=True) + 1e-5)
+    y = yr.reshape(B, Lx, F)
+    if rope is not None:
+        cos, sin, off = rope
+        R = cos.shape[-1]
+        c = cos[off:off + Lx].double().view(1, Lx, 1, R)
+        s = sin[off:off + Lx].double().view(1, Lx, 1, R)
+        blk = y.reshape(B, Lx, F // (2 * R), 2 * R)
+        x0, x1 = blk[..., :R], blk[..., R:]
+        y = torch.cat([x0 * c - x1 * s, x0 * s + x1 * c], -1).reshape(B, Lx, F)
+    return y
+
+
+@pytest.mark.parametrize("silu", [False, True])
+@pytest.mark.parametrize("norm", [None, "l2", "rms"])
+@pytest.mark.parametrize("rope", [False, True])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_preprocess_backward_is_the_vjp(silu, norm, rope, dtype):
+    g = torch.Generator().manual_seed(int(silu) + 2 * len(str(norm)) + int(rope))
+    B, Lx, H, hd = 2, 9, 2, 64
+    x = (torch.randn(B, Lx, H * hd, generator=g) * 1.5).to(dtype)
+    gout = torch.randn(B, Lx, H * hd, generator=g).to(torch.bfloat16 if rope else dtype)
+    rp = (*MU.rope_tables(32, 1e4, 20), 3) if rope else None
+    ours = MU.preprocess_rows_bwd(x, gout, silu=silu, norm=norm, rows_of=hd, rope=rp)
+    assert ours.dtype == dtype and ours.shape == x.shape
+    xd = x.double().requires_grad_()
+    _pre_fp64(xd, silu, norm, hd, rp).backward(gout.double())
+    ref = xd.grad
+    tol = 1e-5 if (dtype == torch.float32 and not rope) else 3e-2
+    err = (ours.double() - ref).abs()
+    assert (err <= tol * ref.abs() + tol * ref.pow(2).mean().sqrt()).all(), err.max()
+
+
+def test_preprocess_backward_planted_mistake_fails():
+    # dropping the projection term of the l2 backward (g / (n + e) alone)
+    # fails the bar the backward passes against autograd
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(1, 4, 64, generator=g)
+    gout = torch.randn(1, 4, 64, generator=g)
+    xd = x.double().requires_grad_()
+    _pre_fp64(xd, False, "l2", None, None).backward(gout.double())
+    ref = xd.grad
+
+    def within(t):
+        err = (t.double() - ref).abs()
+        return bool((err <= 3e-2 * ref.abs() + 3e-2 * ref.pow(2).mean().sqrt()).all())
+
+    good = MU.preprocess_rows_bwd(x, gout, norm="l2")
+    wrong = gout / (x.norm(dim=-1, keepdim=True) + 1e-5)
+    assert within(good) and not within(wrong)
+    # the l2 backward is orthogonal to the row (up to the eps term)
+    assert ((good * x).sum(-1).abs() < 1e-4 * (good.abs() * x.abs()).sum(-1)).all()
 
 
 def test_head_tokens_and_lr_tokens_index_map():

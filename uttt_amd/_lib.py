@@ -108,10 +108,14 @@ SIGNATURES = {
          c_int, c_int, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_sz, c_p],
     ),
     "uttt_transpose_2byte": (c_int, [c_p, c_int, c_int, c_int, c_p, c_p]),
-    "uttt_rows_silu_l2norm": (c_int, [c_p, c_int, c_i64, c_int, c_i64, c_int, c_int, c_p, c_i64,
-                                      c_p]),
+    "uttt_rows_preprocess": (c_int, [c_p, c_int, c_i64, c_int, c_i64, c_int, c_int, c_p, c_p,
+                                     c_int, c_int, c_int, c_int, c_int, c_p, c_i64, c_p]),
+    "uttt_rows_preprocess_bwd": (c_int, [c_p, c_int, c_p, c_i64, c_int, c_i64, c_i64, c_int,
+                                         c_int, c_p, c_p, c_int, c_int, c_int, c_int, c_int, c_p,
+                                         c_p]),
     "uttt_debug_set_supertile_min_tiles": (ctypes.c_longlong, [ctypes.c_longlong]),
     "uttt_debug_set_apply_path": (c_int, [c_int]),
+    "uttt_debug_set_gemm_layout": (c_int, [c_int]),
     "uttt_grouped_gemm_nt2": (c_int, [c_p, c_p, c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int,
                                       c_p, c_p]),
     "uttt_grouped_gemm_tn2": (c_int, [c_p, c_p, c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int,

@@ -1,13 +1,20 @@
 // Asynchronous MFMA GEMM pipeline for gfx950 (the core of every grouped
 // fast-weight GEMM).
 //
-// Workgroup: 256 threads = 4 waves in a 2x2 grid.  Per K step of kBK = 64 a
-// workgroup multiplies two 128-row A tiles (A0, A1) by a 256-row B tile (two
-// 128-row halves B0, B1) into two fp32 accumulators acc0 = A0 B^T and
-// acc1 = A1 B^T (each 128 x 256).  Wave (wm, wn) owns rows [64 wm, 64 wm + 64)
-// of both accumulators and columns [128 wn, 128 wn + 128): 2 x 4 blocks of
-// 32x32 per accumulator, each fed by v_mfma_f32_32x32x16_bf16 (fp32
-// accumulate): per k-substep of 16, 16 MFMAs per 8 fragment reads.
+// Per K step of kBK = 64 a workgroup multiplies two 128-row A tiles (A0, A1)
+// by a 256-row B tile (two 128-row halves B0, B1) into two fp32 accumulators
+// acc0 = A0 B^T and acc1 = A1 B^T (each 128 x 256), with
+// v_mfma_f32_32x32x16_bf16 (fp32 accumulate) on 32x32 blocks.  Two wave
+// layouts, NA = the 32-row blocks of each A tile that one wave owns:
+//   NA = 2: 256 threads = 4 waves (one per SIMD) in a 2x2 grid; wave
+//     (wm, wn) owns rows [64 wm, 64 wm + 64) of both accumulators and columns
+//     [128 wn, 128 wn + 128): 2 x 4 blocks per accumulator, 256 fp32
+//     accumulators per lane; per k-substep 16 MFMAs per 8 fragment reads.
+//   NA = 1: 512 threads = 8 waves (two per SIMD) in a 4x2 grid; wave (wm, wn)
+//     owns rows [32 wm, 32 wm + 32) and the same 128 columns: 1 x 4 blocks
+//     per accumulator, 128 accumulators per lane; per k-substep 8 MFMAs per
+//     6 fragment reads.  A SIMD holds two waves, so one wave's MFMAs run
+//     while the other waits on its reads, loads or barrier.
 //
 // Global -> LDS: global_load_lds_dwordx4 (16 bytes per lane straight into LDS,
 // no register staging) into two 64 KiB stages (kBK = 64), the loads of stage
@@ -42,7 +49,7 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef short i16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 256;                                    // NA = 2 layout (and APPLY)
 constexpr int kBK = 64;
 constexpr int kTileRows = 128;                                   // rows per LDS tile
 constexpr int kBRows = 2 * kTileRows;                            // B rows per workgroup
@@ -55,6 +62,15 @@ constexpr int kLoadsPerTile = kTileBytes / 16 / kThreads;        // 4 per thread
 constexpr int kLoadsPerStage = 4 * kLoadsPerTile;                // 16 per wave
 constexpr int kNB = 4;                                           // 32-col blocks per wave
 constexpr int kXcds = 8;                                         // MI355X: 8 XCDs, 32 CUs each
+
+// Wave layout NA (see above): waves, threads, and LDS-DMA loads per thread
+// per tile and per stage.
+template <int NA> constexpr int kWavesOf = 8 / NA;
+template <int NA> constexpr int kThreadsOf = 64 * kWavesOf<NA>;
+template <int NA> constexpr int kLoadsPerTileOf = kTileBytes / 16 / kThreadsOf<NA>;
+template <int NA> constexpr int kLoadsPerStageOf = 4 * kLoadsPerTileOf<NA>;
+// Staged-epilogue items (token, 8-row group) per thread per 64-token quarter.
+template <int NA> constexpr int kItemsOf = 64 * 16 / kThreadsOf<NA>;
 
 enum Major { KMajor = 0, RMajor = 1 };
 
@@ -145,8 +161,11 @@ __device__ __forceinline__ int rswz(int k) { return (k & 3) << 2; }
 constexpr int kBufferWord3 = 0x00020000;
 typedef __amdgpu_buffer_rsrc_t Rsrc;
 
-template <int MAJOR>
+// NW: the workgroup's waves (each lane of each wave loads kLPT chunks of a tile).
+template <int MAJOR, int NW = 4>
 struct TileLoader {
+  static constexpr int kLPT = kTileBytes / 16 / (64 * NW);
+  static_assert(kLPT >= 1 && kLPT <= kLoadsPerTile, "4 or 8 waves");
   const uint8_t* base;    // wave-uniform: byte address of the tile origin at step 0
   int64_t kstep;          // bytes advanced per K step
   int last;               // last step holding data
@@ -154,6 +173,8 @@ struct TileLoader {
   int nvalid;             // valid rows from the tile origin (KMajor: rows of 8 per load)
   int ld2;                // RMajor: bytes per k-row of the operand
   int col2;               // RMajor: byte offset of the tile origin inside its k-row
+  // kLPT entries used; the array has a fixed bound (a bound that depends on
+  // NW made hipcc's host pass reject later uses of the loader's functions)
   uint32_t off[kLoadsPerTile];
   int wofs;               // wave-uniform: this wave's LDS byte offset inside a tile
 
@@ -181,8 +202,8 @@ struct TileLoader {
     base = uniform_ptr(reinterpret_cast<const uint8_t*>(org));
     kstep = MAJOR == KMajor ? (int64_t)kBK * 2 : (int64_t)kBK * op.ld * 2;
 #pragma unroll
-    for (int t = 0; t < kLoadsPerTile; ++t) {
-      const int s = (t * 4 + w) * 64 + lane;
+    for (int t = 0; t < kLPT; ++t) {
+      const int s = (t * NW + w) * 64 + lane;
       if constexpr (MAJOR == KMajor) {
         const int r = s / kChunks;
         const int c = (s % kChunks) ^ kswz(r);
@@ -216,8 +237,8 @@ struct TileLoader {
         recs = 0x80000000u;
         const int lane = threadIdx.x & 63, w = wofs >> 10, kt = k_end % kBK;
 #pragma unroll
-        for (int t = 0; t < kLoadsPerTile; ++t) {
-          const int sl = (t * 4 + w) * 64 + lane;
+        for (int t = 0; t < kLPT; ++t) {
+          const int sl = (t * NW + w) * 64 + lane;
           const int r = sl / kChunks;
           const int c = (sl % kChunks) ^ kswz(r);
           if (c * 8 >= kt) off[t] |= 0x80000000u;
@@ -229,18 +250,19 @@ struct TileLoader {
   }
 
   // Issue load t of this wave's share of a step (descriptor rs) into LDS tile
-  // `dst`.  SKIP_ROWS (KMajor token tiles of the APPLY products): a load whose
+  // `dst`.  issue_rows (KMajor token tiles of the APPLY products): a load whose
   // 8 rows all lie past the valid rows is not issued; its LDS slots keep stale
   // values, which only reach the products of token columns that are never
   // stored.  Fewer loads per stage than kLoadsPerStage: the pipeline then
   // waits on vmcnt(0) wherever it would count loads.
-  template <bool SKIP_ROWS = false>
   __device__ __forceinline__ void issue(const Rsrc& rs, int t, uint8_t* dst) const {
-    uint8_t* d = dst + t * 4 * 64 * 16 + wofs;
-    if constexpr (SKIP_ROWS && MAJOR == KMajor) {
-      if (t * 4 * (64 / kChunks) + (wofs >> 7) >= nvalid) return;  // wave-uniform
-    }
+    uint8_t* d = dst + t * NW * 64 * 16 + wofs;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, UTTT_LDS(d), 16, off[t], 0, 0, 0);
+  }
+  __device__ __forceinline__ void issue_rows(const Rsrc& rs, int t, uint8_t* dst) const {
+    static_assert(MAJOR == KMajor, "row skipping is for KMajor token tiles");
+    if (t * NW * (64 / kChunks) + (wofs >> 7) >= nvalid) return;  // wave-uniform
+    issue(rs, t, dst);
   }
 };
 
@@ -312,14 +334,16 @@ __device__ __forceinline__ bf16x8 frag_at(uint32_t base) {
 }
 
 // Fragments of one k-substep (16 k) of a stage: this wave's 4 column blocks of
-// B and its 2 row blocks of A0 / A1.
+// B and its NA row blocks of A0 / A1.
+template <int NA>
 struct HalfFrags {
-  bf16x8 b[kNB], a0[2], a1[2];
+  bf16x8 b[kNB], a0[NA], a1[NA];
 };
 
-// ONLY >= 0: fragment ONLY alone (0 .. NB-1: B blocks, then a0[0], a1[0], a0[1], a1[1]).
-template <int AMAJ, int BMAJ, int KS, int NB = kNB, int ONLY = -1>
-__device__ __forceinline__ void read_half(HalfFrags& f, const uint8_t* st, int wm, int wn) {
+// ONLY >= 0: fragment ONLY alone (0 .. NB-1: B blocks, then a0[0], a1[0], a0[1], a1[1]
+// for NA = 2, a0[0], a1[0] for NA = 1).
+template <int AMAJ, int BMAJ, int KS, int NB = kNB, int ONLY = -1, int NA = 2>
+__device__ __forceinline__ void read_half(HalfFrags<NA>& f, const uint8_t* st, int wm, int wn) {
   constexpr int kRow = kChunks * 16;  // bytes per KMajor tile row
   const uint32_t s = lds_addr(st);
   const uint32_t sb = s + (2 + wn) * kTileBytes;  // this wave's B half
@@ -336,8 +360,8 @@ __device__ __forceinline__ void read_half(HalfFrags& f, const uint8_t* st, int w
     });
   }
   if constexpr (AMAJ == KMajor) {
-    const uint32_t a = s + wm * 64 * kRow + kmaj_lane<KS>();
-    static_for<2>([&](auto I) __attribute__((always_inline)) {
+    const uint32_t a = s + wm * 32 * NA * kRow + kmaj_lane<KS>();
+    static_for<NA>([&](auto I) __attribute__((always_inline)) {
       constexpr int i = decltype(I)::value;
       if constexpr (ONLY < 0 || ONLY == NB + 2 * i)
         f.a0[I] = frag_at<KMajor, KS, i * 32 * kRow>(a);
@@ -345,10 +369,10 @@ __device__ __forceinline__ void read_half(HalfFrags& f, const uint8_t* st, int w
         f.a1[I] = frag_at<KMajor, KS, kTileBytes + i * 32 * kRow>(a);
     });
   } else {
-    static_for<2>([&](auto I) __attribute__((always_inline)) {
+    static_for<NA>([&](auto I) __attribute__((always_inline)) {
       constexpr int i = decltype(I)::value;
       if constexpr (ONLY < 0 || ONLY == NB + 2 * i || ONLY == NB + 2 * i + 1) {
-        const uint32_t a = s + rmaj_lane(wm * 64 + i * 32);
+        const uint32_t a = s + rmaj_lane(wm * 32 * NA + i * 32);
         if constexpr (ONLY < 0 || ONLY == NB + 2 * i) f.a0[I] = frag_at<RMajor, KS, 0>(a);
         if constexpr (ONLY < 0 || ONLY == NB + 2 * i + 1)
           f.a1[I] = frag_at<RMajor, KS, kTileBytes>(a);
@@ -359,15 +383,15 @@ __device__ __forceinline__ void read_half(HalfFrags& f, const uint8_t* st, int w
 
 // LDS instructions of one read_half: a KMajor fragment is one ds_read_b128,
 // an RMajor one two ds_read_b64_tr_b16.
-template <int AMAJ, int BMAJ, int NB = kNB>
+template <int AMAJ, int BMAJ, int NB = kNB, int NA = 2>
 constexpr int half_lds_ops() {
-  return NB * (BMAJ == KMajor ? 1 : 2) + 4 * (AMAJ == KMajor ? 1 : 2);
+  return NB * (BMAJ == KMajor ? 1 : 2) + 2 * NA * (AMAJ == KMajor ? 1 : 2);
 }
 
 // s_waitcnt on the LDS counter that the compiler must treat as redefining the
 // fragment registers, so no MFMA reading them can move above it.
 template <int N>
-__device__ __forceinline__ void lgkm_wait_tied(HalfFrags& f) {
+__device__ __forceinline__ void lgkm_wait_tied(HalfFrags<2>& f) {
   i32x4 r[8] = {__builtin_bit_cast(i32x4, f.b[0]),  __builtin_bit_cast(i32x4, f.b[1]),
                 __builtin_bit_cast(i32x4, f.b[2]),  __builtin_bit_cast(i32x4, f.b[3]),
                 __builtin_bit_cast(i32x4, f.a0[0]), __builtin_bit_cast(i32x4, f.a0[1]),
@@ -386,60 +410,81 @@ __device__ __forceinline__ void lgkm_wait_tied(HalfFrags& f) {
   f.a1[0] = __builtin_bit_cast(bf16x8, r[6]);
   f.a1[1] = __builtin_bit_cast(bf16x8, r[7]);
 }
+template <int N>
+__device__ __forceinline__ void lgkm_wait_tied(HalfFrags<1>& f) {
+  i32x4 r[6] = {__builtin_bit_cast(i32x4, f.b[0]),  __builtin_bit_cast(i32x4, f.b[1]),
+                __builtin_bit_cast(i32x4, f.b[2]),  __builtin_bit_cast(i32x4, f.b[3]),
+                __builtin_bit_cast(i32x4, f.a0[0]), __builtin_bit_cast(i32x4, f.a1[0])};
+  asm volatile("s_waitcnt lgkmcnt(%6)"
+               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5])
+               : "i"(N)
+               : "memory");
+  f.b[0] = __builtin_bit_cast(bf16x8, r[0]);
+  f.b[1] = __builtin_bit_cast(bf16x8, r[1]);
+  f.b[2] = __builtin_bit_cast(bf16x8, r[2]);
+  f.b[3] = __builtin_bit_cast(bf16x8, r[3]);
+  f.a0[0] = __builtin_bit_cast(bf16x8, r[4]);
+  f.a1[0] = __builtin_bit_cast(bf16x8, r[5]);
+}
+
+// MFMAs per k-substep and wave: both accumulators x NA row blocks x kNB
+// column blocks.
+template <int NA> constexpr int kMmaOf = 2 * NA * kNB;
 
 // acc_a[i][j] += A_a(wave rows i) * B(wave cols j) over one k-substep, a = 0, 1.
-// MFMA q of a substep: the four of column block 0 first, then the other 12,
+// MFMA q of a substep: the 2 NA of column block 0 first, then the others,
 // which a wave whose block 0 already covers every token of its columns skips
 // (`full` false: small experts' tiles under skewed routing).  The fragment
 // reads are the same either way, so every wait count holds on both paths.
 // (Without skipping, the order is accumulator-major: consecutive MFMAs share
 // their A fragment.)
-template <int Q, bool SKIP>
-__device__ __forceinline__ void mma_q(f32x16 (&acc0)[2][kNB], f32x16 (&acc1)[2][kNB],
-                                      const HalfFrags& f) {
-  constexpr int j = SKIP ? (Q < 4 ? 0 : 1 + (Q - 4) / 4) : Q % 4;
-  constexpr int a = SKIP ? (Q % 4) / 2 : Q / 8;
-  constexpr int i = SKIP ? Q % 2 : (Q / 4) % 2;
+template <int Q, bool SKIP, int NA>
+__device__ __forceinline__ void mma_q(f32x16 (&acc0)[NA][kNB], f32x16 (&acc1)[NA][kNB],
+                                      const HalfFrags<NA>& f) {
+  constexpr int j = SKIP ? Q / (2 * NA) : Q % kNB;
+  constexpr int a = SKIP ? (Q % (2 * NA)) / NA : Q / (kNB * NA);
+  constexpr int i = SKIP ? Q % NA : (Q / kNB) % NA;
   if constexpr (a == 0)
     acc0[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a0[i], f.b[j], acc0[i][j], 0, 0, 0);
   else
     acc1[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a1[i], f.b[j], acc1[i][j], 0, 0, 0);
 }
 
-template <bool SKIP>
-__device__ __forceinline__ void mma_half(f32x16 (&acc0)[2][kNB], f32x16 (&acc1)[2][kNB],
-                                         const HalfFrags& f, bool full) {
-  static_for<4>([&](auto Q) __attribute__((always_inline)) { mma_q<Q, SKIP>(acc0, acc1, f); });
+template <bool SKIP, int NA>
+__device__ __forceinline__ void mma_half(f32x16 (&acc0)[NA][kNB], f32x16 (&acc1)[NA][kNB],
+                                         const HalfFrags<NA>& f, bool full) {
+  static_for<2 * NA>([&](auto Q) __attribute__((always_inline)) { mma_q<Q, SKIP>(acc0, acc1, f); });
   if (!SKIP || full)
-    static_for<12>([&](auto Q) __attribute__((always_inline)) {
-      mma_q<4 + decltype(Q)::value, SKIP>(acc0, acc1, f);
+    static_for<kMmaOf<NA> - 2 * NA>([&](auto Q) __attribute__((always_inline)) {
+      mma_q<2 * NA + decltype(Q)::value, SKIP>(acc0, acc1, f);
     });
 }
 
-// The same MFMAs with between(q) (a compile-time constant, 0 .. 15) issued
-// after MFMA q, each in its own scheduling region: the wave issues the work of
-// `between` while the matrix core is busy; without the 12 MFMAs, their slots'
-// work is issued back to back.
-template <bool SKIP, class Between>
-__device__ __forceinline__ void mma_half(f32x16 (&acc0)[2][kNB], f32x16 (&acc1)[2][kNB],
-                                         const HalfFrags& f, bool full, Between&& between) {
-  static_for<4>([&](auto Q) __attribute__((always_inline)) {
+// The same MFMAs with between(q) (a compile-time constant, 0 .. kMmaOf - 1)
+// issued after MFMA q, each in its own scheduling region: the wave issues the
+// work of `between` while the matrix core is busy; without the skipped MFMAs,
+// their slots' work is issued back to back.
+template <bool SKIP, int NA, class Between>
+__device__ __forceinline__ void mma_half(f32x16 (&acc0)[NA][kNB], f32x16 (&acc1)[NA][kNB],
+                                         const HalfFrags<NA>& f, bool full, Between&& between) {
+  constexpr int kFirst = 2 * NA;
+  static_for<kFirst>([&](auto Q) __attribute__((always_inline)) {
     mma_q<Q, SKIP>(acc0, acc1, f);
     __builtin_amdgcn_sched_barrier(0);
     between(Q);
     __builtin_amdgcn_sched_barrier(0);
   });
   if (!SKIP || full) {
-    static_for<12>([&](auto Q) __attribute__((always_inline)) {
-      constexpr int q = 4 + decltype(Q)::value;
+    static_for<kMmaOf<NA> - kFirst>([&](auto Q) __attribute__((always_inline)) {
+      constexpr int q = kFirst + decltype(Q)::value;
       mma_q<q, SKIP>(acc0, acc1, f);
       __builtin_amdgcn_sched_barrier(0);
       between(std::integral_constant<int, q>{});
       __builtin_amdgcn_sched_barrier(0);
     });
   } else {
-    static_for<12>([&](auto Q) __attribute__((always_inline)) {
-      between(std::integral_constant<int, 4 + decltype(Q)::value>{});
+    static_for<kMmaOf<NA> - kFirst>([&](auto Q) __attribute__((always_inline)) {
+      between(std::integral_constant<int, kFirst + decltype(Q)::value>{});
     });
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -450,33 +495,34 @@ __device__ __forceinline__ void mma_half(f32x16 (&acc0)[2][kNB], f32x16 (&acc1)[
 // which doubles what a CU's L1 can stream from L2).
 //   prep(kt)                 readies the loads of stage kt (operand switch,
 //                            per-stage descriptors)
-//   issue(p, stage)          issues load p (0 .. kLoadsPerStage-1, a constant)
-//                            of the prepared stage into `stage`
+//   issue(p, stage)          issues load p (0 .. kLoadsPerStageOf<NA>-1, a
+//                            constant) of the prepared stage into `stage`
 //   read(stage, ks, frags, only)  the fragment reads of k-substep ks (a
-//                            constant), inline asm: fragment `only` (0 .. 7:
-//                            B blocks 0-3, then A0/A1 of row block 0, then of
-//                            row block 1) or, for only = -1, all of them
+//                            constant), inline asm: fragment `only` (B blocks
+//                            0-3, then A0/A1 of row block 0, then of row
+//                            block 1 for NA = 2) or, for only = -1, all of them
 // Stage kt (buffer cur, next buffer nxt), fragments double-buffered in f[2]:
-//   substeps j < kSubsteps-1: wait for f[j&1]; its 16 MFMAs, with the reads of
-//     (kt, j+1) -> f[(j+1)&1] one fragment after each of the first 8 MFMAs,
-//     and the loads of stage kt+1 that the previous stage left over (below);
-//     prep(kt+2) after substep kSubsteps-2
+//   substeps j < kSubsteps-1: wait for f[j&1]; its kMmaOf MFMAs, with the
+//     reads of (kt, j+1) -> f[(j+1)&1] one fragment after each of the first
+//     MFMAs, and the loads of stage kt+1 that the previous stage left over
+//     (below); prep(kt+2) after substep kSubsteps-2
 //   last substep: wait for this wave's loads of stage kt+1 and for the last
 //     fragments, barrier (stage kt+1 has landed for every wave, and every wave
 //     is done reading stage kt), then the MFMAs of the last substep with the
 //     reads of (kt+1, 0) -> f[0] and the first loads of stage kt+2 into cur
 //     between them.
-// With one wave per SIMD the matrix core only stays busy if the wave issues
-// its next MFMA as soon as the previous one leaves the pipe (32 clocks for
-// 32x32x16), so everything else rides between MFMAs in small pieces:
+// With one wave per SIMD (NA = 2) the matrix core only stays busy if the wave
+// issues its next MFMA as soon as the previous one leaves the pipe (32 clocks
+// for 32x32x16), so everything else rides between MFMAs in small pieces:
 // measured with clock stamps around each phase, the 16 loads of a stage issued
 // back to back cost ~1000 clocks of idle matrix core per stage, and 8 to 16
 // reads issued as a block plus the wait for the first of them ~100 clocks per
-// substep.  Hence one fragment read after each of 8 MFMAs, loads of 3 scalar
-// instructions each (buffer descriptor and M0 prepared per stage, no branch),
-// and the loads of one stage spread over the last substep of stage kt and the
-// first substeps of stage kt+1 (kLdSplit); those issued in stage kt+1 still
-// have its last substeps to land.
+// substep.  Hence one fragment read after each of the first MFMAs, loads of 3
+// scalar instructions each (buffer descriptor and M0 prepared per stage, no
+// branch), and the loads of one stage spread over the last substep of stage kt
+// and the first substep of stage kt+1 (kLdSplit); those issued in stage kt+1
+// still have its last substeps to land.  NA = 1 keeps the same schedule with
+// half the MFMAs, reads and loads per wave, two waves per SIMD.
 // The fragment reads are inline asm because the compiler's wait-count pass
 // cannot tell them from the in-flight LDS-DMA writes and would drain every
 // load (vmcnt(0)) or every read (lgkmcnt(0)) in front of them; every wait
@@ -485,46 +531,54 @@ __device__ __forceinline__ void mma_half(f32x16 (&acc0)[2][kNB], f32x16 (&acc1)[
 #ifndef UTTT_LD_SPLIT
 #define UTTT_LD_SPLIT 8, 8, 0, 0
 #endif
-// Loads of a stage issued in: the last substep of the stage before, then
-// substeps 0, 1, 2 of the stage before the one they fill.
+// Loads of a stage (in sixteenths) issued in: the last substep of the stage
+// before, then substeps 0, 1, 2 of the stage before the one they fill.
 constexpr int kLdSplit[4] = {UTTT_LD_SPLIT};
-static_assert(kLdSplit[0] + kLdSplit[1] + kLdSplit[2] + kLdSplit[3] == kLoadsPerStage,
+static_assert(kLdSplit[0] + kLdSplit[1] + kLdSplit[2] + kLdSplit[3] == 16,
               "every load of a stage has a slot");
 
-// The load (0 .. kLoadsPerStage-1) issued after MFMA q of phase ph (0 = last
-// substep, 1..3 = substeps 0..2 of the next stage), or -1: phase ph's n loads
-// sit after MFMAs 0, 16/n, 2*16/n, ...
-template <int PH, int Q>
+// The load (0 .. kLoadsPerStageOf<NA>-1) issued after MFMA q of phase ph (0 =
+// last substep, 1..3 = substeps 0..2 of the next stage), or -1: phase ph's n
+// loads sit after MFMAs 0, M/n, 2*M/n, ... of the M = kMmaOf<NA> of a substep.
+template <int PH, int Q, int NA>
 constexpr int load_slot() {
+  constexpr int per = kLoadsPerStageOf<NA>;
   int lo = 0;
-  for (int i = 0; i < PH; ++i) lo += kLdSplit[i];
-  const int n = kLdSplit[PH];
+  for (int i = 0; i < PH; ++i) lo += kLdSplit[i] * per / 16;
+  const int n = kLdSplit[PH] * per / 16;
+  if (n == 0) return -1;
   for (int i = 0; i < n; ++i)
-    if (i * 16 / n == Q) return lo + i;
+    if (i * kMmaOf<NA> / n == Q) return lo + i;
   return -1;
 }
 
-template <int NLDS, bool SKIP, class PrepFn, class IssueFn, class ReadFn>
+template <int NLDS, bool SKIP, int NA, class PrepFn, class IssueFn, class ReadFn>
 __device__ __forceinline__ void run_pipeline(int nk, bool full, PrepFn&& prep, IssueFn&& issue,
                                              ReadFn&& read,
-                                             f32x16 (&acc0)[2][kNB], f32x16 (&acc1)[2][kNB],
+                                             f32x16 (&acc0)[NA][kNB], f32x16 (&acc1)[NA][kNB],
                                              uint8_t* const (&ring)[kStages]) {
   if (nk <= 0) return;
+  constexpr int kFrags = kNB + 2 * NA;  // fragment reads of a substep (one per MFMA slot)
+  constexpr int kPerStage = kLoadsPerStageOf<NA>;
   static_assert(kSubsteps % 2 == 0 && kSubsteps == 4, "fragment double buffer parity");
-  static_assert(NLDS <= 16, "two LDS reads per MFMA slot at most");
+  static_assert(NLDS <= 2 * kMmaOf<NA>, "two LDS reads per MFMA slot at most");
+  static_assert(kFrags <= kMmaOf<NA>, "one fragment per MFMA slot");
+  static_assert(kLdSplit[0] * kPerStage % 16 == 0 && kLdSplit[1] * kPerStage % 16 == 0 &&
+                    kLdSplit[2] * kPerStage % 16 == 0 && kLdSplit[3] * kPerStage % 16 == 0,
+                "the load split must divide the stage's loads");
   using All = std::integral_constant<int, -1>;
-  HalfFrags f[2];
+  HalfFrags<NA> f[2];
   static_for<kStages>([&](auto i) __attribute__((always_inline)) {
     prep(decltype(i)::value);
-    static_for<kLoadsPerStage>([&](auto p) __attribute__((always_inline)) {
+    static_for<kPerStage>([&](auto p) __attribute__((always_inline)) {
       issue(p, ring[decltype(i)::value]);
     });
   });
-  // stage 0 landed: counted while stage 1 issued its kLoadsPerStage DMAs
+  // stage 0 landed: counted while stage 1 issued its kPerStage DMAs
   if (SKIP)  // the token tiles may issue fewer loads per stage
     wait_vmcnt<0>();
   else
-    wait_vmcnt<(kStages - 1) * kLoadsPerStage>();
+    wait_vmcnt<(kStages - 1) * kPerStage>();
   block_barrier();
   read(ring[0], std::integral_constant<int, 0>{}, f[0], All{});
   // stage 1 was loaded whole before the loop: stage 0 has no leftover loads
@@ -535,10 +589,10 @@ __device__ __forceinline__ void run_pipeline(int nk, bool full, PrepFn&& prep, I
       lgkm_wait_tied<0>(f[j & 1]);
       mma_half<SKIP>(acc0, acc1, f[j & 1], full, [&](auto q) __attribute__((always_inline)) {
         constexpr int Q = decltype(q)::value;
-        if constexpr (Q < 8)
+        if constexpr (Q < kFrags)
           read(cur, std::integral_constant<int, j + 1>{}, f[(j + 1) & 1],
                std::integral_constant<int, Q>{});
-        constexpr int p = load_slot<j + 1, Q>();
+        constexpr int p = load_slot<j + 1, Q, NA>();
         if constexpr (p >= 0)
           if (leftovers) issue(std::integral_constant<int, p>{}, nxt);
       });
@@ -546,16 +600,16 @@ __device__ __forceinline__ void run_pipeline(int nk, bool full, PrepFn&& prep, I
       __builtin_amdgcn_sched_barrier(0);
     });
     constexpr int jl = kSubsteps - 1;
-    wait_vmcnt<(kStages - 2) * kLoadsPerStage>();
+    wait_vmcnt<(kStages - 2) * kPerStage>();
     lgkm_wait_tied<0>(f[jl & 1]);
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_sched_barrier(0);
     mma_half<SKIP>(acc0, acc1, f[jl & 1], full, [&](auto q) __attribute__((always_inline)) {
-      if constexpr (decltype(q)::value < 8)
+      if constexpr (decltype(q)::value < kFrags)
         read(nxt, std::integral_constant<int, 0>{}, f[(jl + 1) & 1],
              std::integral_constant<int, decltype(q)::value>{});
-      constexpr int p = load_slot<0, decltype(q)::value>();
+      constexpr int p = load_slot<0, decltype(q)::value, NA>();
       if constexpr (p >= 0) issue(std::integral_constant<int, p>{}, cur);
     });
     leftovers = true;

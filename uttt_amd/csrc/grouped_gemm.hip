@@ -51,26 +51,27 @@ struct TnArgs {
 // Loop over this wave's accumulator quads: f(t, r, n, v[4]) with tile t, tile
 // row r (rows r..r+3 hold v[0..3]) and tile token column n.  Indices are
 // compile-time (static_for) so the accumulators stay in registers.
-template <class F>
-__device__ __forceinline__ void for_quads(const f32x16 (&acc0)[2][kNB], const f32x16 (&acc1)[2][kNB],
-                                          int wm, int wn, bool two, F&& f) {
-  static_for<2 * 2 * kNB * 4>([&](auto idx) __attribute__((always_inline)) {
-    constexpr int t = idx / (2 * kNB * 4);
-    constexpr int i = (idx / (kNB * 4)) % 2;
+template <int NA, class F>
+__device__ __forceinline__ void for_quads(const f32x16 (&acc0)[NA][kNB],
+                                          const f32x16 (&acc1)[NA][kNB], int wm, int wn, bool two,
+                                          F&& f) {
+  static_for<2 * NA * kNB * 4>([&](auto idx) __attribute__((always_inline)) {
+    constexpr int t = idx / (NA * kNB * 4);
+    constexpr int i = (idx / (kNB * 4)) % NA;
     constexpr int j = (idx / 4) % kNB;
     constexpr int q = idx % 4;
     if (t == 1 && !two) return;
     const f32x16& a = t == 0 ? acc0[i][j] : acc1[i][j];
     const float v[4] = {a[q * 4], a[q * 4 + 1], a[q * 4 + 2], a[q * 4 + 3]};
-    f(t, wm * 64 + i * 32 + acc_row(q * 4), wn * 128 + j * 32 + acc_col(), v);
+    f(t, wm * 32 * NA + i * 32 + acc_row(q * 4), wn * 128 + j * 32 + acc_col(), v);
   });
 }
 
 // Paired quads of the two accumulators (same rows of A0 and A1): f(r, n, a[4], b[4]).
-template <class F>
-__device__ __forceinline__ void for_pairs(const f32x16 (&acc0)[2][kNB], const f32x16 (&acc1)[2][kNB],
-                                          int wm, int wn, F&& f) {
-  static_for<2 * kNB * 4>([&](auto idx) __attribute__((always_inline)) {
+template <int NA, class F>
+__device__ __forceinline__ void for_pairs(const f32x16 (&acc0)[NA][kNB],
+                                          const f32x16 (&acc1)[NA][kNB], int wm, int wn, F&& f) {
+  static_for<NA * kNB * 4>([&](auto idx) __attribute__((always_inline)) {
     constexpr int i = idx / (kNB * 4);
     constexpr int j = (idx / 4) % kNB;
     constexpr int q = idx % 4;
@@ -78,7 +79,7 @@ __device__ __forceinline__ void for_pairs(const f32x16 (&acc0)[2][kNB], const f3
                         acc0[i][j][q * 4 + 3]};
     const float b[4] = {acc1[i][j][q * 4], acc1[i][j][q * 4 + 1], acc1[i][j][q * 4 + 2],
                         acc1[i][j][q * 4 + 3]};
-    f(wm * 64 + i * 32 + acc_row(q * 4), wn * 128 + j * 32 + acc_col(), a, b);
+    f(wm * 32 * NA + i * 32 + acc_row(q * 4), wn * 128 + j * 32 + acc_col(), a, b);
   });
 }
 
@@ -97,17 +98,17 @@ struct TileCtx {
 // fp32 [token][128 rows] (16-byte chunks XOR-swizzled by token, conflict-free),
 // then thread t takes token (t / 16) and rows 8 (t % 16) .. +7, so 16 lanes
 // cover 128 contiguous rows of one token: 16-byte global loads and stores.
-template <int Q>
-__device__ __forceinline__ void stage_quarter(const f32x16 (&acc0)[2][kNB],
-                                              const f32x16 (&acc1)[2][kNB], const TileCtx& c) {
+template <int Q, int NA>
+__device__ __forceinline__ void stage_quarter(const f32x16 (&acc0)[NA][kNB],
+                                              const f32x16 (&acc1)[NA][kNB], const TileCtx& c) {
   if (c.wn != Q / 2) return;
-  static_for<2 * 2 * 4>([&](auto idx) __attribute__((always_inline)) {
+  static_for<NA * 2 * 4>([&](auto idx) __attribute__((always_inline)) {
     constexpr int i = idx / 8;
     constexpr int jl = (idx / 4) % 2;
     constexpr int q = idx % 4;
     constexpr int jj = 2 * (Q % 2) + jl;
     const int n = jl * 32 + acc_col();
-    const int r = c.wm * 64 + i * 32 + acc_row(q * 4);
+    const int r = c.wm * 32 * NA + i * 32 + acc_row(q * 4);
     const int off = n * 128 + (((r >> 2) ^ (n & 31)) << 2);
     *reinterpret_cast<float4*>(c.lds0 + off) =
         make_float4(acc0[i][jj][q * 4], acc0[i][jj][q * 4 + 1], acc0[i][jj][q * 4 + 2],
@@ -188,9 +189,9 @@ __device__ __forceinline__ void store8(float* p, const float (&v)[8]) {
 // s_barrier): a __syncthreads() would also wait for every global store of the
 // quarter to complete (its workgroup-scope fence), four store drains per tile
 // with the matrix core idle.
-template <class Body>
-__device__ __forceinline__ void staged_epilogue(const f32x16 (&acc0)[2][kNB],
-                                                const f32x16 (&acc1)[2][kNB], const TileCtx& c,
+template <int NA, class Body>
+__device__ __forceinline__ void staged_epilogue(const f32x16 (&acc0)[NA][kNB],
+                                                const f32x16 (&acc1)[NA][kNB], const TileCtx& c,
                                                 Body&& body) {
   block_barrier();  // every wave is done reading the stage buffers
   static_for<4>([&](auto QQ) __attribute__((always_inline)) {
@@ -198,8 +199,8 @@ __device__ __forceinline__ void staged_epilogue(const f32x16 (&acc0)[2][kNB],
     stage_quarter<Q>(acc0, acc1, c);
     block_barrier();
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int it = threadIdx.x + kThreads * k;
+    for (int k = 0; k < kItemsOf<NA>; ++k) {
+      const int it = threadIdx.x + kThreadsOf<NA> * k;
       body(it >> 4, Q * 64 + (it >> 4), it & 15);
     }
     block_barrier();
@@ -212,25 +213,25 @@ __device__ __forceinline__ void staged_epilogue(const f32x16 (&acc0)[2][kNB],
 // in flight together and overlap the staging -- then use(nl, n, g, raw) on
 // each.  (Loads inside a per-item `if (valid)` would each be waited for
 // before the next item's loads issue.)
-template <class FetchFn, class UseFn>
-__device__ __forceinline__ void staged_epilogue_prefetch(const f32x16 (&acc0)[2][kNB],
-                                                         const f32x16 (&acc1)[2][kNB],
+template <int NA, class FetchFn, class UseFn>
+__device__ __forceinline__ void staged_epilogue_prefetch(const f32x16 (&acc0)[NA][kNB],
+                                                         const f32x16 (&acc1)[NA][kNB],
                                                          const TileCtx& c, FetchFn&& fetch,
                                                          UseFn&& use) {
   block_barrier();  // every wave is done reading the stage buffers
   static_for<4>([&](auto QQ) __attribute__((always_inline)) {
     constexpr int Q = QQ;
-    decltype(fetch(0, 0)) raw[4];
+    decltype(fetch(0, 0)) raw[kItemsOf<NA>];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int it = threadIdx.x + kThreads * k;
+    for (int k = 0; k < kItemsOf<NA>; ++k) {
+      const int it = threadIdx.x + kThreadsOf<NA> * k;
       raw[k] = fetch(Q * 64 + (it >> 4), it & 15);
     }
     stage_quarter<Q>(acc0, acc1, c);
     block_barrier();
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int it = threadIdx.x + kThreads * k;
+    for (int k = 0; k < kItemsOf<NA>; ++k) {
+      const int it = threadIdx.x + kThreadsOf<NA> * k;
       use(it >> 4, Q * 64 + (it >> 4), it & 15, raw[k]);
     }
     block_barrier();
@@ -259,8 +260,10 @@ template <class OutT, bool STAGED = false>
 struct EpiStore {
   static constexpr bool kStaleColumnsUnused = true;  // per-column stores, masked by segment
   using Args = EpiStoreArgs<OutT>;
-  __device__ __forceinline__ static void apply(const Args& ea, const f32x16 (&acc0)[2][kNB],
-                               const f32x16 (&acc1)[2][kNB], const TileCtx& c, bool two) {
+  template <int NA>
+  __device__ __forceinline__ static void apply(const Args& ea, const f32x16 (&acc0)[NA][kNB],
+                                               const f32x16 (&acc1)[NA][kNB], const TileCtx& c,
+                                               bool two) {
     OutT* ob = ea.out + (int64_t)c.b * ea.N * ea.ld;
     if constexpr (STAGED) {
       staged_epilogue(acc0, acc1, c, [&](int nl, int n, int g) __attribute__((always_inline)) {
@@ -332,8 +335,10 @@ template <bool SYM = false>
 struct EpiLinComb {
   static constexpr bool kStaleColumnsUnused = true;
   using Args = EpiLinCombArgs;
-  __device__ __forceinline__ static void apply(const Args& ea, const f32x16 (&acc0)[2][kNB],
-                               const f32x16 (&acc1)[2][kNB], const TileCtx& c, bool two) {
+  template <int NA>
+  __device__ __forceinline__ static void apply(const Args& ea, const f32x16 (&acc0)[NA][kNB],
+                                               const f32x16 (&acc1)[NA][kNB], const TileCtx& c,
+                                               bool two) {
     const int64_t bo = (int64_t)c.b * ea.N * ea.ld;
     (void)two;  // past col_end when tile 1 is not multiplied
     // `in` is read from valid addresses whether or not it is given (out's,
@@ -345,10 +350,10 @@ struct EpiLinComb {
     static_for<4>([&](auto QQ) __attribute__((always_inline)) {
       constexpr int Q = QQ;
       // the tile itself: token nl of the quarter, rows 8 g .. 8 g + 7 of each part
-      uint4 xt[4][2];
+      uint4 xt[kItemsOf<NA>][2];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int it = threadIdx.x + kThreads * k;
+      for (int k = 0; k < kItemsOf<NA>; ++k) {
+        const int it = threadIdx.x + kThreadsOf<NA> * k;
         const int nl = it >> 4, g = it & 15;
         const bool tok_ok = c.tt.n0 + Q * 64 + nl < c.tt.size;
         const int64_t tok = c.tt.start + c.tt.n0 + Q * 64 + nl;
@@ -360,11 +365,11 @@ struct EpiLinComb {
         }
       }
       // its transpose: row `col` of the output, 8 consecutive tokens
-      uint4 xm[8];
+      uint4 xm[2 * kItemsOf<NA>];
       if (mirror) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const int it = threadIdx.x + kThreads * k;
+        for (int k = 0; k < 2 * kItemsOf<NA>; ++k) {
+          const int it = threadIdx.x + kThreadsOf<NA> * k;
           const int r = it & 127, part = (it >> 7) & 1, g8 = it >> 8;
           const int nq = Q * 64 + 8 * g8;
           const int col = c.m0 + part * kTileRows + r;
@@ -376,8 +381,8 @@ struct EpiLinComb {
       stage_quarter<Q>(acc0, acc1, c);
       block_barrier();
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int it = threadIdx.x + kThreads * k;
+      for (int k = 0; k < kItemsOf<NA>; ++k) {
+        const int it = threadIdx.x + kThreadsOf<NA> * k;
         const int nl = it >> 4, g = it & 15;
         if (c.tt.n0 + Q * 64 + nl >= c.tt.size) continue;
         const int64_t tok = c.tt.start + c.tt.n0 + Q * 64 + nl;
@@ -392,8 +397,8 @@ struct EpiLinComb {
       }
       if (mirror) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const int it = threadIdx.x + kThreads * k;
+        for (int k = 0; k < 2 * kItemsOf<NA>; ++k) {
+          const int it = threadIdx.x + kThreadsOf<NA> * k;
           const int r = it & 127, part = (it >> 7) & 1, g8 = it >> 8;
           const int nq = Q * 64 + 8 * g8;
           const int col = c.m0 + part * kTileRows + r;
@@ -420,8 +425,10 @@ struct EpiSwiGLU {
     uint16_t* out;
     int I, N, token_major;
   };
-  __device__ __forceinline__ static void apply(const Args& ea, const f32x16 (&acc0)[2][kNB],
-                               const f32x16 (&acc1)[2][kNB], const TileCtx& c, bool) {
+  template <int NA>
+  __device__ __forceinline__ static void apply(const Args& ea, const f32x16 (&acc0)[NA][kNB],
+                                               const f32x16 (&acc1)[NA][kNB], const TileCtx& c,
+                                               bool) {
     uint16_t* hb = ea.out + (int64_t)c.b * ea.N * ea.I;
     for_pairs(acc0, acc1, c.wm, c.wn, [&](int r, int n, const float* y0, const float* y2) __attribute__((always_inline)) {
       const int m = c.m0 + r;
@@ -455,8 +462,10 @@ struct EpiS1 {
     uint16_t* dh_save;  // optional [B, N, I]: bf16(DH)
     int I, N, token_major;
   };
-  __device__ __forceinline__ static void apply(const Args& ea, const f32x16 (&acc0)[2][kNB],
-                               const f32x16 (&acc1)[2][kNB], const TileCtx& c, bool) {
+  template <int NA>
+  __device__ __forceinline__ static void apply(const Args& ea, const f32x16 (&acc0)[NA][kNB],
+                                               const f32x16 (&acc1)[NA][kNB], const TileCtx& c,
+                                               bool) {
     const int I = ea.I, I2 = 2 * I;
     const float* dhb = ea.dh + (int64_t)c.b * ea.N * I;
     uint16_t* dyb = ea.dy + (int64_t)c.b * ea.N * I2;
@@ -545,8 +554,10 @@ struct EpiBwd {
     float* lr_part;
     int I, N, B, m_tiles;
   };
-  __device__ __forceinline__ static void apply(const Args& ea, const f32x16 (&acc0)[2][kNB],
-                               const f32x16 (&acc1)[2][kNB], const TileCtx& c, bool) {
+  template <int NA>
+  __device__ __forceinline__ static void apply(const Args& ea, const f32x16 (&acc0)[NA][kNB],
+                                               const f32x16 (&acc1)[NA][kNB], const TileCtx& c,
+                                               bool) {
     const int I = ea.I, I2 = 2 * I;
     const int64_t bo2 = (int64_t)c.b * ea.N * I2, bo1 = (int64_t)c.b * ea.N * I;
     const int64_t plane = (int64_t)ea.m_tiles * ea.B * ea.N;
@@ -649,8 +660,10 @@ struct EpiBwdSaved {
     float* lr_part;
     int I, N, B, m_tiles;
   };
-  __device__ __forceinline__ static void apply(const Args& ea, const f32x16 (&acc0)[2][kNB],
-                               const f32x16 (&acc1)[2][kNB], const TileCtx& c, bool) {
+  template <int NA>
+  __device__ __forceinline__ static void apply(const Args& ea, const f32x16 (&acc0)[NA][kNB],
+                                               const f32x16 (&acc1)[NA][kNB], const TileCtx& c,
+                                               bool) {
     const int I = ea.I, I2 = 2 * I;
     const int64_t bo2 = (int64_t)c.b * ea.N * I2, bo1 = (int64_t)c.b * ea.N * I;
     const int64_t plane = (int64_t)ea.m_tiles * ea.B * ea.N;
@@ -733,8 +746,8 @@ struct EpiBwdSaved {
   }
 };
 
-template <int AMAJ, class Epi, bool SKIP>
-__global__ __launch_bounds__(kThreads) void tn_kernel(TnArgs a, typename Epi::Args ea) {
+template <int AMAJ, class Epi, bool SKIP, int NA>
+__global__ __launch_bounds__(kThreadsOf<NA>) void tn_kernel(TnArgs a, typename Epi::Args ea) {
   __shared__ __attribute__((aligned(16))) uint8_t st0[kStageBytes];
   __shared__ __attribute__((aligned(16))) uint8_t st1[kStageBytes];
 
@@ -776,11 +789,11 @@ __global__ __launch_bounds__(kThreads) void tn_kernel(TnArgs a, typename Epi::Ar
   const int r0 = m0 + a.row_off[0], r1 = m0 + a.row_off[1];
   const bool two = a.two != 0;
 
-  f32x16 acc0[2][kNB], acc1[2][kNB];
+  f32x16 acc0[NA][kNB], acc1[NA][kNB];
   zero(acc0);
   zero(acc1);
-  TileLoader<AMAJ> la0, la1;
-  TileLoader<KMajor> lx0, lx1;
+  TileLoader<AMAJ, kWavesOf<NA>> la0, la1;
+  TileLoader<KMajor, kWavesOf<NA>> lx0, lx1;
   la0.init(A00, r0);
   la1.init(A01, r1);
   lx0.init(X0, tt.n0);
@@ -800,12 +813,14 @@ __global__ __launch_bounds__(kThreads) void tn_kernel(TnArgs a, typename Epi::Ar
     rs[3] = lx1.rsrc(lstep);
   };
   auto issue = [&](auto p, uint8_t* st) __attribute__((always_inline)) {
-    constexpr int tile = decltype(p)::value / kLoadsPerTile;
-    constexpr int t = decltype(p)::value % kLoadsPerTile;
+    constexpr int tile = decltype(p)::value / kLoadsPerTileOf<NA>;
+    constexpr int t = decltype(p)::value % kLoadsPerTileOf<NA>;
     if constexpr (tile == 0) la0.issue(rs[0], t, st);
     else if constexpr (tile == 1) la1.issue(rs[1], t, st + kTileBytes);
-    else if constexpr (tile == 2) lx0.template issue<SKIP>(rs[2], t, st + 2 * kTileBytes);
-    else lx1.template issue<SKIP>(rs[3], t, st + 3 * kTileBytes);
+    else if constexpr (tile == 2 && SKIP) lx0.issue_rows(rs[2], t, st + 2 * kTileBytes);
+    else if constexpr (tile == 2) lx0.issue(rs[2], t, st + 2 * kTileBytes);
+    else if constexpr (SKIP) lx1.issue_rows(rs[3], t, st + 3 * kTileBytes);
+    else lx1.issue(rs[3], t, st + 3 * kTileBytes);
   };
   const int w = threadIdx.x >> 6;
   const int wm = w >> 1, wn = w & 1;
@@ -818,12 +833,12 @@ __global__ __launch_bounds__(kThreads) void tn_kernel(TnArgs a, typename Epi::Ar
   const int vt = tt.size - tt.n0 - wn * (kBRows / 2);
   const bool full = !SKIP || __builtin_amdgcn_readfirstlane(vt > 32 ? 1 : 0) != 0;
   (void)vt;
-  auto read = [&](const uint8_t* st, auto ks, HalfFrags& f, auto only)
+  auto read = [&](const uint8_t* st, auto ks, HalfFrags<NA>& f, auto only)
                   __attribute__((always_inline)) {
-    read_half<AMAJ, KMajor, decltype(ks)::value, kNB, decltype(only)::value>(f, st, wm, wn);
+    read_half<AMAJ, KMajor, decltype(ks)::value, kNB, decltype(only)::value, NA>(f, st, wm, wn);
   };
-  run_pipeline<half_lds_ops<AMAJ, KMajor>(), SKIP>(nk0 + nk1, full, prep, issue, read, acc0,
-                                                    acc1, ring);
+  run_pipeline<half_lds_ops<AMAJ, KMajor, kNB, NA>(), SKIP>(nk0 + nk1, full, prep, issue, read,
+                                                             acc0, acc1, ring);
   const TokenTile tte{tt.e, after_loop(tt.start), after_loop(tt.size), after_loop(tt.n0)};
   const TileCtx c{after_loop(b), after_loop(m0), after_loop(wm), after_loop(wn), mt, tte,
                   reinterpret_cast<float*>(st0), reinterpret_cast<float*>(st1)};
@@ -1130,8 +1145,8 @@ struct WgTask {
 
 // SPLIT: fp32 partials (the two epilogues in one kernel do not fit the
 // register file: each alone does)
-template <bool SPLIT>
-__global__ __launch_bounds__(kThreads) void wg_kernel(WgTask t0, WgTask t1,
+template <bool SPLIT, int NA>
+__global__ __launch_bounds__(kThreadsOf<NA>) void wg_kernel(WgTask t0, WgTask t1,
                                                       const int32_t* __restrict__ gs, int E,
                                                       int N, int BE, int splits) {
   __shared__ __attribute__((aligned(16))) uint8_t st0[kStageBytes];
@@ -1161,10 +1176,10 @@ __global__ __launch_bounds__(kThreads) void wg_kernel(WgTask t0, WgTask t1,
   const Operand P{tk.p + ((int64_t)b * N + start) * Y, Y, Y, size};
   const Operand Q{tk.q + ((int64_t)b * N + start) * X, X, X, size};
 
-  f32x16 acc0[2][kNB], acc1[2][kNB];
+  f32x16 acc0[NA][kNB], acc1[NA][kNB];
   zero(acc0);
   zero(acc1);
-  TileLoader<RMajor> lp0, lp1, lq0, lq1;
+  TileLoader<RMajor, kWavesOf<NA>> lp0, lp1, lq0, lq1;
   lp0.init(P, y0);
   lp1.init(P, y0 + kTileRows);
   lq0.init(Q, x0);
@@ -1177,8 +1192,8 @@ __global__ __launch_bounds__(kThreads) void wg_kernel(WgTask t0, WgTask t1,
     rs[3] = lq1.rsrc(kt);
   };
   auto issue = [&](auto p, uint8_t* st) __attribute__((always_inline)) {
-    constexpr int tile = decltype(p)::value / kLoadsPerTile;
-    constexpr int t = decltype(p)::value % kLoadsPerTile;
+    constexpr int tile = decltype(p)::value / kLoadsPerTileOf<NA>;
+    constexpr int t = decltype(p)::value % kLoadsPerTileOf<NA>;
     if constexpr (tile == 0) lp0.issue(rs[0], t, st);
     else if constexpr (tile == 1) lp1.issue(rs[1], t, st + kTileBytes);
     else if constexpr (tile == 2) lq0.issue(rs[2], t, st + 2 * kTileBytes);
@@ -1186,13 +1201,13 @@ __global__ __launch_bounds__(kThreads) void wg_kernel(WgTask t0, WgTask t1,
   };
   const int w = threadIdx.x >> 6;
   const int wm = w >> 1, wn = w & 1;
-  auto read = [&](const uint8_t* st, auto ks, HalfFrags& f, auto only)
+  auto read = [&](const uint8_t* st, auto ks, HalfFrags<NA>& f, auto only)
                   __attribute__((always_inline)) {
-    read_half<RMajor, RMajor, decltype(ks)::value, kNB, decltype(only)::value>(f, st, wm, wn);
+    read_half<RMajor, RMajor, decltype(ks)::value, kNB, decltype(only)::value, NA>(f, st, wm, wn);
   };
   uint8_t* const ring[kStages] = {st0, st1};
-  run_pipeline<half_lds_ops<RMajor, RMajor>(), false>((size + kBK - 1) / kBK, true, prep, issue,
-                                                      read, acc0, acc1, ring);
+  run_pipeline<half_lds_ops<RMajor, RMajor, kNB, NA>(), false>((size + kBK - 1) / kBK, true, prep,
+                                                               issue, read, acc0, acc1, ring);
 
   // the epilogue re-derives its indices from an opaque copy of the block id,
   // so none of them is held across the K loop
@@ -1480,6 +1495,48 @@ static_assert(kSkippable<KMajor, EpiSwiGLU> <= EpiSwiGLU::kStaleColumnsUnused &&
                   !kSkippable<KMajor, EpiBwdSaved<BF16T>>,
               "the SKIP variant needs an epilogue that ignores stale token columns");
 
+// Wave layout of the token-grouped and weight-gradient products (NA of
+// gemm_pipe.h): 2 = four waves, one per SIMD; 1 = eight waves, two per SIMD.
+// kDefaultNA is the layout each family launches with;
+// uttt_debug_set_gemm_layout forces one process-wide (tests run both).
+// Measured at the 760M batched-update shapes (interleaved runs, per launch):
+// the staged bf16 stores (GD and grad_K, row-major A: 2279 -> 2185-2207 us;
+// grad_V: 1720 / 1722 us) take eight waves; the weight gradients
+// (2393-2408 against 2440-2448 us) and the rest (stage 1 2358 / 2346-2351,
+// DH 1057-1060 / 1054-1068) keep four.
+template <class Epi>
+constexpr int kDefaultNA = 2;
+template <>
+constexpr int kDefaultNA<EpiStore<uint16_t, true>> = 1;
+constexpr int kDefaultWgNA = 2;
+// Epilogues whose eight-wave kernel would spill (the saved-tensor backward
+// epilogue holds four 8-element inputs per item): four waves only.
+template <class Epi>
+constexpr bool kHasNA1 = true;
+template <class LR>
+constexpr bool kHasNA1<EpiBwdSaved<LR>> = false;
+int g_gemm_na = 0;  // 0: each family's default
+int pick_na(int def) { return g_gemm_na != 0 ? g_gemm_na : def; }
+
+template <int AMAJ, class Epi, bool SKIP, int NA>
+void launch_tn_kernel(int64_t blocks, const TnArgs& t, const typename Epi::Args& ea,
+                      hipStream_t st) {
+  hipLaunchKernelGGL((tn_kernel<AMAJ, Epi, SKIP, NA>), dim3((unsigned)blocks),
+                     dim3(kThreadsOf<NA>), 0, st, t, ea);
+}
+
+template <int AMAJ, class Epi, bool SKIP>
+void launch_tn_layout(int64_t blocks, const TnArgs& t, const typename Epi::Args& ea,
+                      hipStream_t st) {
+  if constexpr (kHasNA1<Epi>) {
+    if (pick_na(kDefaultNA<Epi>) == 1) {
+      launch_tn_kernel<AMAJ, Epi, SKIP, 1>(blocks, t, ea, st);
+      return;
+    }
+  }
+  launch_tn_kernel<AMAJ, Epi, SKIP, 2>(blocks, t, ea, st);
+}
+
 template <int AMAJ, class Epi>
 int launch_tn(TnArgs t, const typename Epi::Args& ea, int B, hipStream_t st,
               const char* what) {
@@ -1506,13 +1563,11 @@ int launch_tn(TnArgs t, const typename Epi::Args& ea, int B, hipStream_t st,
   if constexpr (kSkippable<AMAJ, Epi>) {
     static_assert(Epi::kStaleColumnsUnused, "SKIP variant with an epilogue that reads stale columns");
     if ((int64_t)t.N < (int64_t)kBRows * t.E) {
-      hipLaunchKernelGGL((tn_kernel<AMAJ, Epi, true>), dim3((unsigned)blocks), dim3(kThreads), 0,
-                         st, t, ea);
+      launch_tn_layout<AMAJ, Epi, true>(blocks, t, ea, st);
       return check_launch(what);
     }
   }
-  hipLaunchKernelGGL((tn_kernel<AMAJ, Epi, false>), dim3((unsigned)blocks), dim3(kThreads), 0, st,
-                     t, ea);
+  launch_tn_layout<AMAJ, Epi, false>(blocks, t, ea, st);
   return check_launch(what);
 }
 
@@ -1658,12 +1713,19 @@ int launch_wg(WgTask t0, WgTask t1, const int32_t* gs, int B, int E, int N, int 
   // the plain epilogue stores 16 bytes at a time
   UTTT_REQUIRE(splits > 1 || (aligned16(t0.out) && (t1.y_tiles * t1.x_tiles == 0 || aligned16(t1.out))),
                "%s: outputs must be 16-byte aligned", what);
-  if (splits == 1)
-    hipLaunchKernelGGL(wg_kernel<false>, dim3((unsigned)blocks), dim3(kThreads), 0, st, t0, t1, gs,
-                       E, N, B * E, 1);
+  const bool eight = pick_na(kDefaultWgNA) == 1;
+  if (splits == 1 && eight)
+    hipLaunchKernelGGL((wg_kernel<false, 1>), dim3((unsigned)blocks), dim3(kThreadsOf<1>), 0, st,
+                       t0, t1, gs, E, N, B * E, 1);
+  else if (splits == 1)
+    hipLaunchKernelGGL((wg_kernel<false, 2>), dim3((unsigned)blocks), dim3(kThreadsOf<2>), 0, st,
+                       t0, t1, gs, E, N, B * E, 1);
+  else if (eight)
+    hipLaunchKernelGGL((wg_kernel<true, 1>), dim3((unsigned)blocks), dim3(kThreadsOf<1>), 0, st,
+                       t0, t1, gs, E, N, B * E, splits);
   else
-    hipLaunchKernelGGL(wg_kernel<true>, dim3((unsigned)blocks), dim3(kThreads), 0, st, t0, t1, gs,
-                       E, N, B * E, splits);
+    hipLaunchKernelGGL((wg_kernel<true, 2>), dim3((unsigned)blocks), dim3(kThreadsOf<2>), 0, st,
+                       t0, t1, gs, E, N, B * E, splits);
   if (int rc = check_launch(what)) return rc;
   if (splits == 1) return UTTT_OK;
   const int64_t n0 = (int64_t)B * E * t0.X * t0.Y, n1 = (int64_t)B * E * t1.X * t1.Y;
@@ -1771,6 +1833,13 @@ extern "C" int uttt_debug_set_apply_path(int path) {
   const int prev = g_apply_path;
   g_apply_path = path < 0 ? -1 : path > 0 ? 1 : 0;
   g_apply_down_two = path == 2;
+  return prev;
+}
+
+extern "C" int uttt_debug_set_gemm_layout(int na) {
+  UTTT_REQUIRE(na == 0 || na == 1 || na == 2, "debug_set_gemm_layout: na=%d (0, 1 or 2)", na);
+  const int prev = g_gemm_na;
+  g_gemm_na = na;
   return prev;
 }
 

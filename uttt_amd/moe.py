@@ -8,8 +8,10 @@ uttt_llm/flame/custom_models/uttt_moe/modeling_recurrent_lact.py
   route, route_writers                      M:147-169 (_route_tokens; route_writers:
                                             all writers of a chunk in one launch)
   apply_moe_fast_weights_grouped            M:296-349
-  preprocess_update_inputs                  M:630-665 (silu, v norm, per-head k norm)
-  rows_silu_l2norm                          l2_norm of ref_base.py:182-186 (+ silu)
+  preprocess_update_inputs                  M:630-665 (silu, v norm, per-head k norm, rotary)
+  preprocess_read_query                     M:588-601 (the read's q path)
+  rows_preprocess, Rope                     l2_norm / rms_norm of ref_base.py:181-195 (+ silu,
+                                            + the rotary of ref_base.py:342-355, rotary.py)
   moe_update_grads_packed /
   compute_moe_update_grads_grouped          M:453-518
   aggregate_moe_update_grads                M:2381-2546 (the writers' raw
@@ -135,38 +137,125 @@ def apply_moe_fast_weights_grouped(x, w0, w1, w2, router_proj_weights, cfg: Rout
     return merge_head_tokens(out.to(input_dtype), seq_len, num_heads), (balance_sums, group_sizes)
 
 
-def rows_silu_l2norm(x: torch.Tensor, silu: bool, l2: bool, rows_of: int | None = None):
-    """Optional silu, then optional l2 norm x / (|x| + 1e-5) (ref_base.py:182-186)
-    over rows of `rows_of` elements (default: the last dimension) on the HIP
-    kernel; rounding in x's dtype as the reference's tensor arithmetic.
-    Returns a new tensor of x's shape.  Forward only: a tensor that needs a
-    gradient is refused (the reference differentiates through these steps)."""
-    L.require_device(x)
-    assert not (x.requires_grad and torch.is_grad_enabled()), (
-        "rows_silu_l2norm has no backward; call it on detached inputs or under no_grad")
-    x = x.contiguous()
-    D = x.shape[-1] if rows_of is None else rows_of
-    assert x.numel() % D == 0, "rows must tile the tensor"
-    out = torch.empty_like(x)
-    L.call("uttt_rows_silu_l2norm", L.ptr(x), L.dtype_code(x.dtype), x.numel() // D, D, D,
-           int(silu), int(l2), L.ptr(out), D, L.stream_of(x))
-    return out
+@dataclass(frozen=True)
+class Rope:
+    """The fast-weight rotary embedding of one call: the reference's bf16
+    cos / sin caches ([positions, rope_dim / 2], RotaryEmbedding
+    _update_cos_sin_cache, rotary.py:394-433, as ref_base.py:342-355 builds
+    it) and the call's seqlen_offset.  Rotary blocks of rope_dim features tile
+    each token's feature vector (rearrange 'b l (nh d) -> b l nh d')."""
+
+    cos: torch.Tensor
+    sin: torch.Tensor
+    seqlen_offset: int = 0
+
+    @property
+    def dim(self) -> int:
+        return 2 * self.cos.shape[-1]
+
+    @staticmethod
+    def tables(dim: int, base: float, max_len: int, device, dtype=torch.bfloat16):
+        """The cos / sin cache as RotaryEmbedding builds it (rotary.py:385-433,
+        no xpos scale): fp32 positions, inv_freq = 1 / base^(2i / dim), freqs =
+        outer(t, inv_freq), cos / sin in fp32 rounded to `dtype`."""
+        inv_freq = 1.0 / (float(base) ** (torch.arange(0, dim, 2, device=device,
+                                                       dtype=torch.float32) / dim))
+        t = torch.arange(max_len, device=device, dtype=torch.float32)
+        freqs = torch.outer(t, inv_freq)
+        return torch.cos(freqs).to(dtype).contiguous(), torch.sin(freqs).to(dtype).contiguous()
+
+
+_NORMS = {None: 0, "l2": 1, "rms": 2}
+
+
+def _prep_geometry(x, rows_of, rope):
+    B, Lx, HD = x.shape
+    D = HD if rows_of is None else rows_of
+    assert HD % D == 0, "rows must tile each token's features"
+    if rope is None:
+        return D, HD // D, Lx, 0, 0, None, None, 0, 0
+    assert rope.cos.dtype == torch.bfloat16 and rope.sin.dtype == torch.bfloat16, (
+        "the rotary tables must be bf16 (the reference's cache dtype)")
+    assert rope.cos.shape == rope.sin.shape, "cos / sin tables of one shape"
+    assert rope.seqlen_offset + Lx <= rope.cos.shape[0], "positions past the rotary tables"
+    assert HD % rope.dim == 0, "rotary blocks must tile the features"
+    return (D, HD // D, Lx, rope.dim, rope.seqlen_offset, rope.cos.contiguous(),
+            rope.sin.contiguous(), rope.cos.shape[0], 1)
+
+
+class _RowsPreprocess(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, silu, norm, rows_of, rope):
+        L.require_device(x)
+        x = x.contiguous()
+        D, rpt, Lx, rdim, off, cos, sin, trows, _ = _prep_geometry(x, rows_of, rope)
+        out_dtype = torch.bfloat16 if rope is not None else x.dtype
+        out = torch.empty(x.shape, dtype=out_dtype, device=x.device)
+        rows = x.numel() // D
+        L.call("uttt_rows_preprocess", L.ptr(x), L.dtype_code(x.dtype), rows, D, D, int(silu),
+               _NORMS[norm], L.ptr(cos) if cos is not None else None,
+               L.ptr(sin) if sin is not None else None, rdim, rpt, Lx, off, trows, L.ptr(out), D,
+               L.stream_of(x))
+        ctx.save_for_backward(x)
+        ctx.args = (silu, norm, rows_of, rope)
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        (x,) = ctx.saved_tensors
+        silu, norm, rows_of, rope = ctx.args
+        D, rpt, Lx, rdim, off, cos, sin, trows, _ = _prep_geometry(x, rows_of, rope)
+        out_dtype = torch.bfloat16 if rope is not None else x.dtype
+        g = g.to(out_dtype).contiguous()
+        gin = torch.empty_like(x)
+        L.call("uttt_rows_preprocess_bwd", L.ptr(x), L.dtype_code(x.dtype), L.ptr(g),
+               x.numel() // D, D, D, D, int(silu), _NORMS[norm],
+               L.ptr(cos) if cos is not None else None, L.ptr(sin) if sin is not None else None,
+               rdim, rpt, Lx, off, trows, L.ptr(gin), L.stream_of(x))
+        return gin, None, None, None, None
+
+
+def rows_preprocess(x: torch.Tensor, *, silu: bool = False, norm: str | None = None,
+                    rows_of: int | None = None, rope: Rope | None = None) -> torch.Tensor:
+    """The reference's row preprocessing of q / k / v [B, L, H*hd] on one HIP
+    kernel: optional F.silu, then the optional parameter-free norm over rows
+    of `rows_of` features (default: the whole vector) -- "l2" is l2_norm,
+    x / (|x| + 1e-5), "rms" is rms_norm, x * rsqrt(mean(x^2) + 1e-5)
+    (ref_base.py:181-195) -- then the optional rotary embedding (the input
+    cast to the bf16 tables' dtype, rotated, bf16 out; rotary.py:83-104).
+    Differentiable: the backward is the conjugate rotation, the norm's and the
+    silu's backward on one kernel, rounded where the reference's autograd
+    rounds.  Returns a new tensor (bf16 with rope, else x's dtype)."""
+    assert norm in _NORMS, f"norm must be None, 'l2' or 'rms', got {norm!r}"
+    return _RowsPreprocess.apply(x, bool(silu), norm, rows_of, rope)
+
+
+def _norm_name(flag: bool, kind: str):
+    assert kind in ("l2", "rms"), f"norm type must be 'l2' or 'rms', got {kind!r}"
+    return kind if flag else None
 
 
 def preprocess_update_inputs(k, v, lr, num_heads: int, *, qkv_silu: bool = False,
-                             v_norm: bool = False, qk_norm: bool = False):
-    """_preprocess_update_inputs (M:630-665) with the l2 norms
-    (memory_norm_type / memory_qk_norm_type "l2"): optional silu of k and v,
-    optional l2 norm of v over its last dimension, optional per-head l2 norm
-    of k (each on the row kernel), then head tokens, and lr [B, L, 3] (shared
-    by the heads) or [B, L, 3H] spread to [B, L*H, 3].  The learned qk
-    rescale and the rotary embedding belong to the model, not to this path:
-    apply them to k first."""
+                             v_norm: bool = False, qk_norm: bool = False,
+                             norm_type: str = "rms", qk_norm_type: str = "l2",
+                             rope: Rope | None = None):
+    """_preprocess_update_inputs (M:630-665) after the learned qk rescale:
+    k -> [silu] -> [qk norm per head, qk_norm_type] -> [rotary] and
+    v -> [silu] -> [v norm over the whole vector, norm_type], in the
+    reference's order (rotary last, on the normalised k), then head tokens,
+    and lr [B, L, 3] (shared by the heads) or [B, L, 3H] spread to
+    [B, L*H, 3].  norm_type / qk_norm_type default to the reference's config
+    defaults (memory_norm_type "rms", memory_qk_norm_type "l2",
+    configuration_recurrent_lact_base.py:66-67).  Differentiable in k, v and
+    lr.  The learned qk rescale (memory_qk_rescale, M:637-638) comes first in
+    the reference and stays with the model: apply it to k before this call."""
     B, Lx, HD = k.shape
-    if qkv_silu or qk_norm:
-        k = rows_silu_l2norm(k, qkv_silu, qk_norm, rows_of=HD // num_heads)
+    hd = HD // num_heads
+    if qkv_silu or qk_norm or rope is not None:
+        k = rows_preprocess(k, silu=qkv_silu, norm=_norm_name(qk_norm, qk_norm_type),
+                            rows_of=hd if qk_norm else None, rope=rope)
     if qkv_silu or v_norm:
-        v = rows_silu_l2norm(v, qkv_silu, v_norm)
+        v = rows_preprocess(v, silu=qkv_silu, norm=_norm_name(v_norm, norm_type))
     k_tokens = reshape_head_tokens(k, num_heads)
     v_tokens = reshape_head_tokens(v, num_heads)
     if lr.shape[2] == 3:
@@ -175,6 +264,18 @@ def preprocess_update_inputs(k, v, lr, num_heads: int, *, qkv_silu: bool = False
         lr_mh = lr.view(B, Lx, num_heads, 3)
     lr_tokens = lr_mh.reshape(B, Lx * num_heads, 3).contiguous()
     return k_tokens, v_tokens, lr_tokens
+
+
+def preprocess_read_query(q, num_heads: int, *, qkv_silu: bool = False, qk_norm: bool = False,
+                          qk_norm_type: str = "l2", rope: Rope | None = None):
+    """The MoE read's q path (M:588-601) after the learned qk rescale:
+    q -> [silu] -> [qk norm per head] -> [rotary], one kernel; returns
+    [B, L, H*hd] for apply_moe_fast_weights_grouped.  Differentiable."""
+    if not (qkv_silu or qk_norm or rope is not None):
+        return q
+    hd = q.shape[-1] // num_heads
+    return rows_preprocess(q, silu=qkv_silu, norm=_norm_name(qk_norm, qk_norm_type),
+                           rows_of=hd if qk_norm else None, rope=rope)
 
 
 def moe_update_grads_packed(k_tokens, v_tokens, lr_tokens, w0_w2, w1, expert_mask, group_sizes,
