@@ -472,11 +472,22 @@ class MoeSweep:
 
     # ---------------------------------------------------------- accounting --
     def apply_symbols(self):
-        """Kernel symbols of the APPLY's gate/up and down projection (the
-        skinny-tile kernel when experts average under 256 rows)."""
-        if self.N < 256 * self.E:
-            return ("apply_kernel<ApSwiGLU, true>", "apply_kernel<ApStore, false>")
-        return ("tn_kernel<0, EpiSwiGLU, false>", "tn_kernel<0, EpiStore<unsigned short, true>, false>")
+        """Kernel symbols of the APPLY's gate/up and down projection, as the
+        library picks them by the sizes: gate/up on the skinny tiles when the
+        experts average at most 256 routed rows; the down projection on them
+        when also the general 256x256 tiles would not fill the 256 CUs once
+        (upper-bound tile count), else on the general tiles (their MFMA-skipping
+        variant below 256 rows per expert)."""
+        N, E, D = self.N, self.E, self.D
+        skinny = N <= 256 * E
+        gate = "apply_kernel<ApSwiGLU, true>" if skinny else "tn_kernel<0, EpiSwiGLU, false>"
+        tn_tiles = -(-D // 256) * (-(-N // 256) + E)
+        if skinny and tn_tiles < 256:
+            down = "apply_kernel<ApStore, false>"
+        else:
+            skip = "true" if N < 256 * E else "false"
+            down = f"tn_kernel<0, EpiStore<unsigned short, true>, {skip}>"
+        return gate, down
 
     def launch_table(self, layers, chunks, batched):
         """Every kernel launch of one sweep that carries GEMM work, grouped by
@@ -658,7 +669,7 @@ def bench_moe(args, key, extras=True):
         sw.sweep(layers, 2, batched)
     torch.cuda.synchronize()
     walls = []
-    with LiveLaunchTimer() as live:
+    with LiveLaunchTimer(sw.apply_symbols()) as live:
         for _ in range(args.steps):
             torch.cuda.synchronize()
             t0 = time.perf_counter()
@@ -773,11 +784,12 @@ class LiveLaunchTimer:
     points that launch exactly one kernel symbol, during the timed sweeps
     (the product code calls the library through uttt_amd._lib.call)."""
 
-    # entry point -> the one kernel symbol it launches in the MoE sweep (the
-    # weight gradients of the UPDATE forward; the APPLY's two products)
-    ENTRIES = {"uttt_grouped_wgrad_pair": "wg_kernel<false>",
-               "uttt_grouped_gate_up": "apply_kernel<ApSwiGLU, true>",
-               "uttt_grouped_gemm_nt": "apply_kernel<ApStore, false>"}
+    def __init__(self, apply_symbols):
+        # entry point -> the one kernel symbol it launches in the MoE sweep (the
+        # weight gradients of the UPDATE forward; the APPLY's two products)
+        gate, down = apply_symbols
+        self.ENTRIES = {"uttt_grouped_wgrad_pair": "wg_kernel<false>",
+                        "uttt_grouped_gate_up": gate, "uttt_grouped_gemm_nt": down}
 
     def __enter__(self):
         import torch

@@ -389,10 +389,11 @@ long long uttt_debug_set_supertile_min_tiles(long long min_tiles);
 
 /* Test hook: which kernel runs the weight-streaming APPLY products
  * (uttt_grouped_gate_up with token_major, uttt_grouped_gemm_nt): -1 by the
- * sizes (the skinny-tile three-stage kernel when N < 256 * E), 0 the general
- * tiles, 1 the skinny tiles (128-row down-projection tiles), 2 the skinny
- * tiles with 256-row down-projection tiles.  Results are identical on every
- * path.  Returns the previous value. */
+ * sizes (gate/up on the skinny-tile three-stage kernel when N <= 256 * E;
+ * uttt_grouped_gemm_nt on it when also the general 256x256 tiles would not
+ * fill the 256 CUs once), 0 the general tiles, 1 the skinny tiles (128-row
+ * down-projection tiles), 2 the skinny tiles with 256-row down-projection
+ * tiles.  Results are identical on every path.  Returns the previous value. */
 int uttt_debug_set_apply_path(int path);
 
 /* Test hook (no reference counterpart): the wave layout of the token-grouped

@@ -1571,15 +1571,32 @@ int launch_tn(TnArgs t, const typename Epi::Args& ea, int B, hipStream_t st,
   return check_launch(what);
 }
 
-// APPLY path: 0 = tn_kernel, 1 = apply_kernel, -1 = by the sizes (apply_kernel
-// when the experts average under 256 routed rows, as the per-layer APPLY does).
-// Both give identical results; a process-wide value so that tests can run
-// either path (uttt_debug_set_apply_path).
+// APPLY path: 0 = tn_kernel, 1 = apply_kernel, -1 = by the sizes.  Both give
+// identical results; a process-wide value so that tests can run either path
+// (uttt_debug_set_apply_path).
 int g_apply_path = -1;
 bool g_apply_down_two = false;  // down products on 256-row tiles (default 128: twice the tiles)
+constexpr int kCUs = 256;       // MI355X compute units
 
+// Gate/up (256-row weight tiles either way): the skinny 128-token tiles when
+// the experts average at most 256 routed rows (configs[3]: 129 -> 100 us per
+// apply with the down projection below; configs[4] gate/up 188 -> 184 us).
 bool use_apply_kernel(int64_t N, int E) {
-  return g_apply_path == 1 || (g_apply_path < 0 && N < (int64_t)kBRows * E);
+  return g_apply_path == 1 || g_apply_path == 2 ||
+         (g_apply_path < 0 && N <= (int64_t)kBRows * E);
+}
+
+// The down projection (and every uttt_grouped_gemm_nt): the skinny tiles
+// (128 weight rows x 128 tokens) when the general 256x256 tiles would not
+// fill the chip once even at their upper-bound count, else the general tiles.
+// configs[3] (3 x 32 tiles of 256): 38.9 -> 21.5 us; configs[4] (6 x 48):
+// the general tiles, 101 us against 110 us on the skinny ones.
+bool use_apply_kernel_nt(int64_t N, int E, int B, int M) {
+  if (g_apply_path >= 0) return g_apply_path > 0;
+  if (N > (int64_t)kBRows * E) return false;
+  const int64_t tn_tiles =
+      (int64_t)B * ((M + kBRows - 1) / kBRows) * ((N + kBRows - 1) / kBRows + E);
+  return tn_tiles < kCUs;
 }
 
 template <class Epi, bool TWO>
@@ -1672,7 +1689,6 @@ WgTask wg_task(const void* p, const void* q, void* out, int X, int Y) {
 // each at least kMinSplitSteps K steps of the mean segment N / E, at most
 // kMaxSplits.  A pure function of the sizes, so the workspace query and the
 // launch agree.
-constexpr int kCUs = 256;
 constexpr int kMinSplitSteps = 8;
 constexpr int kMaxSplits = 32;
 
@@ -1772,7 +1788,7 @@ extern "C" int uttt_grouped_gemm_nt(const void* w, const void* x, const int32_t*
   UTTT_REQUIRE(w && x && group_sizes && y, "grouped_gemm_nt: null pointer");
   UTTT_REQUIRE(aligned16(w) && aligned16(x) && aligned16(y),
                "grouped_gemm_nt: tensors must be 16-byte aligned");
-  if (use_apply_kernel(N, E)) {
+  if (use_apply_kernel_nt(N, E, B, M)) {
     const ApStore::Args ea{static_cast<uint16_t*>(y), M, M, N};
     if (g_apply_down_two) {
       const ApArgs a = apply_args(w, x, K, (int64_t)M * K, kTileRows, M, M, 2 * kTileRows, B, E, N,
