@@ -426,6 +426,25 @@ int uttt_write_step(const float* master, const void* fast_in, const void* grad, 
                     int64_t rows_per_batch, int C, int seg, int norm_from_fast, int renorm_master,
                     float* master_out, void* fast_out, float* mom_out, void* stream);
 
+/* Sequence-start row norms of the single-layer LaCT's prenorm write
+ * (w0_norm = w0.norm(dim=2) etc., uttt_nvs/models/kernels/ttt_operation.py:
+ * 258-260): norms[r] = |w row r| in fp32 for `rows` rows of C elements
+ * (dtype UTTT_F32, UTTT_BF16 or UTTT_F16; C a multiple of 4, at most 4096;
+ * w 16-byte aligned). */
+int uttt_row_norms(const void* w, int dtype, int64_t rows, int C, float* norms, void* stream);
+
+/* Prenorm WRITE of the single-layer LaCT (prenorm_block_causal_lact_swiglu,
+ * uttt_nvs/models/kernels/ttt_operation.py:217-367; the write at :341-353):
+ * per row r of C elements, U = main + grad (fp32; the step carries its
+ * learning rates, no scale), main_out = U and
+ * fast_out = bf16(U / (|U| + 1e-5) * norms[r]), norms being the row norms
+ * captured at the start of the sequence (uttt_row_norms).  main and
+ * main_out fp32 (may alias), grad fp32 / bf16 / fp16, fast_out bf16; C a
+ * multiple of 4, at most 4096. */
+int uttt_write_prenorm(const float* main_w, const void* grad, int grad_dtype,
+                       const float* norms, int64_t rows, int C, float* main_out,
+                       void* fast_out, void* stream);
+
 /* Unit-row WRITE of the NVS block.  Replaces the write of apply_raw_update
  * (uttt_nvs/models/uttt_moe_block.py:665-714; Muon, when on, runs before it
  * through uttt_newton_schulz5):

@@ -64,7 +64,11 @@ def test_dense_write_matches_oracle(master_renorm, mom):
     b, h, d, r = 1, 4, 96, 2   # configs[0] head shape: d = 96, d_h = 192
     shapes = [(b, h, r * d, d), (b, h, d, r * d), (b, h, r * d, d)]
     masters = [_rand(s, i) / d ** 0.5 for i, s in enumerate(shapes)]
-    fast = [(w * 1.003).to(torch.bfloat16) for w in masters]
+    # fast weights 3-6% off their masters, row by row: a write that took the
+    # norms from the masters instead of the fast weights fails the bar below
+    gap = torch.Generator().manual_seed(31)
+    fast = [(w * (1.03 + 0.03 * torch.rand(w.shape[:-1] + (1,), generator=gap)))
+            .to(torch.bfloat16) for w in masters]
     grads = [_rand(s, 10 + i, 0.02) for i, s in enumerate(shapes)]
     moms = [_rand(s, 20 + i, 0.02) for i, s in enumerate(shapes)] if mom else None
     coeffs = [torch.full((b, 1, 1, 1), 0.4), torch.full((b, 1, 1, 1), 0.6)] if mom else None
@@ -84,6 +88,14 @@ def test_dense_write_matches_oracle(master_renorm, mom):
             assert torch.equal(om[i].cpu(), rm[i])
         if mom:
             assert torch.equal(omom[i].cpu(), rmom[i])
+    if not master_renorm:
+        # planted mistake: the same write with the norms of the masters (the
+        # master-renorm mode's source) is off the kernel's result by more
+        # than the fast-weight bar
+        wf, _, _ = OW.dense_write(grads, [w.to(torch.bfloat16) for w in masters], masters, r,
+                                  moms, coeff, lr_scale=0.5, master_renorm=False)
+        assert max(((of[i].cpu().float() - wf[i].float()).abs()
+                    / (wf[i].float().abs() + 1e-6)).max().item() for i in range(3)) > 2e-2
 
 
 def test_write_in_place_equals_out_of_place():

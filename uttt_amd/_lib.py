@@ -108,6 +108,8 @@ SIGNATURES = {
          c_int, c_int, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_sz, c_p],
     ),
     "uttt_transpose_2byte": (c_int, [c_p, c_int, c_int, c_int, c_p, c_p]),
+    "uttt_row_norms": (c_int, [c_p, c_int, c_i64, c_int, c_p, c_p]),
+    "uttt_write_prenorm": (c_int, [c_p, c_p, c_int, c_p, c_i64, c_int, c_p, c_p, c_p]),
     "uttt_rows_preprocess": (c_int, [c_p, c_int, c_i64, c_int, c_i64, c_int, c_int, c_p, c_p,
                                      c_int, c_int, c_int, c_int, c_int, c_p, c_i64, c_p]),
     "uttt_rows_preprocess_bwd": (c_int, [c_p, c_int, c_p, c_i64, c_int, c_i64, c_i64, c_int,

@@ -16,8 +16,8 @@
 //     6 fragment reads.  A SIMD holds two waves, so one wave's MFMAs run
 //     while the other waits on its reads, loads or barrier.
 //
-// Global -> LDS: global_load_lds_dwordx4 (16 bytes per lane straight into LDS,
-// no register staging) into two 64 KiB stages (kBK = 64), the loads of stage
+// Global -> LDS: buffer_load_dwordx4 ... lds (16 bytes per lane straight into
+// LDS, no register staging) into two 64 KiB stages (kBK = 64), the loads of stage
 // k+1 in flight while stage k is multiplied; the only waits are
 // explicit s_waitcnt vmcnt counts and one s_barrier per step.  Each stage lives
 // in its own __shared__ array so the compiler can tell the in-flight LDS

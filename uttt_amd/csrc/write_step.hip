@@ -202,6 +202,76 @@ __global__ __launch_bounds__(kWS) void write_unit_rows_kernel(
   }
 }
 
+// Prenorm write of the single-layer LaCT (prenorm_block_causal_lact_swiglu,
+// uttt_nvs/models/kernels/ttt_operation.py:217-367): U = main + grad (one fp32
+// add: the step carries its learning rates), main_out = U and
+// fast_out = bf16(U / (|U| + 1e-5) * nu) with nu = norms[row], the row norm
+// captured once at the start of the sequence (ttt_operation.py:258-260), so
+// every chunk's weights are projected back onto the same norms
+// (ttt_operation.py:351-353).  One wave per row, as write_step_kernel; main_out
+// may alias main.
+template <class GT, int NV>
+__global__ __launch_bounds__(kWS) void write_prenorm_kernel(
+    const float* main_w, const typename GT::S* __restrict__ grad,
+    const float* __restrict__ norms, int64_t nrows, int C, float* main_out,
+    uint16_t* __restrict__ fast_out) {
+#pragma clang fp contract(off)
+  const int64_t row = (int64_t)blockIdx.x * (kWS / kWave) + threadIdx.x / kWave;
+  if (row >= nrows) return;  // whole wave leaves together
+  const int lane = lane_id();
+  const int64_t base = row * C;
+  const float nu = norms[row];
+  float4 u[NV];
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int e = 4 * (lane + kWave * i);
+    const bool ok = e < C;
+    const int ec = ok ? e : 0;
+    const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const float4 wl = nt_load4(main_w + base + ec);
+    const float4 gl = load_grad4<GT>(grad + base + ec);
+    const float4 w = ok ? wl : z;
+    const float4 g = ok ? gl : z;
+    u[i] = make_float4(w.x + g.x, w.y + g.y, w.z + g.z, w.w + g.w);
+    ss += sumsq4(u[i]);
+  }
+  const float den = sqrtf(wave_sum(ss)) + 1e-5f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int e = 4 * (lane + kWave * i);
+    if (e < C) {
+      nt_store4(main_out + base + e, u[i]);
+      Half4 f;
+      f.h[0] = f32_to_bf16(u[i].x / den * nu);
+      f.h[1] = f32_to_bf16(u[i].y / den * nu);
+      f.h[2] = f32_to_bf16(u[i].z / den * nu);
+      f.h[3] = f32_to_bf16(u[i].w / den * nu);
+      nt_store_h4(fast_out + base + e, f);
+    }
+  }
+}
+
+// norms[row] = |row| in fp32 (the sequence-start norms of the prenorm write).
+template <class TT, int NV>
+__global__ __launch_bounds__(kWS) void row_norms_kernel(const typename TT::S* __restrict__ w,
+                                                        int64_t nrows, int C,
+                                                        float* __restrict__ norms) {
+  const int64_t row = (int64_t)blockIdx.x * (kWS / kWave) + threadIdx.x / kWave;
+  if (row >= nrows) return;
+  const int lane = lane_id();
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int e = 4 * (lane + kWave * i);
+    const bool ok = e < C;
+    const float4 v = load_grad4<TT>(w + row * C + (ok ? e : 0));
+    ss += ok ? sumsq4(v) : 0.0f;
+  }
+  ss = wave_sum(ss);
+  if (lane == 0) norms[row] = sqrtf(ss);
+}
+
 inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 // out = raw + m_coeff[b] * mom (fp32, the product rounded before the sum as the
@@ -350,4 +420,59 @@ extern "C" int uttt_write_unit_rows(const float* master, int64_t master_gs, cons
   });
 #undef UTTT_WU_LAUNCH
   return check_launch("write_unit_rows");
+}
+
+// NV = vectors of 4 per lane: C <= 256 * NV
+#define UTTT_NV_SWITCH(C, NV, ...)                                   \
+  if ((C) <= 256) { constexpr int NV = 1; __VA_ARGS__; }             \
+  else if ((C) <= 1024) { constexpr int NV = 4; __VA_ARGS__; }       \
+  else if ((C) <= 2048) { constexpr int NV = 8; __VA_ARGS__; }       \
+  else { constexpr int NV = 16; __VA_ARGS__; }
+
+extern "C" int uttt_row_norms(const void* w, int dtype, int64_t rows, int C, float* norms,
+                              void* stream) {
+  UTTT_REQUIRE(rows >= 0 && C >= 0, "row_norms: bad sizes");
+  if (rows == 0) return UTTT_OK;
+  UTTT_REQUIRE(w && norms, "row_norms: null pointer");
+  UTTT_REQUIRE(C % 4 == 0 && C > 0 && C <= 4096,
+               "row_norms: rows of %d elements (a multiple of 4, at most 4096)", C);
+  UTTT_REQUIRE(aligned(w, 16), "row_norms: w must be 16-byte aligned");
+  UTTT_REQUIRE(dtype == UTTT_F32 || dtype == UTTT_BF16 || dtype == UTTT_F16,
+               "row_norms: unsupported dtype %d", dtype);
+  const int64_t blocks = (rows + kWS / kWave - 1) / (kWS / kWave);
+  UTTT_REQUIRE(blocks <= 0x7fffffffLL, "row_norms: too many rows");
+  hipStream_t st = as_stream(stream);
+  UTTT_DTYPE_SWITCH_LR(dtype, TT, {
+    UTTT_NV_SWITCH(C, NV, {
+      hipLaunchKernelGGL((row_norms_kernel<TT, NV>), dim3((unsigned)blocks), dim3(kWS), 0, st,
+                         static_cast<const typename TT::S*>(w), rows, C, norms);
+    });
+  });
+  return check_launch("row_norms");
+}
+
+extern "C" int uttt_write_prenorm(const float* main_w, const void* grad, int grad_dtype,
+                                  const float* norms, int64_t rows, int C, float* main_out,
+                                  void* fast_out, void* stream) {
+  UTTT_REQUIRE(rows >= 0 && C >= 0, "write_prenorm: bad sizes");
+  if (rows == 0) return UTTT_OK;
+  UTTT_REQUIRE(main_w && grad && norms && main_out && fast_out, "write_prenorm: null pointer");
+  UTTT_REQUIRE(C % 4 == 0 && C > 0 && C <= 4096,
+               "write_prenorm: rows of %d elements (a multiple of 4, at most 4096)", C);
+  UTTT_REQUIRE(aligned(main_w, 16) && aligned(grad, 8) && aligned(main_out, 16) &&
+                   aligned(fast_out, 8),
+               "write_prenorm: misaligned tensor");
+  UTTT_REQUIRE(grad_dtype == UTTT_F32 || grad_dtype == UTTT_BF16 || grad_dtype == UTTT_F16,
+               "write_prenorm: unsupported grad dtype %d", grad_dtype);
+  const int64_t blocks = (rows + kWS / kWave - 1) / (kWS / kWave);
+  UTTT_REQUIRE(blocks <= 0x7fffffffLL, "write_prenorm: too many rows");
+  hipStream_t st = as_stream(stream);
+  UTTT_DTYPE_SWITCH_LR(grad_dtype, GT, {
+    UTTT_NV_SWITCH(C, NV, {
+      hipLaunchKernelGGL((write_prenorm_kernel<GT, NV>), dim3((unsigned)blocks), dim3(kWS), 0, st,
+                         main_w, static_cast<const typename GT::S*>(grad), norms, rows, C,
+                         main_out, static_cast<uint16_t*>(fast_out));
+    });
+  });
+  return check_launch("write_prenorm");
 }

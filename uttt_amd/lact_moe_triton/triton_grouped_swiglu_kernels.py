@@ -2,7 +2,8 @@
 
 Drop-in for the reference module
 uttt_llm/flame/custom_models/uttt_moe/lact_moe_triton/triton_grouped_swiglu_kernels.py
-(cited S:line); kernel in csrc/grouped_gemm.hip (gate_up_kernel).
+(cited S:line); kernels in csrc/grouped_gemm.hip (tn_kernel with the EpiSwiGLU
+epilogue; apply_kernel<ApSwiGLU> for the token-major per-layer APPLY).
 """
 from __future__ import annotations
 
