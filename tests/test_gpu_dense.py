@@ -230,3 +230,57 @@ def test_fused_dense_update_stage1(BH, N, d, dh, with_lr):
     dy2, hl2 = DN._update_stage1(W02, W1, kh, vh, lr3, gs, DN._pack_update(W02, W1))
     torch.cuda.synchronize()
     assert torch.equal(dy2, dy) and torch.equal(hl2, hl)
+
+
+@pytest.mark.parametrize("use_moun,with_mom,master_renorm", [
+    (False, True, False), (True, False, False), (True, True, False), (True, True, True)])
+def test_bank_momentum_and_muon_equal_the_functional_write(use_moun, with_mom, master_renorm):
+    # the bank's write (batched UPDATE of one layer, momentum on the
+    # (batch, head) buffers, Newton-Schulz per d x d slice of the packed
+    # weights) against fast_weight_write.apply_shared_update on the same
+    # aggregate update, whose arithmetic is checked against the oracle in
+    # tests/test_gpu_write.py and tests/test_gpu_muon.py: bit-identical
+    from uttt_amd import fast_weight_write as FWW
+
+    b, H, d, r, l = 2, 4, 96, 2, 512
+    fast = tuple(w.to(torch.bfloat16).to(DEV) for w in _weights(b, H, d, r, seed=11))
+    g = torch.Generator().manual_seed(12)
+    masters = tuple((w.float().cpu() * (1 + 0.01 * torch.rand(w.shape, generator=g))).to(DEV)
+                    for w in fast)
+    moms = tuple((torch.randn(w.shape, generator=g) * 0.01).to(DEV) for w in fast)
+    coeffs = [torch.rand(b, 1, 1, 1, generator=g).to(DEV) for _ in range(1)]
+    q, k, v, lr = (t.to(DEV) for t in _layer(b, l, H, d, seed=13))
+    bank = DN.SharedFastWeights(*fast, r=r, masters=masters, lr_scale=0.7,
+                                master_renorm=master_renorm, use_momentum=with_mom,
+                                use_moun=use_moun)
+    bank.set_weights(fast, masters, moms if with_mom else None)
+    agg = DN.compute_update(k, v, lr, fast)
+    bank.write([k], [v], [lr], momentum_coeffs=coeffs if with_mom else None)
+    rf, rm, rmom = FWW.apply_shared_update(agg, fast, masters, moms if with_mom else None,
+                                           coeffs if with_mom else None, r=r, lr_scale=0.7,
+                                           master_renorm=master_renorm, use_moun=use_moun)
+    (bf, bm) = bank.weights()
+    for i in range(3):
+        assert torch.equal(bf[i], rf[i]), f"fast {i}"
+        assert torch.equal(bm[i], rm[i]), f"master {i}"
+    if with_mom:
+        for x, y in zip(bank.momentum(), rmom):
+            assert torch.equal(x, y)
+
+
+def test_bank_owns_its_weights():
+    # weights() hands out copies: editing one leaves the bank's reads alone
+    b, H, d, r, l = 1, 4, 96, 2, 64
+    fast = tuple(w.to(torch.bfloat16).to(DEV) for w in _weights(b, H, d, r, seed=21))
+    q = _layer(b, l, H, d, seed=22)[0].to(DEV)
+    bank = DN.SharedFastWeights(*fast, r=r)
+    before = bank.read(q).clone()
+    bank.read(q)                                   # second read: the packed copy is built
+    (w0, w1, w2), _ = bank.weights()
+    w0.zero_()
+    assert torch.equal(bank.read(q), before)
+    # set_weights replaces the state and drops the packed copy
+    bank.set_weights((w0, w1, w2))
+    assert not torch.equal(bank.read(q), before)
+    fresh = DN.SharedFastWeights(w0, w1, w2, r=r)
+    assert torch.equal(bank.read(q), fresh.read(q))

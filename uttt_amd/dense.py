@@ -219,13 +219,17 @@ class SharedFastWeights:
     """The shared fast-weight bank of uTTT-Dense (D:1801-1863), aggregate
     schedule: read() every layer of a chunk with the chunk-start weights, then
     write() once from the mean (or sum) of the layers' updates, projected per
-    d x d slice onto the old slice norms (_apply_shared_update).
+    d x d slice onto the old slice norms (_apply_shared_update, D:1109-1240),
+    with the optional momentum (the buffer keeps the pre-Muon aggregate,
+    D:1175-1185) and Muon (Newton-Schulz per d x d slice, D:1192-1203) of the
+    shipped configs.
 
     w0, w2: [b, H, r*d, d]; w1: [b, H, d, r*d]; masters fp32 (default: the
-    given weights in fp32).  Momentum and Muon are not part of this write."""
+    given weights in fp32).  The bank owns its weights: weights() returns
+    copies and set_weights() replaces them (and drops the read's packed copy)."""
 
     def __init__(self, w0, w1, w2, r, masters=None, lr_scale=1.0, reduce="mean",
-                 master_renorm=False):
+                 master_renorm=False, use_momentum=False, use_moun=False):
         b, H, dh, d = w0.shape
         if dh != r * d or tuple(w1.shape) != (b, H, d, r * d) or w2.shape != w0.shape:
             raise ValueError(f"invalid shared fast state shapes for r={r}")
@@ -234,13 +238,9 @@ class SharedFastWeights:
         L.require_device(w0, w1, w2)
         self.b, self.H, self.d, self.dh, self.r = b, H, d, dh, r
         self.lr_scale, self.reduce, self.master_renorm = float(lr_scale), reduce, master_renorm
-        m0, m1, m2 = masters if masters is not None else (w0, w1, w2)
-        self.M02 = torch.cat([m0, m2], dim=2).float().reshape(b * H, 1, 2 * dh, d).contiguous()
-        self.M1 = m1.float().reshape(b * H, 1, d, dh).contiguous()
-        self.W02 = torch.cat([w0, w2], dim=2).to(torch.bfloat16).reshape(b * H, 1, 2 * dh, d).contiguous()
-        self.W1 = w1.to(torch.bfloat16).reshape(b * H, 1, d, dh).contiguous()
-        self._spare02 = torch.empty_like(self.W02)
-        self._spare1 = torch.empty_like(self.W1)
+        self.use_momentum, self.use_moun = bool(use_momentum), bool(use_moun)
+        self._spare02 = torch.empty((b * H, 1, 2 * dh, d), dtype=torch.bfloat16, device=w0.device)
+        self._spare1 = torch.empty((b * H, 1, d, dh), dtype=torch.bfloat16, device=w0.device)
         # The read's fragment-ordered copy of W02/W1 (one extra pass over the
         # weights) pays off only when the same weights are read more than once:
         # it is rebuilt at a write that aggregated several layers (the next
@@ -248,9 +248,29 @@ class SharedFastWeights:
         supported = L.lib().uttt_dense_read_supported(d, dh)
         self.P = (torch.empty(b * H * 3 * dh * d, dtype=torch.bfloat16, device=w0.device)
                   if supported else None)
-        self._packed, self._reads = False, 0
         self._upacked = (torch.empty(b * H * 3 * dh * d, dtype=torch.bfloat16, device=w0.device)
                          if L.lib().uttt_dense_update_supported(d, dh) else None)
+        self.set_weights((w0, w1, w2), masters)
+
+    def set_weights(self, fastw, masters=None, momentum=None):
+        """Load (w0, w1, w2) fast weights (and fp32 masters, default the fast
+        weights in fp32; and the momentum buffers, default zero) into the
+        bank's own storage (copies: the writes update it in place)."""
+        b, H, dh, d = self.b, self.H, self.dh, self.d
+        w0, w1, w2 = fastw
+        m0, m1, m2 = masters if masters is not None else fastw
+        self.M02 = torch.cat([m0, m2], dim=2).float().reshape(b * H, 1, 2 * dh, d).contiguous()
+        self.M1 = m1.to(torch.float32, copy=True).reshape(b * H, 1, d, dh).contiguous()
+        self.W02 = torch.cat([w0, w2], dim=2).to(torch.bfloat16).reshape(b * H, 1, 2 * dh, d).contiguous()
+        self.W1 = w1.to(torch.bfloat16, copy=True).reshape(b * H, 1, d, dh).contiguous()
+        if momentum is not None:
+            o0, o1, o2 = momentum
+            self.MOM02 = torch.cat([o0, o2], dim=2).float().reshape(b * H, 1, 2 * dh, d).contiguous()
+            self.MOM1 = o1.to(torch.float32, copy=True).reshape(b * H, 1, d, dh).contiguous()
+        else:
+            self.MOM02 = torch.zeros_like(self.M02) if self.use_momentum else None
+            self.MOM1 = torch.zeros_like(self.M1) if self.use_momentum else None
+        self._reads, self._packed = 0, False
 
     def read(self, q):
         """One layer's read of a chunk: q [b, l, H*d] -> [b, l, H*d] bf16."""
@@ -261,21 +281,63 @@ class SharedFastWeights:
         return _read_packed(q, self.P if self._packed else None, self.W02, self.W1, self.b,
                             self.H)
 
-    def write(self, ks, vs, lrs):
+    def _coeff(self, momentum_coeffs):
+        """The per-(batch, head) momentum coefficient: the mean of the layers'
+        [b, 1, 1, 1] coefficients (D:1140-1146), repeated over the heads."""
+        c = (momentum_coeffs if torch.is_tensor(momentum_coeffs)
+             else torch.stack(list(momentum_coeffs), dim=0).mean(dim=0))
+        c = c.reshape(-1).float()
+        assert c.numel() == self.b, "momentum coefficients must hold one value per batch"
+        return c.repeat_interleave(self.H).contiguous()
+
+    def _steps_moun(self, g02, g1, scale):
+        """bf16(NS5(slice) * scale) of every d x d slice (D:1192-1209): the
+        w0 / w2 rows are 2r row blocks of d per (batch, head), the w1 slices
+        r column blocks of d."""
+        from .fast_weight_write import newton_schulz5
+
+        B, d, r = self.b * self.H, self.d, self.r
+        s02 = newton_schulz5(g02.reshape(B * 2 * r, d, d), scale).reshape(B, 1, 2 * r * d, d)
+        sl1 = g1.reshape(B, d, r, d).permute(0, 2, 1, 3).reshape(B * r, d, d)
+        s1 = newton_schulz5(sl1, scale).reshape(B, r, d, d).permute(0, 2, 1, 3)
+        return s02, s1.reshape(B, 1, d, r * d).contiguous()
+
+    def write(self, ks, vs, lrs, momentum_coeffs=None):
         """The chunk's aggregate write from every layer's preprocessed k, v
-        [b, l, H*d] and lr ([b, l, 3] or [b, l, H*3])."""
+        [b, l, H*d] and lr ([b, l, 3] or [b, l, H*3]); momentum_coeffs: the
+        layers' [b, 1, 1, 1] momentum coefficients (a list, averaged) or one
+        tensor, used when the bank has momentum."""
         dW02, dW1 = _update(self.W02, self.W1, ks, vs, lrs, self.b, self.H, self._upacked)
-        scale = self.lr_scale / (len(ks) if self.reduce == "mean" else 1)
+        per_layer = 1.0 / (len(ks) if self.reduce == "mean" else 1)
         st = L.stream_of(dW02)
         nf = 0 if self.master_renorm else 1
         B, d, dh = self.b * self.H, self.d, self.dh
+        use_mom = self.use_momentum and momentum_coeffs is not None
+        g02, g1, gdt, scale = dW02, dW1, L.BF16, self.lr_scale * per_layer
+        mom02 = mom1 = cb = None
+        if use_mom or self.use_moun:
+            # the aggregate itself (the mean of the layers' updates) in fp32
+            g02 = dW02.float().mul_(per_layer)
+            g1 = dW1.float().mul_(per_layer)
+            gdt, scale = L.F32, self.lr_scale
+        if use_mom:
+            cb = self._coeff(momentum_coeffs)
+            mom02, mom1 = self.MOM02, self.MOM1
+        if self.use_moun:
+            if use_mom:
+                from .fast_weight_write import _momentum
+                g02 = self.MOM02 = _momentum(g02, self.MOM02, cb)
+                g1 = self.MOM1 = _momentum(g1, self.MOM1, cb)
+                mom02 = mom1 = cb = None
+            g02, g1 = self._steps_moun(g02, g1, self.lr_scale)
+            gdt, scale = L.BF16, 1.0
         # W0_W2 rows are whole d x d slice rows; W1 rows hold r slices of d
-        L.call("uttt_write_step", L.ptr(self.M02), L.ptr(self.W02), L.ptr(dW02), L.BF16, None,
-               None, scale, B, 2 * dh, d, d, nf, int(self.master_renorm), L.ptr(self.M02),
-               L.ptr(self._spare02), None, st)
-        L.call("uttt_write_step", L.ptr(self.M1), L.ptr(self.W1), L.ptr(dW1), L.BF16, None, None,
-               scale, B, d, dh, d, nf, int(self.master_renorm), L.ptr(self.M1),
-               L.ptr(self._spare1), None, st)
+        L.call("uttt_write_step", L.ptr(self.M02), L.ptr(self.W02), L.ptr(g02), gdt,
+               L.ptr(mom02), L.ptr(cb), scale, B, 2 * dh, d, d, nf, int(self.master_renorm),
+               L.ptr(self.M02), L.ptr(self._spare02), L.ptr(mom02), st)
+        L.call("uttt_write_step", L.ptr(self.M1), L.ptr(self.W1), L.ptr(g1), gdt,
+               L.ptr(mom1), L.ptr(cb), scale, B, d, dh, d, nf, int(self.master_renorm),
+               L.ptr(self.M1), L.ptr(self._spare1), L.ptr(mom1), st)
         self.W02, self._spare02 = self._spare02, self.W02
         self.W1, self._spare1 = self._spare1, self.W1
         self._reads, self._packed = 0, False
@@ -284,11 +346,21 @@ class SharedFastWeights:
             self._packed = True
 
     def weights(self):
-        """((w0, w1, w2) bf16, (w0, w1, w2) fp32 masters) in the reference layout."""
+        """Copies of ((w0, w1, w2) bf16, (w0, w1, w2) fp32 masters) in the
+        reference layout (the bank keeps its own storage)."""
         b, H, dh, d = self.b, self.H, self.dh, self.d
 
         def split(W02, W1):
             w02 = W02.reshape(b, H, 2 * dh, d)
-            return w02[:, :, :dh].contiguous(), W1.reshape(b, H, d, dh), w02[:, :, dh:].contiguous()
+            return (w02[:, :, :dh].clone(), W1.reshape(b, H, d, dh).clone(),
+                    w02[:, :, dh:].clone())
 
         return split(self.W02, self.W1), split(self.M02, self.M1)
+
+    def momentum(self):
+        """Copies of the (w0, w1, w2) momentum buffers, or None."""
+        if self.MOM02 is None:
+            return None
+        b, H, dh, d = self.b, self.H, self.dh, self.d
+        m = self.MOM02.reshape(b, H, 2 * dh, d)
+        return m[:, :, :dh].clone(), self.MOM1.reshape(b, H, d, dh).clone(), m[:, :, dh:].clone()
