@@ -179,6 +179,12 @@ def bench_permute(args):
     reps = max(3 * args.steps, 30)
     t_map = timed(rowmap, reps)
     t_p = timed(permute, reps)
+
+    def rowmap_permute(s):   # what permute_with_expert_mask runs (L/triton_permute.py:1184-1187)
+        rowmap(s)
+        permute(s)
+
+    t_mp = timed(rowmap_permute, reps)
     t_u = timed(unpermute, reps)
     # practical streaming ceiling on the same buffers: a plain device copy
     t_copy = timed(lambda s: s["y"].copy_(s["x"]), reps)
@@ -216,9 +222,13 @@ def bench_permute(args):
             traffic=_profile_traffic("permute_unpermute_c2.txt", "permute_chunk_kernel"),
             algorithmic_bytes=perm_bytes, avg_launch_us=round(t_p * 1e6, 3),
         ),
+        permute_end_to_end=dict(
+            us=round(t_mp * 1e6, 3), GBs=round((perm_bytes + map_bytes) / t_mp / 1e9, 1),
+            hbm_frac=round((perm_bytes + map_bytes) / t_mp / 1e9 / HBM_PEAK_GBS, 4),
+            what="permute_with_expert_mask as one call: the row map from the mask, then the "
+                 "permute (algorithmic bytes of both)"),
         kernels={
-            "row_id_map(3 launches)": dict(us=round(t_map * 1e6, 3),
-                                           GBs=round(map_bytes / t_map / 1e9, 1)),
+            "row_id_map": dict(us=round(t_map * 1e6, 3), GBs=round(map_bytes / t_map / 1e9, 1)),
             "permute_chunk_kernel": dict(us=round(t_p * 1e6, 3), GBs=round(perm_bytes / t_p / 1e9, 1),
                                        hbm_frac=round(perm_bytes / t_p / 1e9 / HBM_PEAK_GBS, 4)),
             "device_copy(x -> y)": dict(us=round(t_copy * 1e6, 3),
@@ -305,6 +315,11 @@ MOE_CONFIGS = {
     # uTTT-MoE 760M training slice: apply fwd + update fwd + update bwd
     "moe760m": dict(E=32, D=1536, I=3072, L=24, zipf=1.1, train=True,
                     label="uTTT-MoE 760M apply+update fwd+bwd training slice (configs[4])"),
+    # configs[4] with the shipped configs' write: momentum and Muon (use_momentum,
+    # use_moun of uttt_llm/configs/main/760M/uttt_moe.json)
+    "moe760m_shipped": dict(E=32, D=1536, I=3072, L=24, zipf=1.1, train=True, shipped=True,
+                            label="uTTT-MoE 760M training slice (configs[4]) with the shipped "
+                                  "write: momentum + Muon (Newton-Schulz per expert matrix)"),
 }
 SEQ, CHUNK, TOPK = 32768, 2048, 2
 
@@ -390,6 +405,13 @@ class MoeSweep:
         if cfg["train"]:
             self.GW02 = randn(1, E, 2 * I, D, scale=0.02)
             self.GW1 = randn(1, E, D, I, scale=0.02)
+        self.shipped = bool(cfg.get("shipped"))
+        if self.shipped:
+            # momentum buffers of the pool and per-write coefficients
+            # (momentum_proj's sigmoid, averaged over the chunk's tokens)
+            self.MOM02, self.MOM1 = torch.zeros_like(self.M02), torch.zeros_like(self.M1)
+            self.mcoeffs = torch.sigmoid(torch.randn(SEQ // CHUNK, 1, generator=g, device=dev))
+            self.n_writes = 0
         self.marks = None   # [(name, event)] when the stages are bracketed
 
     def _mark(self, name):
@@ -441,8 +463,16 @@ class MoeSweep:
         from uttt_amd import fast_weight_write as FWW
 
         self._mark("write")
-        FWW.apply_moe_update_packed(dW02, dW1, self.M02, self.M1, lr_scale=1.0,
-                                    out=((self.W02, self.W1), (self.M02, self.M1)))
+        if not self.shipped:
+            FWW.apply_moe_update_packed(dW02, dW1, self.M02, self.M1, lr_scale=1.0,
+                                        out=((self.W02, self.W1), (self.M02, self.M1)))
+            return
+        c = self.mcoeffs[self.n_writes % self.mcoeffs.shape[0]]
+        self.n_writes += 1
+        _, _, (self.MOM02, self.MOM1) = FWW.apply_moe_update_packed(
+            dW02, dW1, self.M02, self.M1, momentum_buf=(self.MOM02, self.MOM1), m_coeff=c,
+            lr_scale=1.0, use_momentum=True, use_moun=True,
+            out=((self.W02, self.W1), (self.M02, self.M1)))
 
     def update_batched(self, layers, first_set):
         sets = [self.sets[(first_set + l) % self.NSETS] for l in range(layers)]
@@ -906,6 +936,16 @@ DENSE_CONFIGS = {
     # configs[0]'s single-layer shape, run on the GPU
     "dense_c0": dict(L=1, H=4, d=96, r=2, S=4096, chunk=512,
                      label="uTTT-Dense single layer, configs[0] shape, on the GPU"),
+    # configs[1] as BASELINE words it: applied and updated sequentially per layer
+    # per chunk (each layer writes right after its read; the reference's
+    # uttt_dense supports only the aggregate schedule)
+    "dense124m_chained": dict(L=12, H=4, d=192, r=2, S=32768, chunk=2048, schedule="chained",
+                              label="uTTT-Dense 124M, chained schedule (configs[1] as worded)"),
+    # configs[1] with the shipped write (uttt_llm/configs/main/124M/uttt_dense_r2.json:
+    # use_momentum, use_moun): momentum + Newton-Schulz per d x d slice
+    "dense124m_shipped": dict(L=12, H=4, d=192, r=2, S=32768, chunk=2048, shipped=True,
+                              label="uTTT-Dense 124M (configs[1]) with the shipped write: "
+                                    "momentum + Muon"),
 }
 
 
@@ -935,23 +975,41 @@ def bench_dense(args, key):
         lr = torch.sigmoid(torch.randn(1, S, 3, generator=g, device=dev)) * 0.1
         sets.append(qkv + [lr])
 
+    schedule = cfg.get("schedule", "aggregate")
+    shipped = bool(cfg.get("shipped"))
+    chunks = (S + c - 1) // c
+    # per (chunk, layer) momentum coefficients (momentum_proj's sigmoid averaged
+    # over the chunk's tokens), [b, 1, 1, 1]
+    mcoef = torch.sigmoid(torch.randn(chunks, L_, 1, 1, 1, 1, generator=g, device=dev))
+
+    def new_bank():
+        return DN.SharedFastWeights(*w, r=r, use_momentum=shipped, use_moun=shipped)
+
     def sweep(bank, chunks):
         for ci in range(chunks):
             c0, c1 = ci * c, min(S, (ci + 1) * c)
+            if schedule == "chained":   # each layer reads, then writes its own update
+                for li in range(L_):
+                    x = sets[li % nsets]
+                    bank.read(x[0][:, c0:c1])
+                    if ci < chunks - 1:
+                        bank.write([x[1][:, c0:c1]], [x[2][:, c0:c1]], [x[3][:, c0:c1]],
+                                   momentum_coeffs=[mcoef[ci, li]] if shipped else None)
+                continue
             for li in range(L_):
                 bank.read(sets[li % nsets][0][:, c0:c1])
             if ci < chunks - 1:
                 st = [sets[li % nsets] for li in range(L_)]
                 bank.write([x[1][:, c0:c1] for x in st], [x[2][:, c0:c1] for x in st],
-                           [x[3][:, c0:c1] for x in st])
+                           [x[3][:, c0:c1] for x in st],
+                           momentum_coeffs=list(mcoef[ci]) if shipped else None)
 
-    chunks = (S + c - 1) // c
     for _ in range(max(args.warmup, 1)):
-        sweep(DN.SharedFastWeights(*w, r=r), min(chunks, 2))
+        sweep(new_bank(), min(chunks, 2))
     torch.cuda.synchronize()
     walls = []
     for _ in range(args.steps):
-        bank = DN.SharedFastWeights(*w, r=r)
+        bank = new_bank()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         sweep(bank, chunks)
@@ -959,7 +1017,7 @@ def bench_dense(args, key):
         walls.append(time.perf_counter() - t0)
     wall = statistics.mean(walls)
     # isolated timings (events around back-to-back calls on the stream)
-    bank = DN.SharedFastWeights(*w, r=r)
+    bank = new_bank()
 
     def timed(fn, reps=10):
         fn()
@@ -975,7 +1033,8 @@ def bench_dense(args, key):
     t_read = timed(lambda: bank.read(q0))
     st = [sets[li % nsets] for li in range(L_)]
     t_write = timed(lambda: bank.write([x[1][:, :c] for x in st], [x[2][:, :c] for x in st],
-                                       [x[3][:, :c] for x in st]))
+                                       [x[3][:, :c] for x in st],
+                                       momentum_coeffs=list(mcoef[0]) if shipped else None))
     nid = c * dh * d * H                                  # one layer-chunk, all heads
     sweep_flops = L_ * (chunks * 6 + (chunks - 1) * 12) * nid
     read_tf = 6 * nid / t_read / 1e12
@@ -988,9 +1047,14 @@ def bench_dense(args, key):
         dtype="bf16",
         config={"workload": cfg["label"], "seq_len": S, "chunk": c, "layers": L_, "fw_heads": H,
                 "head_dim": d, "fw_hidden": dh, "r": r,
-                "schedule": "aggregate (the reference's uttt_dense): all layers read the "
-                            "chunk-start snapshot; one mean-reduced write per chunk",
-                "write": "per-slice norm-preserving, norms from the bf16 fast weights"},
+                "schedule": ("aggregate (the reference's uttt_dense): all layers read the "
+                             "chunk-start snapshot; one mean-reduced write per chunk"
+                             if schedule == "aggregate" else
+                             "chained: each layer reads the current weights, then writes its "
+                             "own update (one write per layer per chunk)"),
+                "write": "per-slice norm-preserving, norms from the bf16 fast weights"
+                         + ("; momentum + Muon (Newton-Schulz per d x d slice)" if shipped
+                            else "")},
         roofline=dict(bound="mfma", kernel="aggregate write (UPDATE over all layers + write)",
                       achieved=round(write_tf, 2), peak=BF16_PEAK_TFLOPS, unit="TFLOP/s",
                       frac=round(write_tf / BF16_PEAK_TFLOPS, 4), traffic=None,
@@ -1296,26 +1360,37 @@ def cpu_baseline_muon(I, D):
 
 
 def other_targets(args):
-    """The other BASELINE targets measured in the same run (no CPU legs):
-    configs[2] permute / unpermute GB/s against HBM peak, the configs[3]
-    uTTT-MoE 124M sweep, and the uTTT-Dense sweeps of configs[1] (124M) and
-    configs[0]'s shape."""
+    """The other BASELINE targets measured in the same run: configs[2]
+    permute / unpermute GB/s against HBM peak (and the C port of the step on
+    one host core), the configs[3] uTTT-MoE 124M sweep, configs[4] with the
+    shipped write (momentum + Muon), the uTTT-Dense sweeps of configs[1]
+    (124M; aggregate, chained and with the shipped write) and configs[0]'s
+    shape on the GPU, and configs[0] itself, the CPU fp32 reference sweep."""
     import copy
 
+    cpu = not args.no_cpu_baseline
     a = copy.copy(args)
-    a.no_cpu_baseline = True
+    a.no_cpu_baseline = not cpu      # configs[2]'s C port (about 10 s of CPU work)
     a.steps, a.warmup = 20, 5
     p = bench_permute(a)
     k = p["kernels"]
+    a.no_cpu_baseline = True
     a.steps, a.warmup = 3, 1
     m = bench_moe(a, "moe124m", extras=False)
+    a.steps, a.warmup = 2, 1
+    ms = bench_moe(a, "moe760m_shipped", extras=False)
     a.steps, a.warmup = 3, 1
     d1 = bench_dense(a, "dense124m")
+    d1c = bench_dense(a, "dense124m_chained")
+    d1s = bench_dense(a, "dense124m_shipped")
+    a.no_cpu_baseline = not cpu      # configs[0]: the full single-layer sweep on the CPU
     d0 = bench_dense(a, "dense_c0")
     dense = lambda r: dict(workload=r["config"]["workload"], value=r["value"], unit=r["unit"],
-                           ms_per_step=r["ms_per_step"], kernels_us={
-                               n: v["us"] for n, v in r["kernels"].items()})
-    return {
+                           ms_per_step=r["ms_per_step"],
+                           sweep_mfma_frac=r["sweep"]["mfma_frac"], kernels_us={
+                               n: v["us"] for n, v in r["kernels"].items()},
+                           roofline=r["roofline"])
+    out = {
         "configs[2]_permute": dict(
             workload=p["config"]["workload"],
             permute_GBs=k["permute_chunk_kernel"]["GBs"],
@@ -1326,9 +1401,19 @@ def other_targets(args):
         "configs[3]_moe124m": dict(workload=m["config"]["workload"], value=m["value"],
                                    unit=m["unit"], ms_per_step=m["ms_per_step"],
                                    sweep_mfma_frac=m["sweep"]["mfma_frac"]),
+        "configs[4]_shipped_write": dict(workload=ms["config"]["workload"], value=ms["value"],
+                                         unit=ms["unit"], ms_per_step=ms["ms_per_step"]),
         "configs[1]_dense124m": dense(d1),
-        "configs[0]_dense": dense(d0),
+        "configs[1]_dense124m_chained": dense(d1c),
+        "configs[1]_dense124m_shipped_write": dense(d1s),
+        "configs[0]_dense_gpu": dense(d0),
     }
+    if "permute_end_to_end" in p:
+        out["configs[2]_permute"]["permute_with_expert_mask"] = p["permute_end_to_end"]
+    if cpu:
+        out["configs[2]_permute"]["cpu_port"] = p.get("cpu_baseline")
+        out["configs[0]_cpu_reference"] = d0.get("cpu_baseline")
+    return out
 
 
 WORKLOADS = {"permute": bench_permute,
@@ -1336,6 +1421,9 @@ WORKLOADS = {"permute": bench_permute,
              "moe760m": lambda a: bench_moe(a, "moe760m"),
              "dense124m": lambda a: bench_dense(a, "dense124m"),
              "dense_c0": lambda a: bench_dense(a, "dense_c0"),
+             "dense124m_chained": lambda a: bench_dense(a, "dense124m_chained"),
+             "dense124m_shipped": lambda a: bench_dense(a, "dense124m_shipped"),
+             "moe760m_shipped": lambda a: bench_moe(a, "moe760m_shipped"),
              "muon760m": bench_muon,
              "decode760m": bench_decode}
 DEFAULT_WORKLOAD = "moe760m"

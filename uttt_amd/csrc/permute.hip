@@ -2,7 +2,9 @@
 //
 // Row map (reference: make_row_id_map, L/triton_permute.py:283-393).  The
 // destination of (token t, expert e) is row(e, t) = off_e + rank(e, t): the
-// permuted buffer is expert-major and token-ascending.  Three launches:
+// permuted buffer is expert-major and token-ascending.  For E <= 24 two
+// launches (count, then rowmap_scan_emit_kernel, which derives each tile's
+// offsets from the counts itself); else three:
 //   count : one workgroup per 256-token tile; each wave ballots the 0/1 mask
 //           of every expert and the per-tile counts go to a [B, E, tiles]
 //           table (expert-major, so the global order is a linear scan);
@@ -84,7 +86,9 @@ __device__ __forceinline__ void wave_counts(const uint32_t bits[kMaxExperts / 32
   }
 }
 
-template <int MB>
+// TM: the count table is tile-major, [B, tiles, E] (read by
+// rowmap_scan_emit_kernel), else expert-major, [B, E, tiles] (rowmap_scan_kernel).
+template <int MB, bool TM = false>
 __global__ __launch_bounds__(kTile) void rowmap_count_kernel(
     const void* map, int64_t s_b, int64_t s_e, int64_t s_t, int T, int E, int ntiles,
     int32_t* counts) {
@@ -100,7 +104,7 @@ __global__ __launch_bounds__(kTile) void rowmap_count_kernel(
     int c = 0;
 #pragma unroll
     for (int i = 0; i < kTile / kWave; ++i) c += wcnt[i][e];
-    counts[((int64_t)b * E + e) * ntiles + tile] = c;
+    counts[TM ? ((int64_t)b * ntiles + tile) * E + e : ((int64_t)b * E + e) * ntiles + tile] = c;
   }
 }
 
@@ -237,6 +241,106 @@ __global__ __launch_bounds__(kTile) void rowmap_emit_kernel(
     toff[e] = offsets[((int64_t)b * E + e) * ntiles + tile];
   __syncthreads();
   emit_tile<STAGE>(bits, T, E, tile, b, wcnt, wmask, toff, stage, row_id_map);
+}
+
+// Scan and emit in one launch (with the tile-major counts of
+// rowmap_count_kernel<MB, true> before it: two launches for the row map),
+// for E <= kScanEmitMaxE.  Every workgroup derives its own tile's offsets
+// from the count table: the table ([tiles, E] ints of the batch, 16 KiB at
+// configs[2]) is read through LDS in chunks of kTile tiles, transposed to
+// [E][kTile]; P = min(32, kTile / E) threads per expert sum runs of it into
+// the expert's total and its count in the tiles before this one, and wave 0
+// scans the totals over the experts.  Redundant over the workgroups, but it
+// replaces the one-workgroup scan launch and the workspace round trip of the
+// offsets.  The LDS chunk lives in the emit's staging buffer (used after it).
+// E <= 24: the staged emit's kTile * (2E + 1) words plus the static tables
+// (12.5 KiB with the reduction table) stay within 64 KiB.
+constexpr int kScanEmitMaxE = 24;
+
+// VEC (T % 4 == 0, 16-byte aligned row_id_map): the staged tile goes out in
+// 16-byte stores (a tile's nt * (2E + 1) words are then a multiple of 4 and
+// start 16-byte aligned).
+template <int MB, bool VEC>
+__global__ __launch_bounds__(kTile) void rowmap_scan_emit_kernel(
+    const void* map, int64_t s_b, int64_t s_e, int64_t s_t, int T, int E, int ntiles,
+    const int32_t* counts, int32_t* group_sizes, int32_t* row_id_map) {
+  extern __shared__ int32_t stage[];  // kTile * (2E + 1) words; first the count chunks
+  __shared__ int wcnt[kTile / kWave][kMaxExperts];
+  __shared__ uint64_t wmask[kTile / kWave][kMaxExperts];
+  __shared__ int toff[kMaxExperts];
+  __shared__ int red[2][kScanEmitMaxE][32];
+  const int tile = blockIdx.x, b = blockIdx.y;
+  const int t = tile * kTile + threadIdx.x;
+  const int64_t base = (int64_t)b * s_b + (int64_t)min(t, T - 1) * s_t;
+  // this tile's mask bits first: their loads are in flight during the scan
+  uint32_t bits[kMaxExperts / 32];
+  load_mask_bits<MB>(map, base, s_e, E, t < T, bits);
+  const int P = min(32, kTile / E);
+  const int er = threadIdx.x / P, part = threadIdx.x - er * P;
+  const int len = (kTile + P - 1) / P;
+  const int32_t* cb = counts + (int64_t)b * ntiles * E;
+  int tot = 0, bef = 0;
+  for (int i0 = 0; i0 < ntiles; i0 += kTile) {
+    const int i = i0 + threadIdx.x;
+    // all of the tile's counts in flight together: clamped (always valid)
+    // addresses, masked values (a runtime-length loop of load -> LDS store
+    // would wait for each load in turn)
+    const int32_t* row = cb + (int64_t)min(i, ntiles - 1) * E;
+    int cv[kScanEmitMaxE];
+#pragma unroll
+    for (int e = 0; e < kScanEmitMaxE; ++e) cv[e] = row[min(e, E - 1)];
+    __syncthreads();  // the previous chunk is consumed
+#pragma unroll
+    for (int e = 0; e < kScanEmitMaxE; ++e)
+      if (e < E) stage[e * kTile + threadIdx.x] = i < ntiles ? cv[e] : 0;
+    __syncthreads();
+    if (er < E) {
+      const int j1 = min(kTile, (part + 1) * len);
+      for (int j = part * len; j < j1; ++j) {
+        const int c = stage[er * kTile + j];
+        tot += c;
+        bef += i0 + j < tile ? c : 0;
+      }
+    }
+  }
+  if (er < E) {
+    red[0][er][part] = tot;
+    red[1][er][part] = bef;
+  }
+  wave_counts(bits, E, wcnt, wmask);
+  __syncthreads();
+  if (threadIdx.x < kWave) {  // wave 0: lane e holds expert e (E <= 24)
+    const int e = threadIdx.x;
+    int te = 0, be = 0;
+    if (e < E)
+      for (int q = 0; q < P; ++q) {
+        te += red[0][e][q];
+        be += red[1][e][q];
+      }
+    int incl = te;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const int o = __shfl_up(incl, d, kWave);
+      if (e >= d) incl += o;
+    }
+    if (e < E) {
+      toff[e] = incl - te + be;
+      if (group_sizes != nullptr && tile == 0) group_sizes[(int64_t)b * E + e] = te;
+    }
+  }
+  __syncthreads();
+  if constexpr (!VEC) {
+    emit_tile<true>(bits, T, E, tile, b, wcnt, wmask, toff, stage, row_id_map);
+  } else {
+    emit_tile<true, false>(bits, T, E, tile, b, wcnt, wmask, toff, stage, nullptr);
+    __syncthreads();
+    const int nt = min(kTile, T - tile * kTile);
+    const int nw4 = nt * (2 * E + 1) / 4;
+    uint4* g = reinterpret_cast<uint4*>(row_id_map + ((int64_t)b * T + (int64_t)tile * kTile) *
+                                                         (2 * E + 1));
+    const uint4* sv = reinterpret_cast<const uint4*>(stage);
+    for (int i = threadIdx.x; i < nw4; i += kTile) g[i] = sv[i];
+  }
 }
 
 // One-launch row map for short batches of a contiguous bool mask (s_t = 1,
@@ -913,6 +1017,20 @@ extern "C" int uttt_make_row_id_map(const void* routing_map, int mask_bytes, int
   int32_t* counts = reinterpret_cast<int32_t*>(workspace);
   auto launch = [&](auto mb) {
     constexpr int MB = decltype(mb)::value;
+    if (E <= kScanEmitMaxE) {  // count, then scan + emit (two launches)
+      hipLaunchKernelGGL((rowmap_count_kernel<MB, true>), dim3(ntiles, B), dim3(kTile), 0, st,
+                         routing_map, s_b, s_e, s_t, T, E, ntiles, counts);
+      const bool vec = T % 4 == 0 && (reinterpret_cast<uintptr_t>(row_id_map) & 15u) == 0;
+      if (vec)
+        hipLaunchKernelGGL((rowmap_scan_emit_kernel<MB, true>), dim3(ntiles, B), dim3(kTile),
+                           sizeof(int32_t) * kTile * (2 * E + 1), st, routing_map, s_b, s_e, s_t,
+                           T, E, ntiles, counts, group_sizes, row_id_map);
+      else
+        hipLaunchKernelGGL((rowmap_scan_emit_kernel<MB, false>), dim3(ntiles, B), dim3(kTile),
+                           sizeof(int32_t) * kTile * (2 * E + 1), st, routing_map, s_b, s_e, s_t,
+                           T, E, ntiles, counts, group_sizes, row_id_map);
+      return;
+    }
     hipLaunchKernelGGL(rowmap_count_kernel<MB>, dim3(ntiles, B), dim3(kTile), 0, st, routing_map,
                        s_b, s_e, s_t, T, E, ntiles, counts);
     hipLaunchKernelGGL(rowmap_scan_kernel, dim3(B), dim3(kScanThreads), 0, st, counts, E, ntiles,
