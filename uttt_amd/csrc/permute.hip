@@ -45,18 +45,19 @@ __device__ __forceinline__ bool mask_bit(const void* map, int64_t idx) {
 // loads of a 32-expert group are in flight before the first is used and a
 // tile pays one memory latency per group.  (Loads under a per-lane condition
 // would each be followed by a wait before the merge of the two paths.)
-template <int MB>
+// NMAX: a compile-time bound on E (only that many loads are issued).
+template <int MB, int NMAX = kMaxExperts>
 __device__ __forceinline__ void load_mask_bits(const void* map, int64_t base, int64_t s_e, int E,
                                                bool valid, uint32_t bits[kMaxExperts / 32]) {
 #pragma unroll
   for (int g = 0; g < kMaxExperts / 32; ++g) {
     bits[g] = 0u;
-    if (32 * g < E) {  // wave-uniform
+    if (32 * g < NMAX && 32 * g < E) {  // wave-uniform
       bool bv[32];
 #pragma unroll
       for (int i = 0; i < 32; ++i) {
         const int e = min(32 * g + i, E - 1);
-        bv[i] = mask_bit<MB>(map, base + (int64_t)e * s_e);
+        bv[i] = 32 * g + i < NMAX && mask_bit<MB>(map, base + (int64_t)e * s_e);
       }
 #pragma unroll
       for (int i = 0; i < 32; ++i)
@@ -72,39 +73,75 @@ __device__ __forceinline__ bool bit_of(const uint32_t bits[kMaxExperts / 32], in
 
 // ------------------------------------------------------------ row map ------
 // Per-wave expert counts of a tile (one ballot per expert), and the ballots
-// themselves when `wmask` is given.
+// themselves when `wmask` is given.  Lane i of pass h keeps the ballot of
+// expert 64 h + i (a select, no branch per expert; the unrolled experts of a
+// 32-bit word are independent, so their compares overlap), and the wave
+// stores 64 experts at once.  NMAX < kMaxExperts: a compile-time bound on E;
+// the ballots of all NMAX experts are taken (those past E are empty), which
+// leaves no branch in the loop.
+template <int NMAX = kMaxExperts>
 __device__ __forceinline__ void wave_counts(const uint32_t bits[kMaxExperts / 32], int E,
                                             int (*wcnt)[kMaxExperts],
                                             uint64_t (*wmask)[kMaxExperts] = nullptr) {
-  const int w = threadIdx.x / kWave;
-  for (int e = 0; e < E; ++e) {
-    const uint64_t bal = __ballot(bit_of(bits, e));
-    if (lane_id() == 0) {
-      wcnt[w][e] = __popcll(bal);
-      if (wmask != nullptr) wmask[w][e] = bal;
+  const int w = threadIdx.x / kWave, lane = lane_id();
+#pragma unroll
+  for (int h = 0; h < kMaxExperts / 64; ++h) {
+    if (64 * h >= NMAX || 64 * h >= E) break;  // wave-uniform
+    uint64_t mine = 0;
+#pragma unroll
+    for (int g2 = 0; g2 < 2; ++g2) {
+      const int g = 2 * h + g2;
+      const int ng = min(32, E - 32 * g);
+      const uint32_t word = bits[g];
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        if (32 * g + i < NMAX && (NMAX < kMaxExperts || i < ng)) {
+          const uint64_t bal = __ballot((word >> i) & 1u);
+          mine = lane == 32 * g2 + i ? bal : mine;
+        }
+      }
+    }
+    const int e = 64 * h + lane;
+    if (e < E) {
+      wcnt[w][e] = __popcll(mine);
+      if (wmask != nullptr) wmask[w][e] = mine;
     }
   }
 }
 
-// TM: the count table is tile-major, [B, tiles, E] (read by
-// rowmap_scan_emit_kernel), else expert-major, [B, E, tiles] (rowmap_scan_kernel).
-template <int MB, bool TM = false>
+// Experts per tile row of the tile-major count table: E rounded up to a power
+// of two, at least 4 (so kTile % Ep == 0); the padding counts zero.
+__host__ __device__ __forceinline__ int padded_experts(int E) {
+  int p = 4;
+  while (p < E) p <<= 1;
+  return p;
+}
+
+// EP > 0: the count table is tile-major, [B, tiles, EP] with EP =
+// padded_experts(E) (read by rowmap_scan_emit_kernel<MB, EP>), else
+// expert-major, [B, E, tiles] (rowmap_scan_kernel).
+template <int MB, int EP = 0>
 __global__ __launch_bounds__(kTile) void rowmap_count_kernel(
     const void* map, int64_t s_b, int64_t s_e, int64_t s_t, int T, int E, int ntiles,
     int32_t* counts) {
+  constexpr bool TM = EP > 0;
+  constexpr int NMAX = TM ? EP : kMaxExperts;
   __shared__ int wcnt[kTile / kWave][kMaxExperts];
   const int tile = blockIdx.x, b = blockIdx.y;
   const int t = tile * kTile + threadIdx.x;
   const int64_t base = (int64_t)b * s_b + (int64_t)min(t, T - 1) * s_t;
   uint32_t bits[kMaxExperts / 32];
-  load_mask_bits<MB>(map, base, s_e, E, t < T, bits);
-  wave_counts(bits, E, wcnt);
+  load_mask_bits<MB, NMAX>(map, base, s_e, E, t < T, bits);
+  wave_counts<NMAX>(bits, E, wcnt);
   __syncthreads();
-  for (int e = threadIdx.x; e < E; e += kTile) {
+  const int Ep = TM ? EP : E;
+  for (int e = threadIdx.x; e < Ep; e += kTile) {
     int c = 0;
+    if (e < E) {
 #pragma unroll
-    for (int i = 0; i < kTile / kWave; ++i) c += wcnt[i][e];
-    counts[TM ? ((int64_t)b * ntiles + tile) * E + e : ((int64_t)b * E + e) * ntiles + tile] = c;
+      for (int i = 0; i < kTile / kWave; ++i) c += wcnt[i][e];
+    }
+    counts[TM ? ((int64_t)b * ntiles + tile) * Ep + e : ((int64_t)b * E + e) * ntiles + tile] = c;
   }
 }
 
@@ -182,8 +219,10 @@ constexpr int kStageMaxW = 57;  // STAGE: kTile * (2E+1) * 4 bytes plus the 6.5 
 // own experts, so the cost per token is its n_routed, not E.  STAGE assembles
 // the tile in LDS (`stage`, kTile * (2E+1) words) and writes it with
 // consecutive lanes on consecutive words; without it each lane stores its own
-// entry, which strides the lanes 4 * (2E+1) bytes apart.
-template <bool STAGE, bool COPY_OUT = STAGE>
+// entry, which strides the lanes 4 * (2E+1) bytes apart.  WOFF: toff holds
+// each wave's first row per expert ([kTile / kWave][kMaxExperts], flattened:
+// the tile's offset plus the earlier waves' counts) instead of the tile's.
+template <bool STAGE, bool COPY_OUT = STAGE, bool WOFF = false>
 __device__ __forceinline__ void emit_tile(const uint32_t bits[kMaxExperts / 32], int T, int E,
                                           int tile, int b, const int (*wcnt)[kMaxExperts],
                                           const uint64_t (*wmask)[kMaxExperts], const int* toff,
@@ -206,8 +245,13 @@ __device__ __forceinline__ void emit_tile(const uint32_t bits[kMaxExperts / 32],
         const int hb = 31 - __clz(m);
         m &= ~(1u << hb);
         const int e = 32 * g + hb;
-        int r = toff[e] + __popcll(wmask[w][e] & below);
-        for (int i = 0; i < w; ++i) r += wcnt[i][e];
+        int r;
+        if constexpr (WOFF) {
+          r = toff[w * kMaxExperts + e] + __popcll(wmask[w][e] & below);
+        } else {
+          r = toff[e] + __popcll(wmask[w][e] & below);
+          for (int i = 0; i < w; ++i) r += wcnt[i][e];
+        }
         row[j] = r;
         row[E + j] = e;
         ++j;
@@ -243,80 +287,89 @@ __global__ __launch_bounds__(kTile) void rowmap_emit_kernel(
   emit_tile<STAGE>(bits, T, E, tile, b, wcnt, wmask, toff, stage, row_id_map);
 }
 
-// Scan and emit in one launch (with the tile-major counts of
-// rowmap_count_kernel<MB, true> before it: two launches for the row map),
-// for E <= kScanEmitMaxE.  Every workgroup derives its own tile's offsets
-// from the count table: the table ([tiles, E] ints of the batch, 16 KiB at
-// configs[2]) is read through LDS in chunks of kTile tiles, transposed to
-// [E][kTile]; P = min(32, kTile / E) threads per expert sum runs of it into
-// the expert's total and its count in the tiles before this one, and wave 0
-// scans the totals over the experts.  Redundant over the workgroups, but it
-// replaces the one-workgroup scan launch and the workspace round trip of the
-// offsets.  The LDS chunk lives in the emit's staging buffer (used after it).
-// E <= 24: the staged emit's kTile * (2E + 1) words plus the static tables
-// (12.5 KiB with the reduction table) stay within 64 KiB.
+// Scan and emit in one launch (after rowmap_count_kernel<MB, EP>: two
+// launches for the row map), for E <= kScanEmitMaxE.  Every workgroup derives
+// its own tile's offsets from the count table ([tiles, EP] ints of the batch,
+// 16 KiB at T = 65536, E = 16).  EP is a power of two dividing kTile, so in a
+// chunk of kTile tiles lane l reads the EP words q * kTile + l, all of expert
+// l % EP, and sums them (and those of the tiles before this one) in
+// registers; lane shuffles and a per-wave table reduce the sums per expert,
+// and wave 0 scans the totals over the experts and leaves each wave's first
+// row per expert for the emit.  The loads of the first chunk are issued
+// together with the tile's mask loads (one memory latency).  Redundant over
+// the workgroups, but it replaces the one-workgroup scan launch and the
+// workspace round trip of the offsets.  E <= 24: the staged emit's
+// kTile * (2E + 1) words plus the static tables stay within 64 KiB.
 constexpr int kScanEmitMaxE = 24;
+
+// One chunk of a batch's tile-major count table from word w0 on, consecutive
+// lanes on consecutive words (cv[q] = word w0 + q * kTile + lane, q < EP);
+// addresses are clamped into the table, so the loads are unconditional and
+// all in flight before the first is used.
+template <int EP>
+__device__ __forceinline__ void load_count_chunk(const int32_t* cb, int w0, int nwords,
+                                                 int cv[EP]) {
+#pragma unroll
+  for (int q = 0; q < EP; ++q) cv[q] = cb[min(w0 + q * kTile + (int)threadIdx.x, nwords - 1)];
+}
 
 // VEC (T % 4 == 0, 16-byte aligned row_id_map): the staged tile goes out in
 // 16-byte stores (a tile's nt * (2E + 1) words are then a multiple of 4 and
 // start 16-byte aligned).
-template <int MB, bool VEC>
+template <int MB, int EP, bool VEC>
 __global__ __launch_bounds__(kTile) void rowmap_scan_emit_kernel(
     const void* map, int64_t s_b, int64_t s_e, int64_t s_t, int T, int E, int ntiles,
     const int32_t* counts, int32_t* group_sizes, int32_t* row_id_map) {
-  extern __shared__ int32_t stage[];  // kTile * (2E + 1) words; first the count chunks
+  extern __shared__ int32_t stage[];  // kTile * (2E + 1) words
   __shared__ int wcnt[kTile / kWave][kMaxExperts];
   __shared__ uint64_t wmask[kTile / kWave][kMaxExperts];
-  __shared__ int toff[kMaxExperts];
-  __shared__ int red[2][kScanEmitMaxE][32];
+  __shared__ int woff[kTile / kWave][kMaxExperts];
+  __shared__ int red[2][kTile / kWave][EP];
   const int tile = blockIdx.x, b = blockIdx.y;
   const int t = tile * kTile + threadIdx.x;
+  const int w = threadIdx.x / kWave, lane = lane_id();
   const int64_t base = (int64_t)b * s_b + (int64_t)min(t, T - 1) * s_t;
-  // this tile's mask bits first: their loads are in flight during the scan
+  const int32_t* cb = counts + (int64_t)b * ntiles * EP;
+  const int nwords = ntiles * EP;
+  int cv[EP];
+  load_count_chunk<EP>(cb, 0, nwords, cv);
   uint32_t bits[kMaxExperts / 32];
-  load_mask_bits<MB>(map, base, s_e, E, t < T, bits);
-  const int P = min(32, kTile / E);
-  const int er = threadIdx.x / P, part = threadIdx.x - er * P;
-  const int len = (kTile + P - 1) / P;
-  const int32_t* cb = counts + (int64_t)b * ntiles * E;
+  load_mask_bits<MB, EP>(map, base, s_e, E, t < T, bits);
+  // word q of this lane: expert lane % EP of tile i0 + q * (kTile / EP) + jl
+  constexpr int tpq = kTile / EP;
+  const int jl = threadIdx.x / EP;
   int tot = 0, bef = 0;
   for (int i0 = 0; i0 < ntiles; i0 += kTile) {
-    const int i = i0 + threadIdx.x;
-    // all of the tile's counts in flight together: clamped (always valid)
-    // addresses, masked values (a runtime-length loop of load -> LDS store
-    // would wait for each load in turn)
-    const int32_t* row = cb + (int64_t)min(i, ntiles - 1) * E;
-    int cv[kScanEmitMaxE];
+    if (i0 > 0) load_count_chunk<EP>(cb, i0 * EP, nwords, cv);
 #pragma unroll
-    for (int e = 0; e < kScanEmitMaxE; ++e) cv[e] = row[min(e, E - 1)];
-    __syncthreads();  // the previous chunk is consumed
-#pragma unroll
-    for (int e = 0; e < kScanEmitMaxE; ++e)
-      if (e < E) stage[e * kTile + threadIdx.x] = i < ntiles ? cv[e] : 0;
-    __syncthreads();
-    if (er < E) {
-      const int j1 = min(kTile, (part + 1) * len);
-      for (int j = part * len; j < j1; ++j) {
-        const int c = stage[er * kTile + j];
-        tot += c;
-        bef += i0 + j < tile ? c : 0;
-      }
+    for (int q = 0; q < EP; ++q) {
+      const int j = i0 + q * tpq + jl;
+      const int c = j < ntiles ? cv[q] : 0;
+      tot += c;
+      bef += j < tile ? c : 0;
     }
   }
-  if (er < E) {
-    red[0][er][part] = tot;
-    red[1][er][part] = bef;
+#pragma unroll
+  for (int d = EP; d < kWave; d <<= 1) {  // lanes of one expert: equal lane % EP
+    tot += __shfl_xor(tot, d, kWave);
+    bef += __shfl_xor(bef, d, kWave);
   }
-  wave_counts(bits, E, wcnt, wmask);
+  if (lane < EP) {
+    red[0][w][lane] = tot;
+    red[1][w][lane] = bef;
+  }
+  wave_counts<EP>(bits, E, wcnt, wmask);
   __syncthreads();
-  if (threadIdx.x < kWave) {  // wave 0: lane e holds expert e (E <= 24)
+  if (threadIdx.x < kWave) {  // wave 0: lane e holds expert e (padding experts count 0)
     const int e = threadIdx.x;
     int te = 0, be = 0;
-    if (e < E)
-      for (int q = 0; q < P; ++q) {
-        te += red[0][e][q];
-        be += red[1][e][q];
+    if (e < EP) {
+#pragma unroll
+      for (int i = 0; i < kTile / kWave; ++i) {
+        te += red[0][i][e];
+        be += red[1][i][e];
       }
+    }
     int incl = te;
 #pragma unroll
     for (int d = 1; d < kWave; d <<= 1) {
@@ -324,15 +377,20 @@ __global__ __launch_bounds__(kTile) void rowmap_scan_emit_kernel(
       if (e >= d) incl += o;
     }
     if (e < E) {
-      toff[e] = incl - te + be;
+      int r = incl - te + be;
+#pragma unroll
+      for (int i = 0; i < kTile / kWave; ++i) {
+        woff[i][e] = r;
+        r += wcnt[i][e];
+      }
       if (group_sizes != nullptr && tile == 0) group_sizes[(int64_t)b * E + e] = te;
     }
   }
   __syncthreads();
   if constexpr (!VEC) {
-    emit_tile<true>(bits, T, E, tile, b, wcnt, wmask, toff, stage, row_id_map);
+    emit_tile<true, true, true>(bits, T, E, tile, b, wcnt, wmask, &woff[0][0], stage, row_id_map);
   } else {
-    emit_tile<true, false>(bits, T, E, tile, b, wcnt, wmask, toff, stage, nullptr);
+    emit_tile<true, false, true>(bits, T, E, tile, b, wcnt, wmask, &woff[0][0], stage, nullptr);
     __syncthreads();
     const int nt = min(kTile, T - tile * kTile);
     const int nw4 = nt * (2 * E + 1) / 4;
@@ -981,7 +1039,8 @@ using namespace uttt;
 extern "C" size_t uttt_row_id_map_workspace_bytes(int B, int T, int E) {
   if (B <= 0 || T <= 0 || E <= 0) return 0;
   const int ntiles = (T + kTile - 1) / kTile;
-  return (size_t)B * E * ntiles * sizeof(int32_t);
+  const int per_tile = E <= kScanEmitMaxE ? padded_experts(E) : E;  // count-table row
+  return (size_t)B * per_tile * ntiles * sizeof(int32_t);
 }
 
 extern "C" int uttt_make_row_id_map(const void* routing_map, int mask_bytes, int64_t s_b,
@@ -1018,17 +1077,27 @@ extern "C" int uttt_make_row_id_map(const void* routing_map, int mask_bytes, int
   auto launch = [&](auto mb) {
     constexpr int MB = decltype(mb)::value;
     if (E <= kScanEmitMaxE) {  // count, then scan + emit (two launches)
-      hipLaunchKernelGGL((rowmap_count_kernel<MB, true>), dim3(ntiles, B), dim3(kTile), 0, st,
-                         routing_map, s_b, s_e, s_t, T, E, ntiles, counts);
       const bool vec = T % 4 == 0 && (reinterpret_cast<uintptr_t>(row_id_map) & 15u) == 0;
-      if (vec)
-        hipLaunchKernelGGL((rowmap_scan_emit_kernel<MB, true>), dim3(ntiles, B), dim3(kTile),
-                           sizeof(int32_t) * kTile * (2 * E + 1), st, routing_map, s_b, s_e, s_t,
-                           T, E, ntiles, counts, group_sizes, row_id_map);
-      else
-        hipLaunchKernelGGL((rowmap_scan_emit_kernel<MB, false>), dim3(ntiles, B), dim3(kTile),
-                           sizeof(int32_t) * kTile * (2 * E + 1), st, routing_map, s_b, s_e, s_t,
-                           T, E, ntiles, counts, group_sizes, row_id_map);
+      const size_t lds = sizeof(int32_t) * kTile * (2 * E + 1);
+      auto two = [&](auto ep) {
+        constexpr int EP = decltype(ep)::value;
+        hipLaunchKernelGGL((rowmap_count_kernel<MB, EP>), dim3(ntiles, B), dim3(kTile), 0, st,
+                           routing_map, s_b, s_e, s_t, T, E, ntiles, counts);
+        if (vec)
+          hipLaunchKernelGGL((rowmap_scan_emit_kernel<MB, EP, true>), dim3(ntiles, B),
+                             dim3(kTile), lds, st, routing_map, s_b, s_e, s_t, T, E, ntiles,
+                             counts, group_sizes, row_id_map);
+        else
+          hipLaunchKernelGGL((rowmap_scan_emit_kernel<MB, EP, false>), dim3(ntiles, B),
+                             dim3(kTile), lds, st, routing_map, s_b, s_e, s_t, T, E, ntiles,
+                             counts, group_sizes, row_id_map);
+      };
+      switch (padded_experts(E)) {
+        case 4: two(std::integral_constant<int, 4>{}); break;
+        case 8: two(std::integral_constant<int, 8>{}); break;
+        case 16: two(std::integral_constant<int, 16>{}); break;
+        default: two(std::integral_constant<int, 32>{}); break;
+      }
       return;
     }
     hipLaunchKernelGGL(rowmap_count_kernel<MB>, dim3(ntiles, B), dim3(kTile), 0, st, routing_map,
