@@ -2240,15 +2240,21 @@ extern "C" int uttt_newton_schulz5(const void* g, int g_dtype, int BE, int rows,
   for (int it = 0; it < 5; ++it) {
     const float ca = kCoef[it][0], cb = kCoef[it][1], cc = kCoef[it][2];
     // A = X X^T and Ac = c A  ([m, m]: x = X as m rows of K = n, A operand = X).
-    // A and B are symmetric: only the 256-tiles on or below the diagonal are
-    // multiplied and those below it also store their transposes (EpiLinComb),
-    // which takes 15 of the 36 tiles of a 1536-wide matrix off the matrix cores
+    // A is symmetric bit for bit (element (i, j) and (j, i) take the same
+    // products in the same k order): only the 256-tiles on or below the
+    // diagonal are multiplied and those below it also store their transposes
+    // (EpiLinComb), which takes 15 of the 36 tiles of a 1536-wide matrix off
+    // the matrix cores
     if (int rc = launch_lincomb<KMajor>(X, X, n, m, n, elems, nullptr, 0.0f, 1.0f, A, Ac, cc, BE, m,
                                         gs, st, "newton_schulz5(X X^T)", true))
       return rc;
-    // B = b A + (c A) A  (x = Ac, A operand = A: A is symmetric, so row j of A is column j)
+    // B = b A + (c A) A  (x = Ac, A operand = A: A is symmetric, so row j of A
+    // is column j).  The full product: (c A) A is symmetric in exact
+    // arithmetic only, since element (i, j) sums bf16(c A[i, k]) A[k, j] and
+    // element (j, i) sums A[i, k] bf16(c A[k, j]), so mirroring one triangle
+    // would round half of B differently from the reference's product
     if (int rc = launch_lincomb<KMajor>(A, Ac, m, m, m, (int64_t)m * m, A, cb, 1.0f, Bm, nullptr,
-                                        0.0f, BE, m, gs, st, "newton_schulz5(B)", true))
+                                        0.0f, BE, m, gs, st, "newton_schulz5(B)", false))
       return rc;
     // X' = a X + B X  ([m, n]: x = B, A operand = X read row-major: A(j, k) = X[k, j])
     if (int rc = launch_lincomb<RMajor>(X, Bm, m, n, n, elems, X, ca, 1.0f, Xn, nullptr, 0.0f, BE,
