@@ -224,10 +224,10 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 
 // 8 consecutive features of one row as fp32 (zero past D or for a dead row).
-template <class XT>
-__device__ __forceinline__ void load8(const typename XT::S* p, int d, int D, bool ok, bool vec,
+template <class XT, bool VEC>
+__device__ __forceinline__ void load8(const typename XT::S* p, int d, int D, bool ok,
                                      float (&o)[8]) {
-  if (vec) {  // wave-uniform: D % 8 == 0 and 16-byte aligned rows
+  if constexpr (VEC) {  // D % 8 == 0 and 16-byte aligned rows
     // unconditional load (a lane that is off reads its row's first 8
     // features and zeroes them), so the loads of consecutive calls stay in
     // flight together; a load under a per-lane condition would be waited
@@ -274,6 +274,51 @@ __device__ __forceinline__ void load8(const typename XT::S* p, int d, int D, boo
   }
 }
 
+// The bytes of 8 consecutive features (16 B for 2-byte types, 32 B for fp32)
+// as loaded, converted only where they are used: a load ring of these keeps
+// its loads in flight (converting right after the load, as load8 does, waits
+// for each load in turn).  Rows of whole 16-byte vectors only (D % 8 == 0,
+// aligned); a lane that is off reads its row's first 8 features and `in`
+// zeroes them at the conversion.
+template <class XT>
+struct Raw8 {
+  static constexpr int kV = sizeof(typename XT::S) / 2;
+  uint4 u[kV];
+  bool in;
+};
+
+template <class XT>
+__device__ __forceinline__ void load_raw8(const typename XT::S* p, int d, int D, bool ok,
+                                          Raw8<XT>& r) {
+  r.in = ok && d + 8 <= D;
+  const uint4* q = reinterpret_cast<const uint4*>(p + (r.in ? d : 0));
+#pragma unroll
+  for (int i = 0; i < Raw8<XT>::kV; ++i) r.u[i] = q[i];
+}
+
+template <class XT>
+__device__ __forceinline__ void cvt8(const Raw8<XT>& r, float (&o)[8]) {
+  float v[8];
+  if constexpr (sizeof(typename XT::S) == 4) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      v[4 * i] = __uint_as_float(r.u[i].x);
+      v[4 * i + 1] = __uint_as_float(r.u[i].y);
+      v[4 * i + 2] = __uint_as_float(r.u[i].z);
+      v[4 * i + 3] = __uint_as_float(r.u[i].w);
+    }
+  } else {
+    const uint32_t w[4] = {r.u[0].x, r.u[0].y, r.u[0].z, r.u[0].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = XT::load(static_cast<typename XT::S>(w[i] & 0xffffu));
+      v[2 * i + 1] = XT::load(static_cast<typename XT::S>(w[i] >> 16));
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = r.in ? v[i] : 0.0f;
+}
+
 // Reductions over the 32 lanes of a half-wave (fixed xor butterflies).
 __device__ __forceinline__ float half_sum(float v) {
 #pragma unroll
@@ -304,10 +349,12 @@ __device__ __forceinline__ void half_argmax(float& v, int& i) {
 // expert index) and combine weights; the sums over experts are butterflies.
 // Writes the token's mask / balance / combine entries when live, and its row
 // of the block partials (zeros when not live).
+// bias_v[q]: the routing bias of expert j + 32 q (0 without a bias), loaded
+// by the caller ahead of time.
 template <int NET>
-__device__ __forceinline__ void select_lanes(const float (&lg)[NET], const SelectArgs& a, int b,
-                                             int t, bool live, int j, float* sb_row,
-                                             uint8_t* sc_row) {
+__device__ __forceinline__ void select_lanes(const float (&lg)[NET], const float (&bias_v)[NET],
+                                             const SelectArgs& a, int b, int t, bool live, int j,
+                                             float* sb_row, uint8_t* sc_row) {
   const int E = a.E;
   float v[NET];
   bool ok[NET];
@@ -352,12 +399,11 @@ __device__ __forceinline__ void select_lanes(const float (&lg)[NET], const Selec
 #pragma unroll
     for (int q = 0; q < NET; ++q) bal[q] = bal[q] / s;
   }
-  const float* bias = a.bias != nullptr ? a.bias + (int64_t)b * a.bias_sb : nullptr;
   float r[NET];
   bool sel[NET];
 #pragma unroll
   for (int q = 0; q < NET; ++q) {
-    r[q] = ok[q] ? (bias != nullptr ? v[q] + bias[j + 32 * q] : v[q]) : -INFINITY;
+    r[q] = ok[q] ? (a.bias != nullptr ? v[q] + bias_v[q] : v[q]) : -INFINITY;
     sel[q] = false;
   }
   for (int k = 0; k < a.topk; ++k) {
@@ -413,11 +459,12 @@ __device__ __forceinline__ void select_lanes(const float (&lg)[NET], const Selec
 // i / TPE and the 8-feature chunks i % TPE + TPE*m, and the TPE partial dot
 // products of an expert are summed with a butterfly.
 // Selection: 32 lanes per token (select_lanes), NW*2 tokens at a time.
+// VEC: rows of whole 16-byte vectors (D % 8 == 0, aligned x and weights).
 constexpr int kSmallT = 8;
-template <class XT, int NET, int NW, bool SMALL>
+template <class XT, int NET, int NW, bool SMALL, bool VEC>
 __global__ __launch_bounds__(NW * kWave) void router_mfma_kernel(
     const typename XT::S* __restrict__ x, const float* __restrict__ rw, int64_t w_sb, int D,
-    bool vec, float* __restrict__ logits_out, SelectArgs a) {
+    float* __restrict__ logits_out, SelectArgs a) {
   constexpr int EB = NET * 32;
   constexpr int NTH = NW * kWave;
   __shared__ float red[SMALL ? 1 : NW][NET][32][33];
@@ -428,6 +475,20 @@ __global__ __launch_bounds__(NW * kWave) void router_mfma_kernel(
   const int w = threadIdx.x / kWave, lane = lane_id();
   const int E = a.E, T = a.T;
   const float* R = rw + (int64_t)b * w_sb;
+  // the routing bias of this lane's experts for the selection, loaded now
+  // (unconditionally, from a valid address without a bias) so that its
+  // latency hides under the logits
+  float bias_v[NET];
+  {
+    const int jl = threadIdx.x % 32;
+    const float* bp = a.bias != nullptr ? a.bias + (int64_t)b * a.bias_sb : R;
+#pragma unroll
+    for (int q = 0; q < NET; ++q) {
+      const int e = jl + 32 * q;
+      const float v = bp[e < E ? e : 0];
+      bias_v[q] = a.bias != nullptr && e < E ? v : 0.0f;
+    }
+  }
   if constexpr (SMALL) {
     static_assert(NTH % EB == 0, "threads must split evenly over the experts");
     constexpr int TPE = NTH / EB;
@@ -446,10 +507,10 @@ __global__ __launch_bounds__(NW * kWave) void router_mfma_kernel(
 #pragma unroll 2
       for (int c = sl; c < nch; c += TPE) {
         float wv[8], xv[NT][8];
-        load8<F32T>(Re, c * 8, D, e < E, vec, wv);
+        load8<F32T, VEC>(Re, c * 8, D, e < E, wv);
 #pragma unroll
         for (int t = 0; t < NT; ++t)
-          load8<XT>(x + ((int64_t)b * T + t0 + t) * D, c * 8, D, true, vec, xv[t]);
+          load8<XT, VEC>(x + ((int64_t)b * T + t0 + t) * D, c * 8, D, true, xv[t]);
 #pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
@@ -485,60 +546,97 @@ __global__ __launch_bounds__(NW * kWave) void router_mfma_kernel(
     f32x16_t acc[NET];
 #pragma unroll
     for (int j = 0; j < NET; ++j) acc[j] = f32x16_t{};
-    auto fetch = [&](int c, float (&xo)[8], float (&wo)[NET][8]) __attribute__((always_inline)) {
-      const int d = c * 16 + 8 * h;
-      const bool in = c < c_hi;
-      load8<XT>(xrow, d, D, tv && in, vec, xo);
+    // one chunk's MFMAs: 16 features (8 per lane half) of the token and NET
+    // expert blocks
+    auto mma = [&](const float (&xo)[8], const float (&wo)[NET][8]) __attribute__((always_inline)) {
+      if constexpr (std::is_same_v<XT, BF16T>) {
+        // bf16 x: each fp32 weight is split exactly into three bf16 parts
+        // (hi + mid + lo = w for normal w: 3 x 8 mantissa bits), so the
+        // products x*hi, x*mid, x*lo are exact and the fp32 accumulation
+        // gives fp32 logits on the bf16 matrix cores (one 32x32x16 MFMA
+        // per part covers the lane pair's 16 features; the f32 path needs 8
+        // 32x32x2 MFMAs of twice the cycles)
+        bf16x8_t xb;
 #pragma unroll
-      for (int j = 0; j < NET; ++j) {
-        const int e = 32 * j + r;
-        load8<F32T>(R + (int64_t)(e < E ? e : 0) * D, d, D, in && e < E, vec, wo[j]);
+        for (int i = 0; i < 8; ++i) xb[i] = static_cast<__bf16>(xo[i]);  // exact
+#pragma unroll
+        for (int j = 0; j < NET; ++j) {
+          bf16x8_t hi, mid, lo;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const float w = wo[j][i];
+            hi[i] = static_cast<__bf16>(w);
+            const float r1 = w - static_cast<float>(hi[i]);
+            mid[i] = static_cast<__bf16>(r1);
+            lo[i] = static_cast<__bf16>(r1 - static_cast<float>(mid[i]));
+          }
+          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xb, hi, acc[j], 0, 0, 0);
+          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xb, mid, acc[j], 0, 0, 0);
+          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xb, lo, acc[j], 0, 0, 0);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < NET; ++j)
+#pragma unroll
+          for (int s8 = 0; s8 < 8; ++s8)
+            acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(xo[s8], wo[j][s8], acc[j], 0, 0, 0);
       }
     };
     // a ring of DEPTH chunks in flight: each chunk's slot is refilled with the
     // chunk DEPTH ahead right after its MFMAs issue; slots past the range
     // hold zeros, whose MFMAs add nothing
-    constexpr int DEPTH = NET <= 2 ? 4 : 2;
-    float xr[DEPTH][8], wr[DEPTH][NET][8];
+    if constexpr (VEC) {
+      // (a deeper ring, or refills pinned in place by scheduling barriers,
+      // measured slower: each load instruction touches 32 rows, and more of
+      // them in flight evict the L1 lines the next chunks reuse)
+      constexpr int DEPTH = NET <= 2 ? 4 : 2;
+      // the ring holds the loaded bytes; each slot is converted when used
+      auto fetch = [&](int c, Raw8<XT>& xo, Raw8<F32T> (&wo)[NET]) __attribute__((always_inline)) {
+        const int d = c * 16 + 8 * h;
+        const bool in = c < c_hi;
+        load_raw8<XT>(xrow, d, D, tv && in, xo);
 #pragma unroll
-    for (int q = 0; q < DEPTH; ++q) fetch(c_lo + q, xr[q], wr[q]);
-    for (int c = c_lo; c < c_hi; c += DEPTH) {
-#pragma unroll
-      for (int q = 0; q < DEPTH; ++q) {
-        if constexpr (std::is_same_v<XT, BF16T>) {
-          // bf16 x: each fp32 weight is split exactly into three bf16 parts
-          // (hi + mid + lo = w for normal w: 3 x 8 mantissa bits), so the
-          // products x*hi, x*mid, x*lo are exact and the fp32 accumulation
-          // gives fp32 logits on the bf16 matrix cores (one 32x32x16 MFMA
-          // per part covers the lane pair's 16 features; the f32 path needs 8
-          // 32x32x2 MFMAs of twice the cycles)
-          bf16x8_t xb;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) xb[i] = static_cast<__bf16>(xr[q][i]);  // exact
-#pragma unroll
-          for (int j = 0; j < NET; ++j) {
-            bf16x8_t hi, mid, lo;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-              const float w = wr[q][j][i];
-              hi[i] = static_cast<__bf16>(w);
-              const float r1 = w - static_cast<float>(hi[i]);
-              mid[i] = static_cast<__bf16>(r1);
-              lo[i] = static_cast<__bf16>(r1 - static_cast<float>(mid[i]));
-            }
-            acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xb, hi, acc[j], 0, 0, 0);
-            acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xb, mid, acc[j], 0, 0, 0);
-            acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xb, lo, acc[j], 0, 0, 0);
-          }
-        } else {
-#pragma unroll
-          for (int j = 0; j < NET; ++j)
-#pragma unroll
-            for (int s8 = 0; s8 < 8; ++s8)
-              acc[j] =
-                  __builtin_amdgcn_mfma_f32_32x32x2f32(xr[q][s8], wr[q][j][s8], acc[j], 0, 0, 0);
+        for (int j = 0; j < NET; ++j) {
+          const int e = 32 * j + r;
+          load_raw8<F32T>(R + (int64_t)(e < E ? e : 0) * D, d, D, in && e < E, wo[j]);
         }
-        fetch(c + q + DEPTH, xr[q], wr[q]);
+      };
+      Raw8<XT> xr[DEPTH];
+      Raw8<F32T> wr[DEPTH][NET];
+#pragma unroll
+      for (int q = 0; q < DEPTH; ++q) fetch(c_lo + q, xr[q], wr[q]);
+      for (int c = c_lo; c < c_hi; c += DEPTH) {
+#pragma unroll
+        for (int q = 0; q < DEPTH; ++q) {
+          float xo[8], wo[NET][8];
+          cvt8<XT>(xr[q], xo);
+#pragma unroll
+          for (int j = 0; j < NET; ++j) cvt8<F32T>(wr[q][j], wo[j]);
+          mma(xo, wo);
+          fetch(c + q + DEPTH, xr[q], wr[q]);
+        }
+      }
+    } else {
+      constexpr int DEPTH = NET <= 2 ? 4 : 2;
+      auto fetch = [&](int c, float (&xo)[8], float (&wo)[NET][8]) __attribute__((always_inline)) {
+        const int d = c * 16 + 8 * h;
+        const bool in = c < c_hi;
+        load8<XT, false>(xrow, d, D, tv && in, xo);
+#pragma unroll
+        for (int j = 0; j < NET; ++j) {
+          const int e = 32 * j + r;
+          load8<F32T, false>(R + (int64_t)(e < E ? e : 0) * D, d, D, in && e < E, wo[j]);
+        }
+      };
+      float xr[DEPTH][8], wr[DEPTH][NET][8];
+#pragma unroll
+      for (int q = 0; q < DEPTH; ++q) fetch(c_lo + q, xr[q], wr[q]);
+      for (int c = c_lo; c < c_hi; c += DEPTH) {
+#pragma unroll
+        for (int q = 0; q < DEPTH; ++q) {
+          mma(xr[q], wr[q]);
+          fetch(c + q + DEPTH, xr[q], wr[q]);
+        }
       }
     }
 #pragma unroll
@@ -569,15 +667,26 @@ __global__ __launch_bounds__(NW * kWave) void router_mfma_kernel(
     float lg[NET];
 #pragma unroll
     for (int q = 0; q < NET; ++q) lg[q] = red[0][q][tok][jl];
-    select_lanes<NET>(lg, a, b, t0 + tok, true, jl, sb[tok], sc[tok]);
+    select_lanes<NET>(lg, bias_v, a, b, t0 + tok, true, jl, sb[tok], sc[tok]);
   }
-  __syncthreads();
+  // only sb / sc are read across threads below: an LDS barrier, which does
+  // not wait for the selection's global stores as __syncthreads() would
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   for (int e = threadIdx.x; e < E; e += NTH) {
+    // all 32 rows read first (one LDS latency), then added in token order
+    float sv[32];
+    int cv[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      sv[i] = sb[i][e];
+      cv[i] = sc[i][e];
+    }
     float s = 0.0f;
     int c = 0;
-    for (int i = 0; i < ntok; ++i) {
-      s += sb[i][e];
-      c += sc[i][e];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      s += i < ntok ? sv[i] : 0.0f;
+      c += i < ntok ? cv[i] : 0;
     }
     put_partial(a, b, blk, e, s, c);
   }
@@ -777,10 +886,15 @@ extern "C" int uttt_route_tokens(const void* x, int x_dtype, const float* router
                                  group_sizes);
   hipStream_t st = as_stream(stream);
   const int net = (E + 31) / 32;
-#define UTTT_ROUTE_LAUNCH(NET, NW, SMALL)                                                   \
-  hipLaunchKernelGGL((router_mfma_kernel<XT, NET, NW, SMALL>), dim3(w.nblk, B),                \
-                     dim3(NW * kWave), 0, st, static_cast<const S*>(x), router_w, w_sb, D, vec, \
-                     logits_out, a)
+#define UTTT_ROUTE_LAUNCH(NET, NW, SMALL)                                                       \
+  if (vec)                                                                                      \
+    hipLaunchKernelGGL((router_mfma_kernel<XT, NET, NW, SMALL, true>), dim3(w.nblk, B),          \
+                       dim3(NW * kWave), 0, st, static_cast<const S*>(x), router_w, w_sb, D,     \
+                       logits_out, a);                                                          \
+  else                                                                                          \
+    hipLaunchKernelGGL((router_mfma_kernel<XT, NET, NW, SMALL, false>), dim3(w.nblk, B),         \
+                       dim3(NW * kWave), 0, st, static_cast<const S*>(x), router_w, w_sb, D,     \
+                       logits_out, a)
   // a few tokens per batch (generation): vector-ALU logits, no padded MFMA rows
   const bool small = T <= kSmallT;
   // rows of whole 16-byte vectors: every feature load is one unconditional vector load
