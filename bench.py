@@ -1376,7 +1376,7 @@ def other_targets(args):
     k = p["kernels"]
     a.no_cpu_baseline = True
     a.steps, a.warmup = 3, 1
-    m = bench_moe(a, "moe124m", extras=False)
+    m = bench_moe(a, "moe124m", extras=True)
     a.steps, a.warmup = 2, 1
     ms = bench_moe(a, "moe760m_shipped", extras=False)
     a.steps, a.warmup = 3, 1
@@ -1400,7 +1400,13 @@ def other_targets(args):
             step_GBs=p["value"], target_hbm_frac=0.70),
         "configs[3]_moe124m": dict(workload=m["config"]["workload"], value=m["value"],
                                    unit=m["unit"], ms_per_step=m["ms_per_step"],
-                                   sweep_mfma_frac=m["sweep"]["mfma_frac"]),
+                                   sweep_mfma_frac=m["sweep"]["mfma_frac"],
+                                   stages_ms_per_sweep=m.get("stages_ms_per_sweep"),
+                                   top_kernels_us={
+                                       k: v["avg_us"] for k, v in list(
+                                           m.get("kernels_by_symbol", {}).get("top", {})
+                                           .items())[:8]},
+                                   roofline=m.get("roofline")),
         "configs[4]_shipped_write": dict(workload=ms["config"]["workload"], value=ms["value"],
                                          unit=ms["unit"], ms_per_step=ms["ms_per_step"]),
         "configs[1]_dense124m": dense(d1),
