@@ -47,6 +47,11 @@ def test_row_id_map_kat_on_gpu():
         (1, 16, 3, 1, torch.bool, False),
         (1, 4096, 65, 2, torch.bool, False),    # E = 65 and T = 4112 take the three launches
         (1, 4112, 8, 2, torch.bool, True),
+        # expert counts below their kernel's compile-time bucket
+        (1, 2048, 20, 2, torch.bool, True),     # one launch, 32-expert bucket
+        (1, 4096, 40, 3, torch.bool, True),     # one launch, 64-expert bucket
+        (2, 5000, 20, 2, torch.bool, True),     # two launches, count rows padded to 32
+        (1, 70000, 24, 4, torch.int32, False),  # two launches, E = 24, two count-table chunks
     ],
 )
 def test_row_id_map_bit_exact(B, T, E, k, mask_dtype, ragged):

@@ -404,14 +404,32 @@ __global__ __launch_bounds__(kTile) void rowmap_scan_emit_kernel(
 // One-launch row map for short batches of a contiguous bool mask (s_t = 1,
 // T % 16 == 0, 16-byte aligned rows): T <= kFusedMaxTiles * kTile tokens and
 // E <= kFusedMaxE.  Every workgroup counts the whole batch itself -- the mask
-// is E * T bytes (64 KiB at T = 2048, E = 32) -- one (expert, 256-token tile)
-// count per thread from 16 independent 16-byte loads, so the count costs one
-// memory latency per 256 pairs; then it takes its tile's offsets from those
-// counts and emits the tile staged in LDS, written out in 16-byte vectors.
+// is E * T bytes (64 KiB at T = 2048, E = 32) -- each (expert, 256-token tile)
+// count by the 16 lanes of one DPP row with one 16-byte load each (summed by
+// DPP adds), 16 pairs per round and 16 rounds of loads in flight together,
+// so the count costs one memory latency per 256 pairs and a wave's loads
+// cover 1 KiB of one expert's row; then it
+// takes its tile's offsets from those counts and emits the tile staged in
+// LDS, written out in 16-byte vectors.
 // This replaces the count / scan / emit launches (and their workspace round
 // trip) where the three launches' fixed costs dominate.
 constexpr int kFusedMaxTiles = 16;
 constexpr int kFusedMaxE = 64;
+
+// Sum over each aligned group of 16 lanes (one DPP row), the total in every
+// lane: four DPP adds (swap neighbours, swap pairs, mirror the 8-lane halves,
+// mirror the row), no LDS round trip as a shuffle takes.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i32(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+__device__ __forceinline__ int row_sum16(int v) {
+  v += dpp_i32<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v += dpp_i32<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v += dpp_i32<0x141>(v);  // row_half_mirror
+  v += dpp_i32<0x140>(v);  // row_mirror
+  return v;
+}
 
 __device__ __forceinline__ int nonzero_bytes(uint32_t w) {
   w |= w >> 4;
@@ -420,6 +438,9 @@ __device__ __forceinline__ int nonzero_bytes(uint32_t w) {
   return __popc(w & 0x01010101u);
 }
 
+// EB: a compile-time bound on E (16, 32 or 64): the mask loads and the
+// ballots of the tile run over EB experts with no per-expert branch.
+template <int EB>
 __global__ __launch_bounds__(kTile) void rowmap_fused_kernel(const uint8_t* __restrict__ map,
                                                              int64_t s_b, int64_t s_e, int T,
                                                              int E, int ntiles,
@@ -435,37 +456,58 @@ __global__ __launch_bounds__(kTile) void rowmap_fused_kernel(const uint8_t* __re
   const uint8_t* mb = map + (int64_t)b * s_b;
   // this tile's bits first: their loads overlap the whole-batch count
   uint32_t bits[kMaxExperts / 32];
-  load_mask_bits<1>(mb, min(t, T - 1), s_e, E, t < T, bits);
-  // whole-batch counts: pair q = (expert, tile), 16 vectors of 16 tokens
+  load_mask_bits<1, EB>(mb, min(t, T - 1), s_e, E, t < T, bits);
+  // whole-batch counts: pair q = (expert, tile) is read by a group of 16
+  // lanes, one 16-token vector each (a wave reads 4 consecutive pairs: 1 KiB
+  // of one expert's row), and summed across the group with shuffles; the
+  // loads of kRounds rounds of 16 pairs go out together, from clamped
+  // (always valid) addresses
   constexpr int kVecPerTile = kTile / 16;
-  const int nvec = T / 16;
-  for (int q = threadIdx.x; q < E * ntiles; q += kTile) {
-    const int e = q / ntiles, i = q - e * ntiles;
-    const uint4* p = reinterpret_cast<const uint4*>(mb + (int64_t)e * s_e) + i * kVecPerTile;
-    const int nv = min(kVecPerTile, nvec - i * kVecPerTile);
-    uint4 v[kVecPerTile];
+  constexpr int kRounds = 16;
+  const int nvec = T / 16, npairs = E * ntiles;
+  const int grp = threadIdx.x / kVecPerTile, gl = threadIdx.x % kVecPerTile;
+  // q / ntiles as a float product: exact here (q < 2^10, ntiles <= 16: the
+  // product stays within 1e-4 of e + (i + 0.5) / ntiles)
+  const float inv_nt = 1.0f / (float)ntiles;
+  for (int q0 = 0; q0 < npairs; q0 += kRounds * (kTile / kVecPerTile)) {
+    uint4 v[kRounds];
+    int qe[kRounds], qi[kRounds];
 #pragma unroll
-    for (int u = 0; u < kVecPerTile; ++u) v[u] = u < nv ? p[u] : make_uint4(0u, 0u, 0u, 0u);
-    int c = 0;
+    for (int r = 0; r < kRounds; ++r) {
+      const int q = min(q0 + r * (kTile / kVecPerTile) + grp, npairs - 1);
+      qe[r] = (int)(((float)q + 0.5f) * inv_nt);
+      qi[r] = q - qe[r] * ntiles;
+      v[r] = reinterpret_cast<const uint4*>(mb + (int64_t)qe[r] * s_e)[min(
+          qi[r] * kVecPerTile + gl, nvec - 1)];
+    }
 #pragma unroll
-    for (int u = 0; u < kVecPerTile; ++u)
-      c += nonzero_bytes(v[u].x) + nonzero_bytes(v[u].y) + nonzero_bytes(v[u].z) +
-           nonzero_bytes(v[u].w);
-    cnt[e][i] = c;
+    for (int r = 0; r < kRounds; ++r) {
+      const int q = q0 + r * (kTile / kVecPerTile) + grp;
+      const int e = qe[r], i = qi[r];
+      const bool live = q < npairs && i * kVecPerTile + gl < nvec;
+      int c = live ? nonzero_bytes(v[r].x) + nonzero_bytes(v[r].y) + nonzero_bytes(v[r].z) +
+                         nonzero_bytes(v[r].w)
+                   : 0;
+      static_assert(kVecPerTile == 16, "one DPP row per pair");
+      c = row_sum16(c);
+      if (gl == 0 && q < npairs) cnt[e][i] = c;
+    }
   }
-  wave_counts(bits, E, wcnt, wmask);
+  wave_counts<EB>(bits, E, wcnt, wmask);
   __syncthreads();
   // offsets of this tile: exclusive scan over experts of the totals (wave 0,
   // E <= 64 = one lane per expert) plus the expert's count in earlier tiles
   if (threadIdx.x < kWave) {
     const int e = threadIdx.x;
     int total = 0, before = 0;
-    if (e < E)
-      for (int i = 0; i < ntiles; ++i) {
-        const int c = cnt[e][i];
+    if (e < E) {
+#pragma unroll
+      for (int i = 0; i < kFusedMaxTiles; ++i) {  // all reads in flight together
+        const int c = i < ntiles ? cnt[e][i] : 0;
         total += c;
         before += i < tile ? c : 0;
       }
+    }
     int incl = total;
 #pragma unroll
     for (int d = 1; d < kWave; d <<= 1) {
@@ -1068,9 +1110,16 @@ extern "C" int uttt_make_row_id_map(const void* routing_map, int mask_bytes, int
                         reinterpret_cast<uintptr_t>(row_id_map)) & 15u) == 0;
   if (mask_bytes == 1 && s_t == 1 && T % 16 == 0 && s_e % 16 == 0 && s_b % 16 == 0 && vec_ok &&
       ntiles <= kFusedMaxTiles && E <= kFusedMaxE) {
-    hipLaunchKernelGGL(rowmap_fused_kernel, dim3(ntiles, B), dim3(kTile), 0, st,
-                       static_cast<const uint8_t*>(routing_map), s_b, s_e, T, E, ntiles,
-                       group_sizes, row_id_map);
+    const uint8_t* m8 = static_cast<const uint8_t*>(routing_map);
+    if (E <= 16)
+      hipLaunchKernelGGL(rowmap_fused_kernel<16>, dim3(ntiles, B), dim3(kTile), 0, st, m8, s_b,
+                         s_e, T, E, ntiles, group_sizes, row_id_map);
+    else if (E <= 32)
+      hipLaunchKernelGGL(rowmap_fused_kernel<32>, dim3(ntiles, B), dim3(kTile), 0, st, m8, s_b,
+                         s_e, T, E, ntiles, group_sizes, row_id_map);
+    else
+      hipLaunchKernelGGL(rowmap_fused_kernel<kFusedMaxE>, dim3(ntiles, B), dim3(kTile), 0, st,
+                         m8, s_b, s_e, T, E, ntiles, group_sizes, row_id_map);
     return check_launch("make_row_id_map");
   }
   int32_t* counts = reinterpret_cast<int32_t*>(workspace);
