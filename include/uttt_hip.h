@@ -86,6 +86,26 @@ int uttt_route_tokens(const void* x, int x_dtype, const float* router_w, int64_t
                       float* combine, float* balance, float* lb_loss, float* balance_sum,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* Scratch bytes for uttt_route_tokens_map at (B, T, E, D). */
+size_t uttt_route_tokens_map_workspace_bytes(int B, int T, int E, int D);
+
+/* The routing and the row map of one routed read in one call:
+ * FastWeightMLPSubNN._route_tokens (M/modeling_recurrent_lact.py:147-169) as
+ * uttt_route_tokens (no logits_out, no lb_loss; balance_sum required), then
+ * make_row_id_map (lact_moe_triton/triton_permute.py:283-393) of its mask as
+ * uttt_make_row_id_map, as _apply_moe_fast_weights_grouped (:296-349) calls
+ * them in turn.  The outputs are those two calls' (the row map, mask, group
+ * sizes, gates and balances bit-identical; balance_sum the same sums added
+ * in another fixed order).  For T % 16 == 0, T <= 4096 and E <= 64 the row
+ * map's one-launch kernel also adds the selection blocks' balance partials,
+ * so the call is two launches instead of four. */
+int uttt_route_tokens_map(const void* x, int x_dtype, const float* router_w, int64_t w_sb, int B,
+                          int T, int D, int E, const float* bias, int64_t bias_sb, int topk,
+                          int router_type, int combine_mode, float alpha, float router_scale,
+                          float norm_eps, void* mask, int32_t* group_sizes, float* combine,
+                          float* balance, float* balance_sum, int32_t* row_id_map,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
 /* Loss-free balancing counts.  Replaces _store_loss_free_counts with
  * _loss_free_counts_for_scope (M/modeling_recurrent_lact.py:1646-1654,
  * 1695-1712) on one GPU (the all-reduce of :1657-1660 is the caller's):

@@ -166,3 +166,29 @@ def test_router_errors():
         RT.create_router_mask_sizes_probs(l, 1, router_type="sigmoid")
     with pytest.raises(RuntimeError, match="topk"):
         RT.create_router_mask_sizes_probs(l, 5)
+
+
+@pytest.mark.parametrize("B,T,D,E,k", [
+    (1, 2048, 1536, 32, 2),   # one routed read at the 760M shape: two launches
+    (2, 512, 768, 16, 2),
+    (1, 20, 64, 8, 2),        # one selection block: the router's sums are final
+    (1, 5000, 256, 16, 2),    # T > 4096: the general row map after the reduce
+    (1, 1030, 128, 70, 3),    # E > 64 and T % 16 != 0
+])
+def test_route_tokens_map_equals_route_then_row_map(B, T, D, E, k):
+    from uttt_amd.lact_moe_triton import triton_permute as TPM
+    g = torch.Generator().manual_seed(T + E)
+    x = torch.randn(B, T, D, generator=g).to(torch.bfloat16).to(DEV)
+    Rw = (torch.randn(E, D, generator=g) * D ** -0.5).to(DEV)
+    bias = (torch.randn(E, generator=g) * 0.5).to(DEV)
+    got = RT.route_tokens_map(x, Rw, k, routing_bias=bias, combine_mode="topk_renorm")
+    ref = RT.route_tokens_lb(x, Rw, k, routing_bias=bias, combine_mode="topk_renorm")
+    for a, b_ in zip(got[:4], ref[:4]):   # mask, group sizes, gates, balances
+        assert torch.equal(a, b_)
+    # the balance sums: the same partials added in another fixed order
+    torch.testing.assert_close(got[4], ref[4], rtol=1e-6, atol=1e-6)
+    rmap = TPM.make_row_id_map(ref[0], B, T, E)
+    assert torch.equal(got[5], rmap)
+    # deterministic
+    again = RT.route_tokens_map(x, Rw, k, routing_bias=bias, combine_mode="topk_renorm")
+    assert all(torch.equal(a, b_) for a, b_ in zip(again, got))

@@ -141,6 +141,13 @@ SIGNATURES = {
          ctypes.c_float, ctypes.c_float, ctypes.c_float, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p,
          c_sz, c_p],
     ),
+    "uttt_route_tokens_map_workspace_bytes": (c_sz, [c_int, c_int, c_int, c_int]),
+    "uttt_route_tokens_map": (
+        c_int,
+        [c_p, c_int, c_p, c_i64, c_int, c_int, c_int, c_int, c_p, c_i64, c_int, c_int, c_int,
+         ctypes.c_float, ctypes.c_float, ctypes.c_float, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_sz,
+         c_p],
+    ),
     "uttt_write_step": (
         c_int,
         [c_p, c_p, c_p, c_int, c_p, c_p, ctypes.c_float, c_int, c_i64, c_int, c_int, c_int, c_int,

@@ -416,6 +416,12 @@ __global__ __launch_bounds__(kTile) void rowmap_scan_emit_kernel(
 constexpr int kFusedMaxTiles = 16;
 constexpr int kFusedMaxE = 64;
 
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int d = kWave / 2; d > 0; d >>= 1) v += __shfl_xor(v, d, kWave);
+  return v;
+}
+
 // Sum over each aligned group of 16 lanes (one DPP row), the total in every
 // lane: four DPP adds (swap neighbours, swap pairs, mirror the 8-lane halves,
 // mirror the row), no LDS round trip as a shuffle takes.
@@ -440,18 +446,46 @@ __device__ __forceinline__ int nonzero_bytes(uint32_t w) {
 
 // EB: a compile-time bound on E (16, 32 or 64): the mask loads and the
 // ballots of the tile run over EB experts with no per-expert branch.
+// part_bal (the router's per-block balance partials [B, nblk_r, E]) given,
+// one more workgroup per batch (blockIdx.x == ntiles) sums them into bal_sum
+// [B, E], beside the tiles: expert e by wave e % 4, lane l adding blocks l
+// and l + 64, then a fixed-order wave sum.
 template <int EB>
 __global__ __launch_bounds__(kTile) void rowmap_fused_kernel(const uint8_t* __restrict__ map,
                                                              int64_t s_b, int64_t s_e, int T,
                                                              int E, int ntiles,
                                                              int32_t* group_sizes,
-                                                             int32_t* row_id_map) {
+                                                             int32_t* row_id_map,
+                                                             const float* __restrict__ part_bal,
+                                                             int nblk_r, float* bal_sum) {
   __shared__ __attribute__((aligned(16))) int32_t stage[kTile * (2 * kFusedMaxE + 1)];
   __shared__ int cnt[kFusedMaxE][kFusedMaxTiles];
   __shared__ int wcnt[kTile / kWave][kMaxExperts];
   __shared__ uint64_t wmask[kTile / kWave][kMaxExperts];
   __shared__ int toff[kMaxExperts];
   const int tile = blockIdx.x, b = blockIdx.y;
+  if (tile == ntiles) {  // the balance-sum workgroup (part_bal given)
+    const int w = threadIdx.x / kWave, lane = lane_id();
+    const float* pb = part_bal + (int64_t)b * nblk_r * E;
+    constexpr int kPer = EB / (kTile / kWave);  // experts per wave
+    float v[kPer][2];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {  // every load first, from clamped addresses
+      const int e = min(w + (kTile / kWave) * u, E - 1);
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        v[u][h] = pb[(int64_t)min(lane + kWave * h, nblk_r - 1) * E + e];
+    }
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int e = w + (kTile / kWave) * u;
+      float x = lane < nblk_r ? v[u][0] : 0.0f;
+      x += lane + kWave < nblk_r ? v[u][1] : 0.0f;
+      x = wave_sum(x);
+      if (lane == 0 && e < E) bal_sum[(int64_t)b * E + e] = x;
+    }
+    return;
+  }
   const int t = tile * kTile + threadIdx.x;
   const uint8_t* mb = map + (int64_t)b * s_b;
   // this tile's bits first: their loads overlap the whole-batch count
@@ -862,11 +896,6 @@ __global__ __launch_bounds__(kTokPerBlock* kWave) void permute_bwd_kernel(
 }
 
 // ------------------------------------------------------------- unpermute ---
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int d = kWave / 2; d > 0; d >>= 1) v += __shfl_xor(v, d, kWave);
-  return v;
-}
 
 template <class TT, int VE>
 __global__ __launch_bounds__(kTokPerBlock* kWave) void unpermute_bwd_kernel(
@@ -1074,6 +1103,30 @@ int pick_ve(int H, std::initializer_list<const void*> ptrs) {
   }
 
 }  // namespace
+
+bool launch_rowmap_fused(const uint8_t* mask, int64_t s_b, int64_t s_e, int B, int T, int E,
+                         int32_t* group_sizes, int32_t* row_id_map, const float* part_bal,
+                         int nblk_r, float* bal_sum, hipStream_t st) {
+  const int ntiles = (T + kTile - 1) / kTile;
+  const bool aligned = ((reinterpret_cast<uintptr_t>(mask) |
+                         reinterpret_cast<uintptr_t>(row_id_map)) & 15u) == 0;
+  if (B < 1 || T < 1 || T % 16 != 0 || s_e % 16 != 0 || s_b % 16 != 0 || !aligned ||
+      ntiles > kFusedMaxTiles || E < 1 || E > kFusedMaxE ||
+      (part_bal != nullptr && (nblk_r < 1 || nblk_r > 2 * kWave)))
+    return false;
+  const dim3 grid(ntiles + (part_bal != nullptr ? 1 : 0), B);
+  if (E <= 16)
+    hipLaunchKernelGGL(rowmap_fused_kernel<16>, grid, dim3(kTile), 0, st, mask, s_b, s_e, T, E,
+                       ntiles, group_sizes, row_id_map, part_bal, nblk_r, bal_sum);
+  else if (E <= 32)
+    hipLaunchKernelGGL(rowmap_fused_kernel<32>, grid, dim3(kTile), 0, st, mask, s_b, s_e, T, E,
+                       ntiles, group_sizes, row_id_map, part_bal, nblk_r, bal_sum);
+  else
+    hipLaunchKernelGGL(rowmap_fused_kernel<kFusedMaxE>, grid, dim3(kTile), 0, st, mask, s_b, s_e,
+                       T, E, ntiles, group_sizes, row_id_map, part_bal, nblk_r, bal_sum);
+  return true;
+}
+
 }  // namespace uttt
 
 using namespace uttt;
@@ -1110,16 +1163,8 @@ extern "C" int uttt_make_row_id_map(const void* routing_map, int mask_bytes, int
                         reinterpret_cast<uintptr_t>(row_id_map)) & 15u) == 0;
   if (mask_bytes == 1 && s_t == 1 && T % 16 == 0 && s_e % 16 == 0 && s_b % 16 == 0 && vec_ok &&
       ntiles <= kFusedMaxTiles && E <= kFusedMaxE) {
-    const uint8_t* m8 = static_cast<const uint8_t*>(routing_map);
-    if (E <= 16)
-      hipLaunchKernelGGL(rowmap_fused_kernel<16>, dim3(ntiles, B), dim3(kTile), 0, st, m8, s_b,
-                         s_e, T, E, ntiles, group_sizes, row_id_map);
-    else if (E <= 32)
-      hipLaunchKernelGGL(rowmap_fused_kernel<32>, dim3(ntiles, B), dim3(kTile), 0, st, m8, s_b,
-                         s_e, T, E, ntiles, group_sizes, row_id_map);
-    else
-      hipLaunchKernelGGL(rowmap_fused_kernel<kFusedMaxE>, dim3(ntiles, B), dim3(kTile), 0, st,
-                         m8, s_b, s_e, T, E, ntiles, group_sizes, row_id_map);
+    launch_rowmap_fused(static_cast<const uint8_t*>(routing_map), s_b, s_e, B, T, E,
+                        group_sizes, row_id_map, nullptr, 0, nullptr, st);
     return check_launch("make_row_id_map");
   }
   int32_t* counts = reinterpret_cast<int32_t*>(workspace);

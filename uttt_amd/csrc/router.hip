@@ -830,6 +830,45 @@ int finish(const Ws& w, int B, int E, int T, int32_t* group_sizes, float* lb_los
   return check_launch(what);
 }
 
+// The fused logits + selection launch of route_tokens (nblk blocks of 32
+// tokens per batch).
+int launch_route_kernel(const void* x, int x_dtype, const float* router_w, int64_t w_sb, int B,
+                        int T, int D, int E, int nblk, const SelectArgs& a, float* logits_out,
+                        hipStream_t st) {
+  const int net = (E + 31) / 32;
+#define UTTT_ROUTE_LAUNCH(NET, NW, SMALL)                                                       \
+  if (vec)                                                                                      \
+    hipLaunchKernelGGL((router_mfma_kernel<XT, NET, NW, SMALL, true>), dim3(nblk, B),          \
+                       dim3(NW * kWave), 0, st, static_cast<const S*>(x), router_w, w_sb, D,     \
+                       logits_out, a);                                                          \
+  else                                                                                          \
+    hipLaunchKernelGGL((router_mfma_kernel<XT, NET, NW, SMALL, false>), dim3(nblk, B),         \
+                       dim3(NW * kWave), 0, st, static_cast<const S*>(x), router_w, w_sb, D,     \
+                       logits_out, a)
+  // a few tokens per batch (generation): vector-ALU logits, no padded MFMA rows
+  const bool small = T <= kSmallT;
+  // rows of whole 16-byte vectors: every feature load is one unconditional vector load
+  const bool vec = D % 8 == 0 && w_sb % 4 == 0 &&
+                   ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(router_w)) & 15u) == 0;
+  UTTT_DTYPE_SWITCH_LR(x_dtype, XT, {
+    using S = typename XT::S;
+    switch (net) {
+      case 1:
+        if (small) UTTT_ROUTE_LAUNCH(1, 8, true);
+        else UTTT_ROUTE_LAUNCH(1, 8, false);
+        break;
+      case 2:
+        if (small) UTTT_ROUTE_LAUNCH(2, 8, true);
+        else UTTT_ROUTE_LAUNCH(2, 8, false);
+        break;
+      case 3: UTTT_ROUTE_LAUNCH(3, 4, false); break;
+      default: UTTT_ROUTE_LAUNCH(4, 4, false); break;
+    }
+  });
+#undef UTTT_ROUTE_LAUNCH
+  return check_launch("route_tokens");
+}
+
 }  // namespace
 }  // namespace uttt
 
@@ -885,37 +924,57 @@ extern "C" int uttt_route_tokens(const void* x, int x_dtype, const float* router
                                  alpha, router_scale, norm_eps, mask, combine, balance,
                                  group_sizes);
   hipStream_t st = as_stream(stream);
-  const int net = (E + 31) / 32;
-#define UTTT_ROUTE_LAUNCH(NET, NW, SMALL)                                                       \
-  if (vec)                                                                                      \
-    hipLaunchKernelGGL((router_mfma_kernel<XT, NET, NW, SMALL, true>), dim3(w.nblk, B),          \
-                       dim3(NW * kWave), 0, st, static_cast<const S*>(x), router_w, w_sb, D,     \
-                       logits_out, a);                                                          \
-  else                                                                                          \
-    hipLaunchKernelGGL((router_mfma_kernel<XT, NET, NW, SMALL, false>), dim3(w.nblk, B),         \
-                       dim3(NW * kWave), 0, st, static_cast<const S*>(x), router_w, w_sb, D,     \
-                       logits_out, a)
-  // a few tokens per batch (generation): vector-ALU logits, no padded MFMA rows
-  const bool small = T <= kSmallT;
-  // rows of whole 16-byte vectors: every feature load is one unconditional vector load
-  const bool vec = D % 8 == 0 && w_sb % 4 == 0 &&
-                   ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(router_w)) & 15u) == 0;
-  UTTT_DTYPE_SWITCH_LR(x_dtype, XT, {
-    using S = typename XT::S;
-    switch (net) {
-      case 1:
-        if (small) UTTT_ROUTE_LAUNCH(1, 8, true);
-        else UTTT_ROUTE_LAUNCH(1, 8, false);
-        break;
-      case 2:
-        if (small) UTTT_ROUTE_LAUNCH(2, 8, true);
-        else UTTT_ROUTE_LAUNCH(2, 8, false);
-        break;
-      case 3: UTTT_ROUTE_LAUNCH(3, 4, false); break;
-      default: UTTT_ROUTE_LAUNCH(4, 4, false); break;
-    }
-  });
-#undef UTTT_ROUTE_LAUNCH
-  if (int rc = check_launch("route_tokens")) return rc;
+  if (int rc = launch_route_kernel(x, x_dtype, router_w, w_sb, B, T, D, E, w.nblk, a, logits_out,
+                                   st))
+    return rc;
   return finish(w, B, E, T, group_sizes, lb_loss, st, "route_tokens");
 }
+
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+extern "C" size_t uttt_route_tokens_map_workspace_bytes(int B, int T, int E, int D) {
+  if (B <= 0 || T <= 0 || E <= 0) return 0;
+  return align256(uttt_router_workspace_bytes(B, T, E, D)) +
+         uttt_row_id_map_workspace_bytes(B, T, E);
+}
+
+extern "C" int uttt_route_tokens_map(const void* x, int x_dtype, const float* router_w,
+                                     int64_t w_sb, int B, int T, int D, int E, const float* bias,
+                                     int64_t bias_sb, int topk, int router_type, int combine_mode,
+                                     float alpha, float router_scale, float norm_eps, void* mask,
+                                     int32_t* group_sizes, float* combine, float* balance,
+                                     float* balance_sum, int32_t* row_id_map, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  if (int rc = check_select_args(B, E, T, topk, router_type, combine_mode, "route_tokens_map"))
+    return rc;
+  UTTT_REQUIRE(D >= 1, "route_tokens_map: D=%d", D);
+  if (B == 0 || T == 0) return UTTT_OK;
+  UTTT_REQUIRE(x && router_w && mask && combine && balance && group_sizes && balance_sum &&
+                   row_id_map,
+               "route_tokens_map: null pointer");
+  Ws w = ws_layout(workspace, B, T, E, 32);
+  const size_t rm_off = align256(w.bytes);
+  const size_t need = rm_off + uttt_row_id_map_workspace_bytes(B, T, E);
+  UTTT_REQUIRE(workspace != nullptr && workspace_bytes >= need,
+               "route_tokens_map: workspace %zu < %zu bytes", workspace_bytes, need);
+  w.bal_sum = balance_sum;
+  const SelectArgs a = make_args(w, bias, bias_sb, B, E, T, topk, router_type, combine_mode,
+                                 alpha, router_scale, norm_eps, mask, combine, balance,
+                                 group_sizes);
+  hipStream_t st = as_stream(stream);
+  if (int rc = launch_route_kernel(x, x_dtype, router_w, w_sb, B, T, D, E, w.nblk, a, nullptr,
+                                   st))
+    return rc;
+  // the one-launch row map also adds the selection blocks' balance partials
+  // (group sizes are its own counts), so no reduce launch runs
+  const uint8_t* m8 = static_cast<const uint8_t*>(mask);
+  const int64_t s_b = (int64_t)E * T, s_e = T;
+  if (launch_rowmap_fused(m8, s_b, s_e, B, T, E, group_sizes, row_id_map,
+                          w.nblk > 1 ? w.part_bal : nullptr, w.nblk, balance_sum, st))
+    return check_launch("route_tokens_map");
+  if (int rc = finish(w, B, E, T, group_sizes, nullptr, st, "route_tokens_map")) return rc;
+  return uttt_make_row_id_map(mask, 1, s_b, s_e, 1, B, T, E, row_id_map, nullptr,
+                              static_cast<uint8_t*>(workspace) + rm_off, workspace_bytes - rm_off,
+                              stream);
+}
+

@@ -40,7 +40,7 @@ from .lact_moe_triton.lact_fw_grad import grouped_lact_swiglu_ffn_fast_weight_gr
 from .lact_moe_triton.lact_swiglu_ffn import grouped_swiglu_ffn_fwd
 from .lact_moe_triton.triton_permute import (permute_kv_and_lrs, permute_with_expert_mask,
                                              unpermute_and_merge_with_probs)
-from .routing import route_tokens, route_tokens_lb
+from .routing import route_tokens, route_tokens_map
 
 
 @dataclass(frozen=True)
@@ -126,11 +126,13 @@ def apply_moe_fast_weights_grouped(x, w0, w1, w2, router_proj_weights, cfg: Rout
     seq_len = x.shape[1]
     input_dtype = x.dtype
     xt = reshape_head_tokens(x, num_heads)
-    expert_mask, group_sizes, router_probs, _, balance_sums = route_tokens_lb(
+    # the routing and its row map in one call (route_tokens_lb, then
+    # make_row_id_map of its mask)
+    expert_mask, group_sizes, router_probs, _, balance_sums, row_id_map = route_tokens_map(
         xt, router_proj_weights, cfg.topk, routing_bias=routing_bias, **cfg.kwargs())
     w0_w2 = _w0_w2(w0, w2, precomputed_w0_w2)
     x_perm, _, row_id_map = permute_with_expert_mask(
-        xt.to(w0_w2.dtype).contiguous(), expert_mask, router_probs, cfg.topk)
+        xt.to(w0_w2.dtype).contiguous(), expert_mask, router_probs, cfg.topk, row_id_map)
     y_perm = grouped_swiglu_ffn_fwd(w0_w2, w1.contiguous(), x_perm, group_sizes)
     out = unpermute_and_merge_with_probs(y_perm, row_id_map, router_probs)
     # _make_lb_info (M:171-176): the balance sums come from the router kernel

@@ -133,6 +133,19 @@ def route_tokens_lb(x, router_proj_weights, topk, alpha=1.0, use_sigmoid=False,
     return out[:4] + (out[5],)
 
 
+def route_tokens_map(x, router_proj_weights, topk, alpha=1.0, use_sigmoid=False,
+                     router_type="softmax", combine_mode="selected_prob", router_scale=0.0,
+                     norm_eps=1e-6, routing_bias=None):
+    """route_tokens_lb followed by make_row_id_map of its mask, as the routed
+    read calls them (M:296-349), in one library call (two launches where the
+    row map's one-launch kernel fits: it also adds the router's balance
+    partials): (expert_mask, group_sizes, router_probs, balance_probs,
+    balance_sums, row_id_map [B, T, 2E+1] int32)."""
+    _check_modes(use_sigmoid, router_type, combine_mode)
+    return _route_map(x, router_proj_weights, int(topk), float(alpha), router_type, combine_mode,
+                      float(router_scale), float(norm_eps), routing_bias)
+
+
 def _route_fake(x, router_proj_weights, topk, alpha, router_type, combine_mode, router_scale,
                 norm_eps, routing_bias, return_logits):
     B, T, _ = x.shape
@@ -174,3 +187,49 @@ def _route(x: Tensor, router_proj_weights: Tensor, topk: int, alpha: float, rout
            L.ptr(logits) if return_logits else None, L.ptr(mask), L.ptr(gs), L.ptr(comb),
            L.ptr(bal), None, L.ptr(bal_sum), L.ptr(ws), nbytes, L.stream_of(x))
     return mask, gs, comb, bal, logits, bal_sum
+
+
+def _route_map_fake(x, router_proj_weights, topk, alpha, router_type, combine_mode, router_scale,
+                    norm_eps, routing_bias):
+    B, T, _ = x.shape
+    E = router_proj_weights.shape[-2]
+    e = x.new_empty
+    return (e((B, E, T), dtype=torch.bool), e((B, E), dtype=torch.int32),
+            e((B, E, T), dtype=torch.float32), e((B, E, T), dtype=torch.float32),
+            e((B, E), dtype=torch.float32), e((B, T, 2 * E + 1), dtype=torch.int32))
+
+
+@traced_op("route_tokens_map", _route_map_fake)
+def _route_map(x: Tensor, router_proj_weights: Tensor, topk: int, alpha: float, router_type: str,
+               combine_mode: str, router_scale: float, norm_eps: float,
+               routing_bias: Optional[Tensor]
+               ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    L.require_device(x, router_proj_weights)
+    assert x.dim() == 3, "x must be [B, T, D]"
+    B, T, D = x.shape
+    x = x.contiguous()
+    R = router_proj_weights.to(torch.float32).contiguous()
+    if R.dim() == 2:
+        E = R.shape[0]
+        w_sb = 0
+    else:
+        assert R.dim() == 3 and R.shape[0] in (1, B), "router weights must be [E,D] or [B,E,D]"
+        E = R.shape[1]
+        w_sb = E * D if R.shape[0] > 1 else 0
+    assert R.shape[-1] == D, "router weights must have x's last dimension"
+    bias, bias_sb = _bias_arg(routing_bias, B, E, x.device)
+    dev = x.device
+    mask = torch.empty((B, E, T), dtype=torch.bool, device=dev)
+    gs = torch.empty((B, E), dtype=torch.int32, device=dev)
+    comb = torch.empty((B, E, T), dtype=torch.float32, device=dev)
+    bal = torch.empty((B, E, T), dtype=torch.float32, device=dev)
+    bal_sum = torch.empty((B, E), dtype=torch.float32, device=dev)
+    rmap = torch.empty((B, T, 2 * E + 1), dtype=torch.int32, device=dev)
+    nbytes = L.lib().uttt_route_tokens_map_workspace_bytes(B, max(T, 1), E, D)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    L.call("uttt_route_tokens_map", L.ptr(x), L.dtype_code(x.dtype), L.ptr(R), w_sb, B, T, D, E,
+           L.ptr(bias), bias_sb, int(topk), ROUTER_TYPES[router_type],
+           COMBINE_MODES[combine_mode], float(alpha), float(router_scale), float(norm_eps),
+           L.ptr(mask), L.ptr(gs), L.ptr(comb), L.ptr(bal), L.ptr(bal_sum), L.ptr(rmap),
+           L.ptr(ws), nbytes, L.stream_of(x))
+    return mask, gs, comb, bal, bal_sum, rmap
