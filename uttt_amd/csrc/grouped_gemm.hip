@@ -238,6 +238,77 @@ __device__ __forceinline__ void staged_epilogue_prefetch(const f32x16 (&acc0)[NA
   });
 }
 
+// The staged epilogue with each quarter's inputs fetched one quarter ahead:
+// fetch(n, g) of quarter Q + 1 is issued before quarter Q's stores.  The
+// vector memory counter counts loads and stores together, in issue order, so a
+// load issued after a quarter's stores is only known to have landed once
+// those stores have completed (written back past L2): fetched after them, a
+// quarter's inputs waited for the previous quarter's stores at every quarter.
+// Ahead of them, the wait at quarter Q + 1 covers only the stores of quarter
+// Q - 1, which had a whole quarter to drain.  start() runs after quarter 0's
+// fetch and before quarter 0 is staged (LDS writes of per-tile values).
+template <int NA, class FetchFn, class UseFn, class StartFn>
+__device__ __forceinline__ void staged_epilogue_ahead(const f32x16 (&acc0)[NA][kNB],
+                                                      const f32x16 (&acc1)[NA][kNB],
+                                                      const TileCtx& c, FetchFn&& fetch,
+                                                      UseFn&& use, StartFn&& start) {
+  using Raw = decltype(fetch(0, 0));
+  Raw raw[2][kItemsOf<NA>];
+  auto fetch_q = [&](auto qq, Raw (&dst)[kItemsOf<NA>]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int k = 0; k < kItemsOf<NA>; ++k) {
+      const int it = threadIdx.x + kThreadsOf<NA> * k;
+      dst[k] = fetch(decltype(qq)::value * 64 + (it >> 4), it & 15);
+    }
+  };
+  block_barrier();  // every wave is done reading the stage buffers
+  fetch_q(std::integral_constant<int, 0>{}, raw[0]);
+  start();
+  static_for<4>([&](auto QQ) __attribute__((always_inline)) {
+    constexpr int Q = QQ;
+    if constexpr (Q < 3) fetch_q(std::integral_constant<int, Q + 1>{}, raw[(Q + 1) & 1]);
+    stage_quarter<Q>(acc0, acc1, c);
+    block_barrier();
+#pragma unroll
+    for (int k = 0; k < kItemsOf<NA>; ++k) {
+      const int it = threadIdx.x + kThreadsOf<NA> * k;
+      use(it >> 4, Q * 64 + (it >> 4), it & 15, raw[Q & 1][k]);
+    }
+    block_barrier();
+  });
+}
+
+// The tile's per-token lr values (three [B, N] arrays) as fp32 in LDS, past
+// the staged quarter in lds0 (64 tokens x 128 rows of fp32): thread t loads
+// the values of tile token t % 256 (clamped to the segment, so every address
+// is valid; a null array reads as 1) before the epilogue's first barrier and
+// writes them from start(); use() reads them with token_lr.  One set of loads
+// per tile instead of three per item and quarter.
+constexpr int kLrLds = 64 * 128;  // float offset in lds0
+template <class LR>
+struct TokenLrs {
+  using S = typename LR::S;
+  S v[3];
+  __device__ __forceinline__ void load(const TileCtx& c, int N, const S* l0, const S* l1,
+                                       const S* l2, const S* fallback) {
+    const int n = threadIdx.x & (kBRows - 1);
+    const int64_t li = (int64_t)c.b * N + c.tt.start + min(c.tt.n0 + n, c.tt.size - 1);
+    v[0] = *(l0 ? l0 + li : fallback);
+    v[1] = *(l1 ? l1 + li : fallback);
+    v[2] = *(l2 ? l2 + li : fallback);
+  }
+  __device__ __forceinline__ void write(const TileCtx& c, bool h0, bool h1, bool h2) const {
+    float* d = c.lds0 + kLrLds;
+    const int n = threadIdx.x & (kBRows - 1);  // threads past 256 write the same values again
+    d[n] = h0 ? LR::load(v[0]) : 1.0f;
+    d[kBRows + n] = h1 ? LR::load(v[1]) : 1.0f;
+    d[2 * kBRows + n] = h2 ? LR::load(v[2]) : 1.0f;
+  }
+};
+__device__ __forceinline__ float token_lr(const TileCtx& c, int j, int n) {
+  return c.lds0[kLrLds + j * kBRows + n];
+}
+
 // --- epilogue: plain store of both tiles into a token-major [B, N, ld] buffer
 // Every epilogue states kStaleColumnsUnused: true only when it reads, stores
 // or reduces nothing of the token columns at or past its segment's end.  The
@@ -473,35 +544,31 @@ struct EpiS1 {
     using S = typename LR::S;
     struct Raw {
       float4 dh0, dh1;
-      S l0, l1, l2;
     };
     auto fetch = [&](int n, int g) __attribute__((always_inline)) {
       const int m = c.m0 + 8 * g;
       const int tok = c.tt.start + min(c.tt.n0 + n, c.tt.size - 1);  // clamped: always valid
       const float* p = dhb + (int64_t)tok * I + (m < I ? m : 0);
-      const int64_t li = (int64_t)c.b * ea.N + tok;
-      // every load from a valid address (a missing lr reads the first element
-      // of dh, which the use ignores): a load under a branch is followed by a
-      // wait on every access in flight, the last quarter's stores included
-      const S* fb = reinterpret_cast<const S*>(ea.dh);
-      const S* q0 = ea.lr0 ? ea.lr0 + li : fb;
-      const S* q1 = ea.lr1 ? ea.lr1 + li : fb;
-      const S* q2 = ea.lr2 ? ea.lr2 + li : fb;
       Raw r;
       r.dh0 = *reinterpret_cast<const float4*>(p);
       r.dh1 = *reinterpret_cast<const float4*>(p + 4);
-      r.l0 = *q0;
-      r.l1 = *q1;
-      r.l2 = *q2;
       return r;
     };
-    staged_epilogue_prefetch(acc0, acc1, c, fetch, [&](int nl, int n, int g, const Raw& rw) __attribute__((always_inline)) {
+    // a missing lr reads the first element of dh (every load from a valid
+    // address: a load under a branch is followed by a wait on every access in
+    // flight) and is stored as 1
+    TokenLrs<LR> lrs;
+    lrs.load(c, ea.N, ea.lr0, ea.lr1, ea.lr2, reinterpret_cast<const S*>(ea.dh));
+    auto start = [&]() __attribute__((always_inline)) {
+      lrs.write(c, ea.lr0 != nullptr, ea.lr1 != nullptr, ea.lr2 != nullptr);
+    };
+    staged_epilogue_ahead(acc0, acc1, c, fetch, [&](int nl, int n, int g, const Raw& rw) __attribute__((always_inline)) {
       const int m = c.m0 + 8 * g;
       if (c.tt.n0 + n >= c.tt.size || m >= I) return;
       const int tok = c.tt.start + c.tt.n0 + n;
-      const float l0 = ea.lr0 ? LR::load(rw.l0) : 1.0f;
-      const float l1 = ea.lr1 ? LR::load(rw.l1) : 1.0f;
-      const float l2 = ea.lr2 ? LR::load(rw.l2) : 1.0f;
+      const float l0 = token_lr(c, 0, n);
+      const float l1 = token_lr(c, 1, n);
+      const float l2 = token_lr(c, 2, n);
       float y0[8], y2[8], d0[8], d2[8], hh[8];
       float dh[8] = {rw.dh0.x, rw.dh0.y, rw.dh0.z, rw.dh0.w,
                      rw.dh1.x, rw.dh1.y, rw.dh1.z, rw.dh1.w};
@@ -532,7 +599,7 @@ struct EpiS1 {
           hb[(int64_t)(m + u) * ea.N + tok] = f32_to_bf16(hh[u]);
         }
       }
-    });
+    }, start);
   }
 };
 
@@ -670,33 +737,31 @@ struct EpiBwdSaved {
     using S = typename LR::S;
     struct Raw {
       uint4 y0, y2, dh, gd;
-      S l0, l1, l2;
     };
     auto fetch = [&](int n, int g) __attribute__((always_inline)) {
       const int m = c.m0 + 8 * g;
       const int tok = c.tt.start + min(c.tt.n0 + n, c.tt.size - 1);  // clamped: always valid
       const int mc = m < I ? m : 0;
-      const int64_t li = (int64_t)c.b * ea.N + tok;
       const int64_t r2 = bo2 + (int64_t)tok * I2, r1 = bo1 + (int64_t)tok * I;
       Raw r;
       r.y0 = *reinterpret_cast<const uint4*>(ea.y_saved + r2 + mc);
       r.y2 = *reinterpret_cast<const uint4*>(ea.y_saved + r2 + I + mc);
       r.dh = *reinterpret_cast<const uint4*>(ea.dh_saved + r1 + mc);
       r.gd = *reinterpret_cast<const uint4*>(ea.gd + r1 + mc);
-      r.l0 = ea.lr0[li];
-      r.l1 = ea.lr1[li];
-      r.l2 = ea.lr2[li];
       return r;
     };
-    staged_epilogue_prefetch(acc0, acc1, c, fetch, [&](int nl, int n, int g, const Raw& rw) __attribute__((always_inline)) {
+    TokenLrs<LR> lrs;
+    lrs.load(c, ea.N, ea.lr0, ea.lr1, ea.lr2, ea.lr0);
+    auto start = [&]() __attribute__((always_inline)) { lrs.write(c, true, true, true); };
+    staged_epilogue_ahead(acc0, acc1, c, fetch, [&](int nl, int n, int g, const Raw& rw) __attribute__((always_inline)) {
       const int m = c.m0 + 8 * g;
       const bool ok = c.tt.n0 + n < c.tt.size && m < I;
       const int tok = c.tt.start + c.tt.n0 + n;
       float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f;
       if (ok) {
-        const float L0 = LR::load(rw.l0);
-        const float L1 = LR::load(rw.l1);
-        const float L2 = LR::load(rw.l2);
+        const float L0 = token_lr(c, 0, n);
+        const float L1 = token_lr(c, 1, n);
+        const float L2 = token_lr(c, 2, n);
         float gy0[8], gy2[8], y0v[8], y2v[8], dh[8], gd[8];
         staged8(c.lds0, nl, g, gy0);
         staged8(c.lds1, nl, g, gy2);
@@ -742,7 +807,7 @@ struct EpiBwdSaved {
         ea.lr_part[plane + o] = s1;
         ea.lr_part[2 * plane + o] = s2;
       }
-    });
+    }, start);
   }
 };
 
