@@ -500,6 +500,45 @@ class MoeSweep:
                         i += 1
         self._mark(None)
 
+    def capture_reads(self, layers):
+        """One HIP graph (torch.cuda.CUDAGraph) of a chunk's `layers` routed
+        reads through the product API.  Every chunk reads the same input sets
+        (layers is a multiple of NSETS) and the pool in place, so the graph
+        replays the reads of any chunk; the writes between replays update the
+        buffers it reads."""
+        import torch
+
+        assert layers % self.NSETS == 0 and self.marks is None
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):   # allocations of the first calls outside the capture
+            for l in range(layers):
+                self.apply(self.sets[l % self.NSETS])
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for l in range(layers):
+                self.apply(self.sets[l % self.NSETS])
+        torch.cuda.synchronize()
+        self.read_graph = graph
+
+    def sweep_graphed(self, layers, chunks, batched):
+        """sweep() with each chunk's routed reads replayed from capture_reads'
+        graph (the updates and writes run eagerly between the replays)."""
+        i = 0
+        for c in range(chunks):
+            self.read_graph.replay()
+            i += layers
+            if c < chunks - 1:
+                if batched:
+                    self.update_batched(layers, i)
+                    i += layers
+                else:
+                    for _ in range(layers):
+                        self.update_one(self.sets[i % self.NSETS])
+                        i += 1
+
     # ---------------------------------------------------------- accounting --
     def apply_symbols(self):
         """Kernel symbols of the APPLY's gate/up and down projection, as the
@@ -741,6 +780,25 @@ def bench_moe(args, key, extras=True):
     )
     if not extras:
         return res
+
+    # the same sweep with each chunk's routed reads replayed from one HIP graph
+    if layers % sw.NSETS == 0:
+        sw.capture_reads(layers)
+        sw.sweep_graphed(layers, 2, batched)
+        gwalls = []
+        for _ in range(max(args.steps, 1)):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            sw.sweep_graphed(layers, chunks, batched)
+            torch.cuda.synchronize()
+            gwalls.append(time.perf_counter() - t0)
+        gwall = statistics.mean(gwalls)
+        res["graphed_reads"] = dict(
+            value=round(tokens / gwall, 1), unit="tokens/s", ms_per_step=round(gwall * 1e3, 3),
+            what="the same sweep, each chunk's L routed reads (router, row map, permute, "
+                 "grouped APPLY, unpermute: the product API calls) captured once in a HIP "
+                 "graph (torch.cuda.CUDAGraph) and replayed; updates and writes eager")
+        sw.read_graph = None
 
     # stage totals of one sweep (events around the product calls)
     sw.marks = []
@@ -1401,6 +1459,7 @@ def other_targets(args):
         "configs[3]_moe124m": dict(workload=m["config"]["workload"], value=m["value"],
                                    unit=m["unit"], ms_per_step=m["ms_per_step"],
                                    sweep_mfma_frac=m["sweep"]["mfma_frac"],
+                                   graphed_reads=m.get("graphed_reads"),
                                    stages_ms_per_sweep=m.get("stages_ms_per_sweep"),
                                    top_kernels_us={
                                        k: v["avg_us"] for k, v in list(
