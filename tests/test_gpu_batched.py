@@ -151,3 +151,62 @@ def test_update_fwd_bwd_at_760m_shape(writers):
                               name="grad_lr " + nm)
             assert_bf16_close(dw.router_probs.grad[0, sub, t].cpu(), ref[5][0, :, 0],
                               name="grad_probs " + nm)
+
+
+def _close_dev(ours, ref, rtol=2e-2, name="", spread=None):
+    """tests.helpers.assert_bf16_close's bar (|ours - ref| <= rtol*|ref| +
+    rtol*rms(ref)) evaluated on the device, for whole pool-sized tensors.
+    spread: sum of the magnitudes of the bf16-rounded terms that make up ref;
+    each term carries up to 2^-9 of its own magnitude of rounding, so 2^-8 *
+    spread is added to the bound (it matters only where the terms cancel)."""
+    o, r = ours.detach().float(), ref.detach().float()
+    assert o.shape == r.shape, (name, o.shape, r.shape)
+    assert bool(torch.isfinite(o).all()), f"{name}: non-finite output"
+    atol = rtol * r.pow(2).mean().sqrt()
+    err = (o - r).abs()
+    bound = rtol * r.abs() + atol
+    if spread is not None:
+        bound = bound + spread * 2.0 ** -8
+    nbad = int((err > bound).sum())
+    assert nbad == 0, (f"{name}: {nbad}/{o.numel()} elements out of tolerance; "
+                       f"max err {err.max().item():.3e}, atol {atol.item():.3e}")
+
+
+def test_batched_update_is_the_sum_over_writers():
+    """Linearity at full size, over every expert and hidden unit: the batched
+    UPDATE of 24 writers (N = 98 304) equals the sum of the 24 one-writer
+    UPDATEs (each checked against the oracle above), the weight gradients of
+    its backward the sum of theirs, and each token's gradients (k, v, lr,
+    router probs) the ones its own writer's call gives.  The batched call
+    accumulates all writers' rows in fp32 and rounds once; the sum adds 24
+    bf16-rounded terms (the reference's own aggregate), so the bar is the
+    bf16 one."""
+    n = 24
+    W02, W1, G02, G1 = _pool(seed=7)
+    ws = _writers(n, seed=4242)
+
+    def run(group):
+        dws = [moe.WriterInputs(w["k"].to(DEV).requires_grad_(), w["v"].to(DEV).requires_grad_(),
+                                w["lr"].to(DEV).requires_grad_(), w["mask"].to(DEV),
+                                w["probs"].to(DEV).requires_grad_()) for w in group]
+        Wl = [W02.clone().requires_grad_(), W1.clone().requires_grad_()]
+        d02, d1 = moe.aggregate_moe_update_grads(dws, None, Wl[1], None, TOPK,
+                                                 precomputed_w0_w2=Wl[0], packed=True)
+        torch.autograd.backward([d02, d1], [G02, G1])
+        return d02.detach(), d1.detach(), Wl[0].grad, Wl[1].grad, dws
+
+    B02, B1, BG02, BG1, bdws = run(ws)
+    sums = [torch.zeros(t.shape, dtype=torch.float32, device=DEV) for t in (B02, B1, BG02, BG1)]
+    spreads = [torch.zeros_like(t) for t in sums]
+    for li, w in enumerate(ws):
+        d02, d1, g02, g1, dws = run([w])
+        for s_, a_, t in zip(sums, spreads, (d02, d1, g02, g1)):
+            s_ += t.float()
+            a_ += t.float().abs()
+        for attr in ("k_tokens", "v_tokens", "lr_tokens", "router_probs"):
+            _close_dev(getattr(bdws[li], attr).grad, getattr(dws[0], attr).grad,
+                       name=f"writer {li} grad {attr}")
+    torch.cuda.synchronize()
+    for t, s_, a_, nm in zip((B02, B1, BG02, BG1), sums, spreads,
+                             ("dW0_W2", "dW1", "grad_W0_W2", "grad_W1")):
+        _close_dev(t, s_, name=f"{nm} (batched) vs sum of writers", spread=a_)
