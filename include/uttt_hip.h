@@ -98,13 +98,19 @@ size_t uttt_route_tokens_map_workspace_bytes(int B, int T, int E, int D);
  * sizes, gates and balances bit-identical; balance_sum the same sums added
  * in another fixed order).  For T % 16 == 0, T <= 4096 and E <= 64 the row
  * map's one-launch kernel also adds the selection blocks' balance partials,
- * so the call is two launches instead of four. */
+ * so the call is two launches instead of four.  src_rows (optional, int32
+ * [B, T * topk]; only where uttt_route_tokens_map_src_rows(T, E) is 1, with
+ * 16-byte aligned mask and row map): the inverse of the row map, src_rows[b,
+ * row] = the token routed to that row, for uttt_grouped_gate_up_gather.  The
+ * reference has no such output (its permute reads the row map). */
+int uttt_route_tokens_map_src_rows(int T, int E);
 int uttt_route_tokens_map(const void* x, int x_dtype, const float* router_w, int64_t w_sb, int B,
                           int T, int D, int E, const float* bias, int64_t bias_sb, int topk,
                           int router_type, int combine_mode, float alpha, float router_scale,
                           float norm_eps, void* mask, int32_t* group_sizes, float* combine,
                           float* balance, float* balance_sum, int32_t* row_id_map,
-                          void* workspace, size_t workspace_bytes, void* stream);
+                          int32_t* src_rows, void* workspace, size_t workspace_bytes,
+                          void* stream);
 
 /* Loss-free balancing counts.  Replaces _store_loss_free_counts with
  * _loss_free_counts_for_scope (M/modeling_recurrent_lact.py:1646-1654,
@@ -241,6 +247,22 @@ int uttt_permute_kv_lrs_bwd(const void* gk, const void* gv, int k_dtype,
 int uttt_grouped_gate_up(const void* w0_w2, const void* x, const int32_t* group_sizes, int B,
                          int E, int I, int D, int N, void* hidden, int token_major,
                          void* stream);
+
+/* uttt_grouped_gate_up (token-major hidden) reading its token rows straight
+ * from the unpermuted x [B, T, D] through the inverse row map src_rows
+ * [B, src_sb] (uttt_route_tokens_map's src_rows): routed row n of batch b is
+ * x[b, src_rows[b, n]], so the permuted copy of x (permute_with_expert_mask,
+ * L/triton_permute.py:1169-1248, fused_two_mm_swiglu_triton's input) is not
+ * made.  Bit-identical to permuting then calling uttt_grouped_gate_up.  Only
+ * for the sizes that take the skinny tiles: uttt_grouped_gate_up_gathers(N, E)
+ * is 1 (else an error).  Indices outside [0, T) read row T - 1; T * D must be
+ * below 2^30.  No counterpart in the reference: the routed read's glue
+ * (_apply_moe_fast_weights_grouped, M:296-349) calls it where no gradient
+ * flows through the read. */
+int uttt_grouped_gate_up_gathers(long long N, int E);
+int uttt_grouped_gate_up_gather(const void* w0_w2, const void* x, int T, const int32_t* src_rows,
+                                long long src_sb, const int32_t* group_sizes, int B, int E, int I,
+                                int D, int N, void* hidden, void* stream);
 
 /* APPLY, down projection (and every "W times token rows" product).
  * Replaces grouped_gemm_transpose_triton (L/triton_grouped_gemm.py:170-243;

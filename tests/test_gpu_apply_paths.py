@@ -64,3 +64,40 @@ def test_apply_paths_identical(B, E, I, D, N, empty):
         # reference's bf16 hidden state between the two products)
         ref = OF.swiglu_ffn_fwd(W02.cpu(), W1.cpu(), X.cpu(), gs.cpu())
         assert_bf16_close(y, ref, name="apply (skinny tiles)")
+
+
+@pytest.mark.parametrize("B,E,I,D,T,k,empty", [
+    (1, 32, 3072, 1536, 2048, 2, (5, 9)),   # the configs[4] routed read
+    (1, 16, 1536, 768, 2048, 2, ()),        # the configs[3] routed read
+    (2, 8, 384, 200, 350, 2, (3,)),         # K tails, two batches
+    (1, 70, 136, 96, 300, 3, (1, 68)),      # > 64 experts, partial row tiles
+])
+def test_gate_up_gather_equals_permuted_copy(B, E, I, D, T, k, empty):
+    """uttt_grouped_gate_up_gather reading x's rows through an inverse row
+    map gives the hidden state of uttt_grouped_gate_up on the permuted copy,
+    bit for bit, on every APPLY path (on the general tiles it copies the rows
+    first); an index outside [0, T) reads row T - 1."""
+    from uttt_amd.lact_moe_triton import _grouped as G
+    N = T * k
+    g = torch.Generator().manual_seed(T + E)
+    W02 = (torch.randn(B, E, 2 * I, D, generator=g) / D ** 0.5).to(torch.bfloat16).to(DEV)
+    x = torch.randn(B, T, D, generator=g).to(torch.bfloat16).to(DEV)
+    gs = _groups(B, E, N, T, empty).to(DEV)
+    src = torch.stack([torch.randperm(N, generator=g) % T for _ in range(B)]).to(torch.int32)
+    src = src.to(DEV)
+    x_perm = torch.gather(x, 1, src.long()[:, :, None].expand(B, N, D)).contiguous()
+    for path in (-1, 0, 1):
+        prev = L.lib().uttt_debug_set_apply_path(path)
+        try:
+            ref = G.gate_up(W02, x_perm, gs, token_major=True)
+            got = G.gate_up_gather(W02, x, src, gs)
+            torch.cuda.synchronize()
+        finally:
+            L.lib().uttt_debug_set_apply_path(prev)
+        assert torch.equal(got, ref), f"gathered gate/up differs on path {path}"
+    bad = src.clone()
+    bad[0, 0], bad[-1, -1] = T + 5, -3
+    want = src.clone()
+    want[0, 0], want[-1, -1] = T - 1, T - 1
+    xw = torch.gather(x, 1, want.long()[:, :, None].expand(B, N, D)).contiguous()
+    assert torch.equal(G.gate_up_gather(W02, x, bad, gs), G.gate_up(W02, xw, gs, token_major=True))

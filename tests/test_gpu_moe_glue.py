@@ -237,3 +237,28 @@ def test_compiled_read_and_update_equal_eager():
     assert torch.equal(d02_e, d02_c) and torch.equal(d1_e, d1_c)
     for ta, tb in zip(a, b):
         assert torch.equal(ta.grad, tb.grad)
+
+
+def test_routed_read_without_gradient_equals_the_permuted_path():
+    """The routed read under no_grad reads its token rows through the inverse
+    row map (no permuted copy); with a gradient to track it permutes as the
+    reference does.  Both give the same output bit for bit (configs[3] and
+    configs[4] chunks)."""
+    for E, D, I in ((16, 768, 1536), (32, 1536, 3072)):
+        g = torch.Generator(device=DEV).manual_seed(E)
+        W02 = (torch.randn(1, E, 2 * I, D, generator=g, device=DEV) * D ** -0.5).to(torch.bfloat16)
+        W1 = (torch.randn(1, E, D, I, generator=g, device=DEV) * D ** -0.5).to(torch.bfloat16)
+        x = torch.randn(1, 2048, D, generator=g, device=DEV)
+        x = (x / x.norm(dim=-1, keepdim=True)).to(torch.bfloat16)
+        R = torch.randn(E, D, generator=g, device=DEV)
+        rb = torch.randn(E, generator=g, device=DEV) * 0.5
+        cfg = moe.RouterConfig(topk=2, combine_mode="topk_renorm")
+        with torch.no_grad():
+            fast, lb = moe.apply_moe_fast_weights_grouped(x, None, W1, None, R, cfg, 1,
+                                                          routing_bias=rb, precomputed_w0_w2=W02)
+        xg = x.clone().requires_grad_()
+        slow, lb2 = moe.apply_moe_fast_weights_grouped(xg, None, W1, None, R, cfg, 1,
+                                                       routing_bias=rb, precomputed_w0_w2=W02)
+        torch.cuda.synchronize()
+        assert torch.equal(fast, slow.detach()), f"E={E}: gathered read differs"
+        assert torch.equal(lb[1], lb2[1])

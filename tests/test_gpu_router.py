@@ -17,6 +17,7 @@ import pytest
 import torch
 
 from oracle import routing as OR
+from uttt_amd import _lib as L
 from uttt_amd import routing as RT
 
 pytestmark = pytest.mark.gpu
@@ -192,3 +193,39 @@ def test_route_tokens_map_equals_route_then_row_map(B, T, D, E, k):
     # deterministic
     again = RT.route_tokens_map(x, Rw, k, routing_bias=bias, combine_mode="topk_renorm")
     assert all(torch.equal(a, b_) for a, b_ in zip(again, got))
+
+
+@pytest.mark.parametrize("B,T,D,E,k", [
+    (1, 2048, 1536, 32, 2),   # the 760M routed read
+    (2, 512, 768, 16, 2),
+    (1, 4096, 256, 64, 4),    # the largest one-launch row map
+    (1, 16, 64, 8, 2),
+])
+def test_route_tokens_map_src_rows_invert_the_row_map(B, T, D, E, k):
+    """The inverse map: every routed (token, expert) row r of the row map has
+    src_rows[b, r] == token, and the rows of a batch are T * k exactly."""
+    assert RT.src_rows_supported(T, E) == bool(L.lib().uttt_route_tokens_map_src_rows(T, E))
+    g = torch.Generator().manual_seed(3 * T + E)
+    x = torch.randn(B, T, D, generator=g).to(torch.bfloat16).to(DEV)
+    Rw = (torch.randn(E, D, generator=g) * D ** -0.5).to(DEV)
+    got = RT.route_tokens_map(x, Rw, k, combine_mode="topk_renorm", with_src_rows=True)
+    plain = RT.route_tokens_map(x, Rw, k, combine_mode="topk_renorm")
+    assert all(torch.equal(a, b_) for a, b_ in zip(got[:4], plain[:4]))
+    assert torch.equal(got[5], plain[5])
+    rmap, src = got[5].cpu(), got[6].cpu()
+    assert src.shape == (B, T * k)
+    n = rmap[:, :, 2 * E]                      # routed experts per token
+    assert bool((n == k).all())
+    rows = rmap[:, :, :k].long()               # each token's k rows
+    tok = torch.arange(T)[None, :, None].expand(B, T, k)
+    inv = torch.full((B, T * k), -1, dtype=torch.int32)
+    inv.scatter_(1, rows.reshape(B, -1), tok.reshape(B, -1).to(torch.int32))
+    assert torch.equal(src, inv)
+
+
+def test_route_tokens_map_src_rows_refused_where_the_row_map_takes_more_launches():
+    x = torch.randn(1, 5000, 64).to(torch.bfloat16).to(DEV)
+    Rw = torch.randn(16, 64).to(DEV)
+    assert not RT.src_rows_supported(5000, 16)
+    with pytest.raises(RuntimeError, match="src_rows"):
+        RT.route_tokens_map(x, Rw, 2, with_src_rows=True)

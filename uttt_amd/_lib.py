@@ -62,6 +62,11 @@ SIGNATURES = {
     "uttt_grouped_gate_up": (
         c_int, [c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int, c_p, c_int, c_p],
     ),
+    "uttt_grouped_gate_up_gathers": (c_int, [ctypes.c_longlong, c_int]),
+    "uttt_grouped_gate_up_gather": (
+        c_int, [c_p, c_p, c_int, c_p, ctypes.c_longlong, c_p, c_int, c_int, c_int, c_int, c_int,
+                c_p, c_p],
+    ),
     "uttt_grouped_gemm_nt": (
         c_int, [c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int, c_p, c_p],
     ),
@@ -142,11 +147,12 @@ SIGNATURES = {
          c_sz, c_p],
     ),
     "uttt_route_tokens_map_workspace_bytes": (c_sz, [c_int, c_int, c_int, c_int]),
+    "uttt_route_tokens_map_src_rows": (c_int, [c_int, c_int]),
     "uttt_route_tokens_map": (
         c_int,
         [c_p, c_int, c_p, c_i64, c_int, c_int, c_int, c_int, c_p, c_i64, c_int, c_int, c_int,
-         ctypes.c_float, ctypes.c_float, ctypes.c_float, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_sz,
-         c_p],
+         ctypes.c_float, ctypes.c_float, ctypes.c_float, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p,
+         c_sz, c_p],
     ),
     "uttt_write_step": (
         c_int,

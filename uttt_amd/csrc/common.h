@@ -23,11 +23,15 @@ int zero_fill_async(void* p, size_t bytes, hipStream_t st, const char* what);
 // The one-launch row map (permute.hip) of a contiguous bool mask [B, E, T]
 // (element strides s_b, s_e, 1), which also sums a router's per-block balance
 // partials part_bal [B, nblk_r, E] into bal_sum [B, E] when part_bal is given.
-// Returns false, launching nothing, when the shape does not fit it (T % 16,
-// T <= 4096, E <= 64, 16-byte aligned mask rows and row map).
+// src_rows (optional, [B] rows of src_sb entries): the inverse map, src_rows
+// [b, row] = the token routed to that row.  Returns false, launching nothing,
+// when the shape does not fit it (rowmap_fused_fits: T % 16, T <= 4096,
+// E <= 64; and 16-byte aligned mask rows and row map).
+bool rowmap_fused_fits(int T, int E);
 bool launch_rowmap_fused(const uint8_t* mask, int64_t s_b, int64_t s_e, int B, int T, int E,
                          int32_t* group_sizes, int32_t* row_id_map, const float* part_bal,
-                         int nblk_r, float* bal_sum, hipStream_t st);
+                         int nblk_r, float* bal_sum, hipStream_t st, int32_t* src_rows = nullptr,
+                         int64_t src_sb = 0);
 
 #define UTTT_REQUIRE(cond, ...)          \
   do {                                   \

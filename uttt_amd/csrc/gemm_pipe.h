@@ -220,6 +220,39 @@ struct TileLoader {
     }
   }
 
+  // KMajor rows gathered through a row index: tile row r is row idx[r] of the
+  // operand at `org` (rows of ld elements, k < k_end valid), for r < nrows
+  // (nrows >= 1); later rows repeat row idx[nrows - 1], as init clamps them.
+  // An index outside [0, rows_total) reads row rows_total - 1 (never out of
+  // bounds).  Offsets stay 32-bit: rows_total rows of ld elements are below
+  // 2^30 elements.
+  __device__ __forceinline__ void init_gather(const uint16_t* org, int64_t ld, int k_end_,
+                                              const int32_t* __restrict__ idx, int nrows,
+                                              int rows_total) {
+    static_assert(MAJOR == KMajor, "gathered rows are KMajor token rows");
+    const int lane = threadIdx.x & 63;
+    const int w = wave_id();
+    k_end = k_end_;
+    last = (k_end + kBK - 1) / kBK - 1;
+    nvalid = nrows;
+    wofs = w * 64 * 16;
+    asm volatile("" : "+s"(wofs));
+    ld2 = (int)ld * 2;
+    col2 = 0;
+    base = uniform_ptr(reinterpret_cast<const uint8_t*>(org));
+    kstep = (int64_t)kBK * 2;
+#pragma unroll
+    for (int t = 0; t < kLPT; ++t) {
+      const int s = (t * NW + w) * 64 + lane;
+      const int r = s / kChunks;
+      const int c = (s % kChunks) ^ kswz(r);
+      const uint32_t ix = (uint32_t)idx[r < nrows ? r : nrows - 1];
+      const int row = ix < (uint32_t)rows_total ? (int)ix : rows_total - 1;
+      off[t] = (uint32_t)(row * (int)ld + c * 8) * 2u;
+      asm volatile("" : "+v"(off[t]));
+    }
+  }
+
   __device__ __forceinline__ int clamp_step(int step) const { return step < last ? step : last; }
 
   // The descriptor of step `step` (call once per step, in step order: the

@@ -946,6 +946,11 @@ struct ApArgs {
   int B, E, N;
   int em;             // one batch: expert-major order over the real pairs (else upper-bound order)
   const int32_t* gs;
+  // gathered token rows (src non-null): routed row p of batch b is row
+  // src[b * src_sb + p] of x [B, T, K] instead of row p of a permuted copy
+  const int32_t* src;
+  int64_t src_sb;
+  int T;
 };
 
 // Per-wave accumulators: acc[t][j] = rows [32 w, 32 w + 32) of tile t x token block j.
@@ -1172,7 +1177,11 @@ __global__ __launch_bounds__(kThreads) void apply_kernel(ApArgs a, typename Epi:
   TileLoader<KMajor> la0, la1, lx;
   la0.init(A0, m0);
   la1.init(A1, m0 + a.row_off1);
-  lx.init(X, tt.n0);
+  if (a.src != nullptr)
+    lx.init_gather(a.x + (int64_t)b * a.T * a.K, a.K, a.K,
+                   a.src + b * a.src_sb + tt.start + tt.n0, tt.size - tt.n0, a.T);
+  else
+    lx.init(X, tt.n0);
   const int nk = (a.K + kBK - 1) / kBK;
   f32x16 acc[2][4];
   zero(acc);
@@ -1843,6 +1852,38 @@ extern "C" int uttt_grouped_gate_up(const void* w0_w2, const void* x, const int3
                            I, B, E, N, group_sizes);
   const EpiSwiGLU::Args ea{static_cast<uint16_t*>(hidden), I, N, token_major};
   return launch_tn<KMajor, EpiSwiGLU>(t, ea, B, as_stream(stream), "grouped_gate_up");
+}
+
+extern "C" int uttt_grouped_gate_up_gathers(long long N, int E) {
+  return use_apply_kernel(N, E) ? 1 : 0;
+}
+
+extern "C" int uttt_grouped_gate_up_gather(const void* w0_w2, const void* x, int T,
+                                           const int32_t* src_rows, long long src_sb,
+                                           const int32_t* group_sizes, int B, int E, int I, int D,
+                                           int N, void* hidden, void* stream) {
+  UTTT_REQUIRE(B >= 0 && E >= 1 && I >= 0 && D >= 0 && N >= 0 && T >= 0 && src_sb >= N,
+               "grouped_gate_up_gather: bad sizes");
+  UTTT_REQUIRE(I % 8 == 0 && D % 8 == 0,
+               "grouped_gate_up_gather: I=%d and D=%d must be multiples of 8", I, D);
+  if (B == 0 || N == 0 || I == 0) return UTTT_OK;
+  UTTT_REQUIRE(use_apply_kernel(N, E),
+               "grouped_gate_up_gather: N=%d routed rows over E=%d experts take the general "
+               "tiles, which read a permuted copy (uttt_grouped_gate_up)", N, E);
+  // the gathered rows' 32-bit lane offsets: every row of x starts below 2^30 elements
+  UTTT_REQUIRE(T >= 1 && (int64_t)T * D < ((int64_t)1 << 30),
+               "grouped_gate_up_gather: T=%d rows of D=%d elements exceed 2^30", T, D);
+  UTTT_REQUIRE(w0_w2 && x && src_rows && group_sizes && hidden,
+               "grouped_gate_up_gather: null pointer");
+  UTTT_REQUIRE(aligned16(w0_w2) && aligned16(x) && aligned16(hidden),
+               "grouped_gate_up_gather: tensors must be 16-byte aligned");
+  ApArgs a = apply_args(w0_w2, x, D, (int64_t)2 * I * D, I, I, 2 * I, kTileRows, B, E, N,
+                        group_sizes);
+  a.src = src_rows;
+  a.src_sb = src_sb;
+  a.T = T;
+  const ApSwiGLU::Args ea{static_cast<uint16_t*>(hidden), I, N};
+  return launch_apply<ApSwiGLU, true>(a, I, ea, as_stream(stream), "grouped_gate_up_gather");
 }
 
 extern "C" int uttt_grouped_gemm_nt(const void* w, const void* x, const int32_t* group_sizes,

@@ -222,11 +222,13 @@ constexpr int kStageMaxW = 57;  // STAGE: kTile * (2E+1) * 4 bytes plus the 6.5 
 // entry, which strides the lanes 4 * (2E+1) bytes apart.  WOFF: toff holds
 // each wave's first row per expert ([kTile / kWave][kMaxExperts], flattened:
 // the tile's offset plus the earlier waves' counts) instead of the tile's.
+// src (batch b's [rows] array, or null): the inverse map, src[row] = token.
 template <bool STAGE, bool COPY_OUT = STAGE, bool WOFF = false>
 __device__ __forceinline__ void emit_tile(const uint32_t bits[kMaxExperts / 32], int T, int E,
                                           int tile, int b, const int (*wcnt)[kMaxExperts],
                                           const uint64_t (*wmask)[kMaxExperts], const int* toff,
-                                          int32_t* stage, int32_t* row_id_map) {
+                                          int32_t* stage, int32_t* row_id_map,
+                                          int32_t* src = nullptr) {
   const int t = tile * kTile + threadIdx.x;
   const int w = threadIdx.x / kWave;
   const int n = __popc(bits[0]) + __popc(bits[1]) + __popc(bits[2]) + __popc(bits[3]);
@@ -256,6 +258,7 @@ __device__ __forceinline__ void emit_tile(const uint32_t bits[kMaxExperts / 32],
         row[E + j] = e;
         ++j;
         if (e >= n) row[e] = r;
+        if (src != nullptr) src[r] = t;
       }
     }
   }
@@ -457,7 +460,8 @@ __global__ __launch_bounds__(kTile) void rowmap_fused_kernel(const uint8_t* __re
                                                              int32_t* group_sizes,
                                                              int32_t* row_id_map,
                                                              const float* __restrict__ part_bal,
-                                                             int nblk_r, float* bal_sum) {
+                                                             int nblk_r, float* bal_sum,
+                                                             int32_t* src_rows, int64_t src_sb) {
   __shared__ __attribute__((aligned(16))) int32_t stage[kTile * (2 * kFusedMaxE + 1)];
   __shared__ int cnt[kFusedMaxE][kFusedMaxTiles];
   __shared__ int wcnt[kTile / kWave][kMaxExperts];
@@ -554,7 +558,8 @@ __global__ __launch_bounds__(kTile) void rowmap_fused_kernel(const uint8_t* __re
     }
   }
   __syncthreads();
-  emit_tile<true, false>(bits, T, E, tile, b, wcnt, wmask, toff, stage, nullptr);
+  emit_tile<true, false>(bits, T, E, tile, b, wcnt, wmask, toff, stage, nullptr,
+                         src_rows != nullptr ? src_rows + b * src_sb : nullptr);
   __syncthreads();
   // the tile's entries are nt * (2E+1) words, a multiple of 4 (nt % 16 == 0),
   // and start 16-byte aligned (T % 16 == 0, aligned output)
@@ -1104,9 +1109,15 @@ int pick_ve(int H, std::initializer_list<const void*> ptrs) {
 
 }  // namespace
 
+bool rowmap_fused_fits(int T, int E) {
+  const int ntiles = (T + kTile - 1) / kTile;
+  return T >= 1 && T % 16 == 0 && ntiles <= kFusedMaxTiles && E >= 1 && E <= kFusedMaxE;
+}
+
 bool launch_rowmap_fused(const uint8_t* mask, int64_t s_b, int64_t s_e, int B, int T, int E,
                          int32_t* group_sizes, int32_t* row_id_map, const float* part_bal,
-                         int nblk_r, float* bal_sum, hipStream_t st) {
+                         int nblk_r, float* bal_sum, hipStream_t st, int32_t* src_rows,
+                         int64_t src_sb) {
   const int ntiles = (T + kTile - 1) / kTile;
   const bool aligned = ((reinterpret_cast<uintptr_t>(mask) |
                          reinterpret_cast<uintptr_t>(row_id_map)) & 15u) == 0;
@@ -1117,13 +1128,14 @@ bool launch_rowmap_fused(const uint8_t* mask, int64_t s_b, int64_t s_e, int B, i
   const dim3 grid(ntiles + (part_bal != nullptr ? 1 : 0), B);
   if (E <= 16)
     hipLaunchKernelGGL(rowmap_fused_kernel<16>, grid, dim3(kTile), 0, st, mask, s_b, s_e, T, E,
-                       ntiles, group_sizes, row_id_map, part_bal, nblk_r, bal_sum);
+                       ntiles, group_sizes, row_id_map, part_bal, nblk_r, bal_sum, src_rows, src_sb);
   else if (E <= 32)
     hipLaunchKernelGGL(rowmap_fused_kernel<32>, grid, dim3(kTile), 0, st, mask, s_b, s_e, T, E,
-                       ntiles, group_sizes, row_id_map, part_bal, nblk_r, bal_sum);
+                       ntiles, group_sizes, row_id_map, part_bal, nblk_r, bal_sum, src_rows, src_sb);
   else
     hipLaunchKernelGGL(rowmap_fused_kernel<kFusedMaxE>, grid, dim3(kTile), 0, st, mask, s_b, s_e,
-                       T, E, ntiles, group_sizes, row_id_map, part_bal, nblk_r, bal_sum);
+                       T, E, ntiles, group_sizes, row_id_map, part_bal, nblk_r, bal_sum, src_rows,
+                       src_sb);
   return true;
 }
 

@@ -938,15 +938,23 @@ extern "C" size_t uttt_route_tokens_map_workspace_bytes(int B, int T, int E, int
          uttt_row_id_map_workspace_bytes(B, T, E);
 }
 
+extern "C" int uttt_route_tokens_map_src_rows(int T, int E) {
+  return rowmap_fused_fits(T, E) ? 1 : 0;
+}
+
 extern "C" int uttt_route_tokens_map(const void* x, int x_dtype, const float* router_w,
                                      int64_t w_sb, int B, int T, int D, int E, const float* bias,
                                      int64_t bias_sb, int topk, int router_type, int combine_mode,
                                      float alpha, float router_scale, float norm_eps, void* mask,
                                      int32_t* group_sizes, float* combine, float* balance,
-                                     float* balance_sum, int32_t* row_id_map, void* workspace,
-                                     size_t workspace_bytes, void* stream) {
+                                     float* balance_sum, int32_t* row_id_map,
+                                     int32_t* src_rows, void* workspace, size_t workspace_bytes,
+                                     void* stream) {
   if (int rc = check_select_args(B, E, T, topk, router_type, combine_mode, "route_tokens_map"))
     return rc;
+  UTTT_REQUIRE(src_rows == nullptr || rowmap_fused_fits(T, E),
+               "route_tokens_map: the inverse map (src_rows) needs T %% 16 == 0, T <= 4096 and "
+               "E <= 64 (T=%d, E=%d)", T, E);
   UTTT_REQUIRE(D >= 1, "route_tokens_map: D=%d", D);
   if (B == 0 || T == 0) return UTTT_OK;
   UTTT_REQUIRE(x && router_w && mask && combine && balance && group_sizes && balance_sum &&
@@ -970,8 +978,12 @@ extern "C" int uttt_route_tokens_map(const void* x, int x_dtype, const float* ro
   const uint8_t* m8 = static_cast<const uint8_t*>(mask);
   const int64_t s_b = (int64_t)E * T, s_e = T;
   if (launch_rowmap_fused(m8, s_b, s_e, B, T, E, group_sizes, row_id_map,
-                          w.nblk > 1 ? w.part_bal : nullptr, w.nblk, balance_sum, st))
+                          w.nblk > 1 ? w.part_bal : nullptr, w.nblk, balance_sum, st, src_rows,
+                          (int64_t)T * topk))
     return check_launch("route_tokens_map");
+  UTTT_REQUIRE(src_rows == nullptr,
+               "route_tokens_map: the inverse map (src_rows) needs 16-byte aligned mask and "
+               "row map");
   if (int rc = finish(w, B, E, T, group_sizes, nullptr, st, "route_tokens_map")) return rc;
   return uttt_make_row_id_map(mask, 1, s_b, s_e, 1, B, T, E, row_id_map, nullptr,
                               static_cast<uint8_t*>(workspace) + rm_off, workspace_bytes - rm_off,

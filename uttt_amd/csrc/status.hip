@@ -59,6 +59,6 @@ int zero_fill_async(void* p, size_t bytes, hipStream_t st, const char* what) {
 
 }  // namespace uttt
 
-extern "C" int uttt_abi_version(void) { return 3; }
+extern "C" int uttt_abi_version(void) { return 4; }
 
 extern "C" const char* uttt_last_error(void) { return g_last_error; }

@@ -53,6 +53,43 @@ def gate_up(W0_W2: Tensor, X: Tensor, group_sizes: Tensor, token_major: bool) ->
     return H
 
 
+def _gate_up_gather_fake(W0_W2, x, src_rows, group_sizes):
+    return x.new_empty((x.shape[0], src_rows.shape[1], W0_W2.shape[2] // 2))
+
+
+def gate_up_gathers(N: int, E: int) -> bool:
+    """Whether gate_up_gather runs at N routed rows over E experts (the sizes
+    that take the skinny tiles)."""
+    return bool(L.lib().uttt_grouped_gate_up_gathers(int(N), int(E)))
+
+
+@traced_op("grouped_gate_up_gather", _gate_up_gather_fake)
+def gate_up_gather(W0_W2: Tensor, x: Tensor, src_rows: Tensor, group_sizes: Tensor) -> Tensor:
+    """gate_up (token-major) of the routed rows x[b, src_rows[b, n]] of the
+    unpermuted x [B, T, D]: [B, N, I] with N = src_rows.shape[1] (the inverse
+    row map of route_tokens_map).  Where the sizes take the skinny tiles the
+    kernel reads the rows through the index (no permuted copy); elsewhere the
+    rows are gathered into a copy first (identical results)."""
+    L.require_device(W0_W2, x, src_rows, group_sizes)
+    _check_bf16(W0_W2, x)
+    B, E, I2, D = W0_W2.shape
+    Bx, T, Dx = x.shape
+    assert Bx == B and Dx == D, "x must be [B, T, D] with matching B, D"
+    assert src_rows.dtype == torch.int32 and src_rows.dim() == 2 and src_rows.shape[0] == B
+    src_rows = src_rows.contiguous()
+    N = src_rows.shape[1]
+    if not gate_up_gathers(N, E):
+        x_perm = torch.gather(x, 1, src_rows.long()[:, :, None].expand(B, N, D)).contiguous()
+        return gate_up(W0_W2, x_perm, group_sizes, token_major=True)
+    I = I2 // 2
+    gs = group_sizes_i32(group_sizes)
+    assert gs.shape == (B, E)
+    H = torch.empty((B, N, I), dtype=torch.bfloat16, device=x.device)
+    L.call("uttt_grouped_gate_up_gather", L.ptr(W0_W2), L.ptr(x), T, L.ptr(src_rows), N,
+           L.ptr(gs), B, E, I, D, N, L.ptr(H), L.stream_of(x))
+    return H
+
+
 def _gemm_nt_fake(W, X_tok, group_sizes):
     return X_tok.new_empty((X_tok.shape[0], X_tok.shape[1], W.shape[2]))
 

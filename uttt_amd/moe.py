@@ -36,11 +36,12 @@ from typing import Sequence
 import torch
 
 from . import _lib as L
+from .lact_moe_triton import _grouped
 from .lact_moe_triton.lact_fw_grad import grouped_lact_swiglu_ffn_fast_weight_grads
 from .lact_moe_triton.lact_swiglu_ffn import grouped_swiglu_ffn_fwd
 from .lact_moe_triton.triton_permute import (permute_kv_and_lrs, permute_with_expert_mask,
                                              unpermute_and_merge_with_probs)
-from .routing import route_tokens, route_tokens_map
+from .routing import route_tokens, route_tokens_map, src_rows_supported
 
 
 @dataclass(frozen=True)
@@ -126,14 +127,29 @@ def apply_moe_fast_weights_grouped(x, w0, w1, w2, router_proj_weights, cfg: Rout
     seq_len = x.shape[1]
     input_dtype = x.dtype
     xt = reshape_head_tokens(x, num_heads)
+    w0_w2 = _w0_w2(w0, w2, precomputed_w0_w2)
+    B, T = xt.shape[0], xt.shape[1]
+    E = router_proj_weights.shape[-2]
+    # Where no gradient flows through the read, the gate/up reads the routed
+    # rows of xt through the inverse row map instead of a permuted copy (one
+    # launch and the copy's traffic less, identical results)
+    no_grad = not torch.is_grad_enabled() or not any(
+        t is not None and t.requires_grad for t in (x, w0, w1, w2, precomputed_w0_w2))
+    gather = no_grad and w0_w2.dtype == torch.bfloat16 and src_rows_supported(T, E)
     # the routing and its row map in one call (route_tokens_lb, then
     # make_row_id_map of its mask)
-    expert_mask, group_sizes, router_probs, _, balance_sums, row_id_map = route_tokens_map(
-        xt, router_proj_weights, cfg.topk, routing_bias=routing_bias, **cfg.kwargs())
-    w0_w2 = _w0_w2(w0, w2, precomputed_w0_w2)
-    x_perm, _, row_id_map = permute_with_expert_mask(
-        xt.to(w0_w2.dtype).contiguous(), expert_mask, router_probs, cfg.topk, row_id_map)
-    y_perm = grouped_swiglu_ffn_fwd(w0_w2, w1.contiguous(), x_perm, group_sizes)
+    routed = route_tokens_map(xt, router_proj_weights, cfg.topk, routing_bias=routing_bias,
+                              with_src_rows=gather, **cfg.kwargs())
+    expert_mask, group_sizes, router_probs, _, balance_sums, row_id_map = routed[:6]
+    if gather:
+        w1c = w1.contiguous()
+        hidden = _grouped.gate_up_gather(w0_w2.contiguous(), xt.to(w0_w2.dtype).contiguous(),
+                                         routed[6], group_sizes)
+        y_perm = _grouped.gemm_nt(w1c, hidden, group_sizes)
+    else:
+        x_perm, _, row_id_map = permute_with_expert_mask(
+            xt.to(w0_w2.dtype).contiguous(), expert_mask, router_probs, cfg.topk, row_id_map)
+        y_perm = grouped_swiglu_ffn_fwd(w0_w2, w1.contiguous(), x_perm, group_sizes)
     out = unpermute_and_merge_with_probs(y_perm, row_id_map, router_probs)
     # _make_lb_info (M:171-176): the balance sums come from the router kernel
     return merge_head_tokens(out.to(input_dtype), seq_len, num_heads), (balance_sums, group_sizes)

@@ -135,15 +135,26 @@ def route_tokens_lb(x, router_proj_weights, topk, alpha=1.0, use_sigmoid=False,
 
 def route_tokens_map(x, router_proj_weights, topk, alpha=1.0, use_sigmoid=False,
                      router_type="softmax", combine_mode="selected_prob", router_scale=0.0,
-                     norm_eps=1e-6, routing_bias=None):
+                     norm_eps=1e-6, routing_bias=None, with_src_rows=False):
     """route_tokens_lb followed by make_row_id_map of its mask, as the routed
     read calls them (M:296-349), in one library call (two launches where the
     row map's one-launch kernel fits: it also adds the router's balance
     partials): (expert_mask, group_sizes, router_probs, balance_probs,
-    balance_sums, row_id_map [B, T, 2E+1] int32)."""
+    balance_sums, row_id_map [B, T, 2E+1] int32).  with_src_rows (only where
+    src_rows_supported(T, E)): also the inverse map src_rows [B, T*topk] int32,
+    the token routed to each permuted row, for the gathered gate/up."""
     _check_modes(use_sigmoid, router_type, combine_mode)
-    return _route_map(x, router_proj_weights, int(topk), float(alpha), router_type, combine_mode,
-                      float(router_scale), float(norm_eps), routing_bias)
+    out = _route_map(x, router_proj_weights, int(topk), float(alpha), router_type, combine_mode,
+                     float(router_scale), float(norm_eps), routing_bias, bool(with_src_rows))
+    return out if with_src_rows else out[:6]
+
+
+def src_rows_supported(T: int, E: int) -> bool:
+    """Whether route_tokens_map can return the inverse row map at (T, E): the
+    one-launch row map's sizes (T a multiple of 16 up to 4096, E up to 64),
+    the rule uttt_route_tokens_map_src_rows states (pure Python, so that
+    torch.compile traces the routed read without calling the library)."""
+    return 1 <= T <= 4096 and T % 16 == 0 and 1 <= E <= 64
 
 
 def _route_fake(x, router_proj_weights, topk, alpha, router_type, combine_mode, router_scale,
@@ -190,20 +201,21 @@ def _route(x: Tensor, router_proj_weights: Tensor, topk: int, alpha: float, rout
 
 
 def _route_map_fake(x, router_proj_weights, topk, alpha, router_type, combine_mode, router_scale,
-                    norm_eps, routing_bias):
+                    norm_eps, routing_bias, with_src_rows):
     B, T, _ = x.shape
     E = router_proj_weights.shape[-2]
     e = x.new_empty
     return (e((B, E, T), dtype=torch.bool), e((B, E), dtype=torch.int32),
             e((B, E, T), dtype=torch.float32), e((B, E, T), dtype=torch.float32),
-            e((B, E), dtype=torch.float32), e((B, T, 2 * E + 1), dtype=torch.int32))
+            e((B, E), dtype=torch.float32), e((B, T, 2 * E + 1), dtype=torch.int32),
+            e((B, T * topk) if with_src_rows else (0,), dtype=torch.int32))
 
 
 @traced_op("route_tokens_map", _route_map_fake)
 def _route_map(x: Tensor, router_proj_weights: Tensor, topk: int, alpha: float, router_type: str,
                combine_mode: str, router_scale: float, norm_eps: float,
-               routing_bias: Optional[Tensor]
-               ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+               routing_bias: Optional[Tensor], with_src_rows: bool
+               ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
     L.require_device(x, router_proj_weights)
     assert x.dim() == 3, "x must be [B, T, D]"
     B, T, D = x.shape
@@ -225,11 +237,12 @@ def _route_map(x: Tensor, router_proj_weights: Tensor, topk: int, alpha: float, 
     bal = torch.empty((B, E, T), dtype=torch.float32, device=dev)
     bal_sum = torch.empty((B, E), dtype=torch.float32, device=dev)
     rmap = torch.empty((B, T, 2 * E + 1), dtype=torch.int32, device=dev)
+    src = torch.empty((B, T * topk) if with_src_rows else (0,), dtype=torch.int32, device=dev)
     nbytes = L.lib().uttt_route_tokens_map_workspace_bytes(B, max(T, 1), E, D)
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
     L.call("uttt_route_tokens_map", L.ptr(x), L.dtype_code(x.dtype), L.ptr(R), w_sb, B, T, D, E,
            L.ptr(bias), bias_sb, int(topk), ROUTER_TYPES[router_type],
            COMBINE_MODES[combine_mode], float(alpha), float(router_scale), float(norm_eps),
            L.ptr(mask), L.ptr(gs), L.ptr(comb), L.ptr(bal), L.ptr(bal_sum), L.ptr(rmap),
-           L.ptr(ws), nbytes, L.stream_of(x))
-    return mask, gs, comb, bal, bal_sum, rmap
+           L.ptr(src) if with_src_rows else None, L.ptr(ws), nbytes, L.stream_of(x))
+    return mask, gs, comb, bal, bal_sum, rmap, src
