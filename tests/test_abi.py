@@ -54,3 +54,17 @@ def test_wgrad_pair_split_rule():
     assert q(4, 1, 192, 96, 512) == 0            # 8 K steps per segment: one run
     assert q(1, 1, 64, 64, 64 * 8 * 40) == 32 * 3 * 64 * 64 * 4  # capped at 32 runs
     assert q(0, 1, I, D, 24576) == 0
+
+
+@pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="library not built")
+def test_inverse_row_map_rule_matches_the_library():
+    """routing.src_rows_supported restates uttt_route_tokens_map_src_rows in
+    Python (so torch.compile traces the routed read); both are pure host
+    rules over (T, E)."""
+    from uttt_amd import routing
+    q = _lib.lib().uttt_route_tokens_map_src_rows
+    for T in (1, 15, 16, 17, 2048, 4080, 4096, 4112, 65536):
+        for E in (1, 16, 32, 63, 64, 65, 128):
+            assert routing.src_rows_supported(T, E) == bool(q(T, E)), (T, E)
+    g = _lib.lib().uttt_grouped_gate_up_gathers
+    assert g(4096, 32) == 1 and g(4096, 16) == 1 and g(65536, 16) == 0

@@ -128,8 +128,7 @@ def apply_moe_fast_weights_grouped(x, w0, w1, w2, router_proj_weights, cfg: Rout
     input_dtype = x.dtype
     xt = reshape_head_tokens(x, num_heads)
     w0_w2 = _w0_w2(w0, w2, precomputed_w0_w2)
-    B, T = xt.shape[0], xt.shape[1]
-    E = router_proj_weights.shape[-2]
+    T, E = xt.shape[1], router_proj_weights.shape[-2]
     # Where no gradient flows through the read, the gate/up reads the routed
     # rows of xt through the inverse row map instead of a permuted copy (one
     # launch and the copy's traffic less, identical results)
