@@ -620,6 +620,31 @@ int uttt_dense_gather_heads(const void* const* k_layers, const void* const* v_la
                             const void* const* lr_layers, int lr_dtype, int lr_per_head, int L,
                             int b, int l, int H, int d, void* kh, void* vh, float* lr0,
                             float* lr1, float* lr2, void* stream);
+/* The aggregate write's UPDATE without the per-head copy: stage 1
+ * (uttt_dense_update_stage1) and the weight gradients (uttt_grouped_wgrad_pair,
+ * one expert per head) reading every layer's own k_layers[li], v_layers[li]
+ * [b, l, H*D] bf16 and lr_layers[li] (as uttt_dense_gather_heads takes them;
+ * NULL for no lr) instead of kh, vh, lr0/1/2.  Token li*l + t of head
+ * bb*H + hh is row bb*l + t of layer li at column hh*D, as the gather lays
+ * it out.  The weight gradients split K once per layer (L runs; fp32
+ * partials in the workspace, uttt_dense_wgrad_pair_layers_workspace_bytes,
+ * summed in layer order), so they are bit-identical to the gathered path
+ * wherever its split count is L (configs[1]: 12 layers, 12 runs).  dy, hid
+ * as uttt_dense_update_stage1's outputs [b*H, L*l, 2I] / [b*H, L*l, I].
+ * l must be a multiple of 64 (of 32 for stage 1), L <= 64, pointer arrays
+ * on the host, every tensor 16-byte aligned.  No reference counterpart: the
+ * reference rearranges per layer and loops over the layers (D:370-398,
+ * D:1302-1386). */
+int uttt_dense_update_stage1_layers(const void* const* k_layers, const void* const* v_layers,
+                                    const void* const* lr_layers, int lr_dtype, int lr_per_head,
+                                    int L, int b, int l, int H, int D, int I, const void* packed,
+                                    void* dy, void* hid, void* stream);
+size_t uttt_dense_wgrad_pair_layers_workspace_bytes(int L, int b, int H, int I, int D);
+int uttt_dense_wgrad_pair_layers(const void* dy0_dy2_tok, const void* const* k_layers,
+                                 const void* hidden_tok, const void* const* v_layers, int L,
+                                 int b, int l, int H, int I, int D, void* dw0_w2, void* dw1,
+                                 void* workspace, size_t workspace_bytes, void* stream);
+
 /* Scatter: '(b h) l hd -> b l (h hd)' of the read output (D:261):
  * y [b*H, l, d] bf16 -> out [b, l, H*d] bf16; d % 8 == 0, 16-byte aligned. */
 int uttt_dense_scatter_heads(const void* y, int b, int l, int H, int d, void* out, void* stream);

@@ -284,3 +284,43 @@ def test_bank_owns_its_weights():
     assert not torch.equal(bank.read(q), before)
     fresh = DN.SharedFastWeights(w0, w1, w2, r=r)
     assert torch.equal(bank.read(q), fresh.read(q))
+
+
+@pytest.mark.parametrize("b,H,d,r,L,l,lr_kind", [
+    (1, 4, 192, 2, 12, 2048, "shared_f32"),   # the configs[1] write: 12 layers, 12 K runs
+    (2, 2, 64, 2, 3, 512, "per_head_bf16"),
+    (1, 4, 96, 2, 1, 512, "none"),            # one layer (configs[0]'s shape)
+])
+def test_layered_update_equals_gathered_heads(b, H, d, r, L, l, lr_kind):
+    """The aggregate write's UPDATE read from every layer's own k, v, lr
+    (uttt_dense_update_stage1_layers, uttt_dense_wgrad_pair_layers) equals
+    the per-head copy path (uttt_dense_gather_heads, then stage 1 and the
+    weight gradients) bit for bit at shapes where the copy path's K split is
+    one run per layer."""
+    import torch
+    from uttt_amd import dense as DN
+    from uttt_amd.lact_moe_triton import _grouped as G
+    dh = r * d
+    g = torch.Generator(device="cuda").manual_seed(L * l + d)
+    W02 = (torch.randn(b * H, 1, 2 * dh, d, generator=g, device="cuda") * d ** -0.5).to(torch.bfloat16)
+    W1 = (torch.randn(b * H, 1, d, dh, generator=g, device="cuda") * d ** -0.5).to(torch.bfloat16)
+    ks = [torch.nn.functional.normalize(torch.randn(b, l, H * d, generator=g, device="cuda"), dim=-1)
+          .to(torch.bfloat16) for _ in range(L)]
+    vs = [torch.randn(b, l, H * d, generator=g, device="cuda").to(torch.bfloat16) for _ in range(L)]
+    if lr_kind == "none":
+        lrs = None
+    elif lr_kind == "shared_f32":
+        lrs = [torch.sigmoid(torch.randn(b, l, 3, generator=g, device="cuda")) * 0.1 for _ in range(L)]
+    else:
+        lrs = [(torch.sigmoid(torch.randn(b, l, 3 * H, generator=g, device="cuda")) * 0.1)
+               .to(torch.bfloat16) for _ in range(L)]
+    lay = DN._layered(ks, vs, lrs, H, d, dh)
+    assert lay is not None
+    got = DN._update_layered(W02, W1, lay[0], lay[1], lay[2], b, l, H, None)
+    kh, vh, lr3 = DN._gather_heads(ks, vs, lrs, H)
+    gs = DN._gs(b * H, L * l, kh.device)
+    dy, hl = DN._update_stage1(W02, W1, kh, vh, lr3, gs)
+    ref = G.wgrad_pair(dy, kh, hl, vh, gs)
+    torch.cuda.synchronize()
+    assert torch.equal(got[0], ref[0]) and torch.equal(got[1], ref[1])
+    assert torch.isfinite(got[0].float()).all() and torch.isfinite(got[1].float()).all()

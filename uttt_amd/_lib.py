@@ -99,6 +99,15 @@ SIGNATURES = {
     "uttt_dense_update_stage1": (
         c_int, [c_p, c_p, c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_p, c_p, c_p, c_p],
     ),
+    "uttt_dense_update_stage1_layers": (
+        c_int, [c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_p, c_p,
+                c_p, c_p],
+    ),
+    "uttt_dense_wgrad_pair_layers_workspace_bytes": (c_sz, [c_int, c_int, c_int, c_int, c_int]),
+    "uttt_dense_wgrad_pair_layers": (
+        c_int, [c_p, c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int, c_int, c_p, c_p, c_p, c_sz,
+                c_p],
+    ),
     "uttt_grouped_wgrad_pair": (
         c_int,
         [c_p, c_p, c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int, c_p, c_p, c_p, c_sz, c_p],

@@ -33,6 +33,13 @@ bool launch_rowmap_fused(const uint8_t* mask, int64_t s_b, int64_t s_e, int B, i
                          int nblk_r, float* bal_sum, hipStream_t st, int32_t* src_rows = nullptr,
                          int64_t src_sb = 0);
 
+// Per-layer base pointers passed by value as a kernel argument (the
+// aggregate uTTT-Dense write reads every layer's own k, v, lr tensors).
+constexpr int kMaxLayers = 64;
+struct LayerPtrs {
+  const void* p[kMaxLayers];
+};
+
 #define UTTT_REQUIRE(cond, ...)          \
   do {                                   \
     if (!(cond)) {                       \

@@ -30,12 +30,7 @@
 namespace uttt {
 namespace {
 
-constexpr int kMaxLayers = 64;
 constexpr int kHeadThreads = 256;
-
-struct LayerPtrs {
-  const void* p[kMaxLayers];
-};
 
 typedef uint32_t nt_u32x4 __attribute__((ext_vector_type(4)));
 

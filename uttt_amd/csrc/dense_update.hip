@@ -95,15 +95,26 @@ __device__ __forceinline__ void store16(uint16_t* p, const float* f) {
   *reinterpret_cast<uint4*>(p) = v;
 }
 
+// The layers' own inputs (LAYERED): token t of head bh = bb * H + hh is row
+// bb * l + t % l of layer t / l, at column hh * D of that layer's [b, l, H*D]
+// k and v; its lr is entry j of the layer's [b, l, 3] lr (lr_per_head: entry
+// 3 hh + j of [b, l, 3H]), fp32 or bf16 (LR), no lr at all when lr.p[0] is
+// null.  The gathered-head layout ([BH, N, D] k, v and fp32 lr [BH, N])
+// holds the same values, so both give the same bits.
+struct S1Layers {
+  LayerPtrs k, v, lr;
+  int l, H, lr_per_head;
+};
+
 // PIPE: two register sets of weight fragments, block b + 1's loads in flight
 // while block b is multiplied and its epilogue runs (the last prefetch
 // re-reads the last block: unconditional loads keep the wait counts exact).
 // It needs 2 x 3 D/16 fragments of registers: D <= 192 only.
-template <int D, bool PIPE>
+template <int D, bool PIPE, class LR, bool LAYERED>
 __global__ __launch_bounds__(kUpdWaves * 64) void dense_update_s1_kernel(
     const uint16_t* __restrict__ kh, const uint16_t* __restrict__ vh,
     const float* __restrict__ lr0, const float* __restrict__ lr1, const float* __restrict__ lr2,
-    int N, int I, const uint16_t* __restrict__ packed, uint16_t* __restrict__ dy,
+    S1Layers ly, int N, int I, const uint16_t* __restrict__ packed, uint16_t* __restrict__ dy,
     uint16_t* __restrict__ hid) {
   constexpr int KS = D / 16;
   const int bh = blockIdx.y;
@@ -111,20 +122,50 @@ __global__ __launch_bounds__(kUpdWaves * 64) void dense_update_s1_kernel(
   const int r = lane & 31, g = lane >> 5;
   const int t = blockIdx.x * kUpdTok + 32 * w + r;
   const bool valid = t < N;
-  const int64_t row = (int64_t)bh * N + min(t, N - 1);  // clamped: always a valid address
+  const int tc = min(t, N - 1);  // clamped: always a valid address
+  const int64_t row = (int64_t)bh * N + tc;
 
   // k^T / v^T fragments of this lane's token, k = 16 s + 8 g .. + 8
   bf16x8_t kf[KS], vf[KS];
+  float l0 = 1.0f, l1 = 1.0f, l2 = 1.0f;
+  if constexpr (LAYERED) {
+    // a wave's 32 tokens lie in one layer (l is a multiple of 32)
+    const int li = __builtin_amdgcn_readfirstlane(tc / ly.l);
+    const int bb = bh / ly.H, hh = bh - bb * ly.H;
+    const int64_t tr = (int64_t)bb * ly.l + (tc - li * ly.l);  // row of the layer's tensors
+    const uint16_t* kp = static_cast<const uint16_t*>(ly.k.p[li]) + (tr * ly.H + hh) * D;
+    const uint16_t* vp = static_cast<const uint16_t*>(ly.v.p[li]) + (tr * ly.H + hh) * D;
 #pragma unroll
-  for (int s = 0; s < KS; ++s) {
-    kf[s] = ld16(kh + row * D + 16 * s + 8 * g);
-    vf[s] = ld16(vh + row * D + 16 * s + 8 * g);
+    for (int s = 0; s < KS; ++s) {
+      kf[s] = ld16(kp + 16 * s + 8 * g);
+      vf[s] = ld16(vp + 16 * s + 8 * g);
+    }
+    using S = typename LR::S;
+    const bool has = ly.lr.p[0] != nullptr;
+    // a missing lr reads the first k element (a valid address) and is ignored
+    const S* lp = has ? static_cast<const S*>(ly.lr.p[li]) +
+                            tr * (ly.lr_per_head ? 3 * ly.H : 3) + (ly.lr_per_head ? 3 * hh : 0)
+                      : reinterpret_cast<const S*>(kp);
+    const S a = lp[0], b = lp[has ? 1 : 0], c = lp[has ? 2 : 0];
+    if (has) {
+      l0 = LR::load(a);
+      l1 = LR::load(b);
+      l2 = LR::load(c);
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      kf[s] = ld16(kh + row * D + 16 * s + 8 * g);
+      vf[s] = ld16(vh + row * D + 16 * s + 8 * g);
+    }
+    // a missing lr reads the first k element (a valid address) and is ignored
+    const float* fb = reinterpret_cast<const float*>(kh);
+    const float l0r = *(lr0 ? lr0 + row : fb), l1r = *(lr1 ? lr1 + row : fb),
+                l2r = *(lr2 ? lr2 + row : fb);
+    l0 = lr0 ? l0r : 1.0f;
+    l1 = lr1 ? l1r : 1.0f;
+    l2 = lr2 ? l2r : 1.0f;
   }
-  // a missing lr reads the first k element (a valid address) and is ignored
-  const float* fb = reinterpret_cast<const float*>(kh);
-  const float l0r = *(lr0 ? lr0 + row : fb), l1r = *(lr1 ? lr1 + row : fb),
-              l2r = *(lr2 ? lr2 + row : fb);
-  const float l0 = lr0 ? l0r : 1.0f, l1 = lr1 ? l1r : 1.0f, l2 = lr2 ? l2r : 1.0f;
 
   const uint16_t* ph = packed + (int64_t)bh * 3 * I * D + lane * 8;
   const int64_t part = (int64_t)I * D;
@@ -193,13 +234,13 @@ __global__ __launch_bounds__(kUpdWaves * 64) void dense_update_s1_kernel(
   }
 }
 
-template <int D>
+template <int D, class LR = F32T, bool LAYERED = false>
 void launch_update_s1(int BH, int N, int I, hipStream_t st, const uint16_t* k, const uint16_t* v,
                       const float* a, const float* b, const float* c, const uint16_t* p,
-                      uint16_t* o, uint16_t* h) {
+                      uint16_t* o, uint16_t* h, const S1Layers& ly = S1Layers{}) {
   const dim3 grid((unsigned)((N + kUpdTok - 1) / kUpdTok), (unsigned)BH);
-  hipLaunchKernelGGL((dense_update_s1_kernel<D, (D <= 192)>), grid, dim3(kUpdWaves * 64), 0, st,
-                     k, v, a, b, c, N, I, p, o, h);
+  hipLaunchKernelGGL((dense_update_s1_kernel<D, (D <= 192), LR, LAYERED>), grid,
+                     dim3(kUpdWaves * 64), 0, st, k, v, a, b, c, ly, N, I, p, o, h);
 }
 
 }  // namespace
@@ -263,4 +304,55 @@ extern "C" int uttt_dense_update_stage1(const void* kh, const void* vh, const vo
     default: launch_update_s1<256>(BH, N, I, st, k, v, a, b, c, p, o, h); break;
   }
   return check_launch("dense_update_stage1");
+}
+
+extern "C" int uttt_dense_update_stage1_layers(const void* const* k_layers,
+                                               const void* const* v_layers,
+                                               const void* const* lr_layers, int lr_dtype,
+                                               int lr_per_head, int L, int b, int l, int H, int D,
+                                               int I, const void* packed, void* dy, void* hid,
+                                               void* stream) {
+  UTTT_REQUIRE(L >= 0 && L <= kMaxLayers && b >= 0 && l >= 0 && H >= 1,
+               "dense_update_stage1_layers: bad sizes (L=%d must be at most %d)", L, kMaxLayers);
+  UTTT_REQUIRE(uttt_dense_update_supported(D, I),
+               "dense_update_stage1_layers: D=%d must be 64, 96, 128, 192 or 256 and I=%d a "
+               "multiple of 32 in [32, 512]", D, I);
+  if (L == 0 || b == 0 || l == 0) return UTTT_OK;
+  UTTT_REQUIRE(l % 32 == 0, "dense_update_stage1_layers: l=%d must be a multiple of 32", l);
+  const int BH = b * H;
+  const int64_t N = (int64_t)L * l;
+  UTTT_REQUIRE(BH <= 65535 && N < ((int64_t)1 << 31) && (int64_t)b * l * H * D < ((int64_t)1 << 40),
+               "dense_update_stage1_layers: sizes too large");
+  UTTT_REQUIRE(k_layers && v_layers && packed && dy && hid,
+               "dense_update_stage1_layers: null pointer");
+  UTTT_REQUIRE(aligned16(packed) && aligned16(dy) && aligned16(hid),
+               "dense_update_stage1_layers: packed, dy and hid must be 16-byte aligned");
+  S1Layers ly{};
+  ly.l = l;
+  ly.H = H;
+  ly.lr_per_head = lr_per_head ? 1 : 0;
+  for (int i = 0; i < L; ++i) {
+    UTTT_REQUIRE(k_layers[i] && v_layers[i] && aligned16(k_layers[i]) && aligned16(v_layers[i]),
+                 "dense_update_stage1_layers: layer %d's k and v must be 16-byte aligned", i);
+    ly.k.p[i] = k_layers[i];
+    ly.v.p[i] = v_layers[i];
+    ly.lr.p[i] = lr_layers ? lr_layers[i] : nullptr;
+    UTTT_REQUIRE(lr_layers == nullptr || lr_layers[i] != nullptr,
+                 "dense_update_stage1_layers: null lr of layer %d", i);
+  }
+  hipStream_t st = as_stream(stream);
+  const auto* p = static_cast<const uint16_t*>(packed);
+  auto* o = static_cast<uint16_t*>(dy);
+  auto* h = static_cast<uint16_t*>(hid);
+  const int n = (int)N;
+  UTTT_DTYPE_SWITCH_LR(lr_dtype, LR, {
+    switch (D) {
+      case 64: launch_update_s1<64, LR, true>(BH, n, I, st, nullptr, nullptr, nullptr, nullptr, nullptr, p, o, h, ly); break;
+      case 96: launch_update_s1<96, LR, true>(BH, n, I, st, nullptr, nullptr, nullptr, nullptr, nullptr, p, o, h, ly); break;
+      case 128: launch_update_s1<128, LR, true>(BH, n, I, st, nullptr, nullptr, nullptr, nullptr, nullptr, p, o, h, ly); break;
+      case 192: launch_update_s1<192, LR, true>(BH, n, I, st, nullptr, nullptr, nullptr, nullptr, nullptr, p, o, h, ly); break;
+      default: launch_update_s1<256, LR, true>(BH, n, I, st, nullptr, nullptr, nullptr, nullptr, nullptr, p, o, h, ly); break;
+    }
+  });
+  return check_launch("dense_update_stage1_layers");
 }

@@ -1217,12 +1217,23 @@ struct WgTask {
   int y_tiles, x_tiles;
 };
 
+// The uTTT-Dense aggregate write's token operands straight from every
+// layer's own tensors (LAYERED): one expert per batch (head) bh = bb * H + hh
+// with all N = L * l tokens, split K once per layer (run = l, a multiple of
+// kBK), and run li reads task 0's P (k) and task 1's Q (v) as layer li's
+// [b, l, H*D] rows bb * l .. + l at column hh * D (row stride H * D).
+struct WgLayers {
+  LayerPtrs k, v;
+  int l, H, D;
+};
+
 // SPLIT: fp32 partials (the two epilogues in one kernel do not fit the
 // register file: each alone does)
-template <bool SPLIT, int NA>
+template <bool SPLIT, int NA, bool LAYERED = false>
 __global__ __launch_bounds__(kThreadsOf<NA>) void wg_kernel(WgTask t0, WgTask t1,
                                                       const int32_t* __restrict__ gs, int E,
-                                                      int N, int BE, int splits) {
+                                                      int N, int BE, int splits,
+                                                      WgLayers ly) {
   __shared__ __attribute__((aligned(16))) uint8_t st0[kStageBytes];
   __shared__ __attribute__((aligned(16))) uint8_t st1[kStageBytes];
 
@@ -1241,14 +1252,29 @@ __global__ __launch_bounds__(kThreadsOf<NA>) void wg_kernel(WgTask t0, WgTask t1
   const int X = tk.X, Y = tk.Y;
 
   int start, size;
-  expert_segment(gs + (int64_t)b * E, e, N, &start, &size);
+  if constexpr (LAYERED) {
+    start = 0;  // the head's whole token axis (group sizes are not read)
+    size = N;
+  } else {
+    expert_segment(gs + (int64_t)b * E, e, N, &start, &size);
+  }
   // this split's run of the segment: whole K steps, the last run may be short or empty
   const int run = ((size + kBK - 1) / kBK + splits - 1) / splits * kBK;
   const int lo = min(size, split * run);
   size = min(size - lo, run);
   start += lo;
-  const Operand P{tk.p + ((int64_t)b * N + start) * Y, Y, Y, size};
-  const Operand Q{tk.q + ((int64_t)b * N + start) * X, X, X, size};
+  Operand P{tk.p + ((int64_t)b * N + start) * Y, Y, Y, size};
+  Operand Q{tk.q + ((int64_t)b * N + start) * X, X, X, size};
+  if constexpr (LAYERED) {
+    // run == l: this split is layer `split`, its first token row bb * l
+    const int bb = b / ly.H, hh = b - bb * ly.H;
+    const int64_t off = (int64_t)bb * ly.l * ly.H * ly.D + (int64_t)hh * ly.D;
+    const int64_t ld = (int64_t)ly.H * ly.D;
+    if (first)
+      P = Operand{static_cast<const uint16_t*>(ly.k.p[split]) + off, ld, Y, size};
+    else
+      Q = Operand{static_cast<const uint16_t*>(ly.v.p[split]) + off, ld, X, size};
+  }
 
   f32x16 acc0[NA][kNB], acc1[NA][kNB];
   zero(acc0);
@@ -1785,7 +1811,8 @@ size_t wg_part_bytes(const WgTask& t0, const WgTask& t1, int B, int E, int split
 
 // splits = 1: one pass, bf16 stores, no workspace
 int launch_wg(WgTask t0, WgTask t1, const int32_t* gs, int B, int E, int N, int splits,
-              void* workspace, size_t workspace_bytes, hipStream_t st, const char* what) {
+              void* workspace, size_t workspace_bytes, hipStream_t st, const char* what,
+              const WgLayers* ly = nullptr) {
   const int64_t per = (int64_t)t0.y_tiles * t0.x_tiles + (int64_t)t1.y_tiles * t1.x_tiles;
   const int64_t blocks = per * E * B * splits;
   if (blocks == 0) return UTTT_OK;
@@ -1804,18 +1831,25 @@ int launch_wg(WgTask t0, WgTask t1, const int32_t* gs, int B, int E, int N, int 
   UTTT_REQUIRE(splits > 1 || (aligned16(t0.out) && (t1.y_tiles * t1.x_tiles == 0 || aligned16(t1.out))),
                "%s: outputs must be 16-byte aligned", what);
   const bool eight = pick_na(kDefaultWgNA) == 1;
-  if (splits == 1 && eight)
+  if (ly != nullptr) {  // the layered operands (four waves)
+    if (splits == 1)
+      hipLaunchKernelGGL((wg_kernel<false, 2, true>), dim3((unsigned)blocks),
+                         dim3(kThreadsOf<2>), 0, st, t0, t1, gs, E, N, B * E, 1, *ly);
+    else
+      hipLaunchKernelGGL((wg_kernel<true, 2, true>), dim3((unsigned)blocks), dim3(kThreadsOf<2>),
+                         0, st, t0, t1, gs, E, N, B * E, splits, *ly);
+  } else if (splits == 1 && eight)
     hipLaunchKernelGGL((wg_kernel<false, 1>), dim3((unsigned)blocks), dim3(kThreadsOf<1>), 0, st,
-                       t0, t1, gs, E, N, B * E, 1);
+                       t0, t1, gs, E, N, B * E, 1, WgLayers{});
   else if (splits == 1)
     hipLaunchKernelGGL((wg_kernel<false, 2>), dim3((unsigned)blocks), dim3(kThreadsOf<2>), 0, st,
-                       t0, t1, gs, E, N, B * E, 1);
+                       t0, t1, gs, E, N, B * E, 1, WgLayers{});
   else if (eight)
     hipLaunchKernelGGL((wg_kernel<true, 1>), dim3((unsigned)blocks), dim3(kThreadsOf<1>), 0, st,
-                       t0, t1, gs, E, N, B * E, splits);
+                       t0, t1, gs, E, N, B * E, splits, WgLayers{});
   else
     hipLaunchKernelGGL((wg_kernel<true, 2>), dim3((unsigned)blocks), dim3(kThreadsOf<2>), 0, st,
-                       t0, t1, gs, E, N, B * E, splits);
+                       t0, t1, gs, E, N, B * E, splits, WgLayers{});
   if (int rc = check_launch(what)) return rc;
   if (splits == 1) return UTTT_OK;
   const int64_t n0 = (int64_t)B * E * t0.X * t0.Y, n1 = (int64_t)B * E * t1.X * t1.Y;
@@ -2053,6 +2087,51 @@ extern "C" int uttt_grouped_wgrad_pair(const void* dy0_dy2_tok, const void* k,
   const WgTask t1 = wg_task(hidden_tok, v, dw1, D, I);
   return launch_wg(t0, t1, group_sizes, B, E, N, wg_splits(t0, t1, B, E, N), workspace,
                    workspace_bytes, as_stream(stream), "grouped_wgrad_pair");
+}
+
+extern "C" size_t uttt_dense_wgrad_pair_layers_workspace_bytes(int L, int b, int H, int I,
+                                                              int D) {
+  if (L <= 1 || b <= 0 || H <= 0 || I <= 0 || D <= 0) return 0;
+  const WgTask t0 = wg_task(nullptr, nullptr, nullptr, 2 * I, D);
+  const WgTask t1 = wg_task(nullptr, nullptr, nullptr, D, I);
+  size_t off1;
+  return wg_part_bytes(t0, t1, b * H, 1, L, &off1);
+}
+
+extern "C" int uttt_dense_wgrad_pair_layers(const void* dy0_dy2_tok, const void* const* k_layers,
+                                            const void* hidden_tok, const void* const* v_layers,
+                                            int L, int b, int l, int H, int I, int D,
+                                            void* dw0_w2, void* dw1, void* workspace,
+                                            size_t workspace_bytes, void* stream) {
+  UTTT_REQUIRE(L >= 0 && L <= kMaxLayers && b >= 0 && l >= 0 && H >= 1 && I >= 0 && D >= 0,
+               "dense_wgrad_pair_layers: bad sizes (L=%d must be at most %d)", L, kMaxLayers);
+  UTTT_REQUIRE(I % 8 == 0 && D % 8 == 0,
+               "dense_wgrad_pair_layers: I=%d and D=%d must be multiples of 8", I, D);
+  if (L == 0 || b == 0 || l == 0 || I == 0 || D == 0) return UTTT_OK;
+  UTTT_REQUIRE(l % kBK == 0, "dense_wgrad_pair_layers: l=%d must be a multiple of %d", l, kBK);
+  const int64_t N = (int64_t)L * l;
+  UTTT_REQUIRE(N < ((int64_t)1 << 30) && (int64_t)H * D < (1 << 23),
+               "dense_wgrad_pair_layers: sizes too large");
+  UTTT_REQUIRE(dy0_dy2_tok && k_layers && hidden_tok && v_layers && dw0_w2 && dw1,
+               "dense_wgrad_pair_layers: null pointer");
+  UTTT_REQUIRE(aligned16(dy0_dy2_tok) && aligned16(hidden_tok) && aligned16(dw0_w2) &&
+                   aligned16(dw1),
+               "dense_wgrad_pair_layers: tensors must be 16-byte aligned");
+  WgLayers ly{};
+  ly.l = l;
+  ly.H = H;
+  ly.D = D;
+  for (int i = 0; i < L; ++i) {
+    UTTT_REQUIRE(k_layers[i] && v_layers[i] && aligned16(k_layers[i]) && aligned16(v_layers[i]),
+                 "dense_wgrad_pair_layers: layer %d's k and v must be 16-byte aligned", i);
+    ly.k.p[i] = k_layers[i];
+    ly.v.p[i] = v_layers[i];
+  }
+  // dW0_W2 [2I][D] = DY^T K;  dW1 [D][I] = V^T Hid; one K run per layer
+  const WgTask t0 = wg_task(nullptr, dy0_dy2_tok, dw0_w2, 2 * I, D);
+  const WgTask t1 = wg_task(hidden_tok, nullptr, dw1, D, I);
+  return launch_wg(t0, t1, nullptr, b * H, 1, (int)N, L, workspace, workspace_bytes,
+                   as_stream(stream), "dense_wgrad_pair_layers", &ly);
 }
 
 extern "C" int uttt_grouped_wgrad(const void* a_tok, const void* b_tok,

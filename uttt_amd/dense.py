@@ -192,10 +192,66 @@ def _update_stage1(W02, W1, kh, vh, lr3, gs, upacked=None):
     return dy, hl
 
 
+def _layered(ks, vs, lrs, H, d, dh):
+    """The layers' own k, v (bf16 [b, l, H*d], 16-byte aligned) and lr for
+    the layered UPDATE (no per-head copy), or None where it does not apply:
+    the fused stage 1's head sizes, l a multiple of 64, at most 64 layers."""
+    n = len(ks)
+    if not (1 <= n <= 64 and vs is not None and len(vs) == n
+            and L.lib().uttt_dense_update_supported(d, dh)):
+        return None
+    ks = [_bf16_rows(k) for k in ks]
+    vs = [_bf16_rows(v) for v in vs]
+    b, l, hd = ks[0].shape
+    if l % 64 or hd != H * d or any(t.shape != (b, l, hd) for t in ks + vs):
+        return None
+    if any(t.data_ptr() % 16 for t in ks + vs):
+        return None
+    if lrs is not None:
+        lrs = [lr.contiguous() for lr in lrs]
+        if any(lr.dtype != lrs[0].dtype or lr.shape not in ((b, l, 3), (b, l, 3 * H))
+               or lr.shape != lrs[0].shape for lr in lrs):
+            return None
+    return ks, vs, lrs, b, l
+
+
+def _update_layered(W02, W1, ks, vs, lrs, b, l, H, upacked):
+    """The UPDATE of several layers straight from each layer's own k, v, lr
+    (uttt_dense_update_stage1_layers, uttt_dense_wgrad_pair_layers): the same
+    products as the per-head copy path, the weight gradients split into one K
+    run per layer."""
+    d, dh = W1.shape[-2], W1.shape[-1]
+    n, BH, N = len(ks), b * H, len(ks) * l
+    dev = ks[0].device
+    upacked = _pack_update(W02, W1, upacked)
+    arr = lambda ts: (ctypes.c_void_p * n)(*[t.data_ptr() for t in ts])
+    dy = torch.empty((BH, N, 2 * dh), dtype=torch.bfloat16, device=dev)
+    hl = torch.empty((BH, N, dh), dtype=torch.bfloat16, device=dev)
+    per_head = int(lrs is not None and lrs[0].shape[2] != 3)
+    code = L.dtype_code(lrs[0].dtype) if lrs is not None else L.F32
+    st = L.stream_of(dy)
+    L.call("uttt_dense_update_stage1_layers", arr(ks), arr(vs), arr(lrs) if lrs else None, code,
+           per_head, n, b, l, H, d, dh, L.ptr(upacked), L.ptr(dy), L.ptr(hl), st)
+    dW02 = torch.empty((BH, 1, 2 * dh, d), dtype=torch.bfloat16, device=dev)
+    dW1 = torch.empty((BH, 1, d, dh), dtype=torch.bfloat16, device=dev)
+    nws = L.lib().uttt_dense_wgrad_pair_layers_workspace_bytes(n, b, H, dh, d)
+    ws = torch.empty(max(nws, 1), dtype=torch.uint8, device=dev)
+    L.call("uttt_dense_wgrad_pair_layers", L.ptr(dy), arr(ks), L.ptr(hl), arr(vs), n, b, l, H,
+           dh, d, L.ptr(dW02), L.ptr(dW1), L.ptr(ws), nws, st)
+    return dW02, dW1
+
+
 def _update(W02, W1, ks, vs, lrs, b, H, upacked=None):
     """The UPDATE of several layers' tokens at once: per head the tokens of
     all layers concatenated.  Returns bf16 (dW0_W2, dW1).  upacked: a buffer
-    of BH * 3 * d_h * d bf16 for the fused stage 1's weight copy."""
+    of BH * 3 * d_h * d bf16 for the fused stage 1's weight copy.  Where the
+    fused stage 1 applies and each layer's l is a multiple of 64, the kernels
+    read every layer's own k, v and lr (no per-head copy)."""
+    lay = _layered(ks, vs, lrs, H, W1.shape[-2], W1.shape[-1])
+    if lay is not None:
+        ks_, vs_, lrs_, b_, l_ = lay
+        assert b_ == b
+        return _update_layered(W02, W1, ks_, vs_, lrs_, b, l_, H, upacked)
     kh, vh, lr3 = _gather_heads(ks, vs, lrs, H)
     gs = _gs(b * H, kh.shape[1], kh.device)
     dy, hl = _update_stage1(W02, W1, kh, vh, lr3, gs, upacked)
