@@ -753,7 +753,7 @@ struct EpiBwdSaved {
     TokenLrs<LR> lrs;
     lrs.load(c, ea.N, ea.lr0, ea.lr1, ea.lr2, ea.lr0);
     auto start = [&]() __attribute__((always_inline)) { lrs.write(c, true, true, true); };
-    staged_epilogue_ahead(acc0, acc1, c, fetch, [&](int nl, int n, int g, const Raw& rw) __attribute__((always_inline)) {
+    auto use = [&](int nl, int n, int g, const Raw& rw) __attribute__((always_inline)) {
       const int m = c.m0 + 8 * g;
       const bool ok = c.tt.n0 + n < c.tt.size && m < I;
       const int tok = c.tt.start + c.tt.n0 + n;
@@ -807,7 +807,18 @@ struct EpiBwdSaved {
         ea.lr_part[plane + o] = s1;
         ea.lr_part[2 * plane + o] = s2;
       }
-    }, start);
+    };
+    // Four waves fetch one quarter ahead (two quarters of inputs in
+    // registers); eight waves have half the registers per thread and fetch
+    // each quarter just before staging it (one quarter in registers: the
+    // double buffer spills there).
+    if constexpr (NA == 2) {
+      staged_epilogue_ahead(acc0, acc1, c, fetch, use, start);
+    } else {
+      block_barrier();  // every wave is done reading the stage buffers
+      start();
+      staged_epilogue_prefetch(acc0, acc1, c, fetch, use);
+    }
   }
 };
 
@@ -1601,20 +1612,21 @@ static_assert(kSkippable<KMajor, EpiSwiGLU> <= EpiSwiGLU::kStaleColumnsUnused &&
 // uttt_debug_set_gemm_layout forces one process-wide (tests run both).
 // Measured at the 760M batched-update shapes (interleaved runs, per launch):
 // the staged bf16 stores (GD and grad_K, row-major A: 2279 -> 2185-2207 us;
-// grad_V: 1720 / 1722 us) take eight waves; the weight gradients
-// (2393-2408 against 2440-2448 us) and the rest (stage 1 2358 / 2346-2351,
-// DH 1057-1060 / 1054-1068) keep four.
+// grad_V: 1720 / 1722 us) and the saved-tensor backward epilogue (bf16 lr:
+// 2845-2849 against 2719-2735 us, its inputs fetched per quarter) take eight
+// waves; the weight gradients (2393-2408 against 2440-2448 us) and the rest
+// (stage 1 2358 / 2346-2351, DH 1057-1060 / 1054-1068) keep four.
 template <class Epi>
 constexpr int kDefaultNA = 2;
 template <>
 constexpr int kDefaultNA<EpiStore<uint16_t, true>> = 1;
+template <>
+constexpr int kDefaultNA<EpiBwdSaved<BF16T>> = 1;
 constexpr int kDefaultWgNA = 2;
-// Epilogues whose eight-wave kernel would spill (the saved-tensor backward
-// epilogue holds four 8-element inputs per item): four waves only.
+// Epilogues with an eight-wave kernel (every one here; a family without one
+// would set this false and launch four waves under a forced layout too).
 template <class Epi>
 constexpr bool kHasNA1 = true;
-template <class LR>
-constexpr bool kHasNA1<EpiBwdSaved<LR>> = false;
 int g_gemm_na = 0;  // 0: each family's default
 int pick_na(int def) { return g_gemm_na != 0 ? g_gemm_na : def; }
 
