@@ -341,6 +341,12 @@ def norm_symbol(name):
             cut = i
             break
     s = s[:cut].strip()
+    # wg_kernel<SPLIT, layout, LAYERED>: the plain weight gradients keep the
+    # name 'wg_kernel<SPLIT>' whichever layout they run, the per-layer-operand
+    # form becomes 'wg_kernel<SPLIT, layered>'
+    m = re.match(r"^wg_kernel<(\w+), [12], (true|false)>$", s)
+    if m:
+        return f"wg_kernel<{m.group(1)}{', layered' if m.group(2) == 'true' else ''}>"
     # the GEMM kernels' last template argument is the wave layout (4 or 8
     # waves): one symbol per product family whichever layout it runs
     return re.sub(r"^((?:tn|wg)_kernel<.*), [12]>$", r"\1>", s)
