@@ -447,6 +447,12 @@ int uttt_debug_set_apply_path(int path);
  * results are identical.  Returns the previous value. */
 int uttt_debug_set_gemm_layout(int na);
 
+/* Test hook (no reference counterpart): which path uttt_newton_schulz5 takes.
+ * 0: by the sizes (one launch for the small matrices it covers), 1: always
+ * the multi-launch path.  Both give identical results.  Returns the previous
+ * value. */
+int uttt_debug_set_ns_path(int path);
+
 /* WRITE step of the fast weights.  Replaces the write of
  * _apply_moe_update_dense (uttt_llm/flame/custom_models/uttt_moe/
  * modeling_recurrent_lact.py:754-825; seg = C, norm_from_fast = 0,
@@ -522,7 +528,11 @@ int uttt_momentum_add(const void* raw, int raw_dtype, const float* mom, const fl
  * out = bf16(X * out_scale) [BE, rows, cols] bf16 (out_scale = the write's
  * step size, which the reference applies to the bf16 result; 1 leaves X).
  * rows and cols must be multiples of 8; the workspace is
- * uttt_newton_schulz5_workspace_bytes(BE, rows, cols) bytes. */
+ * uttt_newton_schulz5_workspace_bytes(BE, rows, cols) bytes.  Matrices whose
+ * sides are multiples of 32 with min * (max + 8) <= 38400 (the uTTT-Dense
+ * d x d slices up to d = 192) and a 16-byte aligned g run in one launch, one
+ * workgroup per matrix with the whole computation in LDS, with the same
+ * result bits as the multi-launch path (the workspace is then unused). */
 size_t uttt_newton_schulz5_workspace_bytes(int BE, int rows, int cols);
 int uttt_newton_schulz5(const void* g, int g_dtype, int BE, int rows, int cols, float out_scale,
                         void* out, void* workspace, size_t workspace_bytes, void* stream);

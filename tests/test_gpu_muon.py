@@ -74,6 +74,52 @@ def test_newton_schulz5_matches_oracle(n, R, C, dtype, scale):
     assert _rel(ours, exact) <= 1.5 * _rel(ref, exact) + 1e-3, (_rel(ours, exact), _rel(ref, exact))
 
 
+def _ns5_kernels(run):
+    """Names of the device kernels that run() launches."""
+    from torch.profiler import ProfilerActivity, profile
+
+    with profile(activities=[ProfilerActivity.CUDA]) as prof:
+        run()
+        torch.cuda.synchronize()
+    return {e.name for e in prof.events() if e.device_type == torch.autograd.DeviceType.CUDA}
+
+
+@pytest.mark.parametrize("n,R,C,dtype,scale", [
+    (16, 192, 192, torch.float32, 1.0),    # the uTTT-Dense 124M w0 / w2 slices
+    (8, 192, 192, torch.bfloat16, 0.5),
+    (4, 96, 96, torch.float32, 1.0),       # configs[0]'s d = 96 slices
+    (3, 64, 128, torch.float32, 1.0),      # wide
+    (3, 192, 96, torch.float32, 0.7),      # tall: X = G^T
+    (2, 32, 192, torch.bfloat16, 1.0),     # one row block
+    (5, 160, 128, torch.float32, 1.0),     # tall, 5 x 4 blocks: uneven wave grid
+])
+def test_one_launch_newton_schulz_equals_multi_launch(n, R, C, dtype, scale):
+    """Matrices with both sides multiples of 32 and at most 192 run the whole
+    iteration in one launch (csrc/ns_small.hip); its result is the
+    multi-launch path's bit for bit (same rounding points, same MFMA
+    accumulation order), and the oracle's at the Newton-Schulz bar."""
+    from uttt_amd import _lib as L
+
+    G = _rand((n, R, C), 7 * R + C).to(dtype).to(DEV)
+    prev = L.lib().uttt_debug_set_ns_path(1)
+    try:
+        multi = FWW.newton_schulz5(G, scale)
+        names_multi = _ns5_kernels(lambda: FWW.newton_schulz5(G, scale))
+    finally:
+        L.lib().uttt_debug_set_ns_path(prev)
+    L.lib().uttt_debug_set_ns_path(0)
+    try:
+        one = FWW.newton_schulz5(G, scale)
+        names_one = _ns5_kernels(lambda: FWW.newton_schulz5(G, scale))
+    finally:
+        L.lib().uttt_debug_set_ns_path(prev)
+    assert any("ns_small_kernel" in k for k in names_one), names_one
+    assert not any("ns_small_kernel" in k for k in names_multi), names_multi
+    assert torch.equal(one, multi), (one.float() - multi.float()).abs().max().item()
+    ref = OW.newton_schulz5(G.cpu()) * scale
+    assert _rel(one.cpu(), ref) <= 1e-2, _rel(one.cpu(), ref)
+
+
 def _gpu_ns5(G):
     """The device Newton-Schulz on the oracle's own input, for the oracle's
     write to consume: isolates the write arithmetic from the iteration's

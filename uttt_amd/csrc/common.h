@@ -33,6 +33,13 @@ bool launch_rowmap_fused(const uint8_t* mask, int64_t s_b, int64_t s_e, int B, i
                          int nblk_r, float* bal_sum, hipStream_t st, int32_t* src_rows = nullptr,
                          int64_t src_sb = 0);
 
+// Newton-Schulz of BE small matrices [rows, cols] in one launch (one
+// workgroup per matrix, the whole computation in LDS; ns_small.hip), for the
+// shapes ns_small_fits accepts; g fp32 or bf16 (g_dtype), 16-byte aligned.
+bool ns_small_fits(int rows, int cols);
+int launch_ns_small(const void* g, int g_dtype, int BE, int rows, int cols, float scale,
+                    uint16_t* out, hipStream_t st);
+
 // Per-layer base pointers passed by value as a kernel argument (the
 // aggregate uTTT-Dense write reads every layer's own k, v, lr tensors).
 constexpr int kMaxLayers = 64;

@@ -1628,6 +1628,7 @@ constexpr int kDefaultWgNA = 2;
 template <class Epi>
 constexpr bool kHasNA1 = true;
 int g_gemm_na = 0;  // 0: each family's default
+int g_ns_path = 0;  // uttt_newton_schulz5: 0 by the sizes, 1 always the multi-launch path
 int pick_na(int def) { return g_gemm_na != 0 ? g_gemm_na : def; }
 
 template <int AMAJ, class Epi, bool SKIP, int NA>
@@ -2001,6 +2002,13 @@ extern "C" int uttt_debug_set_apply_path(int path) {
   const int prev = g_apply_path;
   g_apply_path = path < 0 ? -1 : path > 0 ? 1 : 0;
   g_apply_down_two = path == 2;
+  return prev;
+}
+
+extern "C" int uttt_debug_set_ns_path(int path) {
+  UTTT_REQUIRE(path == 0 || path == 1, "debug_set_ns_path: path=%d (0 or 1)", path);
+  const int prev = g_ns_path;
+  g_ns_path = path;
   return prev;
 }
 
@@ -2394,6 +2402,9 @@ extern "C" int uttt_newton_schulz5(const void* g, int g_dtype, int BE, int rows,
   UTTT_REQUIRE(workspace_bytes >= w.total, "newton_schulz5: workspace %zu < %zu bytes",
                workspace_bytes, w.total);
   hipStream_t st = as_stream(stream);
+  if (g_ns_path == 0 && aligned16(g) && ns_small_fits(rows, cols))
+    return launch_ns_small(g, g_dtype, BE, rows, cols, out_scale, static_cast<uint16_t*>(out),
+                           st);
   uint8_t* wb = static_cast<uint8_t*>(workspace);
   int32_t* gs = reinterpret_cast<int32_t*>(wb + w.gs);
   float* denom = reinterpret_cast<float*>(wb + w.denom);

@@ -353,9 +353,12 @@ class SharedFastWeights:
         from .fast_weight_write import newton_schulz5
 
         B, d, r = self.b * self.H, self.d, self.r
-        s02 = newton_schulz5(g02.reshape(B * 2 * r, d, d), scale).reshape(B, 1, 2 * r * d, d)
+        # every slice is orthogonalised on its own, so the w0 / w2 and the w1
+        # slices go through one call (one launch where the slices are small)
         sl1 = g1.reshape(B, d, r, d).permute(0, 2, 1, 3).reshape(B * r, d, d)
-        s1 = newton_schulz5(sl1, scale).reshape(B, r, d, d).permute(0, 2, 1, 3)
+        s = newton_schulz5(torch.cat([g02.reshape(B * 2 * r, d, d), sl1], dim=0), scale)
+        s02 = s[:B * 2 * r].reshape(B, 1, 2 * r * d, d)
+        s1 = s[B * 2 * r:].reshape(B, r, d, d).permute(0, 2, 1, 3)
         return s02, s1.reshape(B, 1, d, r * d).contiguous()
 
     def write(self, ks, vs, lrs, momentum_coeffs=None):
