@@ -396,12 +396,24 @@ __global__ __launch_bounds__(kNsbThreads) void ns_small_kernel(const typename TT
   uint16_t* ob = out + (int64_t)blockIdx.x * elems;
   for (int i = tid; i < elems / 8; i += kNsbThreads) {
     const int r = (8 * i) / cols, c = 8 * i - r * cols;
+    uint16_t x[8];
+    if (trans) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) x[u] = xs[(c + u) * ldx + r];
+    } else {
+      const uint4 q = *reinterpret_cast<const uint4*>(xs + r * ldx + c);
+      const uint32_t wq[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        x[2 * u] = (uint16_t)(wq[u] & 0xffff);
+        x[2 * u + 1] = (uint16_t)(wq[u] >> 16);
+      }
+    }
+    // (one rounding: packing rounds x * scale to bf16 as the multi-launch
+    // path's bf16(bf16(x * scale)) does)
     float v[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const uint16_t x = trans ? xs[(c + u) * ldx + r] : xs[r * ldx + c + u];
-      v[u] = nsb_round(bf16_to_f32(x) * scale);
-    }
+    for (int u = 0; u < 8; ++u) v[u] = bf16_to_f32(x[u]) * scale;
     uint4 o;
     o.x = pack_bf16x2(v[0], v[1]);
     o.y = pack_bf16x2(v[2], v[3]);
