@@ -453,6 +453,15 @@ int uttt_debug_set_gemm_layout(int na);
  * value. */
 int uttt_debug_set_ns_path(int path);
 
+/* Test hook (no reference counterpart): which kernel runs the fused uTTT-Dense
+ * stage 1 (uttt_dense_update_stage1, uttt_dense_update_stage1_layers) for
+ * heads of D <= 192.  0: by the grid (the staged eight-wave kernel, weights
+ * through LDS, for grids of at least 256 workgroups; the four-wave kernel
+ * with register prefetch below that), 1: always the staged kernel, 2: always
+ * the four-wave kernel.  Both give identical results.  Returns the previous
+ * mode. */
+int uttt_debug_set_s1_staged(int mode);
+
 /* WRITE step of the fast weights.  Replaces the write of
  * _apply_moe_update_dense (uttt_llm/flame/custom_models/uttt_moe/
  * modeling_recurrent_lact.py:754-825; seg = C, norm_from_fast = 0,

@@ -232,6 +232,42 @@ def test_fused_dense_update_stage1(BH, N, d, dh, with_lr):
     assert torch.equal(dy2, dy) and torch.equal(hl2, hl)
 
 
+@pytest.mark.parametrize("BH,N,d,dh", [
+    (4, 3000, 192, 384),   # configs[1] head, ragged token tiles
+    (4, 1024, 96, 192),    # configs[0] head
+    (2, 77, 128, 96),      # one partial tile, odd block count (3 blocks: a lone last block)
+    (3, 128, 64, 32),      # one hidden block
+])
+def test_staged_stage1_equals_four_wave_kernel(BH, N, d, dh):
+    """The two kernels of the fused stage 1 for D <= 192 -- eight waves with
+    the weight fragments staged through LDS (taken for grids of >= 256
+    workgroups) and four waves with register prefetch (smaller grids) --
+    compute every output with the same MFMA chain and epilogue, so they agree
+    bit for bit; both forced on the same inputs, with and without lr."""
+    from uttt_amd import _lib as L
+
+    g = torch.Generator().manual_seed(7 * N + d)
+    W02 = (torch.randn(BH, 1, 2 * dh, d, generator=g) / d ** 0.5).to(torch.bfloat16).to(DEV)
+    W1 = (torch.randn(BH, 1, d, dh, generator=g) / dh ** 0.5).to(torch.bfloat16).to(DEV)
+    kh, vh = (torch.nn.functional.normalize(torch.randn(BH, N, d, generator=g), dim=-1)
+              .to(torch.bfloat16).to(DEV) for _ in range(2))
+    lr3 = [(torch.sigmoid(torch.randn(BH, N, generator=g)) * 0.1).to(DEV) for _ in range(3)]
+    gs = DN._gs(BH, N, DEV)
+    for lr in (lr3, None):
+        outs = []
+        for mode in (1, 2):
+            prev = L.lib().uttt_debug_set_s1_staged(mode)
+            try:
+                outs.append(DN._update_stage1(W02, W1, kh, vh, lr, gs))
+            finally:
+                L.lib().uttt_debug_set_s1_staged(prev)
+        torch.cuda.synchronize()
+        (dy_s, hl_s), (dy_f, hl_f) = outs
+        assert torch.equal(dy_s.view(torch.int16), dy_f.view(torch.int16))
+        assert torch.equal(hl_s.view(torch.int16), hl_f.view(torch.int16))
+        assert torch.isfinite(dy_s.float()).all() and torch.isfinite(hl_s.float()).all()
+
+
 @pytest.mark.parametrize("use_moun,with_mom,master_renorm", [
     (False, True, False), (True, False, False), (True, True, False), (True, True, True)])
 def test_bank_momentum_and_muon_equal_the_functional_write(use_moun, with_mom, master_renorm):

@@ -133,6 +133,7 @@ SIGNATURES = {
     "uttt_debug_set_apply_path": (c_int, [c_int]),
     "uttt_debug_set_gemm_layout": (c_int, [c_int]),
     "uttt_debug_set_ns_path": (c_int, [c_int]),
+    "uttt_debug_set_s1_staged": (c_int, [c_int]),
     "uttt_grouped_gemm_nt2": (c_int, [c_p, c_p, c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int,
                                       c_p, c_p]),
     "uttt_grouped_gemm_tn2": (c_int, [c_p, c_p, c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int,

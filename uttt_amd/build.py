@@ -34,12 +34,13 @@ COMMON_FLAGS = [
 ]
 
 
-# Sources whose kernels must not use scratch memory: the grouped GEMMs issue
-# their LDS fragment reads as inline asm with explicit waits, so a register
-# spill between a read and its wait would save the value from before the read;
+# Sources whose kernels must not use scratch memory: the grouped GEMMs and the
+# staged uTTT-Dense stage 1 issue their LDS fragment reads as inline asm with
+# explicit waits, so a register spill between a read and its wait would save
+# the value from before the read;
 # the one-launch Newton-Schulz holds its accumulators and the products it
 # writes back across barriers, where a spill would cost more than the work.
-NO_SCRATCH = {"grouped_gemm.hip", "ns_small.hip"}
+NO_SCRATCH = {"grouped_gemm.hip", "ns_small.hip", "dense_update.hip"}
 
 
 def _scratch_kernels(remarks: str) -> list:

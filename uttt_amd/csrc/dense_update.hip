@@ -10,16 +10,18 @@
 // the grouped stage 1 (a DH product to fp32, then the SwiGLU-derivative
 // epilogue on fp32 Y0 / Y2 / DH).
 //
-// One workgroup = 4 waves; each wave owns 32 tokens of one head and keeps
-// their k^T and v^T fragments in registers for the whole kernel.  It walks
-// the head's 32-unit hidden blocks: Y0, Y2 and DH of a block land in the same
+// One workgroup = 128 tokens of one head, 32 per token group; a wave keeps
+// its group's k^T and v^T fragments in registers for the whole kernel and
+// walks 32-unit hidden blocks: Y0, Y2 and DH of a block land in the same
 // accumulator layout (lane = token, 16 hidden units per lane), so the
 // epilogue is lane-local and DH never leaves the registers.  The weights come
 // from a fragment-ordered copy (uttt_dense_pack_update_weights) in which the
 // A-operand rows of every block are permuted so that each lane's 16
 // accumulator rows are 16 consecutive hidden units: every output row segment
-// is two 16-byte stores.  The 4 waves of a workgroup stream the same weight
-// fragments at about the same time (L2 / vector-cache reuse).
+// is two 16-byte stores.  For D <= 192 (dense_update_s1_staged_kernel) two
+// waves share a token group and split the blocks, the weight fragments pass
+// through LDS once per workgroup; for larger heads (dense_update_s1_kernel)
+// 4 waves each walk every block, loading the fragments into registers.
 #include <stdint.h>
 
 #include "common.h"
@@ -106,10 +108,96 @@ struct S1Layers {
   int l, H, lr_per_head;
 };
 
-// PIPE: two register sets of weight fragments, block b + 1's loads in flight
-// while block b is multiplied and its epilogue runs (the last prefetch
-// re-reads the last block: unconditional loads keep the wait counts exact).
-// It needs 2 x 3 D/16 fragments of registers: D <= 192 only.
+// The inputs of one lane's token t of head bh: its k^T and v^T fragments
+// (k = 16 s + 8 g .. + 8), its three lr values (1 without lr) and its row of
+// the head's outputs.  t past N is clamped to N - 1 (every address valid).
+template <int D, class LR, bool LAYERED>
+struct S1Token {
+  bf16x8_t kf[D / 16], vf[D / 16];
+  float l0 = 1.0f, l1 = 1.0f, l2 = 1.0f;
+  int64_t row;
+  bool valid;
+
+  __device__ __forceinline__ void load(const uint16_t* kh, const uint16_t* vh, const float* lr0,
+                                       const float* lr1, const float* lr2, const S1Layers& ly,
+                                       int N, int bh, int t, int g) {
+    constexpr int KS = D / 16;
+    valid = t < N;
+    const int tc = min(t, N - 1);
+    row = (int64_t)bh * N + tc;
+    if constexpr (LAYERED) {
+      // a wave's 32 tokens lie in one layer (l is a multiple of 32)
+      const int li = __builtin_amdgcn_readfirstlane(tc / ly.l);
+      const int bb = bh / ly.H, hh = bh - bb * ly.H;
+      const int64_t tr = (int64_t)bb * ly.l + (tc - li * ly.l);  // row of the layer's tensors
+      const uint16_t* kp = static_cast<const uint16_t*>(ly.k.p[li]) + (tr * ly.H + hh) * D;
+      const uint16_t* vp = static_cast<const uint16_t*>(ly.v.p[li]) + (tr * ly.H + hh) * D;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        kf[s] = ld16(kp + 16 * s + 8 * g);
+        vf[s] = ld16(vp + 16 * s + 8 * g);
+      }
+      using S = typename LR::S;
+      const bool has = ly.lr.p[0] != nullptr;
+      // a missing lr reads the first k element (a valid address) and is ignored
+      const S* lp = has ? static_cast<const S*>(ly.lr.p[li]) +
+                              tr * (ly.lr_per_head ? 3 * ly.H : 3) + (ly.lr_per_head ? 3 * hh : 0)
+                        : reinterpret_cast<const S*>(kp);
+      const S a = lp[0], b = lp[has ? 1 : 0], c = lp[has ? 2 : 0];
+      if (has) {
+        l0 = LR::load(a);
+        l1 = LR::load(b);
+        l2 = LR::load(c);
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        kf[s] = ld16(kh + row * D + 16 * s + 8 * g);
+        vf[s] = ld16(vh + row * D + 16 * s + 8 * g);
+      }
+      // a missing lr reads the first k element (a valid address) and is ignored
+      const float* fb = reinterpret_cast<const float*>(kh);
+      const float l0r = *(lr0 ? lr0 + row : fb), l1r = *(lr1 ? lr1 + row : fb),
+                  l2r = *(lr2 ? lr2 + row : fb);
+      l0 = lr0 ? l0r : 1.0f;
+      l1 = lr1 ? l1r : 1.0f;
+      l2 = lr2 ? l2r : 1.0f;
+    }
+  }
+
+  // The SwiGLU-derivative epilogue of hidden block blk from its accumulators
+  // (lane = token, 16 consecutive hidden units per lane) and its six 16-byte
+  // stores (valid tokens only).
+  __device__ __forceinline__ void epilogue(const f32x16_t& y0, const f32x16_t& y2,
+                                           const f32x16_t& dh, uint16_t* dyr, uint16_t* hr, int I,
+                                           int blk) const {
+    float d0[16], d2[16], hh[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const float sg = sigm(y0[u]);
+      const float sw = sg * y0[u];
+      d0[u] = sg * y2[u] * dh[u] * (1.0f + y0[u] * (1.0f - sg)) * l0;
+      d2[u] = sw * dh[u] * l2;
+      hh[u] = sw * y2[u] * l1;
+    }
+    if (valid) {
+      uint16_t* o = dyr + 32 * blk;
+      store16(o, d0);
+      store16(o + 8, d0 + 8);
+      store16(o + I, d2);
+      store16(o + I + 8, d2 + 8);
+      store16(hr + 32 * blk, hh);
+      store16(hr + 32 * blk + 8, hh + 8);
+    }
+  }
+};
+
+// Four waves, one per 32 tokens, each walking all hidden blocks with its
+// weight fragments loaded from the packed copy into registers per block
+// (larger heads, and grids too small to fill the chip).  PIPE (D <= 192):
+// two register sets, block b + 1's loads in flight while block b is
+// multiplied and its epilogue runs (the last prefetch re-reads the last
+// block: unconditional loads keep the wait counts exact).
 template <int D, bool PIPE, class LR, bool LAYERED>
 __global__ __launch_bounds__(kUpdWaves * 64) void dense_update_s1_kernel(
     const uint16_t* __restrict__ kh, const uint16_t* __restrict__ vh,
@@ -120,57 +208,12 @@ __global__ __launch_bounds__(kUpdWaves * 64) void dense_update_s1_kernel(
   const int bh = blockIdx.y;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int r = lane & 31, g = lane >> 5;
-  const int t = blockIdx.x * kUpdTok + 32 * w + r;
-  const bool valid = t < N;
-  const int tc = min(t, N - 1);  // clamped: always a valid address
-  const int64_t row = (int64_t)bh * N + tc;
-
-  // k^T / v^T fragments of this lane's token, k = 16 s + 8 g .. + 8
-  bf16x8_t kf[KS], vf[KS];
-  float l0 = 1.0f, l1 = 1.0f, l2 = 1.0f;
-  if constexpr (LAYERED) {
-    // a wave's 32 tokens lie in one layer (l is a multiple of 32)
-    const int li = __builtin_amdgcn_readfirstlane(tc / ly.l);
-    const int bb = bh / ly.H, hh = bh - bb * ly.H;
-    const int64_t tr = (int64_t)bb * ly.l + (tc - li * ly.l);  // row of the layer's tensors
-    const uint16_t* kp = static_cast<const uint16_t*>(ly.k.p[li]) + (tr * ly.H + hh) * D;
-    const uint16_t* vp = static_cast<const uint16_t*>(ly.v.p[li]) + (tr * ly.H + hh) * D;
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      kf[s] = ld16(kp + 16 * s + 8 * g);
-      vf[s] = ld16(vp + 16 * s + 8 * g);
-    }
-    using S = typename LR::S;
-    const bool has = ly.lr.p[0] != nullptr;
-    // a missing lr reads the first k element (a valid address) and is ignored
-    const S* lp = has ? static_cast<const S*>(ly.lr.p[li]) +
-                            tr * (ly.lr_per_head ? 3 * ly.H : 3) + (ly.lr_per_head ? 3 * hh : 0)
-                      : reinterpret_cast<const S*>(kp);
-    const S a = lp[0], b = lp[has ? 1 : 0], c = lp[has ? 2 : 0];
-    if (has) {
-      l0 = LR::load(a);
-      l1 = LR::load(b);
-      l2 = LR::load(c);
-    }
-  } else {
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      kf[s] = ld16(kh + row * D + 16 * s + 8 * g);
-      vf[s] = ld16(vh + row * D + 16 * s + 8 * g);
-    }
-    // a missing lr reads the first k element (a valid address) and is ignored
-    const float* fb = reinterpret_cast<const float*>(kh);
-    const float l0r = *(lr0 ? lr0 + row : fb), l1r = *(lr1 ? lr1 + row : fb),
-                l2r = *(lr2 ? lr2 + row : fb);
-    l0 = lr0 ? l0r : 1.0f;
-    l1 = lr1 ? l1r : 1.0f;
-    l2 = lr2 ? l2r : 1.0f;
-  }
-
+  S1Token<D, LR, LAYERED> tk;
+  tk.load(kh, vh, lr0, lr1, lr2, ly, N, bh, blockIdx.x * kUpdTok + 32 * w + r, g);
   const uint16_t* ph = packed + (int64_t)bh * 3 * I * D + lane * 8;
   const int64_t part = (int64_t)I * D;
-  uint16_t* dyr = dy + row * 2 * I + 16 * g;
-  uint16_t* hr = hid + row * I + 16 * g;
+  uint16_t* dyr = dy + tk.row * 2 * I + 16 * g;
+  uint16_t* hr = hid + tk.row * I + 16 * g;
   const int nblk = I / 32;
 
   auto load_blk = [&](bf16x8_t (&a0)[KS], bf16x8_t (&a2)[KS], bf16x8_t (&a1)[KS], int blk)
@@ -190,28 +233,11 @@ __global__ __launch_bounds__(kUpdWaves * 64) void dense_update_s1_kernel(
     for (int v = 0; v < 16; ++v) y0[v] = y2[v] = dh[v] = 0.0f;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      y0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0[s], kf[s], y0, 0, 0, 0);
-      y2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2[s], kf[s], y2, 0, 0, 0);
-      dh = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1[s], vf[s], dh, 0, 0, 0);
+      y0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0[s], tk.kf[s], y0, 0, 0, 0);
+      y2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2[s], tk.kf[s], y2, 0, 0, 0);
+      dh = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1[s], tk.vf[s], dh, 0, 0, 0);
     }
-    float d0[16], d2[16], hh[16];
-#pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      const float sg = sigm(y0[u]);
-      const float sw = sg * y0[u];
-      d0[u] = sg * y2[u] * dh[u] * (1.0f + y0[u] * (1.0f - sg)) * l0;
-      d2[u] = sw * dh[u] * l2;
-      hh[u] = sw * y2[u] * l1;
-    }
-    if (valid) {
-      uint16_t* o = dyr + 32 * blk;
-      store16(o, d0);
-      store16(o + 8, d0 + 8);
-      store16(o + I, d2);
-      store16(o + I + 8, d2 + 8);
-      store16(hr + 32 * blk, hh);
-      store16(hr + 32 * blk + 8, hh + 8);
-    }
+    tk.epilogue(y0, y2, dh, dyr, hr, I, blk);
   };
 
   if constexpr (PIPE) {
@@ -234,11 +260,157 @@ __global__ __launch_bounds__(kUpdWaves * 64) void dense_update_s1_kernel(
   }
 }
 
+// D <= 192: 8 waves, two per group of 32 tokens.  Waves w and w + 4 hold the
+// same tokens' k / v fragments and take the even / odd hidden block of each
+// pair of blocks, so the two waves of a SIMD share its matrix core and vector
+// ALU (one's epilogue can run beside the other's products).  A pair's weight
+// fragments -- six per k step, each 1 KiB of the packed copy -- go straight
+// from global memory into LDS once per workgroup (global_load_lds, one
+// fragment per wave instruction; each wave read all of them from the vector
+// cache in the four-wave kernel), double-buffered: per pair, the next pair's
+// loads issue first, then this block's products read the current buffer.
+// The fragment reads are inline asm, which the compiler's wait-count pass
+// does not model, so it does not hold them behind the loads into the other
+// buffer (it cannot tell the two apart); every wait on them is explicit.
+// After the products one wait covers the next pair's loads (older memory
+// operations: the previous block's stores), then the epilogue stores, then
+// an LDS-only barrier.
+constexpr int kStgWaves = 8;
+// grids of at least this many workgroups take the staged kernel
+// (uttt_debug_set_s1_staged moves it)
+int g_s1_staged_min_grid = 256;
+
+typedef int s1_i32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ s1_i32x4 s1_ds_read(uint32_t addr) {
+  s1_i32x4 v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr) : "memory");
+  return v;
+}
+// s_waitcnt lgkmcnt(N), tied to the fragment registers, so that no MFMA
+// reading them moves above it
+template <int N>
+__device__ __forceinline__ void s1_lgkm_wait(s1_i32x4& a, s1_i32x4& b, s1_i32x4& c) {
+  asm volatile("s_waitcnt lgkmcnt(%3)" : "+v"(a), "+v"(b), "+v"(c) : "i"(N) : "memory");
+}
+__device__ __forceinline__ void s1_lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+template <int D, class LR, bool LAYERED>
+__global__ __launch_bounds__(kStgWaves * 64) void dense_update_s1_staged_kernel(
+    const uint16_t* __restrict__ kh, const uint16_t* __restrict__ vh,
+    const float* __restrict__ lr0, const float* __restrict__ lr1, const float* __restrict__ lr2,
+    S1Layers ly, int N, int I, const uint16_t* __restrict__ packed, uint16_t* __restrict__ dy,
+    uint16_t* __restrict__ hid) {
+  constexpr int KS = D / 16;
+  constexpr int kBlkChunks = 3 * KS * 64;    // 16-byte chunks of one block's three parts
+  constexpr int kPairChunks = 2 * kBlkChunks;
+  constexpr int kFrags = 6 * KS;             // 1 KiB fragments of a pair
+  constexpr int kFragsPerWave = (kFrags + kStgWaves - 1) / kStgWaves;
+  // two arrays, so that the compiler sees a stage's reads apart from the loads
+  // into the other
+  __shared__ __attribute__((aligned(16))) uint4 st0[kPairChunks];
+  __shared__ __attribute__((aligned(16))) uint4 st1[kPairChunks];
+  const int bh = blockIdx.y;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int half = w >> 2, tw = w & 3;  // block parity, token group
+  const int r = lane & 31, g = lane >> 5;
+  S1Token<D, LR, LAYERED> tk;
+  tk.load(kh, vh, lr0, lr1, lr2, ly, N, bh, blockIdx.x * kUpdTok + 32 * tw + r, g);
+  const uint16_t* ph = packed + (int64_t)bh * 3 * I * D;
+  const int64_t part = (int64_t)I * D;
+  uint16_t* dyr = dy + tk.row * 2 * I + 16 * g;
+  uint16_t* hr = hid + tk.row * I + 16 * g;
+  const int nblk = I / 32, npair = (nblk + 1) / 2;
+
+  // pair p's fragment f (block 2 p + f / (3 KS) clamped to the last block,
+  // part, k step) straight into the LDS stage at f KiB
+  auto issue = [&](uint4 (&dst)[kPairChunks], int p) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < kFragsPerWave; ++i) {
+      const int f = w + kStgWaves * i;  // wave-uniform
+      if (kFrags % kStgWaves == 0 || f < kFrags) {
+        const int slot = f / (3 * KS), rem = f - slot * (3 * KS);
+        const int pt = rem / KS, s = rem - pt * KS;
+        const int blk = min(2 * p + slot, nblk - 1);
+        const uint16_t* src = ph + pt * part + ((int64_t)blk * KS + s) * 64 * 8 + lane * 8;
+        __builtin_amdgcn_global_load_lds(
+            src, (__attribute__((address_space(3))) void*)(&dst[f * 64]), 16, 0, 0);
+      }
+    }
+  };
+  auto step = [&](const uint4 (&cur)[kPairChunks], uint4 (&nxt)[kPairChunks], int p)
+      __attribute__((always_inline)) {
+    const int blk = 2 * p + half;
+    if (p + 1 < npair) issue(nxt, p + 1);
+    const bool mine = blk < nblk;  // wave-uniform
+    f32x16_t y0, y2, dh;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) y0[v] = y2[v] = dh[v] = 0.0f;
+    if (mine) {
+      // fragment (part, k step s) of this wave's block at base + 1 KiB
+      // (part KS + s); step s + 1's three reads issue before step s's MFMAs
+      const uint32_t base = (uint32_t)(uintptr_t)(
+          (const __attribute__((address_space(3))) uint4*)(&cur[half * kBlkChunks + lane]));
+      s1_i32x4 f0 = s1_ds_read(base), f2 = s1_ds_read(base + (KS << 10)),
+               f1 = s1_ds_read(base + (2 * KS << 10));
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        s1_i32x4 n0, n2, n1;
+        if (s + 1 < KS) {
+          n0 = s1_ds_read(base + ((s + 1) << 10));
+          n2 = s1_ds_read(base + ((KS + s + 1) << 10));
+          n1 = s1_ds_read(base + ((2 * KS + s + 1) << 10));
+          s1_lgkm_wait<3>(f0, f2, f1);
+        } else {
+          s1_lgkm_wait<0>(f0, f2, f1);
+        }
+        y0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, f0), tk.kf[s],
+                                                     y0, 0, 0, 0);
+        y2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, f2), tk.kf[s],
+                                                     y2, 0, 0, 0);
+        dh = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, f1), tk.vf[s],
+                                                     dh, 0, 0, 0);
+        if (s + 1 < KS) {
+          f0 = n0;
+          f2 = n2;
+          f1 = n1;
+        }
+      }
+    }
+    // the next pair's loads have landed before this block's stores issue
+    // (tied to the accumulators, so it stays after this block's MFMAs)
+    asm volatile("s_waitcnt vmcnt(0)" : "+v"(y0), "+v"(y2), "+v"(dh) :: "memory");
+    if (mine) tk.epilogue(y0, y2, dh, dyr, hr, I, blk);
+    s1_lds_barrier();  // every wave's loads into nxt are in, every read of cur done
+  };
+
+  issue(st0, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  s1_lds_barrier();
+  for (int p = 0; p < npair; p += 2) {
+    step(st0, st1, p);
+    if (p + 1 >= npair) break;
+    step(st1, st0, p + 1);
+  }
+}
+
 template <int D, class LR = F32T, bool LAYERED = false>
 void launch_update_s1(int BH, int N, int I, hipStream_t st, const uint16_t* k, const uint16_t* v,
                       const float* a, const float* b, const float* c, const uint16_t* p,
                       uint16_t* o, uint16_t* h, const S1Layers& ly = S1Layers{}) {
   const dim3 grid((unsigned)((N + kUpdTok - 1) / kUpdTok), (unsigned)BH);
+  // the staged kernel where the grid fills the chip (configs[1]'s write:
+  // 768 workgroups, 100 -> 89 us); on small grids (configs[0]: 16) its
+  // per-pair load wait and barrier cost more than the shared loads save
+  // (50.5 -> 56.7 us), and the four-wave kernel with register prefetch runs
+  if constexpr (D <= 192) {
+    if ((int64_t)grid.x * grid.y >= g_s1_staged_min_grid) {
+      hipLaunchKernelGGL((dense_update_s1_staged_kernel<D, LR, LAYERED>), grid,
+                         dim3(kStgWaves * 64), 0, st, k, v, a, b, c, ly, N, I, p, o, h);
+      return;
+    }
+  }
   hipLaunchKernelGGL((dense_update_s1_kernel<D, (D <= 192), LR, LAYERED>), grid,
                      dim3(kUpdWaves * 64), 0, st, k, v, a, b, c, ly, N, I, p, o, h);
 }
@@ -247,6 +419,13 @@ void launch_update_s1(int BH, int N, int I, hipStream_t st, const uint16_t* k, c
 }  // namespace uttt
 
 using namespace uttt;
+
+extern "C" int uttt_debug_set_s1_staged(int mode) {
+  UTTT_REQUIRE(mode >= 0 && mode <= 2, "debug_set_s1_staged: mode=%d (0, 1 or 2)", mode);
+  const int prev = g_s1_staged_min_grid == 256 ? 0 : g_s1_staged_min_grid == 0 ? 1 : 2;
+  g_s1_staged_min_grid = mode == 0 ? 256 : mode == 1 ? 0 : 0x7fffffff;
+  return prev;
+}
 
 extern "C" int uttt_dense_update_supported(int D, int I) {
   return (D == 64 || D == 96 || D == 128 || D == 192 || D == 256) && I >= 32 && I <= 512 &&
