@@ -75,9 +75,9 @@ int uttt_router_select(const float* logits, int64_t l_sb, int64_t l_se, int64_t 
 /* Replaces FastWeightMLPSubNN._route_tokens (M/modeling_recurrent_lact.py:147-169):
  * logits[b,e,t] = sum_d router_w[b,e,d] x[b,t,d] in fp32 (x [B,T,D]
  * contiguous of x_dtype, router_w fp32 [E,D] with batch stride w_sb, 0 =
- * shared), then the selection of uttt_router_select (D is cut into slices
- * summed in a fixed order when the token tiles alone would not fill the
- * chip).  logits_out: optional fp32 [B,E,T]; lb_loss and balance_sum as in
+ * shared), then the selection of uttt_router_select (32 tokens per
+ * workgroup, whose waves take slices of D summed in a fixed order).
+ * logits_out: optional fp32 [B,E,T]; lb_loss and balance_sum as in
  * uttt_router_select. */
 int uttt_route_tokens(const void* x, int x_dtype, const float* router_w, int64_t w_sb, int B,
                       int T, int D, int E, const float* bias, int64_t bias_sb, int topk,
