@@ -69,3 +69,17 @@ def test_routed_read_graph_replays(T, E, D, I, topk):
         torch.cuda.synchronize()
         assert torch.equal(out_static, ref), f"replay {i}: graph output differs from eager"
         assert torch.isfinite(ref.float()).all()
+
+
+def test_stream_of_is_torchs_current_stream():
+    """The glue launches on torch's current stream of the tensor's device:
+    the default stream, a side stream inside `torch.cuda.stream`, and the
+    default again after it."""
+    from uttt_amd import _lib as L
+
+    t = torch.empty(4, device=DEV)
+    assert L.stream_of(t) == torch.cuda.current_stream().cuda_stream
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        assert L.stream_of(t) == side.cuda_stream == torch.cuda.current_stream().cuda_stream
+    assert L.stream_of(t) == torch.cuda.current_stream().cuda_stream

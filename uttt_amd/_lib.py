@@ -249,8 +249,18 @@ def ptr(t) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+# torch's own raw-handle lookup of the current stream (what its compiled code
+# uses): one C call by device index, against ~3 us of Python device resolution
+# in torch.cuda.current_stream(device) on every kernel call of the glue
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(t: torch.Tensor) -> int:
-    """hipStream_t of torch's current stream on t's device."""
+    """hipStream_t of torch's current stream on t's device (the capture
+    stream while a HIP graph is being captured)."""
+    idx = t.get_device()
+    if _raw_stream is not None and idx >= 0:
+        return _raw_stream(idx)
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
