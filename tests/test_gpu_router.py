@@ -124,6 +124,8 @@ def _check_balance_sums(x, Rw, k, bias, mask, bal, **kw):
 @pytest.mark.parametrize("B,T,D,E,k,dtype", [
     (8, 1, 1536, 32, 2, torch.bfloat16),   # the 760M decode step
     (3, 5, 768, 16, 2, torch.bfloat16),
+    (4, 4, 768, 16, 2, torch.bfloat16),    # grouped loads, three chunks a group
+    (1, 8, 1536, 32, 2, torch.bfloat16),   # grouped loads, two chunks, the most tokens
     (2, 3, 100, 64, 4, torch.float32),     # two experts per lane, ragged D
     (2, 7, 256, 128, 3, torch.bfloat16),   # matrix-core logits for E > 64
     (2, 40, 128, 7, 2, torch.bfloat16),    # two blocks per batch
