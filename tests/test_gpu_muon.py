@@ -92,6 +92,7 @@ def _ns5_kernels(run):
     (3, 192, 96, torch.float32, 0.7),      # tall: X = G^T
     (2, 32, 192, torch.bfloat16, 1.0),     # one row block
     (5, 160, 128, torch.float32, 1.0),     # tall, 5 x 4 blocks: uneven wave grid
+    (2, 32, 32, torch.float32, 1.0),       # the smallest shape the one launch takes
 ])
 def test_one_launch_newton_schulz_equals_multi_launch(n, R, C, dtype, scale):
     """Matrices with both sides multiples of 32 and at most 192 run the whole
@@ -118,6 +119,29 @@ def test_one_launch_newton_schulz_equals_multi_launch(n, R, C, dtype, scale):
     assert torch.equal(one, multi), (one.float() - multi.float()).abs().max().item()
     ref = OW.newton_schulz5(G.cpu()) * scale
     assert _rel(one.cpu(), ref) <= 1e-2, _rel(one.cpu(), ref)
+
+
+def test_newton_schulz5_zero_slice():
+    """A zero slice orthogonalises to zero on both paths (the reference's
+    X = G / (|G| + 1e-7) is 0 and every step keeps it 0), beside non-zero
+    slices of the same call, whose norms are their own."""
+    from uttt_amd import _lib as L
+
+    G = _rand((3, 96, 96), 5)
+    G[1] = 0.0
+    outs = []
+    for path in (0, 1):   # the one launch, then the multi-launch path
+        prev = L.lib().uttt_debug_set_ns_path(path)
+        try:
+            outs.append(FWW.newton_schulz5(G.to(DEV), 1.0).cpu())
+        finally:
+            L.lib().uttt_debug_set_ns_path(prev)
+    assert torch.equal(outs[0], outs[1])
+    assert (outs[0][1] == 0).all()
+    ref = OW.newton_schulz5(G)
+    assert (ref[1] == 0).all()
+    for i in (0, 2):
+        assert _rel(outs[0][i], ref[i]) <= 1e-2, (i, _rel(outs[0][i], ref[i]))
 
 
 def _gpu_ns5(G):
